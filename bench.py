@@ -1,0 +1,183 @@
+#!/usr/bin/env python3
+"""rxw8 benchmark: W8A16 decode GEMV HBM GB/s.
+
+One step = one pass of the decode dequant-GEMV over the whole sweep
+B in {1, 4, 16} x N in {4096, 6144, 24576}, K = 4096, per-output-channel
+scales (9 launches). Every launch reads its own copy of the int8 weights
+(copies rotate, >= 6 x 143 MB of distinct weights), so the 256 MB MALL holds
+no reusable weight bytes and the figure is HBM bandwidth.
+
+value        = sweep algorithmic bytes / wall time of the timed steps (GB/s)
+roofline     = the GEMV kernel: algorithmic bytes per launch / mean launch
+               duration from HIP events recorded on the runtime's stream
+cpu_baseline = the CPU oracle (reference-order restatement, OpenMP) timed on
+               this host over a bounded sample of the same sweep
+
+Algorithmic bytes per launch: N*K (u8 weights) + 4*N (f32 scales)
++ 2*B*K (bf16 x) + 2*B*N (bf16 y).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+K = 4096
+BS = (1, 4, 16)
+NS = (4096, 6144, 24576)
+
+
+def gemv_bytes(b, n, k=K):
+    return n * k + 4 * n + 2 * b * k + 2 * b * n
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(budget_s=12.0):
+    """Oracle (reference-order CPU restatement) over the same sweep shapes."""
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(0)
+    ws = {n: oracle.quantize_w8((rng.standard_normal((n, K)) * 0.02).astype(np.float32), K)
+          for n in NS}
+    xs = {b: oracle.round_bf16(rng.standard_normal((b, K)).astype(np.float32)) for b in BS}
+    total_bytes, total_t, passes = 0, 0.0, 0
+    while total_t < budget_s and passes < 8:
+        for n in NS:
+            for b in BS:
+                u8, s = ws[n]
+                t0 = time.perf_counter()
+                oracle.quantized_linear(xs[b], u8, s, oracle.COMPUTE_BF16, threads=threads)
+                total_t += time.perf_counter() - t0
+                total_bytes += gemv_bytes(b, n)
+        passes += 1
+    return {"value": round(total_bytes / total_t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{passes} pass(es) of the 9-shape sweep (B in {list(BS)}, N in {list(NS)}, "
+                      f"K={K}) through oracle.quantized_linear (bf16 compute, f32 accumulation), "
+                      f"{total_t:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--copies", type=int, default=6)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are "
+              "not part of this build", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import rxla_amd as rx
+
+    rt = rx.Runtime(0)
+    info = rt.device_info()
+    stream = torch.cuda.Stream()  # default priority
+    rt.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    log(f"device {info}; allocating {args.copies} weight copies per N")
+    with torch.cuda.stream(stream):
+        weights = {n: [(torch.randint(1, 256, (n, K), dtype=torch.uint8, device="cuda",
+                                      generator=gen),
+                        torch.rand((n, 1), dtype=torch.float32, device="cuda",
+                                   generator=gen) * 1e-3 + 1e-4)
+                       for _ in range(args.copies)] for n in NS}
+        xs = {b: torch.randn((b, K), device="cuda", generator=gen).to(torch.bfloat16) for b in BS}
+        ys = {(b, n): torch.empty((b, n), dtype=torch.bfloat16, device="cuda")
+              for b in BS for n in NS}
+    stream.synchronize()
+    wb = {n: [(rt.wrap_tensor(u), rt.wrap_tensor(s)) for u, s in weights[n]] for n in NS}
+    xb = {b: rt.wrap_tensor(xs[b]) for b in BS}
+    yb = {k: rt.wrap_tensor(v) for k, v in ys.items()}
+    plan = [(b, n) for n in NS for b in BS]
+    step_bytes = sum(gemv_bytes(b, n) for b, n in plan)
+    counter = [0]
+
+    def step(events=None):
+        for b, n in plan:
+            u, s = wb[n][counter[0] % args.copies]
+            counter[0] += 1
+            if events is not None:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+            rx.quantized_linear(rt, xb[b], u, s, rx.DType.BF16, out=yb[(b, n)])
+            if events is not None:
+                e1.record(stream)
+                events.append((b, n, e0, e1))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(events)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    log(f"timed {args.steps} steps in {wall:.4f} s")
+
+    per_shape = {}
+    for b, n, e0, e1 in events:
+        per_shape.setdefault((b, n), []).append(e0.elapsed_time(e1) * 1e-3)
+    launch_bytes = [gemv_bytes(b, n) for b, n, _, _ in events]
+    launch_s = [e0.elapsed_time(e1) * 1e-3 for _, _, e0, e1 in events]
+    mean_bytes = float(np.mean(launch_bytes))
+    mean_s = float(np.mean(launch_s))
+    achieved = mean_bytes / mean_s / 1e9
+    sweep = {f"B{b}_N{n}": {"us": round(float(np.median(v)) * 1e6, 2),
+                            "GBs": round(gemv_bytes(b, n) / float(np.median(v)) / 1e9, 1)}
+             for (b, n), v in sorted(per_shape.items())}
+    log(json.dumps(sweep))
+
+    value = step_bytes * args.steps / wall / 1e9
+    out = {
+        "metric": "W8A16 GEMV HBM GB/s (% peak) + decode tokens/sec, synthetic Qwen-style 28L",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (torch.randint u8 codes, uniform scales, randn bf16 activations; "
+                "seed 0)",
+        "config": {"workload": "decode dequant-GEMV sweep (BASELINE configs[1])",
+                   "batch": list(BS), "out_features": list(NS), "in_features": K,
+                   "scales": "per-output-channel f32", "weight_copies": args.copies,
+                   "launches_per_step": len(plan), "bytes_per_step": step_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "rxw8_gemv_w8_mb1",
+                     "mean_launch_us": round(mean_s * 1e6, 3),
+                     "mean_launch_bytes": int(mean_bytes)},
+        "sweep": sweep,
+        "device": info,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (oracle) ...")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

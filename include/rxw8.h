@@ -1,0 +1,233 @@
+/*
+ * rxw8 -- MI355X-native (gfx950) W8A16 decode/prefill hot path of RXLA,
+ * exposed as a plain C ABI.
+ *
+ * The reference (SunDoge/rxla) reaches this path through Rust:
+ *   rxla_nn::QuantizedLinear::apply            crates/rxla-nn/src/layers.rs:251-298
+ *   Tensor::grouped_query_attention            crates/rxla-core/src/attention.rs:83-135
+ *   Tensor::scaled_dot_product_attention       crates/rxla-core/src/attention.rs:150-252
+ *   KvCache::{update_at, update_at_checked}    crates/rxla-core/src/kv_cache.rs:53-111
+ *   AppliedModel::compile / CompiledModel::{bind_parameters, run}
+ *                                              crates/rxla-nn/src/applied.rs:135-239,808-815
+ * and executes through a PJRT plugin (crates/rxla-pjrt/src/runtime.rs). This
+ * header replaces that plugin boundary for the path: status codes use the
+ * PJRT_Error_Code numbering (vendor/xla/pjrt/c/pjrt_c_api.h:168-186), buffers
+ * are refcounted device allocations owned by a runtime (runtime.rs:1446,1523),
+ * and every entry point validates shapes and dtypes before anything is
+ * launched, leaving outputs and state untouched on error.
+ *
+ * Threading: a runtime owns one HIP stream; all work on it is stream-ordered.
+ * Entry points are thread-safe (internal mutex). Entry points that return
+ * new buffers enqueue work and return; rxw8_buffer_to_host and
+ * rxw8_runtime_synchronize block until the stream has drained.
+ */
+#ifndef RXW8_H
+#define RXW8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RXW8_ABI_VERSION 1
+
+/* ---- status (PJRT_Error_Code numbering, pjrt_c_api.h:168-186) ------------ */
+typedef enum rxw8_status {
+  RXW8_OK = 0,
+  RXW8_CANCELLED = 1,
+  RXW8_UNKNOWN = 2,
+  RXW8_INVALID_ARGUMENT = 3,
+  RXW8_DEADLINE_EXCEEDED = 4,
+  RXW8_NOT_FOUND = 5,
+  RXW8_ALREADY_EXISTS = 6,
+  RXW8_PERMISSION_DENIED = 7,
+  RXW8_RESOURCE_EXHAUSTED = 8,
+  RXW8_FAILED_PRECONDITION = 9,
+  RXW8_ABORTED = 10,
+  RXW8_OUT_OF_RANGE = 11,
+  RXW8_UNIMPLEMENTED = 12,
+  RXW8_INTERNAL = 13,
+  RXW8_UNAVAILABLE = 14,
+  RXW8_DATA_LOSS = 15,
+  RXW8_UNAUTHENTICATED = 16
+} rxw8_status;
+
+/* Message of the last failing call on this thread (UTF-8, never NULL). */
+const char *rxw8_last_error(void);
+/* PjrtErrorCode::is_retryable (crates/rxla-pjrt/src/runtime.rs:93-104). */
+int rxw8_status_is_retryable(int status);
+int rxw8_abi_version(void);
+
+/* ---- dtypes (the Element types of crates/rxla-pjrt/src/runtime.rs:1422-1440) */
+typedef enum rxw8_dtype {
+  RXW8_U8 = 1,
+  RXW8_I32 = 2,
+  RXW8_F16 = 3,
+  RXW8_BF16 = 4,
+  RXW8_F32 = 5
+} rxw8_dtype;
+
+#define RXW8_MAX_RANK 8
+
+typedef struct rxw8_runtime rxw8_runtime;
+typedef struct rxw8_buffer rxw8_buffer;
+
+/* ---- runtime (replaces Client::load, runtime.rs:768) --------------------- */
+
+/* Select HIP device `device`, create its stream, load the gfx950 kernels.
+ * FAILED_PRECONDITION when the device is not gfx950 or no device exists. */
+int rxw8_runtime_create(int device, rxw8_runtime **out);
+/* Drops the caller's reference; the runtime lives until its last buffer is
+ * released. */
+int rxw8_runtime_destroy(rxw8_runtime *rt);
+/* Enqueue subsequent work on an external hipStream_t (NULL: the runtime's
+ * own stream). The caller keeps the stream alive while it is in use. */
+int rxw8_runtime_set_stream(rxw8_runtime *rt, void *hip_stream);
+int rxw8_runtime_stream(rxw8_runtime *rt, void **hip_stream);
+int rxw8_runtime_synchronize(rxw8_runtime *rt);
+/* Compute units and device name (for roofline bookkeeping). */
+int rxw8_runtime_device_info(rxw8_runtime *rt, int *compute_units,
+                             char *name, size_t name_len);
+
+/* ---- buffers (Client::buffer runtime.rs:920, Buffer::to_vec :1885) -------- */
+
+/* New device buffer of dtype/dims; contents zeroed. */
+int rxw8_buffer_create(rxw8_runtime *rt, int dtype, const int64_t *dims,
+                       int rank, rxw8_buffer **out);
+/* New device buffer holding a copy of `data` (row-major, packed). */
+int rxw8_buffer_from_host(rxw8_runtime *rt, int dtype, const int64_t *dims,
+                          int rank, const void *data, rxw8_buffer **out);
+/* Non-owning view of caller-owned device memory (e.g. a torch tensor). The
+ * caller keeps the memory alive for the lifetime of the view. */
+int rxw8_buffer_wrap(rxw8_runtime *rt, int dtype, const int64_t *dims,
+                     int rank, void *device_ptr, rxw8_buffer **out);
+/* Blocking copy of the whole buffer to host; `bytes` must equal its size. */
+int rxw8_buffer_to_host(rxw8_buffer *buf, void *dst, size_t bytes);
+/* Blocking copy from host into an existing buffer. */
+int rxw8_buffer_copy_from_host(rxw8_buffer *buf, const void *src, size_t bytes);
+int rxw8_buffer_retain(rxw8_buffer *buf);
+int rxw8_buffer_release(rxw8_buffer *buf);
+int rxw8_buffer_dtype(const rxw8_buffer *buf, int *dtype);
+/* Writes up to RXW8_MAX_RANK dims; *rank receives the rank. */
+int rxw8_buffer_dims(const rxw8_buffer *buf, int64_t *dims, int *rank);
+int rxw8_buffer_device_ptr(const rxw8_buffer *buf, void **ptr);
+
+/* ---- ops --------------------------------------------------------------------
+ * Allocating forms return a new buffer in *out; `_into` forms write into a
+ * caller buffer of the exact shape/dtype and allocate nothing per call
+ * (split-K workspaces are runtime-owned, grown on first use). */
+
+/* W8 dequantisation (layers.rs:277-287): W = (f32(u8) - 128) * scale[n, k/G]
+ * -> F32 (bit-exact) or BF16 (RNE of the f32 value). weight U8 [N,K],
+ * scale F32 [N,K/G]. */
+int rxw8_dequantize(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer *scale,
+                    int out_dtype, rxw8_buffer **out);
+
+/* QuantizedLinear::apply (layers.rs:257-298) with the layer compute dtype:
+ *   x [..., K] F32 or BF16; weight U8 [N,K] (int8 + 128); scale F32 [N,K/G];
+ *   compute_dtype BF16 (W8A16: bf16(x) . bf16 weights, f32 accumulation,
+ *   bf16-rounded result) or F32 (f32 x, f32 dequantised weights).
+ *   y [..., N] of out_dtype F32 or BF16 (same values: the BF16 compute result
+ *   is bf16-valued; F32 compute requires F32 out).
+ * Errors (before launch): INVALID_ARGUMENT for rank 0, non-positive widths,
+ * K % G != 0, weight/scale shape or dtype mismatch (the InvalidLayerInput
+ * checks of layers.rs:258-274 and validate_buffer of applied.rs:1274). */
+int rxw8_quantized_linear(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
+                          rxw8_buffer *scale, int compute_dtype, int out_dtype,
+                          rxw8_buffer **y);
+int rxw8_quantized_linear_into(rxw8_runtime *rt, rxw8_buffer *x,
+                               rxw8_buffer *weight, rxw8_buffer *scale,
+                               int compute_dtype, rxw8_buffer *y);
+
+/* Dense linear with BF16 weights (bf16-stored embedding reused as lm_head,
+ * layers.rs Linear with parameter storage BF16, lib.rs:478-487):
+ * y = bf16(bf16(x) . W^T). x [..., K] F32|BF16, weight BF16 [N,K]. */
+int rxw8_linear_bf16(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
+                     int out_dtype, rxw8_buffer **y);
+int rxw8_linear_bf16_into(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
+                          rxw8_buffer *y);
+
+/* Grouped-query decode attention (attention.rs:83-135 + SDPA :150-252, F32
+ * semantics) over a contiguous per-sequence KV cache:
+ *   q [B,Hq,D] F32|BF16; k_cache/v_cache [B,Hkv,Lmax,D] BF16|F32;
+ *   lens I32 [B] (device): sequence b sees keys 0..lens[b]-1, which is the
+ *   causal mask key_pos <= q_pos (attention.rs:14-32) for q_pos = lens[b]-1;
+ *   mask: optional additive F32 [B|1, Hq|1, Lmax] (NULL = none);
+ *   scale: <= 0 selects 1/sqrt(D).
+ * Query head h reads kv head h / (Hq/Hkv). out [B,Hq,D] F32|BF16.
+ * lens entries outside [1, Lmax] are clamped into it by the kernel. */
+int rxw8_gqa_decode(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
+                    rxw8_buffer *v_cache, rxw8_buffer *lens, rxw8_buffer *mask,
+                    float scale, int out_dtype, rxw8_buffer **out);
+int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q,
+                         rxw8_buffer *k_cache, rxw8_buffer *v_cache,
+                         rxw8_buffer *lens, rxw8_buffer *mask, float scale,
+                         rxw8_buffer *out);
+
+/* KvCache::update_at / update_at_checked (kv_cache.rs:53-111): paired
+ * dynamic_update_slice of k_update/v_update (equal shapes, rank = cache rank,
+ * same dtype) into k_cache/v_cache in place, at `starts` (device I32 [rank]).
+ * Unchecked: each start is clamped to [0, dim - update_dim]
+ * (indexing.rs:663-678). Checked: the update happens only when every start
+ * lies in that range; otherwise both caches stay unchanged. accepted
+ * (optional, device F32 scalar [] or [1]) receives 1 or 0. */
+int rxw8_kv_update_at(rxw8_runtime *rt, rxw8_buffer *k_cache,
+                      rxw8_buffer *v_cache, rxw8_buffer *k_update,
+                      rxw8_buffer *v_update, rxw8_buffer *starts, int checked,
+                      rxw8_buffer *accepted);
+
+/* ---- decoder plan (AppliedModel::compile -> CompiledModel::bind_parameters
+ *      -> run, applied.rs:135-239,808-815; model composition
+ *      crates/rxla-models/src/qwen3_5/mod.rs:199-273) ------------------------ */
+
+typedef struct rxw8_decoder_config {
+  int64_t layers, hidden, q_heads, kv_heads, head_dim, intermediate, vocab;
+  int64_t max_batch, max_seq; /* KV capacity */
+  int64_t group;              /* W8 group size; == hidden for per-channel */
+  float eps, theta;
+  int32_t qk_norm; /* per-head q/k RMSNorm before RoPE */
+} rxw8_decoder_config;
+
+typedef struct rxw8_decoder rxw8_decoder;
+
+/* Validate the config and allocate the KV cache and activations. */
+int rxw8_decoder_create(rxw8_runtime *rt, const rxw8_decoder_config *cfg,
+                        rxw8_decoder **out);
+int rxw8_decoder_destroy(rxw8_decoder *dec);
+/* Number of parameter paths and the i-th path / dtype / dims (schema). */
+int rxw8_decoder_num_parameters(rxw8_decoder *dec, int *count);
+int rxw8_decoder_parameter_info(rxw8_decoder *dec, int index, const char **path,
+                                int *dtype, int64_t *dims, int *rank);
+/* Bind one parameter by path (order_parameters / validate_buffer,
+ * applied.rs:948-990,1274): NOT_FOUND for an unknown path, ALREADY_EXISTS
+ * for a second binding, INVALID_ARGUMENT for a shape/dtype mismatch. The
+ * decoder retains the buffer. */
+int rxw8_decoder_bind_parameter(rxw8_decoder *dec, const char *path,
+                                rxw8_buffer *buffer);
+/* Reset every sequence length to 0 (cache contents become unreachable). */
+int rxw8_decoder_reset(rxw8_decoder *dec);
+/* Run `s` tokens per sequence for `b` sequences (ids device I32 [b, s]),
+ * starting at each sequence's current length: prefill when s > 1, one decode
+ * step when s == 1. FAILED_PRECONDITION when a parameter is unbound,
+ * OUT_OF_RANGE when a sequence would exceed max_seq (nothing is mutated).
+ * next_ids (device I32 [b]) receives the greedy argmax of the last position's
+ * logits; logits (optional, device F32 [b, vocab]) receives those logits. */
+int rxw8_decoder_forward(rxw8_decoder *dec, rxw8_buffer *ids, int64_t b,
+                         int64_t s, rxw8_buffer *next_ids, rxw8_buffer *logits);
+/* Prefill `prompt` (device I32 [b, s]) then `steps` greedy decode steps;
+ * out_ids (device I32 [b, steps + 1]) receives the token chosen after the
+ * prompt followed by one token per decode step. With use_graph != 0 the
+ * decode step is captured once into a HIP graph and replayed. */
+int rxw8_decoder_generate(rxw8_decoder *dec, rxw8_buffer *prompt, int64_t b,
+                          int64_t s, int64_t steps, rxw8_buffer *out_ids,
+                          int use_graph);
+/* Copy of the current sequence lengths to host (int32 [max_batch]). */
+int rxw8_decoder_lens(rxw8_decoder *dec, int32_t *lens, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RXW8_H */

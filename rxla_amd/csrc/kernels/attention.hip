@@ -1,0 +1,357 @@
+// K3: grouped-query decode attention over a contiguous bf16 KV cache.
+//
+// Semantics (crates/rxla-core/src/attention.rs:83-252, F32 throughout):
+//   s_j = (q . k_j) * scale + mask_j,  p = softmax(s),  out = sum_j p_j v_j
+// for the keys j < lens[b] of sequence b; query head h reads kv head
+// h / (Hq / Hkv) (consecutive heads share a kv head, attention.rs:83-135).
+//
+// Layout: q [B, Hq, D] f32|bf16, caches [B, Hkv, Lmax, D] bf16, out
+// [B, Hq, D] f32|bf16. One workgroup (4 waves) handles one (b, kv head,
+// 256-key chunk); each wave takes 64 keys. The G = Hq/Hkv query rows of the
+// kv head share every K/V byte the workgroup loads.
+//
+// QK^T runs on v_mfma_f32_16x16x32_bf16 with K as the A operand (16 keys x
+// 32 dims per fragment, 16-byte loads of contiguous K rows) and q^T as the B
+// operand. q is f32, so it is split into bf16 hi + lo parts and both are
+// contracted (two MFMAs), which keeps the scores at f32 accuracy; K is exactly
+// bf16. Softmax statistics are reduced per wave with cross-lane shuffles,
+// probabilities go through LDS, and P.V runs on the VALU in f32 with each lane
+// owning 8 dims of every fourth key (16-byte V loads, 1 KiB per wave load).
+// Waves merge (max, sum, acc) in LDS; chunks of one (b, kv head) merge in the
+// last-arriving workgroup (deterministic order).
+#include "common.h"
+
+struct AttnArgs {
+  const void *q;        // [B, Hq, D]
+  const uint16_t *kc;   // [B, Hkv, Lmax, D] bf16
+  const uint16_t *vc;   // [B, Hkv, Lmax, D] bf16
+  const int32_t *lens;  // [B]
+  const float *mask;    // additive, mask[b * mask_sb + h * mask_sh + j], or null
+  void *out;            // [B, Hq, D]
+  float *ws;            // partials [B, Hkv, max_chunks, G, 2 + D]
+  unsigned *counters;   // [B * Hkv]
+  int64_t mask_sb, mask_sh;
+  int B, Hq, Hkv, Lmax, max_chunks;
+  float scale;
+  int q_f32, out_f32;
+};
+
+namespace {
+
+constexpr int D = 128;
+constexpr int KW = 64;            // keys per wave
+constexpr int NW = 4;             // waves per workgroup
+constexpr int KC = KW * NW;       // keys per chunk
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ float wave_max4(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float wave_sum4(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+template <int G>
+__device__ void attn_chunk(const AttnArgs &a) {
+  constexpr int GP = (G + 3) / 4 * 4;  // padded heads in the LDS P tile
+  __shared__ float p_lds[NW][KW][GP];
+  __shared__ float m_lds[NW][G], l_lds[NW][G];
+  __shared__ float o_lds[NW][G][D];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int chunk = blockIdx.x % a.max_chunks;
+  const int bh = blockIdx.x / a.max_chunks;  // b * Hkv + kvh
+  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
+  int len = a.lens[b];
+  len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
+  const int nchunks = (len + KC - 1) / KC;
+  if (chunk >= nchunks) return;  // uniform per workgroup
+
+  const int j0 = chunk * KC + wave * KW;  // first key of this wave
+  const int64_t row_base = (int64_t)bh * a.Lmax;
+  const int col = lane & 15, g4 = lane >> 4;
+
+  // q fragments (B operand): lane (head = col, dgroup = g4), 8 dims per step.
+  u32x4 qhi[4], qlo[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    float qv[8];
+    if (col < G) {
+      const int64_t off = ((int64_t)b * a.Hq + kvh * G + col) * D + 32 * t + 8 * g4;
+      if (a.q_f32) {
+        const float4 *p = (const float4 *)((const float *)a.q + off);
+        float4 x0 = p[0], x1 = p[1];
+        qv[0] = x0.x; qv[1] = x0.y; qv[2] = x0.z; qv[3] = x0.w;
+        qv[4] = x1.x; qv[5] = x1.y; qv[6] = x1.z; qv[7] = x1.w;
+      } else {
+        const u32x4 r = *(const u32x4 *)((const uint16_t *)a.q + off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qv[2 * e] = bf16_bits_to_f32(r[e] & 0xffffu);
+          qv[2 * e + 1] = bf16_bits_to_f32(r[e] >> 16);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float h0 = round_bf16(qv[2 * e]), h1 = round_bf16(qv[2 * e + 1]);
+      qhi[t][e] = pack_bf16x2(h0, h1);
+      qlo[t][e] = pack_bf16x2(qv[2 * e] - h0, qv[2 * e + 1] - h1);
+    }
+  }
+
+  // K fragments (A operand): lane (key = col, dgroup = g4); 4 key blocks x 4 steps.
+  u32x4 kf[4][4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const int key = j0 + 16 * kb + col;
+    const bool valid = key < len;
+    const uint16_t *krow = a.kc + (row_base + (valid ? key : 0)) * D + 8 * g4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      kf[kb][t] = valid ? __builtin_nontemporal_load((const u32x4 *)(krow + 32 * t))
+                        : u32x4{0, 0, 0, 0};
+  }
+  // V rows: lane (kq = g4, dgroup = col) takes keys 4 * it + kq, dims 8*col..+7.
+  u32x4 vf[16];
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+    const int key = j0 + 4 * it + g4;
+    vf[it] = key < len ? __builtin_nontemporal_load(
+                             (const u32x4 *)(a.vc + (row_base + key) * D + 8 * col))
+                       : u32x4{0, 0, 0, 0};
+  }
+
+  // Scores S^T[key][head]: lane holds key 16*kb + 4*g4 + i for head col.
+  float s[4][4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      acc = mfma16x16x32(as_bf16x8(kf[kb][t]), as_bf16x8(qhi[t]), acc);
+      acc = mfma16x16x32(as_bf16x8(kf[kb][t]), as_bf16x8(qlo[t]), acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = j0 + 16 * kb + 4 * g4 + i;
+      float v = kNegInf;
+      if (key < len) {
+        v = acc[i] * a.scale;
+        if (a.mask && col < G)
+          v += a.mask[(int64_t)b * a.mask_sb + (int64_t)(kvh * G + col) * a.mask_sh + key];
+      }
+      s[kb][i] = v;
+    }
+  }
+  float m = kNegInf;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, s[kb][i]);
+  m = wave_max4(m);
+  float l = 0.f;
+  const bool any = m != kNegInf;  // some visible key in this wave for this head
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float e = any ? __expf(s[kb][i] - m) : 0.f;
+      s[kb][i] = e;
+      l += e;
+    }
+  l = wave_sum4(l);
+  if (col < G) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p_lds[wave][16 * kb + 4 * g4 + i][col] = s[kb][i];
+    if (g4 == 0) {
+      m_lds[wave][col] = m;
+      l_lds[wave][col] = l;
+    }
+  }
+  __syncthreads();
+
+  // P.V on VALU: acc[h][e] for dims 8*col + e over keys 4*it + g4.
+  float o[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = bf16_bits_to_f32(vf[it][e] & 0xffffu);
+      v[2 * e + 1] = bf16_bits_to_f32(vf[it][e] >> 16);
+    }
+    const float *prow = p_lds[wave][4 * it + g4];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float p = prow[h];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] += p * v[e];
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = wave_sum4(o[h][e]);
+  if (g4 == 0)
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o_lds[wave][h][8 * col + e] = o[h][e];
+  __syncthreads();
+
+  // Merge the waves: thread t handles (head, dim) pairs.
+  const bool single = nchunks == 1;
+  float *part = a.ws + (((int64_t)bh * a.max_chunks + chunk) * G) * (2 + D);
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int h = idx / D, d = idx - h * D;
+    float M = kNegInf;
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, m_lds[w][h]);
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < NW; ++w) {
+      const float mw = m_lds[w][h];
+      const float f = mw == kNegInf ? 0.f : __expf(mw - M);
+      L += f * l_lds[w][h];
+      O += f * o_lds[w][h][d];
+    }
+    if (single) {
+      const float r = O / L;
+      const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
+      if (a.out_f32)
+        ((float *)a.out)[oi] = r;
+      else
+        ((uint16_t *)a.out)[oi] = f32_to_bf16_bits(r);
+    } else {
+      float *ph = part + h * (2 + D);
+      if (d == 0) {
+        ph[0] = M;
+        ph[1] = L;
+      }
+      ph[2 + d] = O;
+    }
+  }
+  if (single) return;
+  if (!splitk_arrive(a.counters + bh, (unsigned)nchunks)) return;
+  // Last workgroup of (b, kvh): merge chunk partials in chunk order.
+  const float *base = a.ws + ((int64_t)bh * a.max_chunks) * G * (2 + D);
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int h = idx / D, d = idx - h * D;
+    float M = kNegInf;
+    for (int c = 0; c < nchunks; ++c)
+      M = fmaxf(M, __hip_atomic_load(base + ((int64_t)c * G + h) * (2 + D), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT));
+    float L = 0.f, O = 0.f;
+    for (int c = 0; c < nchunks; ++c) {
+      const float *ph = base + ((int64_t)c * G + h) * (2 + D);
+      const float mc = __hip_atomic_load(ph, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float lc = __hip_atomic_load(ph + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float oc = __hip_atomic_load(ph + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float f = mc == kNegInf ? 0.f : __expf(mc - M);
+      L += f * lc;
+      O += f * oc;
+    }
+    const float r = O / L;
+    const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
+    if (a.out_f32)
+      ((float *)a.out)[oi] = r;
+    else
+      ((uint16_t *)a.out)[oi] = f32_to_bf16_bits(r);
+  }
+}
+
+}  // namespace
+
+#define RXW8_ATTN(G)                                                               \
+  extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_decode_d128_g##G(AttnArgs a) { \
+    attn_chunk<G>(a);                                                              \
+  }
+RXW8_ATTN(1)
+RXW8_ATTN(2)
+RXW8_ATTN(4)
+RXW8_ATTN(8)
+
+// ---- generic decode attention (any D <= 256, any group, f32 or bf16 cache):
+// one workgroup per (b, query head); scores staged in LDS (Lmax <= 8192).
+struct AttnGenericArgs {
+  const void *q;
+  const void *kc;
+  const void *vc;
+  const int32_t *lens;
+  const float *mask;
+  void *out;
+  int64_t mask_sb, mask_sh;
+  int B, Hq, Hkv, Lmax, D;
+  float scale;
+  int q_f32, cache_f32, out_f32;
+};
+
+__device__ __forceinline__ float ld_elem(const void *p, int64_t i, int f32) {
+  return f32 ? ((const float *)p)[i] : bf16_bits_to_f32(((const uint16_t *)p)[i]);
+}
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_decode_generic(AttnGenericArgs a) {
+  __shared__ float sc[8192];
+  __shared__ float red[256];
+  const int bh = blockIdx.x;
+  const int b = bh / a.Hq, h = bh - b * a.Hq;
+  const int kvh = h / (a.Hq / a.Hkv);
+  int len = a.lens[b];
+  len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
+  const int64_t qoff = ((int64_t)b * a.Hq + h) * a.D;
+  const int64_t kvoff = ((int64_t)b * a.Hkv + kvh) * a.Lmax * a.D;
+  float mx = -__builtin_huge_valf();
+  for (int j = threadIdx.x; j < len; j += blockDim.x) {
+    float acc = 0.f;
+    for (int d = 0; d < a.D; ++d)
+      acc += ld_elem(a.q, qoff + d, a.q_f32) * ld_elem(a.kc, kvoff + (int64_t)j * a.D + d, a.cache_f32);
+    float s = acc * a.scale;
+    if (a.mask) s += a.mask[(int64_t)b * a.mask_sb + (int64_t)h * a.mask_sh + j];
+    sc[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  red[threadIdx.x] = mx;
+  __syncthreads();
+  for (int st = blockDim.x / 2; st > 0; st >>= 1) {
+    if (threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
+    __syncthreads();
+  }
+  mx = red[0];
+  __syncthreads();
+  float sum = 0.f;
+  for (int j = threadIdx.x; j < len; j += blockDim.x) {
+    const float e = __expf(sc[j] - mx);
+    sc[j] = e;
+    sum += e;
+  }
+  red[threadIdx.x] = sum;
+  __syncthreads();
+  for (int st = blockDim.x / 2; st > 0; st >>= 1) {
+    if (threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
+    __syncthreads();
+  }
+  sum = red[0];
+  for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+    float acc = 0.f;
+    for (int j = 0; j < len; ++j)
+      acc += (sc[j] / sum) * ld_elem(a.vc, kvoff + (int64_t)j * a.D + d, a.cache_f32);
+    const int64_t oi = qoff + d;
+    if (a.out_f32)
+      ((float *)a.out)[oi] = acc;
+    else
+      ((uint16_t *)a.out)[oi] = f32_to_bf16_bits(acc);
+  }
+}

@@ -1,0 +1,84 @@
+// Shared device helpers for the rxw8 gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16_t;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
+
+#define RXW8_WAVE 64
+
+// bf16 bits -> f32 (exact).
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// f32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  bf16_t b = (bf16_t)f;
+  return __builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+// Two f32 -> packed bf16x2 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
+
+// Four u8 codes of one dword -> two dwords of bf16 pairs (exact: 0..255 fit
+// bf16's 8 significant bits). v_cvt_f32_ubyte{0..3} + v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint2 u8x4_to_bf16x4(uint32_t w) {
+  float f0 = (float)(w & 0xffu);
+  float f1 = (float)((w >> 8) & 0xffu);
+  float f2 = (float)((w >> 16) & 0xffu);
+  float f3 = (float)(w >> 24);
+  return uint2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Load 8 consecutive activations as a bf16x8 fragment from bf16 or f32 storage
+// (f32 rounded to bf16, RNE -- the x.cast(BF16) of the W8A16 layer).
+__device__ __forceinline__ u32x4 load_x8(const void *x, int64_t off, bool x_f32) {
+  if (x_f32) {
+    const float4 *p = (const float4 *)((const float *)x + off);
+    float4 a = p[0], b = p[1];
+    u32x4 r;
+    r[0] = pack_bf16x2(a.x, a.y);
+    r[1] = pack_bf16x2(a.z, a.w);
+    r[2] = pack_bf16x2(b.x, b.y);
+    r[3] = pack_bf16x2(b.z, b.w);
+    return r;
+  }
+  return *(const u32x4 *)((const uint16_t *)x + off);
+}
+
+// Deterministic split-K completion: every workgroup of a tile publishes its
+// partial, then the last one to arrive (counter) reduces all partials in
+// split order. The counter is reset by that last workgroup, so no clearing is
+// needed between launches. Returns true in the last-arriving workgroup.
+__device__ __forceinline__ bool splitk_arrive(unsigned *counter, unsigned nsplit) {
+  __shared__ unsigned s_last;
+  __threadfence();  // release this workgroup's partial stores (agent scope)
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    bool last = prev == nsplit - 1;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1u : 0u;
+  }
+  __syncthreads();
+  bool last = s_last != 0;
+  if (last) __threadfence();  // acquire the other workgroups' partials
+  return last;
+}

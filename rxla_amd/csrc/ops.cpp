@@ -1,0 +1,593 @@
+// rxw8 op entry points: validation (before any launch) and kernel dispatch.
+//
+// Validation mirrors the reference's InvalidLayerInput / BufferShape /
+// BufferDType checks (crates/rxla-nn/src/layers.rs:258-274,
+// crates/rxla-nn/src/applied.rs:1274-1297, attention.rs:83-252,
+// kv_cache.rs:53-111); a rejected call launches nothing and mutates nothing.
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+
+#include "internal.h"
+
+namespace rxw8 {
+
+// Kernel argument structs (must match the .hip definitions byte for byte).
+struct GemvArgs {
+  const void *x;
+  const void *w;
+  const float *scale;
+  void *y;
+  float *ws;
+  unsigned *counters;
+  int M, N, K, G;
+  int ksplit;
+  int x_f32, y_f32;
+};
+
+struct GemmArgs {
+  const void *x;
+  const uint8_t *w;
+  const float *scale;
+  void *y;
+  int M, N, K, G;
+  int x_f32, y_f32;
+};
+
+struct DequantArgs {
+  const uint8_t *w;
+  const float *scale;
+  void *out;
+  int64_t n, k, g;
+  int out_bf16;
+};
+
+struct GenericLinearArgs {
+  const void *x;
+  const void *w;
+  const float *scale;
+  void *y;
+  int64_t m, n, k, g;
+  int x_f32, y_f32, compute_bf16, w_kind;
+};
+
+struct KvUpdateArgs {
+  void *kc;
+  void *vc;
+  const void *ku;
+  const void *vu;
+  const int32_t *starts;
+  float *accepted;
+  int64_t dims[8];
+  int64_t udims[8];
+  int64_t total;
+  int rank;
+  int elem;
+  int checked;
+};
+
+struct AttnArgs {
+  const void *q;
+  const uint16_t *kc;
+  const uint16_t *vc;
+  const int32_t *lens;
+  const float *mask;
+  void *out;
+  float *ws;
+  unsigned *counters;
+  int64_t mask_sb, mask_sh;
+  int B, Hq, Hkv, Lmax, max_chunks;
+  float scale;
+  int q_f32, out_f32;
+};
+
+struct AttnGenericArgs {
+  const void *q;
+  const void *kc;
+  const void *vc;
+  const int32_t *lens;
+  const float *mask;
+  void *out;
+  int64_t mask_sb, mask_sh;
+  int B, Hq, Hkv, Lmax, D;
+  float scale;
+  int q_f32, cache_f32, out_f32;
+};
+
+static unsigned grid_for(int64_t n, int per_block = 256, int64_t cap = 1 << 16) {
+  int64_t g = (n + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
+static int env_int(const char *name, int dflt) {
+  const char *v = std::getenv(name);
+  return v && *v ? std::atoi(v) : dflt;
+}
+
+// Split-K factor for the GEMV: minimise ceil(tiles*ks / CUs) / ks (time per
+// CU in units of a full-K tile), preferring the smaller split on ties.
+static int choose_ksplit(const Runtime *rt, int64_t n, int64_t k, int64_t g, int64_t unit) {
+  const int forced = env_int("RXW8_GEMV_KSPLIT", 0);
+  const int64_t tiles = (n + 63) / 64;
+  const bool per_channel = g == k;
+  int best = 1;
+  double best_cost = 1e30;
+  for (int ks = 1; ks <= 32; ks *= 2) {
+    if (k % ks) continue;
+    const int64_t kc = k / ks;
+    if (kc % unit) continue;
+    if (!per_channel && kc % g) continue;
+    if (forced) {
+      if (ks == forced) return ks;
+      continue;
+    }
+    const int64_t wgs = tiles * ks;
+    const double cost = (double)((wgs + rt->cus - 1) / rt->cus) / ks;
+    if (cost < best_cost - 1e-9) {
+      best_cost = cost;
+      best = ks;
+    }
+  }
+  return best;
+}
+
+static bool is_f(int dt) { return dt == RXW8_F32 || dt == RXW8_BF16; }
+
+// Runs y[M, N] = linear(x[M, K]) on the GEMV kernel in chunks of <= 64 rows.
+static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf16,
+                    const float *scale, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
+                    int64_t G) {
+  const int64_t unit = w_bf16 ? 32 : 64;
+  const int ks = choose_ksplit(rt, N, K, G, unit);
+  const int64_t tiles = (N + 63) / 64;
+  const int64_t mchunk = 64;
+  const size_t xe = x_f32 ? 4 : 2, ye = y_f32 ? 4 : 2;
+  if (ks > 1) {
+    int rc = ensure_workspace(rt, rt->partials, (size_t)ks * mchunk * N * sizeof(float), false);
+    if (rc) return rc;
+    rc = ensure_workspace(rt, rt->counters, (size_t)tiles * sizeof(unsigned), true);
+    if (rc) return rc;
+  }
+  for (int64_t m0 = 0; m0 < M; m0 += mchunk) {
+    const int64_t mm = M - m0 < mchunk ? M - m0 : mchunk;
+    GemvArgs a;
+    a.x = (const char *)x + m0 * K * xe;
+    a.w = w;
+    a.scale = scale;
+    a.y = (char *)y + m0 * N * ye;
+    a.ws = (float *)rt->partials.ptr;
+    a.counters = (unsigned *)rt->counters.ptr;
+    a.M = (int)mm;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.G = (int)G;
+    a.ksplit = ks;
+    a.x_f32 = x_f32;
+    a.y_f32 = y_f32;
+    const int mb = mm <= 16 ? 1 : (mm <= 32 ? 2 : 4);
+    char kname[64];
+    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s_mb%d", w_bf16 ? "bf16" : "w8", mb);
+    int rc = launch(rt, kname, dim3((unsigned)(tiles * ks)), dim3(256), a);
+    if (rc) return rc;
+  }
+  return RXW8_OK;
+}
+
+static int run_generic_linear(Runtime *rt, const void *x, int x_f32, const void *w, int w_kind,
+                              const float *scale, void *y, int y_f32, int64_t M, int64_t N,
+                              int64_t K, int64_t G, int compute_bf16) {
+  GenericLinearArgs a;
+  a.x = x;
+  a.w = w;
+  a.scale = scale;
+  a.y = y;
+  a.m = M;
+  a.n = N;
+  a.k = K;
+  a.g = G;
+  a.x_f32 = x_f32;
+  a.y_f32 = y_f32;
+  a.compute_bf16 = compute_bf16;
+  a.w_kind = w_kind;
+  return launch(rt, "rxw8_linear_generic", dim3(grid_for(M * N)), dim3(256), a);
+}
+
+// Shared validation of QuantizedLinear operands; fills M, N, K, G.
+static int check_qlinear(const Buffer *x, const Buffer *w, const Buffer *s, int compute,
+                         int64_t *M, int64_t *N, int64_t *K, int64_t *G) {
+  if (!x || !w || !s) return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear: NULL buffer");
+  if (x->rt != w->rt || x->rt != s->rt)
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear: buffers belong to different runtimes");
+  if (compute != RXW8_BF16 && compute != RXW8_F32)
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear: compute dtype must be BF16 or F32");
+  if (x->rank < 1 || !is_f(x->dtype))
+    return fail(RXW8_INVALID_ARGUMENT,
+                "QuantizedLinear requires an F32 (or bf16-valued BF16) input with rank at least one");
+  if (compute == RXW8_F32 && x->dtype != RXW8_F32)
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear: F32 compute requires an F32 input");
+  if (w->dtype != RXW8_U8 || w->rank != 2)
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear weight: dtype does not match the schema (U8 [out, in])");
+  if (s->dtype != RXW8_F32 || s->rank != 2)
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear scale: dtype does not match the schema (F32 [out, groups])");
+  *K = x->dims[x->rank - 1];
+  *N = w->dims[0];
+  const int64_t groups = s->dims[1];
+  if (*N <= 0 || *K <= 0 || groups <= 0 || *K % groups != 0)
+    return fail(RXW8_INVALID_ARGUMENT,
+                "QuantizedLinear requires positive widths and a group size dividing the input width");
+  if (w->dims[1] != *K)
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear weight %s: shape does not match input width %lld",
+                dims_str(w).c_str(), (long long)*K);
+  if (s->dims[0] != *N)
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear scale %s: shape does not match weight %s",
+                dims_str(s).c_str(), dims_str(w).c_str());
+  *G = *K / groups;
+  *M = 1;
+  for (int i = 0; i < x->rank - 1; ++i) *M *= x->dims[i];
+  return RXW8_OK;
+}
+
+int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, const float *s,
+                   void *y, int y_f32, int64_t M, int64_t N, int64_t K, int64_t G,
+                   int compute_bf16);
+
+}  // namespace rxw8
+
+using namespace rxw8;
+
+namespace rxw8 {
+
+int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, const float *s,
+                   void *y, int y_f32, int64_t M, int64_t N, int64_t K, int64_t G,
+                   int compute_bf16) {
+  if (M == 0) return RXW8_OK;
+  const bool mfma_ok = compute_bf16 && K % 64 == 0 && N % 16 == 0 && (G == K || G % 64 == 0) &&
+                       K <= (1LL << 30) && N <= (1LL << 30) && !env_int("RXW8_FORCE_GENERIC", 0);
+  if (mfma_ok) {
+    const bool gemm_ok = M > 64 && N % 256 == 0 && K % 64 == 0 && (G == K || G % 64 == 0) &&
+                         rt->fn("rxw8_w8a16_gemm") && !env_int("RXW8_NO_GEMM", 0);
+    if (gemm_ok) {
+      GemmArgs a;
+      a.x = x;
+      a.w = w;
+      a.scale = s;
+      a.y = y;
+      a.M = (int)M;
+      a.N = (int)N;
+      a.K = (int)K;
+      a.G = (int)G;
+      a.x_f32 = x_f32;
+      a.y_f32 = y_f32;
+      const unsigned mt = (unsigned)((M + 255) / 256), nt = (unsigned)(N / 256);
+      return launch(rt, "rxw8_w8a16_gemm", dim3(mt * nt), dim3(256), a);
+    }
+    return run_gemv(rt, x, x_f32, w, false, s, y, y_f32, M, N, K, G);
+  }
+  return run_generic_linear(rt, x, x_f32, w, 0, s, y, y_f32, M, N, K, G, compute_bf16);
+}
+
+int bf16_linear_launch(Runtime *rt, const void *x, int x_f32, const uint16_t *w, void *y,
+                       int y_f32, int64_t M, int64_t N, int64_t K) {
+  if (M == 0) return RXW8_OK;
+  if (K % 32 == 0 && N % 16 == 0 && !env_int("RXW8_FORCE_GENERIC", 0))
+    return run_gemv(rt, x, x_f32, w, true, nullptr, y, y_f32, M, N, K, K);
+  return run_generic_linear(rt, x, x_f32, w, 1, nullptr, y, y_f32, M, N, K, K, 1);
+}
+
+int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
+                     int cache_f32, const int32_t *lens, const float *mask, int64_t mask_sb,
+                     int64_t mask_sh, void *out, int out_f32, int64_t B, int64_t Hq,
+                     int64_t Hkv, int64_t Lmax, int64_t D, float scale) {
+  if (B == 0) return RXW8_OK;
+  const int64_t G = Hq / Hkv;
+  const bool fast = !cache_f32 && D == 128 && (G == 1 || G == 2 || G == 4 || G == 8) &&
+                    !env_int("RXW8_FORCE_GENERIC", 0);
+  if (fast) {
+    const int64_t KC = 256;
+    const int64_t max_chunks = (Lmax + KC - 1) / KC;
+    int rc = ensure_workspace(rt, rt->scratch,
+                              (size_t)B * Hkv * max_chunks * G * (2 + D) * sizeof(float), false);
+    if (rc) return rc;
+    // attention counters live after the GEMV counters region
+    rc = ensure_workspace(rt, rt->counters, (size_t)(B * Hkv + 65536) * sizeof(unsigned), true);
+    if (rc) return rc;
+    AttnArgs a;
+    a.q = q;
+    a.kc = (const uint16_t *)kc;
+    a.vc = (const uint16_t *)vc;
+    a.lens = lens;
+    a.mask = mask;
+    a.out = out;
+    a.ws = (float *)rt->scratch.ptr;
+    a.counters = (unsigned *)rt->counters.ptr + 65536;
+    a.mask_sb = mask_sb;
+    a.mask_sh = mask_sh;
+    a.B = (int)B;
+    a.Hq = (int)Hq;
+    a.Hkv = (int)Hkv;
+    a.Lmax = (int)Lmax;
+    a.max_chunks = (int)max_chunks;
+    a.scale = scale;
+    a.q_f32 = q_f32;
+    a.out_f32 = out_f32;
+    char kname[64];
+    std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_d128_g%d", (int)G);
+    return launch(rt, kname, dim3((unsigned)(B * Hkv * max_chunks)), dim3(256), a);
+  }
+  if (Lmax > 8192)
+    return fail(RXW8_UNIMPLEMENTED, "decode attention: the generic kernel supports Lmax <= 8192");
+  AttnGenericArgs a;
+  a.q = q;
+  a.kc = kc;
+  a.vc = vc;
+  a.lens = lens;
+  a.mask = mask;
+  a.out = out;
+  a.mask_sb = mask_sb;
+  a.mask_sh = mask_sh;
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.Lmax = (int)Lmax;
+  a.D = (int)D;
+  a.scale = scale;
+  a.q_f32 = q_f32;
+  a.cache_f32 = cache_f32;
+  a.out_f32 = out_f32;
+  return launch(rt, "rxw8_gqa_decode_generic", dim3((unsigned)(B * Hq)), dim3(256), a);
+}
+
+}  // namespace rxw8
+
+extern "C" {
+
+int rxw8_dequantize(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer *scale, int out_dtype,
+                    rxw8_buffer **out) {
+  if (!rt || !weight || !scale || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if (weight->dtype != RXW8_U8 || weight->rank != 2)
+    return fail(RXW8_INVALID_ARGUMENT, "dequantize: weight must be U8 [out, in]");
+  if (scale->dtype != RXW8_F32 || scale->rank != 2 || scale->dims[0] != weight->dims[0])
+    return fail(RXW8_INVALID_ARGUMENT, "dequantize: scale must be F32 [out, groups]");
+  if (out_dtype != RXW8_F32 && out_dtype != RXW8_BF16)
+    return fail(RXW8_INVALID_ARGUMENT, "dequantize: out dtype must be F32 or BF16");
+  const int64_t n = weight->dims[0], k = weight->dims[1], groups = scale->dims[1];
+  if (n <= 0 || k <= 0 || groups <= 0 || k % groups)
+    return fail(RXW8_INVALID_ARGUMENT, "dequantize: group count must divide the input width");
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  Buffer *o = nullptr;
+  int rc = new_buffer(rt, out_dtype, weight->dims, 2, false, &o);
+  if (rc) return rc;
+  DequantArgs a;
+  a.w = (const uint8_t *)weight->ptr;
+  a.scale = (const float *)scale->ptr;
+  a.out = o->ptr;
+  a.n = n;
+  a.k = k;
+  a.g = k / groups;
+  a.out_bf16 = out_dtype == RXW8_BF16;
+  rc = launch(rt, "rxw8_dequant", dim3(grid_for(n * k, 256, 1 << 14)), dim3(256), a);
+  if (rc) {
+    rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+    return rc;
+  }
+  *out = static_cast<rxw8_buffer *>(o);
+  return RXW8_OK;
+}
+
+int rxw8_quantized_linear_into(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
+                               rxw8_buffer *scale, int compute_dtype, rxw8_buffer *y) {
+  if (!rt || !y) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  int64_t M, N, K, G;
+  int rc = check_qlinear(x, weight, scale, compute_dtype, &M, &N, &K, &G);
+  if (rc) return rc;
+  if (!is_f(y->dtype) || (compute_dtype == RXW8_F32 && y->dtype != RXW8_F32))
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear output: dtype does not match the schema");
+  bool shape_ok = y->rank == x->rank && y->dims[y->rank - 1] == N;
+  for (int i = 0; shape_ok && i < x->rank - 1; ++i) shape_ok = y->dims[i] == x->dims[i];
+  if (!shape_ok)
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear output %s: shape does not match the schema",
+                dims_str(y).c_str());
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  return qlinear_launch(rt, x->ptr, x->dtype == RXW8_F32, (const uint8_t *)weight->ptr,
+                        (const float *)scale->ptr, y->ptr, y->dtype == RXW8_F32, M, N, K, G,
+                        compute_dtype == RXW8_BF16);
+}
+
+int rxw8_quantized_linear(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
+                          rxw8_buffer *scale, int compute_dtype, int out_dtype,
+                          rxw8_buffer **y) {
+  if (!rt || !y) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  int64_t M, N, K, G;
+  int rc = check_qlinear(x, weight, scale, compute_dtype, &M, &N, &K, &G);
+  if (rc) return rc;
+  if (!is_f(out_dtype) || (compute_dtype == RXW8_F32 && out_dtype != RXW8_F32))
+    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear: out dtype must be F32 (or BF16 with BF16 compute)");
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  int64_t dims[RXW8_MAX_RANK];
+  for (int i = 0; i < x->rank; ++i) dims[i] = x->dims[i];
+  dims[x->rank - 1] = N;
+  Buffer *o = nullptr;
+  rc = new_buffer(rt, out_dtype, dims, x->rank, false, &o);
+  if (rc) return rc;
+  rc = rxw8_quantized_linear_into(rt, x, weight, scale, compute_dtype, static_cast<rxw8_buffer *>(o));
+  if (rc) {
+    rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+    return rc;
+  }
+  *y = static_cast<rxw8_buffer *>(o);
+  return RXW8_OK;
+}
+
+static int check_bf16_linear(const Buffer *x, const Buffer *w, int64_t *M, int64_t *N, int64_t *K) {
+  if (!x || !w) return fail(RXW8_INVALID_ARGUMENT, "Linear: NULL buffer");
+  if (x->rt != w->rt) return fail(RXW8_INVALID_ARGUMENT, "Linear: buffers belong to different runtimes");
+  if (x->rank < 1 || !is_f(x->dtype))
+    return fail(RXW8_INVALID_ARGUMENT, "Linear requires an F32 or BF16 input with rank at least one");
+  if (w->dtype != RXW8_BF16 || w->rank != 2)
+    return fail(RXW8_INVALID_ARGUMENT, "Linear weight: dtype does not match the schema (BF16 [out, in])");
+  *K = x->dims[x->rank - 1];
+  *N = w->dims[0];
+  if (*K <= 0 || *N <= 0 || w->dims[1] != *K)
+    return fail(RXW8_INVALID_ARGUMENT, "Linear weight %s: shape does not match input width %lld",
+                dims_str(w).c_str(), (long long)*K);
+  *M = 1;
+  for (int i = 0; i < x->rank - 1; ++i) *M *= x->dims[i];
+  return RXW8_OK;
+}
+
+int rxw8_linear_bf16_into(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight, rxw8_buffer *y) {
+  if (!rt || !y) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  int64_t M, N, K;
+  int rc = check_bf16_linear(x, weight, &M, &N, &K);
+  if (rc) return rc;
+  bool shape_ok = is_f(y->dtype) && y->rank == x->rank && y->dims[y->rank - 1] == N;
+  for (int i = 0; shape_ok && i < x->rank - 1; ++i) shape_ok = y->dims[i] == x->dims[i];
+  if (!shape_ok) return fail(RXW8_INVALID_ARGUMENT, "Linear output: shape or dtype mismatch");
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  return bf16_linear_launch(rt, x->ptr, x->dtype == RXW8_F32, (const uint16_t *)weight->ptr,
+                            y->ptr, y->dtype == RXW8_F32, M, N, K);
+}
+
+int rxw8_linear_bf16(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight, int out_dtype,
+                     rxw8_buffer **y) {
+  if (!rt || !y) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  int64_t M, N, K;
+  int rc = check_bf16_linear(x, weight, &M, &N, &K);
+  if (rc) return rc;
+  if (!is_f(out_dtype)) return fail(RXW8_INVALID_ARGUMENT, "Linear: out dtype must be F32 or BF16");
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  int64_t dims[RXW8_MAX_RANK];
+  for (int i = 0; i < x->rank; ++i) dims[i] = x->dims[i];
+  dims[x->rank - 1] = N;
+  Buffer *o = nullptr;
+  rc = new_buffer(rt, out_dtype, dims, x->rank, false, &o);
+  if (rc) return rc;
+  rc = rxw8_linear_bf16_into(rt, x, weight, static_cast<rxw8_buffer *>(o));
+  if (rc) {
+    rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+    return rc;
+  }
+  *y = static_cast<rxw8_buffer *>(o);
+  return RXW8_OK;
+}
+
+static int check_gqa(const Buffer *q, const Buffer *k, const Buffer *v, const Buffer *lens,
+                     const Buffer *mask, int64_t *mask_sb, int64_t *mask_sh) {
+  if (!q || !k || !v || !lens) return fail(RXW8_INVALID_ARGUMENT, "GQA: NULL buffer");
+  if (q->rank != 3 || k->rank != 4 || v->rank != 4)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA decode requires q [B,Hq,D] and caches [B,Hkv,Lmax,D]");
+  if (!is_f(q->dtype) || !is_f(k->dtype) || k->dtype != v->dtype)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA decode requires F32/BF16 q and matching F32/BF16 caches");
+  const int64_t B = q->dims[0], Hq = q->dims[1], D = q->dims[2];
+  for (int i = 0; i < 4; ++i)
+    if (k->dims[i] != v->dims[i])
+      return fail(RXW8_INVALID_ARGUMENT, "GQA: K/V caches must have equal shapes");
+  if (k->dims[0] != B || Hq <= 0 || k->dims[1] <= 0 || Hq % k->dims[1] != 0 || k->dims[3] != D ||
+      D <= 0 || k->dims[2] <= 0)
+    return fail(RXW8_INVALID_ARGUMENT,
+                "GQA requires equal batch prefixes and divisible positive head counts");
+  if (lens->dtype != RXW8_I32 || lens->rank != 1 || lens->dims[0] != B)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA: lens must be I32 [B]");
+  *mask_sb = *mask_sh = 0;
+  if (mask) {
+    const int64_t L = k->dims[2];
+    if (mask->dtype != RXW8_F32 || mask->rank != 3 || mask->dims[2] != L ||
+        (mask->dims[0] != 1 && mask->dims[0] != B) || (mask->dims[1] != 1 && mask->dims[1] != Hq))
+      return fail(RXW8_INVALID_ARGUMENT, "GQA: mask must be F32 [B|1, Hq|1, Lmax]");
+    *mask_sh = mask->dims[1] == 1 ? 0 : L;
+    *mask_sb = mask->dims[0] == 1 ? 0 : mask->dims[1] * L;
+  }
+  return RXW8_OK;
+}
+
+int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
+                         rxw8_buffer *v_cache, rxw8_buffer *lens, rxw8_buffer *mask, float scale,
+                         rxw8_buffer *out) {
+  if (!rt || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  int64_t sb, sh;
+  int rc = check_gqa(q, k_cache, v_cache, lens, mask, &sb, &sh);
+  if (rc) return rc;
+  if (!is_f(out->dtype) || out->rank != 3 || out->dims[0] != q->dims[0] ||
+      out->dims[1] != q->dims[1] || out->dims[2] != q->dims[2])
+    return fail(RXW8_INVALID_ARGUMENT, "GQA output: shape or dtype mismatch");
+  if (!std::isfinite(scale)) return fail(RXW8_INVALID_ARGUMENT, "attention scale must be finite");
+  const int64_t D = q->dims[2];
+  if (scale <= 0.f) scale = 1.0f / std::sqrt((float)D);
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  return attention_launch(rt, q->ptr, q->dtype == RXW8_F32, k_cache->ptr, v_cache->ptr,
+                          k_cache->dtype == RXW8_F32, (const int32_t *)lens->ptr,
+                          mask ? (const float *)mask->ptr : nullptr, sb, sh, out->ptr,
+                          out->dtype == RXW8_F32, q->dims[0], q->dims[1], k_cache->dims[1],
+                          k_cache->dims[2], D, scale);
+}
+
+int rxw8_gqa_decode(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache, rxw8_buffer *v_cache,
+                    rxw8_buffer *lens, rxw8_buffer *mask, float scale, int out_dtype,
+                    rxw8_buffer **out) {
+  if (!rt || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  int64_t sb, sh;
+  int rc = check_gqa(q, k_cache, v_cache, lens, mask, &sb, &sh);
+  if (rc) return rc;
+  if (!is_f(out_dtype)) return fail(RXW8_INVALID_ARGUMENT, "GQA: out dtype must be F32 or BF16");
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  Buffer *o = nullptr;
+  rc = new_buffer(rt, out_dtype, q->dims, 3, false, &o);
+  if (rc) return rc;
+  rc = rxw8_gqa_decode_into(rt, q, k_cache, v_cache, lens, mask, scale, static_cast<rxw8_buffer *>(o));
+  if (rc) {
+    rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+    return rc;
+  }
+  *out = static_cast<rxw8_buffer *>(o);
+  return RXW8_OK;
+}
+
+int rxw8_kv_update_at(rxw8_runtime *rt, rxw8_buffer *k_cache, rxw8_buffer *v_cache,
+                      rxw8_buffer *k_update, rxw8_buffer *v_update, rxw8_buffer *starts,
+                      int checked, rxw8_buffer *accepted) {
+  if (!rt || !k_cache || !v_cache || !k_update || !v_update || !starts)
+    return fail(RXW8_INVALID_ARGUMENT, "KvCache::update_at: NULL argument");
+  if (k_update->rank != v_update->rank || k_update->dtype != v_update->dtype)
+    return fail(RXW8_INVALID_ARGUMENT, "K/V updates must have equal shapes");
+  for (int i = 0; i < k_update->rank; ++i)
+    if (k_update->dims[i] != v_update->dims[i])
+      return fail(RXW8_INVALID_ARGUMENT, "K/V updates must have equal shapes");
+  const int rank = k_cache->rank;
+  if (rank < 1 || rank > 8 || v_cache->rank != rank || k_update->rank != rank)
+    return fail(RXW8_INVALID_ARGUMENT, "KvCache::update_at: cache and update ranks must match (1..8)");
+  if (k_cache->dtype != v_cache->dtype || k_update->dtype != k_cache->dtype)
+    return fail(RXW8_INVALID_ARGUMENT, "KvCache::update_at: cache/update dtypes must match");
+  for (int i = 0; i < rank; ++i) {
+    if (k_cache->dims[i] != v_cache->dims[i])
+      return fail(RXW8_INVALID_ARGUMENT, "KvCache::update_at: K/V caches must have equal shapes");
+    if (k_update->dims[i] > k_cache->dims[i])
+      return fail(RXW8_INVALID_ARGUMENT, "KvCache::update_at: update larger than the cache");
+  }
+  if (starts->dtype != RXW8_I32 || starts->rank != 1 || starts->dims[0] != rank)
+    return fail(RXW8_INVALID_ARGUMENT, "KvCache::update_at: starts must be I32 [rank]");
+  if (accepted && (accepted->dtype != RXW8_F32 || accepted->numel() != 1))
+    return fail(RXW8_INVALID_ARGUMENT, "KvCache::update_at: accepted must be an F32 scalar");
+  if (k_cache == v_cache) return fail(RXW8_INVALID_ARGUMENT, "K and V caches must be distinct buffers");
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  KvUpdateArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.kc = k_cache->ptr;
+  a.vc = v_cache->ptr;
+  a.ku = k_update->ptr;
+  a.vu = v_update->ptr;
+  a.starts = (const int32_t *)starts->ptr;
+  a.accepted = accepted ? (float *)accepted->ptr : nullptr;
+  for (int i = 0; i < rank; ++i) {
+    a.dims[i] = k_cache->dims[i];
+    a.udims[i] = k_update->dims[i];
+  }
+  a.total = k_update->numel();
+  a.rank = rank;
+  a.elem = (int)dtype_size(k_cache->dtype);
+  a.checked = checked ? 1 : 0;
+  return launch(rt, "rxw8_kv_update", dim3(grid_for(a.total, 256, 4096)), dim3(256), a);
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol that
+include/rxw8.h declares, and reports errors with the PJRT numbering -- all
+without a GPU (no compute call is made)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "rxw8.h")
+LIB = os.path.join(ROOT, "rxla_amd", "librxw8.so")
+
+
+def _ensure_built():
+    if not os.path.exists(LIB):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "rxla_amd", "csrc")], check=True)
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rxw8_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_op_surface():
+    syms = declared_symbols()
+    for name in ("rxw8_quantized_linear", "rxw8_gqa_decode", "rxw8_kv_update_at",
+                 "rxw8_decoder_bind_parameter", "rxw8_decoder_forward", "rxw8_dequantize"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    _ensure_built()
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (rxw8_\w+)", out))
+    missing = [s for s in declared_symbols() if s not in exported]
+    assert not missing, missing
+    import rxla_amd._ffi as ffi
+    assert sorted(ffi.EXPORTS) == declared_symbols()
+
+
+def test_library_has_no_cpu_compute_path():
+    """The product library must not link the oracle or carry a CPU fallback."""
+    _ensure_built()
+    out = subprocess.run(["nm", "-D", LIB], capture_output=True, text=True, check=True).stdout
+    assert "rxo_" not in out
+    needed = subprocess.run(["readelf", "-d", LIB], capture_output=True, text=True).stdout
+    assert "librxw8_oracle" not in needed and "libamdhip64" in needed
+
+
+def test_status_codes_and_errors_without_gpu():
+    _ensure_built()
+    import rxla_amd as rx
+
+    lib = rx._lib
+    assert lib.rxw8_abi_version() == 1
+    assert [int(s) for s in rx.Status][:4] == [0, 1, 2, 3]
+    assert rx.Status.UNAUTHENTICATED == 16
+    retry = {s for s in rx.Status if lib.rxw8_status_is_retryable(int(s))}
+    assert retry == {rx.Status.CANCELLED, rx.Status.DEADLINE_EXCEEDED,
+                     rx.Status.RESOURCE_EXHAUSTED, rx.Status.ABORTED, rx.Status.UNAVAILABLE}
+    # NULL handles are rejected before anything touches a device
+    assert lib.rxw8_runtime_create(0, None) == rx.Status.INVALID_ARGUMENT
+    assert b"NULL" in lib.rxw8_last_error()
+    assert lib.rxw8_buffer_release(None) == rx.Status.INVALID_ARGUMENT
+    assert lib.rxw8_quantized_linear(None, None, None, None, 4, 5, None) == rx.Status.INVALID_ARGUMENT
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is present")
+def test_runtime_create_without_device_is_failed_precondition():
+    _ensure_built()
+    import rxla_amd as rx
+
+    with pytest.raises(rx.Error) as e:
+        rx.Runtime(0)
+    assert e.value.code == rx.Status.FAILED_PRECONDITION
+    assert not e.value.is_retryable

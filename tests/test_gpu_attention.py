@@ -1,0 +1,173 @@
+"""GPU parity for GQA decode attention (K3) and the paired KV update, against
+the CPU oracle and the reference's golden vectors, through the C ABI."""
+import json
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import golden_json, golden_npz, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def rx():
+    import rxla_amd
+    return rxla_amd
+
+
+def run_gqa(rt, q, kc_bits, vc_bits, lens, mask=None, q_bf16=False, out_bf16=False):
+    r = rx()
+    qb = rt.buffer(oracle.bf16_bits(q), r.DType.BF16) if q_bf16 else rt.buffer(q)
+    out = r.grouped_query_attention(
+        rt, qb, rt.buffer(kc_bits, r.DType.BF16), rt.buffer(vc_bits, r.DType.BF16),
+        rt.buffer(np.asarray(lens, np.int32)), rt.buffer(mask) if mask is not None else None,
+        out_dtype=r.DType.BF16 if out_bf16 else r.DType.F32).to_numpy()
+    return r.bf16_to_f32(out) if out_bf16 else out
+
+
+def test_c4_ragged_decode_full_size(rt):
+    # B=8, 32 q / 8 kv heads, D=128, bf16 q/K/V ~N(0,1), lens ~U[512,8192]
+    rng = np.random.default_rng(40)
+    b, hq, hkv, lmax, d = 8, 32, 8, 8192, 128
+    lens = rng.integers(512, 8193, b).astype(np.int32)
+    q = oracle.round_bf16(rng.standard_normal((b, hq, d)).astype(np.float32))
+    kc = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    vc = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    ref = oracle.gqa_decode_bf16cache(q, kc, vc, lens, threads=16)
+    out = run_gqa(rt, q, kc, vc, lens, q_bf16=True)
+    err = rel_err(out, ref)
+    print(f"C4 lens={lens.tolist()} rel_err={err:.3e}")
+    assert err <= 1e-2
+    assert err <= 1e-4  # f32 softmax semantics: far inside the bf16 bar
+    out16 = run_gqa(rt, q, kc, vc, lens, q_bf16=True, out_bf16=True)
+    assert rel_err(out16, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+@pytest.mark.parametrize("lens", [[1, 2, 255, 256], [257, 511, 512, 513], [1000, 1, 64, 1023]])
+def test_edge_lengths_and_groups(rt, group, lens):
+    rng = np.random.default_rng(group * 100 + lens[0])
+    b, hkv, lmax, d = 4, 2, 1023, 128
+    hq = hkv * group
+    q = rng.standard_normal((b, hq, d)).astype(np.float32)
+    kc = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    vc = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    ref = oracle.gqa_decode_bf16cache(q, kc, vc, np.array(lens, np.int32))
+    assert rel_err(run_gqa(rt, q, kc, vc, lens), ref) <= 1e-4
+
+
+def test_keys_beyond_length_are_never_read(rt):
+    rng = np.random.default_rng(41)
+    b, hq, hkv, lmax, d = 2, 8, 2, 600, 128
+    lens = np.array([300, 513], np.int32)
+    q = rng.standard_normal((b, hq, d)).astype(np.float32)
+    k = rng.standard_normal((b, hkv, lmax, d)).astype(np.float32)
+    v = rng.standard_normal((b, hkv, lmax, d)).astype(np.float32)
+    for bi in range(b):
+        k[bi, :, lens[bi]:] = np.nan
+        v[bi, :, lens[bi]:] = np.inf
+    kc, vc = oracle.bf16_bits(k), oracle.bf16_bits(v)
+    out = run_gqa(rt, q, kc, vc, lens)
+    assert np.all(np.isfinite(out))
+    assert rel_err(out, oracle.gqa_decode_bf16cache(q, kc, vc, lens)) <= 1e-4
+
+
+def test_additive_mask(rt):
+    r = rx()
+    rng = np.random.default_rng(42)
+    b, hq, hkv, lmax, d = 2, 8, 2, 300, 128
+    lens = np.array([300, 200], np.int32)
+    q = rng.standard_normal((b, hq, d)).astype(np.float32)
+    kc = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    vc = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    mask = (rng.standard_normal((1, hq, lmax)) * 0.5).astype(np.float32)
+    mask[0, :, ::7] = -np.inf
+    out = run_gqa(rt, q, kc, vc, lens, mask=mask)
+    vis = np.where(np.arange(lmax)[None, :] < lens[:, None], 0.0, -np.inf).astype(np.float32)
+    full = mask[0][None, :, None, :] + vis[:, None, None, :]
+    ref = oracle.gqa_attention(q[:, :, None, :], oracle.bf16_to_f32(kc), oracle.bf16_to_f32(vc),
+                               full)[:, :, 0, :]
+    assert rel_err(out, ref) <= 1e-4
+
+
+def test_generic_kernel_shapes(rt):
+    """D != 128 and f32 caches take the generic kernel."""
+    r = rx()
+    rng = np.random.default_rng(43)
+    b, hq, hkv, lmax, d = 3, 6, 2, 70, 64
+    lens = np.array([70, 1, 33], np.int32)
+    q = rng.standard_normal((b, hq, d)).astype(np.float32)
+    k = rng.standard_normal((b, hkv, lmax, d)).astype(np.float32)
+    v = rng.standard_normal((b, hkv, lmax, d)).astype(np.float32)
+    mask = np.where(np.arange(lmax)[None, :] < lens[:, None], 0.0, -np.inf).astype(np.float32)
+    ref = oracle.gqa_attention(q[:, :, None, :], k, v, mask[:, None, None, :])[:, :, 0, :]
+    out = r.grouped_query_attention(rt, rt.buffer(q), rt.buffer(k), rt.buffer(v),
+                                    rt.buffer(lens)).to_numpy()
+    assert rel_err(out, ref) <= 1e-5
+
+
+def test_reference_masked_decode_steps_on_gpu(rt):
+    """crates/rxla-core/tests/masked_decode.rs:54-142 through KvCache +
+    grouped_query_attention on the GPU (f32 caches; 2e-6 like the reference)."""
+    r = rx()
+    g = golden_npz("masked_decode.npz")
+    cache = r.KvCache(rt, None, keys=rt.buffer(np.full((1, 2, 4, 2), g["init_k"], np.float32)),
+                      values=rt.buffer(np.full((1, 2, 4, 2), g["init_v"], np.float32)))
+    for step in range(4):
+        cache.update_at(rt.buffer(g["k"][step][None]), rt.buffer(g["v"][step][None]),
+                        [0, 0, step, 0])
+        q = g["q"][step][:, 0, :][None]  # [1, 2 heads, 2 dims]
+        out = r.grouped_query_attention(rt, rt.buffer(q), cache.keys, cache.values,
+                                        rt.buffer(np.array([step + 1], np.int32))).to_numpy()
+        assert np.max(np.abs(out[0] - g["expected"][step])) < 2e-6
+
+
+def test_kv_update_clamps_like_reference(rt):
+    r = rx()
+    t = golden_json("kv_clamp.json")
+    cache = r.KvCache(rt, t["shape"], r.DType.F32)
+    for pos, k, v in t["steps"]:
+        cache.update_at(rt.buffer(np.full(t["update_shape"], k, np.float32)),
+                        rt.buffer(np.full(t["update_shape"], v, np.float32)), [pos, 0])
+    np.testing.assert_array_equal(cache.keys.to_numpy().ravel(), t["expected_keys"])
+    np.testing.assert_array_equal(cache.values.to_numpy().ravel(), t["expected_values"])
+
+
+def test_kv_update_checked_table(rt):
+    r = rx()
+    t = golden_json("kv_checked.json")
+    cache = r.KvCache(rt, t["shape"], r.DType.F32)
+    for st in t["steps"]:
+        keys = np.array([np.nan if x is None else x for x in st["keys"]], np.float32)
+        acc = cache.update_at_checked(rt.buffer(keys.reshape(2, 2)),
+                                      rt.buffer(np.array(st["values"], np.float32).reshape(2, 2)),
+                                      [st["row"], st["col"]])
+        assert float(acc.to_numpy()) == st["accepted"]
+        np.testing.assert_array_equal(cache.keys.to_numpy().ravel(), st["expected_keys"])
+        np.testing.assert_array_equal(cache.values.to_numpy().ravel(), st["expected_values"])
+
+
+def test_kv_update_rank4_bf16_matches_oracle(rt):
+    r = rx()
+    rng = np.random.default_rng(44)
+    shape, ushape = (8, 8, 64, 128), (8, 8, 1, 128)
+    k0 = rng.integers(0, 65535, shape).astype(np.uint16)
+    v0 = rng.integers(0, 65535, shape).astype(np.uint16)
+    cache = r.KvCache(rt, None, keys=rt.buffer(k0, r.DType.BF16), values=rt.buffer(v0, r.DType.BF16))
+    ku = rng.integers(0, 65535, ushape).astype(np.uint16)
+    vu = rng.integers(0, 65535, ushape).astype(np.uint16)
+    for starts in ([0, 0, 17, 0], [0, 0, 63, 0], [0, 0, 99, 5], [-2, 1, -1, 0]):
+        cache.update_at(rt.buffer(ku, r.DType.BF16), rt.buffer(vu, r.DType.BF16), starts)
+        k0, v0, _ = oracle.kv_update_at(k0, v0, ku, vu, starts)
+        np.testing.assert_array_equal(cache.keys.to_numpy(), k0)
+        np.testing.assert_array_equal(cache.values.to_numpy(), v0)
+
+
+def test_attention_validation(rt):
+    r = rx()
+    q = rt.buffer(np.zeros((2, 6, 128), np.float32))
+    kc = rt.buffer(np.zeros((2, 4, 16, 128), np.uint16), r.DType.BF16)
+    with pytest.raises(r.Error) as e:  # 6 % 4 != 0
+        r.grouped_query_attention(rt, q, kc, kc, rt.buffer(np.ones(2, np.int32)))
+    assert e.value.code == r.Status.INVALID_ARGUMENT

@@ -1,0 +1,173 @@
+"""GPU parity for the W8A16 linear (K1 GEMV, generic kernel) and dequantisation
+against the CPU oracle, through the C ABI (rxla_amd -> librxw8.so).
+
+Tolerance: max relative error <= 1e-2, measured
+normwise as max|gpu - oracle| / max|oracle|. Dequantisation is bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def rx():
+    import rxla_amd
+    return rxla_amd
+
+
+def quantized(rng, n, k, g, std=0.02):
+    w = (rng.standard_normal((n, k)) * std).astype(np.float32)
+    return oracle.quantize_w8(w, g)
+
+
+def run_linear(rt, x, u8, s, x_dtype=None, out_dtype=None, compute=None):
+    r = rx()
+    x_dtype = x_dtype or r.DType.F32
+    out_dtype = out_dtype or r.DType.F32
+    compute = compute or r.DType.BF16
+    xb = rt.buffer(oracle.bf16_bits(x) if x_dtype == r.DType.BF16 else x, x_dtype)
+    y = r.quantized_linear(rt, xb, rt.buffer(u8, r.DType.U8), rt.buffer(s, r.DType.F32),
+                           compute, out_dtype).to_numpy()
+    return r.bf16_to_f32(y) if out_dtype == r.DType.BF16 else y
+
+
+def test_c1_single_linear_f32_boundary(rt):
+    # x f32 [8,1024] ~N(0,1); W [1024,1024] ~N(0,0.02), per-channel, seed 0
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((8, 1024)).astype(np.float32)
+    u8, s = quantized(rng, 1024, 1024, 1024)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16)
+    y = run_linear(rt, x, u8, s)
+    print(f"C1 rel_err={rel_err(y, ref):.3e}")
+    assert rel_err(y, ref) <= TOL
+    np.testing.assert_array_equal(oracle.round_bf16(y), y)  # bf16-valued, like the reference
+
+
+@pytest.mark.parametrize("n", [4096, 6144, 24576])
+@pytest.mark.parametrize("b", [1, 4, 16])
+def test_c2_decode_gemv_sweep(rt, b, n):
+    rng = np.random.default_rng(1000 + 10 * b + n)
+    x = oracle.round_bf16(rng.standard_normal((b, 4096)).astype(np.float32))
+    u8, s = quantized(rng, n, 4096, 4096)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16, threads=16)
+    y = run_linear(rt, x, u8, s, x_dtype=rx().DType.BF16, out_dtype=rx().DType.BF16)
+    err = rel_err(y, ref)
+    print(f"C2 B={b} N={n} rel_err={err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("g", [64, 128, 512])
+def test_grouped_scales(rt, g):
+    rng = np.random.default_rng(g)
+    x = rng.standard_normal((8, 2048)).astype(np.float32)
+    u8, s = quantized(rng, 1024, 2048, g)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16)
+    err = rel_err(run_linear(rt, x, u8, s), ref)
+    print(f"G={g} rel_err={err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("m,n,k,g", [(2, 32, 64, 32), (3, 40, 96, 32), (5, 24, 64, 8),
+                                     (70, 128, 256, 256), (200, 64, 128, 64)])
+def test_other_shapes(rt, m, n, k, g):
+    """Shapes outside the MFMA tiling (generic kernel) and M > 64 (chunked)."""
+    rng = np.random.default_rng(m + n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    u8, s = quantized(rng, n, k, g)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16)
+    assert rel_err(run_linear(rt, x, u8, s), ref) <= TOL
+
+
+def test_f32_compute_path(rt):
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((4, 256)).astype(np.float32)
+    u8, s = quantized(rng, 64, 256, 128)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_F32)
+    y = run_linear(rt, x, u8, s, compute=rx().DType.F32)
+    assert rel_err(y, ref) < 1e-5
+
+
+def test_rank3_input_and_empty_batch(rt):
+    r = rx()
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 3, 512)).astype(np.float32)
+    u8, s = quantized(rng, 256, 512, 512)
+    y = run_linear(rt, x, u8, s)
+    assert y.shape == (2, 3, 256)
+    assert rel_err(y, oracle.quantized_linear(x, u8, s).reshape(2, 3, 256)) <= TOL
+    empty = rt.buffer(np.zeros((0, 512), np.float32))
+    out = r.quantized_linear(rt, empty, rt.buffer(u8), rt.buffer(s))
+    assert out.shape == (0, 256)
+
+
+def test_dequant_bit_exact_all_codes(rt):
+    r = rx()
+    codes = np.tile(np.arange(256, dtype=np.uint8), (64, 4))  # [64, 1024]
+    rng = np.random.default_rng(5)
+    for groups in (1, 8):
+        s = (np.abs(rng.standard_normal((64, groups))) * 1e-3).astype(np.float32)
+        s[0, 0] = np.float32(1e-12) / np.float32(127.0)
+        want = oracle.dequantize_w8(codes, s)
+        got = r.dequantize(rt, rt.buffer(codes), rt.buffer(s), r.DType.F32).to_numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        got16 = r.dequantize(rt, rt.buffer(codes), rt.buffer(s), r.DType.BF16).to_numpy()
+        np.testing.assert_array_equal(got16, oracle.bf16_bits(want))
+
+
+def test_gemv_codes_exact_on_integer_inputs(rt):
+    """With s = 1 and one-hot x the W8A16 result is exact, so every code
+    (0..255 -> -128..127) and the -128 fold are checked bit for bit."""
+    k = np.arange(4096)
+    codes = ((k[None, :] + 4 * np.arange(64)[:, None]) % 256).astype(np.uint8)  # [64, 4096]
+    s = np.ones((64, 1), np.float32)
+    x = np.zeros((5, 4096), np.float32)
+    for r in range(4):
+        x[r, r] = 1.0  # y[r, i] = code[i, r] - 128: r + 4 i covers all 256 codes
+    x[4, :256] = 1.0   # one full cycle: sum(-128..127) = -128
+    want = (x.astype(np.float64) @ (codes.astype(np.float64) - 128).T).astype(np.float32)
+    assert sorted(set(want[:4].ravel().tolist())) == list(range(-128, 128))
+    y = run_linear(rt, x, codes, s)
+    np.testing.assert_array_equal(y, want)
+
+
+def test_deterministic_split_k(rt):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((4, 4096)).astype(np.float32)
+    u8, s = quantized(rng, 4096, 4096, 4096)
+    a = run_linear(rt, x, u8, s)
+    b = run_linear(rt, x, u8, s)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_validation_rejects_before_launch(rt):
+    r = rx()
+    x = rt.buffer(np.zeros((2, 64), np.float32))
+    w = rt.buffer(np.zeros((32, 64), np.uint8))
+    bad_scale = rt.buffer(np.zeros((32, 3), np.float32))  # 64 % 3 != 0
+    with pytest.raises(r.Error) as e:
+        r.quantized_linear(rt, x, w, bad_scale)
+    assert e.value.code == r.Status.INVALID_ARGUMENT
+    with pytest.raises(r.Error):
+        r.quantized_linear(rt, x, rt.buffer(np.zeros((32, 64), np.float32)),
+                           rt.buffer(np.zeros((32, 1), np.float32)))
+    y = rt.buffer(np.full((2, 16), 7.0, np.float32))  # wrong width: untouched
+    with pytest.raises(r.Error):
+        r.quantized_linear(rt, x, w, rt.buffer(np.ones((32, 1), np.float32)), out=y)
+    np.testing.assert_array_equal(y.to_numpy(), 7.0)
+    with pytest.raises(r.Error):
+        r.QuantizedLinear(32, 48).apply(rt, x, w, rt.buffer(np.ones((32, 1), np.float32)))
+
+
+def test_bf16_weight_linear_lm_head(rt):
+    r = rx()
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((8, 2048)).astype(np.float32)
+    e = oracle.bf16_bits(rng.standard_normal((4096, 2048)).astype(np.float32) * 0.02)
+    ref = oracle.linear_bf16w(x, e)
+    y = r.linear_bf16(rt, rt.buffer(x), rt.buffer(e, r.DType.BF16)).to_numpy()
+    assert rel_err(y, ref) <= TOL
