@@ -3,13 +3,18 @@
 
 One step = one pass of the decode dequant-GEMV over the whole sweep
 B in {1, 4, 16} x N in {4096, 6144, 24576}, K = 4096, per-output-channel
-scales (9 launches). Every launch reads its own copy of the int8 weights
-(copies rotate, >= 6 x 143 MB of distinct weights), so the 256 MB MALL holds
-no reusable weight bytes and the figure is HBM bandwidth.
+scales (9 launches). Weights are in the tiled layout of rxw8_pack_weight
+(packed once, outside the timed region; same bytes as the row-major U8).
+Every launch reads its own copy of the int8 weights (copies rotate,
+>= 6 x 143 MB of distinct weights), so the 256 MB MALL holds no reusable
+weight bytes and the figure is HBM bandwidth.
 
-value        = sweep algorithmic bytes / wall time of the timed steps (GB/s)
-roofline     = the GEMV kernel: algorithmic bytes per launch / mean launch
-               duration from HIP events recorded on the runtime's stream
+value        = sweep algorithmic bytes / wall time of the timed steps (GB/s);
+               each step is one HIP-graph replay of the 9 launches
+roofline     = the GEMV kernel serving B <= 4 (rxw8_gemv_w8_pk_mb1_rw1_u4, 6
+               of the 9 launches): algorithmic bytes per launch / mean launch
+               duration, from HIP events on the runtime's stream around runs
+               of back-to-back launches of one shape
 cpu_baseline = the CPU oracle (reference-order restatement, OpenMP) timed on
                this host over a bounded sample of the same sweep
 
@@ -53,7 +58,7 @@ def cpu_baseline(budget_s=12.0):
           for n in NS}
     xs = {b: oracle.round_bf16(rng.standard_normal((b, K)).astype(np.float32)) for b in BS}
     total_bytes, total_t, passes = 0, 0.0, 0
-    while total_t < budget_s and passes < 8:
+    while total_t < budget_s and passes < 200:
         for n in NS:
             for b in BS:
                 u8, s = ws[n]
@@ -101,17 +106,18 @@ def main():
         ys = {(b, n): torch.empty((b, n), dtype=torch.bfloat16, device="cuda")
               for b in BS for n in NS}
     stream.synchronize()
-    wb = {n: [(rt.wrap_tensor(u), rt.wrap_tensor(s)) for u, s in weights[n]] for n in NS}
+    layout = os.environ.get("RXW8_BENCH_LAYOUT", "packed")
+    wb = {n: [((rx.pack_weight(rt, rt.wrap_tensor(u)) if layout == "packed" else rt.wrap_tensor(u)),
+               rt.wrap_tensor(s)) for u, s in weights[n]] for n in NS}
+    rt.synchronize()
     xb = {b: rt.wrap_tensor(xs[b]) for b in BS}
     yb = {k: rt.wrap_tensor(v) for k, v in ys.items()}
     plan = [(b, n) for n in NS for b in BS]
     step_bytes = sum(gemv_bytes(b, n) for b, n in plan)
-    counter = [0]
 
-    def step(events=None):
+    def launch_all(copy, events=None):
         for b, n in plan:
-            u, s = wb[n][counter[0] % args.copies]
-            counter[0] += 1
+            u, s = wb[n][copy]
             if events is not None:
                 e0 = torch.cuda.Event(enable_timing=True)
                 e1 = torch.cuda.Event(enable_timing=True)
@@ -121,26 +127,72 @@ def main():
                 e1.record(stream)
                 events.append((b, n, e0, e1))
 
-    for _ in range(args.warmup):
-        step()
+    # Eager warmup (sizes workspaces, resolves kernels), then one HIP graph per
+    # weight copy holding the 9 launches of a step.
+    for i in range(args.warmup):
+        launch_all(i % args.copies)
     torch.cuda.synchronize()
-    events = []
+    eager = {k: v.clone() for k, v in ys.items()}
+    graphs = []
+    for c in range(args.copies):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            launch_all(c)
+        graphs.append(g)
+    for i in range(args.warmup):
+        graphs[i % args.copies].replay()
+    torch.cuda.synchronize()
+    launch_all((args.warmup - 1) % args.copies)  # eager result of the last graph's copy
+    torch.cuda.synchronize()
+    ref = {k: v.clone() for k, v in ys.items()}
+    graphs[(args.warmup - 1) % args.copies].replay()
+    torch.cuda.synchronize()
+    assert all(torch.equal(ys[k], ref[k]) for k in ys), "graph replay differs from eager launch"
+
+    # Timed region: K steps = K graph replays, synchronized on both sides.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(events)
+    for i in range(args.steps):
+        graphs[i % args.copies].replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    log(f"timed {args.steps} steps in {wall:.4f} s")
+    log(f"timed {args.steps} graph steps in {wall:.4f} s")
+
+    # Kernel durations: per shape, one HIP event pair on the runtime stream
+    # around `copies` back-to-back eager launches (one per weight copy), queued
+    # behind a 1 GiB fill so the host submits them all before the GPU reaches
+    # the first event; shapes interleave so no copy is reused from the MALL.
+    spacer = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    events = []
+    rounds = max(3, args.steps // args.copies)
+    for _ in range(rounds):
+        for b, n in plan:
+            with torch.cuda.stream(stream):
+                spacer.zero_()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for c in range(args.copies):
+                u, s = wb[n][c]
+                rx.quantized_linear(rt, xb[b], u, s, rx.DType.BF16, out=yb[(b, n)])
+            e1.record(stream)
+            events.append((b, n, e0, e1))
+    torch.cuda.synchronize()
+    per_launch = lambda e0, e1: e0.elapsed_time(e1) * 1e-3 / args.copies  # noqa: E731
 
     per_shape = {}
     for b, n, e0, e1 in events:
-        per_shape.setdefault((b, n), []).append(e0.elapsed_time(e1) * 1e-3)
-    launch_bytes = [gemv_bytes(b, n) for b, n, _, _ in events]
-    launch_s = [e0.elapsed_time(e1) * 1e-3 for _, _, e0, e1 in events]
-    mean_bytes = float(np.mean(launch_bytes))
-    mean_s = float(np.mean(launch_s))
+        per_shape.setdefault((b, n), []).append(per_launch(e0, e1))
+
+    def kernel_stats(sel):
+        ev = [(b, n, e0, e1) for b, n, e0, e1 in events if sel(b)]
+        mb = float(np.mean([gemv_bytes(b, n) for b, n, _, _ in ev]))
+        ms = float(np.mean([per_launch(e0, e1) for _, _, e0, e1 in ev]))
+        return mb, ms
+
+    mean_bytes, mean_s = kernel_stats(lambda b: b <= 4)
     achieved = mean_bytes / mean_s / 1e9
+    b16_bytes, b16_s = kernel_stats(lambda b: b > 4)
     sweep = {f"B{b}_N{n}": {"us": round(float(np.median(v)) * 1e6, 2),
                             "GBs": round(gemv_bytes(b, n) / float(np.median(v)) / 1e9, 1)}
              for (b, n), v in sorted(per_shape.items())}
@@ -164,12 +216,22 @@ def main():
         "config": {"workload": "decode dequant-GEMV sweep (BASELINE configs[1])",
                    "batch": list(BS), "out_features": list(NS), "in_features": K,
                    "scales": "per-output-channel f32", "weight_copies": args.copies,
+                   "weight_layout": layout,
                    "launches_per_step": len(plan), "bytes_per_step": step_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "rxw8_gemv_w8_mb1",
+                     "kernel": "rxw8_gemv_w8_pk_mb1_rw1_u4" if layout == "packed"
+                     else "rxw8_gemv_w8_mb1_rw1_u4",
                      "mean_launch_us": round(mean_s * 1e6, 3),
-                     "mean_launch_bytes": int(mean_bytes)},
+                     "mean_launch_bytes": int(mean_bytes),
+                     "timing": "HIP event pair on the runtime stream around "
+                               f"{args.copies} back-to-back launches of one shape, divided by "
+                               f"{args.copies} (includes the inter-kernel gaps)"},
+        "roofline_b16": {"bound": "hbm", "achieved": round(b16_bytes / b16_s / 1e9, 2),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(b16_bytes / b16_s / 1e9 / HBM_PEAK_GBS, 4),
+                         "kernels": "rxw8_gemv_w8_pk_mb1_rw4_u4 + rxw8_gemv_splitk_reduce",
+                         "mean_launch_us": round(b16_s * 1e6, 3)},
         "sweep": sweep,
         "device": info,
     }

@@ -125,8 +125,19 @@ int rxw8_buffer_device_ptr(const rxw8_buffer *buf, void **ptr);
 int rxw8_dequantize(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer *scale,
                     int out_dtype, rxw8_buffer **out);
 
+/* Tiled copy of a weight for the packed GEMV kernels (no counterpart in the
+ * reference, which hands XLA row-major U8/BF16 parameters): U8 [N,K] ->
+ * U8 [N/16, K/64, 1024] and BF16 [N,K] -> BF16 [N/16, K/32, 512]. Block (t, c)
+ * holds, for lane l = 0..63, the 16 bytes of row 16t + l%16 starting at column
+ * c*kb + (l/16)*(kb/4) (kb = 64 for U8, 32 for BF16), so one wavefront load is
+ * one contiguous KiB. Requires N % 16 == 0 and K % kb == 0. The packed buffer
+ * is accepted wherever the row-major weight is (quantized_linear, linear_bf16,
+ * decoder parameters), holds the same bytes and gives the same results. */
+int rxw8_pack_weight(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer **packed);
+
 /* QuantizedLinear::apply (layers.rs:257-298) with the layer compute dtype:
- *   x [..., K] F32 or BF16; weight U8 [N,K] (int8 + 128); scale F32 [N,K/G];
+ *   x [..., K] F32 or BF16; weight U8 [N,K] (int8 + 128), or its packed form
+ *   U8 [N/16, K/64, 1024] (rxw8_pack_weight); scale F32 [N,K/G];
  *   compute_dtype BF16 (W8A16: bf16(x) . bf16 weights, f32 accumulation,
  *   bf16-rounded result) or F32 (f32 x, f32 dequantised weights).
  *   y [..., N] of out_dtype F32 or BF16 (same values: the BF16 compute result
@@ -143,7 +154,8 @@ int rxw8_quantized_linear_into(rxw8_runtime *rt, rxw8_buffer *x,
 
 /* Dense linear with BF16 weights (bf16-stored embedding reused as lm_head,
  * layers.rs Linear with parameter storage BF16, lib.rs:478-487):
- * y = bf16(bf16(x) . W^T). x [..., K] F32|BF16, weight BF16 [N,K]. */
+ * y = bf16(bf16(x) . W^T). x [..., K] F32|BF16, weight BF16 [N,K] or its
+ * packed form BF16 [N/16, K/32, 512]. */
 int rxw8_linear_bf16(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
                      int out_dtype, rxw8_buffer **y);
 int rxw8_linear_bf16_into(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,

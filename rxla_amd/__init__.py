@@ -229,6 +229,13 @@ def dequantize(rt: Runtime, weight: Buffer, scale: Buffer, out_dtype=DType.F32) 
     return Buffer(h)
 
 
+def pack_weight(rt: Runtime, weight: Buffer) -> Buffer:
+    """Tiled copy of a U8 [N,K] or BF16 [N,K] weight for the packed GEMV path."""
+    h = c_void_p()
+    _check(_lib.rxw8_pack_weight(rt.handle, weight.handle, byref(h)))
+    return Buffer(h)
+
+
 def quantized_linear(rt: Runtime, x: Buffer, weight: Buffer, scale: Buffer,
                      compute_dtype=DType.BF16, out_dtype=DType.F32, out: Buffer | None = None):
     if out is not None:
@@ -268,7 +275,8 @@ class QuantizedLinear:
                         "the input width")
         ws, ss = weight.shape, scale.shape
         in_features = x.shape[-1] if x.shape else 0
-        if (ws[0] != self.out_features or in_features % self.group_size
+        out = ws[0] * 16 if len(ws) == 3 else ws[0]  # packed [N/16, K/64, 1024]
+        if (out != self.out_features or in_features % self.group_size
                 or ss != (self.out_features, in_features // self.group_size)):
             raise Error(Status.INVALID_ARGUMENT,
                         f"QuantizedLinear({self.out_features}, {self.group_size}) does not "
@@ -323,6 +331,7 @@ class KvCache:
 
 from .model import DecoderConfig, DecoderModel  # noqa: E402  (needs the classes above)
 
-__all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "dequantize", "quantized_linear",
+__all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "dequantize", "pack_weight",
+           "quantized_linear",
            "linear_bf16", "QuantizedLinear", "grouped_query_attention", "KvCache",
            "DecoderConfig", "DecoderModel", "bf16_to_f32"]

@@ -21,7 +21,7 @@ EXPORTS = [
     "rxw8_buffer_create", "rxw8_buffer_from_host", "rxw8_buffer_wrap", "rxw8_buffer_to_host",
     "rxw8_buffer_copy_from_host", "rxw8_buffer_retain", "rxw8_buffer_release",
     "rxw8_buffer_dtype", "rxw8_buffer_dims", "rxw8_buffer_device_ptr",
-    "rxw8_dequantize", "rxw8_quantized_linear", "rxw8_quantized_linear_into",
+    "rxw8_dequantize", "rxw8_pack_weight", "rxw8_quantized_linear", "rxw8_quantized_linear_into",
     "rxw8_linear_bf16", "rxw8_linear_bf16_into", "rxw8_gqa_decode", "rxw8_gqa_decode_into",
     "rxw8_kv_update_at",
     "rxw8_decoder_create", "rxw8_decoder_destroy", "rxw8_decoder_num_parameters",
@@ -61,6 +61,7 @@ def _declare(L):
         "rxw8_buffer_dims": (c_int, [vp, i64p, POINTER(c_int)]),
         "rxw8_buffer_device_ptr": (c_int, [vp, POINTER(vp)]),
         "rxw8_dequantize": (c_int, [vp, vp, vp, c_int, POINTER(vp)]),
+        "rxw8_pack_weight": (c_int, [vp, vp, POINTER(vp)]),
         "rxw8_quantized_linear": (c_int, [vp, vp, vp, vp, c_int, c_int, POINTER(vp)]),
         "rxw8_quantized_linear_into": (c_int, [vp, vp, vp, vp, c_int, vp]),
         "rxw8_linear_bf16": (c_int, [vp, vp, vp, c_int, POINTER(vp)]),

@@ -4,20 +4,33 @@
 //
 // Layout: u8 weights [N, K] row-major (RXLA's U8 = int8 + 128 storage,
 // crates/rxla-nn/src/layers.rs:277-287), f32 scales [N, K/G], activations
-// [M, K] bf16 (or f32, rounded to bf16 on load), output [M, N] bf16 or f32.
+// [M, K] bf16 (or f32, rounded to bf16 when staged), output [M, N] bf16 or f32.
 //
-// Mapping: one wave owns 16 output channels; a 256-thread workgroup owns 64
-// channels and one K-split of length Kc = K / ksplit. Every lane streams
-// 16-byte slices of one weight row (lane = row + 16 * slice), so a wave load
-// covers 16 rows x 64 contiguous bytes. The 16 codes of a slice become two
-// bf16x8 A-fragments of v_mfma_f32_16x16x32_bf16 (u8 -> f32 -> bf16 is exact
-// for 0..255); the activations are the B operand (batch rows as columns).
-// The -128 offset is folded exactly by a second MFMA with an all-ones A
-// operand, which yields sum_k x[m, k] per column: acc - 128 * ones.
-// Scales are applied per group (G a multiple of 64) or once per channel
-// (G == K) after accumulation. Split-K partials are reduced deterministically
-// by the last-arriving workgroup of each 64-channel tile.
+// Mapping: a 256-thread workgroup (4 waves) owns 16*RW output channels and
+// one K-split [k0, k0 + Kc) (Kc = K / ksplit). Its waves form RW row groups
+// of 16 channels x KW = 4 / RW slices of Kc; the KW slices of a row group are
+// reduced through LDS in slice order at the end. The workgroup first stages
+// its activation slice x[0:M, k0:k0+Kc] in LDS as bf16 (padded rows) and, for
+// grouped scales, its scale tile, so the streaming loop issues nothing but
+// weight loads to global memory. Every lane streams 16-byte slices of one
+// weight row (lane = row + 16 * slice): a wave load covers 16 rows x 64
+// contiguous bytes. Loads are double-buffered in two register sets of U slices
+// (issue B, consume A, issue A', consume B): U to 2U loads per lane stay in
+// flight, and the straight-line buffers keep the compiler's vmcnt waits exact.
+// The 16 codes of a slice become two bf16x8 A-fragments of
+// v_mfma_f32_16x16x32_bf16 (u8 -> f32 -> bf16 is exact for 0..255); the
+// activations from LDS are the B operand (batch rows as columns; columns >= M
+// read a valid row and are never stored). The -128 offset is folded exactly by
+// a second MFMA with an all-ones A operand, which yields sum_k x[m, k] per
+// column: acc - 128 * ones. Scales are applied per group (G a multiple of 64)
+// or once per channel (G == K).
+//
+// With ksplit > 1 each workgroup writes its unscaled (per-channel) or scaled
+// (grouped) f32 partial tile with plain stores and rxw8_gemv_splitk_reduce sums
+// the partials in split order in a second launch: deterministic, and the
+// kernel boundary makes the partials visible without device-scope fences.
 #include <type_traits>
+
 #include "common.h"
 
 struct GemvArgs {
@@ -26,141 +39,153 @@ struct GemvArgs {
   const float *scale; // [N, K / G] (unused for the dense variant)
   void *y;            // [M, N] bf16 or f32
   float *ws;          // [ksplit, M, N] split-K partials
-  unsigned *counters; // [ceil(N / 64)] split-K arrival counters (zeroed once)
   int M, N, K, G;     // G == K for per-channel scales
   int ksplit;
   int x_f32, y_f32;
 };
 
+struct SplitkReduceArgs {
+  const float *ws;    // [ksplit, M, N]
+  const float *scale; // [N] per-channel scale or null
+  void *y;            // [M, N]
+  int M, N, ksplit;
+  int y_f32;
+};
+
 namespace {
 
-constexpr int kRowsPerWave = 16;
-constexpr int kWaves = 4;
-constexpr int kRowsPerBlock = kRowsPerWave * kWaves;
+constexpr int kXPad = 8;  // bf16 elements of padding per staged activation row
 
-template <int MB>
-__device__ __forceinline__ void store_out(const GemvArgs &a, int b, int n, f32x4 v) {
-  if (b >= a.M) return;
-  if (a.y_f32) {
+__device__ __forceinline__ void store_out(void *y, int y_f32, int64_t N, int b, int n, f32x4 v) {
+  if (y_f32) {
     float4 o = {round_bf16(v[0]), round_bf16(v[1]), round_bf16(v[2]), round_bf16(v[3])};
-    *(float4 *)((float *)a.y + (int64_t)b * a.N + n) = o;
+    *(float4 *)((float *)y + (int64_t)b * N + n) = o;
   } else {
     uint2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    *(uint2 *)((uint16_t *)a.y + (int64_t)b * a.N + n) = o;
+    *(uint2 *)((uint16_t *)y + (int64_t)b * N + n) = o;
   }
 }
 
-// Finish a 16-channel x (16*MB) batch tile: either write it out (ksplit == 1)
-// or publish the partial and let the last workgroup reduce.
-template <int MB>
-__device__ __forceinline__ void finish_tile(const GemvArgs &a, bool active, int row0,
-                                            int sp, f32x4 (&total)[MB], bool per_channel) {
+// Stage x[0:M, k0:k0+Kc] as bf16 into LDS rows of stride Kc + kXPad.
+__device__ __forceinline__ void stage_x(const GemvArgs &a, uint16_t *xs, int k0, int Kc) {
+  const int ldx = Kc + kXPad;
+  const int per_row = Kc / 8;
+  const int total = a.M * per_row;
+  for (int i = threadIdx.x; i < total; i += blockDim.x) {
+    const int b = i / per_row, kk = (i - b * per_row) * 8;
+    const int64_t off = (int64_t)b * a.K + k0 + kk;
+    *(u32x4 *)(xs + b * ldx + kk) = load_x8(a.x, off, a.x_f32 != 0);
+  }
+}
+
+// Reduce the KW k-slices of each row group through LDS (slice order), then
+// write the tile (ksplit == 1, scaled here when per-channel) or its partial.
+template <int MB, int RW>
+__device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int rows0, int sp,
+                                            f32x4 (&total)[MB], bool scale_here) {
+  constexpr int KW = 4 / RW;
   const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rg = wave % RW, kq = wave / RW;
+  if (KW > 1) {
+    __syncthreads();  // staged x/scales are no longer read; reuse LDS
+    if (kq > 0)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        *(f32x4 *)(red + (((kq - 1) * RW + rg) * MB + mb) * 256 + lane * 4) = total[mb];
+    __syncthreads();
+    if (kq > 0) return;
+#pragma unroll
+    for (int q = 1; q < KW; ++q)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        total[mb] += *(const f32x4 *)(red + (((q - 1) * RW + rg) * MB + mb) * 256 + lane * 4);
+  }
   const int j = lane >> 4, col = lane & 15;
-  const int n = row0 + 4 * j;
-  f32x4 sc = {1.f, 1.f, 1.f, 1.f};
-  if (active && per_channel) {
-    const float4 s4 = *(const float4 *)(a.scale + n);
-    sc[0] = s4.x; sc[1] = s4.y; sc[2] = s4.z; sc[3] = s4.w;
-  }
-  if (a.ksplit == 1) {
-    if (active)
-      for (int mb = 0; mb < MB; ++mb) store_out<MB>(a, col + 16 * mb, n, total[mb] * sc);
-    return;
-  }
-  if (active)
+  const int n = rows0 + rg * 16 + 4 * j;
+  if (n >= a.N) return;
+  if (a.ksplit > 1) {
+#pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const int b = col + 16 * mb;
       if (b < a.M) *(f32x4 *)(a.ws + ((int64_t)sp * a.M + b) * a.N + n) = total[mb];
     }
-  const int tile = blockIdx.x / a.ksplit;
-  if (!splitk_arrive(a.counters + tile, (unsigned)a.ksplit)) return;
-  if (!active) return;
+    return;
+  }
+  f32x4 sc = {1.f, 1.f, 1.f, 1.f};
+  if (scale_here) {
+    const float4 s4 = *(const float4 *)(a.scale + n);
+    sc = f32x4{s4.x, s4.y, s4.z, s4.w};
+  }
+#pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int b = col + 16 * mb;
-    if (b >= a.M) continue;
-    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.ksplit; ++s) {
-      const float *p = a.ws + ((int64_t)s * a.M + b) * a.N + n;
-      for (int i = 0; i < 4; ++i)
-        sum[i] += __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    store_out<MB>(a, b, n, sum * sc);
+    if (b < a.M) store_out(a.y, a.y_f32, a.N, b, n, total[mb] * sc);
   }
 }
 
-// Process NU consecutive 64-k chunks starting at chunk c (relative to k0).
-template <int MB, int NU>
-__device__ __forceinline__ void w8_chunks(const GemvArgs &a, const uint8_t *wrow, int k0,
-                                          int c, int row0, int chunks_per_group,
-                                          bool per_channel, f32x4 (&acc)[MB],
-                                          f32x4 (&ones)[MB], f32x4 (&total)[MB]) {
-  const int lane = threadIdx.x & 63;
-  const int j = lane >> 4, col = lane & 15;
-  u32x4 wv[NU];
-#pragma unroll
-  for (int u = 0; u < NU; ++u)
-    wv[u] = __builtin_nontemporal_load((const u32x4 *)(wrow + (int64_t)(c + u) * 64));
-  u32x4 xv[NU][MB][2];
-#pragma unroll
-  for (int u = 0; u < NU; ++u)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int b = col + 16 * mb;
-      if (b < a.M) {
-        const int64_t off = (int64_t)b * a.K + k0 + (int64_t)(c + u) * 64 + j * 16;
-        xv[u][mb][0] = load_x8(a.x, off, a.x_f32);
-        xv[u][mb][1] = load_x8(a.x, off + 8, a.x_f32);
-      } else {
-        xv[u][mb][0] = u32x4{0, 0, 0, 0};
-        xv[u][mb][1] = u32x4{0, 0, 0, 0};
-      }
-    }
-  const u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
-  const bf16x8 onesf = as_bf16x8(ones_bits);
-#pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    const uint2 p0 = u8x4_to_bf16x4(wv[u][0]), p1 = u8x4_to_bf16x4(wv[u][1]);
-    const uint2 p2 = u8x4_to_bf16x4(wv[u][2]), p3 = u8x4_to_bf16x4(wv[u][3]);
-    const u32x4 a0 = {p0.x, p0.y, p1.x, p1.y}, a1 = {p2.x, p2.y, p3.x, p3.y};
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const bf16x8 x0 = as_bf16x8(xv[u][mb][0]), x1 = as_bf16x8(xv[u][mb][1]);
-      acc[mb] = mfma16x16x32(as_bf16x8(a0), x0, acc[mb]);
-      acc[mb] = mfma16x16x32(as_bf16x8(a1), x1, acc[mb]);
-      ones[mb] = mfma16x16x32(onesf, x0, ones[mb]);
-      ones[mb] = mfma16x16x32(onesf, x1, ones[mb]);
-    }
-    if (!per_channel && ((c + u + 1) % chunks_per_group) == 0) {
-      // fold one scale group: total += s[n, g] * (acc - 128 * ones)
-      const int groups = a.K / a.G;
-      const int g = (k0 + (c + u) * 64) / a.G;
-      f32x4 sc;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] = a.scale[(int64_t)(row0 + 4 * j + i) * groups + g];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        total[mb] += sc * (acc[mb] - 128.f * ones[mb]);
-        acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        ones[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    }
-  }
-}
-
-template <int MB, int U>
+// PK (packed): weights in the tiled layout [N/16][K/64][64 lanes][16 B] where
+// block (t, c) holds, for lane l, the 16 codes W[16t + l%16][64c + 16(l/16) ..]:
+// every wave load is then one contiguous 1 KiB block (rxw8_pack_w8 builds it).
+// Row-major weights ([N, K], the reference's U8 storage) use PK = false.
+template <int MB, int RW, int U, bool PK>
 __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
+  constexpr int KW = 4 / RW;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int rg = wave % RW, kq = wave / RW;
   const int tile = blockIdx.x / a.ksplit;
   const int sp = blockIdx.x - tile * a.ksplit;
   const int Kc = a.K / a.ksplit;
   const int k0 = sp * Kc;
-  const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave;
+  const int Kw = Kc / KW;                   // this wave's slice of the split
+  const int rows0 = tile * 16 * RW;
+  const int row0 = rows0 + rg * 16;
   const bool active = row0 < a.N;
   const bool per_channel = a.G == a.K;
-  const int chunks = Kc / 64;
+  const int chunks = Kw / 64;
   const int chunks_per_group = per_channel ? chunks : a.G / 64;
+  const int groups = a.K / a.G;
+  const int ldx = Kc + kXPad;
+  const int r = lane & 15, j = lane >> 4, col = lane & 15;
+  const int kbase = kq * Kw;  // offset of this wave's slice within the split
+  // Inactive row groups (past N) re-read the tile's first rows; nothing of
+  // theirs is stored.
+  const int wrow16 = (active ? row0 : rows0) / 16;
+  const uint8_t *wp;
+  int64_t wstep;
+  if (PK) {
+    wp = (const uint8_t *)a.w + ((int64_t)wrow16 * (a.K / 64) + (k0 + kbase) / 64) * 1024 + lane * 16;
+    wstep = 1024;
+  } else {
+    wp = (const uint8_t *)a.w + (int64_t)(wrow16 * 16 + r) * a.K + k0 + kbase + j * 16;
+    wstep = 64;
+  }
+  const int last = chunks - 1;
+  u32x4 bufA[U], bufB[U];
+  auto load_group = [&](u32x4(&wb)[U], int c0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      wb[u] = __builtin_nontemporal_load((const u32x4 *)(wp + (int64_t)min(c0 + u, last) * wstep));
+  };
+  // The first weight group is in flight while x and the scales are staged.
+  load_group(bufA, 0);
+
+  // Grouped scales of this workgroup's rows and K-split, staged after x:
+  // ss[row_in_block * gps + g_local] (f32).
+  const int gps = per_channel ? 0 : Kc / a.G;
+  float *ss = (float *)(xs + a.M * ldx);
+  if (!per_channel) {
+    const int g0 = k0 / a.G;
+    for (int i = threadIdx.x; i < 16 * RW * gps; i += blockDim.x) {
+      const int rr = i / gps, gl = i - rr * gps;
+      const int n = rows0 + rr;
+      ss[i] = n < a.N ? a.scale[(int64_t)n * groups + g0 + gl] : 0.f;
+    }
+  }
+  stage_x(a, xs, k0, Kc);
+  __syncthreads();
 
   f32x4 acc[MB], ones[MB], total[MB];
 #pragma unroll
@@ -169,107 +194,202 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
     ones[mb] = acc[mb];
     total[mb] = acc[mb];
   }
-  if (active) {
-    const int r = lane & 15, j = lane >> 4;
-    const uint8_t *wrow = (const uint8_t *)a.w + (int64_t)(row0 + r) * a.K + k0 + j * 16;
-    int c = 0;
-    for (; c + U <= chunks; c += U)
-      w8_chunks<MB, U>(a, wrow, k0, c, row0, chunks_per_group, per_channel, acc, ones, total);
-    for (; c < chunks; ++c)
-      w8_chunks<MB, 1>(a, wrow, k0, c, row0, chunks_per_group, per_channel, acc, ones, total);
-    if (per_channel)
+  // B-operand rows: batch column col + 16*mb, clamped to a valid staged row.
+  const uint16_t *xrow[MB];
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) total[mb] = acc[mb] - 128.f * ones[mb];
+  for (int mb = 0; mb < MB; ++mb) {
+    const int b = col + 16 * mb;
+    xrow[mb] = xs + (b < a.M ? b : a.M - 1) * ldx + kbase + j * 16;
   }
-  finish_tile<MB>(a, active, row0, sp, total, per_channel);
+  const u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  const bf16x8 onesf = as_bf16x8(ones_bits);
+
+  // Process one 64-k chunk c (of this wave's slice) held in register slice w.
+  auto process = [&](const u32x4 w, const int c) {
+    const uint2 p0 = u8x4_to_bf16x4(w[0]), p1 = u8x4_to_bf16x4(w[1]);
+    const uint2 p2 = u8x4_to_bf16x4(w[2]), p3 = u8x4_to_bf16x4(w[3]);
+    const u32x4 a0 = {p0.x, p0.y, p1.x, p1.y}, a1 = {p2.x, p2.y, p3.x, p3.y};
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const u32x4 *xp = (const u32x4 *)(xrow[mb] + c * 64);
+      const bf16x8 x0 = as_bf16x8(xp[0]), x1 = as_bf16x8(xp[1]);
+      acc[mb] = mfma16x16x32(as_bf16x8(a0), x0, acc[mb]);
+      acc[mb] = mfma16x16x32(as_bf16x8(a1), x1, acc[mb]);
+      ones[mb] = mfma16x16x32(onesf, x0, ones[mb]);
+      ones[mb] = mfma16x16x32(onesf, x1, ones[mb]);
+    }
+    if (!per_channel && ((c + 1) % chunks_per_group) == 0) {
+      // fold one scale group: total += s[n, g] * (acc - 128 * ones)
+      const int gl = (kbase + c * 64) / a.G;
+      const float *srow = ss + (rg * 16 + 4 * j) * gps + gl;
+      const f32x4 sc = {srow[0], srow[gps], srow[2 * gps], srow[3 * gps]};
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        total[mb] += sc * (acc[mb] - 128.f * ones[mb]);
+        acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        ones[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  // A/B double buffer: issue B, consume A, issue A', consume B.
+  // chunks % (2U) == 0 (host); loads past the last chunk are clamped to it.
+  for (int c0 = 0; c0 < chunks; c0 += 2 * U) {
+    load_group(bufB, c0 + U);
+#pragma unroll
+    for (int u = 0; u < U; ++u) process(bufA[u], c0 + u);
+    load_group(bufA, c0 + 2 * U);
+#pragma unroll
+    for (int u = 0; u < U; ++u) process(bufB[u], c0 + U + u);
+  }
+  if (per_channel)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) total[mb] = acc[mb] - 128.f * ones[mb];
+  finish_tile<MB, RW>(a, (float *)xs, rows0, sp, total, per_channel);
 }
 
 // Dense bf16 weights (lm_head): one 16-byte slice = one MFMA A-fragment.
-template <int MB, int U>
+// PK: tiled layout [N/16][K/32][64 lanes][16 B], lane l holding
+// W[16t + l%16][32c + 8(l/16) .. +8] (rxw8_pack_bf16 builds it).
+template <int MB, int RW, int U, bool PK>
 __device__ __forceinline__ void gemv_bf16(const GemvArgs &a) {
+  constexpr int KW = 4 / RW;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int rg = wave % RW, kq = wave / RW;
   const int tile = blockIdx.x / a.ksplit;
   const int sp = blockIdx.x - tile * a.ksplit;
   const int Kc = a.K / a.ksplit;
   const int k0 = sp * Kc;
-  const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave;
+  const int Kw = Kc / KW;
+  const int rows0 = tile * 16 * RW;
+  const int row0 = rows0 + rg * 16;
   const bool active = row0 < a.N;
+  const int ldx = Kc + kXPad;
   const int r = lane & 15, j = lane >> 4, col = lane & 15;
+
+  const int wrow16 = (active ? row0 : rows0) / 16;
+  const uint16_t *wrow;
+  int64_t wstep;
+  if (PK) {
+    wrow = (const uint16_t *)a.w + ((int64_t)wrow16 * (a.K / 32) + (k0 + kq * Kw) / 32) * 512 +
+           lane * 8;
+    wstep = 512;
+  } else {
+    wrow = (const uint16_t *)a.w + (int64_t)(wrow16 * 16 + r) * a.K + k0 + kq * Kw + j * 8;
+    wstep = 32;
+  }
+  const int steps = Kw / 32;
+  const int last = steps - 1;
+  u32x4 bufA[U], bufB[U];
+  // The first weight group is in flight while x is staged.
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    bufA[u] = __builtin_nontemporal_load((const u32x4 *)(wrow + (int64_t)min(u, last) * wstep));
+  stage_x(a, xs, k0, Kc);
+  __syncthreads();
+
   f32x4 total[MB];
+  const uint16_t *xrow[MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) total[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (active) {
-    const uint16_t *wrow = (const uint16_t *)a.w + (int64_t)(row0 + r) * a.K + k0 + j * 8;
-    const int steps = Kc / 32;
-    int c = 0;
-    auto run = [&](auto nu_tag) {
-      constexpr int NU = decltype(nu_tag)::value;
-      u32x4 wv[NU];
-#pragma unroll
-      for (int u = 0; u < NU; ++u)
-        wv[u] = __builtin_nontemporal_load((const u32x4 *)(wrow + (int64_t)(c + u) * 32));
-      u32x4 xv[NU][MB];
-#pragma unroll
-      for (int u = 0; u < NU; ++u)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const int b = col + 16 * mb;
-          xv[u][mb] = b < a.M ? load_x8(a.x, (int64_t)b * a.K + k0 + (int64_t)(c + u) * 32 + j * 8,
-                                        a.x_f32)
-                              : u32x4{0, 0, 0, 0};
-        }
-#pragma unroll
-      for (int u = 0; u < NU; ++u)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          total[mb] = mfma16x16x32(as_bf16x8(wv[u]), as_bf16x8(xv[u][mb]), total[mb]);
-    };
-    for (; c + U <= steps; c += U) run(std::integral_constant<int, U>{});
-    for (; c < steps; ++c) run(std::integral_constant<int, 1>{});
-  }
-  // no scale for dense weights: finish with scale 1
-  const int jj = lane >> 4;
-  const int n = row0 + 4 * jj;
-  if (a.ksplit == 1) {
-    if (active)
-      for (int mb = 0; mb < MB; ++mb) store_out<MB>(a, col + 16 * mb, n, total[mb]);
-    return;
-  }
-  if (active)
-    for (int mb = 0; mb < MB; ++mb) {
-      const int b = col + 16 * mb;
-      if (b < a.M) *(f32x4 *)(a.ws + ((int64_t)sp * a.M + b) * a.N + n) = total[mb];
-    }
-  if (!splitk_arrive(a.counters + tile, (unsigned)a.ksplit)) return;
-  if (!active) return;
   for (int mb = 0; mb < MB; ++mb) {
+    total[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int b = col + 16 * mb;
-    if (b >= a.M) continue;
-    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.ksplit; ++s) {
-      const float *p = a.ws + ((int64_t)s * a.M + b) * a.N + n;
-      for (int i = 0; i < 4; ++i)
-        sum[i] += __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    store_out<MB>(a, b, n, sum);
+    xrow[mb] = xs + (b < a.M ? b : a.M - 1) * ldx + kq * Kw + j * 8;
   }
+  {
+    auto process = [&](const u32x4 w, const int c) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        total[mb] = mfma16x16x32(as_bf16x8(w), as_bf16x8(*(const u32x4 *)(xrow[mb] + c * 32)),
+                                 total[mb]);
+    };
+    for (int c0 = 0; c0 < steps; c0 += 2 * U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        bufB[u] = __builtin_nontemporal_load(
+            (const u32x4 *)(wrow + (int64_t)min(c0 + U + u, last) * wstep));
+#pragma unroll
+      for (int u = 0; u < U; ++u) process(bufA[u], c0 + u);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        bufA[u] = __builtin_nontemporal_load(
+            (const u32x4 *)(wrow + (int64_t)min(c0 + 2 * U + u, last) * wstep));
+#pragma unroll
+      for (int u = 0; u < U; ++u) process(bufB[u], c0 + U + u);
+    }
+  }
+  finish_tile<MB, RW>(a, (float *)xs, rows0, sp, total, false);
 }
 
 }  // namespace
 
-#define RXW8_GEMV_W8(MB, U)                                                          \
-  extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_w8_mb##MB(GemvArgs a) { \
-    gemv_w8<MB, U>(a);                                                               \
+// Second launch of a split GEMV: y[b, n] = s[n] * sum_sp ws[sp, b, n] (split
+// order), rounded to bf16. One thread per 4 consecutive outputs.
+extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(SplitkReduceArgs a) {
+  const int64_t quads = (int64_t)a.M * a.N / 4;
+  for (int64_t qd = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; qd < quads;
+       qd += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e = qd * 4;
+    const int b = (int)(e / a.N), n = (int)(e - (int64_t)b * a.N);
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < a.ksplit; ++s) {
+      const float4 p = *(const float4 *)(a.ws + ((int64_t)s * a.M + b) * a.N + n);
+      sum += f32x4{p.x, p.y, p.z, p.w};
+    }
+    if (a.scale) {
+      const float4 s4 = *(const float4 *)(a.scale + n);
+      sum *= f32x4{s4.x, s4.y, s4.z, s4.w};
+    }
+    store_out(a.y, a.y_f32, a.N, b, n, sum);
   }
-RXW8_GEMV_W8(1, 8)
-RXW8_GEMV_W8(2, 4)
-RXW8_GEMV_W8(4, 2)
+}
 
-#define RXW8_GEMV_BF16(MB, U)                                                          \
-  extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_bf16_mb##MB(GemvArgs a) { \
-    gemv_bf16<MB, U>(a);                                                               \
+#define RXW8_GEMV(KIND, MB, RW, U)                                              \
+  extern "C" __global__ void __launch_bounds__(256)                             \
+      rxw8_gemv_##KIND##_mb##MB##_rw##RW##_u##U(GemvArgs a) {                   \
+    gemv_##KIND<MB, RW, U, false>(a);                                           \
+  }                                                                             \
+  extern "C" __global__ void __launch_bounds__(256)                             \
+      rxw8_gemv_##KIND##_pk_mb##MB##_rw##RW##_u##U(GemvArgs a) {                \
+    gemv_##KIND<MB, RW, U, true>(a);                                            \
   }
-RXW8_GEMV_BF16(1, 8)
-RXW8_GEMV_BF16(2, 4)
-RXW8_GEMV_BF16(4, 2)
+#define RXW8_GEMV_U(KIND, MB, RW) \
+  RXW8_GEMV(KIND, MB, RW, 8)      \
+  RXW8_GEMV(KIND, MB, RW, 4)      \
+  RXW8_GEMV(KIND, MB, RW, 2)      \
+  RXW8_GEMV(KIND, MB, RW, 1)
+#define RXW8_GEMV_ALL(KIND) \
+  RXW8_GEMV_U(KIND, 1, 1)   \
+  RXW8_GEMV_U(KIND, 1, 4)   \
+  RXW8_GEMV_U(KIND, 2, 1)   \
+  RXW8_GEMV_U(KIND, 2, 4)
+
+RXW8_GEMV_ALL(w8)
+RXW8_GEMV_ALL(bf16)
+
+// Tiled weight layouts for the packed GEMV kernels. One thread moves one
+// 16-byte lane slice: dst block (t, c), lane l <- src row 16t + l%16.
+struct PackArgs {
+  const void *src;  // [N, K] row-major
+  void *dst;        // [N/16, K/kb, 1024 B]
+  int64_t n, k;     // elements
+  int kb;           // k per block: 64 (u8) or 32 (bf16)
+  int esize;        // bytes per element: 1 or 2
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_pack_tiles(PackArgs a) {
+  const int64_t blocks_k = a.k / a.kb;
+  const int64_t slices = a.n / 16 * blocks_k * 64;
+  const int per_lane = 16 / a.esize;  // elements per 16-byte slice
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < slices;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t blk = i >> 6;
+    const int lane = (int)(i & 63);
+    const int64_t t = blk / blocks_k, c = blk - t * blocks_k;
+    const int64_t row = 16 * t + (lane & 15);
+    const int64_t kk = c * a.kb + (int64_t)(lane >> 4) * per_lane;
+    const u32x4 v = *(const u32x4 *)((const char *)a.src + (row * a.k + kk) * a.esize);
+    *(u32x4 *)((char *)a.dst + i * 16) = v;
+  }
+}

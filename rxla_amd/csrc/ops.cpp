@@ -19,10 +19,25 @@ struct GemvArgs {
   const float *scale;
   void *y;
   float *ws;
-  unsigned *counters;
   int M, N, K, G;
   int ksplit;
   int x_f32, y_f32;
+};
+
+struct PackArgs {
+  const void *src;
+  void *dst;
+  int64_t n, k;
+  int kb;
+  int esize;
+};
+
+struct SplitkReduceArgs {
+  const float *ws;
+  const float *scale;
+  void *y;
+  int M, N, ksplit;
+  int y_f32;
 };
 
 struct GemmArgs {
@@ -106,48 +121,85 @@ static int env_int(const char *name, int dflt) {
   return v && *v ? std::atoi(v) : dflt;
 }
 
-// Split-K factor for the GEMV: minimise ceil(tiles*ks / CUs) / ks (time per
-// CU in units of a full-K tile), preferring the smaller split on ties.
-static int choose_ksplit(const Runtime *rt, int64_t n, int64_t k, int64_t g, int64_t unit) {
-  const int forced = env_int("RXW8_GEMV_KSPLIT", 0);
-  const int64_t tiles = (n + 63) / 64;
+// GEMV launch plan: row groups per workgroup (RW), K-split, double-buffer depth.
+struct GemvPlan {
+  int rw = 0, ks = 0, u = 0, mb = 1;
+  size_t lds = 0;
+};
+
+// LDS of one GEMV workgroup: the [m, kc] bf16 activation slice (rows padded by
+// 8), the grouped-scale tile [16*rw, kc/g] f32, and the cross-wave reduction
+// area (reused after the loop) of (4/rw - 1) * rw * mb f32 tiles of 16x16.
+static size_t gemv_lds(int64_t m, int64_t kc, int64_t k, int64_t g, int rw, int mb,
+                       bool w_bf16) {
+  (void)w_bf16;
+  const size_t stage = (size_t)m * (kc + 8) * 2 + (g == k ? 0 : (size_t)16 * rw * (kc / g) * 4);
+  const size_t red = (size_t)(4 / rw - 1) * rw * mb * 256 * 4;
+  return stage > red ? stage : red;
+}
+
+// Workgroups cover 16 channels (4 waves split K) for m <= 4, else 64 channels
+// (x staged once for 4 row groups). The split is the smallest power of two
+// that gives every CU a workgroup while the staged slice fits 64 KiB and each
+// wave gets an even number of 16-byte slices. RXW8_GEMV_KSPLIT /
+// RXW8_GEMV_RW override for tuning.
+static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, int64_t g,
+                          bool w_bf16) {
+  GemvPlan p;
+  p.mb = m <= 16 ? 1 : 2;
+  const int forced_rw = env_int("RXW8_GEMV_RW", 0);
+  p.rw = forced_rw == 1 || forced_rw == 4 ? forced_rw : (m <= 4 ? 1 : 4);
+  const int kw = 4 / p.rw;
+  const int64_t slice = w_bf16 ? 32 : 64;  // k per 16-byte lane load
+  const int64_t tiles = (n + 16 * p.rw - 1) / (16 * p.rw);
+  const int forced_ks = env_int("RXW8_GEMV_KSPLIT", 0);
   const bool per_channel = g == k;
-  int best = 1;
-  double best_cost = 1e30;
-  for (int ks = 1; ks <= 32; ks *= 2) {
+  int valid[8], nvalid = 0;
+  for (int ks = 1; ks <= 64; ks *= 2) {
     if (k % ks) continue;
     const int64_t kc = k / ks;
-    if (kc % unit) continue;
+    if (kc % kw || (kc / kw) % (2 * slice)) continue;  // even slices per wave
     if (!per_channel && kc % g) continue;
-    if (forced) {
-      if (ks == forced) return ks;
-      continue;
-    }
-    const int64_t wgs = tiles * ks;
-    const double cost = (double)((wgs + rt->cus - 1) / rt->cus) / ks;
-    if (cost < best_cost - 1e-9) {
-      best_cost = cost;
-      best = ks;
-    }
+    if (gemv_lds(m, kc, k, g, p.rw, p.mb, w_bf16) > 65536) continue;
+    valid[nvalid++] = ks;
   }
-  return best;
+  if (nvalid == 0) return p;
+  int pick = valid[nvalid - 1];
+  if (forced_ks) {
+    pick = 0;
+    for (int i = 0; i < nvalid; ++i)
+      if (valid[i] == forced_ks) pick = forced_ks;
+    if (!pick) return p;
+  } else {
+    for (int i = 0; i < nvalid; ++i)
+      if (tiles * valid[i] >= rt->cus) {
+        pick = valid[i];
+        break;
+      }
+  }
+  p.ks = pick;
+  p.lds = gemv_lds(m, k / pick, k, g, p.rw, p.mb, w_bf16);
+  const int64_t chunks = k / pick / kw / slice;
+  const int forced_u = env_int("RXW8_GEMV_U", 0);
+  p.u = forced_u == 8 || forced_u == 2 || forced_u == 1 ? forced_u : 4;
+  while (chunks % (2 * p.u)) p.u /= 2;
+  return p;
 }
 
 static bool is_f(int dt) { return dt == RXW8_F32 || dt == RXW8_BF16; }
 
-// Runs y[M, N] = linear(x[M, K]) on the GEMV kernel in chunks of <= 64 rows.
+// y[M, N] = linear(x[M, K]) on the GEMV kernel in chunks of <= 32 rows.
+// Returns UNIMPLEMENTED (nothing launched) when no plan fits.
 static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf16,
-                    const float *scale, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
-                    int64_t G) {
-  const int64_t unit = w_bf16 ? 32 : 64;
-  const int ks = choose_ksplit(rt, N, K, G, unit);
-  const int64_t tiles = (N + 63) / 64;
-  const int64_t mchunk = 64;
+                    bool packed, const float *scale, void *y, int y_f32, int64_t M, int64_t N,
+                    int64_t K, int64_t G) {
+  const int64_t mchunk = M <= 16 ? 16 : 32;
+  const GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16);
+  if (p.ks == 0 || N % 4) return RXW8_UNIMPLEMENTED;
+  const int64_t tiles = (N + 16 * p.rw - 1) / (16 * p.rw);
   const size_t xe = x_f32 ? 4 : 2, ye = y_f32 ? 4 : 2;
-  if (ks > 1) {
-    int rc = ensure_workspace(rt, rt->partials, (size_t)ks * mchunk * N * sizeof(float), false);
-    if (rc) return rc;
-    rc = ensure_workspace(rt, rt->counters, (size_t)tiles * sizeof(unsigned), true);
+  if (p.ks > 1) {
+    int rc = ensure_workspace(rt, rt->partials, (size_t)p.ks * mchunk * N * sizeof(float), false);
     if (rc) return rc;
   }
   for (int64_t m0 = 0; m0 < M; m0 += mchunk) {
@@ -158,19 +210,33 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     a.scale = scale;
     a.y = (char *)y + m0 * N * ye;
     a.ws = (float *)rt->partials.ptr;
-    a.counters = (unsigned *)rt->counters.ptr;
     a.M = (int)mm;
     a.N = (int)N;
     a.K = (int)K;
     a.G = (int)G;
-    a.ksplit = ks;
+    a.ksplit = p.ks;
     a.x_f32 = x_f32;
     a.y_f32 = y_f32;
-    const int mb = mm <= 16 ? 1 : (mm <= 32 ? 2 : 4);
+    const int mb = mm <= 16 ? 1 : 2;
     char kname[64];
-    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s_mb%d", w_bf16 ? "bf16" : "w8", mb);
-    int rc = launch(rt, kname, dim3((unsigned)(tiles * ks)), dim3(256), a);
+    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s_mb%d_rw%d_u%d", w_bf16 ? "bf16" : "w8",
+                  packed ? "_pk" : "", mb, p.rw, p.u);
+    int rc = launch(rt, kname, dim3((unsigned)(tiles * p.ks)), dim3(256), a,
+                    gemv_lds(mm, K / p.ks, K, G, p.rw, mb, w_bf16));
     if (rc) return rc;
+    if (p.ks > 1) {
+      SplitkReduceArgs r;
+      r.ws = (const float *)rt->partials.ptr;
+      r.scale = (!w_bf16 && G == K) ? scale : nullptr;
+      r.y = a.y;
+      r.M = (int)mm;
+      r.N = (int)N;
+      r.ksplit = p.ks;
+      r.y_f32 = y_f32;
+      rc = launch(rt, "rxw8_gemv_splitk_reduce", dim3(grid_for(mm * N / 4, 256, 4096)),
+                  dim3(256), r);
+      if (rc) return rc;
+    }
   }
   return RXW8_OK;
 }
@@ -207,17 +273,20 @@ static int check_qlinear(const Buffer *x, const Buffer *w, const Buffer *s, int 
                 "QuantizedLinear requires an F32 (or bf16-valued BF16) input with rank at least one");
   if (compute == RXW8_F32 && x->dtype != RXW8_F32)
     return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear: F32 compute requires an F32 input");
-  if (w->dtype != RXW8_U8 || w->rank != 2)
-    return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear weight: dtype does not match the schema (U8 [out, in])");
+  const bool packed = w->rank == 3;
+  if (w->dtype != RXW8_U8 || (w->rank != 2 && !(packed && w->dims[2] == 1024)))
+    return fail(RXW8_INVALID_ARGUMENT,
+                "QuantizedLinear weight: dtype does not match the schema (U8 [out, in], or packed "
+                "U8 [out/16, in/64, 1024])");
   if (s->dtype != RXW8_F32 || s->rank != 2)
     return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear scale: dtype does not match the schema (F32 [out, groups])");
   *K = x->dims[x->rank - 1];
-  *N = w->dims[0];
+  *N = packed ? w->dims[0] * 16 : w->dims[0];
   const int64_t groups = s->dims[1];
   if (*N <= 0 || *K <= 0 || groups <= 0 || *K % groups != 0)
     return fail(RXW8_INVALID_ARGUMENT,
                 "QuantizedLinear requires positive widths and a group size dividing the input width");
-  if (w->dims[1] != *K)
+  if ((packed ? w->dims[1] * 64 : w->dims[1]) != *K)
     return fail(RXW8_INVALID_ARGUMENT, "QuantizedLinear weight %s: shape does not match input width %lld",
                 dims_str(w).c_str(), (long long)*K);
   if (s->dims[0] != *N)
@@ -229,9 +298,9 @@ static int check_qlinear(const Buffer *x, const Buffer *w, const Buffer *s, int 
   return RXW8_OK;
 }
 
-int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, const float *s,
-                   void *y, int y_f32, int64_t M, int64_t N, int64_t K, int64_t G,
-                   int compute_bf16);
+int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
+                   const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
+                   int64_t G, int compute_bf16);
 
 }  // namespace rxw8
 
@@ -239,10 +308,19 @@ using namespace rxw8;
 
 namespace rxw8 {
 
-int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, const float *s,
-                   void *y, int y_f32, int64_t M, int64_t N, int64_t K, int64_t G,
-                   int compute_bf16) {
+int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
+                   const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
+                   int64_t G, int compute_bf16) {
   if (M == 0) return RXW8_OK;
+  if (packed) {
+    int rc = compute_bf16 ? run_gemv(rt, x, x_f32, w, false, true, s, y, y_f32, M, N, K, G)
+                          : (int)RXW8_UNIMPLEMENTED;
+    if (rc == RXW8_UNIMPLEMENTED)
+      return fail(RXW8_UNIMPLEMENTED,
+                  "packed W8 weights need BF16 compute and a GEMV tiling for N=%lld K=%lld G=%lld",
+                  (long long)N, (long long)K, (long long)G);
+    return rc;
+  }
   const bool mfma_ok = compute_bf16 && K % 64 == 0 && N % 16 == 0 && (G == K || G % 64 == 0) &&
                        K <= (1LL << 30) && N <= (1LL << 30) && !env_int("RXW8_FORCE_GENERIC", 0);
   if (mfma_ok) {
@@ -263,16 +341,26 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, cons
       const unsigned mt = (unsigned)((M + 255) / 256), nt = (unsigned)(N / 256);
       return launch(rt, "rxw8_w8a16_gemm", dim3(mt * nt), dim3(256), a);
     }
-    return run_gemv(rt, x, x_f32, w, false, s, y, y_f32, M, N, K, G);
+    int rc = run_gemv(rt, x, x_f32, w, false, false, s, y, y_f32, M, N, K, G);
+    if (rc != RXW8_UNIMPLEMENTED) return rc;
   }
   return run_generic_linear(rt, x, x_f32, w, 0, s, y, y_f32, M, N, K, G, compute_bf16);
 }
 
-int bf16_linear_launch(Runtime *rt, const void *x, int x_f32, const uint16_t *w, void *y,
-                       int y_f32, int64_t M, int64_t N, int64_t K) {
+int bf16_linear_launch(Runtime *rt, const void *x, int x_f32, const uint16_t *w, bool packed,
+                       void *y, int y_f32, int64_t M, int64_t N, int64_t K) {
   if (M == 0) return RXW8_OK;
-  if (K % 32 == 0 && N % 16 == 0 && !env_int("RXW8_FORCE_GENERIC", 0))
-    return run_gemv(rt, x, x_f32, w, true, nullptr, y, y_f32, M, N, K, K);
+  if (packed) {
+    int rc = run_gemv(rt, x, x_f32, w, true, true, nullptr, y, y_f32, M, N, K, K);
+    if (rc == RXW8_UNIMPLEMENTED)
+      return fail(RXW8_UNIMPLEMENTED, "packed BF16 weights need a GEMV tiling for N=%lld K=%lld",
+                  (long long)N, (long long)K);
+    return rc;
+  }
+  if (K % 32 == 0 && N % 16 == 0 && !env_int("RXW8_FORCE_GENERIC", 0)) {
+    int rc = run_gemv(rt, x, x_f32, w, true, false, nullptr, y, y_f32, M, N, K, K);
+    if (rc != RXW8_UNIMPLEMENTED) return rc;
+  }
   return run_generic_linear(rt, x, x_f32, w, 1, nullptr, y, y_f32, M, N, K, K, 1);
 }
 
@@ -376,6 +464,38 @@ int rxw8_dequantize(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer *scale, i
   return RXW8_OK;
 }
 
+int rxw8_pack_weight(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer **packed) {
+  if (!rt || !weight || !packed) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  const bool u8 = weight->dtype == RXW8_U8;
+  if ((!u8 && weight->dtype != RXW8_BF16) || weight->rank != 2)
+    return fail(RXW8_INVALID_ARGUMENT, "pack_weight: weight must be U8 or BF16 [out, in]");
+  const int64_t n = weight->dims[0], k = weight->dims[1];
+  const int kb = u8 ? 64 : 32;
+  if (n <= 0 || k <= 0 || n % 16 || k % kb)
+    return fail(RXW8_INVALID_ARGUMENT, "pack_weight: out %% 16 and in %% %d must be 0 (got [%lld, %lld])",
+                kb, (long long)n, (long long)k);
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  const int64_t dims[3] = {n / 16, k / kb, u8 ? 1024 : 512};
+  Buffer *o = nullptr;
+  int rc = new_buffer(rt, weight->dtype, dims, 3, false, &o);
+  if (rc) return rc;
+  PackArgs a;
+  a.src = weight->ptr;
+  a.dst = o->ptr;
+  a.n = n;
+  a.k = k;
+  a.kb = kb;
+  a.esize = u8 ? 1 : 2;
+  rc = launch(rt, "rxw8_pack_tiles", dim3(grid_for(n / 16 * (k / kb) * 64, 256, 1 << 14)),
+              dim3(256), a);
+  if (rc) {
+    rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+    return rc;
+  }
+  *packed = static_cast<rxw8_buffer *>(o);
+  return RXW8_OK;
+}
+
 int rxw8_quantized_linear_into(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
                                rxw8_buffer *scale, int compute_dtype, rxw8_buffer *y) {
   if (!rt || !y) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
@@ -391,8 +511,8 @@ int rxw8_quantized_linear_into(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *we
                 dims_str(y).c_str());
   std::lock_guard<std::recursive_mutex> g(rt->mu);
   return qlinear_launch(rt, x->ptr, x->dtype == RXW8_F32, (const uint8_t *)weight->ptr,
-                        (const float *)scale->ptr, y->ptr, y->dtype == RXW8_F32, M, N, K, G,
-                        compute_dtype == RXW8_BF16);
+                        weight->rank == 3, (const float *)scale->ptr, y->ptr,
+                        y->dtype == RXW8_F32, M, N, K, G, compute_dtype == RXW8_BF16);
 }
 
 int rxw8_quantized_linear(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
@@ -425,11 +545,14 @@ static int check_bf16_linear(const Buffer *x, const Buffer *w, int64_t *M, int64
   if (x->rt != w->rt) return fail(RXW8_INVALID_ARGUMENT, "Linear: buffers belong to different runtimes");
   if (x->rank < 1 || !is_f(x->dtype))
     return fail(RXW8_INVALID_ARGUMENT, "Linear requires an F32 or BF16 input with rank at least one");
-  if (w->dtype != RXW8_BF16 || w->rank != 2)
-    return fail(RXW8_INVALID_ARGUMENT, "Linear weight: dtype does not match the schema (BF16 [out, in])");
+  const bool packed = w->rank == 3;
+  if (w->dtype != RXW8_BF16 || (w->rank != 2 && !(packed && w->dims[2] == 512)))
+    return fail(RXW8_INVALID_ARGUMENT,
+                "Linear weight: dtype does not match the schema (BF16 [out, in], or packed BF16 "
+                "[out/16, in/32, 512])");
   *K = x->dims[x->rank - 1];
-  *N = w->dims[0];
-  if (*K <= 0 || *N <= 0 || w->dims[1] != *K)
+  *N = packed ? w->dims[0] * 16 : w->dims[0];
+  if (*K <= 0 || *N <= 0 || (packed ? w->dims[1] * 32 : w->dims[1]) != *K)
     return fail(RXW8_INVALID_ARGUMENT, "Linear weight %s: shape does not match input width %lld",
                 dims_str(w).c_str(), (long long)*K);
   *M = 1;
@@ -447,7 +570,7 @@ int rxw8_linear_bf16_into(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,
   if (!shape_ok) return fail(RXW8_INVALID_ARGUMENT, "Linear output: shape or dtype mismatch");
   std::lock_guard<std::recursive_mutex> g(rt->mu);
   return bf16_linear_launch(rt, x->ptr, x->dtype == RXW8_F32, (const uint16_t *)weight->ptr,
-                            y->ptr, y->dtype == RXW8_F32, M, N, K);
+                            weight->rank == 3, y->ptr, y->dtype == RXW8_F32, M, N, K);
 }
 
 int rxw8_linear_bf16(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight, int out_dtype,

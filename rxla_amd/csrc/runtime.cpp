@@ -7,6 +7,7 @@
 // PJRT_Error_Code (vendor/xla/pjrt/c/pjrt_c_api.h:168-186) and
 // PjrtErrorCode::is_retryable (:93-104).
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "internal.h"
@@ -232,16 +233,29 @@ int rxw8_runtime_create(int device, rxw8_runtime **out) {
   rt->cus = prop.multiProcessorCount;
   rt->name = prop.name;
   const struct {
+    const char *name;
     const unsigned char *begin, *end;
-  } blobs[] = {{rxw8_co_gemv, rxw8_co_gemv_end},
-               {rxw8_co_misc, rxw8_co_misc_end},
-               {rxw8_co_attention, rxw8_co_attention_end},
-               {rxw8_co_gemm, rxw8_co_gemm_end},
-               {rxw8_co_decoder, rxw8_co_decoder_end}};
+  } blobs[] = {{"gemv", rxw8_co_gemv, rxw8_co_gemv_end},
+               {"misc", rxw8_co_misc, rxw8_co_misc_end},
+               {"attention", rxw8_co_attention, rxw8_co_attention_end},
+               {"gemm", rxw8_co_gemm, rxw8_co_gemm_end},
+               {"decoder", rxw8_co_decoder, rxw8_co_decoder_end}};
+  // Development hook: RXW8_CODE_OBJECT_DIR=<dir> loads <dir>/<name>.hsaco in
+  // place of the embedded code object of that name when the file exists.
+  const char *override_dir = std::getenv("RXW8_CODE_OBJECT_DIR");
   for (auto &blob : blobs) {
     if (blob.end - blob.begin <= 0) continue;
     hipModule_t m = nullptr;
-    e = hipModuleLoadData(&m, blob.begin);
+    std::string path;
+    if (override_dir && *override_dir) {
+      path = std::string(override_dir) + "/" + blob.name + ".hsaco";
+      if (FILE *f = std::fopen(path.c_str(), "rb")) {
+        std::fclose(f);
+      } else {
+        path.clear();
+      }
+    }
+    e = path.empty() ? hipModuleLoadData(&m, blob.begin) : hipModuleLoad(&m, path.c_str());
     if (e != hipSuccess) {
       int rc = hip_fail(e, "hipModuleLoadData");
       for (hipModule_t mm : rt->modules) (void)hipModuleUnload(mm);

@@ -171,3 +171,47 @@ def test_bf16_weight_linear_lm_head(rt):
     ref = oracle.linear_bf16w(x, e)
     y = r.linear_bf16(rt, rt.buffer(x), rt.buffer(e, r.DType.BF16)).to_numpy()
     assert rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("b,n,k,g", [(1, 4096, 4096, 4096), (16, 6144, 4096, 4096),
+                                     (8, 2048, 2048, 128), (4, 1024, 6144, 6144)])
+def test_packed_weights_bit_identical(rt, b, n, k, g):
+    """The tiled layout holds the same bytes: results equal the row-major path."""
+    r = rx()
+    rng = np.random.default_rng(b * 7 + n)
+    x = oracle.round_bf16(rng.standard_normal((b, k)).astype(np.float32))
+    u8, s = quantized(rng, n, k, g)
+    wb = rt.buffer(u8)
+    packed = r.pack_weight(rt, wb)
+    assert packed.shape == (n // 16, k // 64, 1024)
+    tiles = packed.to_numpy()
+    # block (t, c), lane l = row 16t + l%16, columns 64c + 16(l/16) .. +16
+    lane = 37
+    np.testing.assert_array_equal(tiles[3, 5, lane * 16:(lane + 1) * 16],
+                                  u8[16 * 3 + lane % 16, 64 * 5 + 16 * (lane // 16):][:16])
+    xb, sb = rt.buffer(oracle.bf16_bits(x), r.DType.BF16), rt.buffer(s)
+    y_row = r.quantized_linear(rt, xb, wb, sb, r.DType.BF16, r.DType.F32).to_numpy()
+    y_pk = r.quantized_linear(rt, xb, packed, sb, r.DType.BF16, r.DType.F32).to_numpy()
+    np.testing.assert_array_equal(y_pk, y_row)
+    assert rel_err(y_pk, oracle.quantized_linear(x, u8, s)) <= TOL
+
+
+def test_packed_bf16_lm_head(rt):
+    r = rx()
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((8, 2048)).astype(np.float32)
+    e = oracle.bf16_bits(rng.standard_normal((4096, 2048)).astype(np.float32) * 0.02)
+    eb = rt.buffer(e, r.DType.BF16)
+    pk = r.pack_weight(rt, eb)
+    assert pk.shape == (256, 64, 512)
+    y_row = r.linear_bf16(rt, rt.buffer(x), eb).to_numpy()
+    y_pk = r.linear_bf16(rt, rt.buffer(x), pk).to_numpy()
+    np.testing.assert_array_equal(y_pk, y_row)
+    assert rel_err(y_pk, oracle.linear_bf16w(x, e)) <= TOL
+
+
+def test_pack_weight_validation(rt):
+    r = rx()
+    with pytest.raises(r.Error) as e:
+        r.pack_weight(rt, rt.buffer(np.zeros((24, 64), np.uint8)))  # 24 % 16 != 0
+    assert e.value.code == r.Status.INVALID_ARGUMENT
