@@ -524,7 +524,9 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
   const int64_t L = cfg->max_seq, G = cfg->group;
   const int64_t QKV = (HQ + 2 * HKV) * D;
   const int64_t T = b * s; /* token rows, row = bi * s + t */
-  if (b <= 0 || s <= 0 || HQ % HKV || H % G || I % G || (HQ * D) % G) return -1;
+  /* group 0: per-output-channel scales (each linear's G is its input width) */
+  const int64_t G_H = G > 0 ? G : H, G_I = G > 0 ? G : I, G_O = G > 0 ? G : HQ * D;
+  if (b <= 0 || s <= 0 || HQ % HKV || H % G_H || I % G_I || (HQ * D) % G_O) return -1;
   for (int64_t bi = 0; bi < b; ++bi)
     if (lens[bi] < 0 || lens[bi] + s > L) return -1;
 
@@ -556,7 +558,7 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
     uint16_t *kcl = k_cache + l * b * HKV * L * D;
     uint16_t *vcl = v_cache + l * b * HKV * L * D;
     rxo_rms_norm(h, T, H, p->in_norm[l], cfg->eps, 0, n);
-    rc = rxo_quantized_linear(n, T, H, p->qkv_w[l], p->qkv_s[l], QKV, G,
+    rc = rxo_quantized_linear(n, T, H, p->qkv_w[l], p->qkv_s[l], QKV, G_H,
                               RXO_COMPUTE_BF16, RXO_ACCUM_F32, qkv, threads);
     if (rc) goto done;
     for (int64_t r = 0; r < T; ++r) {
@@ -591,17 +593,17 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
                                  vcl + (bi * HKV + hh / (HQ / HKV)) * L * D, &len,
                                  1, 1, 1, L, D, scale, 0, att + (r * HQ + hh) * D, 1);
       }
-    rc = rxo_quantized_linear(att, T, HQ * D, p->o_w[l], p->o_s[l], H, G,
+    rc = rxo_quantized_linear(att, T, HQ * D, p->o_w[l], p->o_s[l], H, G_O,
                               RXO_COMPUTE_BF16, RXO_ACCUM_F32, tmp, threads);
     if (rc) goto done;
     for (int64_t i = 0; i < T * H; ++i) h[i] += tmp[i];
     rxo_rms_norm(h, T, H, p->post_norm[l], cfg->eps, 0, n);
-    rc = rxo_quantized_linear(n, T, H, p->gu_w[l], p->gu_s[l], 2 * I, G,
+    rc = rxo_quantized_linear(n, T, H, p->gu_w[l], p->gu_s[l], 2 * I, G_H,
                               RXO_COMPUTE_BF16, RXO_ACCUM_F32, gu, threads);
     if (rc) goto done;
     for (int64_t r = 0; r < T; ++r)
       rxo_silu_mul(gu + r * 2 * I, gu + r * 2 * I + I, I, act + r * I);
-    rc = rxo_quantized_linear(act, T, I, p->down_w[l], p->down_s[l], H, G,
+    rc = rxo_quantized_linear(act, T, I, p->down_w[l], p->down_s[l], H, G_I,
                               RXO_COMPUTE_BF16, RXO_ACCUM_F32, tmp, threads);
     if (rc) goto done;
     for (int64_t i = 0; i < T * H; ++i) h[i] += tmp[i];

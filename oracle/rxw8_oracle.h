@@ -146,7 +146,7 @@ void rxo_argmax_rows(const float *x, int64_t rows, int64_t cols, int32_t *out);
 typedef struct rxo_decoder_config {
   int64_t layers, hidden, q_heads, kv_heads, head_dim, intermediate, vocab;
   int64_t max_seq; /* KV capacity per sequence */
-  int64_t group;   /* W8 group size (hidden and intermediate multiples) */
+  int64_t group;   /* W8 group size; 0 = per-output-channel (G = input width) */
   float eps, theta;
   int32_t qk_norm; /* per-head RMSNorm on q and k before RoPE */
 } rxo_decoder_config;

@@ -5,10 +5,12 @@
 // for the keys j < lens[b] of sequence b; query head h reads kv head
 // h / (Hq / Hkv) (consecutive heads share a kv head, attention.rs:83-135).
 //
-// Layout: q [B, Hq, D] f32|bf16, caches [B, Hkv, Lmax, D] bf16, out
-// [B, Hq, D] f32|bf16. One workgroup (4 waves) handles one (b, kv head,
-// 256-key chunk); each wave takes 64 keys. The G = Hq/Hkv query rows of the
-// kv head share every K/V byte the workgroup loads.
+// Layout: q [R, Hq, D] f32|bf16 (one query row per decoding sequence, or one
+// per prompt token in prefill), caches [Bc, Hkv, Lmax, D] bf16, out
+// [R, Hq, D] f32|bf16. Row r reads cache slot row_seq[r] (r when null) and
+// sees its first lens[r] keys. One workgroup (4 waves) handles one (row, kv
+// head, 256-key chunk); each wave takes 64 keys. The G = Hq/Hkv query heads
+// of the kv head share every K/V byte the workgroup loads.
 //
 // QK^T runs on v_mfma_f32_16x16x32_bf16 with K as the A operand (16 keys x
 // 32 dims per fragment, 16-byte loads of contiguous K rows) and q^T as the B
@@ -17,21 +19,23 @@
 // bf16. Softmax statistics are reduced per wave with cross-lane shuffles,
 // probabilities go through LDS, and P.V runs on the VALU in f32 with each lane
 // owning 8 dims of every fourth key (16-byte V loads, 1 KiB per wave load).
-// Waves merge (max, sum, acc) in LDS; chunks of one (b, kv head) merge in the
-// last-arriving workgroup (deterministic order).
+// Waves merge (max, sum, acc) in LDS. A row with one chunk writes its output
+// directly; otherwise every chunk writes (max, sum, acc) partials and
+// rxw8_gqa_decode_combine merges them in chunk order in a second launch
+// (deterministic; the kernel boundary makes the partials visible).
 #include "common.h"
 
 struct AttnArgs {
-  const void *q;        // [B, Hq, D]
-  const uint16_t *kc;   // [B, Hkv, Lmax, D] bf16
-  const uint16_t *vc;   // [B, Hkv, Lmax, D] bf16
-  const int32_t *lens;  // [B]
-  const float *mask;    // additive, mask[b * mask_sb + h * mask_sh + j], or null
-  void *out;            // [B, Hq, D]
-  float *ws;            // partials [B, Hkv, max_chunks, G, 2 + D]
-  unsigned *counters;   // [B * Hkv]
+  const void *q;           // [R, Hq, D]
+  const uint16_t *kc;      // [Bc, Hkv, Lmax, D] bf16
+  const uint16_t *vc;      // [Bc, Hkv, Lmax, D] bf16
+  const int32_t *lens;     // [R] visible keys of row r
+  const int32_t *row_seq;  // [R] cache slot of row r, or null (slot r)
+  const float *mask;       // additive, mask[r * mask_sb + h * mask_sh + j], or null
+  void *out;               // [R, Hq, D]
+  float *ws;               // partials [R, Hkv, max_chunks, G, 2 + D]
   int64_t mask_sb, mask_sh;
-  int B, Hq, Hkv, Lmax, max_chunks;
+  int R, Hq, Hkv, Lmax, max_chunks;
   float scale;
   int q_f32, out_f32;
 };
@@ -65,15 +69,16 @@ __device__ void attn_chunk(const AttnArgs &a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int chunk = blockIdx.x % a.max_chunks;
-  const int bh = blockIdx.x / a.max_chunks;  // b * Hkv + kvh
-  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
+  const int bh = blockIdx.x / a.max_chunks;  // row * Hkv + kvh
+  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;  // b: query row
   int len = a.lens[b];
   len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
   const int nchunks = (len + KC - 1) / KC;
   if (chunk >= nchunks) return;  // uniform per workgroup
 
   const int j0 = chunk * KC + wave * KW;  // first key of this wave
-  const int64_t row_base = (int64_t)bh * a.Lmax;
+  const int seq = a.row_seq ? a.row_seq[b] : b;
+  const int64_t row_base = ((int64_t)seq * a.Hkv + kvh) * a.Lmax;
   const int col = lane & 15, g4 = lane >> 4;
 
   // q fragments (B operand): lane (head = col, dgroup = g4), 8 dims per step.
@@ -244,25 +249,30 @@ __device__ void attn_chunk(const AttnArgs &a) {
       ph[2 + d] = O;
     }
   }
-  if (single) return;
-  if (!splitk_arrive(a.counters + bh, (unsigned)nchunks)) return;
-  // Last workgroup of (b, kvh): merge chunk partials in chunk order.
+}
+
+// Second launch: merge the chunk partials of rows with more than one chunk,
+// in chunk order. One workgroup per (row, kv head); thread = (head, dim).
+template <int G>
+__device__ void attn_combine(const AttnArgs &a) {
+  const int bh = blockIdx.x;
+  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
+  int len = a.lens[b];
+  len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
+  const int nchunks = (len + KC - 1) / KC;
+  if (nchunks == 1) return;  // written by the chunk kernel
   const float *base = a.ws + ((int64_t)bh * a.max_chunks) * G * (2 + D);
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
     float M = kNegInf;
-    for (int c = 0; c < nchunks; ++c)
-      M = fmaxf(M, __hip_atomic_load(base + ((int64_t)c * G + h) * (2 + D), __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT));
+    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, base[((int64_t)c * G + h) * (2 + D)]);
     float L = 0.f, O = 0.f;
     for (int c = 0; c < nchunks; ++c) {
       const float *ph = base + ((int64_t)c * G + h) * (2 + D);
-      const float mc = __hip_atomic_load(ph, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float lc = __hip_atomic_load(ph + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float oc = __hip_atomic_load(ph + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float mc = ph[0];
       const float f = mc == kNegInf ? 0.f : __expf(mc - M);
-      L += f * lc;
-      O += f * oc;
+      L += f * ph[1];
+      O += f * ph[2 + d];
     }
     const float r = O / L;
     const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
@@ -275,9 +285,13 @@ __device__ void attn_chunk(const AttnArgs &a) {
 
 }  // namespace
 
-#define RXW8_ATTN(G)                                                               \
+#define RXW8_ATTN(G)                                                                 \
   extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_decode_d128_g##G(AttnArgs a) { \
-    attn_chunk<G>(a);                                                              \
+    attn_chunk<G>(a);                                                                \
+  }                                                                                  \
+  extern "C" __global__ void __launch_bounds__(256)                                  \
+      rxw8_gqa_decode_combine_d128_g##G(AttnArgs a) {                                \
+    attn_combine<G>(a);                                                              \
   }
 RXW8_ATTN(1)
 RXW8_ATTN(2)
@@ -290,7 +304,8 @@ struct AttnGenericArgs {
   const void *q;
   const void *kc;
   const void *vc;
-  const int32_t *lens;
+  const int32_t *lens;     // [R]
+  const int32_t *row_seq;  // [R] cache slot, or null
   const float *mask;
   void *out;
   int64_t mask_sb, mask_sh;
@@ -307,12 +322,13 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_decode_generic(AttnGe
   __shared__ float sc[8192];
   __shared__ float red[256];
   const int bh = blockIdx.x;
-  const int b = bh / a.Hq, h = bh - b * a.Hq;
+  const int b = bh / a.Hq, h = bh - b * a.Hq;  // b: query row
   const int kvh = h / (a.Hq / a.Hkv);
   int len = a.lens[b];
   len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
+  const int seq = a.row_seq ? a.row_seq[b] : b;
   const int64_t qoff = ((int64_t)b * a.Hq + h) * a.D;
-  const int64_t kvoff = ((int64_t)b * a.Hkv + kvh) * a.Lmax * a.D;
+  const int64_t kvoff = ((int64_t)seq * a.Hkv + kvh) * a.Lmax * a.D;
   float mx = -__builtin_huge_valf();
   for (int j = threadIdx.x; j < len; j += blockDim.x) {
     float acc = 0.f;

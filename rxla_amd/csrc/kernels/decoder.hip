@@ -1,5 +1,272 @@
-// Decoder step kernels (filled in with the decoder plan).
+// Decoder-step kernels for the synthetic Qwen-style dense W8 decoder
+// (composition of crates/rxla-models/src/qwen3_5/mod.rs:199-273 and
+// layers.rs:28-101,270-293 with dense full-attention layers):
+// token positions, embedding gather, RMSNorm to bf16, per-head q/k RMSNorm +
+// RoPE + KV-cache append, SiLU(gate) * up, first-max argmax, length advance.
+// Every kernel reads sequence lengths from device memory, so a decode step
+// can be captured once in a HIP graph and replayed.
 #include "common.h"
-extern "C" __global__ void rxw8_decoder_placeholder(int *p) {
-  if (p) *p = 0;
+
+// ---- positions: token t = (b, i) sits at pos = lens[b] + i --------------------
+struct DecPosArgs {
+  const int32_t *lens;  // [B]
+  int32_t *pos;         // [T]
+  int32_t *row_seq;     // [T] cache slot of token t
+  int32_t *row_len;     // [T] keys visible to token t (causal: pos + 1)
+  int b, s;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_positions(DecPosArgs a) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= a.b * a.s) return;
+  const int bi = t / a.s;
+  const int p = a.lens[bi] + (t - bi * a.s);
+  a.pos[t] = p;
+  a.row_seq[t] = bi;
+  a.row_len[t] = p + 1;
+}
+
+struct DecAdvanceArgs {
+  int32_t *lens;
+  int b, s;
+};
+
+extern "C" __global__ void rxw8_dec_advance(DecAdvanceArgs a) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < a.b) a.lens[i] += a.s;
+}
+
+// ---- embedding: h[t] = f32(E[clamp(ids[t], 0, V-1)]) (indexing.rs:637-656) ----
+struct EmbedArgs {
+  const int32_t *ids;
+  const uint16_t *table;  // [V, H] bf16
+  float *h;               // [T, H]
+  int64_t T, V, H;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_embed(EmbedArgs a) {
+  const int64_t t = blockIdx.x;
+  int64_t id = a.ids[t];
+  id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
+  const uint16_t *src = a.table + id * a.H;
+  float *dst = a.h + t * a.H;
+  for (int64_t i = threadIdx.x; i < a.H; i += blockDim.x) dst[i] = bf16_bits_to_f32(src[i]);
+}
+
+// ---- RMSNorm (ops.rs:929-944): y = bf16((x * rsqrt(mean(x^2) + eps)) * w) -------
+// One workgroup per output row; src_rows (optional) picks the input row.
+struct RmsNormArgs {
+  const float *x;          // [rows_in, H]
+  const float *w;          // [H]
+  uint16_t *y;             // [rows, H] bf16
+  const int32_t *src_row;  // optional: input row of output row r
+  int64_t H;
+  int rows;
+  int src_stride, src_offset;  // without src_row: input row = r * stride + offset
+  float eps;
+};
+
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+  // deterministic: wave-level butterfly, then the 4 wave sums in order
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_rmsnorm(RmsNormArgs a) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const int64_t src = a.src_row ? a.src_row[r] : (int64_t)r * a.src_stride + a.src_offset;
+  const float *x = a.x + src * a.H;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < a.H; i += blockDim.x) ss += x[i] * x[i];
+  ss = block_sum_256(ss, red);
+  const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+  uint16_t *y = a.y + (int64_t)r * a.H;
+  for (int64_t i = threadIdx.x; i < a.H; i += blockDim.x)
+    y[i] = f32_to_bf16_bits((x[i] * scale) * a.w[i]);
+}
+
+// ---- q/k RMSNorm + RoPE + KV append (qwen3_5/layers.rs:28-101; rotary.rs:17-74;
+// kv_cache.rs:53-68 at start [seq, head, pos, 0]).
+// qkv [T, (Hq + 2 Hkv) * D] bf16 (the bf16 result of the fused projection).
+// One wave per head: lane l owns the SplitHalf pairs (i, i + D/2), i = l + 64 j.
+struct QkRopeArgs {
+  const uint16_t *qkv;
+  const float *q_norm;  // [D] or null
+  const float *k_norm;  // [D] or null
+  const float *freqs;   // [D/2] theta^(-2i/D), f32
+  const int32_t *pos;   // [T]
+  const int32_t *row_seq;
+  float *q_out;         // [T, Hq, D] f32
+  uint16_t *kc;         // [Bc, Hkv, Lmax, D] bf16 (this layer)
+  uint16_t *vc;
+  int T, Hq, Hkv, D, Lmax;
+  float eps;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_qk_rope_kv(QkRopeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int heads = a.Hq + 2 * a.Hkv;
+  const int gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // global wave
+  const int t = gw / heads, h = gw - t * heads;
+  if (t >= a.T) return;
+  const int D = a.D, half = D / 2;
+  const uint16_t *src = a.qkv + ((int64_t)t * heads + h) * D;
+  const int seq = a.row_seq[t];
+  const int p = a.pos[t];
+  if (h >= a.Hq + a.Hkv) {  // value head: copy the bf16 projection into the cache
+    const int kvh = h - a.Hq - a.Hkv;
+    uint16_t *dst = a.vc + (((int64_t)seq * a.Hkv + kvh) * a.Lmax + p) * D;
+    for (int i = lane; i < D; i += 64) dst[i] = src[i];
+    return;
+  }
+  const bool is_q = h < a.Hq;
+  const float *nw = is_q ? a.q_norm : a.k_norm;
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) {
+    const float v = bf16_bits_to_f32(src[i]);
+    ss += v * v;
+  }
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const float scale = nw ? 1.0f / sqrtf(ss / (float)D + a.eps) : 1.0f;
+  const float fp = (float)p;
+  for (int i = lane; i < half; i += 64) {
+    float x0 = bf16_bits_to_f32(src[i]), x1 = bf16_bits_to_f32(src[i + half]);
+    if (nw) {
+      x0 = (x0 * scale) * nw[i];
+      x1 = (x1 * scale) * nw[i + half];
+    }
+    const float ang = fp * a.freqs[i];
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    const float r0 = x0 * cs - x1 * sn;
+    const float r1 = x1 * cs + x0 * sn;
+    if (is_q) {
+      float *dst = a.q_out + ((int64_t)t * a.Hq + h) * D;
+      dst[i] = r0;
+      dst[i + half] = r1;
+    } else {
+      const int kvh = h - a.Hq;
+      uint16_t *dst = a.kc + (((int64_t)seq * a.Hkv + kvh) * a.Lmax + p) * D;
+      dst[i] = f32_to_bf16_bits(r0);
+      dst[i + half] = f32_to_bf16_bits(r1);
+    }
+  }
+}
+
+// ---- SwiGLU middle (ops.rs:331-342): act = bf16(silu(g) * u), gu = [g | u] ----
+struct SiluMulArgs {
+  const uint16_t *gu;  // [T, 2I]
+  uint16_t *act;       // [T, I]
+  int64_t T, I;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_silu_mul(SiluMulArgs a) {
+  const int64_t total = a.T * a.I;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = e / a.I, i = e - t * a.I;
+    const float g = bf16_bits_to_f32(a.gu[t * 2 * a.I + i]);
+    const float u = bf16_bits_to_f32(a.gu[t * 2 * a.I + a.I + i]);
+    // sigmoid with a nonpositive exponent argument (ops.rs:331-338)
+    const float e_ = __expf(-fabsf(g));
+    const float sig = g >= 0.f ? 1.0f / (1.0f + e_) : e_ / (1.0f + e_);
+    a.act[e] = f32_to_bf16_bits((g * sig) * u);
+  }
+}
+
+// ---- argmax (indexing.rs:350-374): lowest index of the maximum; a NaN beats
+// every number and the first NaN wins. Pass 1: per-chunk partials; pass 2:
+// chunks in order.
+struct ArgmaxArgs {
+  const float *x;   // [rows, cols]
+  float *pval;      // [rows, chunks]
+  int32_t *pidx;
+  int32_t *out;     // [rows]
+  int64_t cols;
+  int rows, chunks;
+};
+
+__device__ __forceinline__ bool am_better(float a, int ia, float b, int ib) {
+  // is (a, ia) preferred over (b, ib)?
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_argmax_partial(ArgmaxArgs a) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int r = blockIdx.x / a.chunks, c = blockIdx.x - r * a.chunks;
+  const int64_t per = (a.cols + a.chunks - 1) / a.chunks;
+  const int64_t lo = c * per, hi = min(a.cols, lo + per);
+  float bv = -__builtin_huge_valf();
+  int bi = (int)(lo < hi ? lo : 0);
+  bool have = false;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+    const float v = a.x[(int64_t)r * a.cols + i];
+    if (!have || am_better(v, (int)i, bv, bi)) {
+      bv = v;
+      bi = (int)i;
+      have = true;
+    }
+  }
+  sv[threadIdx.x] = have ? bv : -__builtin_huge_valf();
+  si[threadIdx.x] = have ? bi : 0x7fffffff;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (threadIdx.x < st) {
+      const float ov = sv[threadIdx.x + st];
+      const int oi = si[threadIdx.x + st];
+      if (oi != 0x7fffffff &&
+          (si[threadIdx.x] == 0x7fffffff || am_better(ov, oi, sv[threadIdx.x], si[threadIdx.x]))) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    a.pval[blockIdx.x] = sv[0];
+    a.pidx[blockIdx.x] = si[0];
+  }
+}
+
+extern "C" __global__ void rxw8_dec_argmax_final(ArgmaxArgs a) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= a.rows) return;
+  float bv = 0.f;
+  int bi = 0x7fffffff;
+  for (int c = 0; c < a.chunks; ++c) {
+    const int i = a.pidx[r * a.chunks + c];
+    if (i == 0x7fffffff) continue;
+    const float v = a.pval[r * a.chunks + c];
+    if (bi == 0x7fffffff || am_better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  a.out[r] = bi == 0x7fffffff ? 0 : bi;
+}
+
+// ---- generate: out[i, step] = next[i]; step advances on device -------------------
+struct RecordArgs {
+  const int32_t *next;
+  int32_t *out;   // [b, ncols]
+  int32_t *step;  // device column counter
+  int b, ncols;
+};
+
+extern "C" __global__ void rxw8_dec_record(RecordArgs a) {
+  __shared__ int col;
+  if (threadIdx.x == 0) col = *a.step;
+  __syncthreads();
+  if (col < a.ncols)
+    for (int i = threadIdx.x; i < a.b; i += blockDim.x) a.out[i * a.ncols + col] = a.next[i];
+  __syncthreads();
+  if (threadIdx.x == 0) *a.step = col + 1;
 }

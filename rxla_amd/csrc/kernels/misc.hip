@@ -38,6 +38,7 @@ struct GenericLinearArgs {
   void *y;
   int64_t m, n, k, g;
   int x_f32, y_f32, compute_bf16, w_kind;
+  int y_mode;  // 1: y is an f32 residual, y += f32(bf16(result))
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_linear_generic(GenericLinearArgs a) {
@@ -63,7 +64,9 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_linear_generic(GenericLin
       acc = __fadd_rn(acc, __fmul_rn(xv, wv));
     }
     if (a.compute_bf16) acc = round_bf16(acc);
-    if (a.y_f32)
+    if (a.y_mode == 1)
+      ((float *)a.y)[e] += acc;
+    else if (a.y_f32)
       ((float *)a.y)[e] = acc;
     else
       ((uint16_t *)a.y)[e] = f32_to_bf16_bits(acc);

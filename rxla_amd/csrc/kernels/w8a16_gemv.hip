@@ -42,6 +42,7 @@ struct GemvArgs {
   int M, N, K, G;     // G == K for per-channel scales
   int ksplit;
   int x_f32, y_f32;
+  int y_mode;         // 0: store y; 1: y is an f32 residual, y += bf16(result)
 };
 
 struct SplitkReduceArgs {
@@ -50,14 +51,24 @@ struct SplitkReduceArgs {
   void *y;            // [M, N]
   int M, N, ksplit;
   int y_f32;
+  int y_mode;
 };
 
 namespace {
 
 constexpr int kXPad = 8;  // bf16 elements of padding per staged activation row
 
-__device__ __forceinline__ void store_out(void *y, int y_f32, int64_t N, int b, int n, f32x4 v) {
-  if (y_f32) {
+__device__ __forceinline__ void store_out(void *y, int y_f32, int y_mode, int64_t N, int b, int n,
+                                          f32x4 v) {
+  if (y_mode == 1) {  // residual: h += f32(bf16(result)) (layers.rs:295-296 + add)
+    float4 *h = (float4 *)((float *)y + (int64_t)b * N + n);
+    float4 o = *h;
+    o.x += round_bf16(v[0]);
+    o.y += round_bf16(v[1]);
+    o.z += round_bf16(v[2]);
+    o.w += round_bf16(v[3]);
+    *h = o;
+  } else if (y_f32) {
     float4 o = {round_bf16(v[0]), round_bf16(v[1]), round_bf16(v[2]), round_bf16(v[3])};
     *(float4 *)((float *)y + (int64_t)b * N + n) = o;
   } else {
@@ -120,7 +131,7 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int b = col + 16 * mb;
-    if (b < a.M) store_out(a.y, a.y_f32, a.N, b, n, total[mb] * sc);
+    if (b < a.M) store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, total[mb] * sc);
   }
 }
 
@@ -341,7 +352,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(Splitk
       const float4 s4 = *(const float4 *)(a.scale + n);
       sum *= f32x4{s4.x, s4.y, s4.z, s4.w};
     }
-    store_out(a.y, a.y_f32, a.N, b, n, sum);
+    store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, sum);
   }
 }
 

@@ -22,6 +22,7 @@ struct GemvArgs {
   int M, N, K, G;
   int ksplit;
   int x_f32, y_f32;
+  int y_mode;
 };
 
 struct PackArgs {
@@ -38,6 +39,7 @@ struct SplitkReduceArgs {
   void *y;
   int M, N, ksplit;
   int y_f32;
+  int y_mode;
 };
 
 struct GemmArgs {
@@ -64,6 +66,7 @@ struct GenericLinearArgs {
   void *y;
   int64_t m, n, k, g;
   int x_f32, y_f32, compute_bf16, w_kind;
+  int y_mode;
 };
 
 struct KvUpdateArgs {
@@ -86,12 +89,12 @@ struct AttnArgs {
   const uint16_t *kc;
   const uint16_t *vc;
   const int32_t *lens;
+  const int32_t *row_seq;
   const float *mask;
   void *out;
   float *ws;
-  unsigned *counters;
   int64_t mask_sb, mask_sh;
-  int B, Hq, Hkv, Lmax, max_chunks;
+  int R, Hq, Hkv, Lmax, max_chunks;
   float scale;
   int q_f32, out_f32;
 };
@@ -101,6 +104,7 @@ struct AttnGenericArgs {
   const void *kc;
   const void *vc;
   const int32_t *lens;
+  const int32_t *row_seq;
   const float *mask;
   void *out;
   int64_t mask_sb, mask_sh;
@@ -192,7 +196,7 @@ static bool is_f(int dt) { return dt == RXW8_F32 || dt == RXW8_BF16; }
 // Returns UNIMPLEMENTED (nothing launched) when no plan fits.
 static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf16,
                     bool packed, const float *scale, void *y, int y_f32, int64_t M, int64_t N,
-                    int64_t K, int64_t G) {
+                    int64_t K, int64_t G, int y_mode = 0) {
   const int64_t mchunk = M <= 16 ? 16 : 32;
   const GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16);
   if (p.ks == 0 || N % 4) return RXW8_UNIMPLEMENTED;
@@ -217,6 +221,7 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     a.ksplit = p.ks;
     a.x_f32 = x_f32;
     a.y_f32 = y_f32;
+    a.y_mode = y_mode;
     const int mb = mm <= 16 ? 1 : 2;
     char kname[64];
     std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s_mb%d_rw%d_u%d", w_bf16 ? "bf16" : "w8",
@@ -233,6 +238,7 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
       r.N = (int)N;
       r.ksplit = p.ks;
       r.y_f32 = y_f32;
+      r.y_mode = y_mode;
       rc = launch(rt, "rxw8_gemv_splitk_reduce", dim3(grid_for(mm * N / 4, 256, 4096)),
                   dim3(256), r);
       if (rc) return rc;
@@ -243,7 +249,7 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
 
 static int run_generic_linear(Runtime *rt, const void *x, int x_f32, const void *w, int w_kind,
                               const float *scale, void *y, int y_f32, int64_t M, int64_t N,
-                              int64_t K, int64_t G, int compute_bf16) {
+                              int64_t K, int64_t G, int compute_bf16, int y_mode = 0) {
   GenericLinearArgs a;
   a.x = x;
   a.w = w;
@@ -257,6 +263,7 @@ static int run_generic_linear(Runtime *rt, const void *x, int x_f32, const void 
   a.y_f32 = y_f32;
   a.compute_bf16 = compute_bf16;
   a.w_kind = w_kind;
+  a.y_mode = y_mode;
   return launch(rt, "rxw8_linear_generic", dim3(grid_for(M * N)), dim3(256), a);
 }
 
@@ -300,7 +307,7 @@ static int check_qlinear(const Buffer *x, const Buffer *w, const Buffer *s, int 
 
 int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
                    const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
-                   int64_t G, int compute_bf16);
+                   int64_t G, int compute_bf16, int y_mode = 0);
 
 }  // namespace rxw8
 
@@ -310,10 +317,10 @@ namespace rxw8 {
 
 int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
                    const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
-                   int64_t G, int compute_bf16) {
+                   int64_t G, int compute_bf16, int y_mode) {
   if (M == 0) return RXW8_OK;
   if (packed) {
-    int rc = compute_bf16 ? run_gemv(rt, x, x_f32, w, false, true, s, y, y_f32, M, N, K, G)
+    int rc = compute_bf16 ? run_gemv(rt, x, x_f32, w, false, true, s, y, y_f32, M, N, K, G, y_mode)
                           : (int)RXW8_UNIMPLEMENTED;
     if (rc == RXW8_UNIMPLEMENTED)
       return fail(RXW8_UNIMPLEMENTED,
@@ -341,10 +348,10 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
       const unsigned mt = (unsigned)((M + 255) / 256), nt = (unsigned)(N / 256);
       return launch(rt, "rxw8_w8a16_gemm", dim3(mt * nt), dim3(256), a);
     }
-    int rc = run_gemv(rt, x, x_f32, w, false, false, s, y, y_f32, M, N, K, G);
+    int rc = run_gemv(rt, x, x_f32, w, false, false, s, y, y_f32, M, N, K, G, y_mode);
     if (rc != RXW8_UNIMPLEMENTED) return rc;
   }
-  return run_generic_linear(rt, x, x_f32, w, 0, s, y, y_f32, M, N, K, G, compute_bf16);
+  return run_generic_linear(rt, x, x_f32, w, 0, s, y, y_f32, M, N, K, G, compute_bf16, y_mode);
 }
 
 int bf16_linear_launch(Runtime *rt, const void *x, int x_f32, const uint16_t *w, bool packed,
@@ -365,34 +372,33 @@ int bf16_linear_launch(Runtime *rt, const void *x, int x_f32, const uint16_t *w,
 }
 
 int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
-                     int cache_f32, const int32_t *lens, const float *mask, int64_t mask_sb,
-                     int64_t mask_sh, void *out, int out_f32, int64_t B, int64_t Hq,
-                     int64_t Hkv, int64_t Lmax, int64_t D, float scale) {
-  if (B == 0) return RXW8_OK;
+                     int cache_f32, const int32_t *lens, const int32_t *row_seq,
+                     const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
+                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale) {
+  if (R == 0) return RXW8_OK;
   const int64_t G = Hq / Hkv;
   const bool fast = !cache_f32 && D == 128 && (G == 1 || G == 2 || G == 4 || G == 8) &&
                     !env_int("RXW8_FORCE_GENERIC", 0);
   if (fast) {
     const int64_t KC = 256;
     const int64_t max_chunks = (Lmax + KC - 1) / KC;
-    int rc = ensure_workspace(rt, rt->scratch,
-                              (size_t)B * Hkv * max_chunks * G * (2 + D) * sizeof(float), false);
-    if (rc) return rc;
-    // attention counters live after the GEMV counters region
-    rc = ensure_workspace(rt, rt->counters, (size_t)(B * Hkv + 65536) * sizeof(unsigned), true);
-    if (rc) return rc;
+    if (max_chunks > 1) {
+      int rc = ensure_workspace(rt, rt->scratch,
+                                (size_t)R * Hkv * max_chunks * G * (2 + D) * sizeof(float), false);
+      if (rc) return rc;
+    }
     AttnArgs a;
     a.q = q;
     a.kc = (const uint16_t *)kc;
     a.vc = (const uint16_t *)vc;
     a.lens = lens;
+    a.row_seq = row_seq;
     a.mask = mask;
     a.out = out;
     a.ws = (float *)rt->scratch.ptr;
-    a.counters = (unsigned *)rt->counters.ptr + 65536;
     a.mask_sb = mask_sb;
     a.mask_sh = mask_sh;
-    a.B = (int)B;
+    a.R = (int)R;
     a.Hq = (int)Hq;
     a.Hkv = (int)Hkv;
     a.Lmax = (int)Lmax;
@@ -402,7 +408,10 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     a.out_f32 = out_f32;
     char kname[64];
     std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_d128_g%d", (int)G);
-    return launch(rt, kname, dim3((unsigned)(B * Hkv * max_chunks)), dim3(256), a);
+    int rc = launch(rt, kname, dim3((unsigned)(R * Hkv * max_chunks)), dim3(256), a);
+    if (rc || max_chunks == 1) return rc;
+    std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_combine_d128_g%d", (int)G);
+    return launch(rt, kname, dim3((unsigned)(R * Hkv)), dim3(256), a);
   }
   if (Lmax > 8192)
     return fail(RXW8_UNIMPLEMENTED, "decode attention: the generic kernel supports Lmax <= 8192");
@@ -411,11 +420,12 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
   a.kc = kc;
   a.vc = vc;
   a.lens = lens;
+  a.row_seq = row_seq;
   a.mask = mask;
   a.out = out;
   a.mask_sb = mask_sb;
   a.mask_sh = mask_sh;
-  a.B = (int)B;
+  a.B = (int)R;
   a.Hq = (int)Hq;
   a.Hkv = (int)Hkv;
   a.Lmax = (int)Lmax;
@@ -424,7 +434,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
   a.q_f32 = q_f32;
   a.cache_f32 = cache_f32;
   a.out_f32 = out_f32;
-  return launch(rt, "rxw8_gqa_decode_generic", dim3((unsigned)(B * Hq)), dim3(256), a);
+  return launch(rt, "rxw8_gqa_decode_generic", dim3((unsigned)(R * Hq)), dim3(256), a);
 }
 
 }  // namespace rxw8
@@ -640,7 +650,7 @@ int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
   if (scale <= 0.f) scale = 1.0f / std::sqrt((float)D);
   std::lock_guard<std::recursive_mutex> g(rt->mu);
   return attention_launch(rt, q->ptr, q->dtype == RXW8_F32, k_cache->ptr, v_cache->ptr,
-                          k_cache->dtype == RXW8_F32, (const int32_t *)lens->ptr,
+                          k_cache->dtype == RXW8_F32, (const int32_t *)lens->ptr, nullptr,
                           mask ? (const float *)mask->ptr : nullptr, sb, sh, out->ptr,
                           out->dtype == RXW8_F32, q->dims[0], q->dims[1], k_cache->dims[1],
                           k_cache->dims[2], D, scale);

@@ -49,7 +49,7 @@ def tiny_params(cfg, seed=0, std=0.02):
 
     def q8(n, k, name):
         w = (rng.standard_normal((n, k)) * std).astype(np.float32)
-        u8, s = quantize(w, G)
+        u8, s = quantize(w, G if G > 0 else k)  # group 0: per-output-channel
         p[name + ".weight"], p[name + ".scale"] = u8, s
 
     for l in range(cfg["layers"]):

@@ -1,0 +1,142 @@
+"""GPU parity for the compiled decoder plan (embedding, 28-layer-style blocks,
+KV cache, greedy decode) against the CPU oracle decoder, through the C ABI.
+
+Both sides are fed the same token ids every step (the oracle's greedy
+choice), so the comparison never depends on a near-tie argmax. Logits must
+match to max relative error <= 1e-2."""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_err
+from decoder_fixtures import tiny_config, tiny_params
+
+pytestmark = pytest.mark.gpu
+
+
+def rx():
+    import rxla_amd
+    return rxla_amd
+
+
+def small_cfg(**kw):
+    # D = 128 and widths that the packed GEMV tiles; 2 query heads per kv head.
+    c = tiny_config(layers=2, hidden=512, q_heads=4, kv_heads=2, head_dim=128,
+                    intermediate=1024, vocab=1008, max_seq=40, group=0)
+    c.update(kw)
+    return c
+
+
+def build(rt, cfg, params, batch):
+    r = rx()
+    dc = r.DecoderConfig(layers=cfg["layers"], hidden=cfg["hidden"], q_heads=cfg["q_heads"],
+                         kv_heads=cfg["kv_heads"], head_dim=cfg["head_dim"],
+                         intermediate=cfg["intermediate"], vocab=cfg["vocab"], max_batch=batch,
+                         max_seq=cfg["max_seq"], group=cfg["group"], eps=cfg["eps"],
+                         theta=cfg["theta"], qk_norm=cfg["qk_norm"])
+    model = r.DecoderModel(rt, dc).compile()
+    schema = model.schema()
+    assert len(schema) == len(params)
+    for path, dtype, shape in schema:
+        arr = params[path]
+        assert tuple(arr.shape) == tuple(shape), path
+        model.bind_parameter(path, rt.buffer(arr, dtype))
+    return model
+
+
+def step_both(rt, model, dec, ids):
+    r = rx()
+    b = ids.shape[0]
+    logits = rt.zeros((b, model.cfg.vocab), r.DType.F32)
+    nxt = model.forward(rt.buffer(ids.astype(np.int32)), logits=logits).to_numpy()
+    ref_logits, ref_next = dec.forward(ids)
+    return logits.to_numpy(), nxt, ref_logits, ref_next
+
+
+@pytest.mark.parametrize("group", [0, 128])
+def test_decoder_prefill_and_decode_match_oracle(rt, group):
+    cfg = small_cfg(group=group)
+    params = tiny_params(cfg, seed=51 + group, std=0.05)
+    batch = 2
+    model = build(rt, cfg, params, batch)
+    dec = oracle.Decoder(cfg, params, batch)
+    rng = np.random.default_rng(52)
+    ids = rng.integers(0, cfg["vocab"], (batch, 7)).astype(np.int32)
+    lg, nxt, rlg, rnxt = step_both(rt, model, dec, ids)
+    err = rel_err(lg, rlg)
+    print(f"prefill group={group} logits rel_err={err:.3e}")
+    assert err <= 1e-2
+    np.testing.assert_array_equal(model.lens()[:batch], [7, 7])
+    for step in range(5):
+        ids = rnxt.reshape(batch, 1).astype(np.int32)
+        lg, nxt, rlg, rnxt = step_both(rt, model, dec, ids)
+        err = rel_err(lg, rlg)
+        print(f"decode step {step} rel_err={err:.3e}")
+        assert err <= 1e-2
+        top2 = np.sort(rlg, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 0.05 * np.abs(top2[:, 1]).max()
+        np.testing.assert_array_equal(nxt[clear], rnxt[clear])
+    np.testing.assert_array_equal(model.lens()[:batch], [12, 12])
+
+
+def test_generate_graph_matches_eager_and_oracle(rt):
+    r = rx()
+    cfg = small_cfg()
+    params = tiny_params(cfg, seed=61, std=0.05)
+    batch, s, steps = 2, 6, 8
+    rng = np.random.default_rng(62)
+    prompt = rng.integers(0, cfg["vocab"], (batch, s)).astype(np.int32)
+    outs = []
+    for use_graph in (False, True, True):  # second graph run replays the captured step
+        model = build(rt, cfg, params, batch)
+        out = model.generate(rt.buffer(prompt), steps, use_graph=use_graph).to_numpy()
+        outs.append(out)
+        np.testing.assert_array_equal(model.lens()[:batch], [s + steps, s + steps])
+    np.testing.assert_array_equal(outs[0], outs[1])
+    np.testing.assert_array_equal(outs[0], outs[2])
+    # greedy oracle on the same prompt
+    dec = oracle.Decoder(cfg, params, batch)
+    _, nxt = dec.forward(prompt)
+    want = [nxt]
+    for _ in range(steps):
+        _, nxt = dec.forward(nxt.reshape(batch, 1))
+        want.append(nxt)
+    want = np.stack(want, axis=1)
+    agree = (outs[0] == want).mean()
+    print(f"generate agreement with oracle: {agree:.3f}")
+    np.testing.assert_array_equal(outs[0][:, :3], want[:, :3])
+
+
+def test_decoder_binding_and_capacity_errors(rt):
+    r = rx()
+    cfg = small_cfg(max_seq=8)
+    params = tiny_params(cfg, seed=71)
+    dc = r.DecoderConfig(layers=2, hidden=512, q_heads=4, kv_heads=2, head_dim=128,
+                         intermediate=1024, vocab=1008, max_batch=2, max_seq=8, group=0)
+    model = r.DecoderModel(rt, dc).compile()
+    ids = rt.buffer(np.zeros((2, 3), np.int32))
+    with pytest.raises(r.Error) as e:  # unbound parameters
+        model.forward(ids)
+    assert e.value.code == r.Status.FAILED_PRECONDITION
+    with pytest.raises(r.Error) as e:
+        model.bind_parameter("layers.9.mlp.down_proj.weight", rt.buffer(np.zeros((512, 1024), np.uint8)))
+    assert e.value.code == r.Status.NOT_FOUND
+    with pytest.raises(r.Error) as e:
+        model.bind_parameter("norm.weight", rt.buffer(np.zeros((511,), np.float32)))
+    assert e.value.code == r.Status.INVALID_ARGUMENT
+    with pytest.raises(r.Error) as e:
+        model.bind_parameter("norm.weight", rt.buffer(np.zeros((512,), np.int32)))
+    assert e.value.code == r.Status.INVALID_ARGUMENT
+    for path, dtype, shape in model.schema():
+        model.bind_parameter(path, rt.buffer(params[path], dtype))
+    with pytest.raises(r.Error) as e:
+        model.bind_parameter("norm.weight", rt.buffer(params["norm.weight"]))
+    assert e.value.code == r.Status.ALREADY_EXISTS
+    model.forward(ids)
+    np.testing.assert_array_equal(model.lens(), [3, 3])
+    with pytest.raises(r.Error) as e:  # 3 + 6 > max_seq 8: nothing runs, lens unchanged
+        model.forward(rt.buffer(np.zeros((2, 6), np.int32)))
+    assert e.value.code == r.Status.OUT_OF_RANGE
+    np.testing.assert_array_equal(model.lens(), [3, 3])
+    model.reset()
+    np.testing.assert_array_equal(model.lens(), [0, 0])
