@@ -87,9 +87,38 @@ def _declare(L):
     return L
 
 
+def _share_torch_hip_runtime():
+    """Make librxw8.so bind to the HIP runtime PyTorch will use.
+
+    PyTorch wheels for ROCm carry their own libamdhip64.so (soname
+    libamdhip64.so.7, found through torch/lib). librxw8.so links
+    libamdhip64.so.7 from /opt/rocm. Whichever is mapped first satisfies the
+    soname; if /opt/rocm's is, a later `import torch` maps a second HIP and
+    HSA runtime by path and finds no GPU. Preloading torch's copy by path
+    (without importing torch) leaves one runtime in the process, so device
+    pointers and streams can be shared both ways. RXW8_SYSTEM_HIP=1 keeps
+    /opt/rocm's runtime (for processes that never use torch).
+    """
+    if os.environ.get("RXW8_SYSTEM_HIP") == "1":
+        return
+    import importlib.util
+    try:
+        spec = importlib.util.find_spec("torch")
+    except (ImportError, ValueError):
+        return
+    if spec is None or not spec.submodule_search_locations:
+        return
+    for d in spec.submodule_search_locations:
+        path = os.path.join(d, "lib", "libamdhip64.so")
+        if os.path.exists(path):
+            ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+            return
+
+
 def load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
             "g.build()'` (there is no CPU fallback for the rxw8 kernels)")
+    _share_torch_hip_runtime()
     return _declare(ctypes.CDLL(LIB_PATH))

@@ -61,24 +61,3 @@ __device__ __forceinline__ u32x4 load_x8(const void *x, int64_t off, bool x_f32)
   }
   return *(const u32x4 *)((const uint16_t *)x + off);
 }
-
-// Deterministic split-K completion: every workgroup of a tile publishes its
-// partial, then the last one to arrive (counter) reduces all partials in
-// split order. The counter is reset by that last workgroup, so no clearing is
-// needed between launches. Returns true in the last-arriving workgroup.
-__device__ __forceinline__ bool splitk_arrive(unsigned *counter, unsigned nsplit) {
-  __shared__ unsigned s_last;
-  __threadfence();  // release this workgroup's partial stores (agent scope)
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-    bool last = prev == nsplit - 1;
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last ? 1u : 0u;
-  }
-  __syncthreads();
-  bool last = s_last != 0;
-  if (last) __threadfence();  // acquire the other workgroups' partials
-  return last;
-}

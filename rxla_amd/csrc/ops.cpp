@@ -48,7 +48,7 @@ struct GemmArgs {
   const float *scale;
   void *y;
   int M, N, K, G;
-  int x_f32, y_f32;
+  int x_f32, y_f32, y_mode, w_packed;
 };
 
 struct DequantArgs {
@@ -315,11 +315,44 @@ using namespace rxw8;
 
 namespace rxw8 {
 
+// Prefill-sized products go to the MFMA GEMM (128 x 128 output tiles; the
+// weight tile is dequantised once per 128 activation rows); smaller M stays on
+// the GEMV, which streams the weights once per 16/32-row chunk.
+static bool gemm_eligible(int64_t M, int64_t N, int64_t G) {
+  static const int64_t min_m = env_int("RXW8_GEMM_MIN_M", 64);
+  return M > min_m && N % 128 == 0 && G % 16 == 0 && M <= (1LL << 30) && !env_int("RXW8_NO_GEMM", 0);
+}
+
+// Requires K % 64 == 0, N % 128 == 0 and G % 16 == 0 (checked by the callers),
+// so every 16-code staging slice lies inside one scale group.
+static int run_gemm(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
+                    const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
+                    int64_t G, int y_mode) {
+  GemmArgs a;
+  a.x = x;
+  a.w = w;
+  a.scale = s;
+  a.y = y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.G = (int)G;
+  a.x_f32 = x_f32;
+  a.y_f32 = y_f32;
+  a.y_mode = y_mode;
+  a.w_packed = packed ? 1 : 0;
+  const int64_t tiles = (M + 127) / 128 * (N / 128);
+  const int64_t per_xcd = (tiles + 7) / 8;
+  return launch(rt, "rxw8_w8a16_gemm", dim3((unsigned)(per_xcd * 8)), dim3(256), a);
+}
+
 int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
                    const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
                    int64_t G, int compute_bf16, int y_mode) {
   if (M == 0) return RXW8_OK;
   if (packed) {
+    if (compute_bf16 && gemm_eligible(M, N, G))
+      return run_gemm(rt, x, x_f32, w, true, s, y, y_f32, M, N, K, G, y_mode);
     int rc = compute_bf16 ? run_gemv(rt, x, x_f32, w, false, true, s, y, y_f32, M, N, K, G, y_mode)
                           : (int)RXW8_UNIMPLEMENTED;
     if (rc == RXW8_UNIMPLEMENTED)
@@ -331,23 +364,7 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
   const bool mfma_ok = compute_bf16 && K % 64 == 0 && N % 16 == 0 && (G == K || G % 64 == 0) &&
                        K <= (1LL << 30) && N <= (1LL << 30) && !env_int("RXW8_FORCE_GENERIC", 0);
   if (mfma_ok) {
-    const bool gemm_ok = M > 64 && N % 256 == 0 && K % 64 == 0 && (G == K || G % 64 == 0) &&
-                         rt->fn("rxw8_w8a16_gemm") && !env_int("RXW8_NO_GEMM", 0);
-    if (gemm_ok) {
-      GemmArgs a;
-      a.x = x;
-      a.w = w;
-      a.scale = s;
-      a.y = y;
-      a.M = (int)M;
-      a.N = (int)N;
-      a.K = (int)K;
-      a.G = (int)G;
-      a.x_f32 = x_f32;
-      a.y_f32 = y_f32;
-      const unsigned mt = (unsigned)((M + 255) / 256), nt = (unsigned)(N / 256);
-      return launch(rt, "rxw8_w8a16_gemm", dim3(mt * nt), dim3(256), a);
-    }
+    if (gemm_eligible(M, N, G)) return run_gemm(rt, x, x_f32, w, false, s, y, y_f32, M, N, K, G, y_mode);
     int rc = run_gemv(rt, x, x_f32, w, false, false, s, y, y_f32, M, N, K, G, y_mode);
     if (rc != RXW8_UNIMPLEMENTED) return rc;
   }

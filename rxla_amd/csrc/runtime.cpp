@@ -77,17 +77,34 @@ std::string dims_str(const Buffer *b) {
   return s + "]";
 }
 
+// Code object holding a kernel, by name prefix (index into `modules`, in the
+// load order of runtime_create). Looking a kernel up only where it lives keeps
+// hipModuleGetFunction from failing: a failed call would leave HIP's per-thread
+// last error set, and the caller's next HIP API check (torch's included)
+// would report it as its own.
+static int module_of(const char *kname) {
+  static const struct {
+    const char *prefix;
+    int module;
+  } routes[] = {{"rxw8_gemv_", 0},      {"rxw8_pack_tiles", 0},     {"rxw8_dequant", 1},
+                {"rxw8_linear_generic", 1}, {"rxw8_kv_update", 1}, {"rxw8_gqa_", 2},
+                {"rxw8_w8a16_gemm", 3}, {"rxw8_dec_", 4}};
+  for (const auto &r : routes)
+    if (std::strncmp(kname, r.prefix, std::strlen(r.prefix)) == 0) return r.module;
+  return -1;
+}
+
 hipFunction_t Runtime::fn(const char *kname) {
   auto it = functions.find(kname);
   if (it != functions.end()) return it->second;
-  for (hipModule_t m : modules) {
-    hipFunction_t f = nullptr;
-    if (hipModuleGetFunction(&f, m, kname) == hipSuccess && f) {
-      functions.emplace(kname, f);
-      return f;
-    }
+  const int mi = module_of(kname);
+  if (mi < 0 || mi >= (int)modules.size()) return nullptr;
+  hipFunction_t f = nullptr;
+  if (hipModuleGetFunction(&f, modules[mi], kname) == hipSuccess && f) {
+    functions.emplace(kname, f);
+    return f;
   }
-  (void)hipGetLastError();
+  (void)hipGetLastError();  // internal naming error; reported by the caller
   return nullptr;
 }
 
@@ -243,8 +260,12 @@ int rxw8_runtime_create(int device, rxw8_runtime **out) {
   // Development hook: RXW8_CODE_OBJECT_DIR=<dir> loads <dir>/<name>.hsaco in
   // place of the embedded code object of that name when the file exists.
   const char *override_dir = std::getenv("RXW8_CODE_OBJECT_DIR");
-  for (auto &blob : blobs) {
-    if (blob.end - blob.begin <= 0) continue;
+  for (auto &blob : blobs) {  // order = module indices of module_of()
+    if (blob.end - blob.begin <= 0) {
+      for (hipModule_t mm : rt->modules) (void)hipModuleUnload(mm);
+      delete rt;
+      return fail(RXW8_INTERNAL, "embedded code object %s is empty", blob.name);
+    }
     hipModule_t m = nullptr;
     std::string path;
     if (override_dir && *override_dir) {

@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -79,3 +80,19 @@ def test_runtime_create_without_device_is_failed_precondition():
         rx.Runtime(0)
     assert e.value.code == rx.Status.FAILED_PRECONDITION
     assert not e.value.is_retryable
+
+
+@pytest.mark.parametrize("order", ["rxla_amd,torch", "torch,rxla_amd"])
+def test_one_hip_runtime_with_torch_in_either_import_order(order):
+    """librxw8.so and PyTorch must share one HIP/HSA runtime whichever is
+    imported first (two runtimes in one process do not see the GPU twice)."""
+    _ensure_built()
+    code = (f"import sys; sys.path.insert(0, {ROOT!r})\n"
+            f"import {order.split(',')[0]}\nimport {order.split(',')[1]}\n"
+            "maps = open('/proc/self/maps').read().splitlines()\n"
+            "hip = {l.split()[-1] for l in maps if 'libamdhip64' in l}\n"
+            "hsa = {l.split()[-1] for l in maps if 'libhsa-runtime64' in l}\n"
+            "print(len(hip), len(hsa))\n")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         timeout=300, check=True).stdout.split()
+    assert out[-2:] == ["1", "1"], out

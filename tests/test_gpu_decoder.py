@@ -79,6 +79,27 @@ def test_decoder_prefill_and_decode_match_oracle(rt, group):
     np.testing.assert_array_equal(model.lens()[:batch], [12, 12])
 
 
+def test_decoder_long_prefill_matches_oracle(rt):
+    """2 x 40 prompt rows: every projection of the prefill runs on the M > 64
+    GEMM, including the residual (h += bf16(o_proj), h += bf16(down)) epilogue."""
+    cfg = small_cfg(max_seq=48, group=128)
+    params = tiny_params(cfg, seed=81, std=0.05)
+    batch = 2
+    model = build(rt, cfg, params, batch)
+    dec = oracle.Decoder(cfg, params, batch)
+    ids = np.random.default_rng(82).integers(0, cfg["vocab"], (batch, 40)).astype(np.int32)
+    lg, nxt, rlg, rnxt = step_both(rt, model, dec, ids)
+    err = rel_err(lg, rlg)
+    print(f"long prefill logits rel_err={err:.3e}")
+    assert err <= 1e-2
+    for step in range(3):
+        lg, nxt, rlg, rnxt = step_both(rt, model, dec, rnxt.reshape(batch, 1).astype(np.int32))
+        err = rel_err(lg, rlg)
+        print(f"decode step {step} rel_err={err:.3e}")
+        assert err <= 1e-2
+    np.testing.assert_array_equal(model.lens()[:batch], [43, 43])
+
+
 def test_generate_graph_matches_eager_and_oracle(rt):
     r = rx()
     cfg = small_cfg()
