@@ -70,8 +70,8 @@ struct Runtime {
   size_t cached_bytes = 0;
   // workspaces
   Workspace partials;  // f32 split-K partials
-  Workspace counters;  // u32 split-K counters, zeroed at allocation
   Workspace scratch;   // general f32 scratch (attention split-K)
+  Workspace xcast;     // bf16 copy of f32 activations ahead of the GEMM
 
   hipFunction_t fn(const char *name);
 };

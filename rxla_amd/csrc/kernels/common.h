@@ -25,9 +25,13 @@ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_bits_to_f32(f32_to_bf16_bits(f));
 }
 
-// Two f32 -> packed bf16x2 (low half = a).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed bf16x2 (low half = a), round to nearest even: one
+// v_cvt_pk_bf16_f32, the same conversion as f32_to_bf16_bits.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
 // Four u8 codes of one dword -> two dwords of bf16 pairs (exact: 0..255 fit

@@ -1,38 +1,82 @@
 // K2: W8A16 prefill dequant-GEMM on gfx950 MFMA.
 //
-//   y[m, n] = bf16( sum_k bf16(x[m, k]) * bf16((u8[n, k] - 128) * s[n, k / G]) )
+//   y[m, n] = bf16( sum_k x[m, k] * bf16((u8[n, k] - 128) * s[n, k / G]) )
 //
-// i.e. exactly the reference's cast points (crates/rxla-nn/src/layers.rs:
-// 277-296): the weight is dequantised in f32, rounded to bf16, contracted
-// against bf16 activations with f32 accumulation, and the result rounded to
-// bf16. In a GEMM each weight element is reused by a whole tile of
-// activation rows, so the dequantisation is done once per element while the
-// tile is staged into LDS.
+// with x already bf16: exactly the reference's cast points (crates/rxla-nn/
+// src/layers.rs:277-296): the weight is dequantised in f32 (one rounding),
+// rounded to bf16, contracted against bf16 activations with f32
+// accumulation, and the result rounded to bf16. (f32 activations are rounded
+// to bf16 by rxw8_gemm_cast_x first, the x.cast(BF16) of the same layer.)
 //
-// Tiling: a 256-thread workgroup (4 waves) computes a 128 (weight rows n) x
-// 128 (activation rows m) output tile; BK = 64. Both operands are staged as
-// bf16 in LDS (double-buffered; the global loads of tile k+1 are in flight
-// while tile k is multiplied). Each wave owns 64 n x 64 m = 4 x 4 tiles of
-// v_mfma_f32_16x16x32_bf16 with the weights as the A operand, so each lane's
-// accumulators hold 4 consecutive n of one m (8-byte bf16 stores).
-// Workgroups are assigned XCD-major: the GPU dispatches workgroup b to XCD
-// b % 8, and this kernel maps the workgroups of one XCD onto a contiguous
-// range of tiles with m fastest, so a weight tile is reused from that XCD's L2.
-// Weights may be row-major [N, K] or in the tiled layout of rxw8_pack_weight.
+// Tiling. A 256-thread workgroup (4 waves) computes a 128 (weight rows n) x TM
+// (activation rows m) output tile, TM = 256 or 128, over k tiles of BK = 64.
+// Wave w owns all 128 n and the m rows [w*TM/4, (w+1)*TM/4): 8 x TM/64
+// v_mfma_f32_16x16x32_bf16 accumulators with the weights as the A operand, so
+// each weight fragment read from LDS feeds TM/64 MFMAs and each activation
+// fragment feeds 8.
+//
+// Staging (double-buffered in LDS, both operands bf16, rows of 64 values =
+// 128 B whose 16-byte chunks are XOR-swizzled by row & 7 so the fragment reads
+// of 8 consecutive rows hit 8 different bank groups):
+//   * activations go global -> LDS by global_load_lds_dwordx4 (LDS DMA: no
+//     VGPRs, no VALU; see dma16); each lane picks the source chunk that lands
+//     in the swizzled slot of its fixed LDS destination;
+//   * int8 weights go through VGPRs and are dequantised once per workgroup:
+//     fma(f32(u), s, -128 s) is the correctly rounded (u - 128) * s (the
+//     exact product plus an exact addend, one rounding; -128 s is exact in f32
+//     for every finite scale below 2^120), then rounded to bf16.
+// The loads of k tile t+1 are issued before the MFMAs of tile t.
+//
+// Tile order is XCD-aware: workgroup b runs on XCD b % 8 and takes the tile
+// b / 8 of that XCD's contiguous share; inside a share tiles go in groups of
+// 8 n tiles with n fastest, so the workgroups an XCD runs at once cover about
+// 8 n x 4 m tiles and reuse both operands from that XCD's L2.
 #include "common.h"
 
+#include <type_traits>
+
+
 struct GemmArgs {
-  const void *x;       // [M, K] bf16 or f32
+  const uint16_t *x;   // [M, K] bf16
   const uint8_t *w;    // [N, K] u8 or packed [N/16, K/64, 1024]
   const float *scale;  // [N, K / G]
   void *y;             // [M, N]
   int M, N, K, G;
-  int x_f32, y_f32, y_mode, w_packed;
+  int y_f32, y_mode, w_packed;
+};
+
+struct CastArgs {
+  const float *x;
+  uint16_t *y;
+  int64_t n;
 };
 
 namespace {
 
-constexpr int TN = 128, TM = 128, BK = 64, LDK = BK + 8;  // LDS row stride (bf16)
+constexpr int TN = 128, BK = 64, GROUP_N = 8;
+
+// global -> LDS DMA of 16 bytes per lane (global_load_lds_dwordx4; lane l
+// writes LDS bytes [lds + 16 l, +16)). Issued from inline asm on purpose: the
+// compiler models the builtin as a flat access of both global memory and LDS
+// and then answers every later LDS or VGPR-load dependency with lgkmcnt(0) /
+// vmcnt(0), which serialises the fragment reads with the MFMAs. The kernels
+// wait for the DMA'd data themselves (explicit vmcnt before each barrier); the
+// compiler, not knowing these loads, can only over-wait for its own.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void *base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, %2"
+               :: "v"(voff), "s"(lds), "s"(base) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const char *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+
+// Byte offset of 16-byte chunk c (0..7) of row r in a swizzled 128-B-row tile.
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 
 __device__ __forceinline__ void gemm_store(const GemmArgs &a, int m, int n, f32x4 v) {
   if (m >= a.M) return;
@@ -53,120 +97,390 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int m, int n, f32x
   }
 }
 
-}  // namespace
+template <int TM>
+__device__ __forceinline__ void gemm_tile(const GemmArgs &a) {
+  constexpr int WM = TM / 4;             // m rows per wave
+  constexpr int FJ = WM / 16;            // m fragments per wave
+  constexpr int W_BYTES = TN * BK * 2;   // bf16 weight tile
+  constexpr int X_BYTES = TM * BK * 2;   // bf16 activation tile
+  constexpr int STAGE = W_BYTES + X_BYTES;
+  constexpr int X_DMA = TM / 32;         // LDS-DMA instructions per wave per k tile
+  constexpr int LOADS = X_DMA + 4;       // vector-memory instructions per lane per k tile
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-extern "C" __global__ void __launch_bounds__(256) rxw8_w8a16_gemm(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sw[2][TN * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sx[2][TM * LDK];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tiles_m = (a.M + TM - 1) / TM, tiles_n = a.N / TN;
   const int ntiles = tiles_m * tiles_n;
-  // XCD-major tile order: workgroup b runs on XCD b % 8.
-  const int b = blockIdx.x;
   const int per_xcd = (ntiles + 7) / 8;
-  const int tile = (b % 8) * per_xcd + b / 8;
-  if (tile >= ntiles) return;
-  const int tn = tile / tiles_m, tm = tile - tn * tiles_m;
-  const int n0 = tn * TN, m0 = tm * TM;
-  const int groups = a.K / a.G;
-  const int KT = a.K / BK;
+  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t >= ntiles) return;
+  const int group = t / (GROUP_N * tiles_m);
+  const int first_n = group * GROUP_N;
+  const int gw = min(GROUP_N, tiles_n - first_n);
+  const int r = t - group * GROUP_N * tiles_m;
+  const int n0 = (first_n + r % gw) * TN, m0 = (r / gw) * TM;
+  const int KT = a.K / BK, groups = a.K / a.G, last = KT - 1;
 
-  // staging assignment: W: 512 slices of 16 codes (row = id / 4, kq = id % 4);
-  // X: 1024 slices of 8 values (row = id / 8, kq = id % 8).
-  u32x4 wreg[2], xreg[4];
-  float wsc[2];
-  auto load_tile = [&](int kt) {
-    const int k0 = kt * BK;
+  // Three LDS stages, stage s = [bf16 weight tile | bf16 activation tile];
+  // k tile kt lives in stage kt % 3.
+  __shared__ __attribute__((aligned(1024))) char smem[3 * STAGE];
+
+  // activation DMA: instruction i of this wave fills LDS rows 8*(wave*X_DMA+i) ..+8;
+  // lane -> row += lane / 8, physical chunk lane % 8 <- logical chunk (lane%8)^(row&7).
+  // Byte offsets from x stay below 2^31 (checked by the host).
+  uint32_t xoff[X_DMA];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int id = tid + 256 * p, row = id >> 2, kq = id & 3;
-      const int n = n0 + row;
-      const uint8_t *src;
-      if (a.w_packed) {
-        const int l = (row & 15) + 16 * kq;
-        src = a.w + (((int64_t)(n >> 4) * (a.K / 64) + kt) * 1024 + l * 16);
-      } else {
-        src = a.w + (int64_t)n * a.K + k0 + kq * 16;
-      }
-      wreg[p] = *(const u32x4 *)src;
-      wsc[p] = a.scale[(int64_t)n * groups + (k0 + kq * 16) / a.G];
-    }
+  for (int i = 0; i < X_DMA; ++i) {
+    const int row = (wave * X_DMA + i) * 8 + (lane >> 3);
+    const int m = min(m0 + row, a.M - 1);  // rows past M repeat the last row (not stored)
+    xoff[i] = (uint32_t)m * (uint32_t)a.K * 2u + ((uint32_t)((lane & 7) ^ (row & 7)) << 4);
+  }
+  const char *xbase = (const char *)a.x;
+  auto issue_x = [&](int kt, int stage) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int id = tid + 256 * p, row = id >> 3, kq = id & 7;
-      const int m = m0 + row;
-      xreg[p] = m < a.M ? load_x8(a.x, (int64_t)m * a.K + k0 + kq * 8, a.x_f32 != 0)
-                        : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int id = tid + 256 * p, row = id >> 2, kq = id & 3;
-      const float s = wsc[p];
-      u32x4 lo, hi;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t w4 = wreg[p][e];
-        const float f0 = ((float)(w4 & 0xffu) + -128.0f) * s;
-        const float f1 = ((float)((w4 >> 8) & 0xffu) + -128.0f) * s;
-        const float f2 = ((float)((w4 >> 16) & 0xffu) + -128.0f) * s;
-        const float f3 = ((float)(w4 >> 24) + -128.0f) * s;
-        const uint32_t p01 = pack_bf16x2(f0, f1), p23 = pack_bf16x2(f2, f3);
-        if (e < 2) {
-          lo[2 * e] = p01;
-          lo[2 * e + 1] = p23;
-        } else {
-          hi[2 * (e - 2)] = p01;
-          hi[2 * (e - 2) + 1] = p23;
-        }
-      }
-      u32x4 *dst = (u32x4 *)(sw[buf] + row * LDK + kq * 16);
-      dst[0] = lo;
-      dst[1] = hi;
-    }
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int id = tid + 256 * p, row = id >> 3, kq = id & 7;
-      *(u32x4 *)(sx[buf] + row * LDK + kq * 8) = xreg[p];
-    }
+    for (int i = 0; i < X_DMA; ++i)
+      dma16(xbase, xoff[i] + (uint32_t)(kt * (BK * 2)),
+            lds_addr(smem + stage * STAGE + W_BYTES + (wave * X_DMA + i) * 1024));
   };
 
-  const int wn = wave & 1, wm = wave >> 1;  // wave's 64 n x 64 m quadrant
+  // weights: 512 slices of 16 codes per k tile, 2 per thread (row = id / 4,
+  // kq = id % 4); G % 64 == 0, so one scale per row and k tile.
+  const int kstride = a.w_packed ? 1024 : BK;  // bytes between k tiles of a slice
+  uint32_t woff[2], soff[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int id = tid + 256 * p, row = id >> 2, kq = id & 3;
+    const int n = n0 + row;
+    woff[p] = a.w_packed
+                  ? ((uint32_t)(n >> 4) * (uint32_t)KT * 1024u + (uint32_t)((row & 15) + 16 * kq) * 16u)
+                  : (uint32_t)n * (uint32_t)a.K + (uint32_t)kq * 16u;
+    soff[p] = (uint32_t)n * (uint32_t)groups;
+  }
+  struct WSet {
+    u32x4 w[2];
+    float s[2];
+  };
+  auto load_w = [&](int kt, WSet &ws) {
+    const int gi = kt * BK / a.G;  // uniform
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      ws.w[p] = *(const u32x4 *)(a.w + woff[p] + (uint32_t)(kt * kstride));
+      ws.s[p] = a.scale[soff[p] + gi];
+    }
+  };
+  f32x4 acc[8][FJ];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Fragment addresses: rows 16 i + r16 share row & 7, so the swizzled chunk
+  // of a fragment depends on (ks, kg, r16) only and i, j move by whole rows.
   const int r16 = lane & 15, kg = lane >> 4;
-  f32x4 acc[4][4];
+  auto frag_a = [&](int stage, int i, int ks) {
+    return as_bf16x8(*(const u32x4 *)(smem + stage * STAGE + swz(16 * i + r16, ks * 4 + kg)));
+  };
+  auto frag_b = [&](int stage, int j, int ks) {
+    return as_bf16x8(
+        *(const u32x4 *)(smem + stage * STAGE + W_BYTES + swz(wave * WM + 16 * j + r16, ks * 4 + kg)));
+  };
+
+  // One piece of the dequantisation of a weight set: 4 codes of slice p,
+  // dword e; after the last dword of a slice its two LDS chunks are stored.
+  uint32_t hq[8];
+  auto dequant_piece = [&](const WSet &ws, int piece, int stage) {
+    const int p = piece >> 2, e = piece & 3;
+    const float sc = ws.s[p], o = -128.0f * sc;
+    const uint32_t w4 = ws.w[p][e];
+    const float f0 = __builtin_fmaf((float)(w4 & 0xffu), sc, o);
+    const float f1 = __builtin_fmaf((float)((w4 >> 8) & 0xffu), sc, o);
+    const float f2 = __builtin_fmaf((float)((w4 >> 16) & 0xffu), sc, o);
+    const float f3 = __builtin_fmaf((float)(w4 >> 24), sc, o);
+    hq[2 * e] = pack_bf16x2(f0, f1);
+    hq[2 * e + 1] = pack_bf16x2(f2, f3);
+    if (e == 3) {
+      const int id = tid + 256 * p, row = id >> 2, kq = id & 3;
+      char *dst = smem + stage * STAGE;
+      *(u32x4 *)(dst + swz(row, 2 * kq)) = u32x4{hq[0], hq[1], hq[2], hq[3]};
+      *(u32x4 *)(dst + swz(row, 2 * kq + 1)) = u32x4{hq[4], hq[5], hq[6], hq[7]};
+    }
+  };
+
+  // Pipeline: activations are DMA'd 2 k tiles ahead, weights loaded 3 ahead
+  // into registers (three sets); tile kt+1's weights are dequantised into
+  // LDS while tile kt is multiplied. Past the last tile the loads repeat tile
+  // KT-1 into slots nobody reads again, so every k tile issues the same
+  // LOADS vector-memory instructions and the wait counts below hold.
+  // Barriers are plain s_barrier after explicit waits: __syncthreads()'s
+  // workgroup fence would also wait for every load in flight (vmcnt(0)),
+  // draining the prefetch each k tile. The "memory" clobbers keep the compiler
+  // from moving LDS accesses across them.
+  WSet w0, w1, w2;
+  issue_x(0, 0);
+  load_w(0, w0);
+  issue_x(min(1, last), 1);
+  load_w(min(1, last), w1);
+  load_w(min(2, last), w2);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int piece = 0; piece < 8; ++piece) dequant_piece(w0, piece, 0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // One k tile in 16 groups (ks, i): the 4 (FJ) MFMAs of weight fragment i
+  // run while the next fragment is read from LDS; during ks = 1 each group
+  // also dequantises a piece of tile kt+1's weights. sched_barrier pins the
+  // group order so register use stays at two weight fragments.
+  auto step = [&](int kt, auto xs, WSet &load_set, const WSet &deq_set) {
+    constexpr int cur = decltype(xs)::value, nxt = (cur + 1) % 3, fut = (cur + 2) % 3;
+    issue_x(min(kt + 2, last), fut);
+    load_w(min(kt + 3, last), load_set);
+    bf16x8 af[2], bf[FJ], bn[FJ];
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) bf[j] = frag_b(cur, j, 0);
+    af[0] = frag_a(cur, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // ks = 0
+      if (i < 7) {
+        af[(i + 1) & 1] = frag_a(cur, i + 1, 0);
+      } else {
+        af[0] = frag_a(cur, 0, 1);
+#pragma unroll
+        for (int j = 0; j < FJ; ++j) bn[j] = frag_b(cur, j, 1);
+      }
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) acc[i][j] = mfma16x16x32(af[i & 1], bf[j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // weights of tile kt+1 were loaded two k tiles ago: at least the 2 * LOADS
+    // instructions of the last two k tiles are younger
+    if constexpr (LOADS == 12) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // ks = 1
+      if (i < 7) af[(i + 1) & 1] = frag_a(cur, i + 1, 1);
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) acc[i][j] = mfma16x16x32(af[i & 1], bn[j], acc[i][j]);
+      dequant_piece(deq_set, i, nxt);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // activation tile kt+1 was DMA'd last k tile: this tile's LOADS are younger
+    if constexpr (LOADS == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  int kt = 0;
+  for (; kt + 3 <= KT; kt += 3) {
+    step(kt, S0{}, w0, w1);
+    step(kt + 1, S1{}, w1, w2);
+    step(kt + 2, S2{}, w2, w0);
+  }
+  if (kt < KT) step(kt, S0{}, w0, w1);
+  if (kt + 1 < KT) step(kt + 1, S1{}, w1, w2);
+
+  // lane holds D[n = 16 i + 4 kg + r][m = 16 j + r16]
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j)
+      gemm_store(a, m0 + wave * WM + 16 * j + r16, n0 + 16 * i + 4 * kg, acc[i][j]);
+}
+
+
+// 256 x 256 output tiles for long inputs: 512 threads (8 waves, two per SIMD,
+// so one wave's LDS and memory waits are covered by the other's MFMAs). Wave w
+// owns weight rows [128 (w & 1), +128) and activation rows [64 (w >> 1), +64):
+// 8 x 4 accumulators, 12 fragment reads per 32 MFMAs. Two LDS stages of
+// [bf16 weight tile 32 KB | bf16 activation tile 32 KB]; activations are DMA'd
+// one k tile ahead, weights loaded two ahead into two register sets.
+__device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
+  constexpr int TNB = 256, TMB = 256;
+  constexpr int W_BYTES = TNB * BK * 2, X_BYTES = TMB * BK * 2, STAGE = W_BYTES + X_BYTES;
+  constexpr int X_DMA = TMB * BK * 2 / 1024 / 8;  // 4 LDS-DMA instructions per wave per k tile
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1, wm = wave >> 1;
+
+  const int tiles_m = (a.M + TMB - 1) / TMB, tiles_n = a.N / TNB;
+  const int ntiles = tiles_m * tiles_n;
+  const int per_xcd = (ntiles + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t >= ntiles) return;
+  constexpr int GN = 4;  // n tiles per group: the 32 workgroups of an XCD cover ~4 n x 8 m tiles
+  const int group = t / (GN * tiles_m);
+  const int first_n = group * GN;
+  const int gw = min(GN, tiles_n - first_n);
+  const int r = t - group * GN * tiles_m;
+  const int n0 = (first_n + r % gw) * TNB, m0 = (r / gw) * TMB;
+  const int KT = a.K / BK, groups = a.K / a.G, last = KT - 1;
+
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+  uint32_t xoff[X_DMA];
+#pragma unroll
+  for (int i = 0; i < X_DMA; ++i) {
+    const int row = (wave * X_DMA + i) * 8 + (lane >> 3);
+    const int m = min(m0 + row, a.M - 1);  // rows past M repeat the last row (not stored)
+    xoff[i] = (uint32_t)m * (uint32_t)a.K * 2u + ((uint32_t)((lane & 7) ^ (row & 7)) << 4);
+  }
+  const char *xbase = (const char *)a.x;
+  auto issue_x = [&](int kt, int stage) {
+#pragma unroll
+    for (int i = 0; i < X_DMA; ++i)
+      dma16(xbase, xoff[i] + (uint32_t)(kt * (BK * 2)),
+            lds_addr(smem + stage * STAGE + W_BYTES + (wave * X_DMA + i) * 1024));
+  };
+
+  // weights: 1024 slices of 16 codes per k tile, 2 per thread (row = id / 4, kq = id % 4)
+  const int kstride = a.w_packed ? 1024 : BK;
+  uint32_t woff[2], soff[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int id = tid + 512 * p, row = id >> 2, kq = id & 3;
+    const int n = n0 + row;
+    woff[p] = a.w_packed
+                  ? ((uint32_t)(n >> 4) * (uint32_t)KT * 1024u + (uint32_t)((row & 15) + 16 * kq) * 16u)
+                  : (uint32_t)n * (uint32_t)a.K + (uint32_t)kq * 16u;
+    soff[p] = (uint32_t)n * (uint32_t)groups;
+  }
+  struct WSet {
+    u32x4 w[2];
+    float s[2];
+  };
+  auto load_w = [&](int kt, WSet &ws) {
+    const int gi = kt * BK / a.G;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      ws.w[p] = *(const u32x4 *)(a.w + woff[p] + (uint32_t)(kt * kstride));
+      ws.s[p] = a.scale[soff[p] + gi];
+    }
+  };
+  uint32_t hq[8];
+  auto dequant_piece = [&](const WSet &ws, int piece, int stage) {
+    const int p = piece >> 2, e = piece & 3;
+    const float sc = ws.s[p], o = -128.0f * sc;
+    const uint32_t w4 = ws.w[p][e];
+    const float f0 = __builtin_fmaf((float)(w4 & 0xffu), sc, o);
+    const float f1 = __builtin_fmaf((float)((w4 >> 8) & 0xffu), sc, o);
+    const float f2 = __builtin_fmaf((float)((w4 >> 16) & 0xffu), sc, o);
+    const float f3 = __builtin_fmaf((float)(w4 >> 24), sc, o);
+    hq[2 * e] = pack_bf16x2(f0, f1);
+    hq[2 * e + 1] = pack_bf16x2(f2, f3);
+    if (e == 3) {
+      const int id = tid + 512 * p, row = id >> 2, kq = id & 3;
+      char *dst = smem + stage * STAGE;
+      *(u32x4 *)(dst + swz(row, 2 * kq)) = u32x4{hq[0], hq[1], hq[2], hq[3]};
+      *(u32x4 *)(dst + swz(row, 2 * kq + 1)) = u32x4{hq[4], hq[5], hq[6], hq[7]};
+    }
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int r16 = lane & 15, kg = lane >> 4;
+  auto frag_a = [&](int stage, int i, int ks) {
+    return as_bf16x8(*(const u32x4 *)(smem + stage * STAGE + swz(wn * 128 + 16 * i + r16, ks * 4 + kg)));
+  };
+  auto frag_b = [&](int stage, int j, int ks) {
+    return as_bf16x8(
+        *(const u32x4 *)(smem + stage * STAGE + W_BYTES + swz(wm * 64 + 16 * j + r16, ks * 4 + kg)));
+  };
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) load_tile(kt + 1);
+  // Every k tile issues X_DMA activation DMAs, then 4 weight/scale loads per
+  // lane (past the last tile they repeat tile KT-1 into slots nobody reads),
+  // so the wait counts are exact. Plain s_barrier after explicit waits, as
+  // __syncthreads()'s fence would wait for all loads in flight.
+  WSet w0, w1;
+  issue_x(0, 0);
+  load_w(0, w0);
+  load_w(min(1, last), w1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      bf16x8 af[4], bfr[4];
+  for (int piece = 0; piece < 8; ++piece) dequant_piece(w0, piece, 0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  auto step = [&](int kt, auto xs, WSet &load_set, const WSet &deq_set) {
+    constexpr int cur = decltype(xs)::value, nxt = cur ^ 1;
+    issue_x(min(kt + 1, last), nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(min(kt + 2, last), load_set);
+    bf16x8 af[2], bf[4], bn[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = as_bf16x8(*(const u32x4 *)(sw[buf] + (wn * 64 + i * 16 + r16) * LDK + ks * 32 + kg * 8));
+    for (int j = 0; j < 4; ++j) bf[j] = frag_b(cur, j, 0);
+    af[0] = frag_a(cur, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bfr[j] = as_bf16x8(*(const u32x4 *)(sx[buf] + (wm * 64 + j * 16 + r16) * LDK + ks * 32 + kg * 8));
+    for (int i = 0; i < 8; ++i) {  // ks = 0
+      if (i < 7) {
+        af[(i + 1) & 1] = frag_a(cur, i + 1, 0);
+      } else {
+        af[0] = frag_a(cur, 0, 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) bn[j] = frag_b(cur, j, 1);
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(af[i & 1], bf[j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (kt + 1 < KT) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-  // epilogue: lane holds D[n = 16i + 4kg + r][m = 16j + r16]
+    // weights of tile kt+1 were loaded last k tile: this tile's 8 loads are younger
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i) {  // ks = 1
+      if (i < 7) af[(i + 1) & 1] = frag_a(cur, i + 1, 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(af[i & 1], bn[j], acc[i][j]);
+      dequant_piece(deq_set, i, nxt);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // activation tile kt+1 (this tile's DMAs) is older than this tile's 4 weight loads
+    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  int kt = 0;
+  for (; kt + 2 <= KT; kt += 2) {
+    step(kt, S0{}, w0, w1);
+    step(kt + 1, S1{}, w1, w0);
+  }
+  if (kt < KT) step(kt, S0{}, w0, w1);
+
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      gemm_store(a, m0 + wm * 64 + j * 16 + r16, n0 + wn * 64 + i * 16 + 4 * kg, acc[i][j]);
+      gemm_store(a, m0 + wm * 64 + 16 * j + r16, n0 + wn * 128 + 16 * i + 4 * kg, acc[i][j]);
+}
+
+}  // namespace
+
+// Launch contract (checked by the host): N % 128 == 0, K % 64 == 0,
+// G % 64 == 0 and K % G == 0, M >= 1, M * K * 2 < 2^31 and the weight bytes
+// < 2^32; grid = 8 * ceil(tiles / 8) workgroups.
+extern "C" __global__ void __launch_bounds__(512) rxw8_w8a16_gemm_t256(GemmArgs a) {
+  gemm_tile_big(a);
+}
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_w8a16_gemm_m256(GemmArgs a) {
+  gemm_tile<256>(a);
+}
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_w8a16_gemm_m128(GemmArgs a) {
+  gemm_tile<128>(a);
+}
+
+// f32 activations -> bf16 (RNE), the x.cast(BF16) ahead of the GEMM.
+extern "C" __global__ void __launch_bounds__(256) rxw8_gemm_cast_x(CastArgs a) {
+  const int64_t n4 = a.n / 4;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float4 v = ((const float4 *)a.x)[i];
+    ((uint2 *)a.y)[i] = uint2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+  }
+  const int64_t tail = a.n - 4 * n4;
+  if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail)
+    a.y[4 * n4 + threadIdx.x] = f32_to_bf16_bits(a.x[4 * n4 + threadIdx.x]);
 }

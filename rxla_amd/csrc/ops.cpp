@@ -43,12 +43,18 @@ struct SplitkReduceArgs {
 };
 
 struct GemmArgs {
-  const void *x;
+  const uint16_t *x;
   const uint8_t *w;
   const float *scale;
   void *y;
   int M, N, K, G;
-  int x_f32, y_f32, y_mode, w_packed;
+  int y_f32, y_mode, w_packed;
+};
+
+struct CastArgs {
+  const float *x;
+  uint16_t *y;
+  int64_t n;
 };
 
 struct DequantArgs {
@@ -318,18 +324,27 @@ namespace rxw8 {
 // Prefill-sized products go to the MFMA GEMM (128 x 128 output tiles; the
 // weight tile is dequantised once per 128 activation rows); smaller M stays on
 // the GEMV, which streams the weights once per 16/32-row chunk.
-static bool gemm_eligible(int64_t M, int64_t N, int64_t G) {
+static bool gemm_eligible(int64_t M, int64_t N, int64_t K, int64_t G) {
   static const int64_t min_m = env_int("RXW8_GEMM_MIN_M", 64);
-  return M > min_m && N % 128 == 0 && G % 16 == 0 && M <= (1LL << 30) && !env_int("RXW8_NO_GEMM", 0);
+  // 32-bit byte offsets inside the kernel: activations M*K*2, weights N*K
+  return M > min_m && N % 128 == 0 && K % 64 == 0 && G % 64 == 0 && M * K * 2 < (1LL << 31) &&
+         N * K < (1LL << 32) && !env_int("RXW8_NO_GEMM", 0);
 }
 
-// Requires K % 64 == 0, N % 128 == 0 and G % 16 == 0 (checked by the callers),
-// so every 16-code staging slice lies inside one scale group.
+// Requires gemm_eligible(): one scale per weight row and 64-deep k tile.
 static int run_gemm(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
                     const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
                     int64_t G, int y_mode) {
+  int rc;
+  if (x_f32) {  // x.cast(BF16) into the runtime's staging buffer, then the bf16 GEMM
+    if ((rc = ensure_workspace(rt, rt->xcast, (size_t)(M * K) * 2, false))) return rc;
+    CastArgs c{(const float *)x, (uint16_t *)rt->xcast.ptr, M * K};
+    if ((rc = launch(rt, "rxw8_gemm_cast_x", dim3(grid_for(M * K / 4 + 1, 256, 4096)), dim3(256), c)))
+      return rc;
+    x = rt->xcast.ptr;
+  }
   GemmArgs a;
-  a.x = x;
+  a.x = (const uint16_t *)x;
   a.w = w;
   a.scale = s;
   a.y = y;
@@ -337,13 +352,36 @@ static int run_gemm(Runtime *rt, const void *x, int x_f32, const uint8_t *w, boo
   a.N = (int)N;
   a.K = (int)K;
   a.G = (int)G;
-  a.x_f32 = x_f32;
   a.y_f32 = y_f32;
   a.y_mode = y_mode;
   a.w_packed = packed ? 1 : 0;
-  const int64_t tiles = (M + 127) / 128 * (N / 128);
+  // Three tilings (one workgroup per CU each): 256 x 256 (8 waves), 256 x 128
+  // and 128 x 128 (4 waves). Pick the best measured per-tile efficiency times
+  // the fraction of CU slots the tile count fills in its last round.
+  struct Tiling {
+    const char *kernel;
+    int tm, tn, threads;
+    double eff;
+  };
+  static const Tiling tilings[] = {{"rxw8_w8a16_gemm_t256", 256, 256, 512, 0.50},
+                                   {"rxw8_w8a16_gemm_m256", 256, 128, 256, 0.36},
+                                   {"rxw8_w8a16_gemm_m128", 128, 128, 256, 0.30}};
+  const int forced = env_int("RXW8_GEMM_TILE", 0);  // 256x256 = 256, 256x128 = 2, 128x128 = 128
+  const Tiling *best = nullptr;
+  double best_score = -1;
+  for (const Tiling &tl : tilings) {
+    if (N % tl.tn) continue;
+    const int code = tl.tn == 256 ? 256 : (tl.tm == 256 ? 2 : 128);
+    if (forced && forced != code) continue;
+    const int64_t tiles = (M + tl.tm - 1) / tl.tm * (N / tl.tn);
+    const int64_t rounds = (tiles + rt->cus - 1) / rt->cus;
+    const double score = tl.eff * (double)tiles / (double)(rounds * rt->cus);
+    if (score > best_score) best_score = score, best = &tl;
+  }
+  if (!best) return fail(RXW8_INVALID_ARGUMENT, "no GEMM tiling for N=%lld", (long long)N);
+  const int64_t tiles = (M + best->tm - 1) / best->tm * (N / best->tn);
   const int64_t per_xcd = (tiles + 7) / 8;
-  return launch(rt, "rxw8_w8a16_gemm", dim3((unsigned)(per_xcd * 8)), dim3(256), a);
+  return launch(rt, best->kernel, dim3((unsigned)(per_xcd * 8)), dim3(best->threads), a);
 }
 
 int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
@@ -351,7 +389,7 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
                    int64_t G, int compute_bf16, int y_mode) {
   if (M == 0) return RXW8_OK;
   if (packed) {
-    if (compute_bf16 && gemm_eligible(M, N, G))
+    if (compute_bf16 && gemm_eligible(M, N, K, G))
       return run_gemm(rt, x, x_f32, w, true, s, y, y_f32, M, N, K, G, y_mode);
     int rc = compute_bf16 ? run_gemv(rt, x, x_f32, w, false, true, s, y, y_f32, M, N, K, G, y_mode)
                           : (int)RXW8_UNIMPLEMENTED;
@@ -364,7 +402,7 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
   const bool mfma_ok = compute_bf16 && K % 64 == 0 && N % 16 == 0 && (G == K || G % 64 == 0) &&
                        K <= (1LL << 30) && N <= (1LL << 30) && !env_int("RXW8_FORCE_GENERIC", 0);
   if (mfma_ok) {
-    if (gemm_eligible(M, N, G)) return run_gemm(rt, x, x_f32, w, false, s, y, y_f32, M, N, K, G, y_mode);
+    if (gemm_eligible(M, N, K, G)) return run_gemm(rt, x, x_f32, w, false, s, y, y_f32, M, N, K, G, y_mode);
     int rc = run_gemv(rt, x, x_f32, w, false, false, s, y, y_f32, M, N, K, G, y_mode);
     if (rc != RXW8_UNIMPLEMENTED) return rc;
   }

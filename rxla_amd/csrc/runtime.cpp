@@ -88,7 +88,7 @@ static int module_of(const char *kname) {
     int module;
   } routes[] = {{"rxw8_gemv_", 0},      {"rxw8_pack_tiles", 0},     {"rxw8_dequant", 1},
                 {"rxw8_linear_generic", 1}, {"rxw8_kv_update", 1}, {"rxw8_gqa_", 2},
-                {"rxw8_w8a16_gemm", 3}, {"rxw8_dec_", 4}};
+                {"rxw8_w8a16_gemm", 3}, {"rxw8_gemm_", 3},   {"rxw8_dec_", 4}};
   for (const auto &r : routes)
     if (std::strncmp(kname, r.prefix, std::strlen(r.prefix)) == 0) return r.module;
   return -1;
@@ -201,7 +201,7 @@ int new_buffer(Runtime *rt, int dtype, const int64_t *dims, int rank, bool zero,
 static void runtime_free(Runtime *rt) {
   if (rt->stream) (void)hipStreamSynchronize(rt->stream);
   for (auto &kv : rt->free_blocks) (void)hipFree(kv.second);
-  for (Workspace *w : {&rt->partials, &rt->counters, &rt->scratch})
+  for (Workspace *w : {&rt->partials, &rt->scratch, &rt->xcast})
     if (w->ptr) (void)hipFree(w->ptr);
   for (hipModule_t m : rt->modules) (void)hipModuleUnload(m);
   if (rt->own_stream) (void)hipStreamDestroy(rt->own_stream);

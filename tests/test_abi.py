@@ -96,3 +96,41 @@ def test_one_hip_runtime_with_torch_in_either_import_order(order):
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
                          timeout=300, check=True).stdout.split()
     assert out[-2:] == ["1", "1"], out
+
+
+def test_every_kernel_routes_to_its_code_object():
+    """runtime.cpp looks a kernel up only in the code object its name prefix
+    selects; every kernel of every source must land in the object built from
+    that source (a miss would surface only as a launch error on the GPU)."""
+    csrc = os.path.join(ROOT, "rxla_amd", "csrc")
+    make = open(os.path.join(csrc, "Makefile")).read()
+    sources = dict(re.findall(r"^CO_(\w+)\s*:=\s*(\S+)", make, flags=re.M))
+    rt_src = open(os.path.join(csrc, "runtime.cpp")).read()
+    order = re.findall(r'\{"(\w+)", rxw8_co_\w+, rxw8_co_\w+_end\}', rt_src)
+    routes = [(p, int(i)) for p, i in re.findall(r'\{"(rxw8_\w+)", (\d+)\}', rt_src)]
+    assert sorted(order) == sorted(sources) and routes
+
+    def module_of(name):
+        for prefix, idx in routes:
+            if name.startswith(prefix):
+                return order[idx]
+        return None
+
+    seen = 0
+    for co, src in sources.items():
+        text = open(os.path.join(csrc, src)).read()
+        # (macro-generated GEMV names are checked by prefix below)
+        names = re.findall(r'extern "C" __global__ void\s+(?:__launch_bounds__\([^)]*\)\s+)?'
+                           r'(rxw8_\w+)\(', text)
+        for name in names:
+            assert module_of(name) == co, (name, co, module_of(name))
+            seen += 1
+    launched = set()
+    for f in ("ops.cpp", "decoder.cpp"):
+        launched |= set(re.findall(r'"(rxw8_[a-z0-9_]+?)(?:%|")', open(os.path.join(csrc, f)).read()))
+    for name in launched:
+        if name.startswith(("rxw8_gemv_w8", "rxw8_gemv_bf16")):
+            continue  # formatted names, checked by prefix below
+        assert module_of(name) is not None, name
+    assert module_of("rxw8_gemv_w8_pk_mb1_rw1_u4") == "gemv"
+    assert seen > 10

@@ -119,3 +119,22 @@ def test_gemm_deterministic(rt):
     a = r.quantized_linear(rt, rt.buffer(x), rt.buffer(u8), rt.buffer(s)).to_numpy()
     b = r.quantized_linear(rt, rt.buffer(x), rt.buffer(u8), rt.buffer(s)).to_numpy()
     np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("tile", [128, 2, 256])  # 128x128, 256x128, 256x256
+@pytest.mark.parametrize("m,n,k,g", [(65, 256, 64, 64), (300, 512, 256, 128), (513, 768, 640, 640)])
+def test_gemm_tile_kernels(rt, monkeypatch, tile, m, n, k, g):
+    """Every tiling (chosen by size in normal use) on ragged M, single- and
+    odd-count k tiles, packed and row-major."""
+    r = rx()
+    monkeypatch.setenv("RXW8_GEMM_TILE", str(tile))
+    rng = np.random.default_rng(m + n + k + tile)
+    x = oracle.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    u8, s = oracle.quantize_w8((rng.standard_normal((n, k)) * 0.02).astype(np.float32), g)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16, oracle.ACCUM_F64, threads=16)
+    xb, wb, sb = rt.buffer(oracle.bf16_bits(x), r.DType.BF16), rt.buffer(u8), rt.buffer(s)
+    y = r.quantized_linear(rt, xb, wb, sb, r.DType.BF16, r.DType.F32).to_numpy()
+    y_pk = r.quantized_linear(rt, xb, r.pack_weight(rt, wb), sb, r.DType.BF16, r.DType.F32).to_numpy()
+    np.testing.assert_array_equal(y_pk, y)
+    err, eq = check(y, ref)
+    print(f"tile={tile} M={m} N={n} K={k} G={g} rel_err={err:.3e} equal={eq:.4f}")
