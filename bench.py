@@ -20,6 +20,20 @@ cpu_baseline = the CPU oracle (reference-order restatement, OpenMP) timed on
 
 Algorithmic bytes per launch: N*K (u8 weights) + 4*N (f32 scales)
 + 2*B*K (bf16 x) + 2*B*N (bf16 y).
+
+Further legs (same JSON line, extra keys; --skip-* to leave one out):
+prefill_gemm  BASELINE configs[2]: x bf16 [M,4096] for M in {512, 2048, 8192}
+              against W [12288,4096] and the [4096,12288] down projection;
+              2*M*N*K flops per launch over the mean launch time (HIP events
+              around back-to-back launches), roofline against dense bf16 MFMA
+decode_attention  BASELINE configs[3]: batch 8, 32/8 heads, D 128, lengths
+              uniform in [512, 8192], bf16 cache; bytes = K and V rows read
+              (lens * 8 heads * 128 * 2 B * 2) + q + out, two cache copies
+decoder       BASELINE configs[4]: 28-layer synthetic decoder (random-init
+              weights, W8 per output channel), batch 8, prompt 1024, 256
+              greedy steps through rxw8_decoder_generate (decode steps replay
+              one HIP graph); decode tokens/s = 8*256 / (generate time -
+              prefill time)
 """
 from __future__ import annotations
 
@@ -35,6 +49,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 K = 4096
 BS = (1, 4, 16)
 NS = (4096, 6144, 24576)
@@ -74,6 +89,147 @@ def cpu_baseline(budget_s=12.0):
                       f"{total_t:.1f} s"}
 
 
+def bench_gemm(rt, rx, torch, stream, reps=10):
+    """C3 prefill dequant-GEMM shapes; returns per-shape TFLOP/s and the MFMA
+    roofline of the largest one."""
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    shapes = [(m, n, k) for m in (512, 2048, 8192) for n, k in ((12288, 4096), (4096, 12288))]
+    with torch.cuda.stream(stream):
+        ws = {(n, k): (torch.randint(1, 256, (n, k), dtype=torch.uint8, device="cuda", generator=gen),
+                       torch.rand((n, 1), device="cuda", generator=gen) * 1e-3 + 1e-4)
+              for n, k in ((12288, 4096), (4096, 12288))}
+        xs = {(m, k): torch.randn((m, k), device="cuda", generator=gen).to(torch.bfloat16)
+              for m in (512, 2048, 8192) for k in (4096, 12288)}
+    stream.synchronize()
+    wb = {key: (rx.pack_weight(rt, rt.wrap_tensor(u)), rt.wrap_tensor(s_)) for key, (u, s_) in ws.items()}
+    rt.synchronize()
+    out = {}
+    for m, n, k in shapes:
+        with torch.cuda.stream(stream):
+            y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        yb, xb, (u, s_) = rt.wrap_tensor(y), rt.wrap_tensor(xs[(m, k)]), wb[(n, k)]
+        for _ in range(2):
+            rx.quantized_linear(rt, xb, u, s_, rx.DType.BF16, out=yb)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            rx.quantized_linear(rt, xb, u, s_, rx.DType.BF16, out=yb)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        out[f"M{m}_N{n}_K{k}"] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * m * n * k / t / 1e12, 1)}
+    big = out["M8192_N12288_K4096"]
+    return out, {"bound": "mfma", "achieved": big["TFLOPs"], "peak": MFMA_BF16_PEAK_TFLOPS,
+                 "unit": "TFLOP/s", "frac": round(big["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                 "traffic": None, "kernel": "rxw8_w8a16_gemm_t256",
+                 "shape": "M=8192 N=12288 K=4096", "mean_launch_us": big["us"],
+                 "timing": f"HIP events around {reps} back-to-back launches"}
+
+
+def bench_attention(rt, rx, torch, stream, reps=20):
+    """C4 decode attention; bytes = the K/V rows each sequence reads + q + out."""
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    B, HQ, HKV, D, LMAX = 8, 32, 8, 128, 8192
+    lens = np.random.default_rng(4).integers(512, 8193, B).astype(np.int32)
+    with torch.cuda.stream(stream):
+        caches = [(torch.randn((B, HKV, LMAX, D), device="cuda", generator=gen).to(torch.bfloat16),
+                   torch.randn((B, HKV, LMAX, D), device="cuda", generator=gen).to(torch.bfloat16))
+                  for _ in range(2)]
+        q = torch.randn((B, HQ, D), device="cuda", generator=gen).to(torch.bfloat16)
+        o = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
+        lt = torch.from_numpy(lens).to("cuda")
+    stream.synchronize()
+    cb = [(rt.wrap_tensor(k), rt.wrap_tensor(v)) for k, v in caches]
+    qb, ob, lb = rt.wrap_tensor(q), rt.wrap_tensor(o), rt.wrap_tensor(lt)
+    nbytes = int(lens.sum()) * HKV * D * 2 * 2 + 2 * B * HQ * D * 2 + 4 * B
+    for c in range(2):
+        rx.grouped_query_attention(rt, qb, cb[c][0], cb[c][1], lb, out=ob)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        rx.grouped_query_attention(rt, qb, cb[i % 2][0], cb[i % 2][1], lb, out=ob)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    gbs = nbytes / t / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernels": "rxw8_gqa_decode_d128_g4 + rxw8_gqa_decode_combine_d128_g4",
+            "us_per_call": round(t * 1e6, 2), "bytes_per_call": nbytes,
+            "lens": lens.tolist(), "timing": f"HIP events around {reps} calls, 2 cache copies"}
+
+
+def bench_decoder(rt, rx, torch, stream, prompt_len=1024, steps=256, batch=8):
+    """C5: random-init W8 decoder; decode tokens/s from generate - prefill."""
+    from rxla_amd.model import DecoderConfig, DecoderModel
+
+    cfg = DecoderConfig(max_batch=batch, max_seq=prompt_len + steps)
+    model = DecoderModel(rt, cfg).compile()
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    keep = []
+    pending_scale = {}
+    with torch.cuda.stream(stream):
+        for path, dtype, shape in model.schema():
+            if path.endswith(".scale"):
+                t = pending_scale.pop(path)
+            elif dtype == rx.DType.U8:
+                w = torch.randn(shape, device="cuda", generator=gen) * 0.02
+                g = cfg.group if cfg.group > 0 else shape[1]
+                wg = w.view(shape[0], shape[1] // g, g)
+                sc = wg.abs().amax(dim=2).clamp_min(1e-12) / 127.0
+                t = (torch.round(wg / sc[:, :, None]).clamp(-127, 127) + 128).to(torch.uint8)
+                t = t.view(shape).contiguous()
+                pending_scale[path[:-len(".weight")] + ".scale"] = sc.contiguous()
+                del w, wg
+            elif dtype == rx.DType.BF16:
+                t = (torch.randn(shape, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+            else:
+                t = torch.ones(shape, device="cuda", dtype=torch.float32)
+            keep.append(t)
+            stream.synchronize()
+            model.bind_parameter(path, rt.wrap_tensor(t))
+    rt.synchronize()
+    ids = np.random.default_rng(5).integers(0, cfg.vocab, (batch, prompt_len)).astype(np.int32)
+    prompt = rt.buffer(ids)
+    out_ids = rt.zeros((batch, steps + 1), rx.DType.I32)
+
+    def timed(fn):
+        model.reset()
+        rt.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        rt.synchronize()
+        return time.perf_counter() - t0
+
+    timed(lambda: model.generate(prompt, steps, out_ids=out_ids, use_graph=True))  # warm + capture
+    t_prefill = min(timed(lambda: model.forward(prompt)) for _ in range(2))
+    t_total = min(timed(lambda: model.generate(prompt, steps, out_ids=out_ids, use_graph=True))
+                  for _ in range(2))
+    t_decode = t_total - t_prefill
+    toks = out_ids.to_numpy()
+    weight_bytes = sum(int(np.prod(sh)) * (1 if dt == rx.DType.U8 else 4 if dt == rx.DType.F32 else 2)
+                       for _, dt, sh in model.schema())
+    kv_bytes = sum(cfg.layers * cfg.kv_heads * cfg.head_dim * 2 * 2 * batch * (prompt_len + i + 1)
+                   for i in range(steps)) / steps
+    step_bytes = weight_bytes + kv_bytes
+    return {"decode_tokens_per_s": round(batch * steps / t_decode, 1),
+            "ms_per_decode_step": round(t_decode / steps * 1e3, 4),
+            "prefill_ms": round(t_prefill * 1e3, 2),
+            "prefill_tokens_per_s": round(batch * prompt_len / t_prefill, 1),
+            "decode_step_bytes": int(step_bytes),
+            "decode_step_GBs": round(step_bytes / (t_decode / steps) / 1e9, 1),
+            "decode_step_hbm_frac": round(step_bytes / (t_decode / steps) / 1e9 / HBM_PEAK_GBS, 4),
+            "config": {"layers": cfg.layers, "hidden": cfg.hidden, "q_heads": cfg.q_heads,
+                       "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim,
+                       "intermediate": cfg.intermediate, "vocab": cfg.vocab, "batch": batch,
+                       "prompt": prompt_len, "steps": steps, "scales": "per-output-channel"},
+            "distinct_tokens": int(len(np.unique(toks))),
+            "timing": "wall clock around rxw8_decoder_generate / rxw8_decoder_forward, "
+                      "synchronized, best of 2"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,6 +237,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--copies", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-gemm", action="store_true")
+    ap.add_argument("--skip-attention", action="store_true")
+    ap.add_argument("--skip-decoder", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are "
@@ -235,6 +394,19 @@ def main():
         "sweep": sweep,
         "device": info,
     }
+    del graphs, weights, wb
+    torch.cuda.synchronize()
+    if not args.skip_gemm:
+        log("prefill GEMM shapes ...")
+        out["prefill_gemm"], out["roofline_gemm"] = bench_gemm(rt, rx, torch, stream)
+        log(json.dumps(out["prefill_gemm"]))
+    if not args.skip_attention:
+        log("decode attention ...")
+        out["roofline_attention"] = bench_attention(rt, rx, torch, stream)
+    if not args.skip_decoder:
+        log("synthetic 28-layer decoder: prefill 8x1024, 256 greedy steps ...")
+        out["decoder"] = bench_decoder(rt, rx, torch, stream)
+        log(json.dumps(out["decoder"]))
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle) ...")
         out["cpu_baseline"] = cpu_baseline()

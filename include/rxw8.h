@@ -197,7 +197,7 @@ int rxw8_kv_update_at(rxw8_runtime *rt, rxw8_buffer *k_cache,
 typedef struct rxw8_decoder_config {
   int64_t layers, hidden, q_heads, kv_heads, head_dim, intermediate, vocab;
   int64_t max_batch, max_seq; /* KV capacity */
-  int64_t group;              /* W8 group size; == hidden for per-channel */
+  int64_t group;              /* W8 group size; 0 = per output channel (every projection) */
   float eps, theta;
   int32_t qk_norm; /* per-head q/k RMSNorm before RoPE */
 } rxw8_decoder_config;

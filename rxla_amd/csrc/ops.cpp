@@ -164,8 +164,11 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
   const int64_t tiles = (n + 16 * p.rw - 1) / (16 * p.rw);
   const int forced_ks = env_int("RXW8_GEMV_KSPLIT", 0);
   const bool per_channel = g == k;
-  int valid[8], nvalid = 0;
-  for (int ks = 1; ks <= 64; ks *= 2) {
+  // k splits: powers of two, and multiples of 3 for widths like 6144 whose
+  // scale groups (e.g. 2048) no power-of-two split keeps whole
+  static const int splits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
+  int valid[12], nvalid = 0;
+  for (int ks : splits) {
     if (k % ks) continue;
     const int64_t kc = k / ks;
     if (kc % kw || (kc / kw) % (2 * slice)) continue;  // even slices per wave

@@ -30,7 +30,7 @@ class DecoderConfig:
     vocab: int = 151936
     max_batch: int = 8
     max_seq: int = 1280
-    group: int = 2048  # == hidden: per-output-channel scales
+    group: int = 0  # 0: per-output-channel scales on every projection
     eps: float = 1e-6
     theta: float = 1e6
     qk_norm: bool = True

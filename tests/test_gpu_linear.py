@@ -174,7 +174,8 @@ def test_bf16_weight_linear_lm_head(rt):
 
 
 @pytest.mark.parametrize("b,n,k,g", [(1, 4096, 4096, 4096), (16, 6144, 4096, 4096),
-                                     (8, 2048, 2048, 128), (4, 1024, 6144, 6144)])
+                                     (8, 2048, 2048, 128), (4, 1024, 6144, 6144),
+                                     (8, 2048, 6144, 2048)])  # 3-way k split
 def test_packed_weights_bit_identical(rt, b, n, k, g):
     """The tiled layout holds the same bytes: results equal the row-major path."""
     r = rx()
