@@ -55,7 +55,13 @@ struct EmbedArgs {
   const int32_t *ids;
   const uint16_t *table;
   float *h;
+  float *ss;
   int64_t T, V, H;
+};
+struct InterleaveArgs {
+  const float *src;
+  float *dst;
+  int64_t half, cols;
 };
 struct RmsNormArgs {
   const float *x;
@@ -80,6 +86,7 @@ struct SiluMulArgs {
   const uint16_t *gu;
   uint16_t *act;
   int64_t T, I;
+  int interleaved;
 };
 struct ArgmaxArgs {
   const float *x;
@@ -95,6 +102,7 @@ struct PackArgs {
   int64_t n, k;
   int kb;
   int esize;
+  int64_t ilv_half;
 };
 struct RecordArgs {
   const int32_t *next;
@@ -113,6 +121,7 @@ struct ParamSpec {
   int64_t dims[2] = {0, 0};
   Buffer *bound = nullptr;   // retained caller buffer
   Buffer *packed = nullptr;  // tiled copy owned by the decoder (U8 weights, embedding)
+  Buffer *perm = nullptr;    // gate|up scales in SwiGLU row order (owned by the decoder)
 };
 
 struct Decoder {
@@ -139,6 +148,10 @@ struct Decoder {
   uint16_t *xl = nullptr;
   float *logits = nullptr, *am_val = nullptr;
   int32_t *am_idx = nullptr, *next = nullptr, *ids1 = nullptr;
+  // sums of squares of residual rows for the fused schedule (<= 32 tokens):
+  // embedding rows [T]; o_proj and down partials [H/16][T]
+  float *ss_embed = nullptr, *ss_o = nullptr, *ss_down = nullptr;
+  bool gu_ilv = false;  // gate|up weights and scales stored in SwiGLU row order
   void *tail_block = nullptr;
   size_t tail_bytes = 0;
   int am_chunks = 64;
@@ -182,6 +195,7 @@ static void free_decoder_memory(Decoder *d) {
   for (ParamSpec &s : d->params) {
     if (s.bound) rxw8_buffer_release(static_cast<rxw8_buffer *>(s.bound));
     if (s.packed) rxw8_buffer_release(static_cast<rxw8_buffer *>(s.packed));
+    if (s.perm) rxw8_buffer_release(static_cast<rxw8_buffer *>(s.perm));
   }
 }
 
@@ -228,9 +242,24 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s)
     DecPosArgs a{d->d_lens, d->pos, d->row_seq, d->row_len, (int)b, (int)s};
     if ((rc = launch(rt, "rxw8_dec_positions", dim3(blocks(T)), dim3(256), a))) return rc;
   }
+  // Decode-sized steps run the fused schedule, 7 launches per layer: the
+  // residual-writing GEMVs (o_proj, down) also emit per-16-channel sums of
+  // squares of the new residual rows, from which the next projection (QKV,
+  // gate|up) forms the RMSNorm scale while it stages its activations; gate|up
+  // applies SiLU*up in its epilogue (weights in 8 gate + 8 up row tiles); no
+  // split-K reduce launches. It needs every projection in one GEMV launch.
+  // Longer inputs (prefill) use the GEMM and separate norm/SwiGLU kernels.
+  const char *unfused = std::getenv("RXW8_DEC_UNFUSED");
+  const bool fused =
+      T <= 32 && !(unfused && *unfused == '1') && d->gu_ilv && d->H % 16 == 0 &&
+      gemv_single_launch(rt, T, d->QKV, d->H, d->group_for(d->H)) &&
+      gemv_single_launch(rt, T, d->H, d->Hq * d->D, d->group_for(d->Hq * d->D)) &&
+      gemv_single_launch(rt, T, 2 * d->I, d->H, d->group_for(d->H)) &&
+      gemv_single_launch(rt, T, d->H, d->I, d->group_for(d->I));
   {
     const ParamSpec &e = d->p(-1, P_EMBED);
-    EmbedArgs a{ids, (const uint16_t *)e.bound->ptr, d->h, T, d->V, d->H};
+    EmbedArgs a{ids, (const uint16_t *)e.bound->ptr, d->h, fused ? d->ss_embed : nullptr, T, d->V,
+                d->H};
     if ((rc = launch(rt, "rxw8_dec_embed", dim3((unsigned)T), dim3(256), a))) return rc;
   }
   const size_t layer_cache = (size_t)d->Bmax * d->Hkv * d->Lmax * d->D;
@@ -241,15 +270,27 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s)
       return (const uint8_t *)(ps.packed ? ps.packed->ptr : ps.bound->ptr);
     };
     auto packed = [&](int kind) { return d->p(l, kind).packed != nullptr; };
-    auto fptr = [&](int kind) { return (const float *)d->p(l, kind).bound->ptr; };
-    // input RMSNorm -> bf16
-    {
+    auto fptr = [&](int kind) {
+      const ParamSpec &ps = d->p(l, kind);
+      return (const float *)(ps.perm ? ps.perm->ptr : ps.bound->ptr);
+    };
+    // input RMSNorm -> fused QKV projection. Decode-sized steps fold the norm
+    // into the GEMV's activation staging (one launch instead of two).
+    if (fused) {
+      GemvOptions o;
+      o.mode = 3, o.norm_w = fptr(P_IN_NORM), o.eps = d->cfg.eps, o.prefer_ks1 = true;
+      o.ss_in = l == 0 ? d->ss_embed : d->ss_down;
+      o.ss_parts = l == 0 ? 1 : (int)(d->H / 16);
+      if ((rc = gemv_launch(rt, d->h, 1, wptr(P_QKV_W), false, packed(P_QKV_W), fptr(P_QKV_S),
+                            d->qkv, 0, T, d->QKV, d->H, d->group_for(d->H), 0, o)))
+        return rc;
+    } else {
       RmsNormArgs a{d->h, fptr(P_IN_NORM), d->xn, nullptr, d->H, (int)T, 1, 0, d->cfg.eps};
       if ((rc = launch(rt, "rxw8_dec_rmsnorm", dim3((unsigned)T), dim3(256), a))) return rc;
+      if ((rc = qlinear_launch(rt, d->xn, 0, wptr(P_QKV_W), packed(P_QKV_W), fptr(P_QKV_S),
+                               d->qkv, 0, T, d->QKV, d->H, d->group_for(d->H), 1, 0)))
+        return rc;
     }
-    if ((rc = qlinear_launch(rt, d->xn, 0, wptr(P_QKV_W), packed(P_QKV_W), fptr(P_QKV_S), d->qkv,
-                             0, T, d->QKV, d->H, d->group_for(d->H), 1, 0)))
-      return rc;
     uint16_t *kcl = (uint16_t *)d->kc + (size_t)l * layer_cache;
     uint16_t *vcl = (uint16_t *)d->vc + (size_t)l * layer_cache;
     {
@@ -264,6 +305,25 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s)
     if ((rc = attention_launch(rt, d->q, 1, kcl, vcl, 0, d->row_len, d->row_seq, nullptr, 0, 0,
                                d->attn, 0, T, d->Hq, d->Hkv, d->Lmax, d->D, scale)))
       return rc;
+    if (fused) {
+      GemvOptions o;
+      o.prefer_ks1 = true, o.ss_out = d->ss_o;
+      if ((rc = gemv_launch(rt, d->attn, 0, wptr(P_O_W), false, packed(P_O_W), fptr(P_O_S), d->h, 1,
+                            T, d->H, d->Hq * d->D, d->group_for(d->Hq * d->D), 1, o)))
+        return rc;
+      GemvOptions g;
+      g.mode = 3, g.norm_w = fptr(P_POST_NORM), g.eps = d->cfg.eps;
+      g.ss_in = d->ss_o, g.ss_parts = (int)(d->H / 16), g.prefer_ks1 = true, g.swiglu = true;
+      if ((rc = gemv_launch(rt, d->h, 1, wptr(P_GU_W), false, packed(P_GU_W), fptr(P_GU_S), d->act,
+                            0, T, 2 * d->I, d->H, d->group_for(d->H), 0, g)))
+        return rc;
+      GemvOptions dn;
+      dn.prefer_ks1 = true, dn.ss_out = d->ss_down;
+      if ((rc = gemv_launch(rt, d->act, 0, wptr(P_DOWN_W), false, packed(P_DOWN_W), fptr(P_DOWN_S),
+                            d->h, 1, T, d->H, d->I, d->group_for(d->I), 1, dn)))
+        return rc;
+      continue;
+    }
     if ((rc = qlinear_launch(rt, d->attn, 0, wptr(P_O_W), packed(P_O_W), fptr(P_O_S), d->h, 1, T,
                              d->H, d->Hq * d->D, d->group_for(d->Hq * d->D), 1, 1)))
       return rc;
@@ -275,7 +335,7 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s)
                              2 * d->I, d->H, d->group_for(d->H), 1, 0)))
       return rc;
     {
-      SiluMulArgs a{d->gu, d->act, T, d->I};
+      SiluMulArgs a{d->gu, d->act, T, d->I, d->gu_ilv ? 1 : 0};
       if ((rc = launch(rt, "rxw8_dec_silu_mul", dim3(blocks(T * d->I, 256 * 4)), dim3(256), a)))
         return rc;
     }
@@ -384,8 +444,10 @@ int rxw8_decoder_create(rxw8_runtime *rt, const rxw8_decoder_config *cfg, rxw8_d
   if (e == hipSuccess) e = hipMalloc(&d->vc, d->cache_bytes);
   if (e == hipSuccess) e = hipMalloc((void **)&d->d_lens, 256 + (size_t)d->Bmax * 4);
   if (e == hipSuccess) e = hipMalloc((void **)&d->d_freqs, (size_t)d->D / 2 * 4);
+  const size_t ss_floats = 32 + 2 * (size_t)(d->H / 16) * 32;
   const size_t tail = (size_t)d->Bmax * d->H * 2 + (size_t)d->Bmax * d->V * 4 +
-                      (size_t)d->Bmax * d->am_chunks * 8 + (size_t)d->Bmax * 8 + 4096;
+                      (size_t)d->Bmax * d->am_chunks * 8 + (size_t)d->Bmax * 8 + ss_floats * 4 +
+                      4096;
   if (e == hipSuccess) e = hipMalloc(&d->tail_block, tail);
   if (e != hipSuccess) {
     rc = hip_fail(e, "hipMalloc (decoder state)");
@@ -401,6 +463,10 @@ int rxw8_decoder_create(rxw8_runtime *rt, const rxw8_decoder_config *cfg, rxw8_d
   d->am_val = (float *)take((size_t)d->Bmax * d->am_chunks * 4);
   d->am_idx = (int32_t *)take((size_t)d->Bmax * d->am_chunks * 4);
   d->next = (int32_t *)take((size_t)d->Bmax * 4);
+  d->ss_embed = (float *)take(32 * 4);
+  d->ss_o = (float *)take((size_t)(d->H / 16) * 32 * 4);
+  d->ss_down = (float *)take((size_t)(d->H / 16) * 32 * 4);
+  d->gu_ilv = d->I % 8 == 0 && (2 * d->I) % 16 == 0 && d->H % 64 == 0;
   d->d_step = d->d_lens + 64;  // device step counter for generate
   std::vector<float> freqs((size_t)d->D / 2);
   for (int64_t i = 0; i < d->D / 2; ++i)
@@ -482,7 +548,8 @@ int rxw8_decoder_bind_parameter(rxw8_decoder *d, const char *path, rxw8_buffer *
     Buffer *pk = nullptr;
     int rc = new_buffer(d->rt, s.dtype, pd, 3, false, &pk);
     if (rc) return rc;
-    PackArgs a{buf->ptr, pk->ptr, s.dims[0], s.dims[1], kb, u8w ? 1 : 2};
+    const int64_t ilv = (s.kind == P_GU_W && d->gu_ilv) ? s.dims[0] / 2 : 0;
+    PackArgs a{buf->ptr, pk->ptr, s.dims[0], s.dims[1], kb, u8w ? 1 : 2, ilv};
     const int64_t slices = s.dims[0] / 16 * (s.dims[1] / kb) * 64;
     rc = launch(d->rt, "rxw8_pack_tiles", dim3((unsigned)std::min<int64_t>((slices + 255) / 256, 1 << 14)),
                 dim3(256), a);
@@ -491,6 +558,18 @@ int rxw8_decoder_bind_parameter(rxw8_decoder *d, const char *path, rxw8_buffer *
       return rc;
     }
     s.packed = pk;
+  }
+  if (s.kind == P_GU_S && d->gu_ilv) {  // scales follow the interleaved weight rows
+    Buffer *pm = nullptr;
+    int rc = new_buffer(d->rt, RXW8_F32, s.dims, s.rank, false, &pm);
+    if (rc) return rc;
+    InterleaveArgs a{(const float *)buf->ptr, (float *)pm->ptr, s.dims[0] / 2, s.dims[1]};
+    rc = launch(d->rt, "rxw8_dec_interleave_rows", dim3(blocks(s.dims[0] * s.dims[1])), dim3(256), a);
+    if (rc) {
+      rxw8_buffer_release(static_cast<rxw8_buffer *>(pm));
+      return rc;
+    }
+    s.perm = pm;
   }
   buf->refs.fetch_add(1);
   s.bound = buf;

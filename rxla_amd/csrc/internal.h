@@ -16,6 +16,26 @@
 
 namespace rxw8 {
 
+// GEMV options. Activation prologue (applied while the activations are
+// staged): mode 0 plain rows; 1 RMSNorm of f32 rows (norm_w, eps); 2 SwiGLU of
+// bf16 gate|up rows; 3 RMSNorm with the rows' sums of squares taken from
+// ss_in (ss_parts producer partials). stride/off: source row stride and offset
+// in elements (0 = dense rows). prefer_ks1: one launch without a split-K
+// reduce kernel. Epilogue: swiglu (weights in 8 gate + 8 up row tiles, y bf16
+// [M, N/2]) and ss_out (per-16-channel sums of squares of the updated
+// residual, with y_mode 1); both need the single-launch plan.
+struct GemvOptions {
+  int mode = 0;
+  int64_t stride = 0, off = 0;
+  const float *norm_w = nullptr;
+  float eps = 0.f;
+  const float *ss_in = nullptr;
+  int ss_parts = 0;
+  bool prefer_ks1 = false;
+  bool swiglu = false;
+  float *ss_out = nullptr;
+};
+
 // Records the thread-local error message and returns `code`.
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t err, const char *what);
@@ -57,6 +77,7 @@ struct Workspace {
 struct Runtime {
   int device = 0;
   int cus = 0;
+  size_t lds_max = 65536;  // LDS bytes one workgroup may allocate (160 KiB on gfx950)
   std::string name;
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
@@ -75,6 +96,16 @@ struct Runtime {
 
   hipFunction_t fn(const char *name);
 };
+
+// y[M,N] = x . W^T on the GEMV kernels (u8 or bf16 weights, row-major or
+// packed). RXW8_UNIMPLEMENTED (nothing launched) when no GEMV tiling fits.
+// Whether gemv_launch can run [M,K] x [N,K]^T (u8 weights, group G) in one
+// launch (no split-K reduce), as the fused epilogues require.
+bool gemv_single_launch(const Runtime *rt, int64_t M, int64_t N, int64_t K, int64_t G);
+int gemv_launch(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf16, bool packed,
+                const float *scale, void *y, int y_f32, int64_t M, int64_t N, int64_t K, int64_t G,
+                int y_mode, const GemvOptions &pro);
+
 
 // Device-side allocation through the runtime's cache.
 int rt_alloc(Runtime *rt, size_t bytes, void **out);

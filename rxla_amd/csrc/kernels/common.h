@@ -65,3 +65,24 @@ __device__ __forceinline__ u32x4 load_x8(const void *x, int64_t off, bool x_f32)
   }
   return *(const u32x4 *)((const uint16_t *)x + off);
 }
+
+// silu(g) * u in f32 (ops.rs:331-342): sigmoid with a nonpositive exponent
+// argument, so exp never overflows. Shared by the SwiGLU kernel and the GEMV
+// activation prologue so both produce identical bits.
+__device__ __forceinline__ float silu_mul_f32(float g, float u) {
+  const float e = __expf(-fabsf(g));
+  const float sig = g >= 0.f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+  return (g * sig) * u;
+}
+
+// Deterministic sum over a 256-thread block: wave butterfly, then the four
+// wave sums in a fixed order. `red` holds 4 floats of LDS.
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+

@@ -41,16 +41,49 @@ struct EmbedArgs {
   const int32_t *ids;
   const uint16_t *table;  // [V, H] bf16
   float *h;               // [T, H]
+  float *ss;              // optional [T]: sum of squares of each written row
   int64_t T, V, H;
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_dec_embed(EmbedArgs a) {
+  __shared__ float red[4];
   const int64_t t = blockIdx.x;
   int64_t id = a.ids[t];
   id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
   const uint16_t *src = a.table + id * a.H;
   float *dst = a.h + t * a.H;
-  for (int64_t i = threadIdx.x; i < a.H; i += blockDim.x) dst[i] = bf16_bits_to_f32(src[i]);
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < a.H; i += blockDim.x) {
+    const float v = bf16_bits_to_f32(src[i]);
+    dst[i] = v;
+    ss += v * v;
+  }
+  if (a.ss) {
+    ss = block_sum_256(ss, red);
+    if (threadIdx.x == 0) a.ss[t] = ss;
+  }
+}
+
+// Row permutation of the fused gate|up projection used by the SwiGLU GEMV
+// epilogue: output row R takes input row (R % 16 < 8 ? 8 (R / 16) + R % 16
+// : half + 8 (R / 16) + R % 16 - 8), i.e. 16-row tiles of 8 gate rows then the
+// 8 matching up rows. Applied to the f32 scales [2 half, cols] here; the
+// weights get it inside rxw8_pack_tiles.
+struct InterleaveArgs {
+  const float *src;
+  float *dst;
+  int64_t half, cols;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_interleave_rows(InterleaveArgs a) {
+  const int64_t total = 2 * a.half * a.cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t R = e / a.cols, c = e - R * a.cols;
+    const int64_t t = R / 16, r = R % 16;
+    const int64_t src_row = r < 8 ? 8 * t + r : a.half + 8 * t + r - 8;
+    a.dst[e] = a.src[src_row * a.cols + c];
+  }
 }
 
 // ---- RMSNorm (ops.rs:929-944): y = bf16((x * rsqrt(mean(x^2) + eps)) * w) -------
@@ -65,16 +98,6 @@ struct RmsNormArgs {
   int src_stride, src_offset;  // without src_row: input row = r * stride + offset
   float eps;
 };
-
-__device__ __forceinline__ float block_sum_256(float v, float *red) {
-  // deterministic: wave-level butterfly, then the 4 wave sums in order
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
-}
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_dec_rmsnorm(RmsNormArgs a) {
   __shared__ float red[4];
@@ -160,9 +183,10 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_qk_rope_kv(QkRopeArgs
 
 // ---- SwiGLU middle (ops.rs:331-342): act = bf16(silu(g) * u), gu = [g | u] ----
 struct SiluMulArgs {
-  const uint16_t *gu;  // [T, 2I]
+  const uint16_t *gu;  // [T, 2I]: gate columns then up columns, or interleaved
   uint16_t *act;       // [T, I]
   int64_t T, I;
+  int interleaved;     // 1: columns in blocks of 8 gate + 8 up (rxw8_dec_interleave_rows order)
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_dec_silu_mul(SiluMulArgs a) {
@@ -170,12 +194,11 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_silu_mul(SiluMulArgs 
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = e / a.I, i = e - t * a.I;
-    const float g = bf16_bits_to_f32(a.gu[t * 2 * a.I + i]);
-    const float u = bf16_bits_to_f32(a.gu[t * 2 * a.I + a.I + i]);
-    // sigmoid with a nonpositive exponent argument (ops.rs:331-338)
-    const float e_ = __expf(-fabsf(g));
-    const float sig = g >= 0.f ? 1.0f / (1.0f + e_) : e_ / (1.0f + e_);
-    a.act[e] = f32_to_bf16_bits((g * sig) * u);
+    const int64_t gc = a.interleaved ? 16 * (i / 8) + i % 8 : i;
+    const int64_t uc = a.interleaved ? gc + 8 : a.I + i;
+    const float g = bf16_bits_to_f32(a.gu[t * 2 * a.I + gc]);
+    const float u = bf16_bits_to_f32(a.gu[t * 2 * a.I + uc]);
+    a.act[e] = f32_to_bf16_bits(silu_mul_f32(g, u));
   }
 }
 

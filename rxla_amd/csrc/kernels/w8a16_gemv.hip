@@ -34,7 +34,7 @@
 #include "common.h"
 
 struct GemvArgs {
-  const void *x;      // [M, K] bf16 or f32
+  const void *x;      // activations, see x_mode
   const void *w;      // [N, K] u8 (or bf16 for the dense variant)
   const float *scale; // [N, K / G] (unused for the dense variant)
   void *y;            // [M, N] bf16 or f32
@@ -42,7 +42,28 @@ struct GemvArgs {
   int M, N, K, G;     // G == K for per-channel scales
   int ksplit;
   int x_f32, y_f32;
-  int y_mode;         // 0: store y; 1: y is an f32 residual, y += bf16(result)
+  // 0: store y; 1: y is an f32 residual, y += bf16(result);
+  // 2: SwiGLU pairs (ksplit 1): in every 16-row weight tile t, rows 0-7 are
+  //    gate channels 8t..8t+7 and rows 8-15 the matching up channels; y is
+  //    bf16 [M, N/2] and receives bf16(silu(bf16(gate)) * bf16(up))
+  int y_mode;
+  // with y_mode 1 and ksplit 1 (optional): per 16-channel group g, the
+  // partial sum of squares of the updated residual row b, ss_out[g * M + b]
+  float *ss_out;
+  // Activation prologue, applied while x is staged:
+  //   0: x row m at x + m * x_stride + x_off (bf16, or f32 when x_f32)
+  //   1: RMSNorm of f32 rows: x = bf16((h * 1/sqrt(mean(h^2) + eps)) * norm_w)
+  //      with h the full K-row at x + m * x_stride + x_off (x_f32 must be 1)
+  //   2: SwiGLU: x = bf16(silu(g) * u) with g = row[k], u = row[K + k] of the
+  //      bf16 gate|up rows at x + m * x_stride (x_stride = 2K)
+  //   3: RMSNorm as mode 1 with the row's sum of squares taken from
+  //      ss_in[p * M + b] summed over p < ss_parts (partials of the producer)
+  int x_mode;
+  int64_t x_stride, x_off;  // elements
+  const float *norm_w;      // [K] (modes 1, 3)
+  float eps;
+  const float *ss_in;       // mode 3
+  int ss_parts;
 };
 
 struct SplitkReduceArgs {
@@ -58,8 +79,9 @@ namespace {
 
 constexpr int kXPad = 8;  // bf16 elements of padding per staged activation row
 
-__device__ __forceinline__ void store_out(void *y, int y_f32, int y_mode, int64_t N, int b, int n,
-                                          f32x4 v) {
+// Returns the squared norm of the updated residual values (y_mode 1), else 0.
+__device__ __forceinline__ float store_out(void *y, int y_f32, int y_mode, int64_t N, int b, int n,
+                                           f32x4 v) {
   if (y_mode == 1) {  // residual: h += f32(bf16(result)) (layers.rs:295-296 + add)
     float4 *h = (float4 *)((float *)y + (int64_t)b * N + n);
     float4 o = *h;
@@ -68,6 +90,7 @@ __device__ __forceinline__ void store_out(void *y, int y_f32, int y_mode, int64_
     o.z += round_bf16(v[2]);
     o.w += round_bf16(v[3]);
     *h = o;
+    return ((o.x * o.x + o.y * o.y) + o.z * o.z) + o.w * o.w;
   } else if (y_f32) {
     float4 o = {round_bf16(v[0]), round_bf16(v[1]), round_bf16(v[2]), round_bf16(v[3])};
     *(float4 *)((float *)y + (int64_t)b * N + n) = o;
@@ -75,26 +98,85 @@ __device__ __forceinline__ void store_out(void *y, int y_f32, int y_mode, int64_
     uint2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     *(uint2 *)((uint16_t *)y + (int64_t)b * N + n) = o;
   }
+  return 0.f;
 }
 
-// Stage x[0:M, k0:k0+Kc] as bf16 into LDS rows of stride Kc + kXPad.
+// Stage x[0:M, k0:k0+Kc] as bf16 into LDS rows of stride Kc + kXPad, applying
+// the activation prologue (x_mode). Mode 1 sums each full row first with the
+// same thread stride and block reduction as rxw8_dec_rmsnorm, so the staged
+// bits equal that kernel's output.
 __device__ __forceinline__ void stage_x(const GemvArgs &a, uint16_t *xs, int k0, int Kc) {
   const int ldx = Kc + kXPad;
   const int per_row = Kc / 8;
   const int total = a.M * per_row;
+  if (a.x_mode == 1 || a.x_mode == 3) {
+    __shared__ float red[4];
+    __shared__ float row_scale[32];
+    if (a.x_mode == 3) {
+      // sums of squares from the producer's partials: one wave per row, lane
+      // l adds partials l, l + 64, ..., then a fixed butterfly (deterministic)
+      const int lane = threadIdx.x & 63, nwaves = blockDim.x >> 6;
+      for (int b = threadIdx.x >> 6; b < a.M; b += nwaves) {
+        float ss = 0.f;
+        for (int p = lane; p < a.ss_parts; p += 64) ss += a.ss_in[(int64_t)p * a.M + b];
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+      }
+    } else {  // mode 1: 256-thread workgroups only (host-checked)
+      for (int b = 0; b < a.M; ++b) {
+        const float *h = (const float *)a.x + b * a.x_stride + a.x_off;
+        float ss = 0.f;
+        for (int i = threadIdx.x; i < a.K; i += blockDim.x) ss += h[i] * h[i];
+        ss = block_sum_256(ss, red);
+        if (threadIdx.x == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < total; i += blockDim.x) {
+      const int b = i / per_row, kk = (i - b * per_row) * 8;
+      const float *h = (const float *)a.x + b * a.x_stride + a.x_off + k0 + kk;
+      const float sc = row_scale[b];
+      const float4 h0 = *(const float4 *)h, h1 = *(const float4 *)(h + 4);
+      const float4 w0 = *(const float4 *)(a.norm_w + k0 + kk), w1 = *(const float4 *)(a.norm_w + k0 + kk + 4);
+      u32x4 v;
+      v[0] = pack_bf16x2((h0.x * sc) * w0.x, (h0.y * sc) * w0.y);
+      v[1] = pack_bf16x2((h0.z * sc) * w0.z, (h0.w * sc) * w0.w);
+      v[2] = pack_bf16x2((h1.x * sc) * w1.x, (h1.y * sc) * w1.y);
+      v[3] = pack_bf16x2((h1.z * sc) * w1.z, (h1.w * sc) * w1.w);
+      *(u32x4 *)(xs + b * ldx + kk) = v;
+    }
+    return;
+  }
+  if (a.x_mode == 2) {
+    for (int i = threadIdx.x; i < total; i += blockDim.x) {
+      const int b = i / per_row, kk = (i - b * per_row) * 8;
+      const uint16_t *row = (const uint16_t *)a.x + b * a.x_stride;
+      const u32x4 g8 = *(const u32x4 *)(row + k0 + kk);
+      const u32x4 u8_ = *(const u32x4 *)(row + a.K + k0 + kk);
+      u32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float g0 = bf16_bits_to_f32(g8[e] & 0xffffu), g1 = bf16_bits_to_f32(g8[e] >> 16);
+        const float u0 = bf16_bits_to_f32(u8_[e] & 0xffffu), u1 = bf16_bits_to_f32(u8_[e] >> 16);
+        v[e] = pack_bf16x2(silu_mul_f32(g0, u0), silu_mul_f32(g1, u1));
+      }
+      *(u32x4 *)(xs + b * ldx + kk) = v;
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < total; i += blockDim.x) {
     const int b = i / per_row, kk = (i - b * per_row) * 8;
-    const int64_t off = (int64_t)b * a.K + k0 + kk;
+    const int64_t off = (int64_t)b * a.x_stride + a.x_off + k0 + kk;
     *(u32x4 *)(xs + b * ldx + kk) = load_x8(a.x, off, a.x_f32 != 0);
   }
 }
 
 // Reduce the KW k-slices of each row group through LDS (slice order), then
 // write the tile (ksplit == 1, scaled here when per-channel) or its partial.
-template <int MB, int RW>
+template <int MB, int RW, int NW = 4>
 __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int rows0, int sp,
                                             f32x4 (&total)[MB], bool scale_here) {
-  constexpr int KW = 4 / RW;
+  constexpr int KW = NW / RW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int rg = wave % RW, kq = wave / RW;
@@ -114,7 +196,7 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
   }
   const int j = lane >> 4, col = lane & 15;
   const int n = rows0 + rg * 16 + 4 * j;
-  if (n >= a.N) return;
+  if (n >= a.N) return;  // uniform per wave when N % 16 == 0 (the only case modes 2 and ss use)
   if (a.ksplit > 1) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -128,10 +210,35 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
     const float4 s4 = *(const float4 *)(a.scale + n);
     sc = f32x4{s4.x, s4.y, s4.z, s4.w};
   }
+  if (a.y_mode == 2) {
+    // gate values sit in lanes j < 2, the matching up values 32 lanes higher
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const f32x4 v = total[mb] * sc;
+      f32x4 up;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(v[i], 32);
+      const int b = col + 16 * mb;
+      if (j < 2 && b < a.M) {
+        const int c = (rows0 + rg * 16) / 2 + 4 * j;  // first of 4 output channels
+        uint2 o = {pack_bf16x2(silu_mul_f32(round_bf16(v[0]), round_bf16(up[0])),
+                               silu_mul_f32(round_bf16(v[1]), round_bf16(up[1]))),
+                   pack_bf16x2(silu_mul_f32(round_bf16(v[2]), round_bf16(up[2])),
+                               silu_mul_f32(round_bf16(v[3]), round_bf16(up[3])))};
+        *(uint2 *)((uint16_t *)a.y + (int64_t)b * (a.N / 2) + c) = o;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int b = col + 16 * mb;
-    if (b < a.M) store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, total[mb] * sc);
+    float ss = b < a.M ? store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, total[mb] * sc) : 0.f;
+    if (a.ss_out) {  // 4 lanes (j) hold the group's 16 channels of row b
+      ss += __shfl_xor(ss, 16);
+      ss += __shfl_xor(ss, 32);
+      if (j == 0 && b < a.M) a.ss_out[(int64_t)((rows0 + rg * 16) / 16) * a.M + b] = ss;
+    }
   }
 }
 
@@ -139,9 +246,12 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 // block (t, c) holds, for lane l, the 16 codes W[16t + l%16][64c + 16(l/16) ..]:
 // every wave load is then one contiguous 1 KiB block (rxw8_pack_w8 builds it).
 // Row-major weights ([N, K], the reference's U8 storage) use PK = false.
-template <int MB, int RW, int U, bool PK>
+// NW: waves per workgroup (4, or 8 / 16 for the wide decode variants that
+// give one workgroup more loads in flight instead of splitting K over
+// workgroups).
+template <int MB, int RW, int U, bool PK, int NW = 4>
 __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
-  constexpr int KW = 4 / RW;
+  constexpr int KW = NW / RW;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -255,7 +365,7 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   if (per_channel)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) total[mb] = acc[mb] - 128.f * ones[mb];
-  finish_tile<MB, RW>(a, (float *)xs, rows0, sp, total, per_channel);
+  finish_tile<MB, RW, NW>(a, (float *)xs, rows0, sp, total, per_channel);
 }
 
 // Dense bf16 weights (lm_head): one 16-byte slice = one MFMA A-fragment.
@@ -370,6 +480,29 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(Splitk
   RXW8_GEMV(KIND, MB, RW, 4)      \
   RXW8_GEMV(KIND, MB, RW, 2)      \
   RXW8_GEMV(KIND, MB, RW, 1)
+// Wide variants: 8 or 16 waves per workgroup = RW row groups x NW/RW k slices.
+#define RXW8_GEMV_WIDE(MB, RW, U, NW)                                           \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                         \
+      rxw8_gemv_w8_mb##MB##_rw##RW##_u##U##_w##NW(GemvArgs a) {                 \
+    gemv_w8<MB, RW, U, false, NW>(a);                                           \
+  }                                                                             \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                         \
+      rxw8_gemv_w8_pk_mb##MB##_rw##RW##_u##U##_w##NW(GemvArgs a) {              \
+    gemv_w8<MB, RW, U, true, NW>(a);                                            \
+  }
+#define RXW8_GEMV_WIDE_U(MB, RW, NW) \
+  RXW8_GEMV_WIDE(MB, RW, 4, NW)      \
+  RXW8_GEMV_WIDE(MB, RW, 2, NW)      \
+  RXW8_GEMV_WIDE(MB, RW, 1, NW)
+#define RXW8_GEMV_WIDE_RW(MB, NW) \
+  RXW8_GEMV_WIDE_U(MB, 1, NW)     \
+  RXW8_GEMV_WIDE_U(MB, 2, NW)     \
+  RXW8_GEMV_WIDE_U(MB, 4, NW)
+RXW8_GEMV_WIDE_RW(1, 8)
+RXW8_GEMV_WIDE_RW(1, 16)
+RXW8_GEMV_WIDE_RW(2, 8)
+RXW8_GEMV_WIDE_RW(2, 16)
+
 #define RXW8_GEMV_ALL(KIND) \
   RXW8_GEMV_U(KIND, 1, 1)   \
   RXW8_GEMV_U(KIND, 1, 4)   \
@@ -382,11 +515,12 @@ RXW8_GEMV_ALL(bf16)
 // Tiled weight layouts for the packed GEMV kernels. One thread moves one
 // 16-byte lane slice: dst block (t, c), lane l <- src row 16t + l%16.
 struct PackArgs {
-  const void *src;  // [N, K] row-major
-  void *dst;        // [N/16, K/kb, 1024 B]
-  int64_t n, k;     // elements
-  int kb;           // k per block: 64 (u8) or 32 (bf16)
-  int esize;        // bytes per element: 1 or 2
+  const void *src;   // [N, K] row-major
+  void *dst;         // [N/16, K/kb, 1024 B]
+  int64_t n, k;      // elements
+  int kb;            // k per block: 64 (u8) or 32 (bf16)
+  int esize;         // bytes per element: 1 or 2
+  int64_t ilv_half;  // 0, or N / 2: interleave gate/up rows (SwiGLU epilogue order)
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_pack_tiles(PackArgs a) {
@@ -398,7 +532,9 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_pack_tiles(PackArgs a) {
     const int64_t blk = i >> 6;
     const int lane = (int)(i & 63);
     const int64_t t = blk / blocks_k, c = blk - t * blocks_k;
-    const int64_t row = 16 * t + (lane & 15);
+    int64_t row = 16 * t + (lane & 15);
+    if (a.ilv_half)  // SwiGLU row order: 8 gate rows then the 8 matching up rows
+      row = (lane & 15) < 8 ? 8 * t + (lane & 15) : a.ilv_half + 8 * t + (lane & 15) - 8;
     const int64_t kk = c * a.kb + (int64_t)(lane >> 4) * per_lane;
     const u32x4 v = *(const u32x4 *)((const char *)a.src + (row * a.k + kk) * a.esize);
     *(u32x4 *)((char *)a.dst + i * 16) = v;

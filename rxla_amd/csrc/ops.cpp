@@ -23,6 +23,13 @@ struct GemvArgs {
   int ksplit;
   int x_f32, y_f32;
   int y_mode;
+  float *ss_out;
+  int x_mode;
+  int64_t x_stride, x_off;
+  const float *norm_w;
+  float eps;
+  const float *ss_in;
+  int ss_parts;
 };
 
 struct PackArgs {
@@ -31,6 +38,7 @@ struct PackArgs {
   int64_t n, k;
   int kb;
   int esize;
+  int64_t ilv_half;
 };
 
 struct SplitkReduceArgs {
@@ -133,7 +141,7 @@ static int env_int(const char *name, int dflt) {
 
 // GEMV launch plan: row groups per workgroup (RW), K-split, double-buffer depth.
 struct GemvPlan {
-  int rw = 0, ks = 0, u = 0, mb = 1;
+  int rw = 0, ks = 0, u = 0, mb = 1, nw = 4;  // nw: waves per workgroup
   size_t lds = 0;
 };
 
@@ -141,10 +149,10 @@ struct GemvPlan {
 // 8), the grouped-scale tile [16*rw, kc/g] f32, and the cross-wave reduction
 // area (reused after the loop) of (4/rw - 1) * rw * mb f32 tiles of 16x16.
 static size_t gemv_lds(int64_t m, int64_t kc, int64_t k, int64_t g, int rw, int mb,
-                       bool w_bf16) {
+                       bool w_bf16, int nw = 4) {
   (void)w_bf16;
   const size_t stage = (size_t)m * (kc + 8) * 2 + (g == k ? 0 : (size_t)16 * rw * (kc / g) * 4);
-  const size_t red = (size_t)(4 / rw - 1) * rw * mb * 256 * 4;
+  const size_t red = (size_t)(nw / rw - 1) * rw * mb * 256 * 4;
   return stage > red ? stage : red;
 }
 
@@ -154,16 +162,44 @@ static size_t gemv_lds(int64_t m, int64_t kc, int64_t k, int64_t g, int rw, int 
 // wave gets an even number of 16-byte slices. RXW8_GEMV_KSPLIT /
 // RXW8_GEMV_RW override for tuning.
 static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, int64_t g,
-                          bool w_bf16) {
+                          bool w_bf16, bool prefer_ks1 = false, bool allow_wide = true) {
   GemvPlan p;
   p.mb = m <= 16 ? 1 : 2;
   const int forced_rw = env_int("RXW8_GEMV_RW", 0);
-  p.rw = forced_rw == 1 || forced_rw == 4 ? forced_rw : (m <= 4 ? 1 : 4);
-  const int kw = 4 / p.rw;
+  p.rw = forced_rw == 1 || forced_rw == 4 ? forced_rw : (m <= 4 || prefer_ks1 ? 1 : 4);
   const int64_t slice = w_bf16 ? 32 : 64;  // k per 16-byte lane load
+  const bool per_channel = g == k;
+  // A single launch without a split-K reduce: 16 or 8 waves per workgroup
+  // split K inside the workgroup when each wave still gets an even number of
+  // 64-k slices (u8 weights, one 16-row group per workgroup).
+  // Wider row tiles (rw 2 or 4 groups of 16 rows) cut the staging each
+  // workgroup does per weight byte; the widest that still gives every CU a
+  // workgroup wins.
+  if (prefer_ks1 && allow_wide && !w_bf16 && forced_rw == 0) {
+    const int forced_nw = env_int("RXW8_GEMV_NW", 0);
+    for (int nw : {16, 8}) {
+      if (forced_nw && forced_nw != nw) continue;
+      for (int rw : {4, 2, 1}) {
+        const int kw = nw / rw;
+        if (rw > 1 && (n + 16 * rw - 1) / (16 * rw) < rt->cus) continue;
+        if (k % kw || (k / kw) % (2 * slice)) continue;
+        if (!per_channel && k % g) continue;
+        const size_t lds = gemv_lds(m, k, k, g, rw, p.mb, w_bf16, nw);
+        if (lds + 256 > rt->lds_max) continue;
+        p.nw = nw;
+        p.rw = rw;
+        p.ks = 1;
+        p.lds = lds;
+        const int64_t chunks = k / kw / slice;
+        p.u = 4;
+        while (chunks % (2 * p.u)) p.u /= 2;
+        return p;
+      }
+    }
+  }
+  const int kw = 4 / p.rw;
   const int64_t tiles = (n + 16 * p.rw - 1) / (16 * p.rw);
   const int forced_ks = env_int("RXW8_GEMV_KSPLIT", 0);
-  const bool per_channel = g == k;
   // k splits: powers of two, and multiples of 3 for widths like 6144 whose
   // scale groups (e.g. 2048) no power-of-two split keeps whole
   static const int splits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
@@ -173,7 +209,8 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
     const int64_t kc = k / ks;
     if (kc % kw || (kc / kw) % (2 * slice)) continue;  // even slices per wave
     if (!per_channel && kc % g) continue;
-    if (gemv_lds(m, kc, k, g, p.rw, p.mb, w_bf16) > 65536) continue;
+    // 256 B stay free for the kernels' static LDS (prologue reductions)
+    if (gemv_lds(m, kc, k, g, p.rw, p.mb, w_bf16) + 256 > rt->lds_max) continue;
     valid[nvalid++] = ks;
   }
   if (nvalid == 0) return p;
@@ -183,6 +220,8 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
     for (int i = 0; i < nvalid; ++i)
       if (valid[i] == forced_ks) pick = forced_ks;
     if (!pick) return p;
+  } else if (prefer_ks1 && valid[0] == 1) {
+    pick = 1;  // one launch, no reduce kernel: cheaper when launches dominate
   } else {
     for (int i = 0; i < nvalid; ++i)
       if (tiles * valid[i] >= rt->cus) {
@@ -201,24 +240,43 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
 
 static bool is_f(int dt) { return dt == RXW8_F32 || dt == RXW8_BF16; }
 
-// y[M, N] = linear(x[M, K]) on the GEMV kernel in chunks of <= 32 rows.
+// y[M, N] = linear(x[M, K]) on the GEMV kernel in chunks of <= 32 rows, with an
+// optional activation prologue (RMSNorm / SwiGLU applied while x is staged).
 // Returns UNIMPLEMENTED (nothing launched) when no plan fits.
 static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf16,
                     bool packed, const float *scale, void *y, int y_f32, int64_t M, int64_t N,
-                    int64_t K, int64_t G, int y_mode = 0) {
+                    int64_t K, int64_t G, int y_mode = 0, const GemvOptions *pro = nullptr) {
+  const GemvOptions plain;
+  if (!pro) pro = &plain;
   const int64_t mchunk = M <= 16 ? 16 : 32;
-  const GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16);
+  GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16, pro->prefer_ks1,
+                         pro->mode != 1);
   if (p.ks == 0 || N % 4) return RXW8_UNIMPLEMENTED;
+  // the fused epilogues need the whole reduction in one launch and whole
+  // 16-channel groups; one chunk of rows keeps the partial layout [g][M]
+  if ((pro->swiglu || pro->ss_out) && (p.ks != 1 || N % 16 || M > mchunk)) return RXW8_UNIMPLEMENTED;
+  if (pro->mode == 3 && M > mchunk) return RXW8_UNIMPLEMENTED;
   const int64_t tiles = (N + 16 * p.rw - 1) / (16 * p.rw);
   const size_t xe = x_f32 ? 4 : 2, ye = y_f32 ? 4 : 2;
   if (p.ks > 1) {
     int rc = ensure_workspace(rt, rt->partials, (size_t)p.ks * mchunk * N * sizeof(float), false);
     if (rc) return rc;
   }
+  // row stride of the activation source, in elements
+  const int64_t xstride = pro->stride > 0 ? pro->stride : (pro->mode == 2 ? 2 * K : K);
+  const size_t xe_src = (pro->mode == 1 || pro->mode == 3) ? 4 : (pro->mode == 2 ? 2 : xe);
   for (int64_t m0 = 0; m0 < M; m0 += mchunk) {
     const int64_t mm = M - m0 < mchunk ? M - m0 : mchunk;
     GemvArgs a;
-    a.x = (const char *)x + m0 * K * xe;
+    a.x = (const char *)x + m0 * xstride * xe_src;
+    a.x_mode = pro->mode;
+    a.x_stride = xstride;
+    a.x_off = pro->off;
+    a.norm_w = pro->norm_w;
+    a.eps = pro->eps;
+    a.ss_in = pro->ss_in;
+    a.ss_parts = pro->ss_parts;
+    a.ss_out = pro->ss_out;
     a.w = w;
     a.scale = scale;
     a.y = (char *)y + m0 * N * ye;
@@ -230,13 +288,15 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     a.ksplit = p.ks;
     a.x_f32 = x_f32;
     a.y_f32 = y_f32;
-    a.y_mode = y_mode;
+    a.y_mode = pro->swiglu ? 2 : y_mode;
     const int mb = mm <= 16 ? 1 : 2;
     char kname[64];
-    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s_mb%d_rw%d_u%d", w_bf16 ? "bf16" : "w8",
-                  packed ? "_pk" : "", mb, p.rw, p.u);
-    int rc = launch(rt, kname, dim3((unsigned)(tiles * p.ks)), dim3(256), a,
-                    gemv_lds(mm, K / p.ks, K, G, p.rw, mb, w_bf16));
+    char wide[8] = "";
+    if (p.nw != 4) std::snprintf(wide, sizeof wide, "_w%d", p.nw);
+    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s_mb%d_rw%d_u%d%s", w_bf16 ? "bf16" : "w8",
+                  packed ? "_pk" : "", mb, p.rw, p.u, wide);
+    int rc = launch(rt, kname, dim3((unsigned)(tiles * p.ks)), dim3(64 * p.nw), a,
+                    gemv_lds(mm, K / p.ks, K, G, p.rw, mb, w_bf16, p.nw));
     if (rc) return rc;
     if (p.ks > 1) {
       SplitkReduceArgs r;
@@ -254,6 +314,17 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     }
   }
   return RXW8_OK;
+}
+
+bool gemv_single_launch(const Runtime *rt, int64_t M, int64_t N, int64_t K, int64_t G) {
+  return M <= 32 && N % 16 == 0 && plan_gemv(rt, M, N, K, G, false, true).ks == 1;
+}
+
+int gemv_launch(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf16, bool packed,
+                const float *scale, void *y, int y_f32, int64_t M, int64_t N, int64_t K, int64_t G,
+                int y_mode, const GemvOptions &pro) {
+  if (M == 0) return RXW8_OK;
+  return run_gemv(rt, x, x_f32, w, w_bf16, packed, scale, y, y_f32, M, N, K, G, y_mode, &pro);
 }
 
 static int run_generic_linear(Runtime *rt, const void *x, int x_f32, const void *w, int w_kind,
@@ -554,6 +625,7 @@ int rxw8_pack_weight(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer **packed
   a.k = k;
   a.kb = kb;
   a.esize = u8 ? 1 : 2;
+  a.ilv_half = 0;
   rc = launch(rt, "rxw8_pack_tiles", dim3(grid_for(n / 16 * (k / kb) * 64, 256, 1 << 14)),
               dim3(256), a);
   if (rc) {

@@ -248,6 +248,7 @@ int rxw8_runtime_create(int device, rxw8_runtime **out) {
   auto *rt = new rxw8_runtime();
   rt->device = device;
   rt->cus = prop.multiProcessorCount;
+  rt->lds_max = prop.sharedMemPerBlock;
   rt->name = prop.name;
   const struct {
     const char *name;

@@ -100,6 +100,27 @@ def test_decoder_long_prefill_matches_oracle(rt):
     np.testing.assert_array_equal(model.lens()[:batch], [43, 43])
 
 
+def test_decoder_c5_widths_match_oracle(rt):
+    """Hidden 2048 / 16 q heads / 8 kv heads / intermediate 2048 (the C5
+    widths): decode steps take the fused schedule on 16-wave GEMV workgroups,
+    with the RMSNorm scale from the residual GEMV's partial sums and SiLU*up
+    in the gate|up epilogue."""
+    cfg = tiny_config(layers=2, hidden=2048, q_heads=16, kv_heads=8, head_dim=128,
+                      intermediate=2048, vocab=1008, max_seq=24, group=0)
+    params = tiny_params(cfg, seed=91, std=0.03)
+    batch = 3
+    model = build(rt, cfg, params, batch)
+    dec = oracle.Decoder(cfg, params, batch)
+    ids = np.random.default_rng(92).integers(0, cfg["vocab"], (batch, 5)).astype(np.int32)
+    lg, nxt, rlg, rnxt = step_both(rt, model, dec, ids)
+    assert rel_err(lg, rlg) <= 1e-2
+    for step in range(4):
+        lg, nxt, rlg, rnxt = step_both(rt, model, dec, rnxt.reshape(batch, 1).astype(np.int32))
+        err = rel_err(lg, rlg)
+        print(f"C5-width decode step {step} rel_err={err:.3e}")
+        assert err <= 1e-2
+
+
 def test_generate_graph_matches_eager_and_oracle(rt):
     r = rx()
     cfg = small_cfg()
