@@ -8,9 +8,10 @@
 // Layout: q [R, Hq, D] f32|bf16 (one query row per decoding sequence, or one
 // per prompt token in prefill), caches [Bc, Hkv, Lmax, D] bf16, out
 // [R, Hq, D] f32|bf16. Row r reads cache slot row_seq[r] (r when null) and
-// sees its first lens[r] keys. One workgroup (4 waves) handles one (row, kv
-// head, 256-key chunk); each wave takes 64 keys. The G = Hq/Hkv query heads
-// of the kv head share every K/V byte the workgroup loads.
+// sees its first lens[r] keys. One workgroup (8 waves) handles one (row, kv
+// head, split) and walks the split in passes of 512 keys, 64 per wave, with an
+// online softmax per wave. The G = Hq/Hkv query heads of the kv head share
+// every K/V byte the workgroup loads.
 //
 // QK^T runs on v_mfma_f32_16x16x32_bf16 with K as the A operand (16 keys x
 // 32 dims per fragment, 16-byte loads of contiguous K rows) and q^T as the B
@@ -19,9 +20,9 @@
 // bf16. Softmax statistics are reduced per wave with cross-lane shuffles,
 // probabilities go through LDS, and P.V runs on the VALU in f32 with each lane
 // owning 8 dims of every fourth key (16-byte V loads, 1 KiB per wave load).
-// Waves merge (max, sum, acc) in LDS. A row with one chunk writes its output
-// directly; otherwise every chunk writes (max, sum, acc) partials and
-// rxw8_gqa_decode_combine merges them in chunk order in a second launch
+// Waves merge (max, sum, acc) in LDS. With one split the workgroup writes the
+// output; otherwise every split writes (max, sum, acc) partials and
+// rxw8_gqa_decode_combine merges them in split order in a second launch
 // (deterministic; the kernel boundary makes the partials visible).
 #include "common.h"
 
@@ -44,8 +45,6 @@ namespace {
 
 constexpr int D = 128;
 constexpr int KW = 64;            // keys per wave
-constexpr int NW = 4;             // waves per workgroup
-constexpr int KC = KW * NW;       // keys per chunk
 constexpr float kNegInf = -__builtin_huge_valf();
 
 __device__ __forceinline__ float wave_max4(float v) {
@@ -59,159 +58,207 @@ __device__ __forceinline__ float wave_sum4(float v) {
   return v;
 }
 
-template <int G>
-__device__ void attn_chunk(const AttnArgs &a) {
-  constexpr int GP = (G + 3) / 4 * 4;  // padded heads in the LDS P tile
-  __shared__ float p_lds[NW][KW][GP];
-  __shared__ float m_lds[NW][G], l_lds[NW][G];
-  __shared__ float o_lds[NW][G][D];
+// Multi-pass variant: one workgroup of NP waves per (row, kv head, split).
+// Split s of a row covers keys [s * per, min(len, (s + 1) * per)), per =
+// ceil(len / S) rounded up to 64; the workgroup walks it in passes of NP * 64
+// keys (wave w takes keys base + 64 w ..), keeping a per-wave online softmax
+// (running max, sum and P.V accumulators rescaled by exp(m_old - m_new)) in
+// registers across passes. S = 1 writes the output directly; otherwise every
+// split writes (max, sum, acc) partials (empty splits: max -inf, sum 0) for
+// rxw8_gqa_decode_combine. a.max_chunks carries S.
+template <int G, int NP>
+__device__ void attn_pass(const AttnArgs &a) {
+  constexpr int GP = (G + 3) / 4 * 4;
+  __shared__ float p_lds[NP][KW][GP];
+  __shared__ float m_lds[NP][G], l_lds[NP][G];
+  __shared__ float o_lds[NP][G][D];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int chunk = blockIdx.x % a.max_chunks;
-  const int bh = blockIdx.x / a.max_chunks;  // row * Hkv + kvh
-  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;  // b: query row
+  const int S = a.max_chunks;
+  const int split = blockIdx.x % S;
+  const int bh = blockIdx.x / S;  // row * Hkv + kvh
+  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
   int len = a.lens[b];
   len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
-  const int nchunks = (len + KC - 1) / KC;
-  if (chunk >= nchunks) return;  // uniform per workgroup
-
-  const int j0 = chunk * KC + wave * KW;  // first key of this wave
+  const int per = ((len + S - 1) / S + KW - 1) / KW * KW;
+  const int start = split * per;
+  const int end = min(len, start + per);
+  float *part = a.ws + (((int64_t)bh * S + split) * G) * (2 + D);
+  if (start >= end) {  // empty split (uniform per workgroup)
+    for (int idx = threadIdx.x; idx < G * (2 + D); idx += blockDim.x)
+      part[idx] = (idx % (2 + D)) == 0 ? kNegInf : 0.f;
+    return;
+  }
   const int seq = a.row_seq ? a.row_seq[b] : b;
   const int64_t row_base = ((int64_t)seq * a.Hkv + kvh) * a.Lmax;
   const int col = lane & 15, g4 = lane >> 4;
 
-  // q fragments (B operand): lane (head = col, dgroup = g4), 8 dims per step.
-  u32x4 qhi[4], qlo[4];
+  // raw q (B operand source): lane (head = col, dgroup = g4), 8 dims per step
+  u32x4 qraw[4][2];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    float qv[8];
-    if (col < G) {
-      const int64_t off = ((int64_t)b * a.Hq + kvh * G + col) * D + 32 * t + 8 * g4;
-      if (a.q_f32) {
-        const float4 *p = (const float4 *)((const float *)a.q + off);
-        float4 x0 = p[0], x1 = p[1];
-        qv[0] = x0.x; qv[1] = x0.y; qv[2] = x0.z; qv[3] = x0.w;
-        qv[4] = x1.x; qv[5] = x1.y; qv[6] = x1.z; qv[7] = x1.w;
-      } else {
-        const u32x4 r = *(const u32x4 *)((const uint16_t *)a.q + off);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          qv[2 * e] = bf16_bits_to_f32(r[e] & 0xffffu);
-          qv[2 * e + 1] = bf16_bits_to_f32(r[e] >> 16);
-        }
-      }
+    const int64_t off = ((int64_t)b * a.Hq + kvh * G + (col < G ? col : 0)) * D + 32 * t + 8 * g4;
+    if (a.q_f32) {
+      const u32x4 *p = (const u32x4 *)((const float *)a.q + off);
+      qraw[t][0] = p[0];
+      qraw[t][1] = p[1];
     } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qv[e] = 0.f;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float h0 = round_bf16(qv[2 * e]), h1 = round_bf16(qv[2 * e + 1]);
-      qhi[t][e] = pack_bf16x2(h0, h1);
-      qlo[t][e] = pack_bf16x2(qv[2 * e] - h0, qv[2 * e + 1] - h1);
+      qraw[t][0] = *(const u32x4 *)((const uint16_t *)a.q + off);
+      qraw[t][1] = u32x4{0, 0, 0, 0};
     }
   }
-
-  // K fragments (A operand): lane (key = col, dgroup = g4); 4 key blocks x 4 steps.
-  u32x4 kf[4][4];
+  // K fragments (A operand): lane (key = col, dgroup = g4); V rows: lane
+  // (kq = g4, dgroup = col) takes keys 4 * it + kq, dims 8 col .. +7
+  u32x4 kf[4][4], vf[16];
+  auto load_k = [&](int j0) {
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    const int key = j0 + 16 * kb + col;
-    const bool valid = key < len;
-    const uint16_t *krow = a.kc + (row_base + (valid ? key : 0)) * D + 8 * g4;
+    for (int kb = 0; kb < 4; ++kb) {
+      const int key = j0 + 16 * kb + col;
+      const bool valid = key < end;
+      const uint16_t *krow = a.kc + (row_base + (valid ? key : 0)) * D + 8 * g4;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      kf[kb][t] = valid ? __builtin_nontemporal_load((const u32x4 *)(krow + 32 * t))
-                        : u32x4{0, 0, 0, 0};
-  }
-  // V rows: lane (kq = g4, dgroup = col) takes keys 4 * it + kq, dims 8*col..+7.
-  u32x4 vf[16];
-#pragma unroll
-  for (int it = 0; it < 16; ++it) {
-    const int key = j0 + 4 * it + g4;
-    vf[it] = key < len ? __builtin_nontemporal_load(
-                             (const u32x4 *)(a.vc + (row_base + key) * D + 8 * col))
-                       : u32x4{0, 0, 0, 0};
-  }
-
-  // Scores S^T[key][head]: lane holds key 16*kb + 4*g4 + i for head col.
-  float s[4][4];
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      acc = mfma16x16x32(as_bf16x8(kf[kb][t]), as_bf16x8(qhi[t]), acc);
-      acc = mfma16x16x32(as_bf16x8(kf[kb][t]), as_bf16x8(qlo[t]), acc);
+      for (int t = 0; t < 4; ++t)
+        kf[kb][t] = valid ? __builtin_nontemporal_load((const u32x4 *)(krow + 32 * t))
+                          : u32x4{0, 0, 0, 0};
     }
+  };
+  auto load_v = [&](int j0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = j0 + 16 * kb + 4 * g4 + i;
-      float v = kNegInf;
-      if (key < len) {
-        v = acc[i] * a.scale;
-        if (a.mask && col < G)
-          v += a.mask[(int64_t)b * a.mask_sb + (int64_t)(kvh * G + col) * a.mask_sh + key];
-      }
-      s[kb][i] = v;
+    for (int it = 0; it < 16; ++it) {
+      const int key = j0 + 4 * it + g4;
+      vf[it] = key < end ? __builtin_nontemporal_load(
+                               (const u32x4 *)(a.vc + (row_base + key) * D + 8 * col))
+                         : u32x4{0, 0, 0, 0};
     }
-  }
-  float m = kNegInf;
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) m = fmaxf(m, s[kb][i]);
-  m = wave_max4(m);
-  float l = 0.f;
-  const bool any = m != kNegInf;  // some visible key in this wave for this head
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float e = any ? __expf(s[kb][i] - m) : 0.f;
-      s[kb][i] = e;
-      l += e;
-    }
-  l = wave_sum4(l);
-  if (col < G) {
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p_lds[wave][16 * kb + 4 * g4 + i][col] = s[kb][i];
-    if (g4 == 0) {
-      m_lds[wave][col] = m;
-      l_lds[wave][col] = l;
-    }
-  }
-  __syncthreads();
-
-  // P.V on VALU: acc[h][e] for dims 8*col + e over keys 4*it + g4.
+  };
+  const int first = start + wave * KW;
+  float m_run = kNegInf, l_run = 0.f;  // per lane: head col (all g4 lanes agree)
   float o[G][8];
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+
+  for (int j0 = first; j0 < end; j0 += NP * KW) {
+    load_k(j0);
+    load_v(j0);
+    // q -> bf16 hi + lo after the block's loads are issued (q is in flight)
+    u32x4 qhi[4], qlo[4];
 #pragma unroll
-  for (int it = 0; it < 16; ++it) {
-    float v[8];
+    for (int t = 0; t < 4; ++t) {
+      float qv[8];
+      if (col < G) {
+        if (a.q_f32) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = bf16_bits_to_f32(vf[it][e] & 0xffffu);
-      v[2 * e + 1] = bf16_bits_to_f32(vf[it][e] >> 16);
+          for (int e = 0; e < 4; ++e) {
+            qv[e] = __uint_as_float(qraw[t][0][e]);
+            qv[4 + e] = __uint_as_float(qraw[t][1][e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            qv[2 * e] = bf16_bits_to_f32(qraw[t][0][e] & 0xffffu);
+            qv[2 * e + 1] = bf16_bits_to_f32(qraw[t][0][e] >> 16);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float h0 = round_bf16(qv[2 * e]), h1 = round_bf16(qv[2 * e + 1]);
+        qhi[t][e] = pack_bf16x2(h0, h1);
+        qlo[t][e] = pack_bf16x2(qv[2 * e] - h0, qv[2 * e + 1] - h1);
+      }
     }
-    const float *prow = p_lds[wave][4 * it + g4];
+    float s[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc = mfma16x16x32(as_bf16x8(kf[kb][t]), as_bf16x8(qhi[t]), acc);
+        acc = mfma16x16x32(as_bf16x8(kf[kb][t]), as_bf16x8(qlo[t]), acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = j0 + 16 * kb + 4 * g4 + i;
+        float v = kNegInf;
+        if (key < end) {
+          v = acc[i] * a.scale;
+          if (a.mask && col < G)
+            v += a.mask[(int64_t)b * a.mask_sb + (int64_t)(kvh * G + col) * a.mask_sh + key];
+        }
+        s[kb][i] = v;
+      }
+    }
+    float m_blk = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m_blk = fmaxf(m_blk, s[kb][i]);
+    m_blk = wave_max4(m_blk);
+    const float m_new = fmaxf(m_run, m_blk);
+    const bool any = m_new != kNegInf;
+    const float f_old = (m_run == kNegInf) ? 0.f : __expf(m_run - m_new);
+    float l_blk = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = any ? __expf(s[kb][i] - m_new) : 0.f;
+        s[kb][i] = e;
+        l_blk += e;
+      }
+    l_blk = wave_sum4(l_blk);
+    l_run = l_run * f_old + l_blk;
+    m_run = m_new;
+    if (col < G)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p_lds[wave][16 * kb + 4 * g4 + i][col] = s[kb][i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // rescale the running P.V of head h by head h's factor (held by lane h)
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float p = prow[h];
+      const float fh = __shfl(f_old, h);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[h][e] += p * v[e];
+      for (int e = 0; e < 8; ++e) o[h][e] *= fh;
     }
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = bf16_bits_to_f32(vf[it][e] & 0xffffu);
+        v[2 * e + 1] = bf16_bits_to_f32(vf[it][e] >> 16);
+      }
+      const float *prow = p_lds[wave][4 * it + g4];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float p = prow[h];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] += p * v[e];
+      }
+    }
+    // p_lds[wave] is rewritten next pass only after every lane read it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = wave_sum4(o[h][e]);
+  if (col < G && g4 == 0) {
+    m_lds[wave][col] = m_run;
+    l_lds[wave][col] = l_run;
+  }
   if (g4 == 0)
 #pragma unroll
     for (int h = 0; h < G; ++h)
@@ -219,21 +266,18 @@ __device__ void attn_chunk(const AttnArgs &a) {
       for (int e = 0; e < 8; ++e) o_lds[wave][h][8 * col + e] = o[h][e];
   __syncthreads();
 
-  // Merge the waves: thread t handles (head, dim) pairs.
-  const bool single = nchunks == 1;
-  float *part = a.ws + (((int64_t)bh * a.max_chunks + chunk) * G) * (2 + D);
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
     float M = kNegInf;
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, m_lds[w][h]);
+    for (int w = 0; w < NP; ++w) M = fmaxf(M, m_lds[w][h]);
     float L = 0.f, O = 0.f;
-    for (int w = 0; w < NW; ++w) {
+    for (int w = 0; w < NP; ++w) {
       const float mw = m_lds[w][h];
       const float f = mw == kNegInf ? 0.f : __expf(mw - M);
       L += f * l_lds[w][h];
       O += f * o_lds[w][h][d];
     }
-    if (single) {
+    if (S == 1) {
       const float r = O / L;
       const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
       if (a.out_f32)
@@ -255,26 +299,39 @@ __device__ void attn_chunk(const AttnArgs &a) {
 // in chunk order. One workgroup per (row, kv head); thread = (head, dim).
 template <int G>
 __device__ void attn_combine(const AttnArgs &a) {
+  constexpr int MAXC = 64;
+  __shared__ float fac[MAXC][G];  // exp(m_c - M) per chunk and head
+  __shared__ float inv_l[G];
   const int bh = blockIdx.x;
   const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
   int len = a.lens[b];
   len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
-  const int nchunks = (len + KC - 1) / KC;
-  if (nchunks == 1) return;  // written by the chunk kernel
+  const int nchunks = a.max_chunks;  // every split wrote a partial (empty: max -inf)
   const float *base = a.ws + ((int64_t)bh * a.max_chunks) * G * (2 + D);
+  // per-head statistics on wave 0: lane c holds chunk c's (max, sum); the
+  // max and the weighted sum use fixed butterflies (deterministic)
+  if (threadIdx.x < 64) {
+    const int c = threadIdx.x;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float *ph = base + ((int64_t)c * G + h) * (2 + D);
+      const float mc = c < nchunks ? ph[0] : kNegInf;
+      const float lc = c < nchunks ? ph[1] : 0.f;
+      float M = mc;
+      for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+      const float f = mc == kNegInf ? 0.f : __expf(mc - M);
+      float L = f * lc;
+      for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
+      if (c < nchunks) fac[c][h] = f;
+      if (c == 0) inv_l[h] = L;
+    }
+  }
+  __syncthreads();
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
-    float M = kNegInf;
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, base[((int64_t)c * G + h) * (2 + D)]);
-    float L = 0.f, O = 0.f;
-    for (int c = 0; c < nchunks; ++c) {
-      const float *ph = base + ((int64_t)c * G + h) * (2 + D);
-      const float mc = ph[0];
-      const float f = mc == kNegInf ? 0.f : __expf(mc - M);
-      L += f * ph[1];
-      O += f * ph[2 + d];
-    }
-    const float r = O / L;
+    float O = 0.f;
+    for (int c = 0; c < nchunks; ++c) O += fac[c][h] * base[((int64_t)c * G + h) * (2 + D) + 2 + d];
+    const float r = O / inv_l[h];
     const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
     if (a.out_f32)
       ((float *)a.out)[oi] = r;
@@ -286,8 +343,8 @@ __device__ void attn_combine(const AttnArgs &a) {
 }  // namespace
 
 #define RXW8_ATTN(G)                                                                 \
-  extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_decode_d128_g##G(AttnArgs a) { \
-    attn_chunk<G>(a);                                                                \
+  extern "C" __global__ void __launch_bounds__(512) rxw8_gqa_decode_d128_g##G(AttnArgs a) { \
+    attn_pass<G, 8>(a);                                                              \
   }                                                                                  \
   extern "C" __global__ void __launch_bounds__(256)                                  \
       rxw8_gqa_decode_combine_d128_g##G(AttnArgs a) {                                \

@@ -509,8 +509,18 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
   const bool fast = !cache_f32 && D == 128 && (G == 1 || G == 2 || G == 4 || G == 8) &&
                     !env_int("RXW8_FORCE_GENERIC", 0);
   if (fast) {
-    const int64_t KC = 256;
-    const int64_t max_chunks = (Lmax + KC - 1) / KC;
+    // 8 waves walk a split of a row's keys in 512-key passes with an online
+    // softmax. S splits per (row, kv head): about one workgroup per CU, and at
+    // most ~1536 keys per workgroup; S = 1 (no combine launch) once the rows
+    // alone fill the GPU (prefill). The combine keeps at most 64 partials.
+    const int forced = env_int("RXW8_ATTN_SPLITS", 0);
+    const int64_t pairs = R * Hkv;
+    int64_t S = std::max<int64_t>((rt->cus + pairs - 1) / pairs, (Lmax + 1535) / 1536);
+    S = std::min<int64_t>(S, (Lmax + 63) / 64);
+    if (forced > 0) S = forced;
+    if (S > 64) S = 64;
+    if (pairs >= 2 * rt->cus && !forced) S = 1;
+    const int64_t max_chunks = S;
     if (max_chunks > 1) {
       int rc = ensure_workspace(rt, rt->scratch,
                                 (size_t)R * Hkv * max_chunks * G * (2 + D) * sizeof(float), false);
@@ -537,7 +547,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     a.out_f32 = out_f32;
     char kname[64];
     std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_d128_g%d", (int)G);
-    int rc = launch(rt, kname, dim3((unsigned)(R * Hkv * max_chunks)), dim3(256), a);
+    int rc = launch(rt, kname, dim3((unsigned)(R * Hkv * max_chunks)), dim3(512), a);
     if (rc || max_chunks == 1) return rc;
     std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_combine_d128_g%d", (int)G);
     return launch(rt, kname, dim3((unsigned)(R * Hkv)), dim3(256), a);
