@@ -11,10 +11,12 @@ weight bytes and the figure is HBM bandwidth.
 
 value        = sweep algorithmic bytes / wall time of the timed steps (GB/s);
                each step is one HIP-graph replay of the 9 launches
-roofline     = the GEMV kernel serving B <= 4 (rxw8_gemv_w8_pk_mb1_rw1_u4, 6
-               of the 9 launches): algorithmic bytes per launch / mean launch
-               duration, from HIP events on the runtime's stream around runs
-               of back-to-back launches of one shape
+roofline     = the B <= 4 GEMV kernel (rxw8_gemv_w8_pk_mb1_rw1_u4) at its
+               largest sweep shape, B=1 N=24576: algorithmic bytes per launch /
+               launch duration, from HIP events on the runtime's stream around
+               runs of back-to-back launches of the shape; traffic = the HBM
+               bytes per launch recorded in profiles/ by two rocprofv3 --pmc
+               passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --pmc-probe gemv`
 cpu_baseline = the CPU oracle (reference-order restatement, OpenMP) timed on
                this host over a bounded sample of the same sweep
 
@@ -61,6 +63,20 @@ def gemv_bytes(b, n, k=K):
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def recorded_traffic():
+    """HBM bytes per launch of the roofline GEMV from the committed counter
+    summary (two rocprofv3 --pmc passes, calibrated by a copy of known size);
+    None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_B1_N24576_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("TRAFFIC_BYTES_PER_LAUNCH="):
+                return int(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(budget_s=12.0):
@@ -230,6 +246,45 @@ def bench_decoder(rt, rx, torch, stream, prompt_len=1024, steps=256, batch=8):
                       "synchronized, best of 2"}
 
 
+def pmc_probe(kind, reps=30):
+    """A short fixed program for rocprofv3 --pmc passes: `reps` launches of one
+    roofline shape plus 4 plain 256 MiB device copies (torch) that calibrate
+    what FETCH_SIZE / WRITE_SIZE read for a known number of bytes."""
+    import torch
+    import rxla_amd as rx
+
+    rt = rx.Runtime(0)
+    stream = torch.cuda.Stream()
+    rt.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    with torch.cuda.stream(stream):
+        src = torch.randn(1 << 26, device="cuda", generator=gen)  # 256 MiB
+        dst = torch.empty_like(src)
+    stream.synchronize()
+    if kind == "gemv":  # B=1, N=24576, K=4096, packed, 6 rotating copies
+        n, b = 24576, 1
+        with torch.cuda.stream(stream):
+            ws = [(torch.randint(1, 256, (n, K), dtype=torch.uint8, device="cuda", generator=gen),
+                   torch.rand((n, 1), device="cuda", generator=gen) * 1e-3) for _ in range(6)]
+            x = torch.randn((b, K), device="cuda", generator=gen).to(torch.bfloat16)
+            y = torch.empty((b, n), dtype=torch.bfloat16, device="cuda")
+        stream.synchronize()
+        wb = [(rx.pack_weight(rt, rt.wrap_tensor(u)), rt.wrap_tensor(s_)) for u, s_ in ws]
+        rt.synchronize()
+        xb, yb = rt.wrap_tensor(x), rt.wrap_tensor(y)
+        for i in range(reps):
+            rx.quantized_linear(rt, xb, wb[i % 6][0], wb[i % 6][1], rx.DType.BF16, out=yb)
+        log(f"pmc probe gemv B={b} N={n} K={K}: {reps} launches, {gemv_bytes(b, n)} algorithmic B each")
+    else:
+        raise SystemExit(f"unknown --pmc-probe {kind}")
+    rt.synchronize()
+    with torch.cuda.stream(stream):
+        for _ in range(4):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    log("pmc probe: 4 copies of 268435456 B")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,7 +295,11 @@ def main():
     ap.add_argument("--skip-gemm", action="store_true")
     ap.add_argument("--skip-attention", action="store_true")
     ap.add_argument("--skip-decoder", action="store_true")
+    ap.add_argument("--pmc-probe", choices=["gemv"], help="counter-collection program only")
     args = ap.parse_args()
+    if args.pmc_probe:
+        pmc_probe(args.pmc_probe)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU runs are "
               "not part of this build", file=sys.stderr)
@@ -350,8 +409,11 @@ def main():
         return mb, ms
 
     mean_bytes, mean_s = kernel_stats(lambda b: b <= 4)
-    achieved = mean_bytes / mean_s / 1e9
     b16_bytes, b16_s = kernel_stats(lambda b: b > 4)
+    # roofline shape: B=1, N=24576 (the largest decode GEMV of the sweep)
+    roof_s = float(np.median(per_shape[(1, 24576)]))
+    roof_bytes = gemv_bytes(1, 24576)
+    achieved = roof_bytes / roof_s / 1e9
     sweep = {f"B{b}_N{n}": {"us": round(float(np.median(v)) * 1e6, 2),
                             "GBs": round(gemv_bytes(b, n) / float(np.median(v)) / 1e9, 1)}
              for (b, n), v in sorted(per_shape.items())}
@@ -378,14 +440,20 @@ def main():
                    "weight_layout": layout,
                    "launches_per_step": len(plan), "bytes_per_step": step_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": recorded_traffic() if layout == "packed" else None,
                      "kernel": "rxw8_gemv_w8_pk_mb1_rw1_u4" if layout == "packed"
                      else "rxw8_gemv_w8_mb1_rw1_u4",
-                     "mean_launch_us": round(mean_s * 1e6, 3),
-                     "mean_launch_bytes": int(mean_bytes),
-                     "timing": "HIP event pair on the runtime stream around "
-                               f"{args.copies} back-to-back launches of one shape, divided by "
-                               f"{args.copies} (includes the inter-kernel gaps)"},
+                     "shape": "B=1 N=24576 K=4096", "launch_us": round(roof_s * 1e6, 3),
+                     "launch_bytes": roof_bytes,
+                     "timing": "median of HIP event pairs on the runtime stream around "
+                               f"{args.copies} back-to-back launches of the shape, divided by "
+                               f"{args.copies} (includes the inter-kernel gaps)",
+                     "traffic_source": "profiles/gemv_B1_N24576_traffic.txt (FETCH_SIZE + "
+                                       "WRITE_SIZE per launch, copy-calibrated)",
+                     "b_le_4_mean": {"achieved": round(mean_bytes / mean_s / 1e9, 2),
+                                     "mean_launch_us": round(mean_s * 1e6, 3),
+                                     "mean_launch_bytes": int(mean_bytes)}},
         "roofline_b16": {"bound": "hbm", "achieved": round(b16_bytes / b16_s / 1e9, 2),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(b16_bytes / b16_s / 1e9 / HBM_PEAK_GBS, 4),

@@ -203,15 +203,20 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
   // k splits: powers of two, and multiples of 3 for widths like 6144 whose
   // scale groups (e.g. 2048) no power-of-two split keeps whole
   static const int splits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
+  // Staged slices up to 64 KiB keep two or more workgroups per CU; larger ones
+  // (up to the 160 KiB a workgroup may hold) only when no split fits in 64 KiB.
+  // 256 B stay free for the kernels' static LDS (prologue reductions).
   int valid[12], nvalid = 0;
-  for (int ks : splits) {
-    if (k % ks) continue;
-    const int64_t kc = k / ks;
-    if (kc % kw || (kc / kw) % (2 * slice)) continue;  // even slices per wave
-    if (!per_channel && kc % g) continue;
-    // 256 B stay free for the kernels' static LDS (prologue reductions)
-    if (gemv_lds(m, kc, k, g, p.rw, p.mb, w_bf16) + 256 > rt->lds_max) continue;
-    valid[nvalid++] = ks;
+  for (size_t cap : {(size_t)65536, rt->lds_max}) {
+    for (int ks : splits) {
+      if (k % ks) continue;
+      const int64_t kc = k / ks;
+      if (kc % kw || (kc / kw) % (2 * slice)) continue;  // even slices per wave
+      if (!per_channel && kc % g) continue;
+      if (gemv_lds(m, kc, k, g, p.rw, p.mb, w_bf16) + 256 > cap) continue;
+      valid[nvalid++] = ks;
+    }
+    if (nvalid) break;
   }
   if (nvalid == 0) return p;
   int pick = valid[nvalid - 1];
@@ -246,7 +251,8 @@ static bool is_f(int dt) { return dt == RXW8_F32 || dt == RXW8_BF16; }
 static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf16,
                     bool packed, const float *scale, void *y, int y_f32, int64_t M, int64_t N,
                     int64_t K, int64_t G, int y_mode = 0, const GemvOptions *pro = nullptr) {
-  const GemvOptions plain;
+  GemvOptions plain;
+  plain.prefer_ks1 = env_int("RXW8_GEMV_PREFER_WIDE", 0) != 0;
   if (!pro) pro = &plain;
   const int64_t mchunk = M <= 16 ? 16 : 32;
   GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16, pro->prefer_ks1,
