@@ -47,10 +47,6 @@ struct DecPosArgs {
   int32_t *pos, *row_seq, *row_len;
   int b, s;
 };
-struct DecAdvanceArgs {
-  int32_t *lens;
-  int b, s;
-};
 struct EmbedArgs {
   const int32_t *ids;
   const uint16_t *table;
@@ -104,6 +100,15 @@ struct PackArgs {
   int esize;
   int64_t ilv_half;
 };
+struct ArgmaxFinalArgs {
+  const float *pval;
+  const int32_t *pidx;
+  int32_t *next;
+  int32_t *lens;
+  int32_t *rec_out;
+  int32_t *rec_step;
+  int rows, chunks, s, ncols;
+};
 struct RecordArgs {
   const int32_t *next;
   int32_t *out;
@@ -154,7 +159,7 @@ struct Decoder {
   bool gu_ilv = false;  // gate|up weights and scales stored in SwiGLU row order
   void *tail_block = nullptr;
   size_t tail_bytes = 0;
-  int am_chunks = 64;
+  int am_chunks = 64;  // argmax partials per row; <= 64 (one lane each in the final pass)
   // decode-step graph for batch g_b
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -234,7 +239,9 @@ static unsigned blocks(int64_t n, int per = 256) { return (unsigned)std::max<int
 
 // Enqueue one forward pass over ids[b, s] (device) starting at the current
 // lengths; writes next ids and logits of the last position; advances lengths.
-static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s) {
+// rec (generate): also store the chosen ids in column *rec->step of rec->out.
+static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
+                           const RecordArgs *rec = nullptr) {
   Runtime *rt = d->rt;
   const int64_t T = b * s;
   int rc;
@@ -360,11 +367,10 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s)
     ArgmaxArgs a{d->logits, d->am_val, d->am_idx, d->next, d->V, (int)b, d->am_chunks};
     if ((rc = launch(rt, "rxw8_dec_argmax_partial", dim3((unsigned)(b * d->am_chunks)), dim3(256), a)))
       return rc;
-    if ((rc = launch(rt, "rxw8_dec_argmax_final", dim3(1), dim3(64), a))) return rc;
-  }
-  {
-    DecAdvanceArgs a{d->d_lens, (int)b, (int)s};
-    if ((rc = launch(rt, "rxw8_dec_advance", dim3(1), dim3(64), a))) return rc;
+    ArgmaxFinalArgs f{d->am_val, d->am_idx, d->next, d->d_lens, rec ? rec->out : nullptr,
+                      rec ? rec->step : nullptr, (int)b, d->am_chunks, (int)s, rec ? rec->ncols : 0};
+    const unsigned threads = 64u * (unsigned)std::min<int64_t>(b, 16);
+    if ((rc = launch(rt, "rxw8_dec_argmax_final", dim3(1), dim3(threads), f))) return rc;
   }
   return RXW8_OK;
 }
@@ -629,16 +635,11 @@ int rxw8_decoder_generate(rxw8_decoder *d, rxw8_buffer *prompt, int64_t b, int64
   if ((rc = ensure_activations(d, b * s))) return rc;
   RXW8_HIP(hipMemsetAsync(d->d_step, 0, 4, rt->stream));
   RecordArgs rec{d->next, (int32_t *)out_ids->ptr, d->d_step, (int)b, (int)(steps + 1)};
-  if ((rc = enqueue_forward(d, (const int32_t *)prompt->ptr, b, s))) return rc;
-  if ((rc = launch(rt, "rxw8_dec_record", dim3(1), dim3(256), rec))) return rc;
+  if ((rc = enqueue_forward(d, (const int32_t *)prompt->ptr, b, s, &rec))) return rc;
   for (int64_t i = 0; i < b; ++i) d->h_lens[(size_t)i] += (int32_t)s;
   if (steps == 0) return RXW8_OK;
   // One decode step: consume the previous argmax (d->next) as the ids.
-  auto step = [&]() -> int {
-    int r = enqueue_forward(d, d->next, b, 1);
-    if (r) return r;
-    return launch(rt, "rxw8_dec_record", dim3(1), dim3(256), rec);
-  };
+  auto step = [&]() -> int { return enqueue_forward(d, d->next, b, 1, &rec); };
   int64_t done = 0;
   if (use_graph) {
     if (d->g_b != b || d->g_out != out_ids->ptr || !d->gexec) {

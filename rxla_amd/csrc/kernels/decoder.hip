@@ -26,15 +26,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_positions(DecPosArgs 
   a.row_len[t] = p + 1;
 }
 
-struct DecAdvanceArgs {
-  int32_t *lens;
-  int b, s;
-};
 
-extern "C" __global__ void rxw8_dec_advance(DecAdvanceArgs a) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < a.b) a.lens[i] += a.s;
-}
 
 // ---- embedding: h[t] = f32(E[clamp(ids[t], 0, V-1)]) (indexing.rs:637-656) ----
 struct EmbedArgs {
@@ -259,37 +251,50 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_argmax_partial(Argmax
   }
 }
 
-extern "C" __global__ void rxw8_dec_argmax_final(ArgmaxArgs a) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= a.rows) return;
-  float bv = 0.f;
-  int bi = 0x7fffffff;
-  for (int c = 0; c < a.chunks; ++c) {
-    const int i = a.pidx[r * a.chunks + c];
-    if (i == 0x7fffffff) continue;
-    const float v = a.pval[r * a.chunks + c];
-    if (bi == 0x7fffffff || am_better(v, i, bv, bi)) {
-      bv = v;
-      bi = i;
-    }
-  }
-  a.out[r] = bi == 0x7fffffff ? 0 : bi;
-}
-
-// ---- generate: out[i, step] = next[i]; step advances on device -------------------
-struct RecordArgs {
-  const int32_t *next;
-  int32_t *out;   // [b, ncols]
-  int32_t *step;  // device column counter
-  int b, ncols;
+// Pass 2 plus the end of a forward step, in one launch: one wave per row
+// reduces the row's chunk partials (lane c holds chunk c; (value, index) under
+// am_better is a total order, so the butterfly returns the same winner as a
+// sequential scan), writes next[r] and advances lens[r] by s; with `rec_out`
+// (generate) it also stores next[r] in column *step of rec_out and then
+// advances *step. One workgroup of 64 * min(rows, 16) threads.
+struct ArgmaxFinalArgs {
+  const float *pval;  // [rows, chunks]
+  const int32_t *pidx;
+  int32_t *next;      // [rows]
+  int32_t *lens;      // [rows] advanced by s
+  int32_t *rec_out;   // optional [rows, ncols]
+  int32_t *rec_step;  // device column counter (with rec_out)
+  int rows, chunks, s, ncols;
 };
 
-extern "C" __global__ void rxw8_dec_record(RecordArgs a) {
+extern "C" __global__ void __launch_bounds__(1024) rxw8_dec_argmax_final(ArgmaxFinalArgs a) {
   __shared__ int col;
-  if (threadIdx.x == 0) col = *a.step;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  if (threadIdx.x == 0) col = a.rec_out ? *a.rec_step : 0;
   __syncthreads();
-  if (col < a.ncols)
-    for (int i = threadIdx.x; i < a.b; i += blockDim.x) a.out[i * a.ncols + col] = a.next[i];
+  for (int r = wave; r < a.rows; r += nwaves) {
+    float bv = -__builtin_huge_valf();
+    int bi = 0x7fffffff;
+    if (lane < a.chunks) {
+      bi = a.pidx[r * a.chunks + lane];
+      if (bi != 0x7fffffff) bv = a.pval[r * a.chunks + lane];
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || am_better(ov, oi, bv, bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      const int id = bi == 0x7fffffff ? 0 : bi;
+      a.next[r] = id;
+      a.lens[r] += a.s;
+      if (a.rec_out && col < a.ncols) a.rec_out[r * a.ncols + col] = id;
+    }
+  }
   __syncthreads();
-  if (threadIdx.x == 0) *a.step = col + 1;
+  if (a.rec_out && threadIdx.x == 0) *a.rec_step = col + 1;
 }
+
