@@ -39,7 +39,8 @@ int bf16_linear_launch(Runtime *rt, const void *x, int x_f32, const uint16_t *w,
 int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
                      int cache_f32, const int32_t *lens, const int32_t *row_seq,
                      const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
-                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale);
+                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
+                     const AttnRope *rope = nullptr);
 
 // Kernel argument structs (match kernels/decoder.hip and w8a16_gemv.hip).
 struct DecPosArgs {
@@ -69,9 +70,14 @@ struct RmsNormArgs {
   int src_stride, src_offset;
   float eps;
 };
+struct RopeTableArgs {
+  const float *freqs;
+  float *tab;
+  int half;
+};
 struct QkRopeArgs {
   const uint16_t *qkv;
-  const float *q_norm, *k_norm, *freqs;
+  const float *q_norm, *k_norm, *rope;
   const int32_t *pos, *row_seq;
   float *q_out;
   uint16_t *kc, *vc;
@@ -142,6 +148,7 @@ struct Decoder {
   int32_t *d_lens = nullptr, *d_step = nullptr;
   std::vector<int32_t> h_lens;
   float *d_freqs = nullptr;
+  float *d_rope = nullptr;  // [Lmax, D] cos / sin table
   // activations (capacity cap_T tokens)
   int64_t cap_T = 0;
   float *h = nullptr, *q = nullptr;
@@ -194,8 +201,8 @@ static void free_decoder_memory(Decoder *d) {
   d->gexec = nullptr;
   d->graph = nullptr;
   (void)hipStreamSynchronize(rt->stream);
-  for (void *p : {d->kc, d->vc, (void *)d->d_lens, (void *)d->d_freqs, d->act_block,
-                  d->tail_block})
+  for (void *p : {d->kc, d->vc, (void *)d->d_lens, (void *)d->d_freqs, (void *)d->d_rope,
+                  d->act_block, d->tail_block})
     if (p) (void)hipFree(p);
   for (ParamSpec &s : d->params) {
     if (s.bound) rxw8_buffer_release(static_cast<rxw8_buffer *>(s.bound));
@@ -263,6 +270,13 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
       gemv_single_launch(rt, T, d->H, d->Hq * d->D, d->group_for(d->Hq * d->D)) &&
       gemv_single_launch(rt, T, 2 * d->I, d->H, d->group_for(d->H)) &&
       gemv_single_launch(rt, T, d->H, d->I, d->group_for(d->I));
+  // RoPE and the KV append fold into the attention launch when every row is a
+  // different sequence's single new token and the D = 128 kernel runs.
+  const char *unfused_rope = std::getenv("RXW8_DEC_UNFUSED_ROPE");
+  const bool fused_rope = fused && s == 1 && d->D == 128 && d->Hq % d->Hkv == 0 &&
+                          (d->Hq / d->Hkv == 1 || d->Hq / d->Hkv == 2 || d->Hq / d->Hkv == 4 ||
+                           d->Hq / d->Hkv == 8) &&
+                          !(unfused_rope && *unfused_rope == '1');
   {
     const ParamSpec &e = d->p(-1, P_EMBED);
     EmbedArgs a{ids, (const uint16_t *)e.bound->ptr, d->h, fused ? d->ss_embed : nullptr, T, d->V,
@@ -300,18 +314,27 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
     }
     uint16_t *kcl = (uint16_t *)d->kc + (size_t)l * layer_cache;
     uint16_t *vcl = (uint16_t *)d->vc + (size_t)l * layer_cache;
-    {
+    if (fused_rope) {
+      // one new token per sequence: q/k norm + RoPE + KV append inside attention
+      AttnRope rp{d->qkv,
+                  d->cfg.qk_norm ? fptr(P_QN) : nullptr,
+                  d->cfg.qk_norm ? fptr(P_KN) : nullptr,
+                  d->d_rope, d->cfg.eps};
+      if ((rc = attention_launch(rt, d->qkv, 0, kcl, vcl, 0, d->row_len, d->row_seq, nullptr, 0, 0,
+                                 d->attn, 0, T, d->Hq, d->Hkv, d->Lmax, d->D, scale, &rp)))
+        return rc;
+    } else {
       QkRopeArgs a{d->qkv,
                    d->cfg.qk_norm ? fptr(P_QN) : nullptr,
                    d->cfg.qk_norm ? fptr(P_KN) : nullptr,
-                   d->d_freqs, d->pos, d->row_seq, d->q, kcl, vcl, (int)T, (int)d->Hq, (int)d->Hkv,
+                   d->d_rope, d->pos, d->row_seq, d->q, kcl, vcl, (int)T, (int)d->Hq, (int)d->Hkv,
                    (int)d->D, (int)d->Lmax, d->cfg.eps};
       const int64_t waves = T * (d->Hq + 2 * d->Hkv);
       if ((rc = launch(rt, "rxw8_dec_qk_rope_kv", dim3(blocks(waves, 4)), dim3(256), a))) return rc;
+      if ((rc = attention_launch(rt, d->q, 1, kcl, vcl, 0, d->row_len, d->row_seq, nullptr, 0, 0,
+                                 d->attn, 0, T, d->Hq, d->Hkv, d->Lmax, d->D, scale)))
+        return rc;
     }
-    if ((rc = attention_launch(rt, d->q, 1, kcl, vcl, 0, d->row_len, d->row_seq, nullptr, 0, 0,
-                               d->attn, 0, T, d->Hq, d->Hkv, d->Lmax, d->D, scale)))
-      return rc;
     if (fused) {
       GemvOptions o;
       o.prefer_ks1 = true, o.ss_out = d->ss_o;
@@ -450,6 +473,7 @@ int rxw8_decoder_create(rxw8_runtime *rt, const rxw8_decoder_config *cfg, rxw8_d
   if (e == hipSuccess) e = hipMalloc(&d->vc, d->cache_bytes);
   if (e == hipSuccess) e = hipMalloc((void **)&d->d_lens, 256 + (size_t)d->Bmax * 4);
   if (e == hipSuccess) e = hipMalloc((void **)&d->d_freqs, (size_t)d->D / 2 * 4);
+  if (e == hipSuccess) e = hipMalloc((void **)&d->d_rope, (size_t)d->Lmax * d->D * 4);
   const size_t ss_floats = 32 + 2 * (size_t)(d->H / 16) * 32;
   const size_t tail = (size_t)d->Bmax * d->H * 2 + (size_t)d->Bmax * d->V * 4 +
                       (size_t)d->Bmax * d->am_chunks * 8 + (size_t)d->Bmax * 8 + ss_floats * 4 +
@@ -483,9 +507,13 @@ int rxw8_decoder_create(rxw8_runtime *rt, const rxw8_decoder_config *cfg, rxw8_d
   if (e == hipSuccess) e = hipMemsetAsync(d->d_lens, 0, 256 + (size_t)d->Bmax * 4, rt->stream);
   if (e == hipSuccess)
     e = hipMemcpyAsync(d->d_freqs, freqs.data(), freqs.size() * 4, hipMemcpyHostToDevice, rt->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
-  if (e != hipSuccess) {
-    rc = hip_fail(e, "decoder state initialisation");
+  if (e == hipSuccess) {
+    RopeTableArgs a{d->d_freqs, d->d_rope, (int)(d->D / 2)};
+    rc = launch(rt, "rxw8_dec_rope_table", dim3((unsigned)d->Lmax), dim3(64), a);
+  }
+  if (e == hipSuccess && rc == RXW8_OK) e = hipStreamSynchronize(rt->stream);
+  if (e != hipSuccess || rc != RXW8_OK) {
+    if (rc == RXW8_OK) rc = hip_fail(e, "decoder state initialisation");
     free_decoder_memory(d);
     delete d;
     return rc;

@@ -49,6 +49,15 @@ int hip_fail(hipError_t err, const char *what);
 size_t dtype_size(int dtype);
 const char *dtype_name(int dtype);
 
+// Decode-step attention that also applies q/k RMSNorm + RoPE and appends the
+// new k/v (one new token per row; see rxw8_gqa_decode_d128_g*).
+struct AttnRope {
+  const uint16_t *qkv;           // [R, Hq + 2 Hkv, D] bf16 projection rows
+  const float *q_norm, *k_norm;  // [D] or null
+  const float *table;            // [Lmax, D] RoPE table (cos then sin per position)
+  float eps;                     // the new token of row r sits at lens[r] - 1
+};
+
 struct Runtime;
 
 struct Buffer {

@@ -39,6 +39,16 @@ struct AttnArgs {
   int R, Hq, Hkv, Lmax, max_chunks;
   float scale;
   int q_f32, out_f32;
+  // Decode steps (one new token per row, at position lens[r] - 1): when qkv
+  // is set, q and the new k / v come from the bf16 projection row
+  // qkv[r, Hq + 2 Hkv, D] (optional per-head RMSNorm with q_norm / k_norm,
+  // then split-half RoPE), and the new k (rounded to bf16) and v are appended
+  // to the caches here: the q/k RoPE + KV append kernel folded into this
+  // launch.
+  const uint16_t *qkv;
+  const float *q_norm, *k_norm;  // [D] or null
+  const float *rope;             // [Lmax, D] RoPE table: cos then sin per position
+  float eps;
 };
 
 namespace {
@@ -58,6 +68,55 @@ __device__ __forceinline__ float wave_sum4(float v) {
   return v;
 }
 
+// Per-head RMSNorm (when nw is set) and split-half RoPE of one head held by
+// the 4 lanes with the same lane & 15, with rope = the RoPE table row of the
+// position (cos of the D/2 frequencies, then sin): the lane holds dims
+// 32 t + 8 g4 + e (t < 4, e < 8); dims of t = 0, 1 pair with t + 2 (d + 64).
+// Same arithmetic as rxw8_dec_qk_rope_kv (ops.rs:929-944, rotary.rs:17-74).
+__device__ __forceinline__ void norm_rope_lane(float (&x)[4][8], const float *nw,
+                                               const float *rope, float eps, int g4) {
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[t][e] * x[t][e];
+  ss = wave_sum4(ss);
+  const float sc = nw ? 1.0f / sqrtf(ss / (float)D + eps) : 1.0f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int i0 = 32 * t + 8 * g4;
+    f32x4 cs[2], sn[2], w0[2], w1[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      cs[j] = *(const f32x4 *)(rope + i0 + 4 * j);
+      sn[j] = *(const f32x4 *)(rope + D / 2 + i0 + 4 * j);
+      if (nw) {
+        w0[j] = *(const f32x4 *)(nw + i0 + 4 * j);
+        w1[j] = *(const f32x4 *)(nw + D / 2 + i0 + 4 * j);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x0 = x[t][e], x1 = x[t + 2][e];
+      if (nw) {
+        x0 = (x0 * sc) * w0[e >> 2][e & 3];
+        x1 = (x1 * sc) * w1[e >> 2][e & 3];
+      }
+      const float c = cs[e >> 2][e & 3], s = sn[e >> 2][e & 3];
+      x[t][e] = x0 * c - x1 * s;
+      x[t + 2][e] = x1 * c + x0 * s;
+    }
+  }
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const u32x4 &r, float *x) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = bf16_bits_to_f32(r[e] & 0xffffu);
+    x[2 * e + 1] = bf16_bits_to_f32(r[e] >> 16);
+  }
+}
+
 // Multi-pass variant: one workgroup of NP waves per (row, kv head, split).
 // Split s of a row covers keys [s * per, min(len, (s + 1) * per)), per =
 // ceil(len / S) rounded up to 64; the workgroup walks it in passes of NP * 64
@@ -66,7 +125,7 @@ __device__ __forceinline__ float wave_sum4(float v) {
 // registers across passes. S = 1 writes the output directly; otherwise every
 // split writes (max, sum, acc) partials (empty splits: max -inf, sum 0) for
 // rxw8_gqa_decode_combine. a.max_chunks carries S.
-template <int G, int NP>
+template <int G, int NP, bool FUSE>
 __device__ void attn_pass(const AttnArgs &a) {
   constexpr int GP = (G + 3) / 4 * 4;
   __shared__ float p_lds[NP][KW][GP];
@@ -83,7 +142,7 @@ __device__ void attn_pass(const AttnArgs &a) {
   len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
   const int per = ((len + S - 1) / S + KW - 1) / KW * KW;
   const int start = split * per;
-  const int end = min(len, start + per);
+  int end = min(len, start + per);
   float *part = a.ws + (((int64_t)bh * S + split) * G) * (2 + D);
   if (start >= end) {  // empty split (uniform per workgroup)
     for (int idx = threadIdx.x; idx < G * (2 + D); idx += blockDim.x)
@@ -96,6 +155,24 @@ __device__ void attn_pass(const AttnArgs &a) {
 
   // raw q (B operand source): lane (head = col, dgroup = g4), 8 dims per step
   u32x4 qraw[4][2];
+  // Fused decode step: the row's new token sits at position pnew = len - 1.
+  // q is its raw bf16 projection (norm + RoPE applied below, after the first
+  // K/V loads are in flight). The split holding key pnew walks only keys
+  // [start, pnew) and its wave 0 adds the new key (raw k / v staged in LDS)
+  // as a last online-softmax step, then appends it to the caches.
+  __shared__ u32x4 new_kv[32];  // raw bf16 k row (16 x 16 B), then v row
+  const uint16_t *src = nullptr;
+  const int pnew = len - 1;
+  const bool own_new = FUSE && end == len;  // uniform
+  if (own_new) end = pnew;
+  if constexpr (FUSE) {
+    src = a.qkv + (int64_t)b * (a.Hq + 2 * a.Hkv) * D;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      qraw[t][0] = *(const u32x4 *)(src + (kvh * G + (col < G ? col : 0)) * D + 32 * t + 8 * g4);
+      qraw[t][1] = u32x4{0, 0, 0, 0};
+    }
+  } else {
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int64_t off = ((int64_t)b * a.Hq + kvh * G + (col < G ? col : 0)) * D + 32 * t + 8 * g4;
@@ -107,6 +184,7 @@ __device__ void attn_pass(const AttnArgs &a) {
       qraw[t][0] = *(const u32x4 *)((const uint16_t *)a.q + off);
       qraw[t][1] = u32x4{0, 0, 0, 0};
     }
+  }
   }
   // K fragments (A operand): lane (key = col, dgroup = g4); V rows: lane
   // (kq = g4, dgroup = col) takes keys 4 * it + kq, dims 8 col .. +7
@@ -140,6 +218,26 @@ __device__ void attn_pass(const AttnArgs &a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
 
+  // fused: q norm + RoPE up front (q then holds f32 bits)
+  if constexpr (FUSE) {
+    float qv[4][8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) unpack_bf16x8(qraw[t][0], qv[t]);
+    norm_rope_lane(qv, a.q_norm, a.rope + (int64_t)pnew * D, a.eps, g4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qraw[t][0][e] = __float_as_uint(qv[t][e]);
+        qraw[t][1][e] = __float_as_uint(qv[t][4 + e]);
+      }
+  }
+  // raw new k (lanes 0-15) and v (lanes 16-31) rows, 16 B per lane; staged
+  // in LDS after the blocks so the load never stalls them
+  u32x4 stage = {0, 0, 0, 0};
+  if (own_new && wave == 0 && lane < 32)
+    stage = *(const u32x4 *)(src + (lane < 16 ? (a.Hq + kvh) * D + 8 * lane
+                                              : (a.Hq + a.Hkv + kvh) * D + 8 * (lane - 16)));
   for (int j0 = first; j0 < end; j0 += NP * KW) {
     load_k(j0);
     load_v(j0);
@@ -149,18 +247,14 @@ __device__ void attn_pass(const AttnArgs &a) {
     for (int t = 0; t < 4; ++t) {
       float qv[8];
       if (col < G) {
-        if (a.q_f32) {
+        if (FUSE || a.q_f32) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             qv[e] = __uint_as_float(qraw[t][0][e]);
             qv[4 + e] = __uint_as_float(qraw[t][1][e]);
           }
         } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            qv[2 * e] = bf16_bits_to_f32(qraw[t][0][e] & 0xffffu);
-            qv[2 * e + 1] = bf16_bits_to_f32(qraw[t][0][e] >> 16);
-          }
+          unpack_bf16x8(qraw[t][0], qv);
         }
       } else {
 #pragma unroll
@@ -250,6 +344,54 @@ __device__ void attn_pass(const AttnArgs &a) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  if (own_new && wave == 0) {
+    // the new key: k = bf16(RoPE(norm(raw k))), scored against q in f32, one
+    // online-softmax step, then append k, v
+    if (lane < 32) new_kv[lane] = stage;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float x[4][8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) unpack_bf16x8(new_kv[4 * t + g4], x[t]);
+    norm_rope_lane(x, a.k_norm, a.rope + (int64_t)pnew * D, a.eps, g4);
+    u32x4 kb[4];
+    float dot = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kb[t][e] = pack_bf16x2(x[t][2 * e], x[t][2 * e + 1]);
+        const float k0 = bf16_bits_to_f32(kb[t][e] & 0xffffu), k1 = bf16_bits_to_f32(kb[t][e] >> 16);
+        const float q0 = __uint_as_float(qraw[t][e >> 1][2 * (e & 1)]);
+        const float q1 = __uint_as_float(qraw[t][e >> 1][2 * (e & 1) + 1]);
+        dot += q0 * k0 + q1 * k1;
+      }
+    dot = wave_sum4(dot);
+    float sc = dot * a.scale;
+    if (a.mask && col < G)
+      sc += a.mask[(int64_t)b * a.mask_sb + (int64_t)(kvh * G + col) * a.mask_sh + pnew];
+    const float m_new = fmaxf(m_run, sc);
+    const float f_old = m_run == kNegInf ? 0.f : __expf(m_run - m_new);
+    const float pe = m_new == kNegInf ? 0.f : __expf(sc - m_new);
+    l_run = l_run * f_old + pe;
+    m_run = m_new;
+    float v[8];
+    const u32x4 vraw = new_kv[16 + col];
+    unpack_bf16x8(vraw, v);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float fh = __shfl(f_old, h), ph = g4 == 0 ? __shfl(pe, h) : 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * fh + ph * v[e];
+    }
+    uint16_t *kd = (uint16_t *)a.kc + (row_base + pnew) * D;
+    uint16_t *vd = (uint16_t *)a.vc + (row_base + pnew) * D;
+    if (col == 0)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) *(u32x4 *)(kd + 32 * t + 8 * g4) = kb[t];
+    if (g4 == 0) *(u32x4 *)(vd + 8 * col) = vraw;
   }
 #pragma unroll
   for (int h = 0; h < G; ++h)
@@ -344,7 +486,11 @@ __device__ void attn_combine(const AttnArgs &a) {
 
 #define RXW8_ATTN(G)                                                                 \
   extern "C" __global__ void __launch_bounds__(512) rxw8_gqa_decode_d128_g##G(AttnArgs a) { \
-    attn_pass<G, 8>(a);                                                              \
+    attn_pass<G, 8, false>(a);                                                       \
+  }                                                                                  \
+  extern "C" __global__ void __launch_bounds__(512)                                  \
+      rxw8_gqa_decode_rope_d128_g##G(AttnArgs a) {                                   \
+    attn_pass<G, 8, true>(a);                                                        \
   }                                                                                  \
   extern "C" __global__ void __launch_bounds__(256)                                  \
       rxw8_gqa_decode_combine_d128_g##G(AttnArgs a) {                                \

@@ -109,11 +109,32 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_rmsnorm(RmsNormArgs a
 // kv_cache.rs:53-68 at start [seq, head, pos, 0]).
 // qkv [T, (Hq + 2 Hkv) * D] bf16 (the bf16 result of the fused projection).
 // One wave per head: lane l owns the SplitHalf pairs (i, i + D/2), i = l + 64 j.
+// ---- RoPE table: row p = cos(p f_i) for i < D/2, then sin(p f_i), with
+// f_i = theta^(-2i/D) in f32 and the angle p * f_i rounded to f32
+// (rotary.rs:17-74 with qwen3_5/mod.rs:211-228). Built once per decoder; the
+// RoPE kernels read it instead of evaluating sin/cos per token.
+struct RopeTableArgs {
+  const float *freqs;  // [D/2]
+  float *tab;          // [Lmax, D]
+  int half;
+};
+
+extern "C" __global__ void __launch_bounds__(64) rxw8_dec_rope_table(RopeTableArgs a) {
+  const int p = blockIdx.x;
+  float *row = a.tab + (int64_t)p * 2 * a.half;
+  for (int i = threadIdx.x; i < a.half; i += blockDim.x) {
+    float sn, cs;
+    sincosf((float)p * a.freqs[i], &sn, &cs);
+    row[i] = cs;
+    row[a.half + i] = sn;
+  }
+}
+
 struct QkRopeArgs {
   const uint16_t *qkv;
   const float *q_norm;  // [D] or null
   const float *k_norm;  // [D] or null
-  const float *freqs;   // [D/2] theta^(-2i/D), f32
+  const float *rope;    // [Lmax, D] RoPE table (rxw8_dec_rope_table)
   const int32_t *pos;   // [T]
   const int32_t *row_seq;
   float *q_out;         // [T, Hq, D] f32
@@ -148,16 +169,14 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_qk_rope_kv(QkRopeArgs
   }
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
   const float scale = nw ? 1.0f / sqrtf(ss / (float)D + a.eps) : 1.0f;
-  const float fp = (float)p;
+  const float *rope = a.rope + (int64_t)p * D;
   for (int i = lane; i < half; i += 64) {
     float x0 = bf16_bits_to_f32(src[i]), x1 = bf16_bits_to_f32(src[i + half]);
     if (nw) {
       x0 = (x0 * scale) * nw[i];
       x1 = (x1 * scale) * nw[i + half];
     }
-    const float ang = fp * a.freqs[i];
-    float sn, cs;
-    sincosf(ang, &sn, &cs);
+    const float cs = rope[i], sn = rope[half + i];
     const float r0 = x0 * cs - x1 * sn;
     const float r1 = x1 * cs + x0 * sn;
     if (is_q) {

@@ -111,6 +111,10 @@ struct AttnArgs {
   int R, Hq, Hkv, Lmax, max_chunks;
   float scale;
   int q_f32, out_f32;
+  const uint16_t *qkv;
+  const float *q_norm, *k_norm;
+  const float *rope;
+  float eps;
 };
 
 struct AttnGenericArgs {
@@ -509,11 +513,13 @@ int bf16_linear_launch(Runtime *rt, const void *x, int x_f32, const uint16_t *w,
 int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
                      int cache_f32, const int32_t *lens, const int32_t *row_seq,
                      const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
-                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale) {
+                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
+                     const AttnRope *rope) {
   if (R == 0) return RXW8_OK;
   const int64_t G = Hq / Hkv;
   const bool fast = !cache_f32 && D == 128 && (G == 1 || G == 2 || G == 4 || G == 8) &&
                     !env_int("RXW8_FORCE_GENERIC", 0);
+  if (rope && !fast) return fail(RXW8_INTERNAL, "fused RoPE attention needs the D = 128 kernel");
   if (fast) {
     // 8 waves walk a split of a row's keys in 512-key passes with an online
     // softmax. S splits per (row, kv head): about one workgroup per CU, and at
@@ -551,8 +557,14 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     a.scale = scale;
     a.q_f32 = q_f32;
     a.out_f32 = out_f32;
+    a.qkv = rope ? rope->qkv : nullptr;
+    a.q_norm = rope ? rope->q_norm : nullptr;
+    a.k_norm = rope ? rope->k_norm : nullptr;
+    a.rope = rope ? rope->table : nullptr;
+    a.eps = rope ? rope->eps : 0.f;
     char kname[64];
-    std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_d128_g%d", (int)G);
+    std::snprintf(kname, sizeof kname, rope ? "rxw8_gqa_decode_rope_d128_g%d" : "rxw8_gqa_decode_d128_g%d",
+                  (int)G);
     int rc = launch(rt, kname, dim3((unsigned)(R * Hkv * max_chunks)), dim3(512), a);
     if (rc || max_chunks == 1) return rc;
     std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_combine_d128_g%d", (int)G);
@@ -799,7 +811,7 @@ int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
                           k_cache->dtype == RXW8_F32, (const int32_t *)lens->ptr, nullptr,
                           mask ? (const float *)mask->ptr : nullptr, sb, sh, out->ptr,
                           out->dtype == RXW8_F32, q->dims[0], q->dims[1], k_cache->dims[1],
-                          k_cache->dims[2], D, scale);
+                          k_cache->dims[2], D, scale, nullptr);
 }
 
 int rxw8_gqa_decode(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache, rxw8_buffer *v_cache,

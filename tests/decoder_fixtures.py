@@ -56,8 +56,9 @@ def tiny_params(cfg, seed=0, std=0.02):
         pre = f"layers.{l}."
         p[pre + "input_layernorm.weight"] = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
         p[pre + "post_attention_layernorm.weight"] = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
-        p[pre + "self_attn.q_norm.weight"] = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
-        p[pre + "self_attn.k_norm.weight"] = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+        if cfg.get("qk_norm", True):
+            p[pre + "self_attn.q_norm.weight"] = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+            p[pre + "self_attn.k_norm.weight"] = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
         q8((HQ + 2 * HKV) * D, H, pre + "self_attn.qkv_proj")
         q8(H, HQ * D, pre + "self_attn.o_proj")
         q8(2 * I, H, pre + "mlp.gate_up_proj")

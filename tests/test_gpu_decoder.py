@@ -121,6 +121,34 @@ def test_decoder_c5_widths_match_oracle(rt):
         assert err <= 1e-2
 
 
+@pytest.mark.parametrize("qk_norm", [True, False])
+def test_decode_fused_rope_matches_separate_kernel(rt, monkeypatch, qk_norm):
+    """Decode steps fold q/k norm + RoPE + the KV append into the attention
+    launch; the separate RoPE/KV kernel (RXW8_DEC_UNFUSED_ROPE=1) must give
+    the same logits, caches and next ids, across splits of several sizes."""
+    cfg = small_cfg(max_seq=1100, qk_norm=qk_norm)
+    params = tiny_params(cfg, seed=95, std=0.05)
+    batch = 3
+    rng = np.random.default_rng(96)
+    prompt = rng.integers(0, cfg["vocab"], (batch, 700)).astype(np.int32)
+    logits = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("RXW8_DEC_UNFUSED_ROPE", mode)
+        model = build(rt, cfg, params, batch)
+        model.forward(rt.buffer(prompt))
+        seq = []
+        for step in range(3):
+            ids = ((np.arange(batch) * 37 + step * 11) % cfg["vocab"]).reshape(batch, 1)
+            out = rt.zeros((batch, cfg["vocab"]), rx().DType.F32)
+            model.forward(rt.buffer(ids.astype(np.int32)), logits=out)
+            seq.append(out.to_numpy())
+        logits[mode] = np.stack(seq)
+        np.testing.assert_array_equal(model.lens()[:batch], [703] * batch)
+    err = rel_err(logits["0"], logits["1"])
+    print(f"qk_norm={qk_norm} fused vs separate RoPE rel_err={err:.3e}")
+    assert err <= 1e-4
+
+
 def test_generate_graph_matches_eager_and_oracle(rt):
     r = rx()
     cfg = small_cfg()
