@@ -480,7 +480,8 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(Splitk
   RXW8_GEMV(KIND, MB, RW, 4)      \
   RXW8_GEMV(KIND, MB, RW, 2)      \
   RXW8_GEMV(KIND, MB, RW, 1)
-// Wide variants: 8 or 16 waves per workgroup = RW row groups x NW/RW k slices.
+// Wide variants: 8, 12 or 16 waves per workgroup = RW row groups x NW/RW k
+// slices (12 waves: 3 row groups of 4, e.g. N = 12288 in 256 workgroups).
 #define RXW8_GEMV_WIDE(MB, RW, U, NW)                                           \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       rxw8_gemv_w8_mb##MB##_rw##RW##_u##U##_w##NW(GemvArgs a) {                 \
@@ -492,6 +493,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(Splitk
   }
 #define RXW8_GEMV_WIDE_U(MB, RW, NW) \
   RXW8_GEMV_WIDE(MB, RW, 4, NW)      \
+  RXW8_GEMV_WIDE(MB, RW, 3, NW)      \
   RXW8_GEMV_WIDE(MB, RW, 2, NW)      \
   RXW8_GEMV_WIDE(MB, RW, 1, NW)
 #define RXW8_GEMV_WIDE_RW(MB, NW) \
@@ -502,6 +504,8 @@ RXW8_GEMV_WIDE_RW(1, 8)
 RXW8_GEMV_WIDE_RW(1, 16)
 RXW8_GEMV_WIDE_RW(2, 8)
 RXW8_GEMV_WIDE_RW(2, 16)
+RXW8_GEMV_WIDE_U(1, 3, 12)
+RXW8_GEMV_WIDE_U(2, 3, 12)
 
 #define RXW8_GEMV_ALL(KIND) \
   RXW8_GEMV_U(KIND, 1, 1)   \

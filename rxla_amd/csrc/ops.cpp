@@ -173,19 +173,26 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
   p.rw = forced_rw == 1 || forced_rw == 4 ? forced_rw : (m <= 4 || prefer_ks1 ? 1 : 4);
   const int64_t slice = w_bf16 ? 32 : 64;  // k per 16-byte lane load
   const bool per_channel = g == k;
-  // A single launch without a split-K reduce: 16 or 8 waves per workgroup
-  // split K inside the workgroup when each wave still gets an even number of
-  // 64-k slices (u8 weights, one 16-row group per workgroup).
-  // Wider row tiles (rw 2 or 4 groups of 16 rows) cut the staging each
-  // workgroup does per weight byte; the widest that still gives every CU a
-  // workgroup wins.
+  // A single launch without a split-K reduce: 16, 12 or 8 waves per
+  // workgroup split K inside the workgroup when each wave still gets an even
+  // number of 64-k slices (u8 weights, rw groups of 16 rows per workgroup).
+  // Wider row tiles cut the staging each workgroup does per weight byte. First
+  // choice: the widest tiling whose workgroups fill the CUs in whole rounds
+  // (no CU idles behind a partial last round); else the widest that still
+  // gives every CU a workgroup. U: the deepest unroll (of 4, 3, 2, 1) that
+  // divides the wave's slices into A/B groups.
   if (prefer_ks1 && allow_wide && !w_bf16 && forced_rw == 0) {
     const int forced_nw = env_int("RXW8_GEMV_NW", 0);
-    for (int nw : {16, 8}) {
-      if (forced_nw && forced_nw != nw) continue;
-      for (int rw : {4, 2, 1}) {
+    static const int shapes[][2] = {{16, 4}, {12, 3}, {16, 2}, {16, 1}, {8, 4}, {8, 2}, {8, 1}};
+    for (int pass = 0; pass < 2; ++pass) {
+      for (const auto &sh : shapes) {
+        const int nw = sh[0], rw = sh[1];
+        if (forced_nw && forced_nw != nw) continue;
         const int kw = nw / rw;
-        if (rw > 1 && (n + 16 * rw - 1) / (16 * rw) < rt->cus) continue;
+        const int64_t tiles = (n + 16 * rw - 1) / (16 * rw);
+        if (pass == 0 && (n % (16 * rw) || tiles % rt->cus)) continue;
+        if (pass == 1 && rw > 1 && tiles < rt->cus) continue;
+        if (pass == 1 && rw == 3) continue;
         if (k % kw || (k / kw) % (2 * slice)) continue;
         if (!per_channel && k % g) continue;
         const size_t lds = gemv_lds(m, k, k, g, rw, p.mb, w_bf16, nw);
@@ -196,7 +203,7 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
         p.lds = lds;
         const int64_t chunks = k / kw / slice;
         p.u = 4;
-        while (chunks % (2 * p.u)) p.u /= 2;
+        while (chunks % (2 * p.u)) --p.u;
         return p;
       }
     }

@@ -100,13 +100,15 @@ def test_decoder_long_prefill_matches_oracle(rt):
     np.testing.assert_array_equal(model.lens()[:batch], [43, 43])
 
 
-def test_decoder_c5_widths_match_oracle(rt):
-    """Hidden 2048 / 16 q heads / 8 kv heads / intermediate 2048 (the C5
-    widths): decode steps take the fused schedule on 16-wave GEMV workgroups,
-    with the RMSNorm scale from the residual GEMV's partial sums and SiLU*up
-    in the gate|up epilogue."""
+@pytest.mark.parametrize("inter", [2048, 6144])
+def test_decoder_c5_widths_match_oracle(rt, inter):
+    """Hidden 2048 / 16 q heads / 8 kv heads and intermediate 6144 (the C5
+    widths) or 2048: decode steps take the fused schedule on wide GEMV
+    workgroups (gate|up N = 12288 on 12-wave, 48-row tiles; down K = 6144
+    with 3-deep loads), with the RMSNorm scale from the residual GEMV's
+    partial sums and SiLU*up in the gate|up epilogue."""
     cfg = tiny_config(layers=2, hidden=2048, q_heads=16, kv_heads=8, head_dim=128,
-                      intermediate=2048, vocab=1008, max_seq=24, group=0)
+                      intermediate=inter, vocab=1008, max_seq=24, group=0)
     params = tiny_params(cfg, seed=91, std=0.03)
     batch = 3
     model = build(rt, cfg, params, batch)
