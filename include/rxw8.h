@@ -178,6 +178,25 @@ int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q,
                          rxw8_buffer *lens, rxw8_buffer *mask, float scale,
                          rxw8_buffer *out);
 
+/* Causal grouped-query prefill attention (attention.rs:83-135 + SDPA
+ * :150-252 with the causal mask key_pos <= q_pos of attention.rs:14-32;
+ * F32 softmax) for S new query rows per sequence whose keys and values are
+ * already in the cache:
+ *   q [B,S,Hq,D] F32|BF16 (token-major, the layout of the projection output);
+ *   k_cache/v_cache [B,Hkv,Lmax,D] BF16 with D = 128 and Hq/Hkv in {1,2,4};
+ *   starts I32 [B] (device): row i of sequence b sits at position
+ *   starts[b] + i and sees keys 0 .. starts[b] + i; entries are clamped by
+ *   the kernel into [0, Lmax - S]; S <= Lmax;
+ *   scale: <= 0 selects 1/sqrt(D).
+ * out [B,S,Hq,D] F32|BF16. Scores use q in f32 accuracy (bf16 hi + lo
+ * parts), probabilities enter P.V rounded to bf16, f32 accumulation. */
+int rxw8_gqa_prefill(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
+                     rxw8_buffer *v_cache, rxw8_buffer *starts, float scale,
+                     int out_dtype, rxw8_buffer **out);
+int rxw8_gqa_prefill_into(rxw8_runtime *rt, rxw8_buffer *q,
+                          rxw8_buffer *k_cache, rxw8_buffer *v_cache,
+                          rxw8_buffer *starts, float scale, rxw8_buffer *out);
+
 /* KvCache::update_at / update_at_checked (kv_cache.rs:53-111): paired
  * dynamic_update_slice of k_update/v_update (equal shapes, rank = cache rank,
  * same dtype) into k_cache/v_cache in place, at `starts` (device I32 [rank]).

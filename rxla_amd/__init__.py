@@ -299,6 +299,23 @@ def grouped_query_attention(rt: Runtime, q: Buffer, k_cache: Buffer, v_cache: Bu
     return Buffer(h)
 
 
+def grouped_query_attention_prefill(rt: Runtime, q: Buffer, k_cache: Buffer, v_cache: Buffer,
+                                    starts: Buffer, scale: float | None = None,
+                                    out_dtype=DType.F32, out: Buffer | None = None) -> Buffer:
+    """Causal attention of S new rows per sequence (q [B,S,Hq,D]) against
+    caches that already hold their keys; row i of sequence b sits at position
+    starts[b] + i (attention.rs:14-32, 83-135)."""
+    s = 0.0 if scale is None else float(scale)
+    if out is not None:
+        _check(_lib.rxw8_gqa_prefill_into(rt.handle, q.handle, k_cache.handle, v_cache.handle,
+                                          starts.handle, ctypes.c_float(s), out.handle))
+        return out
+    h = c_void_p()
+    _check(_lib.rxw8_gqa_prefill(rt.handle, q.handle, k_cache.handle, v_cache.handle,
+                                 starts.handle, ctypes.c_float(s), int(out_dtype), byref(h)))
+    return Buffer(h)
+
+
 class KvCache:
     """Paired fixed-capacity K/V state (crates/rxla-core/src/kv_cache.rs:7-111)."""
 
@@ -333,5 +350,6 @@ from .model import DecoderConfig, DecoderModel  # noqa: E402  (needs the classes
 
 __all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "dequantize", "pack_weight",
            "quantized_linear",
-           "linear_bf16", "QuantizedLinear", "grouped_query_attention", "KvCache",
+           "linear_bf16", "QuantizedLinear", "grouped_query_attention",
+           "grouped_query_attention_prefill", "KvCache",
            "DecoderConfig", "DecoderModel", "bf16_to_f32"]

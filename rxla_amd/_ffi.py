@@ -23,7 +23,7 @@ EXPORTS = [
     "rxw8_buffer_dtype", "rxw8_buffer_dims", "rxw8_buffer_device_ptr",
     "rxw8_dequantize", "rxw8_pack_weight", "rxw8_quantized_linear", "rxw8_quantized_linear_into",
     "rxw8_linear_bf16", "rxw8_linear_bf16_into", "rxw8_gqa_decode", "rxw8_gqa_decode_into",
-    "rxw8_kv_update_at",
+    "rxw8_gqa_prefill", "rxw8_gqa_prefill_into", "rxw8_kv_update_at",
     "rxw8_decoder_create", "rxw8_decoder_destroy", "rxw8_decoder_num_parameters",
     "rxw8_decoder_parameter_info", "rxw8_decoder_bind_parameter", "rxw8_decoder_reset",
     "rxw8_decoder_forward", "rxw8_decoder_generate", "rxw8_decoder_lens",
@@ -68,6 +68,8 @@ def _declare(L):
         "rxw8_linear_bf16_into": (c_int, [vp, vp, vp, vp]),
         "rxw8_gqa_decode": (c_int, [vp, vp, vp, vp, vp, vp, c_float, c_int, POINTER(vp)]),
         "rxw8_gqa_decode_into": (c_int, [vp, vp, vp, vp, vp, vp, c_float, vp]),
+        "rxw8_gqa_prefill": (c_int, [vp, vp, vp, vp, vp, c_float, c_int, POINTER(vp)]),
+        "rxw8_gqa_prefill_into": (c_int, [vp, vp, vp, vp, vp, c_float, vp]),
         "rxw8_kv_update_at": (c_int, [vp, vp, vp, vp, vp, vp, c_int, vp]),
         "rxw8_decoder_create": (c_int, [vp, POINTER(DecoderConfig), POINTER(vp)]),
         "rxw8_decoder_destroy": (c_int, [vp]),

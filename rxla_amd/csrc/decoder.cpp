@@ -41,6 +41,12 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
                      const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
                      int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
                      const AttnRope *rope = nullptr);
+bool prefill_supported(int64_t Hq, int64_t Hkv, int64_t D, int cache_f32);
+int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                   const uint16_t *kc, const uint16_t *vc, const int32_t *starts,
+                   const int32_t *slots, void *out, int out_f32, int64_t o_sb, int64_t o_ss,
+                   int64_t o_sh, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t Lmax,
+                   float scale);
 
 // Kernel argument structs (match kernels/decoder.hip and w8a16_gemv.hip).
 struct DecPosArgs {
@@ -270,6 +276,11 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
       gemv_single_launch(rt, T, d->H, d->Hq * d->D, d->group_for(d->Hq * d->D)) &&
       gemv_single_launch(rt, T, 2 * d->I, d->H, d->group_for(d->H)) &&
       gemv_single_launch(rt, T, d->H, d->I, d->group_for(d->I));
+  // Prompts of 16 or more rows per sequence take the causal prefill kernel
+  // (K/V read once per 64 rows instead of once per row).
+  const char *no_prefill = std::getenv("RXW8_DEC_ROWWISE_PREFILL");
+  const bool use_prefill = s >= 16 && prefill_supported(d->Hq, d->Hkv, d->D, 0) &&
+                           !(no_prefill && *no_prefill == '1');
   // RoPE and the KV append fold into the attention launch when every row is a
   // different sequence's single new token and the D = 128 kernel runs.
   const char *unfused_rope = std::getenv("RXW8_DEC_UNFUSED_ROPE");
@@ -331,9 +342,18 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
                    (int)d->D, (int)d->Lmax, d->cfg.eps};
       const int64_t waves = T * (d->Hq + 2 * d->Hkv);
       if ((rc = launch(rt, "rxw8_dec_qk_rope_kv", dim3(blocks(waves, 4)), dim3(256), a))) return rc;
-      if ((rc = attention_launch(rt, d->q, 1, kcl, vcl, 0, d->row_len, d->row_seq, nullptr, 0, 0,
-                                 d->attn, 0, T, d->Hq, d->Hkv, d->Lmax, d->D, scale)))
+      if (use_prefill) {
+        // causal blocks of 64 prompt rows per (sequence, kv head); lens still
+        // holds each sequence's length before this forward = its first position
+        const int64_t rs = d->Hq * d->D;
+        if ((rc = prefill_launch(rt, d->q, 1, s * rs, rs, d->D, kcl, vcl, d->d_lens, nullptr,
+                                 d->attn, 0, s * rs, rs, d->D, b, s, d->Hq, d->Hkv, d->Lmax,
+                                 scale)))
+          return rc;
+      } else if ((rc = attention_launch(rt, d->q, 1, kcl, vcl, 0, d->row_len, d->row_seq, nullptr,
+                                        0, 0, d->attn, 0, T, d->Hq, d->Hkv, d->Lmax, d->D, scale))) {
         return rc;
+      }
     }
     if (fused) {
       GemvOptions o;

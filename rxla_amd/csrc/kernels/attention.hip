@@ -501,6 +501,234 @@ RXW8_ATTN(2)
 RXW8_ATTN(4)
 RXW8_ATTN(8)
 
+// ---- causal prefill attention (flash-style): S query rows per sequence ----
+//
+// Query row i of sequence b sits at position starts[b] + i and sees keys
+// 0 .. starts[b] + i of its cache slot (the causal mask key_pos <= q_pos,
+// attention.rs:14-32, over the grouped heads of attention.rs:83-135). One
+// workgroup (4 waves) takes 64 consecutive query rows of one (sequence, kv
+// head) and the G query heads sharing it; wave w owns rows 16 w .. 16 w + 15.
+// Keys go by in blocks of 64, staged once per workgroup in LDS: K row-major
+// with 16-byte chunks XOR-swizzled by row (conflict-free fragment reads), V
+// transposed (V^T rows of 64 keys) so P.V can read its MFMA operand along
+// keys. Per wave and head:
+//   S^T = K Q^T   on v_mfma_f32_16x16x32_bf16 (A = K from LDS, B = q split
+//                 into bf16 hi + lo parts, so the scores keep f32 accuracy),
+//   online softmax per query row (lane & 15 = row; the 4 lanes of a row hold
+//                 16 keys each and reduce with two shuffles),
+//   O^T += V^T P^T  (A = V^T from LDS, B = P rounded to bf16 straight from
+//                 the score registers: lane (row, g) holds keys 4g..4g+3 of two
+//                 16-key tiles, and the V^T operand is read in that key order).
+// Blocks past a wave's last visible key are skipped; the last row block of a
+// ragged S computes clamped rows and stores only the valid ones. Workgroups
+// are ordered longest-first (late row blocks see the most keys).
+struct PrefillArgs {
+  const void *q;            // element (b, i, h, d) at b*q_sb + i*q_ss + h*q_sh + d
+  const uint16_t *kc, *vc;  // [Bc, Hkv, Lmax, D] bf16
+  const int32_t *starts;    // [B] position of row 0 of sequence b
+  const int32_t *slots;     // [B] cache slot of sequence b, or null (slot b)
+  void *out;                // element (b, i, h, d) at b*o_sb + i*o_ss + h*o_sh + d
+  int64_t q_sb, q_ss, q_sh, o_sb, o_ss, o_sh;
+  int B, S, Hq, Hkv, Lmax, nqb;
+  float scale;
+  int q_f32, out_f32;
+};
+
+namespace {
+
+constexpr int PKB = 64;        // keys per block
+constexpr int VROW = PKB + 4;  // V^T row pitch (elements): 136 B, 8-byte aligned reads
+
+template <int G>
+__device__ void attn_prefill(const PrefillArgs &a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[PKB * D];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VROW];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, g4 = lane >> 4;
+  const int per_qb = a.B * a.Hkv;
+  const int qb = a.nqb - 1 - (int)(blockIdx.x / per_qb);
+  const int rem = blockIdx.x - (a.nqb - 1 - qb) * per_qb;
+  const int b = rem / a.Hkv, kvh = rem - (rem / a.Hkv) * a.Hkv;
+  int start = a.starts[b];  // clamped so rows sit in [0, Lmax) (host: S <= Lmax)
+  start = start < 0 ? 0 : (start > a.Lmax - a.S ? a.Lmax - a.S : start);
+  const int slot = a.slots ? a.slots[b] : b;
+  const int64_t kv_base = ((int64_t)slot * a.Hkv + kvh) * a.Lmax * D;
+  const int i0 = qb * 64 + wave * 16;
+  const int kv_end = min(start + min(a.S, qb * 64 + 64), a.Lmax);  // keys the workgroup reads
+  const int nblk = (kv_end + PKB - 1) / PKB;
+  const int my_i = min(i0 + col, a.S - 1);
+  const int my_pos = start + my_i;  // last visible key of this lane's row
+  const int wave_last = start + min(i0 + 15, a.S - 1);
+
+  // q^T fragments: lane (row col, dims 32 t + 8 g4 ..), bf16 hi + lo
+  u32x4 qhi[G][4], qlo[G][4];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t off = (int64_t)b * a.q_sb + (int64_t)my_i * a.q_ss +
+                          (int64_t)(kvh * G + h) * a.q_sh + 32 * t + 8 * g4;
+      float v[8];
+      if (a.q_f32) {
+        const f32x4 lo = *(const f32x4 *)((const float *)a.q + off);
+        const f32x4 hi = *(const f32x4 *)((const float *)a.q + off + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = lo[e];
+          v[4 + e] = hi[e];
+        }
+      } else {
+        unpack_bf16x8(*(const u32x4 *)((const uint16_t *)a.q + off), v);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float h0 = round_bf16(v[2 * e]), h1 = round_bf16(v[2 * e + 1]);
+        qhi[h][t][e] = pack_bf16x2(h0, h1);
+        qlo[h][t][e] = pack_bf16x2(v[2 * e] - h0, v[2 * e + 1] - h1);
+      }
+    }
+
+  f32x4 o[G][8];
+  float m_run[G], l_run[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m_run[h] = kNegInf;
+    l_run[h] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // block staging: thread chunk q = tid + 256 u is (key q / 16, 16-byte chunk q % 16)
+  u32x4 kreg[4], vreg[4];
+  auto gload = [&](int blk) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int qc = threadIdx.x + 256 * u;
+      const int key = blk * PKB + (qc >> 4);
+      const int64_t off = kv_base + (int64_t)key * D + (qc & 15) * 8;
+      const bool ok = key < kv_end;
+      kreg[u] = ok ? *(const u32x4 *)(a.kc + off) : u32x4{0, 0, 0, 0};
+      vreg[u] = ok ? *(const u32x4 *)(a.vc + off) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto lds_store = [&]() {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int qc = threadIdx.x + 256 * u;
+      const int r = qc >> 4, c = qc & 15;
+      *(u32x4 *)(ks_lds + r * D + ((c ^ (r & 15)) << 3)) = kreg[u];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt_lds[(8 * c + 2 * e) * VROW + r] = (uint16_t)(vreg[u][e] & 0xffffu);
+        vt_lds[(8 * c + 2 * e + 1) * VROW + r] = (uint16_t)(vreg[u][e] >> 16);
+      }
+    }
+  };
+
+  gload(0);
+  for (int blk = 0; blk < nblk; ++blk) {
+    __syncthreads();  // every wave is done reading the previous block
+    lds_store();
+    __syncthreads();
+    if (blk + 1 < nblk) gload(blk + 1);
+    const int j0 = blk * PKB;
+    if (j0 > wave_last) continue;  // wave-uniform: every key of the block is in this wave's future
+    // S^T tiles: s[h][kt] lane (key j0 + 16 kt + 4 g4 + i, row col)
+    f32x4 s[G][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const int r = kt * 16 + col;
+      u32x4 kf[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) kf[t] = *(const u32x4 *)(ks_lds + r * D + (((4 * t + g4) ^ col) << 3));
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc = mfma16x16x32(as_bf16x8(kf[t]), as_bf16x8(qhi[h][t]), acc);
+          acc = mfma16x16x32(as_bf16x8(kf[t]), as_bf16x8(qlo[h][t]), acc);
+        }
+        s[h][kt] = acc;
+      }
+    }
+    u32x4 pb[G][2];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float mb = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = j0 + 16 * kt + 4 * g4 + i;
+          const float v = key <= my_pos ? s[h][kt][i] * a.scale : kNegInf;
+          s[h][kt][i] = v;
+          mb = fmaxf(mb, v);
+        }
+      mb = wave_max4(mb);
+      // key 0 is visible to every row and block 0 is never skipped, so m_new
+      // is finite from the first block on
+      const float m_new = fmaxf(m_run[h], mb);
+      const float f = m_run[h] == kNegInf ? 0.f : __expf(m_run[h] - m_new);
+      float ls = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = __expf(s[h][kt][i] - m_new);
+          s[h][kt][i] = e;
+          ls += e;
+        }
+      l_run[h] = l_run[h] * f + wave_sum4(ls);
+      m_run[h] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[h][dt] *= f;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        pb[h][ks] = u32x4{pack_bf16x2(s[h][2 * ks][0], s[h][2 * ks][1]),
+                          pack_bf16x2(s[h][2 * ks][2], s[h][2 * ks][3]),
+                          pack_bf16x2(s[h][2 * ks + 1][0], s[h][2 * ks + 1][1]),
+                          pack_bf16x2(s[h][2 * ks + 1][2], s[h][2 * ks + 1][3])};
+    }
+    // O^T += V^T P^T: the V^T operand in the key order of pb
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint16_t *vrow = vt_lds + (dt * 16 + col) * VROW + 32 * ks + 4 * g4;
+        const uint2 lo = *(const uint2 *)vrow, hi = *(const uint2 *)(vrow + 16);
+        const u32x4 va = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+        for (int h = 0; h < G; ++h) o[h][dt] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[h][ks]), o[h][dt]);
+      }
+  }
+  if (i0 + col >= a.S) return;
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float inv = 1.0f / l_run[h];
+    const int64_t ob = (int64_t)b * a.o_sb + (int64_t)(i0 + col) * a.o_ss + (int64_t)(kvh * G + h) * a.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const f32x4 r = o[h][dt] * inv;
+      const int64_t oi = ob + dt * 16 + 4 * g4;
+      if (a.out_f32)
+        *(f32x4 *)((float *)a.out + oi) = r;
+      else
+        *(uint2 *)((uint16_t *)a.out + oi) = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+    }
+  }
+}
+
+}  // namespace
+
+#define RXW8_PREFILL(G)                                                              \
+  extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_prefill_d128_g##G(PrefillArgs a) { \
+    attn_prefill<G>(a);                                                              \
+  }
+RXW8_PREFILL(1)
+RXW8_PREFILL(2)
+RXW8_PREFILL(4)
+
 // ---- generic decode attention (any D <= 256, any group, f32 or bf16 cache):
 // one workgroup per (b, query head); scores staged in LDS (Lmax <= 8192).
 struct AttnGenericArgs {

@@ -117,6 +117,18 @@ struct AttnArgs {
   float eps;
 };
 
+struct PrefillArgs {
+  const void *q;
+  const uint16_t *kc, *vc;
+  const int32_t *starts;
+  const int32_t *slots;
+  void *out;
+  int64_t q_sb, q_ss, q_sh, o_sb, o_ss, o_sh;
+  int B, S, Hq, Hkv, Lmax, nqb;
+  float scale;
+  int q_f32, out_f32;
+};
+
 struct AttnGenericArgs {
   const void *q;
   const void *kc;
@@ -601,6 +613,46 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
   return launch(rt, "rxw8_gqa_decode_generic", dim3((unsigned)(R * Hq)), dim3(256), a);
 }
 
+// Causal prefill attention: q / out element (b, i, h, d) at b*sb + i*ss + h*sh
+// + d; row i of sequence b at position starts[b] + i (clamped on the device
+// into [0, Lmax - S]). D = 128, bf16 caches, Hq / Hkv in {1, 2, 4}.
+bool prefill_supported(int64_t Hq, int64_t Hkv, int64_t D, int cache_f32) {
+  const int64_t G = Hkv > 0 ? Hq / Hkv : 0;
+  return !cache_f32 && D == 128 && Hkv > 0 && Hq % Hkv == 0 && (G == 1 || G == 2 || G == 4);
+}
+
+int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                   const uint16_t *kc, const uint16_t *vc, const int32_t *starts,
+                   const int32_t *slots, void *out, int out_f32, int64_t o_sb, int64_t o_ss,
+                   int64_t o_sh, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t Lmax,
+                   float scale) {
+  if (B == 0 || S == 0) return RXW8_OK;
+  if (!prefill_supported(Hq, Hkv, 128, 0) || S > Lmax)
+    return fail(RXW8_UNIMPLEMENTED, "prefill attention: needs D = 128, Hq/Hkv in {1,2,4}, S <= Lmax");
+  PrefillArgs a;
+  a.q = q;
+  a.kc = kc;
+  a.vc = vc;
+  a.starts = starts;
+  a.slots = slots;
+  a.out = out;
+  a.q_sb = q_sb, a.q_ss = q_ss, a.q_sh = q_sh;
+  a.o_sb = o_sb, a.o_ss = o_ss, a.o_sh = o_sh;
+  a.B = (int)B;
+  a.S = (int)S;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.Lmax = (int)Lmax;
+  a.nqb = (int)((S + 63) / 64);
+  a.scale = scale;
+  a.q_f32 = q_f32;
+  a.out_f32 = out_f32;
+  char kname[48];
+  std::snprintf(kname, sizeof kname, "rxw8_gqa_prefill_d128_g%d", (int)(Hq / Hkv));
+  return launch(rt, kname, dim3((unsigned)(a.nqb * B * Hkv)), dim3(256), a);
+}
+
+
 }  // namespace rxw8
 
 extern "C" {
@@ -771,6 +823,26 @@ int rxw8_linear_bf16(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight, int 
   return RXW8_OK;
 }
 
+
+static int check_prefill(const Buffer *q, const Buffer *k, const Buffer *v, const Buffer *starts) {
+  if (!q || !k || !v || !starts) return fail(RXW8_INVALID_ARGUMENT, "GQA prefill: NULL buffer");
+  if (q->rank != 4 || k->rank != 4 || v->rank != 4)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA prefill requires q [B,S,Hq,D] and caches [B,Hkv,Lmax,D]");
+  if (!is_f(q->dtype) || k->dtype != RXW8_BF16 || v->dtype != RXW8_BF16)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA prefill requires F32/BF16 q and BF16 caches");
+  for (int i = 0; i < 4; ++i)
+    if (k->dims[i] != v->dims[i])
+      return fail(RXW8_INVALID_ARGUMENT, "GQA: K/V caches must have equal shapes");
+  const int64_t B = q->dims[0], S = q->dims[1], Hq = q->dims[2], D = q->dims[3];
+  if (k->dims[0] != B || k->dims[3] != D || S < 1 || S > k->dims[2])
+    return fail(RXW8_INVALID_ARGUMENT, "GQA prefill: batch/dim mismatch or S outside [1, Lmax]");
+  if (!prefill_supported(Hq, k->dims[1], D, 0))
+    return fail(RXW8_UNIMPLEMENTED, "GQA prefill: needs D = 128 and Hq/Hkv in {1, 2, 4}");
+  if (starts->dtype != RXW8_I32 || starts->rank != 1 || starts->dims[0] != B)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA prefill: starts must be I32 [B]");
+  return RXW8_OK;
+}
+
 static int check_gqa(const Buffer *q, const Buffer *k, const Buffer *v, const Buffer *lens,
                      const Buffer *mask, int64_t *mask_sb, int64_t *mask_sh) {
   if (!q || !k || !v || !lens) return fail(RXW8_INVALID_ARGUMENT, "GQA: NULL buffer");
@@ -834,6 +906,46 @@ int rxw8_gqa_decode(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache, rxw8
   rc = new_buffer(rt, out_dtype, q->dims, 3, false, &o);
   if (rc) return rc;
   rc = rxw8_gqa_decode_into(rt, q, k_cache, v_cache, lens, mask, scale, static_cast<rxw8_buffer *>(o));
+  if (rc) {
+    rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+    return rc;
+  }
+  *out = static_cast<rxw8_buffer *>(o);
+  return RXW8_OK;
+}
+
+int rxw8_gqa_prefill_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
+                          rxw8_buffer *v_cache, rxw8_buffer *starts, float scale,
+                          rxw8_buffer *out) {
+  if (!rt || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  int rc = check_prefill(q, k_cache, v_cache, starts);
+  if (rc) return rc;
+  if (!is_f(out->dtype) || out->rank != 4)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA prefill output: shape or dtype mismatch");
+  for (int i = 0; i < 4; ++i)
+    if (out->dims[i] != q->dims[i])
+      return fail(RXW8_INVALID_ARGUMENT, "GQA prefill output: shape or dtype mismatch");
+  if (!std::isfinite(scale)) return fail(RXW8_INVALID_ARGUMENT, "attention scale must be finite");
+  const int64_t B = q->dims[0], S = q->dims[1], Hq = q->dims[2], D = q->dims[3];
+  if (scale <= 0.f) scale = 1.0f / std::sqrt((float)D);
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  return prefill_launch(rt, q->ptr, q->dtype == RXW8_F32, S * Hq * D, Hq * D, D,
+                        (const uint16_t *)k_cache->ptr, (const uint16_t *)v_cache->ptr,
+                        (const int32_t *)starts->ptr, nullptr, out->ptr, out->dtype == RXW8_F32,
+                        S * Hq * D, Hq * D, D, B, S, Hq, k_cache->dims[1], k_cache->dims[2], scale);
+}
+
+int rxw8_gqa_prefill(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache, rxw8_buffer *v_cache,
+                     rxw8_buffer *starts, float scale, int out_dtype, rxw8_buffer **out) {
+  if (!rt || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  int rc = check_prefill(q, k_cache, v_cache, starts);
+  if (rc) return rc;
+  if (!is_f(out_dtype)) return fail(RXW8_INVALID_ARGUMENT, "GQA prefill: out dtype must be F32 or BF16");
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  Buffer *o = nullptr;
+  rc = new_buffer(rt, out_dtype, q->dims, 4, false, &o);
+  if (rc) return rc;
+  rc = rxw8_gqa_prefill_into(rt, q, k_cache, v_cache, starts, scale, static_cast<rxw8_buffer *>(o));
   if (rc) {
     rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
     return rc;

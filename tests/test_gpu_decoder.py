@@ -151,6 +151,31 @@ def test_decode_fused_rope_matches_separate_kernel(rt, monkeypatch, qk_norm):
     assert err <= 1e-4
 
 
+def test_decoder_prefill_kernel_matches_rowwise(rt, monkeypatch):
+    """Prompts of >= 16 rows take the causal prefill kernel; the row-wise
+    decode kernel (RXW8_DEC_ROWWISE_PREFILL=1) must give the same logits, for
+    a first chunk at position 0 and a second chunk that starts mid-cache."""
+    cfg = small_cfg(max_seq=400)
+    params = tiny_params(cfg, seed=97, std=0.05)
+    batch = 2
+    rng = np.random.default_rng(98)
+    chunks = [rng.integers(0, cfg["vocab"], (batch, n)).astype(np.int32) for n in (200, 70)]
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("RXW8_DEC_ROWWISE_PREFILL", mode)
+        model = build(rt, cfg, params, batch)
+        got = []
+        for ids in chunks:
+            out = rt.zeros((batch, cfg["vocab"]), rx().DType.F32)
+            model.forward(rt.buffer(ids), logits=out)
+            got.append(out.to_numpy())
+        outs[mode] = np.stack(got)
+        np.testing.assert_array_equal(model.lens()[:batch], [270, 270])
+    err = rel_err(outs["0"], outs["1"])
+    print(f"prefill kernel vs row-wise logits rel_err={err:.3e}")
+    assert err <= 5e-3
+
+
 def test_generate_graph_matches_eager_and_oracle(rt):
     r = rx()
     cfg = small_cfg()
