@@ -102,6 +102,7 @@ struct Runtime {
   Workspace partials;  // f32 split-K partials
   Workspace scratch;   // general f32 scratch (attention split-K)
   Workspace xcast;     // bf16 copy of f32 activations ahead of the GEMM
+  Workspace wdeq;      // bf16 dequantised weights ahead of the large-M GEMM
 
   hipFunction_t fn(const char *name);
 };

@@ -43,6 +43,9 @@ struct GemmArgs {
   void *y;             // [M, N]
   int M, N, K, G;
   int y_f32, y_mode, w_packed;
+  int group_n;         // n tiles per tile-order group of the 256 x 256 kernel (0: default)
+  int ksplit;          // 256 x 256 u8 kernel: k splits (f32 partials to ws, reduced after)
+  float *ws;           // [ksplit, M, N] f32 partials when ksplit > 1
 };
 
 struct CastArgs {
@@ -54,6 +57,9 @@ struct CastArgs {
 namespace {
 
 constexpr int TN = 128, BK = 64, GROUP_N = 8;
+#ifndef RXW8_GEMM_PREFETCH
+#define RXW8_GEMM_PREFETCH 2
+#endif
 
 // global -> LDS DMA of 16 bytes per lane (global_load_lds_dwordx4; lane l
 // writes LDS bytes [lds + 16 l, +16)). Issued from inline asm on purpose: the
@@ -305,16 +311,21 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
 
   const int tiles_m = (a.M + TMB - 1) / TMB, tiles_n = a.N / TNB;
   const int ntiles = tiles_m * tiles_n;
-  const int per_xcd = (ntiles + 7) / 8;
-  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-  if (t >= ntiles) return;
-  constexpr int GN = 4;  // n tiles per group: the 32 workgroups of an XCD cover ~4 n x 8 m tiles
+  const int S = a.ksplit > 1 ? a.ksplit : 1;  // split = the slowest index of the work
+  const int per_xcd = (ntiles * S + 7) / 8;
+  const int t_all = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t_all >= ntiles * S) return;
+  const int split = t_all / ntiles, t = t_all - split * ntiles;
+  // n tiles per group: the 32 workgroups of an XCD cover ~4 n x 8 m tiles
+  const int GN = a.group_n > 0 ? a.group_n : 4;
   const int group = t / (GN * tiles_m);
   const int first_n = group * GN;
   const int gw = min(GN, tiles_n - first_n);
   const int r = t - group * GN * tiles_m;
   const int n0 = (first_n + r % gw) * TNB, m0 = (r / gw) * TMB;
-  const int KT = a.K / BK, groups = a.K / a.G, last = KT - 1;
+  // k tiles [kb, ke) of this split
+  const int KTall = a.K / BK, groups = a.K / a.G;
+  const int kb = split * KTall / S, ke = (split + 1) * KTall / S, last = ke - 1;
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
@@ -341,7 +352,7 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
     const int id = tid + 512 * p, row = id >> 2, kq = id & 3;
     const int n = n0 + row;
     woff[p] = a.w_packed
-                  ? ((uint32_t)(n >> 4) * (uint32_t)KT * 1024u + (uint32_t)((row & 15) + 16 * kq) * 16u)
+                  ? ((uint32_t)(n >> 4) * (uint32_t)KTall * 1024u + (uint32_t)((row & 15) + 16 * kq) * 16u)
                   : (uint32_t)n * (uint32_t)a.K + (uint32_t)kq * 16u;
     soff[p] = (uint32_t)n * (uint32_t)groups;
   }
@@ -391,49 +402,46 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
   };
 
   // Every k tile issues X_DMA activation DMAs, then 4 weight/scale loads per
-  // lane (past the last tile they repeat tile KT-1 into slots nobody reads),
+  // lane (past the split's last tile they repeat it into slots nobody reads),
   // so the wait counts are exact. Plain s_barrier after explicit waits, as
   // __syncthreads()'s fence would wait for all loads in flight.
   WSet w0, w1;
-  issue_x(0, 0);
-  load_w(0, w0);
-  load_w(min(1, last), w1);
+  issue_x(kb, 0);
+  load_w(kb, w0);
+  load_w(min(kb + 1, last), w1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
   for (int piece = 0; piece < 8; ++piece) dequant_piece(w0, piece, 0);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
+  // 16 groups per k tile, g = 8 ks + i: the 4 MFMAs of weight fragment (ks, i);
+  // fragment reads run PREFETCH groups ahead (a ring of PREFETCH + 1 weight
+  // fragments), the activation fragments of ks = 1 two groups before use.
+  constexpr int PREFETCH = RXW8_GEMM_PREFETCH;
   auto step = [&](int kt, auto xs, WSet &load_set, const WSet &deq_set) {
     constexpr int cur = decltype(xs)::value, nxt = cur ^ 1;
     issue_x(min(kt + 1, last), nxt);
     __builtin_amdgcn_sched_barrier(0);
     load_w(min(kt + 2, last), load_set);
-    bf16x8 af[2], bf[4], bn[4];
+    bf16x8 af[PREFETCH + 1], bf[4], bn[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) bf[j] = frag_b(cur, j, 0);
-    af[0] = frag_a(cur, 0, 0);
+#pragma unroll
+    for (int g = 0; g < PREFETCH; ++g) af[g] = frag_a(cur, g & 7, g >> 3);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {  // ks = 0
-      if (i < 7) {
-        af[(i + 1) & 1] = frag_a(cur, i + 1, 0);
-      } else {
-        af[0] = frag_a(cur, 0, 1);
+    for (int g = 0; g < 16; ++g) {
+      const int i = g & 7, ks = g >> 3;
+      if (g + PREFETCH < 16) af[(g + PREFETCH) % (PREFETCH + 1)] = frag_a(cur, (g + PREFETCH) & 7, (g + PREFETCH) >> 3);
+      if (g == 6)
 #pragma unroll
         for (int j = 0; j < 4; ++j) bn[j] = frag_b(cur, j, 1);
-      }
+      // weights of tile kt+1 were loaded last k tile: this tile's 8 loads are younger
+      if (g == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(af[i & 1], bf[j], acc[i][j]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // weights of tile kt+1 were loaded last k tile: this tile's 8 loads are younger
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {  // ks = 1
-      if (i < 7) af[(i + 1) & 1] = frag_a(cur, i + 1, 1);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(af[i & 1], bn[j], acc[i][j]);
-      dequant_piece(deq_set, i, nxt);
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = mfma16x16x32(af[g % (PREFETCH + 1)], ks ? bn[j] : bf[j], acc[i][j]);
+      if (ks) dequant_piece(deq_set, i, nxt);
       __builtin_amdgcn_sched_barrier(0);
     }
     // activation tile kt+1 (this tile's DMAs) is older than this tile's 4 weight loads
@@ -441,12 +449,131 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
   };
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
-  int kt = 0;
-  for (; kt + 2 <= KT; kt += 2) {
+  int kt = kb;
+  for (; kt + 2 <= ke; kt += 2) {
     step(kt, S0{}, w0, w1);
     step(kt + 1, S1{}, w1, w0);
   }
-  if (kt < KT) step(kt, S0{}, w0, w1);
+  if (kt < ke) step(kt, S0{}, w0, w1);
+
+  if (S > 1) {  // raw f32 partials; rxw8_gemv_splitk_reduce sums them in split order
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = m0 + wm * 64 + 16 * j + r16;
+        if (m < a.M)
+          *(f32x4 *)(a.ws + ((int64_t)split * a.M + m) * a.N + n0 + wn * 128 + 16 * i + 4 * kg) = acc[i][j];
+      }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      gemm_store(a, m0 + wm * 64 + 16 * j + r16, n0 + wn * 128 + 16 * i + 4 * kg, acc[i][j]);
+}
+
+// 256 x 256 tiles over weights already dequantised to bf16 (row-major
+// [N, K], written by rxw8_gemm_dequant_w): both operands go global -> LDS by
+// LDS DMA, so the k loop issues only DMAs, fragment reads and MFMAs. Same
+// waves, fragments and tile order as gemm_tile_big; two stages, the DMAs of
+// tile kt+1 in flight while tile kt is multiplied.
+__device__ __forceinline__ void gemm_tile_bf16w(const GemmArgs &a) {
+  constexpr int TNB = 256, TMB = 256;
+  constexpr int W_BYTES = TNB * BK * 2, X_BYTES = TMB * BK * 2, STAGE = W_BYTES + X_BYTES;
+  constexpr int DMA = TMB * BK * 2 / 1024 / 8;  // 4 LDS-DMA instructions per wave per operand
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1, wm = wave >> 1;
+
+  const int tiles_m = (a.M + TMB - 1) / TMB, tiles_n = a.N / TNB;
+  const int ntiles = tiles_m * tiles_n;
+  const int per_xcd = (ntiles + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t >= ntiles) return;
+  const int GN = a.group_n > 0 ? a.group_n : 4;
+  const int group = t / (GN * tiles_m);
+  const int first_n = group * GN;
+  const int gw = min(GN, tiles_n - first_n);
+  const int r = t - group * GN * tiles_m;
+  const int n0 = (first_n + r % gw) * TNB, m0 = (r / gw) * TMB;
+  const int KT = a.K / BK, last = KT - 1;
+
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+  // DMA instruction i of this wave fills tile rows 8 (wave DMA + i) .. + 8;
+  // lane -> row += lane / 8, physical chunk lane % 8 <- logical chunk (lane % 8) ^ (row & 7)
+  uint32_t xoff[DMA], woff[DMA];
+#pragma unroll
+  for (int i = 0; i < DMA; ++i) {
+    const int row = (wave * DMA + i) * 8 + (lane >> 3);
+    const uint32_t chunk = (uint32_t)((lane & 7) ^ (row & 7)) << 4;
+    const int m = min(m0 + row, a.M - 1);  // rows past M repeat the last row (not stored)
+    xoff[i] = (uint32_t)m * (uint32_t)a.K * 2u + chunk;
+    woff[i] = (uint32_t)(n0 + row) * (uint32_t)a.K * 2u + chunk;
+  }
+  const char *xbase = (const char *)a.x, *wbase = (const char *)a.w;
+  auto issue = [&](int kt, int stage) {
+#pragma unroll
+    for (int i = 0; i < DMA; ++i)
+      dma16(wbase, woff[i] + (uint32_t)(kt * (BK * 2)),
+            lds_addr(smem + stage * STAGE + (wave * DMA + i) * 1024));
+#pragma unroll
+    for (int i = 0; i < DMA; ++i)
+      dma16(xbase, xoff[i] + (uint32_t)(kt * (BK * 2)),
+            lds_addr(smem + stage * STAGE + W_BYTES + (wave * DMA + i) * 1024));
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int r16 = lane & 15, kg = lane >> 4;
+  auto frag_a = [&](int stage, int i, int ks) {
+    return as_bf16x8(*(const u32x4 *)(smem + stage * STAGE + swz(wn * 128 + 16 * i + r16, ks * 4 + kg)));
+  };
+  auto frag_b = [&](int stage, int j, int ks) {
+    return as_bf16x8(
+        *(const u32x4 *)(smem + stage * STAGE + W_BYTES + swz(wm * 64 + 16 * j + r16, ks * 4 + kg)));
+  };
+
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  constexpr int PREFETCH = RXW8_GEMM_PREFETCH;
+  auto step = [&](int kt, auto xs) {
+    constexpr int cur = decltype(xs)::value, nxt = cur ^ 1;
+    issue(min(kt + 1, last), nxt);
+    bf16x8 af[PREFETCH + 1], bf[4], bn[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bf[j] = frag_b(cur, j, 0);
+#pragma unroll
+    for (int g = 0; g < PREFETCH; ++g) af[g] = frag_a(cur, g & 7, g >> 3);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const int i = g & 7, ks = g >> 3;
+      if (g + PREFETCH < 16) af[(g + PREFETCH) % (PREFETCH + 1)] = frag_a(cur, (g + PREFETCH) & 7, (g + PREFETCH) >> 3);
+      if (g == 6)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bn[j] = frag_b(cur, j, 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = mfma16x16x32(af[g % (PREFETCH + 1)], ks ? bn[j] : bf[j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // tile kt+1 is in LDS once this wave's DMAs land; the barrier covers every wave's
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  int kt = 0;
+  for (; kt + 2 <= KT; kt += 2) {
+    step(kt, S0{});
+    step(kt + 1, S1{});
+  }
+  if (kt < KT) step(kt, S0{});
 
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -456,6 +583,54 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
 }
 
 }  // namespace
+
+// Exact dequantisation into a bf16 [N, K] row-major workspace, the input of
+// rxw8_w8a16_gemm_bf16w_t256: w = bf16(fma(f32(u), s, -128 s)), the same
+// arithmetic as the in-loop dequantisation (layers.rs:277-294). One thread per
+// 16 codes (G % 16 == 0, so one scale); row-major or packed source.
+struct DequantWArgs {
+  const uint8_t *w;
+  const float *scale;
+  uint16_t *out;
+  int N, K, G, packed;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_gemm_dequant_w(DequantWArgs a) {
+  const int64_t slices = (int64_t)a.N * (a.K / 16);
+  const int64_t sl = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (sl >= slices) return;
+  int row, k0;
+  if (a.packed) {  // [N/16][K/64][64 lanes][16 B]: lane l holds row 16 t + l % 16, k 64 c + 16 (l / 16)
+    const int l = (int)(sl & 63);
+    const int64_t tc = sl >> 6;
+    const int kc = a.K / 64;
+    const int tt = (int)(tc / kc), c = (int)(tc - (int64_t)tt * kc);
+    row = 16 * tt + (l & 15);
+    k0 = 64 * c + 16 * (l >> 4);
+  } else {
+    const int per_row = a.K / 16;
+    row = (int)(sl / per_row);
+    k0 = (int)(sl - (int64_t)row * per_row) * 16;
+  }
+  const u32x4 w = __builtin_nontemporal_load((const u32x4 *)(a.w + sl * 16));
+  const float sc = a.scale[(int64_t)row * (a.K / a.G) + k0 / a.G], o = -128.0f * sc;
+  uint32_t h[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t w4 = w[e];
+    h[2 * e] = pack_bf16x2(__builtin_fmaf((float)(w4 & 0xffu), sc, o),
+                           __builtin_fmaf((float)((w4 >> 8) & 0xffu), sc, o));
+    h[2 * e + 1] = pack_bf16x2(__builtin_fmaf((float)((w4 >> 16) & 0xffu), sc, o),
+                               __builtin_fmaf((float)(w4 >> 24), sc, o));
+  }
+  u32x4 *dst = (u32x4 *)(a.out + (int64_t)row * a.K + k0);
+  dst[0] = u32x4{h[0], h[1], h[2], h[3]};
+  dst[1] = u32x4{h[4], h[5], h[6], h[7]};
+}
+
+extern "C" __global__ void __launch_bounds__(512) rxw8_w8a16_gemm_bf16w_t256(GemmArgs a) {
+  gemm_tile_bf16w(a);
+}
 
 // Launch contract (checked by the host): N % 128 == 0, K % 64 == 0,
 // G % 64 == 0 and K % G == 0, M >= 1, M * K * 2 < 2^31 and the weight bytes

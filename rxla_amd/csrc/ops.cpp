@@ -57,6 +57,16 @@ struct GemmArgs {
   void *y;
   int M, N, K, G;
   int y_f32, y_mode, w_packed;
+  int group_n;
+  int ksplit;
+  float *ws;
+};
+
+struct DequantWArgs {
+  const uint8_t *w;
+  const float *scale;
+  uint16_t *out;
+  int N, K, G, packed;
 };
 
 struct CastArgs {
@@ -458,9 +468,14 @@ static int run_gemm(Runtime *rt, const void *x, int x_f32, const uint8_t *w, boo
   a.y_f32 = y_f32;
   a.y_mode = y_mode;
   a.w_packed = packed ? 1 : 0;
+  a.group_n = env_int("RXW8_GEMM_GN", 0);
+  a.ksplit = 1;
+  a.ws = nullptr;
   // Three tilings (one workgroup per CU each): 256 x 256 (8 waves), 256 x 128
-  // and 128 x 128 (4 waves). Pick the best measured per-tile efficiency times
-  // the fraction of CU slots the tile count fills in its last round.
+  // and 128 x 128 (4 waves); the 256 x 256 one may also split K (f32 partials
+  // summed in split order by a second launch). Pick the least modelled time:
+  // whole rounds of workgroups x one tile's MFMA time at the tiling's measured
+  // efficiency, plus the partials' HBM round trip for splits.
   struct Tiling {
     const char *kernel;
     int tm, tn, threads;
@@ -470,20 +485,63 @@ static int run_gemm(Runtime *rt, const void *x, int x_f32, const uint8_t *w, boo
                                    {"rxw8_w8a16_gemm_m256", 256, 128, 256, 0.36},
                                    {"rxw8_w8a16_gemm_m128", 128, 128, 256, 0.30}};
   const int forced = env_int("RXW8_GEMM_TILE", 0);  // 256x256 = 256, 256x128 = 2, 128x128 = 128
+  const int forced_ks = env_int("RXW8_GEMM_KSPLIT", 0);
+  const double cu_flops = 2.5e15 / 256.0, hbm = 4.0e12;  // per-CU bf16 MFMA peak, B/s
   const Tiling *best = nullptr;
-  double best_score = -1;
+  int best_ks = 1;
+  double best_t = 1e30;
   for (const Tiling &tl : tilings) {
     if (N % tl.tn) continue;
     const int code = tl.tn == 256 ? 256 : (tl.tm == 256 ? 2 : 128);
     if (forced && forced != code) continue;
     const int64_t tiles = (M + tl.tm - 1) / tl.tm * (N / tl.tn);
-    const int64_t rounds = (tiles + rt->cus - 1) / rt->cus;
-    const double score = tl.eff * (double)tiles / (double)(rounds * rt->cus);
-    if (score > best_score) best_score = score, best = &tl;
+    for (int ks : {1, 2, 3, 4, 6, 8}) {
+      if (ks > 1 && (tl.tn != 256 || ks > K / 64)) continue;
+      if (forced_ks && forced_ks != ks && (tl.tn != 256 || forced_ks <= K / 64 || ks > 1)) continue;
+      const int64_t rounds = (tiles * ks + rt->cus - 1) / rt->cus;
+      double t = (double)rounds * tl.tm * tl.tn * (double)K / ks * 2.0 / (cu_flops * tl.eff);
+      if (ks > 1) t += (ks + 1.0) * (double)M * N * 4.0 / hbm + 3e-6;
+      if (t < best_t) best_t = t, best = &tl, best_ks = ks;
+    }
   }
   if (!best) return fail(RXW8_INVALID_ARGUMENT, "no GEMM tiling for N=%lld", (long long)N);
   const int64_t tiles = (M + best->tm - 1) / best->tm * (N / best->tn);
   const int64_t per_xcd = (tiles + 7) / 8;
+  // Long inputs: dequantise the weights once into a bf16 workspace (a
+  // bandwidth-bound pass of N K (1 + 2) bytes) and run the 256 x 256 tiles on
+  // bf16 x bf16, both operands DMA'd into LDS: the k loop then carries no
+  // dequantisation, which costs more than the pass once M reaches a few
+  // thousand rows. Same weight values bit for bit.
+  const int bf16w_env = env_int("RXW8_GEMM_BF16W", -1);
+  const bool bf16w = best->tn == 256 && best_ks == 1 && N * K * 2 < (1LL << 31) &&
+                     (bf16w_env == 1 || (bf16w_env < 0 && M >= 4096));
+  if (bf16w) {
+    if ((rc = ensure_workspace(rt, rt->wdeq, (size_t)(N * K) * 2, false))) return rc;
+    DequantWArgs d{w, s, (uint16_t *)rt->wdeq.ptr, (int)N, (int)K, (int)G, packed ? 1 : 0};
+    const int64_t slices = N * (K / 16);
+    if ((rc = launch(rt, "rxw8_gemm_dequant_w", dim3((unsigned)((slices + 255) / 256)), dim3(256), d)))
+      return rc;
+    a.w = (const uint8_t *)rt->wdeq.ptr;
+    a.w_packed = 0;
+    return launch(rt, "rxw8_w8a16_gemm_bf16w_t256", dim3((unsigned)(per_xcd * 8)), dim3(512), a);
+  }
+  if (best_ks > 1) {
+    if ((rc = ensure_workspace(rt, rt->partials, (size_t)best_ks * M * N * 4, false))) return rc;
+    a.ksplit = best_ks;
+    a.ws = (float *)rt->partials.ptr;
+    const int64_t work = (tiles * best_ks + 7) / 8 * 8;
+    if ((rc = launch(rt, best->kernel, dim3((unsigned)work), dim3(best->threads), a))) return rc;
+    SplitkReduceArgs r;
+    r.ws = (const float *)rt->partials.ptr;
+    r.scale = nullptr;
+    r.y = y;
+    r.M = (int)M;
+    r.N = (int)N;
+    r.ksplit = best_ks;
+    r.y_f32 = y_f32;
+    r.y_mode = y_mode;
+    return launch(rt, "rxw8_gemv_splitk_reduce", dim3(grid_for(M * N / 4, 256, 4096)), dim3(256), r);
+  }
   return launch(rt, best->kernel, dim3((unsigned)(per_xcd * 8)), dim3(best->threads), a);
 }
 

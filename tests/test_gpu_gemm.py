@@ -121,14 +121,21 @@ def test_gemm_deterministic(rt):
     np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize("tile", [128, 2, 256])  # 128x128, 256x128, 256x256
+@pytest.mark.parametrize("tile", [128, 2, 256, "256w", "256k2", "256k3"])
 @pytest.mark.parametrize("m,n,k,g", [(65, 256, 64, 64), (300, 512, 256, 128), (513, 768, 640, 640)])
 def test_gemm_tile_kernels(rt, monkeypatch, tile, m, n, k, g):
     """Every tiling (chosen by size in normal use) on ragged M, single- and
-    odd-count k tiles, packed and row-major."""
+    odd-count k tiles, packed and row-major: 128x128, 256x128, 256x256;
+    "256w" is the 256 x 256 kernel over weights first dequantised to a bf16
+    workspace (the long-input path), "256kS" the 256 x 256 kernel split S
+    ways over K (uneven k-tile ranges; a single-k-tile K runs unsplit)."""
     r = rx()
-    monkeypatch.setenv("RXW8_GEMM_TILE", str(tile))
-    rng = np.random.default_rng(m + n + k + tile)
+    name = str(tile)
+    base, _, ks = name.partition("k")
+    monkeypatch.setenv("RXW8_GEMM_TILE", base.rstrip("w"))
+    monkeypatch.setenv("RXW8_GEMM_BF16W", "1" if base.endswith("w") else "0")
+    monkeypatch.setenv("RXW8_GEMM_KSPLIT", ks or "1")
+    rng = np.random.default_rng(m + n + k + sum(map(ord, name)))
     x = oracle.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
     u8, s = oracle.quantize_w8((rng.standard_normal((n, k)) * 0.02).astype(np.float32), g)
     ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16, oracle.ACCUM_F64, threads=16)
