@@ -284,8 +284,13 @@ static bool is_f(int dt) { return dt == RXW8_F32 || dt == RXW8_BF16; }
 static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf16,
                     bool packed, const float *scale, void *y, int y_f32, int64_t M, int64_t N,
                     int64_t K, int64_t G, int y_mode = 0, const GemvOptions *pro = nullptr) {
+  // Plain calls take the wide single-launch tilings when even 64-row tiles
+  // give every CU a workgroup (e.g. N = 24576): x is then staged once per 64
+  // rows and no split-K reduce runs. Smaller N keep the 4-wave plans, which
+  // fill the CUs with more, narrower tiles.
   GemvOptions plain;
-  plain.prefer_ks1 = env_int("RXW8_GEMV_PREFER_WIDE", 0) != 0;
+  const int wide_env = env_int("RXW8_GEMV_PREFER_WIDE", -1);
+  plain.prefer_ks1 = wide_env >= 0 ? wide_env != 0 : (!w_bf16 && N / 64 >= rt->cus);
   if (!pro) pro = &plain;
   const int64_t mchunk = M <= 16 ? 16 : 32;
   GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16, pro->prefer_ks1,
