@@ -11,8 +11,9 @@ weight bytes and the figure is HBM bandwidth.
 
 value        = sweep algorithmic bytes / wall time of the timed steps (GB/s);
                each step is one HIP-graph replay of the 9 launches
-roofline     = the B <= 4 GEMV kernel (rxw8_gemv_w8_pk_mb1_rw1_u4) at its
-               largest sweep shape, B=1 N=24576: algorithmic bytes per launch /
+roofline     = the GEMV kernel of the largest sweep shape, B=1 N=24576
+               (rxw8_gemv_w8_pk_mb1_rw3_u4_w12: 12 waves, 48-row tiles, 512
+               workgroups = 2 whole rounds): algorithmic bytes per launch /
                launch duration, from HIP events on the runtime's stream around
                runs of back-to-back launches of the shape; traffic = the HBM
                bytes per launch recorded in profiles/ by two rocprofv3 --pmc
@@ -31,6 +32,9 @@ prefill_gemm  BASELINE configs[2]: x bf16 [M,4096] for M in {512, 2048, 8192}
 decode_attention  BASELINE configs[3]: batch 8, 32/8 heads, D 128, lengths
               uniform in [512, 8192], bf16 cache; bytes = K and V rows read
               (lens * 8 heads * 128 * 2 B * 2) + q + out, two cache copies
+prefill_attention  the C5 prompt's causal attention (8 x 1024 rows, 16/8
+              heads, D 128) on rxw8_gqa_prefill: flops over HIP-event time,
+              roofline against dense bf16 MFMA
 decoder       BASELINE configs[4]: 28-layer synthetic decoder (random-init
               weights, W8 per output channel), batch 8, prompt 1024, 256
               greedy steps through rxw8_decoder_generate (decode steps replay
@@ -124,7 +128,10 @@ def bench_gemm(rt, rx, torch, stream, reps=10):
         with torch.cuda.stream(stream):
             y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
         yb, xb, (u, s_) = rt.wrap_tensor(y), rt.wrap_tensor(xs[(m, k)]), wb[(n, k)]
-        for _ in range(2):
+        # steady state: about 60 ms of back-to-back launches before timing, so
+        # the clocks have settled at their sustained level under MFMA load
+        warm = max(3, int(0.06 / (2 * m * n * k / 1.0e15)))
+        for _ in range(warm):
             rx.quantized_linear(rt, xb, u, s_, rx.DType.BF16, out=yb)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
@@ -138,9 +145,11 @@ def bench_gemm(rt, rx, torch, stream, reps=10):
     big = out["M8192_N12288_K4096"]
     return out, {"bound": "mfma", "achieved": big["TFLOPs"], "peak": MFMA_BF16_PEAK_TFLOPS,
                  "unit": "TFLOP/s", "frac": round(big["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS, 4),
-                 "traffic": None, "kernel": "rxw8_w8a16_gemm_t256",
+                 "traffic": None,
+                 "kernel": "rxw8_gemm_dequant_w + rxw8_w8a16_gemm_bf16w_t256 (M >= 4096 path)",
                  "shape": "M=8192 N=12288 K=4096", "mean_launch_us": big["us"],
-                 "timing": f"HIP events around {reps} back-to-back launches"}
+                 "timing": f"HIP events around {reps} back-to-back launches after ~60 ms "
+                           "of warmup launches of the shape"}
 
 
 def bench_attention(rt, rx, torch, stream, reps=20):
@@ -159,8 +168,8 @@ def bench_attention(rt, rx, torch, stream, reps=20):
     cb = [(rt.wrap_tensor(k), rt.wrap_tensor(v)) for k, v in caches]
     qb, ob, lb = rt.wrap_tensor(q), rt.wrap_tensor(o), rt.wrap_tensor(lt)
     nbytes = int(lens.sum()) * HKV * D * 2 * 2 + 2 * B * HQ * D * 2 + 4 * B
-    for c in range(2):
-        rx.grouped_query_attention(rt, qb, cb[c][0], cb[c][1], lb, out=ob)
+    for c in range(100):
+        rx.grouped_query_attention(rt, qb, cb[c % 2][0], cb[c % 2][1], lb, out=ob)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -175,6 +184,41 @@ def bench_attention(rt, rx, torch, stream, reps=20):
             "kernels": "rxw8_gqa_decode_d128_g4 + rxw8_gqa_decode_combine_d128_g4",
             "us_per_call": round(t * 1e6, 2), "bytes_per_call": nbytes,
             "lens": lens.tolist(), "timing": f"HIP events around {reps} calls, 2 cache copies"}
+
+
+def bench_prefill_attention(rt, rx, torch, stream, reps=10):
+    """C5 prompt attention: 8 sequences x 1024 causal rows, 16 q / 8 kv heads,
+    D 128, keys already in a bf16 cache [8, 8, 1280, 128]; f32 q, bf16 out.
+    Flops = 4 * D * Hq * sum over rows of (visible keys) (QK^T and P.V)."""
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    B, S, HQ, HKV, D, LMAX = 8, 1024, 16, 8, 128, 1280
+    with torch.cuda.stream(stream):
+        q = torch.randn((B, S, HQ, D), device="cuda", generator=gen)
+        kc = torch.randn((B, HKV, LMAX, D), device="cuda", generator=gen).to(torch.bfloat16)
+        vc = torch.randn((B, HKV, LMAX, D), device="cuda", generator=gen).to(torch.bfloat16)
+        o = torch.empty((B, S, HQ, D), dtype=torch.bfloat16, device="cuda")
+        starts = torch.zeros(B, dtype=torch.int32, device="cuda")
+    stream.synchronize()
+    qb, kb, vb, ob, sb = (rt.wrap_tensor(t) for t in (q, kc, vc, o, starts))
+    for _ in range(400):  # ~60 ms of warmup: sustained clocks under MFMA load
+        rx.grouped_query_attention_prefill(rt, qb, kb, vb, sb, out=ob)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        rx.grouped_query_attention_prefill(rt, qb, kb, vb, sb, out=ob)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    flops = 4 * D * HQ * B * S * (S + 1) // 2
+    tf = flops / t / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "rxw8_gqa_prefill_d128_g2", "us_per_call": round(t * 1e6, 1),
+            "flops_per_call": flops, "shape": "B=8 S=1024 Hq=16 Hkv=8 D=128, causal from 0",
+            "note": "flops count the visible (causal) keys once; q enters as bf16 hi + lo, "
+                    "so the MFMA work is 1.5x this count",
+            "timing": f"HIP events around {reps} back-to-back calls after 400 warmup calls"}
 
 
 def bench_decoder(rt, rx, torch, stream, prompt_len=1024, steps=256, batch=8):
@@ -442,8 +486,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": recorded_traffic() if layout == "packed" else None,
-                     "kernel": "rxw8_gemv_w8_pk_mb1_rw1_u4" if layout == "packed"
-                     else "rxw8_gemv_w8_mb1_rw1_u4",
+                     "kernel": "rxw8_gemv_w8_pk_mb1_rw3_u4_w12" if layout == "packed"
+                     else "rxw8_gemv_w8_mb1_rw3_u4_w12",
                      "shape": "B=1 N=24576 K=4096", "launch_us": round(roof_s * 1e6, 3),
                      "launch_bytes": roof_bytes,
                      "timing": "median of HIP event pairs on the runtime stream around "
@@ -457,7 +501,8 @@ def main():
         "roofline_b16": {"bound": "hbm", "achieved": round(b16_bytes / b16_s / 1e9, 2),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(b16_bytes / b16_s / 1e9 / HBM_PEAK_GBS, 4),
-                         "kernels": "rxw8_gemv_w8_pk_mb1_rw4_u4 + rxw8_gemv_splitk_reduce",
+                         "kernels": "N=24576: rxw8_gemv_w8_pk_mb1_rw3_u4_w12; N=4096, 6144: "
+                                    "rxw8_gemv_w8_pk_mb1_rw4_u4 + rxw8_gemv_splitk_reduce",
                          "mean_launch_us": round(b16_s * 1e6, 3)},
         "sweep": sweep,
         "device": info,
@@ -471,6 +516,9 @@ def main():
     if not args.skip_attention:
         log("decode attention ...")
         out["roofline_attention"] = bench_attention(rt, rx, torch, stream)
+    if not args.skip_attention:
+        log("prefill attention ...")
+        out["roofline_prefill_attention"] = bench_prefill_attention(rt, rx, torch, stream)
     if not args.skip_decoder:
         log("synthetic 28-layer decoder: prefill 8x1024, 256 greedy steps ...")
         out["decoder"] = bench_decoder(rt, rx, torch, stream)
