@@ -42,6 +42,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
                      int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
                      const AttnRope *rope = nullptr);
 bool prefill_supported(int64_t Hq, int64_t Hkv, int64_t D, int cache_f32);
+bool gemm_eligible(int64_t M, int64_t N, int64_t K, int64_t G);
 int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                    const uint16_t *kc, const uint16_t *vc, const int32_t *starts,
                    const int32_t *slots, void *out, int out_f32, int64_t o_sb, int64_t o_ss,
@@ -381,10 +382,15 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
       RmsNormArgs a{d->h, fptr(P_POST_NORM), d->xn, nullptr, d->H, (int)T, 1, 0, d->cfg.eps};
       if ((rc = launch(rt, "rxw8_dec_rmsnorm", dim3((unsigned)T), dim3(256), a))) return rc;
     }
-    if ((rc = qlinear_launch(rt, d->xn, 0, wptr(P_GU_W), packed(P_GU_W), fptr(P_GU_S), d->gu, 0, T,
-                             2 * d->I, d->H, d->group_for(d->H), 1, 0)))
-      return rc;
-    {
+    if (d->gu_ilv && gemm_eligible(T, 2 * d->I, d->H, d->group_for(d->H))) {
+      // the GEMM epilogue applies SiLU(gate) * up over the interleaved tiles
+      if ((rc = qlinear_launch(rt, d->xn, 0, wptr(P_GU_W), packed(P_GU_W), fptr(P_GU_S), d->act, 0,
+                               T, 2 * d->I, d->H, d->group_for(d->H), 1, 2)))
+        return rc;
+    } else {
+      if ((rc = qlinear_launch(rt, d->xn, 0, wptr(P_GU_W), packed(P_GU_W), fptr(P_GU_S), d->gu, 0,
+                               T, 2 * d->I, d->H, d->group_for(d->H), 1, 0)))
+        return rc;
       SiluMulArgs a{d->gu, d->act, T, d->I, d->gu_ilv ? 1 : 0};
       if ((rc = launch(rt, "rxw8_dec_silu_mul", dim3(blocks(T * d->I, 256 * 4)), dim3(256), a)))
         return rc;

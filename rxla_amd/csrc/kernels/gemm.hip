@@ -84,7 +84,28 @@ __device__ __forceinline__ uint32_t lds_addr(const char *p) {
 // Byte offset of 16-byte chunk c (0..7) of row r in a swizzled 128-B-row tile.
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 
+// Epilogue of one accumulator: lane holds y[m, n .. n+3]. Called by every
+// lane of the wave (y_mode 2 exchanges values between lanes).
+//   y_mode 0: bf16 or (bf16-rounded) f32 y;  1: f32 residual y += bf16(v);
+//   2: SwiGLU over weight rows interleaved in 16-row tiles of 8 gate + 8 up
+//      rows (16 t + j and 16 t + 8 + j are channel 8 t + j): y bf16 [M, N/2]
+//      gets bf16(silu(bf16(g)) * bf16(u)) (ops.rs:331-342); the up partner of
+//      a gate lane (n % 16 < 8) sits 32 lanes higher.
 __device__ __forceinline__ void gemm_store(const GemmArgs &a, int m, int n, f32x4 v) {
+  if (a.y_mode == 2) {
+    f32x4 up;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(v[i], 32);
+    if ((n & 15) < 8 && m < a.M) {
+      const int c = (n >> 4) * 8 + (n & 7);
+      *(uint2 *)((uint16_t *)a.y + (int64_t)m * (a.N / 2) + c) =
+          uint2{pack_bf16x2(silu_mul_f32(round_bf16(v[0]), round_bf16(up[0])),
+                            silu_mul_f32(round_bf16(v[1]), round_bf16(up[1]))),
+                pack_bf16x2(silu_mul_f32(round_bf16(v[2]), round_bf16(up[2])),
+                            silu_mul_f32(round_bf16(v[3]), round_bf16(up[3])))};
+    }
+    return;
+  }
   if (m >= a.M) return;
   if (a.y_mode == 1) {
     float4 *h = (float4 *)((float *)a.y + (int64_t)m * a.N + n);

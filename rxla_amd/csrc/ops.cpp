@@ -442,7 +442,7 @@ namespace rxw8 {
 // Prefill-sized products go to the MFMA GEMM (128 x 128 output tiles; the
 // weight tile is dequantised once per 128 activation rows); smaller M stays on
 // the GEMV, which streams the weights once per 16/32-row chunk.
-static bool gemm_eligible(int64_t M, int64_t N, int64_t K, int64_t G) {
+bool gemm_eligible(int64_t M, int64_t N, int64_t K, int64_t G) {
   static const int64_t min_m = env_int("RXW8_GEMM_MIN_M", 64);
   // 32-bit byte offsets inside the kernel: activations M*K*2, weights N*K
   return M > min_m && N % 128 == 0 && K % 64 == 0 && G % 64 == 0 && M * K * 2 < (1LL << 31) &&
@@ -501,7 +501,7 @@ static int run_gemm(Runtime *rt, const void *x, int x_f32, const uint8_t *w, boo
     if (forced && forced != code) continue;
     const int64_t tiles = (M + tl.tm - 1) / tl.tm * (N / tl.tn);
     for (int ks : {1, 2, 3, 4, 6, 8}) {
-      if (ks > 1 && (tl.tn != 256 || ks > K / 64)) continue;
+      if (ks > 1 && (tl.tn != 256 || ks > K / 64 || y_mode == 2)) continue;
       if (forced_ks && forced_ks != ks && (tl.tn != 256 || forced_ks <= K / 64 || ks > 1)) continue;
       const int64_t rounds = (tiles * ks + rt->cus - 1) / rt->cus;
       double t = (double)rounds * tl.tm * tl.tn * (double)K / ks * 2.0 / (cu_flops * tl.eff);
