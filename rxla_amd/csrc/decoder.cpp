@@ -341,8 +341,14 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
                    d->cfg.qk_norm ? fptr(P_KN) : nullptr,
                    d->d_rope, d->pos, d->row_seq, d->q, kcl, vcl, (int)T, (int)d->Hq, (int)d->Hkv,
                    (int)d->D, (int)d->Lmax, d->cfg.eps};
-      const int64_t waves = T * (d->Hq + 2 * d->Hkv);
-      if ((rc = launch(rt, "rxw8_dec_qk_rope_kv", dim3(blocks(waves, 4)), dim3(256), a))) return rc;
+      const int64_t rows = T * (d->Hq + 2 * d->Hkv);
+      const char *generic_rope = std::getenv("RXW8_DEC_GENERIC_ROPE");
+      if (d->D == 128 && !(generic_rope && *generic_rope == '1')) {  // 8 lanes per (token, head) row
+        if ((rc = launch(rt, "rxw8_dec_qk_rope_kv_d128", dim3(blocks(rows, 32)), dim3(256), a)))
+          return rc;
+      } else if ((rc = launch(rt, "rxw8_dec_qk_rope_kv", dim3(blocks(rows, 4)), dim3(256), a))) {
+        return rc;
+      }
       if (use_prefill) {
         // causal blocks of 64 prompt rows per (sequence, kv head); lens still
         // holds each sequence's length before this forward = its first position

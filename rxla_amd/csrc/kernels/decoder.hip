@@ -192,6 +192,78 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_qk_rope_kv(QkRopeArgs
   }
 }
 
+// The same for D = 128 with 8 lanes per (token, head) row: lane j handles
+// dims 8j .. 8j+7 and their RoPE partners 64 + 8j .. (16-byte loads and
+// stores); the row's sum of squares is reduced over its 8 lanes.
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_qk_rope_kv_d128(QkRopeArgs a) {
+  constexpr int D = 128, HALF = 64;
+  const int heads = a.Hq + 2 * a.Hkv;
+  const int64_t unit = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
+  const int j = threadIdx.x & 7;
+  const bool live = unit < (int64_t)a.T * heads;  // lanes past the end still join the shuffles
+  const int64_t u = live ? unit : 0;
+  const int t = (int)(u / heads), h = (int)(u - (int64_t)t * heads);
+  const uint16_t *src = a.qkv + ((int64_t)t * heads + h) * D;
+  const int seq = a.row_seq[t];
+  const int p = a.pos[t];
+  const int i0 = 8 * j;
+  const u32x4 lo = *(const u32x4 *)(src + i0), hi = *(const u32x4 *)(src + HALF + i0);
+  if (h >= a.Hq + a.Hkv) {  // value head (uniform over the 8 lanes)
+    if (live) {
+      uint16_t *dst = a.vc + (((int64_t)seq * a.Hkv + (h - a.Hq - a.Hkv)) * a.Lmax + p) * D;
+      *(u32x4 *)(dst + i0) = lo;
+      *(u32x4 *)(dst + HALF + i0) = hi;
+    }
+    return;
+  }
+  float x0[8], x1[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x0[2 * e] = bf16_bits_to_f32(lo[e] & 0xffffu);
+    x0[2 * e + 1] = bf16_bits_to_f32(lo[e] >> 16);
+    x1[2 * e] = bf16_bits_to_f32(hi[e] & 0xffffu);
+    x1[2 * e + 1] = bf16_bits_to_f32(hi[e] >> 16);
+  }
+  const bool is_q = h < a.Hq;
+  const float *nw = is_q ? a.q_norm : a.k_norm;
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x0[e] * x0[e] + x1[e] * x1[e];
+  ss += __shfl_xor(ss, 1);
+  ss += __shfl_xor(ss, 2);
+  ss += __shfl_xor(ss, 4);
+  if (nw) {
+    const float sc = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x0[e] = (x0[e] * sc) * nw[i0 + e];
+      x1[e] = (x1[e] * sc) * nw[HALF + i0 + e];
+    }
+  }
+  const float *rope = a.rope + (int64_t)p * D;
+  float r0[8], r1[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float cs = rope[i0 + e], sn = rope[HALF + i0 + e];
+    r0[e] = x0[e] * cs - x1[e] * sn;
+    r1[e] = x1[e] * cs + x0[e] * sn;
+  }
+  if (!live) return;
+  if (is_q) {
+    float *dst = a.q_out + ((int64_t)t * a.Hq + h) * D;
+    *(f32x4 *)(dst + i0) = f32x4{r0[0], r0[1], r0[2], r0[3]};
+    *(f32x4 *)(dst + i0 + 4) = f32x4{r0[4], r0[5], r0[6], r0[7]};
+    *(f32x4 *)(dst + HALF + i0) = f32x4{r1[0], r1[1], r1[2], r1[3]};
+    *(f32x4 *)(dst + HALF + i0 + 4) = f32x4{r1[4], r1[5], r1[6], r1[7]};
+  } else {
+    uint16_t *dst = a.kc + (((int64_t)seq * a.Hkv + (h - a.Hq)) * a.Lmax + p) * D;
+    *(u32x4 *)(dst + i0) = u32x4{pack_bf16x2(r0[0], r0[1]), pack_bf16x2(r0[2], r0[3]),
+                                 pack_bf16x2(r0[4], r0[5]), pack_bf16x2(r0[6], r0[7])};
+    *(u32x4 *)(dst + HALF + i0) = u32x4{pack_bf16x2(r1[0], r1[1]), pack_bf16x2(r1[2], r1[3]),
+                                        pack_bf16x2(r1[4], r1[5]), pack_bf16x2(r1[6], r1[7])};
+  }
+}
+
 // ---- SwiGLU middle (ops.rs:331-342): act = bf16(silu(g) * u), gu = [g | u] ----
 struct SiluMulArgs {
   const uint16_t *gu;  // [T, 2I]: gate columns then up columns, or interleaved

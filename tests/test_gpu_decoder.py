@@ -148,7 +148,36 @@ def test_decode_fused_rope_matches_separate_kernel(rt, monkeypatch, qk_norm):
         np.testing.assert_array_equal(model.lens()[:batch], [703] * batch)
     err = rel_err(logits["0"], logits["1"])
     print(f"qk_norm={qk_norm} fused vs separate RoPE rel_err={err:.3e}")
-    assert err <= 1e-4
+    # the two paths sum a head's squares (q/k RMSNorm) in different orders, so
+    # a cached bf16 key element can differ by one ulp; the logits stay close
+    assert err <= 2e-3
+
+
+@pytest.mark.parametrize("qk_norm", [True, False])
+def test_rope_kv_kernels_agree(rt, monkeypatch, qk_norm):
+    """The 8-lanes-per-row RoPE/KV kernel (D = 128) and the one-wave-per-row
+    kernel, each against the oracle decoder on a 300-row prompt and 2 decode
+    steps (the two sum a head's squares in different orders, so they are
+    compared with the oracle, not bit for bit with each other)."""
+    cfg = small_cfg(max_seq=320, qk_norm=qk_norm)
+    params = tiny_params(cfg, seed=93, std=0.05)
+    batch = 2
+    prompt = np.random.default_rng(94).integers(0, cfg["vocab"], (batch, 300)).astype(np.int32)
+    chunks = (prompt, prompt[:, :1], prompt[:, 1:2])
+    dec = oracle.Decoder(cfg, params, batch)
+    want = np.stack([dec.forward(np.ascontiguousarray(ids))[0] for ids in chunks])
+    for mode in ("0", "1"):
+        monkeypatch.setenv("RXW8_DEC_GENERIC_ROPE", mode)
+        monkeypatch.setenv("RXW8_DEC_UNFUSED_ROPE", "1")
+        model = build(rt, cfg, params, batch)
+        got = []
+        for ids in chunks:
+            out = rt.zeros((batch, cfg["vocab"]), rx().DType.F32)
+            model.forward(rt.buffer(np.ascontiguousarray(ids)), logits=out)
+            got.append(out.to_numpy())
+        err = rel_err(np.stack(got), want)
+        print(f"qk_norm={qk_norm} rope {'generic' if mode == '1' else 'd128'} vs oracle rel_err={err:.3e}")
+        assert err <= 1e-2
 
 
 def test_decoder_prefill_kernel_matches_rowwise(rt, monkeypatch):
