@@ -209,6 +209,36 @@ int rxw8_kv_update_at(rxw8_runtime *rt, rxw8_buffer *k_cache,
                       rxw8_buffer *v_update, rxw8_buffer *starts, int checked,
                       rxw8_buffer *accepted);
 
+/* ---- safetensors checkpoints (crates/rxla-safetensors/src/model.rs:340-440;
+ *      the W8 layout written by benchmarks/quantize_qwen3_5_w8.py:27-55) ----
+ * The file is memory-mapped and every header entry is validated at open
+ * (known dtype, offsets inside the data section matching numel, no overlap);
+ * payloads are read only by rxw8_safetensors_upload. Tensors of dtypes with no
+ * rxw8 counterpart (I64, F64, ...) are listed with dtype 0 and cannot be
+ * uploaded. The handle is immutable after open; it must outlive no runtime. */
+typedef struct rxw8_safetensors rxw8_safetensors;
+
+int rxw8_safetensors_open(const char *path, rxw8_safetensors **out);
+int rxw8_safetensors_close(rxw8_safetensors *st);
+int rxw8_safetensors_num_tensors(rxw8_safetensors *st, int64_t *count);
+/* name stays valid until close; dims receives up to RXW8_MAX_RANK values */
+int rxw8_safetensors_tensor_info(rxw8_safetensors *st, int64_t index,
+                                 const char **name, int *dtype, int64_t *dims,
+                                 int *rank);
+/* NOT_FOUND when absent */
+int rxw8_safetensors_find(rxw8_safetensors *st, const char *name,
+                          int64_t *index);
+/* "__metadata__" string value (e.g. "format", "group_size"); NOT_FOUND when absent */
+int rxw8_safetensors_metadata(rxw8_safetensors *st, const char *key,
+                              const char **value);
+/* Copy tensor `index` into dst at element offset `offset` (elements of dst's
+ * dtype), converting as the reference loader does: U8 -> U8 and I32 -> I32
+ * verbatim; F32 / F16 / BF16 -> F32 / F16 / BF16 exactly when widening or
+ * equal, round-to-nearest-even when narrowing. Several tensors may fill one
+ * buffer (fused projections: q, k, v rows one after another). */
+int rxw8_safetensors_upload(rxw8_safetensors *st, int64_t index,
+                            rxw8_buffer *dst, int64_t offset);
+
 /* ---- decoder plan (AppliedModel::compile -> CompiledModel::bind_parameters
  *      -> run, applied.rs:135-239,808-815; model composition
  *      crates/rxla-models/src/qwen3_5/mod.rs:199-273) ------------------------ */

@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import ctypes
 import enum
+import os
 from ctypes import POINTER, byref, c_int, c_int32, c_int64, c_void_p
 
 import numpy as np
@@ -346,10 +347,80 @@ class KvCache:
         return acc
 
 
+class SafeTensors:
+    """A memory-mapped safetensors checkpoint (crates/rxla-safetensors/src/
+    model.rs:340-440): headers are validated at open, payloads are read only by
+    ``upload`` / ``to_buffer``, which convert like the reference loader (U8 and
+    I32 verbatim; F32 / F16 / BF16 among themselves, narrowing with
+    round-to-nearest-even)."""
+
+    def __init__(self, path):
+        h = c_void_p()
+        _check(_lib.rxw8_safetensors_open(os.fsencode(os.fspath(path)), byref(h)))
+        self._h = h
+        self.path = os.fspath(path)
+        n = c_int64()
+        _check(_lib.rxw8_safetensors_num_tensors(h, byref(n)))
+        self._info = {}
+        for i in range(n.value):
+            name = ctypes.c_char_p()
+            dt = c_int()
+            dims = (c_int64 * 8)()
+            rank = c_int()
+            _check(_lib.rxw8_safetensors_tensor_info(h, i, byref(name), byref(dt), dims, byref(rank)))
+            self._info[name.value.decode()] = (i, DType(dt.value) if dt.value else None,
+                                               tuple(dims[j] for j in range(rank.value)))
+
+    def close(self):
+        if self._h:
+            _check(_lib.rxw8_safetensors_close(self._h))
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self):
+        """{name: (dtype or None when not representable, shape)}"""
+        return {k: (v[1], v[2]) for k, v in self._info.items()}
+
+    def metadata(self, key: str, default=None):
+        v = ctypes.c_char_p()
+        rc = _lib.rxw8_safetensors_metadata(self._h, key.encode(), byref(v))
+        if rc == Status.NOT_FOUND:
+            return default
+        _check(rc)
+        return v.value.decode()
+
+    def upload(self, name: str, dst: Buffer, offset: int = 0):
+        if name not in self._info:
+            raise Error(Status.NOT_FOUND, f"missing tensor {name!r}")
+        _check(_lib.rxw8_safetensors_upload(self._h, self._info[name][0], dst.handle, int(offset)))
+
+    def to_buffer(self, rt: Runtime, name: str, dtype: DType | None = None) -> Buffer:
+        if name not in self._info:
+            raise Error(Status.NOT_FOUND, f"missing tensor {name!r}")
+        _, sdt, shape = self._info[name]
+        dt = dtype if dtype is not None else sdt
+        if dt is None:
+            raise Error(Status.UNIMPLEMENTED, f"tensor {name!r} has no rxw8 dtype")
+        buf = rt.zeros(shape, dt)
+        self.upload(name, buf)
+        return buf
+
+
 from .model import DecoderConfig, DecoderModel  # noqa: E402  (needs the classes above)
 
 __all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "dequantize", "pack_weight",
            "quantized_linear",
            "linear_bf16", "QuantizedLinear", "grouped_query_attention",
-           "grouped_query_attention_prefill", "KvCache",
+           "grouped_query_attention_prefill", "KvCache", "SafeTensors",
            "DecoderConfig", "DecoderModel", "bf16_to_f32"]

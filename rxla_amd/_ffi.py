@@ -24,6 +24,9 @@ EXPORTS = [
     "rxw8_dequantize", "rxw8_pack_weight", "rxw8_quantized_linear", "rxw8_quantized_linear_into",
     "rxw8_linear_bf16", "rxw8_linear_bf16_into", "rxw8_gqa_decode", "rxw8_gqa_decode_into",
     "rxw8_gqa_prefill", "rxw8_gqa_prefill_into", "rxw8_kv_update_at",
+    "rxw8_safetensors_open", "rxw8_safetensors_close", "rxw8_safetensors_num_tensors",
+    "rxw8_safetensors_tensor_info", "rxw8_safetensors_find", "rxw8_safetensors_metadata",
+    "rxw8_safetensors_upload",
     "rxw8_decoder_create", "rxw8_decoder_destroy", "rxw8_decoder_num_parameters",
     "rxw8_decoder_parameter_info", "rxw8_decoder_bind_parameter", "rxw8_decoder_reset",
     "rxw8_decoder_forward", "rxw8_decoder_generate", "rxw8_decoder_lens",
@@ -71,6 +74,14 @@ def _declare(L):
         "rxw8_gqa_prefill": (c_int, [vp, vp, vp, vp, vp, c_float, c_int, POINTER(vp)]),
         "rxw8_gqa_prefill_into": (c_int, [vp, vp, vp, vp, vp, c_float, vp]),
         "rxw8_kv_update_at": (c_int, [vp, vp, vp, vp, vp, vp, c_int, vp]),
+        "rxw8_safetensors_open": (c_int, [c_char_p, POINTER(vp)]),
+        "rxw8_safetensors_close": (c_int, [vp]),
+        "rxw8_safetensors_num_tensors": (c_int, [vp, i64p]),
+        "rxw8_safetensors_tensor_info": (c_int, [vp, c_int64, POINTER(c_char_p), POINTER(c_int),
+                                                 i64p, POINTER(c_int)]),
+        "rxw8_safetensors_find": (c_int, [vp, c_char_p, i64p]),
+        "rxw8_safetensors_metadata": (c_int, [vp, c_char_p, POINTER(c_char_p)]),
+        "rxw8_safetensors_upload": (c_int, [vp, c_int64, vp, c_int64]),
         "rxw8_decoder_create": (c_int, [vp, POINTER(DecoderConfig), POINTER(vp)]),
         "rxw8_decoder_destroy": (c_int, [vp]),
         "rxw8_decoder_num_parameters": (c_int, [vp, POINTER(c_int)]),

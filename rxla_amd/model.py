@@ -16,7 +16,9 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from . import Buffer, DType, Error, Runtime, Status, _check, _ffi, _lib
+import re
+
+from . import Buffer, DType, Error, Runtime, SafeTensors, Status, _check, _ffi, _lib, dequantize
 
 
 @dataclass
@@ -97,6 +99,112 @@ class DecoderModel:
     def bind_parameters(self, params: dict) -> "DecoderModel":
         for path, buf in params.items():
             self.bind_parameter(path, buf)
+        return self
+
+    # ---- checkpoints ------------------------------------------------------------
+    CHECKPOINT_PREFIXES = ("", "model.", "model.language_model.")
+    _FUSED = ((re.compile(r"^(layers\.\d+\.self_attn\.)qkv_proj\.(weight|scale)$"),
+               ("q_proj", "k_proj", "v_proj")),
+              (re.compile(r"^(layers\.\d+\.mlp\.)gate_up_proj\.(weight|scale)$"),
+               ("gate_proj", "up_proj")))
+
+    def checkpoint_plan(self, st: SafeTensors, mapping: dict | None = None) -> dict:
+        """Schema path -> (checkpoint keys stacked along dim 0, dequantise), all
+        validated before any payload is read (rxla-safetensors model.rs:384-440:
+        exact path match or an explicit mapping, dtype compatibility, shapes).
+
+        Keys are found under the prefixes "", "model." and
+        "model.language_model." (the names quantize_qwen3_5_w8.py keeps). The
+        fused projections take q_proj / k_proj / v_proj and gate_proj / up_proj
+        rows in that order (projections.rs:21-69). A float schema parameter
+        stored as U8 codes with a sibling ".scale" (the encoder quantizes every
+        2-D tensor, e.g. embed_tokens) is dequantised exactly on the device:
+        bf16((u - 128) * s) (layers.rs:277-294)."""
+        info = st.tensors()
+
+        def find(key):
+            for p in self.CHECKPOINT_PREFIXES:
+                if p + key in info:
+                    return p + key
+            return None
+
+        floats = (DType.F32, DType.F16, DType.BF16)
+        plan, errors = {}, []
+        for path, dtype, shape in self.schema():
+            if mapping and path in mapping:
+                keys = [mapping[path]] if isinstance(mapping[path], str) else list(mapping[path])
+                missing = [k for k in keys if k not in info]
+            else:
+                k = find(path)
+                keys, missing = ([k], []) if k else ([], [path])
+                if not k:
+                    for pat, parts in self._FUSED:
+                        m = pat.match(path)
+                        if m:
+                            found = [find(f"{m.group(1)}{part}.{m.group(2)}") for part in parts]
+                            if all(found):
+                                keys, missing = found, []
+                            else:
+                                missing = [f"{m.group(1)}{part}.{m.group(2)}"
+                                           for part, f in zip(parts, found) if not f]
+            if missing:
+                errors.append(f"{path}: missing checkpoint tensor(s) {missing}")
+                continue
+            deq = False
+            rows = 0
+            for k in keys:
+                sdt, sshape = info[k]
+                if dtype in floats and sdt == DType.U8:
+                    scale = k[:-len(".weight")] + ".scale" if k.endswith(".weight") else None
+                    if len(keys) != 1 or scale not in info or len(sshape) != 2:
+                        errors.append(f"{path}: {k} is U8 without a usable .scale for {dtype.name} storage")
+                        break
+                    deq = True
+                elif not (sdt == dtype or (dtype in floats and sdt in floats)):
+                    errors.append(f"{path}: incompatible checkpoint dtype {sdt} of {k} for "
+                                  f"{dtype.name} storage")
+                    break
+                if len(sshape) != len(shape) or tuple(sshape[1:]) != tuple(shape[1:]):
+                    errors.append(f"{path}: {k} has shape {sshape}, schema {shape}")
+                    break
+                rows += sshape[0] if sshape else 1
+            else:
+                if (shape and rows != shape[0]) or (not shape and rows != 1):
+                    errors.append(f"{path}: checkpoint rows {rows} != schema {shape}")
+                    continue
+                plan[path] = (keys, deq)
+        if errors:
+            raise Error(Status.INVALID_ARGUMENT, "checkpoint does not match the decoder schema: "
+                        + "; ".join(errors[:8]) + (" ..." if len(errors) > 8 else ""))
+        return plan
+
+    def load_safetensors(self, checkpoint, mapping: dict | None = None) -> "DecoderModel":
+        """Validate every parameter against the checkpoint, then upload and bind
+        (CompiledModel::bind_parameters over load_parameter_schema_with_mapping)."""
+        st = checkpoint if isinstance(checkpoint, SafeTensors) else SafeTensors(checkpoint)
+        try:
+            g = st.metadata("group_size")
+            if g is not None and self.cfg.group not in (0, int(g)):
+                raise Error(Status.INVALID_ARGUMENT,
+                            f"checkpoint group_size {g} != decoder group {self.cfg.group}")
+            plan = self.checkpoint_plan(st, mapping)
+            info = st.tensors()
+            for path, dtype, shape in self.schema():
+                keys, deq = plan[path]
+                if deq:
+                    w = st.to_buffer(self.rt, keys[0])
+                    s_ = st.to_buffer(self.rt, keys[0][:-len(".weight")] + ".scale", DType.F32)
+                    buf = dequantize(self.rt, w, s_, dtype)
+                else:
+                    buf = self.rt.zeros(shape, dtype)
+                    off = 0
+                    for k in keys:
+                        st.upload(k, buf, off)
+                        off += int(np.prod(info[k][1], dtype=np.int64))
+                self.bind_parameter(path, buf)
+        finally:
+            if st is not checkpoint:
+                st.close()
         return self
 
     def reset(self):
