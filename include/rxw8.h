@@ -287,6 +287,53 @@ int rxw8_decoder_generate(rxw8_decoder *dec, rxw8_buffer *prompt, int64_t b,
 /* Copy of the current sequence lengths to host (int32 [max_batch]). */
 int rxw8_decoder_lens(rxw8_decoder *dec, int32_t *lens, int64_t n);
 
+/* ---- Qwen3.5 hybrid W8 text model ------------------------------------------
+ * Replaces qwen3_5(cx, token_ids, config) (crates/rxla-models/src/qwen3_5/
+ * mod.rs:197-273) compiled and bound through the applied-model flow
+ * (crates/rxla-nn/src/applied.rs:156-239): full-sequence inference, token ids
+ * [batch, sequence] -> logits [batch, sequence, vocabulary], every sequence
+ * starting at position 0. Gated-delta linear-attention layers
+ * (qwen3_5/layers.rs:113-268) and output-gated full-attention layers
+ * (:28-100), the SwiGLU MLP (:270-293), the W8 embedding and tied W8 LM head
+ * (mod.rs:134-195, optional F32 LoRA on the head). The fields follow
+ * Qwen3_5Config (mod.rs:16-33); layer i is full attention iff
+ * layer_kinds[i] != 0 (or, with layer_kinds NULL, iff (i + 1) %
+ * full_attention_interval == 0, the 0.8B topology with interval 4). */
+typedef struct rxw8_qwen35_config {
+  int64_t vocab, hidden, intermediate, layers;
+  int64_t heads, kv_heads, head_dim;      /* full attention */
+  int64_t linear_heads, linear_head_dim;  /* gated delta */
+  int64_t conv_kernel, max_positions, rotary_dim, group;
+  int64_t full_attention_interval;
+  const int32_t *layer_kinds; /* [layers] 0 = linear, 1 = full (copied at create), or NULL */
+  float theta, eps;
+  int64_t lora_rank; /* 0 = no LoRA on the tied head */
+  float lora_alpha;
+  int64_t max_batch, max_seq; /* activation capacity of one forward */
+} rxw8_qwen35_config;
+
+typedef struct rxw8_qwen35 rxw8_qwen35;
+
+/* Validate the config (Qwen3_5Config::validate, mod.rs:100-131, plus the
+ * widths the kernels support) and allocate activations. */
+int rxw8_qwen35_create(rxw8_runtime *rt, const rxw8_qwen35_config *cfg,
+                       rxw8_qwen35 **out);
+int rxw8_qwen35_destroy(rxw8_qwen35 *m);
+/* Parameter schema under the reference's paths ("model.language_model.
+ * layers.{i}.linear_attn.in_proj_qkv.weight", ...): U8 codes + F32 scales
+ * for every projection, F32 norms / conv / A_log / dt_bias. */
+int rxw8_qwen35_num_parameters(rxw8_qwen35 *m, int *count);
+int rxw8_qwen35_parameter_info(rxw8_qwen35 *m, int index, const char **path,
+                               int *dtype, int64_t *dims, int *rank);
+/* Same contract as rxw8_decoder_bind_parameter (applied.rs:948-990,1274). */
+int rxw8_qwen35_bind_parameter(rxw8_qwen35 *m, const char *path,
+                               rxw8_buffer *buffer);
+/* ids: device I32 [b, s]; logits: device F32 [b, s, vocab]. INVALID_ARGUMENT
+ * for a sequence outside [1, max_positions] (InvalidQwenTokens, mod.rs:
+ * 201-209) or a shape mismatch, OUT_OF_RANGE beyond the activation capacity,
+ * FAILED_PRECONDITION while a parameter is unbound. */
+int rxw8_qwen35_forward(rxw8_qwen35 *m, rxw8_buffer *ids, rxw8_buffer *logits);
+
 #ifdef __cplusplus
 }
 #endif

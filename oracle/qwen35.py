@@ -11,7 +11,8 @@ crates/rxla-models/src/qwen3_5/mod.rs:234-273 (model) and layers.rs (mixers):
   * gated-delta linear attention (causal depthwise conv + SiLU,
     L2-normalised q/k, delta-rule recurrence, gated RMSNorm)      layers.rs:113-268
   * SwiGLU MLP                                                    layers.rs:270-293
-  * tied W8 LM head: f32 logits against the dequantised table     mod.rs:181-195
+  * tied W8 LM head: f32 logits against the dequantised table,
+    plus the optional F32 LoRA update (lora_rank, lora_alpha)     mod.rs:158-195
 It returns logits for every position ([B, S, V]), as the reference does.
 """
 from __future__ import annotations
@@ -201,7 +202,14 @@ def forward(cfg, p, ids):
         n = rms_norm(h, p[pre + "post_attention_layernorm.weight"], cfg["eps"], True).astype(np.float32)
         h = h + mlp(n, p, pre + "mlp.")
     n = rms_norm(h, p[root + "norm.weight"], cfg["eps"], True)
-    return n @ table.astype(np.float64).T
+    logits = n @ table.astype(np.float64).T
+    rank = cfg.get("lora_rank", 0)
+    if rank:
+        # tied-head LoRA (mod.rs:174-195): base + (n A^T) B^T * (alpha / rank)
+        a = np.asarray(p[root + "embed_tokens.lora_A.weight"], np.float64)
+        b_ = np.asarray(p[root + "embed_tokens.lora_B.weight"], np.float64)
+        logits = logits + ((n @ a.T) @ b_.T) * (np.float32(cfg["lora_alpha"]) / np.float32(rank))
+    return logits
 
 
 def random_params(cfg, seed=0, std=0.05):
@@ -253,6 +261,10 @@ def random_params(cfg, seed=0, std=0.05):
         q8(pre + "mlp.up_proj", I, H)
         q8(pre + "mlp.down_proj", H, I)
     p[root + "norm.weight"] = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    rank = cfg.get("lora_rank", 0)
+    if rank:
+        p[root + "embed_tokens.lora_A.weight"] = (0.1 * rng.standard_normal((rank, H))).astype(np.float32)
+        p[root + "embed_tokens.lora_B.weight"] = (0.1 * rng.standard_normal((cfg["vocab"], rank))).astype(np.float32)
     return p
 
 

@@ -417,10 +417,10 @@ class SafeTensors:
         return buf
 
 
-from .model import DecoderConfig, DecoderModel  # noqa: E402  (needs the classes above)
+from .model import DecoderConfig, DecoderModel, Qwen35Config, Qwen35Model  # noqa: E402
 
 __all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "dequantize", "pack_weight",
            "quantized_linear",
            "linear_bf16", "QuantizedLinear", "grouped_query_attention",
            "grouped_query_attention_prefill", "KvCache", "SafeTensors",
-           "DecoderConfig", "DecoderModel", "bf16_to_f32"]
+           "DecoderConfig", "DecoderModel", "Qwen35Config", "Qwen35Model", "bf16_to_f32"]

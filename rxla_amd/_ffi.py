@@ -30,6 +30,8 @@ EXPORTS = [
     "rxw8_decoder_create", "rxw8_decoder_destroy", "rxw8_decoder_num_parameters",
     "rxw8_decoder_parameter_info", "rxw8_decoder_bind_parameter", "rxw8_decoder_reset",
     "rxw8_decoder_forward", "rxw8_decoder_generate", "rxw8_decoder_lens",
+    "rxw8_qwen35_create", "rxw8_qwen35_destroy", "rxw8_qwen35_num_parameters",
+    "rxw8_qwen35_parameter_info", "rxw8_qwen35_bind_parameter", "rxw8_qwen35_forward",
 ]
 
 
@@ -39,6 +41,17 @@ class DecoderConfig(Structure):
                 ("vocab", c_int64), ("max_batch", c_int64), ("max_seq", c_int64),
                 ("group", c_int64), ("eps", c_float), ("theta", c_float),
                 ("qk_norm", c_int32)]
+
+
+class Qwen35Config(Structure):
+    _fields_ = [("vocab", c_int64), ("hidden", c_int64), ("intermediate", c_int64),
+                ("layers", c_int64), ("heads", c_int64), ("kv_heads", c_int64),
+                ("head_dim", c_int64), ("linear_heads", c_int64), ("linear_head_dim", c_int64),
+                ("conv_kernel", c_int64), ("max_positions", c_int64), ("rotary_dim", c_int64),
+                ("group", c_int64), ("full_attention_interval", c_int64),
+                ("layer_kinds", POINTER(c_int32)), ("theta", c_float), ("eps", c_float),
+                ("lora_rank", c_int64), ("lora_alpha", c_float), ("max_batch", c_int64),
+                ("max_seq", c_int64)]
 
 
 def _declare(L):
@@ -92,6 +105,13 @@ def _declare(L):
         "rxw8_decoder_forward": (c_int, [vp, vp, c_int64, c_int64, vp, vp]),
         "rxw8_decoder_generate": (c_int, [vp, vp, c_int64, c_int64, c_int64, vp, c_int]),
         "rxw8_decoder_lens": (c_int, [vp, POINTER(c_int32), c_int64]),
+        "rxw8_qwen35_create": (c_int, [vp, POINTER(Qwen35Config), POINTER(vp)]),
+        "rxw8_qwen35_destroy": (c_int, [vp]),
+        "rxw8_qwen35_num_parameters": (c_int, [vp, POINTER(c_int)]),
+        "rxw8_qwen35_parameter_info": (c_int, [vp, c_int, POINTER(c_char_p), POINTER(c_int),
+                                               i64p, POINTER(c_int)]),
+        "rxw8_qwen35_bind_parameter": (c_int, [vp, c_char_p, vp]),
+        "rxw8_qwen35_forward": (c_int, [vp, vp, vp]),
     }
     for name, (res, args) in sigs.items():
         f = getattr(L, name)

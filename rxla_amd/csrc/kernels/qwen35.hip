@@ -1,0 +1,340 @@
+// Kernels of the hybrid Qwen3.5 W8 text model
+// (crates/rxla-models/src/qwen3_5/mod.rs:158-273, layers.rs:4-293): the W8
+// embedding, zero-centred / gated RMSNorm, the full-attention prologue (gate,
+// q/k norm, partial RoPE), the gated-delta pieces (causal depthwise conv +
+// SiLU, L2 norms, beta / decay, the delta-rule recurrence) and SwiGLU. The
+// projections run on the shared W8A16 GEMM/GEMV paths; the full-sequence
+// attention on the shared GQA kernels. Token t = b * S + i sits at position i
+// of sequence b (the reference runs whole sequences from position 0).
+#include "common.h"
+
+namespace {
+__device__ __forceinline__ float sigmoid_f32(float x) {  // rxla-core ops.rs:330-338
+  const float e = __expf(-fabsf(x));
+  return x >= 0.f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+}
+__device__ __forceinline__ float ld(const void *p, int64_t i, int f32) {
+  return f32 ? ((const float *)p)[i] : bf16_bits_to_f32(((const uint16_t *)p)[i]);
+}
+}  // namespace
+
+// ---- W8 embedding: h[t, c] = (f32(u8[id, c]) - 128) * scale[id, c / G], ids
+// clamped to [0, V - 1] (mod.rs:158-179, indexing.rs:637-656) -------------------
+struct Q35EmbedArgs {
+  const int32_t *ids;
+  const uint8_t *w;     // [V, H]
+  const float *scale;   // [V, H / G]
+  float *h;             // [T, H]
+  int64_t T, V, H, G;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_embed(Q35EmbedArgs a) {
+  const int64_t n = a.T * a.H;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = e / a.H, c = e - t * a.H;
+    int64_t id = a.ids[t];
+    id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
+    a.h[e] = ((float)a.w[id * a.H + c] + -128.0f) * a.scale[id * (a.H / a.G) + c / a.G];
+  }
+}
+
+// ---- RMSNorm over rows of L values (rxla-nn layers.rs:459-495):
+//   y = x * rsqrt(mean(x^2) + eps) * (zero_centered ? 1 + w : w)
+// optionally times silu(z) (the gated output norm, layers.rs:241-259).
+// Row r reads x + r * x_stride, writes out + r * out_stride (bf16 or f32).
+struct Q35NormArgs {
+  const float *x;
+  const float *w;        // [L]
+  const void *z;         // [rows, L] gate (bf16 or f32) or null
+  void *out;
+  int64_t rows, L, x_stride, out_stride, z_stride;
+  float eps;
+  int zero_centered, out_f32, z_f32;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a) {
+  __shared__ float red[8];
+  const int64_t r = blockIdx.x;
+  if (r >= a.rows) return;
+  const float *x = a.x + r * a.x_stride;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < a.L; i += blockDim.x) ss += x[i] * x[i];
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += red[i];
+  const float sc = 1.0f / sqrtf(tot / (float)a.L + a.eps);
+  for (int64_t i = threadIdx.x; i < a.L; i += blockDim.x) {
+    const float w = a.zero_centered ? 1.0f + a.w[i] : a.w[i];
+    float y = (x[i] * sc) * w;
+    if (a.z) {
+      const float zv = ld(a.z, r * a.z_stride + i, a.z_f32);
+      y *= zv * sigmoid_f32(zv);
+    }
+    if (a.out_f32)
+      ((float *)a.out)[r * a.out_stride + i] = y;
+    else
+      ((uint16_t *)a.out)[r * a.out_stride + i] = f32_to_bf16_bits(y);
+  }
+}
+
+// ---- full attention prologue (layers.rs:28-99): one wave per (token, head).
+// Query heads h < Hq: qg[t, h] = [query (D) | gate (D)] (bf16 projection);
+// gate_out[t, h*D + d] = sigmoid(gate); q_out[t, h, :] = RoPE(norm(query)).
+// KV heads: k = RoPE(norm(k)), v copied; both into f32 [B, Hkv, Lmax, D] at
+// the token's position. norm: zero-centred RMSNorm over D; RoPE: split-half
+// over the first rot channels with angle pos * freqs[i] (mod.rs:209-229).
+struct Q35FaPrepArgs {
+  const uint16_t *qg;    // [T, Hq * 2D]
+  const uint16_t *kp;    // [T, Hkv * D]
+  const uint16_t *vp;    // [T, Hkv * D]
+  const float *q_norm, *k_norm;  // [D]
+  const float *freqs;    // [rot / 2]
+  float *q_out;          // [T, Hq, D]
+  float *gate_out;       // [T, Hq * D]
+  float *kc, *vc;        // [B, Hkv, Lmax, D]
+  int T, S, Hq, Hkv, D, rot, Lmax;
+  float eps;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs a) {
+  __shared__ float rowbuf[4][256 + 8];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int heads = a.Hq + a.Hkv;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + wv;
+  if (unit >= (int64_t)a.T * heads) return;  // wave-uniform
+  const int t = (int)(unit / heads), h = (int)(unit - (int64_t)t * heads);
+  const int bseq = t / a.S, pos = t - bseq * a.S;
+  const int D = a.D;
+  const bool is_q = h < a.Hq;
+  const uint16_t *src = is_q ? a.qg + ((int64_t)t * a.Hq + h) * 2 * D
+                             : a.kp + ((int64_t)t * a.Hkv + (h - a.Hq)) * D;
+  float *row = rowbuf[wv];
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) {
+    const float v = bf16_bits_to_f32(src[i]);
+    row[i] = v;
+    ss += v * v;
+  }
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const float sc = 1.0f / sqrtf(ss / (float)D + a.eps);
+  const float *nw = is_q ? a.q_norm : a.k_norm;
+  for (int i = lane; i < D; i += 64) row[i] = (row[i] * sc) * (1.0f + nw[i]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int half = a.rot / 2;
+  float *dst = is_q ? a.q_out + ((int64_t)t * a.Hq + h) * D
+                    : a.kc + (((int64_t)bseq * a.Hkv + (h - a.Hq)) * a.Lmax + pos) * D;
+  for (int i = lane; i < D; i += 64) {
+    float y = row[i];
+    if (i < a.rot) {
+      const int fi = i < half ? i : i - half;
+      float sn, cs;
+      sincosf((float)pos * a.freqs[fi], &sn, &cs);
+      y = i < half ? row[i] * cs - row[i + half] * sn : row[i] * cs + row[i - half] * sn;
+    }
+    dst[i] = y;
+  }
+  if (is_q) {
+    for (int i = lane; i < D; i += 64)
+      a.gate_out[(int64_t)t * a.Hq * D + (int64_t)h * D + i] = sigmoid_f32(bf16_bits_to_f32(src[D + i]));
+  } else {
+    const uint16_t *vs = a.vp + ((int64_t)t * a.Hkv + (h - a.Hq)) * D;
+    float *vd = a.vc + (((int64_t)bseq * a.Hkv + (h - a.Hq)) * a.Lmax + pos) * D;
+    for (int i = lane; i < D; i += 64) vd[i] = bf16_bits_to_f32(vs[i]);
+  }
+}
+
+// ---- elementwise product (attended * gate, layers.rs:93-94), in place ------
+struct Q35MulArgs {
+  float *x;
+  const float *y;
+  int64_t n;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_mul(Q35MulArgs a) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < a.n;
+       e += (int64_t)gridDim.x * blockDim.x)
+    a.x[e] *= a.y[e];
+}
+
+// ---- causal depthwise conv over each sequence + SiLU (layers.rs:131-146):
+// out[t, c] = silu(sum_j w[c, j] * x[t - (k-1) + j, c]), zero before position 0.
+struct Q35ConvArgs {
+  const uint16_t *x;   // [T, C] bf16 projection
+  const float *w;      // [C, k]
+  float *out;          // [T, C]
+  int64_t T, C;
+  int S, k;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_conv_silu(Q35ConvArgs a) {
+  const int64_t n = a.T * a.C;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = e / a.C, c = e - t * a.C;
+    const int pos = (int)(t % a.S);
+    float acc = 0.f;
+    for (int j = 0; j < a.k; ++j) {
+      const int src = pos - (a.k - 1) + j;
+      if (src >= 0) acc += a.w[c * a.k + j] * bf16_bits_to_f32(a.x[(t - pos + src) * a.C + c]);
+    }
+    a.out[e] = acc * sigmoid_f32(acc);
+  }
+}
+
+// ---- q, k of the gated-delta mixer (layers.rs:147-161): per (token, head)
+// q = l2norm(q) / sqrt(Dl), k = l2norm(k), l2norm(x) = x * rsqrt(sum x^2 + 1e-6);
+// in place in the conv output [T, 3W] (q at 0, k at W). One wave per row.
+struct Q35L2Args {
+  float *mixed;
+  int64_t T;
+  int Hl, Dl;
+  float q_scale;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_qk_l2norm(Q35L2Args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (t, which, head)
+  if (unit >= a.T * 2 * a.Hl) return;
+  const int64_t t = unit / (2 * a.Hl);
+  const int r = (int)(unit - t * 2 * a.Hl), which = r / a.Hl, h = r - which * a.Hl;
+  float *x = a.mixed + t * 3 * (int64_t)a.Hl * a.Dl + (int64_t)which * a.Hl * a.Dl + (int64_t)h * a.Dl;
+  float ss = 0.f;
+  for (int i = lane; i < a.Dl; i += 64) ss += x[i] * x[i];
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const float sc = (1.0f / sqrtf(ss + 1e-6f)) * (which == 0 ? a.q_scale : 1.0f);
+  for (int i = lane; i < a.Dl; i += 64) x[i] *= sc;
+}
+
+// ---- beta = sigmoid(b); g = exp(softplus(a + dt_bias) * -exp(A_log))
+// (layers.rs:180-195; softplus = max(x, 0) + log1p(exp(-|x|)), ops.rs:256-262)
+struct Q35GateArgs {
+  const uint16_t *b, *a;  // [T, Hl] bf16 projections
+  const float *a_log, *dt_bias;  // [Hl]
+  float *beta, *g;        // [T, Hl]
+  int64_t n;
+  int Hl;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_beta_decay(Q35GateArgs p) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < p.n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int h = (int)(e % p.Hl);
+    p.beta[e] = sigmoid_f32(bf16_bits_to_f32(p.b[e]));
+    const float x = bf16_bits_to_f32(p.a[e]) + p.dt_bias[h];
+    const float sp = fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
+    p.g[e] = expf(sp * -expf(p.a_log[h]));
+  }
+}
+
+// ---- delta-rule recurrence (layers.rs:197-234): one workgroup of DL threads
+// per (sequence, head); thread j keeps column j of the state S (DL x DL, f32)
+// in registers and walks the positions in order:
+//   S *= g_t;  pred_j = sum_i S_ij k_i;  delta_j = (v_j - pred_j) beta_t;
+//   S_ij += k_i delta_j;  out_j = sum_i S_ij q_i.
+// q_t and k_t go through LDS (double-buffered); the next step's values are
+// loaded while the current one is computed.
+struct Q35DeltaArgs {
+  const float *mixed;  // [T, 3W]: q (scaled, normed), k (normed), v
+  const float *beta, *g;  // [T, Hl]
+  float *out;          // [T, Hl, Dl]
+  int B, S, Hl;
+};
+
+template <int DL>
+__device__ void delta_rule(const Q35DeltaArgs &a) {
+  __shared__ float qk[2][2][DL];
+  const int j = threadIdx.x;
+  const int bh = blockIdx.x, b = bh / a.Hl, h = bh - b * a.Hl;
+  const int64_t W = (int64_t)a.Hl * DL;
+  float st[DL];
+#pragma unroll
+  for (int i = 0; i < DL; ++i) st[i] = 0.f;
+  auto row = [&](int pos) { return (int64_t)b * a.S + pos; };
+  float qn = 0.f, kn = 0.f, vn = 0.f, bn = 0.f, gn = 0.f;
+  auto fetch = [&](int pos) {
+    const float *m = a.mixed + row(pos) * 3 * W + (int64_t)h * DL + j;
+    qn = m[0];
+    kn = m[W];
+    vn = m[2 * W];
+    bn = a.beta[row(pos) * a.Hl + h];
+    gn = a.g[row(pos) * a.Hl + h];
+  };
+  fetch(0);
+  for (int pos = 0; pos < a.S; ++pos) {
+    const int buf = pos & 1;
+    qk[buf][0][j] = qn;
+    qk[buf][1][j] = kn;
+    const float v = vn, beta = bn, gt = gn;
+    __syncthreads();  // q_t, k_t visible; the other buffer is free again
+    if (pos + 1 < a.S) fetch(pos + 1);
+    float pred = 0.f;
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+      st[i] *= gt;
+      pred += st[i] * qk[buf][1][i];
+    }
+    const float delta = (v - pred) * beta;
+    float o = 0.f;
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+      st[i] += qk[buf][1][i] * delta;
+      o += st[i] * qk[buf][0][i];
+    }
+    a.out[row(pos) * W + (int64_t)h * DL + j] = o;
+  }
+}
+
+// Launched with exactly DL threads (every thread takes part in the barriers).
+#define RXW8_Q35_DELTA(DL)                                                         \
+  extern "C" __global__ void __launch_bounds__(DL) rxw8_q35_delta_rule_d##DL(Q35DeltaArgs a) { \
+    delta_rule<DL>(a);                                                             \
+  }
+RXW8_Q35_DELTA(8)
+RXW8_Q35_DELTA(16)
+RXW8_Q35_DELTA(32)
+RXW8_Q35_DELTA(64)
+RXW8_Q35_DELTA(128)
+
+// ---- F32 LoRA on the tied head (mod.rs:174-195): down = x A^T, then
+// logits += (alpha / rank) * down B^T. One thread per output element.
+struct Q35LoraArgs {
+  const float *x;   // [T, K]
+  const float *w;   // [N, K]
+  float *y;         // [T, N]
+  int64_t T, N, K;
+  float alpha;
+  int accumulate;   // 0: y = x w^T; 1: y += alpha * (x w^T)
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_lora(Q35LoraArgs a) {
+  const int64_t n = a.T * a.N;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = e / a.N, c = e - t * a.N;
+    float acc = 0.f;
+    for (int64_t k = 0; k < a.K; ++k) acc += a.x[t * a.K + k] * a.w[c * a.K + k];
+    if (a.accumulate)
+      a.y[e] += acc * a.alpha;
+    else
+      a.y[e] = acc;
+  }
+}
+
+// ---- SwiGLU of separate gate / up projections (layers.rs:270-293):
+// act = bf16(silu(g) * u) with g, u the bf16 projection outputs.
+struct Q35SiluArgs {
+  const uint16_t *g, *u;
+  uint16_t *act;
+  int64_t n;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_silu_mul(Q35SiluArgs a) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < a.n;
+       e += (int64_t)gridDim.x * blockDim.x)
+    a.act[e] = f32_to_bf16_bits(silu_mul_f32(bf16_bits_to_f32(a.g[e]), bf16_bits_to_f32(a.u[e])));
+}

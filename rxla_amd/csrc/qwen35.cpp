@@ -1,0 +1,572 @@
+// Qwen3.5 hybrid W8 text model: full-sequence inference behind the C ABI.
+//
+// Follows qwen3_5(cx, token_ids, config) (crates/rxla-models/src/qwen3_5/
+// mod.rs:197-273) through the applied-model flow (crates/rxla-nn/src/
+// applied.rs:156-239): W8 embedding gather (mod.rs:134-157); per layer a
+// zero-centred input RMSNorm, a gated-delta (layers.rs:113-268) or
+// output-gated full-attention (layers.rs:28-100) mixer with residual, a
+// zero-centred post-attention RMSNorm and the SwiGLU MLP (layers.rs:270-293)
+// with residual; the final zero-centred norm and the tied W8 LM head with an
+// optional F32 LoRA update (mod.rs:158-195). Every sequence of the batch runs
+// from position 0 (mod.rs:211-229: positions iota, angles pos * theta^(-2i/r)).
+//
+// Projections are QuantizedLinear with compute dtype BF16 (bf16 x, bf16
+// dequantised weights, f32 accumulation, bf16-rounded result) on the shared
+// W8A16 GEMM / GEMV / generic paths; the LM head computes in F32 (a plain
+// linear against the f32 dequantised table). Token t = b * S + i is position
+// i of sequence b.
+//
+// Parameter schema (prefix P = "model.language_model."):
+//   P embed_tokens.{weight U8 [V, H], scale F32 [V, H/G]}        (tied head)
+//   P embed_tokens.lora_{A,B}.weight F32 [r, H], [V, r]          (lora_rank r > 0)
+//   P layers.{i}.{input,post_attention}_layernorm.weight F32 [H]
+//   linear layers, P layers.{i}.linear_attn.:
+//     in_proj_qkv [3W, H], in_proj_z [W, H], in_proj_b [Hl, H], in_proj_a [Hl, H],
+//     out_proj [H, W] (U8 weight + F32 scale [N, K/G] each); conv1d.weight
+//     F32 [3W, 1, k]; A_log, dt_bias F32 [Hl]; norm.weight F32 [Dl]   (W = Hl Dl)
+//   full layers, P layers.{i}.self_attn.:
+//     q_proj [2 Hq D, H], k_proj / v_proj [Hkv D, H], o_proj [H, Hq D];
+//     q_norm.weight / k_norm.weight F32 [D]
+//   P layers.{i}.mlp.{gate_proj, up_proj} [I, H], down_proj [H, I]
+//   P norm.weight F32 [H]
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "internal.h"
+
+namespace rxw8 {
+
+int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
+                   const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
+                   int64_t G, int compute_bf16, int y_mode);
+int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
+                     int cache_f32, const int32_t *lens, const int32_t *row_seq,
+                     const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
+                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
+                     const AttnRope *rope);
+
+namespace {
+
+// Kernel argument structs (match kernels/qwen35.hip and kernels/decoder.hip).
+struct DecPosArgs {
+  const int32_t *lens;
+  int32_t *pos, *row_seq, *row_len;
+  int b, s;
+};
+struct Q35EmbedArgs {
+  const int32_t *ids;
+  const uint8_t *w;
+  const float *scale;
+  float *h;
+  int64_t T, V, H, G;
+};
+struct Q35NormArgs {
+  const float *x;
+  const float *w;
+  const void *z;
+  void *out;
+  int64_t rows, L, x_stride, out_stride, z_stride;
+  float eps;
+  int zero_centered, out_f32, z_f32;
+};
+struct Q35FaPrepArgs {
+  const uint16_t *qg, *kp, *vp;
+  const float *q_norm, *k_norm, *freqs;
+  float *q_out, *gate_out, *kc, *vc;
+  int T, S, Hq, Hkv, D, rot, Lmax;
+  float eps;
+};
+struct Q35MulArgs {
+  float *x;
+  const float *y;
+  int64_t n;
+};
+struct Q35ConvArgs {
+  const uint16_t *x;
+  const float *w;
+  float *out;
+  int64_t T, C;
+  int S, k;
+};
+struct Q35L2Args {
+  float *mixed;
+  int64_t T;
+  int Hl, Dl;
+  float q_scale;
+};
+struct Q35GateArgs {
+  const uint16_t *b, *a;
+  const float *a_log, *dt_bias;
+  float *beta, *g;
+  int64_t n;
+  int Hl;
+};
+struct Q35DeltaArgs {
+  const float *mixed, *beta, *g;
+  float *out;
+  int B, S, Hl;
+};
+struct Q35SiluArgs {
+  const uint16_t *g, *u;
+  uint16_t *act;
+  int64_t n;
+};
+struct Q35LoraArgs {
+  const float *x;   // [T, K]
+  const float *w;   // [N, K]
+  float *y;         // [T, N]
+  int64_t T, N, K;
+  float alpha;      // y = x w^T (accumulate == 0) or y += alpha * x w^T
+  int accumulate;
+};
+
+unsigned grid_n(int64_t n, int64_t cap = 1 << 16) {
+  int64_t g = (n + 255) / 256;
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(g, cap));
+}
+
+const char *kRoot = "model.language_model.";
+
+struct Param {
+  std::string path;
+  int dtype = 0, rank = 0;
+  int64_t dims[3] = {0, 0, 0};
+  Buffer *bound = nullptr;
+};
+
+// Parameter indices of one layer (-1 where the layer kind has none).
+struct Layer {
+  int full = 0;
+  int in_norm = -1, post_norm = -1;
+  int qkv = -1, conv = -1, z = -1, b = -1, a = -1, a_log = -1, dt_bias = -1, lnorm = -1, out = -1;
+  int q = -1, k = -1, v = -1, qn = -1, kn = -1, o = -1;
+  int gate = -1, up = -1, down = -1;  // a projection's index is its weight; scale = index + 1
+};
+
+}  // namespace
+
+struct Qwen35 {
+  Runtime *rt = nullptr;
+  rxw8_qwen35_config cfg{};
+  int64_t H = 0, I = 0, V = 0, Hq = 0, Hkv = 0, D = 0, Hl = 0, Dl = 0, W = 0, G = 0;
+  int64_t Bmax = 0, Smax = 0;
+  std::vector<Param> params;
+  std::unordered_map<std::string, int> index;
+  std::vector<Layer> layers;
+  int embed = -1, final_norm = -1, lora_a = -1, lora_b = -1;
+  bool any_full = false, any_linear = false;
+  // device memory: one block for activations, caches and constants
+  void *block = nullptr;
+  float *freqs = nullptr;
+  int32_t *zero_lens = nullptr, *pos = nullptr, *row_seq = nullptr, *row_len = nullptr;
+  float *h = nullptr, *fin = nullptr, *lora_mid = nullptr;
+  uint16_t *xn = nullptr;
+  // linear layers
+  uint16_t *raw = nullptr, *zp = nullptr, *bp = nullptr, *ap = nullptr, *gated = nullptr;
+  float *mixed = nullptr, *beta = nullptr, *g = nullptr, *dout = nullptr;
+  // full layers
+  uint16_t *qg = nullptr, *kp = nullptr, *vp = nullptr;
+  float *q = nullptr, *gate = nullptr, *att = nullptr, *kc = nullptr, *vc = nullptr;
+  // MLP
+  uint16_t *gp = nullptr, *upp = nullptr, *act = nullptr;
+
+  void *ptr(int i) const { return params[(size_t)i].bound->ptr; }
+  const float *f32(int i) const { return (const float *)ptr(i); }
+};
+
+namespace {
+
+int add_param(Qwen35 *m, const std::string &path, int dtype, int64_t d0, int64_t d1 = 0,
+              int64_t d2 = 0) {
+  Param p;
+  p.path = path;
+  p.dtype = dtype;
+  p.rank = d2 > 0 ? 3 : (d1 > 0 ? 2 : 1);
+  p.dims[0] = d0;
+  p.dims[1] = d1;
+  p.dims[2] = d2;
+  m->index[path] = (int)m->params.size();
+  m->params.push_back(p);
+  return (int)m->params.size() - 1;
+}
+
+// U8 weight [n, k] then F32 scale [n, k / G]; returns the weight's index.
+int add_proj(Qwen35 *m, const std::string &base, int64_t n, int64_t k) {
+  const int w = add_param(m, base + ".weight", RXW8_U8, n, k);
+  add_param(m, base + ".scale", RXW8_F32, n, k / m->G);
+  return w;
+}
+
+void build_schema(Qwen35 *m) {
+  const std::string root = kRoot;
+  m->embed = add_proj(m, root + "embed_tokens", m->V, m->H);
+  if (m->cfg.lora_rank > 0) {
+    m->lora_a = add_param(m, root + "embed_tokens.lora_A.weight", RXW8_F32, m->cfg.lora_rank, m->H);
+    m->lora_b = add_param(m, root + "embed_tokens.lora_B.weight", RXW8_F32, m->V, m->cfg.lora_rank);
+  }
+  for (size_t i = 0; i < m->layers.size(); ++i) {
+    Layer &L = m->layers[i];
+    const std::string pre = root + "layers." + std::to_string(i) + ".";
+    L.in_norm = add_param(m, pre + "input_layernorm.weight", RXW8_F32, m->H);
+    if (L.full) {
+      const std::string a = pre + "self_attn.";
+      L.q = add_proj(m, a + "q_proj", 2 * m->Hq * m->D, m->H);
+      L.qn = add_param(m, a + "q_norm.weight", RXW8_F32, m->D);
+      L.k = add_proj(m, a + "k_proj", m->Hkv * m->D, m->H);
+      L.kn = add_param(m, a + "k_norm.weight", RXW8_F32, m->D);
+      L.v = add_proj(m, a + "v_proj", m->Hkv * m->D, m->H);
+      L.o = add_proj(m, a + "o_proj", m->H, m->Hq * m->D);
+    } else {
+      const std::string a = pre + "linear_attn.";
+      L.qkv = add_proj(m, a + "in_proj_qkv", 3 * m->W, m->H);
+      L.conv = add_param(m, a + "conv1d.weight", RXW8_F32, 3 * m->W, 1, m->cfg.conv_kernel);
+      L.z = add_proj(m, a + "in_proj_z", m->W, m->H);
+      L.b = add_proj(m, a + "in_proj_b", m->Hl, m->H);
+      L.a = add_proj(m, a + "in_proj_a", m->Hl, m->H);
+      L.a_log = add_param(m, a + "A_log", RXW8_F32, m->Hl);
+      L.dt_bias = add_param(m, a + "dt_bias", RXW8_F32, m->Hl);
+      L.lnorm = add_param(m, a + "norm.weight", RXW8_F32, m->Dl);
+      L.out = add_proj(m, a + "out_proj", m->H, m->W);
+    }
+    L.post_norm = add_param(m, pre + "post_attention_layernorm.weight", RXW8_F32, m->H);
+    L.gate = add_proj(m, pre + "mlp.gate_proj", m->I, m->H);
+    L.up = add_proj(m, pre + "mlp.up_proj", m->I, m->H);
+    L.down = add_proj(m, pre + "mlp.down_proj", m->H, m->I);
+  }
+  m->final_norm = add_param(m, root + "norm.weight", RXW8_F32, m->H);
+}
+
+// Carve the device block: [offset, bytes] pairs, 256-byte aligned.
+struct Carver {
+  size_t off = 0;
+  std::vector<std::pair<void **, size_t>> items;
+  template <typename T>
+  void add(T **p, int64_t count) {
+    items.push_back({(void **)p, (size_t)count * sizeof(T)});
+  }
+  size_t total() const {
+    size_t o = 0;
+    for (auto &it : items) o += (it.second + 255) & ~(size_t)255;
+    return o;
+  }
+  void assign(void *base) {
+    size_t o = 0;
+    for (auto &it : items) {
+      *it.first = it.second ? (char *)base + o : nullptr;
+      o += (it.second + 255) & ~(size_t)255;
+    }
+  }
+};
+
+int allocate(Qwen35 *m) {
+  const int64_t T = m->Bmax * m->Smax;
+  Carver c;
+  c.add(&m->freqs, std::max<int64_t>(1, m->cfg.rotary_dim / 2));
+  c.add(&m->zero_lens, m->Bmax);
+  c.add(&m->pos, T);
+  c.add(&m->row_seq, T);
+  c.add(&m->row_len, T);
+  c.add(&m->h, T * m->H);
+  c.add(&m->fin, T * m->H);
+  c.add(&m->xn, T * m->H);
+  if (m->cfg.lora_rank > 0) c.add(&m->lora_mid, T * m->cfg.lora_rank);
+  if (m->any_linear) {
+    c.add(&m->raw, T * 3 * m->W);
+    c.add(&m->mixed, T * 3 * m->W);
+    c.add(&m->zp, T * m->W);
+    c.add(&m->bp, T * m->Hl);
+    c.add(&m->ap, T * m->Hl);
+    c.add(&m->beta, T * m->Hl);
+    c.add(&m->g, T * m->Hl);
+    c.add(&m->dout, T * m->W);
+    c.add(&m->gated, T * m->W);
+  }
+  if (m->any_full) {
+    c.add(&m->qg, T * 2 * m->Hq * m->D);
+    c.add(&m->kp, T * m->Hkv * m->D);
+    c.add(&m->vp, T * m->Hkv * m->D);
+    c.add(&m->q, T * m->Hq * m->D);
+    c.add(&m->gate, T * m->Hq * m->D);
+    c.add(&m->att, T * m->Hq * m->D);
+    c.add(&m->kc, m->Bmax * m->Hkv * m->Smax * m->D);
+    c.add(&m->vc, m->Bmax * m->Hkv * m->Smax * m->D);
+  }
+  c.add(&m->gp, T * m->I);
+  c.add(&m->upp, T * m->I);
+  c.add(&m->act, T * m->I);
+  const size_t bytes = c.total();
+  hipError_t e = hipMalloc(&m->block, bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(RXW8_RESOURCE_EXHAUSTED, "qwen35: cannot allocate %zu bytes of activations", bytes);
+  }
+  c.assign(m->block);
+  RXW8_HIP(hipMemsetAsync(m->block, 0, bytes, m->rt->stream));
+  // RoPE frequencies theta^(-2i / rotary_dim) in f32 on the host (mod.rs:211-219).
+  std::vector<float> f((size_t)std::max<int64_t>(1, m->cfg.rotary_dim / 2), 0.f);
+  for (int64_t i = 0; i < m->cfg.rotary_dim / 2; ++i)
+    f[(size_t)i] = powf(m->cfg.theta, -2.0f * (float)i / (float)m->cfg.rotary_dim);
+  RXW8_HIP(hipMemcpyAsync(m->freqs, f.data(), f.size() * sizeof(float), hipMemcpyHostToDevice,
+                          m->rt->stream));
+  RXW8_HIP(hipStreamSynchronize(m->rt->stream));
+  return RXW8_OK;
+}
+
+// QuantizedLinear with compute dtype BF16 on projection `p` (weight p, scale p + 1).
+int proj(Qwen35 *m, int p, const void *x, int x_f32, void *y, int y_mode, int64_t T) {
+  const Param &w = m->params[(size_t)p];
+  return qlinear_launch(m->rt, x, x_f32, (const uint8_t *)m->ptr(p), false, m->f32(p + 1), y, 0, T,
+                        w.dims[0], w.dims[1], m->G, 1, y_mode);
+}
+
+int norm(Qwen35 *m, const float *x, const float *w, void *out, int64_t rows, int64_t L,
+         bool zero_centered, bool out_f32, const void *z = nullptr) {
+  Q35NormArgs a{x, w, z, out, rows, L, L, L, L, m->cfg.eps, zero_centered ? 1 : 0, out_f32 ? 1 : 0, 0};
+  return launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)rows), dim3(256), a);
+}
+
+int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
+  Runtime *rt = m->rt;
+  const int64_t T = B * S;
+  int rc;
+  if ((rc = proj(m, L.qkv, m->xn, 0, m->raw, 0, T))) return rc;
+  Q35ConvArgs cv{m->raw, m->f32(L.conv), m->mixed, T, 3 * m->W, (int)S, (int)m->cfg.conv_kernel};
+  if ((rc = launch(rt, "rxw8_q35_conv_silu", dim3(grid_n(T * 3 * m->W)), dim3(256), cv))) return rc;
+  Q35L2Args l2{m->mixed, T, (int)m->Hl, (int)m->Dl, 1.0f / sqrtf((float)m->Dl)};
+  if ((rc = launch(rt, "rxw8_q35_qk_l2norm", dim3((unsigned)((T * 2 * m->Hl + 3) / 4)), dim3(256), l2)))
+    return rc;
+  if ((rc = proj(m, L.z, m->xn, 0, m->zp, 0, T))) return rc;
+  if ((rc = proj(m, L.b, m->xn, 0, m->bp, 0, T))) return rc;
+  if ((rc = proj(m, L.a, m->xn, 0, m->ap, 0, T))) return rc;
+  Q35GateArgs ga{m->bp, m->ap, m->f32(L.a_log), m->f32(L.dt_bias), m->beta, m->g, T * m->Hl, (int)m->Hl};
+  if ((rc = launch(rt, "rxw8_q35_beta_decay", dim3(grid_n(T * m->Hl)), dim3(256), ga))) return rc;
+  Q35DeltaArgs da{m->mixed, m->beta, m->g, m->dout, (int)B, (int)S, (int)m->Hl};
+  char kname[40];
+  std::snprintf(kname, sizeof kname, "rxw8_q35_delta_rule_d%d", (int)m->Dl);
+  if ((rc = launch(rt, kname, dim3((unsigned)(B * m->Hl)), dim3((unsigned)m->Dl), da))) return rc;
+  // gated RMSNorm over each (token, head) row of Dl: plain weight, times silu(z)
+  if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, false, m->zp)))
+    return rc;
+  return proj(m, L.out, m->gated, 0, m->h, 1, T);
+}
+
+int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
+  Runtime *rt = m->rt;
+  const int64_t T = B * S;
+  int rc;
+  if ((rc = proj(m, L.q, m->xn, 0, m->qg, 0, T))) return rc;
+  if ((rc = proj(m, L.k, m->xn, 0, m->kp, 0, T))) return rc;
+  if ((rc = proj(m, L.v, m->xn, 0, m->vp, 0, T))) return rc;
+  Q35FaPrepArgs fa{m->qg, m->kp, m->vp, m->f32(L.qn), m->f32(L.kn), m->freqs, m->q, m->gate,
+                   m->kc, m->vc, (int)T, (int)S, (int)m->Hq, (int)m->Hkv, (int)m->D,
+                   (int)m->cfg.rotary_dim, (int)m->Smax, m->cfg.eps};
+  const int64_t units = T * (m->Hq + m->Hkv);
+  if ((rc = launch(rt, "rxw8_q35_fa_prep", dim3((unsigned)((units + 3) / 4)), dim3(256), fa))) return rc;
+  if ((rc = attention_launch(rt, m->q, 1, m->kc, m->vc, 1, m->row_len, m->row_seq, nullptr, 0, 0,
+                             m->att, 1, T, m->Hq, m->Hkv, m->Smax, m->D, 1.0f / sqrtf((float)m->D),
+                             nullptr)))
+    return rc;
+  Q35MulArgs mu{m->att, m->gate, T * m->Hq * m->D};
+  if ((rc = launch(rt, "rxw8_q35_mul", dim3(grid_n(T * m->Hq * m->D)), dim3(256), mu))) return rc;
+  return proj(m, L.o, m->att, 1, m->h, 1, T);
+}
+
+int enqueue_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int64_t S) {
+  Runtime *rt = m->rt;
+  const int64_t T = B * S;
+  int rc;
+  DecPosArgs pa{m->zero_lens, m->pos, m->row_seq, m->row_len, (int)B, (int)S};
+  if ((rc = launch(rt, "rxw8_dec_positions", dim3(grid_n(T)), dim3(256), pa))) return rc;
+  Q35EmbedArgs ea{ids, (const uint8_t *)m->ptr(m->embed), m->f32(m->embed + 1), m->h, T, m->V, m->H, m->G};
+  if ((rc = launch(rt, "rxw8_q35_embed", dim3(grid_n(T * m->H)), dim3(256), ea))) return rc;
+  for (const Layer &L : m->layers) {
+    if ((rc = norm(m, m->h, m->f32(L.in_norm), m->xn, T, m->H, true, false))) return rc;
+    if ((rc = L.full ? full_mixer(m, L, B, S) : linear_mixer(m, L, B, S))) return rc;
+    if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, false))) return rc;
+    if ((rc = proj(m, L.gate, m->xn, 0, m->gp, 0, T))) return rc;
+    if ((rc = proj(m, L.up, m->xn, 0, m->upp, 0, T))) return rc;
+    Q35SiluArgs sa{m->gp, m->upp, m->act, T * m->I};
+    if ((rc = launch(rt, "rxw8_q35_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
+    if ((rc = proj(m, L.down, m->act, 0, m->h, 1, T))) return rc;
+  }
+  if ((rc = norm(m, m->h, m->f32(m->final_norm), m->fin, T, m->H, true, true))) return rc;
+  // tied head: f32 hidden . f32 dequantised table (compute F32)
+  if ((rc = qlinear_launch(rt, m->fin, 1, (const uint8_t *)m->ptr(m->embed), false,
+                           m->f32(m->embed + 1), logits, 1, T, m->V, m->H, m->G, 0, 0)))
+    return rc;
+  if (m->cfg.lora_rank > 0) {
+    const int64_t r = m->cfg.lora_rank;
+    Q35LoraArgs down{m->fin, m->f32(m->lora_a), m->lora_mid, T, r, m->H, 1.0f, 0};
+    if ((rc = launch(rt, "rxw8_q35_lora", dim3(grid_n(T * r)), dim3(256), down))) return rc;
+    Q35LoraArgs upd{m->lora_mid, m->f32(m->lora_b), logits, T, m->V, r,
+                    m->cfg.lora_alpha / (float)r, 1};
+    if ((rc = launch(rt, "rxw8_q35_lora", dim3(grid_n(T * m->V)), dim3(256), upd))) return rc;
+  }
+  return RXW8_OK;
+}
+
+void free_model(Qwen35 *m) {
+  if (m->block) {
+    (void)hipStreamSynchronize(m->rt->stream);
+    (void)hipFree(m->block);
+    m->block = nullptr;
+  }
+  for (Param &p : m->params)
+    if (p.bound) rxw8_buffer_release(static_cast<rxw8_buffer *>(p.bound));
+}
+
+}  // namespace
+}  // namespace rxw8
+
+using namespace rxw8;
+
+struct rxw8_qwen35 : rxw8::Qwen35 {};
+
+extern "C" {
+
+int rxw8_qwen35_create(rxw8_runtime *rt, const rxw8_qwen35_config *cfg, rxw8_qwen35 **out) {
+  if (!rt || !cfg || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  const rxw8_qwen35_config &c = *cfg;
+  // Qwen3_5Config::validate (mod.rs:100-131)
+  const bool valid = c.vocab > 0 && c.hidden > 0 && c.intermediate > 0 && c.layers > 0 &&
+                     c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0 && c.head_dim > 0 &&
+                     c.linear_heads > 0 && c.linear_head_dim > 0 && c.conv_kernel > 0 &&
+                     c.max_positions > 0 && c.rotary_dim > 0 && c.rotary_dim <= c.head_dim &&
+                     c.rotary_dim % 2 == 0 && c.group > 0 && c.hidden % c.group == 0 &&
+                     std::isfinite(c.theta) && c.theta > 0 && std::isfinite(c.eps) && c.eps > 0 &&
+                     c.lora_rank >= 0 && (c.lora_rank == 0 || std::isfinite(c.lora_alpha)) &&
+                     (c.layer_kinds || c.full_attention_interval > 0);
+  if (!valid)
+    return fail(RXW8_INVALID_ARGUMENT, "invalid Qwen3.5 configuration (InvalidQwenConfiguration)");
+  if (c.max_batch <= 0 || c.max_seq <= 0)
+    return fail(RXW8_INVALID_ARGUMENT, "max_batch and max_seq must be positive");
+  std::unique_ptr<rxw8_qwen35> m(new rxw8_qwen35());
+  Qwen35 *q = m.get();
+  q->cfg = c;
+  q->cfg.layer_kinds = nullptr;
+  q->H = c.hidden, q->I = c.intermediate, q->V = c.vocab, q->Hq = c.heads, q->Hkv = c.kv_heads;
+  q->D = c.head_dim, q->Hl = c.linear_heads, q->Dl = c.linear_head_dim, q->W = c.linear_heads * c.linear_head_dim;
+  q->G = c.group;
+  q->Bmax = c.max_batch;
+  q->Smax = std::min<int64_t>(c.max_seq, c.max_positions);
+  q->layers.resize((size_t)c.layers);
+  for (int64_t i = 0; i < c.layers; ++i) {
+    const int full = c.layer_kinds ? (c.layer_kinds[i] != 0) : ((i + 1) % c.full_attention_interval == 0);
+    q->layers[(size_t)i].full = full;
+    (full ? q->any_full : q->any_linear) = true;
+  }
+  // every projection's input width must be a whole number of groups
+  std::vector<int64_t> widths = {c.hidden, c.intermediate};
+  if (q->any_full) widths.push_back(c.heads * c.head_dim);
+  if (q->any_linear) widths.push_back(q->W);
+  for (int64_t k : widths)
+    if (k % c.group != 0)
+      return fail(RXW8_INVALID_ARGUMENT, "qwen35: group %lld does not divide projection width %lld",
+                  (long long)c.group, (long long)k);
+  if (q->any_linear && !(q->Dl == 8 || q->Dl == 16 || q->Dl == 32 || q->Dl == 64 || q->Dl == 128))
+    return fail(RXW8_UNIMPLEMENTED, "qwen35: linear_head_dim %lld (supported: 8, 16, 32, 64, 128)",
+                (long long)q->Dl);
+  if (q->any_full && (q->D > 256 || q->D % 2 != 0))
+    return fail(RXW8_UNIMPLEMENTED, "qwen35: head_dim %lld (supported: even, <= 256)", (long long)q->D);
+  if (q->any_full && q->Smax > 8192)
+    return fail(RXW8_UNIMPLEMENTED, "qwen35: full-attention sequences of at most 8192 positions");
+  const int64_t T = q->Bmax * q->Smax;
+  if (T > (1LL << 31) / std::max<int64_t>({q->H, 3 * q->W, q->I, 2 * q->Hq * q->D}))
+    return fail(RXW8_INVALID_ARGUMENT, "qwen35: max_batch * max_seq too large");
+  q->rt = rt;
+  rt->refs.fetch_add(1);
+  build_schema(q);
+  int rc;
+  {
+    std::lock_guard<std::recursive_mutex> g(rt->mu);
+    rc = allocate(q);
+  }
+  if (rc) {
+    free_model(q);
+    runtime_release(rt);
+    return rc;
+  }
+  *out = m.release();
+  return RXW8_OK;
+}
+
+int rxw8_qwen35_destroy(rxw8_qwen35 *m) {
+  if (!m) return fail(RXW8_INVALID_ARGUMENT, "model is NULL");
+  Runtime *rt = m->rt;
+  {
+    std::lock_guard<std::recursive_mutex> g(rt->mu);
+    free_model(m);
+  }
+  delete m;
+  runtime_release(rt);
+  return RXW8_OK;
+}
+
+int rxw8_qwen35_num_parameters(rxw8_qwen35 *m, int *count) {
+  if (!m || !count) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  *count = (int)m->params.size();
+  return RXW8_OK;
+}
+
+int rxw8_qwen35_parameter_info(rxw8_qwen35 *m, int index, const char **path, int *dtype,
+                               int64_t *dims, int *rank) {
+  if (!m) return fail(RXW8_INVALID_ARGUMENT, "model is NULL");
+  if (index < 0 || index >= (int)m->params.size())
+    return fail(RXW8_OUT_OF_RANGE, "parameter index %d outside [0, %zu)", index, m->params.size());
+  const Param &p = m->params[(size_t)index];
+  if (path) *path = p.path.c_str();
+  if (dtype) *dtype = p.dtype;
+  if (rank) *rank = p.rank;
+  if (dims)
+    for (int i = 0; i < p.rank; ++i) dims[i] = p.dims[i];
+  return RXW8_OK;
+}
+
+int rxw8_qwen35_bind_parameter(rxw8_qwen35 *m, const char *path, rxw8_buffer *buf) {
+  if (!m || !path || !buf) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  auto it = m->index.find(path);
+  if (it == m->index.end()) return fail(RXW8_NOT_FOUND, "parameter \"%s\" is absent from the schema", path);
+  Param &p = m->params[(size_t)it->second];
+  if (p.bound) return fail(RXW8_ALREADY_EXISTS, "duplicate parameter binding \"%s\"", path);
+  if (buf->rt != m->rt)
+    return fail(RXW8_INVALID_ARGUMENT, "parameter \"%s\": buffer belongs to another runtime", path);
+  bool shape_ok = buf->rank == p.rank;
+  for (int i = 0; shape_ok && i < p.rank; ++i) shape_ok = buf->dims[i] == p.dims[i];
+  if (!shape_ok)
+    return fail(RXW8_INVALID_ARGUMENT, "parameter \"%s\" %s: shape does not match the schema", path,
+                dims_str(buf).c_str());
+  if (buf->dtype != p.dtype)
+    return fail(RXW8_INVALID_ARGUMENT, "parameter \"%s\": dtype %s does not match the schema (%s)",
+                path, dtype_name(buf->dtype), dtype_name(p.dtype));
+  rxw8_buffer_retain(buf);
+  p.bound = buf;
+  return RXW8_OK;
+}
+
+int rxw8_qwen35_forward(rxw8_qwen35 *m, rxw8_buffer *ids, rxw8_buffer *logits) {
+  if (!m || !ids || !logits) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if (ids->dtype != RXW8_I32 || ids->rank != 2)
+    return fail(RXW8_INVALID_ARGUMENT, "token ids must be I32 [batch, sequence] (InvalidQwenTokenShape)");
+  const int64_t B = ids->dims[0], S = ids->dims[1];
+  if (S <= 0 || S > m->cfg.max_positions || B <= 0)
+    return fail(RXW8_INVALID_ARGUMENT, "sequence %lld outside [1, %lld] (InvalidQwenTokens)",
+                (long long)S, (long long)m->cfg.max_positions);
+  if (B > m->Bmax || S > m->Smax)
+    return fail(RXW8_OUT_OF_RANGE, "batch %lld x sequence %lld exceeds the capacity %lld x %lld",
+                (long long)B, (long long)S, (long long)m->Bmax, (long long)m->Smax);
+  if (logits->dtype != RXW8_F32 || logits->rank != 3 || logits->dims[0] != B ||
+      logits->dims[1] != S || logits->dims[2] != m->V)
+    return fail(RXW8_INVALID_ARGUMENT, "logits must be F32 [batch, sequence, vocab]");
+  if (ids->rt != m->rt || logits->rt != m->rt)
+    return fail(RXW8_INVALID_ARGUMENT, "buffers belong to another runtime");
+  for (const Param &p : m->params)
+    if (!p.bound) return fail(RXW8_FAILED_PRECONDITION, "missing parameter binding \"%s\"", p.path.c_str());
+  std::lock_guard<std::recursive_mutex> g(m->rt->mu);
+  return enqueue_forward(m, (const int32_t *)ids->ptr, (float *)logits->ptr, B, S);
+}
+
+}  // extern "C"

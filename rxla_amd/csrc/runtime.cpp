@@ -19,6 +19,7 @@ extern const unsigned char rxw8_co_misc[], rxw8_co_misc_end[];
 extern const unsigned char rxw8_co_attention[], rxw8_co_attention_end[];
 extern const unsigned char rxw8_co_gemm[], rxw8_co_gemm_end[];
 extern const unsigned char rxw8_co_decoder[], rxw8_co_decoder_end[];
+extern const unsigned char rxw8_co_qwen35[], rxw8_co_qwen35_end[];
 }
 
 namespace rxw8 {
@@ -88,7 +89,8 @@ static int module_of(const char *kname) {
     int module;
   } routes[] = {{"rxw8_gemv_", 0},      {"rxw8_pack_tiles", 0},     {"rxw8_dequant", 1},
                 {"rxw8_linear_generic", 1}, {"rxw8_kv_update", 1}, {"rxw8_gqa_", 2},
-                {"rxw8_w8a16_gemm", 3}, {"rxw8_gemm_", 3},   {"rxw8_dec_", 4}};
+                {"rxw8_w8a16_gemm", 3}, {"rxw8_gemm_", 3},   {"rxw8_dec_", 4},
+                {"rxw8_q35_", 5}};
   for (const auto &r : routes)
     if (std::strncmp(kname, r.prefix, std::strlen(r.prefix)) == 0) return r.module;
   return -1;
@@ -257,7 +259,8 @@ int rxw8_runtime_create(int device, rxw8_runtime **out) {
                {"misc", rxw8_co_misc, rxw8_co_misc_end},
                {"attention", rxw8_co_attention, rxw8_co_attention_end},
                {"gemm", rxw8_co_gemm, rxw8_co_gemm_end},
-               {"decoder", rxw8_co_decoder, rxw8_co_decoder_end}};
+               {"decoder", rxw8_co_decoder, rxw8_co_decoder_end},
+               {"qwen35", rxw8_co_qwen35, rxw8_co_qwen35_end}};
   // Development hook: RXW8_CODE_OBJECT_DIR=<dir> loads <dir>/<name>.hsaco in
   // place of the embedded code object of that name when the file exists.
   const char *override_dir = std::getenv("RXW8_CODE_OBJECT_DIR");

@@ -1,4 +1,5 @@
-"""Decoder plan: the compiled Qwen-style dense W8 decoder behind the C ABI.
+"""Compiled model plans behind the C ABI: the Qwen-style dense W8 decoder
+(DecoderModel) and the Qwen3.5 hybrid W8 text model (Qwen35Model).
 
 Mirrors the reference's model ABI flow (crates/rxla-nn/src/applied.rs):
 ``AppliedModel::compile`` (:808-815) -> ``CompiledModel::bind_parameters``
@@ -47,27 +48,36 @@ class DecoderConfig:
         return dict(self.__dict__)
 
 
-class DecoderModel:
-    """``compile()`` validates the config and allocates the plan (KV cache,
-    activations); ``bind_parameters`` attaches weights by schema path;
-    ``forward`` / ``generate`` run it."""
+class _CompiledPlan:
+    """Shared model ABI flow of the compiled plans: ``compile()`` validates the
+    config and allocates the plan; ``schema()`` lists path-addressed
+    parameters; ``bind_parameter(s)`` attaches weights (retained by the plan);
+    ``load_safetensors`` validates a checkpoint against the schema, then
+    uploads and binds. Subclasses name their C entry points by ``_PREFIX``."""
 
-    def __init__(self, rt: Runtime, cfg: DecoderConfig):
+    _PREFIX = ""
+    CHECKPOINT_PREFIXES = ("",)
+    _FUSED = ()
+
+    def __init__(self, rt: Runtime, cfg):
         self.rt = rt
         self.cfg = cfg
         self._h = None
         self._bound = []
 
-    def compile(self) -> "DecoderModel":
+    def _fn(self, name):
+        return getattr(_lib, self._PREFIX + name)
+
+    def compile(self):
         h = c_void_p()
-        c = self.cfg.c()
-        _check(_lib.rxw8_decoder_create(self.rt.handle, byref(c), byref(h)))
+        self._c = self.cfg.c()  # kept alive while the plan exists
+        _check(self._fn("create")(self.rt.handle, byref(self._c), byref(h)))
         self._h = h
         return self
 
     def close(self):
         if self._h:
-            _check(_lib.rxw8_decoder_destroy(self._h))
+            _check(self._fn("destroy")(self._h))
             self._h = None
 
     def __del__(self):
@@ -79,35 +89,28 @@ class DecoderModel:
     def schema(self):
         """[(path, dtype, shape)] in declaration order."""
         n = c_int()
-        _check(_lib.rxw8_decoder_num_parameters(self._h, byref(n)))
+        _check(self._fn("num_parameters")(self._h, byref(n)))
         out = []
         for i in range(n.value):
             path = c_char_p()
             dt = c_int()
             dims = (c_int64 * 8)()
             rank = c_int()
-            _check(_lib.rxw8_decoder_parameter_info(self._h, i, byref(path), byref(dt), dims,
-                                                    byref(rank)))
+            _check(self._fn("parameter_info")(self._h, i, byref(path), byref(dt), dims, byref(rank)))
             out.append((path.value.decode(), DType(dt.value),
                         tuple(dims[j] for j in range(rank.value))))
         return out
 
     def bind_parameter(self, path: str, buf: Buffer):
-        _check(_lib.rxw8_decoder_bind_parameter(self._h, path.encode(), buf.handle))
+        _check(self._fn("bind_parameter")(self._h, path.encode(), buf.handle))
         self._bound.append(buf)
 
-    def bind_parameters(self, params: dict) -> "DecoderModel":
+    def bind_parameters(self, params: dict):
         for path, buf in params.items():
             self.bind_parameter(path, buf)
         return self
 
     # ---- checkpoints ------------------------------------------------------------
-    CHECKPOINT_PREFIXES = ("", "model.", "model.language_model.")
-    _FUSED = ((re.compile(r"^(layers\.\d+\.self_attn\.)qkv_proj\.(weight|scale)$"),
-               ("q_proj", "k_proj", "v_proj")),
-              (re.compile(r"^(layers\.\d+\.mlp\.)gate_up_proj\.(weight|scale)$"),
-               ("gate_proj", "up_proj")))
-
     def checkpoint_plan(self, st: SafeTensors, mapping: dict | None = None) -> dict:
         """Schema path -> (checkpoint keys stacked along dim 0, dequantise), all
         validated before any payload is read (rxla-safetensors model.rs:384-440:
@@ -178,7 +181,7 @@ class DecoderModel:
                         + "; ".join(errors[:8]) + (" ..." if len(errors) > 8 else ""))
         return plan
 
-    def load_safetensors(self, checkpoint, mapping: dict | None = None) -> "DecoderModel":
+    def load_safetensors(self, checkpoint, mapping: dict | None = None):
         """Validate every parameter against the checkpoint, then upload and bind
         (CompiledModel::bind_parameters over load_parameter_schema_with_mapping)."""
         st = checkpoint if isinstance(checkpoint, SafeTensors) else SafeTensors(checkpoint)
@@ -207,6 +210,18 @@ class DecoderModel:
                 st.close()
         return self
 
+
+class DecoderModel(_CompiledPlan):
+    """The dense decoder plan (KV cache, activations); ``forward`` /
+    ``generate`` run it."""
+
+    _PREFIX = "rxw8_decoder_"
+    CHECKPOINT_PREFIXES = ("", "model.", "model.language_model.")
+    _FUSED = ((re.compile(r"^(layers\.\d+\.self_attn\.)qkv_proj\.(weight|scale)$"),
+               ("q_proj", "k_proj", "v_proj")),
+              (re.compile(r"^(layers\.\d+\.mlp\.)gate_up_proj\.(weight|scale)$"),
+               ("gate_proj", "up_proj")))
+
     def reset(self):
         _check(_lib.rxw8_decoder_reset(self._h))
 
@@ -230,3 +245,78 @@ class DecoderModel:
         _check(_lib.rxw8_decoder_generate(self._h, prompt.handle, b, s, steps, out.handle,
                                           int(use_graph)))
         return out
+
+
+LINEAR, FULL = 0, 1
+
+
+@dataclass
+class Qwen35Config:
+    """Qwen3_5Config (crates/rxla-models/src/qwen3_5/mod.rs:16-33); defaults
+    are the official 0.8B text topology (qwen3_5_0_8b_w8, mod.rs:59-85), with
+    ``layers`` either a count (every ``full_attention_interval``-th layer is
+    full attention) or an explicit list of LINEAR / FULL kinds."""
+    vocab: int = 248320
+    hidden: int = 1024
+    intermediate: int = 3584
+    layers: object = 24
+    heads: int = 8
+    kv_heads: int = 2
+    head_dim: int = 256
+    linear_heads: int = 16
+    linear_head_dim: int = 128
+    conv_kernel: int = 4
+    max_positions: int = 262144
+    rotary_dim: int = 64
+    group: int = 128
+    full_attention_interval: int = 4
+    theta: float = 1e7
+    eps: float = 1e-6
+    lora_rank: int = 0
+    lora_alpha: float = 0.0
+    max_batch: int = 1
+    max_seq: int = 4096
+
+    @classmethod
+    def tiny(cls, **kw):
+        """Qwen3_5Config::tiny (mod.rs:36-57)."""
+        c = dict(vocab=128, hidden=32, intermediate=64, layers=[LINEAR, FULL], heads=4, kv_heads=2,
+                 head_dim=8, linear_heads=4, linear_head_dim=8, conv_kernel=4, max_positions=128,
+                 rotary_dim=4, group=8, max_seq=128)
+        c.update(kw)
+        return cls(**c)
+
+    def kinds(self):
+        if isinstance(self.layers, int):
+            return [FULL if (i + 1) % self.full_attention_interval == 0 else LINEAR
+                    for i in range(self.layers)]
+        return [FULL if k in (FULL, "full") else LINEAR for k in self.layers]
+
+    def c(self):
+        kinds = self.kinds()
+        arr = (c_int32 * len(kinds))(*kinds)
+        c = _ffi.Qwen35Config(self.vocab, self.hidden, self.intermediate, len(kinds), self.heads,
+                              self.kv_heads, self.head_dim, self.linear_heads,
+                              self.linear_head_dim, self.conv_kernel, self.max_positions,
+                              self.rotary_dim, self.group, self.full_attention_interval,
+                              ctypes.cast(arr, ctypes.POINTER(c_int32)), self.theta, self.eps,
+                              self.lora_rank, self.lora_alpha, self.max_batch, self.max_seq)
+        c._kinds = arr  # the array must outlive the create call
+        return c
+
+
+class Qwen35Model(_CompiledPlan):
+    """The Qwen3.5 hybrid W8 plan: ``forward(ids [B, S] I32)`` returns logits
+    [B, S, V] F32 for every position, as qwen3_5 (mod.rs:197-273) does.
+    Checkpoints written by the reference encoder (quantize_qwen3_5_w8.py:
+    "model.language_model." names, U8 codes + F32 scales) bind verbatim."""
+
+    _PREFIX = "rxw8_qwen35_"
+    CHECKPOINT_PREFIXES = ("",)
+
+    def forward(self, ids: Buffer, logits: Buffer | None = None) -> Buffer:
+        shape = tuple(ids.shape)
+        if logits is None:  # a wrong rank reaches the C check (InvalidQwenTokenShape)
+            logits = self.rt.zeros(shape + (self.cfg.vocab,) if len(shape) == 2 else (1,), DType.F32)
+        _check(_lib.rxw8_qwen35_forward(self._h, ids.handle, logits.handle))
+        return logits

@@ -1,0 +1,188 @@
+"""Qwen3.5 hybrid W8 model on the GPU (rxw8_qwen35_*) against the numpy
+oracle of crates/rxla-models/src/qwen3_5 (oracle/qwen35.py): logits of every
+position within 1e-2 normwise (bf16 projections), the schema equal to the
+reference encoder's layout (quantize_qwen3_5_w8.py), checkpoint loading, and
+the error contract of qwen3_5 / Qwen3_5Config::validate (mod.rs:100-131,
+197-209)."""
+import numpy as np
+import pytest
+
+import st_fixtures as stf
+from conftest import rel_err
+from oracle import qwen35 as q35
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def rx():
+    import rxla_amd
+    return rxla_amd
+
+
+CONFIGS = {
+    # Qwen3_5Config::tiny: every projection on the generic path (K = 32, G = 8)
+    "tiny": dict(q35.config(), max_batch=2, max_seq=24),
+    # widths on the MFMA GEMV / GEMM paths, D = 64 with partial RoPE, Dl = 32
+    "small": dict(q35.config(vocab=512, hidden=256, intermediate=512,
+                             layers=[q35.LINEAR, q35.FULL, q35.LINEAR, q35.FULL], heads=4,
+                             kv_heads=2, head_dim=64, linear_heads=4, linear_head_dim=32,
+                             rotary_dim=16, group=64), max_batch=2, max_seq=80),
+    # the 0.8B layer widths (hidden 1024, D 256, rotary 64, Hl 16 x Dl 128,
+    # intermediate 3584, G 128) on 4 layers and a 2048-entry vocabulary, with
+    # weights ~N(0, 0.02): at std 0.05 these widths make the random network
+    # amplify bf16 rounding flips (the oracle itself moves by 7e-3 when only
+    # its accumulation order changes), at 0.02 by 4e-4
+    "wide": dict(q35.config(vocab=2048, hidden=1024, intermediate=3584,
+                            layers=q35.layer_types(4), heads=8, kv_heads=2, head_dim=256,
+                            linear_heads=16, linear_head_dim=128, rotary_dim=64, group=128),
+                 max_batch=1, max_seq=32, std=0.02),
+}
+CONFIGS["wide_linear"] = dict(CONFIGS["wide"], layers=[q35.LINEAR])
+CONFIGS["wide_full"] = dict(CONFIGS["wide"], layers=[q35.FULL])
+
+
+def model_config(cfg):
+    r = rx()
+    return r.Qwen35Config(vocab=cfg["vocab"], hidden=cfg["hidden"], intermediate=cfg["intermediate"],
+                          layers=[r.model.FULL if k == q35.FULL else r.model.LINEAR
+                                  for k in cfg["layers"]],
+                          heads=cfg["heads"], kv_heads=cfg["kv_heads"], head_dim=cfg["head_dim"],
+                          linear_heads=cfg["linear_heads"], linear_head_dim=cfg["linear_head_dim"],
+                          conv_kernel=cfg["conv_kernel"], max_positions=cfg.get("max_positions", 4096),
+                          rotary_dim=cfg["rotary_dim"], group=cfg["group"], theta=cfg["theta"],
+                          eps=cfg["eps"], lora_rank=cfg.get("lora_rank", 0),
+                          lora_alpha=cfg.get("lora_alpha", 0.0), max_batch=cfg["max_batch"],
+                          max_seq=cfg["max_seq"])
+
+
+def build(rt, cfg, params):
+    m = rx().Qwen35Model(rt, model_config(cfg)).compile()
+    for path, dtype, shape in m.schema():
+        m.bind_parameter(path, rt.buffer(np.ascontiguousarray(params[path]), dtype))
+    return m
+
+
+def run(rt, m, ids):
+    r = rx()
+    return m.forward(rt.buffer(ids.astype(np.int32))).to_numpy()
+
+
+@pytest.mark.parametrize("name,b,s", [("tiny", 2, 13), ("small", 2, 13), ("small", 2, 70),
+                                      ("small", 1, 1), ("wide_linear", 1, 16),
+                                      ("wide_full", 1, 16), ("wide", 1, 16), ("wide", 1, 32)])
+def test_logits_match_the_oracle(rt, name, b, s):
+    cfg = CONFIGS[name]
+    p = q35.random_params(cfg, seed=11, std=cfg.get("std", 0.05))
+    ids = np.random.default_rng(12).integers(0, cfg["vocab"], (b, s))
+    got = run(rt, build(rt, cfg, p), ids)
+    want = q35.forward(cfg, p, ids)
+    assert got.shape == (b, s, cfg["vocab"])
+    err = rel_err(got, want)
+    print(f"qwen35 {name} b={b} s={s}: rel err {err:.2e}")
+    assert err <= TOL
+    # the greedy token of every position agrees wherever the oracle's margin is clear
+    top2 = np.sort(want, axis=-1)[..., -2:]
+    clear = (top2[..., 1] - top2[..., 0]) > 0.05 * np.abs(want).max()
+    np.testing.assert_array_equal(got.argmax(-1)[clear], want.argmax(-1)[clear])
+
+
+def test_sequences_are_independent_and_causal(rt):
+    """Row b of the batch depends only on sequence b; position i only on
+    tokens <= i (bit for bit: the same kernels see the same shapes)."""
+    cfg = CONFIGS["small"]
+    m = build(rt, cfg, q35.random_params(cfg, seed=13))
+    rng = np.random.default_rng(14)
+    ids = rng.integers(0, cfg["vocab"], (2, 40))
+    a = run(rt, m, ids)
+    ids2 = ids.copy()
+    ids2[1] = rng.integers(0, cfg["vocab"], 40)  # other sequence changed
+    ids2[0, 25:] = (ids2[0, 25:] + 7) % cfg["vocab"]  # future of sequence 0 changed
+    b = run(rt, m, ids2)
+    np.testing.assert_array_equal(a[0, :25], b[0, :25])
+    assert np.abs(a[0, 25:] - b[0, 25:]).max() > 0
+    np.testing.assert_array_equal(run(rt, m, ids), a)  # deterministic
+
+
+def test_lora_head(rt):
+    cfg = dict(CONFIGS["small"], lora_rank=4, lora_alpha=64.0)
+    p = q35.random_params(cfg, seed=15)
+    ids = np.random.default_rng(16).integers(0, cfg["vocab"], (2, 9))
+    got = run(rt, build(rt, cfg, p), ids)
+    want = q35.forward(cfg, p, ids)
+    nolora = dict(cfg, lora_rank=0)
+    base = q35.forward(nolora, p, ids)
+    got_base = run(rt, build(rt, nolora, p), ids)
+    print(f"lora: base {rel_err(got_base, base):.2e} update {rel_err(got - got_base, want - base):.2e} "
+          f"total {rel_err(got, want):.2e} visible {rel_err(want, base):.2e}")
+    assert rel_err(want, base) > 0.05  # the update is visible at this tolerance
+    # the update alone (its input, the final norm, carries the base's bf16 deviations)
+    assert rel_err(got - got_base, want - base) <= TOL
+    assert rel_err(got, want) <= TOL
+
+
+def test_schema_is_the_encoder_layout(rt):
+    """Paths, dtypes and shapes equal the reference encoder's output for the
+    same topology (random_params follows quantize_qwen3_5_w8.py:27-55)."""
+    r = rx()
+    for name in ("small", "wide"):
+        cfg = CONFIGS[name]
+        p = q35.random_params(cfg, seed=0)
+        m = r.Qwen35Model(rt, model_config(cfg)).compile()
+        sch = m.schema()
+        assert sorted(path for path, _, _ in sch) == sorted(p)
+        for path, dtype, shape in sch:
+            assert tuple(p[path].shape) == shape, path
+            assert dtype == (r.DType.U8 if p[path].dtype == np.uint8 else r.DType.F32), path
+
+
+def test_checkpoint_loads_verbatim(rt, tmp_path):
+    r = rx()
+    cfg = CONFIGS["small"]
+    p = q35.random_params(cfg, seed=17)
+    ck = tmp_path / "q35.safetensors"
+    stf.write(ck, {k: ("U8" if v.dtype == np.uint8 else "F32", v) for k, v in p.items()},
+              {"format": "rxla-qwen3.5-w8-v1", "group_size": str(cfg["group"])})
+    ids = np.random.default_rng(18).integers(0, cfg["vocab"], (2, 11))
+    direct = run(rt, build(rt, cfg, p), ids)
+    loaded = r.Qwen35Model(rt, model_config(cfg)).compile().load_safetensors(ck)
+    np.testing.assert_array_equal(run(rt, loaded, ids), direct)
+    bad = tmp_path / "g.safetensors"
+    stf.write(bad, {k: ("U8" if v.dtype == np.uint8 else "F32", v) for k, v in p.items()},
+              {"group_size": "32"})
+    with pytest.raises(r.Error) as e:
+        r.Qwen35Model(rt, model_config(cfg)).compile().load_safetensors(bad)
+    assert "group_size" in str(e.value)
+
+
+def test_error_contract(rt):
+    r = rx()
+    cfg = dict(CONFIGS["tiny"], max_positions=16)
+    p = q35.random_params(cfg, seed=19)
+    m = build(rt, cfg, p)
+
+    def code(fn):
+        with pytest.raises(r.Error) as e:
+            fn()
+        return e.value.code
+
+    assert code(lambda: m.forward(rt.buffer(np.zeros((1, 17), np.int32)))) == r.Status.INVALID_ARGUMENT
+    assert code(lambda: m.forward(rt.buffer(np.zeros((3, 4), np.int32)))) == r.Status.OUT_OF_RANGE
+    assert code(lambda: m.forward(rt.buffer(np.zeros(4, np.int32)))) == r.Status.INVALID_ARGUMENT
+    assert code(lambda: m.forward(rt.buffer(np.zeros((1, 4), np.int32)),
+                                  rt.zeros((1, 4, 3), r.DType.F32))) == r.Status.INVALID_ARGUMENT
+    unbound = r.Qwen35Model(rt, model_config(cfg)).compile()
+    assert code(lambda: unbound.forward(rt.buffer(np.zeros((1, 4), np.int32)))) == \
+        r.Status.FAILED_PRECONDITION
+    path, dtype, shape = unbound.schema()[0]
+    assert code(lambda: unbound.bind_parameter("nope", rt.zeros(shape, dtype))) == r.Status.NOT_FOUND
+    assert code(lambda: unbound.bind_parameter(path, rt.zeros((1,), dtype))) == r.Status.INVALID_ARGUMENT
+    unbound.bind_parameter(path, rt.zeros(shape, dtype))
+    assert code(lambda: unbound.bind_parameter(path, rt.zeros(shape, dtype))) == r.Status.ALREADY_EXISTS
+    for bad in (dict(rotary_dim=9), dict(rotary_dim=12), dict(heads=3), dict(group=5),
+                dict(eps=0.0)):
+        assert code(lambda: r.Qwen35Model(rt, model_config(dict(cfg, **bad))).compile()) == \
+            r.Status.INVALID_ARGUMENT, bad
+    assert code(lambda: r.Qwen35Model(rt, model_config(dict(cfg, linear_head_dim=12))).compile()) == \
+        r.Status.UNIMPLEMENTED

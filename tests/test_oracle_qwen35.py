@@ -108,3 +108,22 @@ def test_forward_runs_and_the_first_row_ignores_the_future():
     lg2 = q35.forward(cfg, p, ids2)
     np.testing.assert_allclose(lg2[:, :3], lg[:, :3], rtol=1e-12, atol=1e-12)  # causal
     assert np.abs(lg2[:, 3:] - lg[:, 3:]).max() > 0
+
+
+def test_lora_head_is_a_low_rank_update_scaled_by_alpha_over_rank():
+    """The LoRA head adds (alpha / r) (n A^T) B^T: zero with B = 0, a matrix of
+    rank <= r over the positions, linear in alpha."""
+    cfg = q35.config(layers=[q35.LINEAR], lora_rank=2, lora_alpha=4.0, vocab=96, hidden=32)
+    p = q35.random_params(cfg, seed=7)
+    ids = np.random.default_rng(8).integers(0, cfg["vocab"], (1, 9))
+    base = q35.forward(dict(cfg, lora_rank=0), p, ids)
+    lg = q35.forward(cfg, p, ids)
+    diff = (lg - base)[0]
+    sv = np.linalg.svd(diff, compute_uv=False)
+    assert sv[1] > 1e-3 * sv[0] and sv[2] < 1e-9 * sv[0]  # rank exactly 2
+    lg2 = q35.forward(dict(cfg, lora_alpha=8.0), p, ids)
+    np.testing.assert_allclose(lg2 - base, 2 * (lg - base), rtol=1e-9, atol=1e-12)
+    zb = dict(p)
+    zb["model.language_model.embed_tokens.lora_B.weight"] = np.zeros_like(
+        p["model.language_model.embed_tokens.lora_B.weight"])
+    np.testing.assert_array_equal(q35.forward(cfg, zb, ids), base)
