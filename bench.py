@@ -290,6 +290,84 @@ def bench_decoder(rt, rx, torch, stream, prompt_len=1024, steps=256, batch=8):
                       "synchronized, best of 2"}
 
 
+def qwen35_weights(rt, rx, torch, stream, model, group, seed=7):
+    """Random-init W8 parameters for a Qwen35Model, generated on the device:
+    2-D weights ~N(0, 0.02) quantised per group as the reference encoder does
+    (quantize_qwen3_5_w8.py:27-44: s = max|w_g| / 127, u8 = rne(w / s) + 128);
+    zero-centred norm weights 0, the gated norm's weight 1, conv ~N(0, 0.1),
+    A_log and dt_bias 0."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    keep, pending = [], {}
+    with torch.cuda.stream(stream):
+        for path, dtype, shape in model.schema():
+            if path.endswith(".scale"):
+                t = pending.pop(path)
+            elif dtype == rx.DType.U8:
+                t = torch.empty(shape, dtype=torch.uint8, device="cuda")
+                sc = torch.empty((shape[0], shape[1] // group), dtype=torch.float32, device="cuda")
+                step = max(1, (1 << 26) // shape[1])  # quantise in row chunks (bounded scratch)
+                for r0 in range(0, shape[0], step):
+                    w = torch.randn((min(step, shape[0] - r0), shape[1]), device="cuda",
+                                    generator=gen) * 0.02
+                    wg = w.view(w.shape[0], shape[1] // group, group)
+                    s_ = wg.abs().amax(dim=2).clamp_min(1e-12) / 127.0
+                    t[r0:r0 + w.shape[0]] = (torch.round(wg / s_[:, :, None]).clamp(-127, 127)
+                                             + 128).to(torch.uint8).view(w.shape)
+                    sc[r0:r0 + w.shape[0]] = s_
+                pending[path[:-len(".weight")] + ".scale"] = sc
+            elif "conv1d" in path:
+                t = torch.randn(shape, device="cuda", generator=gen) * 0.1
+            elif path.endswith("linear_attn.norm.weight"):
+                t = torch.ones(shape, device="cuda", dtype=torch.float32)
+            else:
+                t = torch.zeros(shape, device="cuda", dtype=torch.float32)
+            keep.append(t)
+            stream.synchronize()
+            model.bind_parameter(path, rt.wrap_tensor(t))
+    rt.synchronize()
+    return keep
+
+
+def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, iterations=10):
+    """The reference's qwen3_5_bench workload (crates/rxla-safetensors/examples/
+    qwen3_5_bench.rs:44-99) on the official 0.8B text topology with random
+    weights: batch 1, token ids 1000 + i, full logits [1, S, 248320] per run;
+    tokens/s = S / mean run time."""
+    cfg = rx.Qwen35Config(max_batch=1, max_seq=max(sequences))
+    model = rx.Qwen35Model(rt, cfg).compile()
+    keep = qwen35_weights(rt, rx, torch, stream, model, cfg.group)
+    weight_bytes = sum(int(np.prod(sh)) * (1 if dt == rx.DType.U8 else 4)
+                       for _, dt, sh in model.schema())
+    res = {}
+    for S in sequences:
+        ids = rt.buffer(np.arange(1000, 1000 + S, dtype=np.int32).reshape(1, S))
+        logits = rt.zeros((1, S, cfg.vocab), rx.DType.F32)
+        for _ in range(warmup):
+            model.forward(ids, logits)
+        rt.synchronize()
+        samples = []
+        for _ in range(iterations):
+            t0 = time.perf_counter()
+            model.forward(ids, logits)
+            rt.synchronize()
+            samples.append(time.perf_counter() - t0)
+        lg = logits.to_numpy()
+        mean = float(np.mean(samples))
+        res[f"S{S}"] = {"mean_ms": round(mean * 1e3, 3),
+                        "p50_ms": round(float(np.median(samples)) * 1e3, 3),
+                        "tokens_per_s": round(S / mean, 1),
+                        "weight_GBs": round(weight_bytes / mean / 1e9, 1),
+                        "finite": bool(np.isfinite(lg).all()),
+                        "checksum": float(lg.astype(np.float64).sum())}
+        del logits
+    del keep, model
+    return {"runs": res, "weight_bytes": weight_bytes,
+            "config": "Qwen3.5-0.8B text topology (24 layers, 18 gated-delta + 6 full attention, "
+                      "hidden 1024, vocab 248320, G 128), batch 1, random W8 weights",
+            "timing": f"wall clock around rxw8_qwen35_forward, synchronized; {warmup} warmup, "
+                      f"mean of {iterations}"}
+
+
 def pmc_probe(kind, reps=30):
     """A short fixed program for rocprofv3 --pmc passes: `reps` launches of one
     roofline shape plus 4 plain 256 MiB device copies (torch) that calibrate
@@ -339,6 +417,7 @@ def main():
     ap.add_argument("--skip-gemm", action="store_true")
     ap.add_argument("--skip-attention", action="store_true")
     ap.add_argument("--skip-decoder", action="store_true")
+    ap.add_argument("--skip-qwen35", action="store_true")
     ap.add_argument("--pmc-probe", choices=["gemv"], help="counter-collection program only")
     args = ap.parse_args()
     if args.pmc_probe:
@@ -523,6 +602,10 @@ def main():
         log("synthetic 28-layer decoder: prefill 8x1024, 256 greedy steps ...")
         out["decoder"] = bench_decoder(rt, rx, torch, stream)
         log(json.dumps(out["decoder"]))
+    if not args.skip_qwen35:
+        log("Qwen3.5-0.8B topology, full-sequence logits ...")
+        out["qwen35"] = bench_qwen35(rt, rx, torch, stream)
+        log(json.dumps(out["qwen35"]))
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle) ...")
         out["cpu_baseline"] = cpu_baseline()

@@ -73,6 +73,153 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_linear_generic(GenericLin
   }
 }
 
+// ---- W8 linear with compute dtype F32 on the matrix cores:
+//   y[t, n] = sum_k x[t, k] * ((u8[n, k] - 128) * s[n, k / G])
+// (layers.rs:277-298 with an f32 compute dtype; also the tied LM head,
+// qwen3_5/mod.rs:158-173). Each f32 activation is split into bf16 parts
+// x = hi + lo + r, hi = bf16(x), lo = bf16(x - hi), |r| <= 2^-17 |x|; the codes
+// u - 128 are exact in bf16, so v_mfma_f32_16x16x32_bf16 forms the products of
+// both parts exactly and accumulates them in f32. The scale is applied per
+// group to the f32 group sums (a reassociation of the reference's
+// x . (q * s): both are f32 sums of the same terms up to f32 rounding).
+//
+// Workgroup: WV waves, 16 output channels per wave (16 WV per workgroup) and
+// 16 R rows of x. The R row tiles of x (hi and lo, rows padded by 16 bytes so
+// the 16 lanes reading one column group hit distinct banks) and the
+// workgroup's scales are staged in LDS once; each lane then streams 16-byte
+// slices of one weight row (lane = row + 16 * slice, 64 contiguous bytes per
+// row per wave load) with PF loads in flight, all other reads being LDS. The
+// 16 codes of a slice are the B operands of two MFMAs (k permuted identically
+// in A and B). Rows of x >= T and channels >= N read clamped, valid addresses
+// and are never stored.
+struct LinearF32Args {
+  const float *x;      // [T, K]
+  const uint8_t *w;    // [N, K]
+  const float *scale;  // [N, K / G]
+  float *y;            // [T, N]
+  int T, N, K, G;
+  int y_mode;          // 0: y = result; 1: y += result (f32 residual)
+};
+
+template <int R, int WV>
+__device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
+  constexpr int PF = 8;
+  extern __shared__ __attribute__((aligned(16))) uint16_t f32lin_lds[];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int K = a.K, ng = K / a.G, gs = a.G / 64, steps = K / 64;
+  const int rowp = K + 8;  // bf16 elements per staged row (16-byte pad)
+  uint16_t *ah = f32lin_lds;
+  uint16_t *al = ah + 16 * R * rowp;
+  float *sc = (float *)(al + 16 * R * rowp);
+  const int m0 = blockIdx.y * 16 * R;
+  const int n0 = blockIdx.x * 16 * WV;
+  // ---- stage x (split into hi / lo) and the scales
+  for (int e = threadIdx.x * 4; e < 16 * R * K; e += blockDim.x * 4) {
+    const int m = e / K, c = e - m * K;
+    const int t = min(m0 + m, a.T - 1);
+    const float4 v = *(const float4 *)(a.x + (int64_t)t * K + c);
+    const float xs[4] = {v.x, v.y, v.z, v.w};
+    uint32_t hb[4], lb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      hb[i] = f32_to_bf16_bits(xs[i]);
+      lb[i] = f32_to_bf16_bits(xs[i] - bf16_bits_to_f32(hb[i]));
+    }
+    *(uint2 *)(ah + m * rowp + c) = uint2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+    *(uint2 *)(al + m * rowp + c) = uint2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+  }
+  for (int e = threadIdx.x; e < 16 * WV * ng; e += blockDim.x) {
+    const int r = e / ng, g = e - r * ng;
+    const int n = min(n0 + r, a.N - 1);
+    sc[e] = a.scale[(int64_t)n * ng + g];
+  }
+  __syncthreads();
+  // ---- stream the weight rows
+  const int col = lane & 15, part = lane >> 4;
+  const int nrow = min(n0 + 16 * wv + col, a.N - 1);
+  const uint8_t *wp = a.w + (int64_t)nrow * K + 16 * part;
+  const float *scl = sc + (16 * wv + col) * ng;
+  f32x4 acc[R], accg[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    accg[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // one K step of 64: the lane's 16 codes as two bf16x8 B operands (u - 128,
+  // exact), four MFMAs per row tile (hi, lo x two k halves); at the end of a
+  // scale group the group sums are scaled into acc (branch-free selects keep
+  // the loop body one basic block, so the load waits stay counted)
+  auto step = [&](const u32x4 cur, int s) {
+    u32x4 b[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const uint32_t q = cur[2 * h + d];
+        b[h][2 * d] = pack_bf16x2((float)(q & 0xffu) - 128.f, (float)((q >> 8) & 0xffu) - 128.f);
+        b[h][2 * d + 1] = pack_bf16x2((float)((q >> 16) & 0xffu) - 128.f, (float)(q >> 24) - 128.f);
+      }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int off = (16 * r + col) * rowp + 64 * s + 16 * part;
+      const u32x4 h0 = *(const u32x4 *)(ah + off), h1 = *(const u32x4 *)(ah + off + 8);
+      const u32x4 l0 = *(const u32x4 *)(al + off), l1 = *(const u32x4 *)(al + off + 8);
+      accg[r] = mfma16x16x32(as_bf16x8(h0), as_bf16x8(b[0]), accg[r]);
+      accg[r] = mfma16x16x32(as_bf16x8(l0), as_bf16x8(b[0]), accg[r]);
+      accg[r] = mfma16x16x32(as_bf16x8(h1), as_bf16x8(b[1]), accg[r]);
+      accg[r] = mfma16x16x32(as_bf16x8(l1), as_bf16x8(b[1]), accg[r]);
+    }
+    const bool fold = (s + 1) % gs == 0;
+    const float sg = fold ? scl[s / gs] : 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[r][i] += sg * accg[r][i];
+        accg[r][i] = fold ? 0.f : accg[r][i];
+      }
+  };
+  // PF slices in flight: the slice of step s + PF is requested as step s is
+  // consumed (clamped to the last slice at the end: re-reads of cached bytes)
+  u32x4 buf[PF];
+#pragma unroll
+  for (int j = 0; j < PF; ++j) buf[j] = *(const u32x4 *)(wp + 64 * min(j, steps - 1));
+  int s0 = 0;
+  for (; s0 + PF <= steps; s0 += PF) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const u32x4 cur = buf[j];
+      buf[j] = *(const u32x4 *)(wp + 64 * min(s0 + j + PF, steps - 1));
+      step(cur, s0 + j);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PF; ++j)
+    if (s0 + j < steps) step(buf[j], s0 + j);
+  // ---- store: lane holds rows 4 part + i of each row tile, channel n0 + 16 wv + col
+  const int n = n0 + 16 * wv + col;
+  if (n < a.N) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = m0 + 16 * r + 4 * part + i;
+        if (t < a.T) {
+          float *yp = a.y + (int64_t)t * a.N + n;
+          *yp = a.y_mode == 1 ? *yp + acc[r][i] : acc[r][i];
+        }
+      }
+  }
+}
+
+#define RXW8_LINEAR_F32(R, WV)                                                          \
+  extern "C" __global__ void __launch_bounds__(64 * WV)                                 \
+      rxw8_linear_f32_mfma_r##R##_w##WV(LinearF32Args a) {                              \
+    linear_f32_mfma<R, WV>(a);                                                          \
+  }
+RXW8_LINEAR_F32(1, 8)
+RXW8_LINEAR_F32(2, 8)
+
 // ---- paired dynamic_update_slice (KvCache::update_at[_checked],
 // crates/rxla-core/src/kv_cache.rs:53-111, indexing.rs:663-678).
 // starts: device I32 [rank]. Unchecked: start_i clamped to [0, dim_i - udim_i].

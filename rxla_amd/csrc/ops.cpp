@@ -93,6 +93,15 @@ struct GenericLinearArgs {
   int y_mode;
 };
 
+struct LinearF32Args {
+  const float *x;
+  const uint8_t *w;
+  const float *scale;
+  float *y;
+  int T, N, K, G;
+  int y_mode;
+};
+
 struct KvUpdateArgs {
   void *kc;
   void *vc;
@@ -391,6 +400,31 @@ static int run_generic_linear(Runtime *rt, const void *x, int x_f32, const void 
   return launch(rt, "rxw8_linear_generic", dim3(grid_for(M * N)), dim3(256), a);
 }
 
+// QuantizedLinear with compute dtype F32 on the matrix cores (x split into
+// bf16 hi + lo parts, exact codes, f32 accumulation): f32 x, row-major U8
+// weights, K and G multiples of 64, 16-byte aligned operands and the staged
+// rows of x within the LDS limit. Returns UNIMPLEMENTED otherwise.
+static int run_linear_f32(Runtime *rt, const float *x, const uint8_t *w, const float *scale,
+                          float *y, int64_t M, int64_t N, int64_t K, int64_t G, int y_mode) {
+  if (K % 64 != 0 || G % 64 != 0 || K > (1 << 20) || N > (1LL << 30) || M > (1LL << 30) ||
+      ((uintptr_t)x | (uintptr_t)w) % 16 != 0 || env_int("RXW8_FORCE_GENERIC", 0))
+    return RXW8_UNIMPLEMENTED;
+  constexpr int WV = 8;
+  const int64_t ng = K / G;
+  for (int R : {M > 16 ? 2 : 1, 1}) {
+    const size_t lds = (size_t)2 * 16 * R * (K + 8) * 2 + (size_t)16 * WV * ng * 4;
+    if (lds > rt->lds_max) continue;
+    LinearF32Args a{x, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode};
+    const int64_t gy = (M + 16 * R - 1) / (16 * R);
+    if (gy > 65535) return RXW8_UNIMPLEMENTED;
+    char kname[40];
+    std::snprintf(kname, sizeof kname, "rxw8_linear_f32_mfma_r%d_w%d", R, WV);
+    return launch(rt, kname, dim3((unsigned)((N + 16 * WV - 1) / (16 * WV)), (unsigned)gy),
+                  dim3(64 * WV), a, lds);
+  }
+  return RXW8_UNIMPLEMENTED;
+}
+
 // Shared validation of QuantizedLinear operands; fills M, N, K, G.
 static int check_qlinear(const Buffer *x, const Buffer *w, const Buffer *s, int compute,
                          int64_t *M, int64_t *N, int64_t *K, int64_t *G) {
@@ -564,6 +598,10 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
                   "packed W8 weights need BF16 compute and a GEMV tiling for N=%lld K=%lld G=%lld",
                   (long long)N, (long long)K, (long long)G);
     return rc;
+  }
+  if (!compute_bf16 && x_f32 && y_f32) {
+    int rc = run_linear_f32(rt, (const float *)x, w, s, (float *)y, M, N, K, G, y_mode);
+    if (rc != RXW8_UNIMPLEMENTED) return rc;
   }
   const bool mfma_ok = compute_bf16 && K % 64 == 0 && N % 16 == 0 && (G == K || G % 64 == 0) &&
                        K <= (1LL << 30) && N <= (1LL << 30) && !env_int("RXW8_FORCE_GENERIC", 0);

@@ -92,6 +92,40 @@ def test_f32_compute_path(rt):
     assert rel_err(y, ref) < 1e-5
 
 
+@pytest.mark.parametrize("m,n,k,g", [(1, 1000, 1024, 128), (16, 4096, 1024, 128),
+                                     (33, 777, 512, 64), (100, 256, 2048, 2048),
+                                     (5, 96, 4096, 4096)])
+def test_f32_compute_matrix_core_path(rt, m, n, k, g):
+    """F32 compute on the matrix cores: x as bf16 hi + lo parts (16 significant
+    bits), exact codes, f32 accumulation; channel and row tails included."""
+    rng = np.random.default_rng(m * 7 + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    u8, s = quantized(rng, n, k, g)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_F32, oracle.ACCUM_F64)
+    y = run_linear(rt, x, u8, s, compute=rx().DType.F32)
+    err = rel_err(y, ref)
+    print(f"F32 compute m={m} n={n} k={k} g={g} rel_err={err:.3e}")
+    assert err < 1e-5
+
+
+def test_f32_compute_exact_on_integer_inputs(rt):
+    """One-hot / small-integer x with unit scales: every product and sum is
+    exact in f32, so the matrix-core F32 path must reproduce it bit for bit
+    (every code 0..255 -> -128..127, and lo parts of integers are zero)."""
+    k = np.arange(1024)
+    codes = ((k[None, :] + 4 * np.arange(160)[:, None]) % 256).astype(np.uint8)  # [160, 1024]
+    s = np.ones((160, 8), np.float32)
+    x = np.zeros((20, 1024), np.float32)
+    for r in range(4):
+        x[r, r] = 1.0
+    x[4:] = np.random.default_rng(3).integers(-3, 4, (16, 1024))
+    x[5] = 0.0
+    x[5, 7], x[5, 9] = 1.0 + 2.0 ** -12, 2.0  # 1 + 2^-12 is not a bf16: needs the lo part
+    want = (x.astype(np.float64) @ (codes.astype(np.float64) - 128).T).astype(np.float32)
+    y = run_linear(rt, x, codes, s, compute=rx().DType.F32)
+    np.testing.assert_array_equal(y, want)
+
+
 def test_rank3_input_and_empty_batch(rt):
     r = rx()
     rng = np.random.default_rng(4)
