@@ -148,6 +148,171 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
   }
 }
 
+// ---- causal full-sequence attention in f32 on the matrix cores
+// (layers.rs:78-92: softmax(q k^T * scale + causal mask) v over positions
+// 0..S-1 of each sequence, GQA head h reading kv head h / G). q, k and v are
+// f32 (v holds bf16 values); v_mfma_f32_16x16x4_f32 multiplies f32 operands
+// and accumulates in f32, and the softmax is the online (flash) form in f32.
+//
+// Workgroup: 4 waves for one (sequence, kv head, query tile); wave w takes
+// query head kv * G + w % G and the 16 queries of sub-tile w / G (4 / G
+// sub-tiles, G in {1, 2, 4}), keeping its q rows (16 x D) and its output rows
+// in registers. Keys go in tiles of 16 through LDS (K and V, f32, rows padded
+// by 4 floats), double-buffered: the next tile's global loads are in flight
+// while the current one is used. Per tile a wave forms S = q k^T (D / 4
+// MFMAs; lane l holds q[l % 16][D/4 * (l / 16) + c] and k[l % 16][same]),
+// masks and rescales with the row max / sum over the 16 lanes of a DPP row,
+// stores P (16 x 16) to its own LDS slice and accumulates O += P V (4 MFMAs
+// per 16 output columns; key 4 (l / 16) + c of the tile for lane l).
+struct Q35AttnArgs {
+  const float *q;        // [T, Hq, D], token t = b * S + i
+  const float *kc, *vc;  // [B, Hkv, Lmax, D]
+  float *out;            // [T, Hq * D]
+  int S, Hq, Hkv, Lmax, qtiles;
+  float scale;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_rot(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_rot<0x128>(v));
+  v = fmaxf(v, dpp_rot<0x124>(v));
+  v = fmaxf(v, dpp_rot<0x4e>(v));
+  return fmaxf(v, dpp_rot<0xb1>(v));
+}
+__device__ __forceinline__ float row_add16(float v) {
+  v += dpp_rot<0x128>(v);
+  v += dpp_rot<0x124>(v);
+  v += dpp_rot<0x4e>(v);
+  return v + dpp_rot<0xb1>(v);
+}
+
+template <int D>
+__device__ void q35_attention(const Q35AttnArgs &a) {
+  constexpr int DC = D / 4, DT = D / 16, KS = D + 4, PS = 20;
+  constexpr int TILE = 16 * KS;                  // floats of one K (or V) tile
+  constexpr int LD = 2 * 16 * D / 4 / 256;       // float4 loads per thread per tile (K and V)
+  extern __shared__ __attribute__((aligned(16))) float attn_lds[];
+  float *plds = attn_lds + 4 * TILE;             // [4 waves][16 q][PS]
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int j = lane >> 4, col = lane & 15;
+  const int G = a.Hq / a.Hkv, sub = 4 / G;
+  int blk = blockIdx.x;
+  const int qt = a.qtiles - 1 - blk % a.qtiles;  // longest tiles first
+  blk /= a.qtiles;
+  const int hk = blk % a.Hkv, b = blk / a.Hkv;
+  const int h = hk * G + wv % G;
+  const int q0 = (qt * sub + wv / G) * 16;
+  const int last_q = min(a.S, (qt + 1) * sub * 16) - 1;
+  const int ntiles = last_q / 16 + 1;
+  const float *kbase = a.kc + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
+  const float *vbase = a.vc + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
+  // q rows of this wave (clamped to S - 1 for loads; rows >= S are not stored)
+  float qreg[DC];
+  {
+    const int qi = min(q0 + col, a.S - 1);
+    const float *qp = a.q + (((int64_t)b * a.S + qi) * a.Hq + h) * D + DC * j;
+#pragma unroll
+    for (int c = 0; c < DC; c += 4) {
+      const float4 v = *(const float4 *)(qp + c);
+      qreg[c] = v.x, qreg[c + 1] = v.y, qreg[c + 2] = v.z, qreg[c + 3] = v.w;
+    }
+  }
+  float4 stage[LD];
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int r = 0; r < LD; ++r) {
+      const int f = threadIdx.x + 256 * r;     // float4 index in [K tile | V tile]
+      const int kv = f / (16 * D / 4), g = f - kv * (16 * D / 4);
+      const int key = min(16 * t + g / (D / 4), a.S - 1), d4 = g % (D / 4);
+      stage[r] = *(const float4 *)((kv ? vbase : kbase) + (int64_t)key * D + 4 * d4);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < LD; ++r) {
+      const int f = threadIdx.x + 256 * r;
+      const int kv = f / (16 * D / 4), g = f - kv * (16 * D / 4);
+      const int key = g / (D / 4), d4 = g % (D / 4);
+      *(float4 *)(attn_lds + (2 * buf + kv) * TILE + key * KS + 4 * d4) = stage[r];
+    }
+  };
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m[i] = -__builtin_huge_valf(), l[i] = 0.f;
+  float *pw = plds + wv * 16 * PS;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load_tile(t + 1);
+    if (16 * t <= q0 + 15) {  // some key of the tile is visible to this wave's queries
+      const float *kt = attn_lds + (2 * buf) * TILE + col * KS + DC * j;
+      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < DC; c += 4) {
+        const float4 kk = *(const float4 *)(kt + c);
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c], kk.x, sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 1], kk.y, sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 2], kk.z, sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 3], kk.w, sc, 0, 0, 0);
+      }
+      const int key = 16 * t + col;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qpos = q0 + 4 * j + i;
+        const float s_ = key <= qpos ? sc[i] * a.scale : -__builtin_huge_valf();
+        const float mn = fmaxf(m[i], row_max16(s_));
+        const float alpha = __expf(m[i] - mn);
+        const float pv = __expf(s_ - mn);
+        l[i] = l[i] * alpha + row_add16(pv);
+        m[i] = mn;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt][i] *= alpha;
+        pw[(4 * j + i) * PS + col] = pv;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float4 pa = *(const float4 *)(pw + col * PS + 4 * j);
+      const float *vt = attn_lds + (2 * buf + 1) * TILE + 4 * j * KS + col;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.x, vt[0 * KS + 16 * dt], o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.y, vt[1 * KS + 16 * dt], o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.z, vt[2 * KS + 16 * dt], o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.w, vt[3 * KS + 16 * dt], o[dt], 0, 0, 0);
+      }
+    }
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int qpos = q0 + 4 * j + i;
+    if (qpos < a.S) {
+      const float inv = 1.0f / l[i];
+      float *op = a.out + ((int64_t)b * a.S + qpos) * a.Hq * D + (int64_t)h * D + col;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) op[16 * dt] = o[dt][i] * inv;
+    }
+  }
+}
+
+#define RXW8_Q35_ATTN(D)                                                                    \
+  extern "C" __global__ void __launch_bounds__(256) rxw8_q35_attention_d##D(Q35AttnArgs a) { \
+    q35_attention<D>(a);                                                                    \
+  }
+RXW8_Q35_ATTN(64)
+RXW8_Q35_ATTN(128)
+RXW8_Q35_ATTN(256)
+
 // ---- elementwise product (attended * gate, layers.rs:93-94), in place ------
 struct Q35MulArgs {
   float *x;
@@ -296,9 +461,102 @@ __device__ void delta_rule(const Q35DeltaArgs &a) {
   }
 RXW8_Q35_DELTA(8)
 RXW8_Q35_DELTA(16)
-RXW8_Q35_DELTA(32)
-RXW8_Q35_DELTA(64)
-RXW8_Q35_DELTA(128)
+
+// Sum over the 16 lanes of a DPP row, the same bits in every lane (each
+// stage adds a lane's value to a rotation of the row: row_ror 8, row_ror 4,
+// then the quad swaps 2 and 1; addition is commutative, so lanes agree).
+__device__ __forceinline__ float row_sum16(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+  return v;
+}
+
+// The same recurrence with each state column spread over the 16 lanes of a
+// DPP row: lane p of column j keeps S[i][j] for i = E p .. E p + E - 1
+// (E = DL / 16), so a position costs E-wide updates plus two row sums instead
+// of DL-long serial loops, and a (sequence, head) runs on DL / 16 workgroups of
+// 16 columns each (the columns of S evolve independently). The q / k slices,
+// v, beta and g of the next NPF positions are in flight while one is computed.
+template <int DL>
+__device__ void delta_rule_rows(const Q35DeltaArgs &a) {
+  constexpr int E = DL / 16, NPF = 4, GROUPS = DL / 16;
+  const int lane = threadIdx.x & 63, p = lane & 15;
+  const int bh = blockIdx.x / GROUPS, grp = blockIdx.x - bh * GROUPS;
+  const int b = bh / a.Hl, h = bh - b * a.Hl;
+  const int j = grp * 16 + (threadIdx.x >> 4);
+  const int64_t W = (int64_t)a.Hl * DL;
+  struct Vals {
+    float q[E], k[E], v, beta, g;
+  };
+  auto fetch = [&](int pos, Vals &o) {
+    const int64_t row = (int64_t)b * a.S + pos;
+    const float *m = a.mixed + row * 3 * W + (int64_t)h * DL;
+    if constexpr (E % 4 == 0) {
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        const float4 qq = *(const float4 *)(m + E * p + e);
+        const float4 kk = *(const float4 *)(m + W + E * p + e);
+        o.q[e] = qq.x, o.q[e + 1] = qq.y, o.q[e + 2] = qq.z, o.q[e + 3] = qq.w;
+        o.k[e] = kk.x, o.k[e + 1] = kk.y, o.k[e + 2] = kk.z, o.k[e + 3] = kk.w;
+      }
+    } else {
+      static_assert(E == 2, "DL in {32, 64, 128}");
+      const float2 qq = *(const float2 *)(m + E * p);
+      const float2 kk = *(const float2 *)(m + W + E * p);
+      o.q[0] = qq.x, o.q[1] = qq.y;
+      o.k[0] = kk.x, o.k[1] = kk.y;
+    }
+    o.v = m[2 * W + j];
+    o.beta = a.beta[row * a.Hl + h];
+    o.g = a.g[row * a.Hl + h];
+  };
+  float st[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) st[e] = 0.f;
+  auto step = [&](const Vals &c, int pos) {
+    float pp = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      st[e] *= c.g;
+      pp += st[e] * c.k[e];
+    }
+    const float delta = (c.v - row_sum16(pp)) * c.beta;
+    float po = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      st[e] += c.k[e] * delta;
+      po += st[e] * c.q[e];
+    }
+    const float o = row_sum16(po);
+    if (p == 0) a.out[((int64_t)b * a.S + pos) * W + (int64_t)h * DL + j] = o;
+  };
+  Vals buf[NPF];
+#pragma unroll
+  for (int i = 0; i < NPF; ++i) fetch(min(i, a.S - 1), buf[i]);
+  int t0 = 0;
+  for (; t0 + NPF <= a.S; t0 += NPF) {
+#pragma unroll
+    for (int i = 0; i < NPF; ++i) {
+      const Vals cur = buf[i];
+      fetch(min(t0 + i + NPF, a.S - 1), buf[i]);
+      step(cur, t0 + i);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NPF; ++i)
+    if (t0 + i < a.S) step(buf[i], t0 + i);
+}
+
+// 256 threads = 16 columns x 16 lanes; grid B * Hl * DL / 16.
+#define RXW8_Q35_DELTA_ROWS(DL)                                                    \
+  extern "C" __global__ void __launch_bounds__(256) rxw8_q35_delta_rule_d##DL(Q35DeltaArgs a) { \
+    delta_rule_rows<DL>(a);                                                        \
+  }
+RXW8_Q35_DELTA_ROWS(32)
+RXW8_Q35_DELTA_ROWS(64)
+RXW8_Q35_DELTA_ROWS(128)
 
 // ---- F32 LoRA on the tied head (mod.rs:174-195): down = x A^T, then
 // logits += (alpha / rank) * down B^T. One thread per output element.

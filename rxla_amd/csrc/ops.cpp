@@ -588,6 +588,7 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
                    const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
                    int64_t G, int compute_bf16, int y_mode) {
   if (M == 0) return RXW8_OK;
+  if (y_mode == 1) y_f32 = 1;  // the residual y is f32 (row offsets of M chunks use it)
   if (packed) {
     if (compute_bf16 && gemm_eligible(M, N, K, G))
       return run_gemm(rt, x, x_f32, w, true, s, y, y_f32, M, N, K, G, y_mode);

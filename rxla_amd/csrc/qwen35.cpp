@@ -80,6 +80,12 @@ struct Q35FaPrepArgs {
   int T, S, Hq, Hkv, D, rot, Lmax;
   float eps;
 };
+struct Q35AttnArgs {
+  const float *q, *kc, *vc;
+  float *out;
+  int S, Hq, Hkv, Lmax, qtiles;
+  float scale;
+};
 struct Q35MulArgs {
   float *x;
   const float *y;
@@ -316,11 +322,12 @@ int allocate(Qwen35 *m) {
   return RXW8_OK;
 }
 
-// QuantizedLinear with compute dtype BF16 on projection `p` (weight p, scale p + 1).
+// QuantizedLinear with compute dtype BF16 on projection `p` (weight p, scale p + 1):
+// y bf16 [T, N], or (y_mode 1) the f32 residual [T, N] that receives y += result.
 int proj(Qwen35 *m, int p, const void *x, int x_f32, void *y, int y_mode, int64_t T) {
   const Param &w = m->params[(size_t)p];
-  return qlinear_launch(m->rt, x, x_f32, (const uint8_t *)m->ptr(p), false, m->f32(p + 1), y, 0, T,
-                        w.dims[0], w.dims[1], m->G, 1, y_mode);
+  return qlinear_launch(m->rt, x, x_f32, (const uint8_t *)m->ptr(p), false, m->f32(p + 1), y,
+                        y_mode == 1 ? 1 : 0, T, w.dims[0], w.dims[1], m->G, 1, y_mode);
 }
 
 int norm(Qwen35 *m, const float *x, const float *w, void *out, int64_t rows, int64_t L,
@@ -347,7 +354,11 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   Q35DeltaArgs da{m->mixed, m->beta, m->g, m->dout, (int)B, (int)S, (int)m->Hl};
   char kname[40];
   std::snprintf(kname, sizeof kname, "rxw8_q35_delta_rule_d%d", (int)m->Dl);
-  if ((rc = launch(rt, kname, dim3((unsigned)(B * m->Hl)), dim3((unsigned)m->Dl), da))) return rc;
+  // Dl <= 16: one workgroup of Dl threads per (sequence, head), one column per
+  // thread; Dl >= 32: 16 lanes per column, Dl / 16 workgroups of 256 threads
+  const bool rows = m->Dl >= 32;
+  const dim3 grid((unsigned)(B * m->Hl * (rows ? m->Dl / 16 : 1)));
+  if ((rc = launch(rt, kname, grid, dim3(rows ? 256u : (unsigned)m->Dl), da))) return rc;
   // gated RMSNorm over each (token, head) row of Dl: plain weight, times silu(z)
   if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, false, m->zp)))
     return rc;
@@ -366,10 +377,22 @@ int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
                    (int)m->cfg.rotary_dim, (int)m->Smax, m->cfg.eps};
   const int64_t units = T * (m->Hq + m->Hkv);
   if ((rc = launch(rt, "rxw8_q35_fa_prep", dim3((unsigned)((units + 3) / 4)), dim3(256), fa))) return rc;
-  if ((rc = attention_launch(rt, m->q, 1, m->kc, m->vc, 1, m->row_len, m->row_seq, nullptr, 0, 0,
-                             m->att, 1, T, m->Hq, m->Hkv, m->Smax, m->D, 1.0f / sqrtf((float)m->D),
-                             nullptr)))
-    return rc;
+  const float scale = 1.0f / sqrtf((float)m->D);
+  const int64_t G = m->Hq / m->Hkv;
+  if ((m->D == 64 || m->D == 128 || m->D == 256) && 4 % G == 0) {
+    // f32 matrix-core flash attention: 4 waves per (sequence, kv head, query tile)
+    const int64_t qtiles = (S + 16 * (4 / G) - 1) / (16 * (4 / G));
+    Q35AttnArgs at{m->q, m->kc, m->vc, m->att, (int)S, (int)m->Hq, (int)m->Hkv, (int)m->Smax,
+                   (int)qtiles, scale};
+    const size_t lds = (size_t)4 * 16 * (m->D + 4) * 4 + 4 * 16 * 20 * 4;
+    char an[40];
+    std::snprintf(an, sizeof an, "rxw8_q35_attention_d%d", (int)m->D);
+    rc = launch(rt, an, dim3((unsigned)(B * m->Hkv * qtiles)), dim3(256), at, lds);
+  } else {
+    rc = attention_launch(rt, m->q, 1, m->kc, m->vc, 1, m->row_len, m->row_seq, nullptr, 0, 0,
+                          m->att, 1, T, m->Hq, m->Hkv, m->Smax, m->D, scale, nullptr);
+  }
+  if (rc) return rc;
   Q35MulArgs mu{m->att, m->gate, T * m->Hq * m->D};
   if ((rc = launch(rt, "rxw8_q35_mul", dim3(grid_n(T * m->Hq * m->D)), dim3(256), mu))) return rc;
   return proj(m, L.o, m->att, 1, m->h, 1, T);

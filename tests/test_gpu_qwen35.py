@@ -39,8 +39,15 @@ CONFIGS = {
                             linear_heads=16, linear_head_dim=128, rotary_dim=64, group=128),
                  max_batch=1, max_seq=32, std=0.02),
 }
-CONFIGS["wide_linear"] = dict(CONFIGS["wide"], layers=[q35.LINEAR])
-CONFIGS["wide_full"] = dict(CONFIGS["wide"], layers=[q35.FULL])
+# Dl 64, D 128 with one KV head (G = 4), a vocabulary that is not a multiple
+# of the head kernel's 128 channels
+CONFIGS["mid"] = dict(q35.config(vocab=1000, hidden=512, intermediate=1024,
+                                 layers=[q35.LINEAR, q35.LINEAR, q35.FULL], heads=4, kv_heads=1,
+                                 head_dim=128, linear_heads=8, linear_head_dim=64, rotary_dim=32,
+                                 group=128), max_batch=2, max_seq=64, std=0.03)
+CONFIGS["wide_linear"] = dict(CONFIGS["wide"], layers=[q35.LINEAR], max_seq=256)
+CONFIGS["small_mha"] = dict(CONFIGS["small"], kv_heads=4, layers=[q35.FULL, q35.LINEAR])  # G = 1
+CONFIGS["wide_full"] = dict(CONFIGS["wide"], layers=[q35.FULL], max_seq=80)
 
 
 def model_config(cfg):
@@ -70,7 +77,9 @@ def run(rt, m, ids):
 
 
 @pytest.mark.parametrize("name,b,s", [("tiny", 2, 13), ("small", 2, 13), ("small", 2, 70),
-                                      ("small", 1, 1), ("wide_linear", 1, 16),
+                                      ("small", 1, 1), ("mid", 2, 37), ("mid", 1, 64),
+                                      ("small_mha", 2, 45), ("wide_linear", 1, 16),
+                                      ("wide_linear", 1, 203), ("wide_full", 1, 77),
                                       ("wide_full", 1, 16), ("wide", 1, 16), ("wide", 1, 32)])
 def test_logits_match_the_oracle(rt, name, b, s):
     cfg = CONFIGS[name]
