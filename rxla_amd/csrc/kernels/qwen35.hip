@@ -42,13 +42,14 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_embed(Q35EmbedArgs a)
 // ---- RMSNorm over rows of L values (rxla-nn layers.rs:459-495):
 //   y = x * rsqrt(mean(x^2) + eps) * (zero_centered ? 1 + w : w)
 // optionally times silu(z) (the gated output norm, layers.rs:241-259).
-// Row r reads x + r * x_stride, writes out + r * out_stride (bf16 or f32).
+// Row r reads x + r * x_stride, writes out + r * out_stride (bf16 or f32);
+// its gate row is z + (r / z_group) * z_stride + (r % z_group) * L.
 struct Q35NormArgs {
   const float *x;
   const float *w;        // [L]
-  const void *z;         // [rows, L] gate (bf16 or f32) or null
+  const void *z;         // gate rows (bf16 or f32) or null
   void *out;
-  int64_t rows, L, x_stride, out_stride, z_stride;
+  int64_t rows, L, x_stride, out_stride, z_stride, z_group;
   float eps;
   int zero_centered, out_f32, z_f32;
 };
@@ -70,7 +71,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a
     const float w = a.zero_centered ? 1.0f + a.w[i] : a.w[i];
     float y = (x[i] * sc) * w;
     if (a.z) {
-      const float zv = ld(a.z, r * a.z_stride + i, a.z_f32);
+      const float zv = ld(a.z, (r / a.z_group) * a.z_stride + (r % a.z_group) * a.L + i, a.z_f32);
       y *= zv * sigmoid_f32(zv);
     }
     if (a.out_f32)
@@ -87,15 +88,15 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a
 // the token's position. norm: zero-centred RMSNorm over D; RoPE: split-half
 // over the first rot channels with angle pos * freqs[i] (mod.rs:209-229).
 struct Q35FaPrepArgs {
-  const uint16_t *qg;    // [T, Hq * 2D]
-  const uint16_t *kp;    // [T, Hkv * D]
-  const uint16_t *vp;    // [T, Hkv * D]
+  const uint16_t *qg;    // [T, Hq * 2D] rows of `stride` elements
+  const uint16_t *kp;    // [T, Hkv * D] rows of `stride` elements
+  const uint16_t *vp;    // [T, Hkv * D] rows of `stride` elements
   const float *q_norm, *k_norm;  // [D]
   const float *freqs;    // [rot / 2]
   float *q_out;          // [T, Hq, D]
   float *gate_out;       // [T, Hq * D]
   float *kc, *vc;        // [B, Hkv, Lmax, D]
-  int T, S, Hq, Hkv, D, rot, Lmax;
+  int T, S, Hq, Hkv, D, rot, Lmax, stride;
   float eps;
 };
 
@@ -109,8 +110,8 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
   const int bseq = t / a.S, pos = t - bseq * a.S;
   const int D = a.D;
   const bool is_q = h < a.Hq;
-  const uint16_t *src = is_q ? a.qg + ((int64_t)t * a.Hq + h) * 2 * D
-                             : a.kp + ((int64_t)t * a.Hkv + (h - a.Hq)) * D;
+  const uint16_t *src = is_q ? a.qg + (int64_t)t * a.stride + (int64_t)h * 2 * D
+                             : a.kp + (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
   float *row = rowbuf[wv];
   float ss = 0.f;
   for (int i = lane; i < D; i += 64) {
@@ -142,7 +143,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
     for (int i = lane; i < D; i += 64)
       a.gate_out[(int64_t)t * a.Hq * D + (int64_t)h * D + i] = sigmoid_f32(bf16_bits_to_f32(src[D + i]));
   } else {
-    const uint16_t *vs = a.vp + ((int64_t)t * a.Hkv + (h - a.Hq)) * D;
+    const uint16_t *vs = a.vp + (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
     float *vd = a.vc + (((int64_t)bseq * a.Hkv + (h - a.Hq)) * a.Lmax + pos) * D;
     for (int i = lane; i < D; i += 64) vd[i] = bf16_bits_to_f32(vs[i]);
   }
@@ -329,10 +330,10 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_mul(Q35MulArgs a) {
 // ---- causal depthwise conv over each sequence + SiLU (layers.rs:131-146):
 // out[t, c] = silu(sum_j w[c, j] * x[t - (k-1) + j, c]), zero before position 0.
 struct Q35ConvArgs {
-  const uint16_t *x;   // [T, C] bf16 projection
+  const uint16_t *x;   // [T, C] bf16 projection, rows of x_stride elements
   const float *w;      // [C, k]
   float *out;          // [T, C]
-  int64_t T, C;
+  int64_t T, C, x_stride;
   int S, k;
 };
 
@@ -345,7 +346,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_conv_silu(Q35ConvArgs
     float acc = 0.f;
     for (int j = 0; j < a.k; ++j) {
       const int src = pos - (a.k - 1) + j;
-      if (src >= 0) acc += a.w[c * a.k + j] * bf16_bits_to_f32(a.x[(t - pos + src) * a.C + c]);
+      if (src >= 0) acc += a.w[c * a.k + j] * bf16_bits_to_f32(a.x[(t - pos + src) * a.x_stride + c]);
     }
     a.out[e] = acc * sigmoid_f32(acc);
   }
@@ -378,19 +379,20 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_qk_l2norm(Q35L2Args a
 // ---- beta = sigmoid(b); g = exp(softplus(a + dt_bias) * -exp(A_log))
 // (layers.rs:180-195; softplus = max(x, 0) + log1p(exp(-|x|)), ops.rs:256-262)
 struct Q35GateArgs {
-  const uint16_t *b, *a;  // [T, Hl] bf16 projections
+  const uint16_t *b, *a;  // [T, Hl] bf16 projections, rows of `stride` elements
   const float *a_log, *dt_bias;  // [Hl]
   float *beta, *g;        // [T, Hl]
-  int64_t n;
+  int64_t n, stride;
   int Hl;
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_q35_beta_decay(Q35GateArgs p) {
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < p.n;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const int h = (int)(e % p.Hl);
-    p.beta[e] = sigmoid_f32(bf16_bits_to_f32(p.b[e]));
-    const float x = bf16_bits_to_f32(p.a[e]) + p.dt_bias[h];
+    const int64_t t = e / p.Hl;
+    const int h = (int)(e - t * p.Hl);
+    p.beta[e] = sigmoid_f32(bf16_bits_to_f32(p.b[t * p.stride + h]));
+    const float x = bf16_bits_to_f32(p.a[t * p.stride + h]) + p.dt_bias[h];
     const float sp = fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
     p.g[e] = expf(sp * -expf(p.a_log[h]));
   }
@@ -586,13 +588,16 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_lora(Q35LoraArgs a) {
 // ---- SwiGLU of separate gate / up projections (layers.rs:270-293):
 // act = bf16(silu(g) * u) with g, u the bf16 projection outputs.
 struct Q35SiluArgs {
-  const uint16_t *g, *u;
-  uint16_t *act;
-  int64_t n;
+  const uint16_t *g, *u;  // [T, I] rows of `stride` elements
+  uint16_t *act;          // [T, I]
+  int64_t n, I, stride;
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_q35_silu_mul(Q35SiluArgs a) {
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < a.n;
-       e += (int64_t)gridDim.x * blockDim.x)
-    a.act[e] = f32_to_bf16_bits(silu_mul_f32(bf16_bits_to_f32(a.g[e]), bf16_bits_to_f32(a.u[e])));
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = e / a.I, c = e - t * a.I;
+    a.act[e] = f32_to_bf16_bits(silu_mul_f32(bf16_bits_to_f32(a.g[t * a.stride + c]),
+                                             bf16_bits_to_f32(a.u[t * a.stride + c])));
+  }
 }

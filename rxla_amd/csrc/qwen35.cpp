@@ -69,7 +69,7 @@ struct Q35NormArgs {
   const float *w;
   const void *z;
   void *out;
-  int64_t rows, L, x_stride, out_stride, z_stride;
+  int64_t rows, L, x_stride, out_stride, z_stride, z_group;
   float eps;
   int zero_centered, out_f32, z_f32;
 };
@@ -77,7 +77,7 @@ struct Q35FaPrepArgs {
   const uint16_t *qg, *kp, *vp;
   const float *q_norm, *k_norm, *freqs;
   float *q_out, *gate_out, *kc, *vc;
-  int T, S, Hq, Hkv, D, rot, Lmax;
+  int T, S, Hq, Hkv, D, rot, Lmax, stride;
   float eps;
 };
 struct Q35AttnArgs {
@@ -95,7 +95,7 @@ struct Q35ConvArgs {
   const uint16_t *x;
   const float *w;
   float *out;
-  int64_t T, C;
+  int64_t T, C, x_stride;
   int S, k;
 };
 struct Q35L2Args {
@@ -108,7 +108,7 @@ struct Q35GateArgs {
   const uint16_t *b, *a;
   const float *a_log, *dt_bias;
   float *beta, *g;
-  int64_t n;
+  int64_t n, stride;
   int Hl;
 };
 struct Q35DeltaArgs {
@@ -119,7 +119,7 @@ struct Q35DeltaArgs {
 struct Q35SiluArgs {
   const uint16_t *g, *u;
   uint16_t *act;
-  int64_t n;
+  int64_t n, I, stride;
 };
 struct Q35LoraArgs {
   const float *x;   // [T, K]
@@ -151,6 +151,11 @@ struct Layer {
   int qkv = -1, conv = -1, z = -1, b = -1, a = -1, a_log = -1, dt_bias = -1, lnorm = -1, out = -1;
   int q = -1, k = -1, v = -1, qn = -1, kn = -1, o = -1;
   int gate = -1, up = -1, down = -1;  // a projection's index is its weight; scale = index + 1
+  // fused input projections (copied at bind time): linear layers [qkv; z; b; a],
+  // full layers [q; k; v], the MLP [gate; up]; rows padded to a multiple of 128
+  uint8_t *in_w = nullptr, *gu_w = nullptr;
+  float *in_s = nullptr, *gu_s = nullptr;
+  int64_t n_in = 0, n_gu = 0;
 };
 
 }  // namespace
@@ -165,20 +170,24 @@ struct Qwen35 {
   std::vector<Layer> layers;
   int embed = -1, final_norm = -1, lora_a = -1, lora_b = -1;
   bool any_full = false, any_linear = false;
-  // device memory: one block for activations, caches and constants
+  // device memory: one block for activations, caches and constants; one for
+  // the fused projection weights (built when the last parameter is bound)
   void *block = nullptr;
+  void *fused = nullptr;
+  int64_t n_in_max = 0;
   float *freqs = nullptr;
   int32_t *zero_lens = nullptr, *pos = nullptr, *row_seq = nullptr, *row_len = nullptr;
   float *h = nullptr, *fin = nullptr, *lora_mid = nullptr;
   uint16_t *xn = nullptr;
+  // fused input projection output [T, n_in] (either layer kind)
+  uint16_t *raw = nullptr;
   // linear layers
-  uint16_t *raw = nullptr, *zp = nullptr, *bp = nullptr, *ap = nullptr, *gated = nullptr;
+  uint16_t *gated = nullptr;
   float *mixed = nullptr, *beta = nullptr, *g = nullptr, *dout = nullptr;
   // full layers
-  uint16_t *qg = nullptr, *kp = nullptr, *vp = nullptr;
   float *q = nullptr, *gate = nullptr, *att = nullptr, *kc = nullptr, *vc = nullptr;
-  // MLP
-  uint16_t *gp = nullptr, *upp = nullptr, *act = nullptr;
+  // MLP: [gate | up] projection [T, 2I], SwiGLU output [T, I]
+  uint16_t *gu = nullptr, *act = nullptr;
 
   void *ptr(int i) const { return params[(size_t)i].bound->ptr; }
   const float *f32(int i) const { return (const float *)ptr(i); }
@@ -244,6 +253,12 @@ void build_schema(Qwen35 *m) {
     L.down = add_proj(m, pre + "mlp.down_proj", m->H, m->I);
   }
   m->final_norm = add_param(m, root + "norm.weight", RXW8_F32, m->H);
+  auto pad128 = [](int64_t n) { return (n + 127) / 128 * 128; };
+  for (Layer &L : m->layers) {
+    L.n_in = pad128(L.full ? 2 * m->Hq * m->D + 2 * m->Hkv * m->D : 4 * m->W + 2 * m->Hl);
+    L.n_gu = pad128(2 * m->I);
+    m->n_in_max = std::max(m->n_in_max, L.n_in);
+  }
 }
 
 // Carve the device block: [offset, bytes] pairs, 256-byte aligned.
@@ -280,29 +295,22 @@ int allocate(Qwen35 *m) {
   c.add(&m->fin, T * m->H);
   c.add(&m->xn, T * m->H);
   if (m->cfg.lora_rank > 0) c.add(&m->lora_mid, T * m->cfg.lora_rank);
+  c.add(&m->raw, T * m->n_in_max);
   if (m->any_linear) {
-    c.add(&m->raw, T * 3 * m->W);
     c.add(&m->mixed, T * 3 * m->W);
-    c.add(&m->zp, T * m->W);
-    c.add(&m->bp, T * m->Hl);
-    c.add(&m->ap, T * m->Hl);
     c.add(&m->beta, T * m->Hl);
     c.add(&m->g, T * m->Hl);
     c.add(&m->dout, T * m->W);
     c.add(&m->gated, T * m->W);
   }
   if (m->any_full) {
-    c.add(&m->qg, T * 2 * m->Hq * m->D);
-    c.add(&m->kp, T * m->Hkv * m->D);
-    c.add(&m->vp, T * m->Hkv * m->D);
     c.add(&m->q, T * m->Hq * m->D);
     c.add(&m->gate, T * m->Hq * m->D);
     c.add(&m->att, T * m->Hq * m->D);
     c.add(&m->kc, m->Bmax * m->Hkv * m->Smax * m->D);
     c.add(&m->vc, m->Bmax * m->Hkv * m->Smax * m->D);
   }
-  c.add(&m->gp, T * m->I);
-  c.add(&m->upp, T * m->I);
+  c.add(&m->gu, T * 2 * m->I);
   c.add(&m->act, T * m->I);
   const size_t bytes = c.total();
   hipError_t e = hipMalloc(&m->block, bytes);
@@ -330,9 +338,17 @@ int proj(Qwen35 *m, int p, const void *x, int x_f32, void *y, int y_mode, int64_
                         y_mode == 1 ? 1 : 0, T, w.dims[0], w.dims[1], m->G, 1, y_mode);
 }
 
+// The same on a fused weight of n rows.
+int proj_fused(Qwen35 *m, const uint8_t *w, const float *sc, int64_t n, const void *x, void *y,
+               int64_t T) {
+  return qlinear_launch(m->rt, x, 0, w, false, sc, y, 0, T, n, m->H, m->G, 1, 0);
+}
+
 int norm(Qwen35 *m, const float *x, const float *w, void *out, int64_t rows, int64_t L,
-         bool zero_centered, bool out_f32, const void *z = nullptr) {
-  Q35NormArgs a{x, w, z, out, rows, L, L, L, L, m->cfg.eps, zero_centered ? 1 : 0, out_f32 ? 1 : 0, 0};
+         bool zero_centered, bool out_f32, const void *z = nullptr, int64_t z_stride = 0,
+         int64_t z_group = 1) {
+  Q35NormArgs a{x, w, z, out, rows, L, L, L, z_stride, z_group, m->cfg.eps, zero_centered ? 1 : 0,
+                out_f32 ? 1 : 0, 0};
   return launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)rows), dim3(256), a);
 }
 
@@ -340,16 +356,17 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   Runtime *rt = m->rt;
   const int64_t T = B * S;
   int rc;
-  if ((rc = proj(m, L.qkv, m->xn, 0, m->raw, 0, T))) return rc;
-  Q35ConvArgs cv{m->raw, m->f32(L.conv), m->mixed, T, 3 * m->W, (int)S, (int)m->cfg.conv_kernel};
+  // raw = xn [qkv; z; b; a]^T: columns [0, 3W) mixed, [3W, 4W) z, then b, a
+  if ((rc = proj_fused(m, L.in_w, L.in_s, L.n_in, m->xn, m->raw, T))) return rc;
+  const uint16_t *zp = m->raw + 3 * m->W, *bp = m->raw + 4 * m->W, *ap = bp + m->Hl;
+  Q35ConvArgs cv{m->raw, m->f32(L.conv), m->mixed, T, 3 * m->W, L.n_in, (int)S,
+                 (int)m->cfg.conv_kernel};
   if ((rc = launch(rt, "rxw8_q35_conv_silu", dim3(grid_n(T * 3 * m->W)), dim3(256), cv))) return rc;
   Q35L2Args l2{m->mixed, T, (int)m->Hl, (int)m->Dl, 1.0f / sqrtf((float)m->Dl)};
   if ((rc = launch(rt, "rxw8_q35_qk_l2norm", dim3((unsigned)((T * 2 * m->Hl + 3) / 4)), dim3(256), l2)))
     return rc;
-  if ((rc = proj(m, L.z, m->xn, 0, m->zp, 0, T))) return rc;
-  if ((rc = proj(m, L.b, m->xn, 0, m->bp, 0, T))) return rc;
-  if ((rc = proj(m, L.a, m->xn, 0, m->ap, 0, T))) return rc;
-  Q35GateArgs ga{m->bp, m->ap, m->f32(L.a_log), m->f32(L.dt_bias), m->beta, m->g, T * m->Hl, (int)m->Hl};
+  Q35GateArgs ga{bp, ap, m->f32(L.a_log), m->f32(L.dt_bias), m->beta, m->g, T * m->Hl, L.n_in,
+                 (int)m->Hl};
   if ((rc = launch(rt, "rxw8_q35_beta_decay", dim3(grid_n(T * m->Hl)), dim3(256), ga))) return rc;
   Q35DeltaArgs da{m->mixed, m->beta, m->g, m->dout, (int)B, (int)S, (int)m->Hl};
   char kname[40];
@@ -360,7 +377,9 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   const dim3 grid((unsigned)(B * m->Hl * (rows ? m->Dl / 16 : 1)));
   if ((rc = launch(rt, kname, grid, dim3(rows ? 256u : (unsigned)m->Dl), da))) return rc;
   // gated RMSNorm over each (token, head) row of Dl: plain weight, times silu(z)
-  if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, false, m->zp)))
+  // row r = (t, head): z of token t at raw + t * n_in + head * Dl
+  if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, false, zp, L.n_in,
+                 m->Hl)))
     return rc;
   return proj(m, L.out, m->gated, 0, m->h, 1, T);
 }
@@ -369,12 +388,12 @@ int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   Runtime *rt = m->rt;
   const int64_t T = B * S;
   int rc;
-  if ((rc = proj(m, L.q, m->xn, 0, m->qg, 0, T))) return rc;
-  if ((rc = proj(m, L.k, m->xn, 0, m->kp, 0, T))) return rc;
-  if ((rc = proj(m, L.v, m->xn, 0, m->vp, 0, T))) return rc;
-  Q35FaPrepArgs fa{m->qg, m->kp, m->vp, m->f32(L.qn), m->f32(L.kn), m->freqs, m->q, m->gate,
+  // raw = xn [q; k; v]^T
+  if ((rc = proj_fused(m, L.in_w, L.in_s, L.n_in, m->xn, m->raw, T))) return rc;
+  const uint16_t *kp = m->raw + 2 * m->Hq * m->D, *vp = kp + m->Hkv * m->D;
+  Q35FaPrepArgs fa{m->raw, kp, vp, m->f32(L.qn), m->f32(L.kn), m->freqs, m->q, m->gate,
                    m->kc, m->vc, (int)T, (int)S, (int)m->Hq, (int)m->Hkv, (int)m->D,
-                   (int)m->cfg.rotary_dim, (int)m->Smax, m->cfg.eps};
+                   (int)m->cfg.rotary_dim, (int)m->Smax, (int)L.n_in, m->cfg.eps};
   const int64_t units = T * (m->Hq + m->Hkv);
   if ((rc = launch(rt, "rxw8_q35_fa_prep", dim3((unsigned)((units + 3) / 4)), dim3(256), fa))) return rc;
   const float scale = 1.0f / sqrtf((float)m->D);
@@ -410,9 +429,8 @@ int enqueue_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int
     if ((rc = norm(m, m->h, m->f32(L.in_norm), m->xn, T, m->H, true, false))) return rc;
     if ((rc = L.full ? full_mixer(m, L, B, S) : linear_mixer(m, L, B, S))) return rc;
     if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, false))) return rc;
-    if ((rc = proj(m, L.gate, m->xn, 0, m->gp, 0, T))) return rc;
-    if ((rc = proj(m, L.up, m->xn, 0, m->upp, 0, T))) return rc;
-    Q35SiluArgs sa{m->gp, m->upp, m->act, T * m->I};
+    if ((rc = proj_fused(m, L.gu_w, L.gu_s, L.n_gu, m->xn, m->gu, T))) return rc;
+    Q35SiluArgs sa{m->gu, m->gu + m->I, m->act, T * m->I, m->I, L.n_gu};
     if ((rc = launch(rt, "rxw8_q35_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
     if ((rc = proj(m, L.down, m->act, 0, m->h, 1, T))) return rc;
   }
@@ -432,12 +450,60 @@ int enqueue_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int
   return RXW8_OK;
 }
 
-void free_model(Qwen35 *m) {
-  if (m->block) {
-    (void)hipStreamSynchronize(m->rt->stream);
-    (void)hipFree(m->block);
-    m->block = nullptr;
+// Fused input projections: the rows of each part copied one after another
+// (row-major U8 [n, H] and F32 scales [n, H / G] stack along dim 0), padded
+// with codes 128 and scales 0 (rows of zeros) to n_in / n_gu rows.
+int prepare(Qwen35 *m) {
+  Runtime *rt = m->rt;
+  const int64_t ng = m->H / m->G;
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  size_t total = 0;
+  for (const Layer &L : m->layers)
+    total += al((size_t)L.n_in * m->H) + al((size_t)L.n_in * ng * 4) + al((size_t)L.n_gu * m->H) +
+             al((size_t)L.n_gu * ng * 4);
+  hipError_t e = hipMalloc(&m->fused, total);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    m->fused = nullptr;
+    return fail(RXW8_RESOURCE_EXHAUSTED, "qwen35: cannot allocate %zu bytes of fused weights", total);
   }
+  char *p = (char *)m->fused;
+  auto stack = [&](const std::vector<int> &parts, int64_t n, uint8_t **w, float **sc) -> int {
+    *w = (uint8_t *)p;
+    p += al((size_t)n * m->H);
+    *sc = (float *)p;
+    p += al((size_t)n * ng * 4);
+    int64_t row = 0;
+    for (int i : parts) {
+      const int64_t rows = m->params[(size_t)i].dims[0];
+      RXW8_HIP(hipMemcpyAsync(*w + row * m->H, m->ptr(i), (size_t)rows * m->H,
+                              hipMemcpyDeviceToDevice, rt->stream));
+      RXW8_HIP(hipMemcpyAsync(*sc + row * ng, m->ptr(i + 1), (size_t)rows * ng * 4,
+                              hipMemcpyDeviceToDevice, rt->stream));
+      row += rows;
+    }
+    if (row < n) {
+      RXW8_HIP(hipMemsetAsync(*w + row * m->H, 128, (size_t)(n - row) * m->H, rt->stream));
+      RXW8_HIP(hipMemsetAsync(*sc + row * ng, 0, (size_t)(n - row) * ng * 4, rt->stream));
+    }
+    return RXW8_OK;
+  };
+  int rc;
+  for (Layer &L : m->layers) {
+    const std::vector<int> in = L.full ? std::vector<int>{L.q, L.k, L.v}
+                                       : std::vector<int>{L.qkv, L.z, L.b, L.a};
+    if ((rc = stack(in, L.n_in, &L.in_w, &L.in_s))) return rc;
+    if ((rc = stack({L.gate, L.up}, L.n_gu, &L.gu_w, &L.gu_s))) return rc;
+  }
+  RXW8_HIP(hipStreamSynchronize(rt->stream));
+  return RXW8_OK;
+}
+
+void free_model(Qwen35 *m) {
+  if (m->block || m->fused) (void)hipStreamSynchronize(m->rt->stream);
+  if (m->block) (void)hipFree(m->block);
+  if (m->fused) (void)hipFree(m->fused);
+  m->block = m->fused = nullptr;
   for (Param &p : m->params)
     if (p.bound) rxw8_buffer_release(static_cast<rxw8_buffer *>(p.bound));
 }
@@ -567,7 +633,11 @@ int rxw8_qwen35_bind_parameter(rxw8_qwen35 *m, const char *path, rxw8_buffer *bu
                 path, dtype_name(buf->dtype), dtype_name(p.dtype));
   rxw8_buffer_retain(buf);
   p.bound = buf;
-  return RXW8_OK;
+  // once the last parameter is bound, copy the fused projection weights
+  for (const Param &q : m->params)
+    if (!q.bound) return RXW8_OK;
+  std::lock_guard<std::recursive_mutex> g(m->rt->mu);
+  return m->fused ? (int)RXW8_OK : prepare(m);
 }
 
 int rxw8_qwen35_forward(rxw8_qwen35 *m, rxw8_buffer *ids, rxw8_buffer *logits) {
@@ -589,6 +659,10 @@ int rxw8_qwen35_forward(rxw8_qwen35 *m, rxw8_buffer *ids, rxw8_buffer *logits) {
   for (const Param &p : m->params)
     if (!p.bound) return fail(RXW8_FAILED_PRECONDITION, "missing parameter binding \"%s\"", p.path.c_str());
   std::lock_guard<std::recursive_mutex> g(m->rt->mu);
+  if (!m->fused) {
+    const int rc = prepare(m);
+    if (rc) return rc;
+  }
   return enqueue_forward(m, (const int32_t *)ids->ptr, (float *)logits->ptr, B, S);
 }
 
