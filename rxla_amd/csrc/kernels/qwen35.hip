@@ -19,24 +19,31 @@ __device__ __forceinline__ float ld(const void *p, int64_t i, int f32) {
 }  // namespace
 
 // ---- W8 embedding: h[t, c] = (f32(u8[id, c]) - 128) * scale[id, c / G], ids
-// clamped to [0, V - 1] (mod.rs:158-179, indexing.rs:637-656) -------------------
+// clamped to [0, V - 1] (mod.rs:134-157, indexing.rs:637-656); one workgroup
+// per token, which also writes the row's sum of squares (ss, optional) for the
+// RMSNorm prologue of the first projection.
 struct Q35EmbedArgs {
   const int32_t *ids;
   const uint8_t *w;     // [V, H]
   const float *scale;   // [V, H / G]
   float *h;             // [T, H]
+  float *ss;            // [T] or null
   int64_t T, V, H, G;
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_q35_embed(Q35EmbedArgs a) {
-  const int64_t n = a.T * a.H;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = e / a.H, c = e - t * a.H;
-    int64_t id = a.ids[t];
-    id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
-    a.h[e] = ((float)a.w[id * a.H + c] + -128.0f) * a.scale[id * (a.H / a.G) + c / a.G];
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x;
+  int64_t id = a.ids[t];
+  id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
+  float ss = 0.f;
+  for (int64_t c = threadIdx.x; c < a.H; c += blockDim.x) {
+    const float v = ((float)a.w[id * a.H + c] + -128.0f) * a.scale[id * (a.H / a.G) + c / a.G];
+    a.h[t * a.H + c] = v;
+    ss += v * v;
   }
+  ss = block_sum_256(ss, red);
+  if (a.ss && threadIdx.x == 0) a.ss[t] = ss;
 }
 
 // ---- RMSNorm over rows of L values (rxla-nn layers.rs:459-495):
@@ -313,6 +320,19 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
 RXW8_Q35_ATTN(64)
 RXW8_Q35_ATTN(128)
 RXW8_Q35_ATTN(256)
+
+// ---- 1 + w of a zero-centred norm weight (layers.rs(nn):476-491), stored once
+// for the GEMV's RMSNorm prologue (which multiplies by the weight as given)
+struct Q35ShiftArgs {
+  const float *w;
+  float *out;
+  int64_t n;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_one_plus(Q35ShiftArgs a) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < a.n) a.out[e] = 1.0f + a.w[e];
+}
 
 // ---- elementwise product (attended * gate, layers.rs:93-94), in place ------
 struct Q35MulArgs {

@@ -480,7 +480,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(Splitk
   RXW8_GEMV(KIND, MB, RW, 4)      \
   RXW8_GEMV(KIND, MB, RW, 2)      \
   RXW8_GEMV(KIND, MB, RW, 1)
-// Wide variants: 8, 12 or 16 waves per workgroup = RW row groups x NW/RW k
+// Wide variants: 8, 12, 14 or 16 waves per workgroup = RW row groups x NW/RW k
 // slices (12 waves: 3 row groups of 4, e.g. N = 12288 in 256 workgroups).
 #define RXW8_GEMV_WIDE(MB, RW, U, NW)                                           \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
@@ -506,6 +506,9 @@ RXW8_GEMV_WIDE_RW(2, 8)
 RXW8_GEMV_WIDE_RW(2, 16)
 RXW8_GEMV_WIDE_U(1, 3, 12)
 RXW8_GEMV_WIDE_U(2, 3, 12)
+// 14 waves over K (K = 14 x 256, e.g. 3584) for narrow N in one launch
+RXW8_GEMV_WIDE_U(1, 1, 14)
+RXW8_GEMV_WIDE_U(2, 1, 14)
 
 #define RXW8_GEMV_ALL(KIND) \
   RXW8_GEMV_U(KIND, 1, 1)   \

@@ -204,7 +204,7 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
   p.rw = forced_rw == 1 || forced_rw == 4 ? forced_rw : (m <= 4 || prefer_ks1 ? 1 : 4);
   const int64_t slice = w_bf16 ? 32 : 64;  // k per 16-byte lane load
   const bool per_channel = g == k;
-  // A single launch without a split-K reduce: 16, 12 or 8 waves per
+  // A single launch without a split-K reduce: 16, 14, 12 or 8 waves per
   // workgroup split K inside the workgroup when each wave still gets an even
   // number of 64-k slices (u8 weights, rw groups of 16 rows per workgroup).
   // Wider row tiles cut the staging each workgroup does per weight byte. First
@@ -214,7 +214,7 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
   // divides the wave's slices into A/B groups.
   if (prefer_ks1 && allow_wide && !w_bf16 && forced_rw == 0) {
     const int forced_nw = env_int("RXW8_GEMV_NW", 0);
-    static const int shapes[][2] = {{16, 4}, {12, 3}, {16, 2}, {16, 1}, {8, 4}, {8, 2}, {8, 1}};
+    static const int shapes[][2] = {{16, 4}, {12, 3}, {16, 2}, {16, 1}, {14, 1}, {8, 4}, {8, 2}, {8, 1}};
     for (int pass = 0; pass < 2; ++pass) {
       for (const auto &sh : shapes) {
         const int nw = sh[0], rw = sh[1];
@@ -238,6 +238,15 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
         return p;
       }
     }
+  }
+  // 4-wave plans: rw = 1 splits K over the 4 waves, so K per split must hold
+  // 4 waves x an even number of slices; narrow K (e.g. 256) falls back to
+  // rw = 4 (one wave per 16-row group, the whole split each)
+  if (forced_rw == 0 && p.rw == 1) {
+    bool any = false;
+    for (int ks = 1; ks <= 64 && !any; ++ks)
+      any = k % ks == 0 && (k / ks) % 4 == 0 && (k / ks / 4) % (2 * slice) == 0;
+    if (!any) p.rw = 4;
   }
   const int kw = 4 / p.rw;
   const int64_t tiles = (n + 16 * p.rw - 1) / (16 * p.rw);

@@ -31,6 +31,7 @@
 //   P norm.weight F32 [H]
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -43,6 +44,7 @@ namespace rxw8 {
 int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool packed,
                    const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
                    int64_t G, int compute_bf16, int y_mode);
+bool gemm_eligible(int64_t M, int64_t N, int64_t K, int64_t G);
 int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
                      int cache_f32, const int32_t *lens, const int32_t *row_seq,
                      const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
@@ -62,6 +64,7 @@ struct Q35EmbedArgs {
   const uint8_t *w;
   const float *scale;
   float *h;
+  float *ss;
   int64_t T, V, H, G;
 };
 struct Q35NormArgs {
@@ -121,6 +124,30 @@ struct Q35SiluArgs {
   uint16_t *act;
   int64_t n, I, stride;
 };
+struct PackArgs {
+  const void *src;
+  void *dst;
+  int64_t n, k;
+  int kb;
+  int esize;
+  int64_t ilv_half;
+};
+struct InterleaveArgs {
+  const float *src;
+  float *dst;
+  int64_t half, cols;
+};
+struct SiluMulArgs {
+  const uint16_t *gu;
+  uint16_t *act;
+  int64_t T, I;
+  int interleaved;
+};
+struct Q35ShiftArgs {
+  const float *w;
+  float *out;
+  int64_t n;
+};
 struct Q35LoraArgs {
   const float *x;   // [T, K]
   const float *w;   // [N, K]
@@ -156,6 +183,11 @@ struct Layer {
   uint8_t *in_w = nullptr, *gu_w = nullptr;
   float *in_s = nullptr, *gu_s = nullptr;
   int64_t n_in = 0, n_gu = 0;
+  // packed mode: every projection weight in the GEMV tile layout (gate|up
+  // rows in SwiGLU order, its scales likewise), the residual projections'
+  // packed copies, and the zero-centred norm weights as 1 + w
+  uint8_t *out_pk = nullptr, *down_pk = nullptr;
+  float *in_nw = nullptr, *post_nw = nullptr;
 };
 
 }  // namespace
@@ -175,6 +207,13 @@ struct Qwen35 {
   void *block = nullptr;
   void *fused = nullptr;
   int64_t n_in_max = 0;
+  bool packed = false;  // widths allow the tile layout (decided at create)
+  // row sums of squares of the residual h (<= 32 rows): embedding [T], residual
+  // GEMV partials [H / 16][T]; ss_cur / ss_parts describe h's current state
+  float *ss_embed = nullptr, *ss_o = nullptr, *ss_down = nullptr;
+  const float *ss_cur = nullptr;
+  int ss_parts = 0;
+  bool chain = false;
   float *freqs = nullptr;
   int32_t *zero_lens = nullptr, *pos = nullptr, *row_seq = nullptr, *row_len = nullptr;
   float *h = nullptr, *fin = nullptr, *lora_mid = nullptr;
@@ -188,6 +227,13 @@ struct Qwen35 {
   float *q = nullptr, *gate = nullptr, *att = nullptr, *kc = nullptr, *vc = nullptr;
   // MLP: [gate | up] projection [T, 2I], SwiGLU output [T, I]
   uint16_t *gu = nullptr, *act = nullptr;
+
+  // forward graph: captured on the second consecutive call with the same
+  // (batch, sequence, ids, logits), replayed while that key repeats
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  int64_t g_key[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int g_calls = 0;
 
   void *ptr(int i) const { return params[(size_t)i].bound->ptr; }
   const float *f32(int i) const { return (const float *)ptr(i); }
@@ -256,7 +302,7 @@ void build_schema(Qwen35 *m) {
   auto pad128 = [](int64_t n) { return (n + 127) / 128 * 128; };
   for (Layer &L : m->layers) {
     L.n_in = pad128(L.full ? 2 * m->Hq * m->D + 2 * m->Hkv * m->D : 4 * m->W + 2 * m->Hl);
-    L.n_gu = pad128(2 * m->I);
+    L.n_gu = m->packed ? 2 * m->I : pad128(2 * m->I);
     m->n_in_max = std::max(m->n_in_max, L.n_in);
   }
 }
@@ -311,6 +357,9 @@ int allocate(Qwen35 *m) {
     c.add(&m->vc, m->Bmax * m->Hkv * m->Smax * m->D);
   }
   c.add(&m->gu, T * 2 * m->I);
+  c.add(&m->ss_embed, 32);
+  c.add(&m->ss_o, 32 * ((m->H + 15) / 16));
+  c.add(&m->ss_down, 32 * ((m->H + 15) / 16));
   c.add(&m->act, T * m->I);
   const size_t bytes = c.total();
   hipError_t e = hipMalloc(&m->block, bytes);
@@ -352,12 +401,92 @@ int norm(Qwen35 *m, const float *x, const float *w, void *out, int64_t rows, int
   return launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)rows), dim3(256), a);
 }
 
+// raw = norm_in(h) [parts]^T (linear layers [qkv; z; b; a], full layers [q; k; v]).
+// Packed mode at up to 64 rows: one GEMV whose prologue applies the RMSNorm.
+int in_proj(Qwen35 *m, const Layer &L, int64_t T) {
+  int rc;
+  if (m->chain && m->ss_cur) {
+    GemvOptions o;
+    o.mode = 3, o.norm_w = L.in_nw, o.eps = m->cfg.eps, o.ss_in = m->ss_cur, o.ss_parts = m->ss_parts;
+    o.prefer_ks1 = true;
+    rc = gemv_launch(m->rt, m->h, 1, L.in_w, false, true, L.in_s, m->raw, 0, T, L.n_in, m->H, m->G,
+                     0, o);
+    if (rc != RXW8_UNIMPLEMENTED) return rc;
+  }
+  if ((rc = norm(m, m->h, m->f32(L.in_norm), m->xn, T, m->H, true, false))) return rc;
+  return qlinear_launch(m->rt, m->xn, 0, L.in_w, m->packed, L.in_s, m->raw, 0, T, L.n_in, m->H,
+                        m->G, 1, 0);
+}
+
+// h += x w^T for a residual projection (packed copy w_pk in packed mode). In
+// the chained mode the GEMV also writes h's new row sums of squares to ss.
+int residual(Qwen35 *m, const uint8_t *w_pk, int p, const void *x, int x_f32, int64_t T, float *ss) {
+  if (!m->packed) return proj(m, p, x, x_f32, m->h, 1, T);
+  const Param &w = m->params[(size_t)p];
+  if (m->chain) {
+    GemvOptions o;
+    o.prefer_ks1 = true, o.ss_out = ss;
+    const int rc = gemv_launch(m->rt, x, x_f32, w_pk, false, true, m->f32(p + 1), m->h, 1, T,
+                               w.dims[0], w.dims[1], m->G, 1, o);
+    if (rc != RXW8_UNIMPLEMENTED) {
+      m->ss_cur = ss, m->ss_parts = (int)(m->H / 16);
+      return rc;
+    }
+  }
+  m->ss_cur = nullptr;
+  return qlinear_launch(m->rt, x, x_f32, w_pk, true, m->f32(p + 1), m->h, 1, T, w.dims[0],
+                        w.dims[1], m->G, 1, 1);
+}
+
+int out_proj(Qwen35 *m, const Layer &L, int p, const void *x, int x_f32, int64_t T) {
+  return residual(m, L.out_pk, p, x, x_f32, T, m->ss_o);
+}
+
+// h += down(silu(gate(x)) * up(x)), x = norm_post(h).
+int mlp(Qwen35 *m, const Layer &L, int64_t T) {
+  Runtime *rt = m->rt;
+  int rc;
+  if (!m->packed) {
+    if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, false))) return rc;
+    if ((rc = proj_fused(m, L.gu_w, L.gu_s, L.n_gu, m->xn, m->gu, T))) return rc;
+    Q35SiluArgs sa{m->gu, m->gu + m->I, m->act, T * m->I, m->I, L.n_gu};
+    if ((rc = launch(rt, "rxw8_q35_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
+    return proj(m, L.down, m->act, 0, m->h, 1, T);
+  }
+  // gate|up rows in SwiGLU order: the GEMV (norm prologue) or GEMM epilogue
+  // writes act = bf16(silu(gate) * up) directly
+  rc = RXW8_UNIMPLEMENTED;
+  if (m->chain && m->ss_cur) {
+    GemvOptions o;
+    o.mode = 3, o.norm_w = L.post_nw, o.eps = m->cfg.eps, o.ss_in = m->ss_cur;
+    o.ss_parts = m->ss_parts, o.swiglu = true, o.prefer_ks1 = true;
+    rc = gemv_launch(rt, m->h, 1, L.gu_w, false, true, L.gu_s, m->act, 0, T, 2 * m->I, m->H, m->G,
+                     0, o);
+    if (rc != RXW8_UNIMPLEMENTED && rc) return rc;
+  }
+  if (rc == RXW8_UNIMPLEMENTED) {
+    if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, false))) return rc;
+    if (gemm_eligible(T, 2 * m->I, m->H, m->G)) {
+      if ((rc = qlinear_launch(rt, m->xn, 0, L.gu_w, true, L.gu_s, m->act, 0, T, 2 * m->I, m->H,
+                               m->G, 1, 2)))
+        return rc;
+    } else {
+      if ((rc = qlinear_launch(rt, m->xn, 0, L.gu_w, true, L.gu_s, m->gu, 0, T, 2 * m->I, m->H,
+                               m->G, 1, 0)))
+        return rc;
+      SiluMulArgs sa{m->gu, m->act, T, m->I, 1};
+      if ((rc = launch(rt, "rxw8_dec_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
+    }
+  }
+  return residual(m, L.down_pk, L.down, m->act, 0, T, m->ss_down);
+}
+
 int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   Runtime *rt = m->rt;
   const int64_t T = B * S;
   int rc;
   // raw = xn [qkv; z; b; a]^T: columns [0, 3W) mixed, [3W, 4W) z, then b, a
-  if ((rc = proj_fused(m, L.in_w, L.in_s, L.n_in, m->xn, m->raw, T))) return rc;
+  if ((rc = in_proj(m, L, T))) return rc;
   const uint16_t *zp = m->raw + 3 * m->W, *bp = m->raw + 4 * m->W, *ap = bp + m->Hl;
   Q35ConvArgs cv{m->raw, m->f32(L.conv), m->mixed, T, 3 * m->W, L.n_in, (int)S,
                  (int)m->cfg.conv_kernel};
@@ -381,7 +510,7 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, false, zp, L.n_in,
                  m->Hl)))
     return rc;
-  return proj(m, L.out, m->gated, 0, m->h, 1, T);
+  return out_proj(m, L, L.out, m->gated, 0, T);
 }
 
 int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
@@ -389,7 +518,7 @@ int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   const int64_t T = B * S;
   int rc;
   // raw = xn [q; k; v]^T
-  if ((rc = proj_fused(m, L.in_w, L.in_s, L.n_in, m->xn, m->raw, T))) return rc;
+  if ((rc = in_proj(m, L, T))) return rc;
   const uint16_t *kp = m->raw + 2 * m->Hq * m->D, *vp = kp + m->Hkv * m->D;
   Q35FaPrepArgs fa{m->raw, kp, vp, m->f32(L.qn), m->f32(L.kn), m->freqs, m->q, m->gate,
                    m->kc, m->vc, (int)T, (int)S, (int)m->Hq, (int)m->Hkv, (int)m->D,
@@ -414,7 +543,7 @@ int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   if (rc) return rc;
   Q35MulArgs mu{m->att, m->gate, T * m->Hq * m->D};
   if ((rc = launch(rt, "rxw8_q35_mul", dim3(grid_n(T * m->Hq * m->D)), dim3(256), mu))) return rc;
-  return proj(m, L.o, m->att, 1, m->h, 1, T);
+  return out_proj(m, L, L.o, m->att, 1, T);
 }
 
 int enqueue_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int64_t S) {
@@ -423,16 +552,18 @@ int enqueue_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int
   int rc;
   DecPosArgs pa{m->zero_lens, m->pos, m->row_seq, m->row_len, (int)B, (int)S};
   if ((rc = launch(rt, "rxw8_dec_positions", dim3(grid_n(T)), dim3(256), pa))) return rc;
-  Q35EmbedArgs ea{ids, (const uint8_t *)m->ptr(m->embed), m->f32(m->embed + 1), m->h, T, m->V, m->H, m->G};
-  if ((rc = launch(rt, "rxw8_q35_embed", dim3(grid_n(T * m->H)), dim3(256), ea))) return rc;
+  // packed mode up to 32 rows: the residual's row sums of squares travel with
+  // it (embedding, then the residual GEMVs' per-16-channel partials), so the
+  // projections after each RMSNorm take it in their prologue (GEMV mode 3)
+  m->chain = m->packed && T <= 32 && m->H % 16 == 0;
+  Q35EmbedArgs ea{ids, (const uint8_t *)m->ptr(m->embed), m->f32(m->embed + 1), m->h,
+                  m->chain ? m->ss_embed : nullptr, T, m->V, m->H, m->G};
+  if ((rc = launch(rt, "rxw8_q35_embed", dim3((unsigned)T), dim3(256), ea))) return rc;
+  m->ss_cur = m->chain ? m->ss_embed : nullptr;
+  m->ss_parts = 1;
   for (const Layer &L : m->layers) {
-    if ((rc = norm(m, m->h, m->f32(L.in_norm), m->xn, T, m->H, true, false))) return rc;
     if ((rc = L.full ? full_mixer(m, L, B, S) : linear_mixer(m, L, B, S))) return rc;
-    if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, false))) return rc;
-    if ((rc = proj_fused(m, L.gu_w, L.gu_s, L.n_gu, m->xn, m->gu, T))) return rc;
-    Q35SiluArgs sa{m->gu, m->gu + m->I, m->act, T * m->I, m->I, L.n_gu};
-    if ((rc = launch(rt, "rxw8_q35_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
-    if ((rc = proj(m, L.down, m->act, 0, m->h, 1, T))) return rc;
+    if ((rc = mlp(m, L, T))) return rc;
   }
   if ((rc = norm(m, m->h, m->f32(m->final_norm), m->fin, T, m->H, true, true))) return rc;
   // tied head: f32 hidden . f32 dequantised table (compute F32)
@@ -452,54 +583,160 @@ int enqueue_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int
 
 // Fused input projections: the rows of each part copied one after another
 // (row-major U8 [n, H] and F32 scales [n, H / G] stack along dim 0), padded
-// with codes 128 and scales 0 (rows of zeros) to n_in / n_gu rows.
+// with codes 128 and scales 0 (rows of zeros) to n_in / n_gu rows. In packed
+// mode the stacked rows go through a staging buffer into the tile layout of
+// the W8 GEMV / GEMM kernels (rxw8_pack_tiles; the [gate; up] rows in SwiGLU
+// order with their scale rows interleaved to match), the residual projections
+// are packed from the bound weights, and the zero-centred norm weights are
+// stored as 1 + w for the GEMV's RMSNorm prologue.
 int prepare(Qwen35 *m) {
   Runtime *rt = m->rt;
   const int64_t ng = m->H / m->G;
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  size_t total = 0;
-  for (const Layer &L : m->layers)
+  size_t total = 0, stage = 0;
+  for (const Layer &L : m->layers) {
     total += al((size_t)L.n_in * m->H) + al((size_t)L.n_in * ng * 4) + al((size_t)L.n_gu * m->H) +
              al((size_t)L.n_gu * ng * 4);
+    if (m->packed) {
+      const int64_t ko = L.full ? m->Hq * m->D : m->W;
+      total += al((size_t)m->H * ko) + al((size_t)m->H * m->I) + 2 * al((size_t)m->H * 4);
+      stage = std::max(stage, al((size_t)std::max(L.n_in, L.n_gu) * m->H) +
+                                  al((size_t)L.n_gu * ng * 4));
+    }
+  }
   hipError_t e = hipMalloc(&m->fused, total);
+  void *tmp = nullptr;
+  if (e == hipSuccess && stage) e = hipMalloc(&tmp, stage);
   if (e != hipSuccess) {
     (void)hipGetLastError();
+    if (m->fused) (void)hipFree(m->fused);
     m->fused = nullptr;
-    return fail(RXW8_RESOURCE_EXHAUSTED, "qwen35: cannot allocate %zu bytes of fused weights", total);
+    return fail(RXW8_RESOURCE_EXHAUSTED, "qwen35: cannot allocate %zu bytes of fused weights",
+                total + stage);
   }
+  uint8_t *tmp_w = (uint8_t *)tmp;
+  float *tmp_s = nullptr;
   char *p = (char *)m->fused;
-  auto stack = [&](const std::vector<int> &parts, int64_t n, uint8_t **w, float **sc) -> int {
-    *w = (uint8_t *)p;
-    p += al((size_t)n * m->H);
-    *sc = (float *)p;
-    p += al((size_t)n * ng * 4);
+  auto take = [&](size_t bytes) {
+    char *r = p;
+    p += al(bytes);
+    return r;
+  };
+  auto stack = [&](const std::vector<int> &parts, int64_t n, uint8_t *w, float *sc) -> int {
     int64_t row = 0;
     for (int i : parts) {
       const int64_t rows = m->params[(size_t)i].dims[0];
-      RXW8_HIP(hipMemcpyAsync(*w + row * m->H, m->ptr(i), (size_t)rows * m->H,
+      RXW8_HIP(hipMemcpyAsync(w + row * m->H, m->ptr(i), (size_t)rows * m->H,
                               hipMemcpyDeviceToDevice, rt->stream));
-      RXW8_HIP(hipMemcpyAsync(*sc + row * ng, m->ptr(i + 1), (size_t)rows * ng * 4,
+      RXW8_HIP(hipMemcpyAsync(sc + row * ng, m->ptr(i + 1), (size_t)rows * ng * 4,
                               hipMemcpyDeviceToDevice, rt->stream));
       row += rows;
     }
     if (row < n) {
-      RXW8_HIP(hipMemsetAsync(*w + row * m->H, 128, (size_t)(n - row) * m->H, rt->stream));
-      RXW8_HIP(hipMemsetAsync(*sc + row * ng, 0, (size_t)(n - row) * ng * 4, rt->stream));
+      RXW8_HIP(hipMemsetAsync(w + row * m->H, 128, (size_t)(n - row) * m->H, rt->stream));
+      RXW8_HIP(hipMemsetAsync(sc + row * ng, 0, (size_t)(n - row) * ng * 4, rt->stream));
     }
     return RXW8_OK;
   };
-  int rc;
+  auto pack = [&](const void *src, void *dst, int64_t n, int64_t k, int64_t ilv) -> int {
+    PackArgs a{src, dst, n, k, 64, 1, ilv};
+    const int64_t slices = n / 16 * (k / 64) * 64;
+    return launch(rt, "rxw8_pack_tiles", dim3((unsigned)std::min<int64_t>((slices + 255) / 256, 1 << 14)),
+                  dim3(256), a);
+  };
+  int rc = RXW8_OK;
   for (Layer &L : m->layers) {
     const std::vector<int> in = L.full ? std::vector<int>{L.q, L.k, L.v}
                                        : std::vector<int>{L.qkv, L.z, L.b, L.a};
-    if ((rc = stack(in, L.n_in, &L.in_w, &L.in_s))) return rc;
-    if ((rc = stack({L.gate, L.up}, L.n_gu, &L.gu_w, &L.gu_s))) return rc;
+    L.in_w = (uint8_t *)take((size_t)L.n_in * m->H);
+    L.in_s = (float *)take((size_t)L.n_in * ng * 4);
+    L.gu_w = (uint8_t *)take((size_t)L.n_gu * m->H);
+    L.gu_s = (float *)take((size_t)L.n_gu * ng * 4);
+    if (!m->packed) {
+      if ((rc = stack(in, L.n_in, L.in_w, L.in_s))) break;
+      if ((rc = stack({L.gate, L.up}, L.n_gu, L.gu_w, L.gu_s))) break;
+      continue;
+    }
+    tmp_s = (float *)((char *)tmp + al((size_t)std::max(L.n_in, L.n_gu) * m->H));
+    if ((rc = stack(in, L.n_in, tmp_w, L.in_s))) break;
+    if ((rc = pack(tmp_w, L.in_w, L.n_in, m->H, 0))) break;
+    if ((rc = stack({L.gate, L.up}, L.n_gu, tmp_w, tmp_s))) break;
+    if ((rc = pack(tmp_w, L.gu_w, L.n_gu, m->H, m->I))) break;
+    InterleaveArgs il{tmp_s, L.gu_s, m->I, ng};
+    if ((rc = launch(rt, "rxw8_dec_interleave_rows", dim3(grid_n(2 * m->I * ng)), dim3(256), il))) break;
+    const int o = L.full ? L.o : L.out;
+    const int64_t ko = m->params[(size_t)o].dims[1];
+    L.out_pk = (uint8_t *)take((size_t)m->H * ko);
+    if ((rc = pack(m->ptr(o), L.out_pk, m->H, ko, 0))) break;
+    L.down_pk = (uint8_t *)take((size_t)m->H * m->I);
+    if ((rc = pack(m->ptr(L.down), L.down_pk, m->H, m->I, 0))) break;
+    L.in_nw = (float *)take((size_t)m->H * 4);
+    L.post_nw = (float *)take((size_t)m->H * 4);
+    Q35ShiftArgs s1{m->f32(L.in_norm), L.in_nw, m->H}, s2{m->f32(L.post_norm), L.post_nw, m->H};
+    if ((rc = launch(rt, "rxw8_q35_one_plus", dim3(grid_n(m->H)), dim3(256), s1))) break;
+    if ((rc = launch(rt, "rxw8_q35_one_plus", dim3(grid_n(m->H)), dim3(256), s2))) break;
   }
-  RXW8_HIP(hipStreamSynchronize(rt->stream));
+  const hipError_t se = hipStreamSynchronize(rt->stream);  // the staging buffer is free after this
+  if (tmp) (void)hipFree(tmp);
+  if (!rc && se != hipSuccess) rc = hip_fail(se, "hipStreamSynchronize");
+  if (rc) {
+    (void)hipFree(m->fused);
+    m->fused = nullptr;
+  }
+  return rc;
+}
+
+void drop_graph(Qwen35 *m) {
+  if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  m->gexec = nullptr;
+  m->graph = nullptr;
+}
+
+// One forward: eager on a new key; the second consecutive call with the same
+// key captures the launch sequence into a HIP graph (every workspace has been
+// sized by the eager call, and the sequence holds kernel launches only); later
+// calls with that key replay it.
+int run_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int64_t S) {
+  static const bool no_graph = std::getenv("RXW8_Q35_NO_GRAPH") && std::getenv("RXW8_Q35_NO_GRAPH")[0] == '1';
+  Runtime *rt = m->rt;
+  // the runtime's workspaces are part of the key: another call that grows
+  // (reallocates) one invalidates the addresses a captured graph holds
+  const int64_t key[8] = {B, S, (int64_t)(intptr_t)ids, (int64_t)(intptr_t)logits,
+                          (int64_t)(intptr_t)rt->partials.ptr, (int64_t)(intptr_t)rt->scratch.ptr,
+                          (int64_t)(intptr_t)rt->xcast.ptr, (int64_t)(intptr_t)rt->wdeq.ptr};
+  const bool same = std::equal(key, key + 8, m->g_key);
+  if (!same) {
+    drop_graph(m);
+    std::copy(key, key + 8, m->g_key);
+    m->g_calls = 0;
+  }
+  ++m->g_calls;
+  if (no_graph || m->g_calls < 2) return enqueue_forward(m, ids, logits, B, S);
+  if (!m->gexec) {
+    RXW8_HIP(hipStreamBeginCapture(rt->stream, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_forward(m, ids, logits, B, S);
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(rt->stream, &graph);
+    if (rc) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&m->gexec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+      (void)hipGraphDestroy(graph);
+      m->gexec = nullptr;
+      return hip_fail(e, "hipGraphInstantiate");
+    }
+    m->graph = graph;
+  }
+  RXW8_HIP(hipGraphLaunch(m->gexec, rt->stream));
   return RXW8_OK;
 }
 
 void free_model(Qwen35 *m) {
+  drop_graph(m);
   if (m->block || m->fused) (void)hipStreamSynchronize(m->rt->stream);
   if (m->block) (void)hipFree(m->block);
   if (m->fused) (void)hipFree(m->fused);
@@ -563,6 +800,10 @@ int rxw8_qwen35_create(rxw8_runtime *rt, const rxw8_qwen35_config *cfg, rxw8_qwe
     return fail(RXW8_UNIMPLEMENTED, "qwen35: head_dim %lld (supported: even, <= 256)", (long long)q->D);
   if (q->any_full && q->Smax > 8192)
     return fail(RXW8_UNIMPLEMENTED, "qwen35: full-attention sequences of at most 8192 positions");
+  // tile layout: 16-row tiles, 64-byte k blocks, gate|up pairs of 8 rows
+  q->packed = c.hidden % 64 == 0 && c.intermediate % 64 == 0 &&
+              (!q->any_linear || q->W % 64 == 0) && (!q->any_full || (c.heads * c.head_dim) % 64 == 0) &&
+              !(std::getenv("RXW8_Q35_UNPACKED") && std::getenv("RXW8_Q35_UNPACKED")[0] == '1');
   const int64_t T = q->Bmax * q->Smax;
   if (T > (1LL << 31) / std::max<int64_t>({q->H, 3 * q->W, q->I, 2 * q->Hq * q->D}))
     return fail(RXW8_INVALID_ARGUMENT, "qwen35: max_batch * max_seq too large");
@@ -663,7 +904,7 @@ int rxw8_qwen35_forward(rxw8_qwen35 *m, rxw8_buffer *ids, rxw8_buffer *logits) {
     const int rc = prepare(m);
     if (rc) return rc;
   }
-  return enqueue_forward(m, (const int32_t *)ids->ptr, (float *)logits->ptr, B, S);
+  return run_forward(m, (const int32_t *)ids->ptr, (float *)logits->ptr, B, S);
 }
 
 }  // extern "C"

@@ -97,6 +97,17 @@ def test_logits_match_the_oracle(rt, name, b, s):
     np.testing.assert_array_equal(got.argmax(-1)[clear], want.argmax(-1)[clear])
 
 
+@pytest.mark.parametrize("s", [13, 70])
+def test_row_major_weight_path(rt, monkeypatch, s):
+    """RXW8_Q35_UNPACKED=1 keeps the fused projections row-major (the path
+    widths outside the tile layout take): same logits within tolerance."""
+    monkeypatch.setenv("RXW8_Q35_UNPACKED", "1")
+    cfg = CONFIGS["small"]
+    p = q35.random_params(cfg, seed=31)
+    ids = np.random.default_rng(32).integers(0, cfg["vocab"], (2, s))
+    assert rel_err(run(rt, build(rt, cfg, p), ids), q35.forward(cfg, p, ids)) <= TOL
+
+
 def test_sequences_are_independent_and_causal(rt):
     """Row b of the batch depends only on sequence b; position i only on
     tokens <= i (bit for bit: the same kernels see the same shapes)."""
@@ -112,6 +123,32 @@ def test_sequences_are_independent_and_causal(rt):
     np.testing.assert_array_equal(a[0, :25], b[0, :25])
     assert np.abs(a[0, 25:] - b[0, 25:]).max() > 0
     np.testing.assert_array_equal(run(rt, m, ids), a)  # deterministic
+
+
+def test_graph_replays_match_the_eager_forward(rt):
+    """The second call with the same buffers is captured into a HIP graph and
+    later calls replay it: every replay equals the eager result bit for bit,
+    with other eager work (including a linear that grows the runtime's
+    workspaces, which forces a re-capture) and synchronizations in between."""
+    r = rx()
+    cfg = CONFIGS["mid"]
+    m = build(rt, cfg, q35.random_params(cfg, seed=21, std=cfg["std"]))
+    ids = rt.buffer(np.random.default_rng(22).integers(0, cfg["vocab"], (2, 37)).astype(np.int32))
+    logits = rt.zeros((2, 37, cfg["vocab"]), r.DType.F32)
+    m.forward(ids, logits)
+    eager = logits.to_numpy()
+    rng = np.random.default_rng(23)
+    for i in range(5):
+        m.forward(ids, logits)
+        rt.synchronize()
+        np.testing.assert_array_equal(logits.to_numpy(), eager)
+        x = rng.standard_normal((64 * (i + 1), 1024)).astype(np.float32)
+        w = rng.integers(0, 256, (4096, 1024)).astype(np.uint8)
+        sc = np.full((4096, 8), 1e-3, np.float32)
+        r.quantized_linear(rt, rt.buffer(x), rt.buffer(w), rt.buffer(sc)).to_numpy()
+    other = rt.zeros((2, 37, cfg["vocab"]), r.DType.F32)  # a new key: eager again
+    m.forward(ids, other)
+    np.testing.assert_array_equal(other.to_numpy(), eager)
 
 
 def test_lora_head(rt):
