@@ -175,6 +175,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
 struct Q35AttnArgs {
   const float *q;        // [T, Hq, D], token t = b * S + i
   const float *kc, *vc;  // [B, Hkv, Lmax, D]
+  const float *gate;     // [T, Hq * D] output gate (layers.rs:93-94), multiplied in at the store
   float *out;            // [T, Hq * D]
   int S, Hq, Hkv, Lmax, qtiles;
   float scale;
@@ -306,9 +307,9 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
     const int qpos = q0 + 4 * j + i;
     if (qpos < a.S) {
       const float inv = 1.0f / l[i];
-      float *op = a.out + ((int64_t)b * a.S + qpos) * a.Hq * D + (int64_t)h * D + col;
+      const int64_t off = ((int64_t)b * a.S + qpos) * a.Hq * D + (int64_t)h * D + col;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) op[16 * dt] = o[dt][i] * inv;
+      for (int dt = 0; dt < DT; ++dt) a.out[off + 16 * dt] = (o[dt][i] * inv) * a.gate[off + 16 * dt];
     }
   }
 }
@@ -347,74 +348,83 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_mul(Q35MulArgs a) {
     a.x[e] *= a.y[e];
 }
 
-// ---- causal depthwise conv over each sequence + SiLU (layers.rs:131-146):
-// out[t, c] = silu(sum_j w[c, j] * x[t - (k-1) + j, c]), zero before position 0.
-struct Q35ConvArgs {
-  const uint16_t *x;   // [T, C] bf16 projection, rows of x_stride elements
-  const float *w;      // [C, k]
-  float *out;          // [T, C]
-  int64_t T, C, x_stride;
-  int S, k;
-};
-
-extern "C" __global__ void __launch_bounds__(256) rxw8_q35_conv_silu(Q35ConvArgs a) {
-  const int64_t n = a.T * a.C;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = e / a.C, c = e - t * a.C;
-    const int pos = (int)(t % a.S);
-    float acc = 0.f;
-    for (int j = 0; j < a.k; ++j) {
-      const int src = pos - (a.k - 1) + j;
-      if (src >= 0) acc += a.w[c * a.k + j] * bf16_bits_to_f32(a.x[(t - pos + src) * a.x_stride + c]);
-    }
-    a.out[e] = acc * sigmoid_f32(acc);
-  }
-}
-
-// ---- q, k of the gated-delta mixer (layers.rs:147-161): per (token, head)
-// q = l2norm(q) / sqrt(Dl), k = l2norm(k), l2norm(x) = x * rsqrt(sum x^2 + 1e-6);
-// in place in the conv output [T, 3W] (q at 0, k at W). One wave per row.
-struct Q35L2Args {
-  float *mixed;
-  int64_t T;
-  int Hl, Dl;
+// ---- gated-delta prologue for one (token, head) per workgroup
+// (layers.rs:131-195): the causal depthwise conv + SiLU of the head's q, k and
+// v channels, out[t, c] = silu(sum_j w[c, j] * x[t - (k-1) + j, c]) (zero
+// before position 0 of the sequence; a correlation, conv2d_oihw with padding
+// (k-1, 0)); q = l2norm(q) / sqrt(Dl), k = l2norm(k) with
+// l2norm(x) = x * rsqrt(sum x^2 + 1e-6) (layers.rs:102-111); and the head's
+// beta = sigmoid(b), g = exp(softplus(a + dt_bias) * -exp(A_log)) with
+// softplus(x) = max(x, 0) + log1p(exp(-|x|)) (ops.rs:256-262).
+// The projection row of token t (bf16, `stride` elements) holds the conv
+// input channels [0, 3W), then z [3W, 4W), b [4W, 4W + Hl), a after b.
+struct Q35MixPrepArgs {
+  const uint16_t *raw;           // [T, stride]
+  const float *conv_w;           // [3W, k]
+  const float *a_log, *dt_bias;  // [Hl]
+  float *mixed;                  // [T, 3W]: q (normed, scaled), k (normed), v
+  float *beta, *g;               // [T, Hl]
+  int64_t stride;
+  int S, Hl, Dl, k;
   float q_scale;
 };
 
-extern "C" __global__ void __launch_bounds__(256) rxw8_q35_qk_l2norm(Q35L2Args a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (t, which, head)
-  if (unit >= a.T * 2 * a.Hl) return;
-  const int64_t t = unit / (2 * a.Hl);
-  const int r = (int)(unit - t * 2 * a.Hl), which = r / a.Hl, h = r - which * a.Hl;
-  float *x = a.mixed + t * 3 * (int64_t)a.Hl * a.Dl + (int64_t)which * a.Hl * a.Dl + (int64_t)h * a.Dl;
-  float ss = 0.f;
-  for (int i = lane; i < a.Dl; i += 64) ss += x[i] * x[i];
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-  const float sc = (1.0f / sqrtf(ss + 1e-6f)) * (which == 0 ? a.q_scale : 1.0f);
-  for (int i = lane; i < a.Dl; i += 64) x[i] *= sc;
-}
-
-// ---- beta = sigmoid(b); g = exp(softplus(a + dt_bias) * -exp(A_log))
-// (layers.rs:180-195; softplus = max(x, 0) + log1p(exp(-|x|)), ops.rs:256-262)
-struct Q35GateArgs {
-  const uint16_t *b, *a;  // [T, Hl] bf16 projections, rows of `stride` elements
-  const float *a_log, *dt_bias;  // [Hl]
-  float *beta, *g;        // [T, Hl]
-  int64_t n, stride;
-  int Hl;
-};
-
-extern "C" __global__ void __launch_bounds__(256) rxw8_q35_beta_decay(Q35GateArgs p) {
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < p.n;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = e / p.Hl;
-    const int h = (int)(e - t * p.Hl);
-    p.beta[e] = sigmoid_f32(bf16_bits_to_f32(p.b[t * p.stride + h]));
-    const float x = bf16_bits_to_f32(p.a[t * p.stride + h]) + p.dt_bias[h];
+extern "C" __global__ void __launch_bounds__(128) rxw8_q35_mix_prep(Q35MixPrepArgs a) {
+  __shared__ float red[2][2];
+  const int64_t t = blockIdx.x / a.Hl;
+  const int h = (int)(blockIdx.x - t * a.Hl);
+  const int pos = (int)(t % a.S);
+  const int64_t W = (int64_t)a.Hl * a.Dl;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  float qv[2], kv[2], vv[2];  // channels c = threadIdx.x and c + 128 (Dl <= 256)
+  float sq = 0.f, sk = 0.f;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = threadIdx.x + 128 * r;
+    qv[r] = kv[r] = vv[r] = 0.f;
+    if (c < a.Dl) {
+      float acc[3] = {0.f, 0.f, 0.f};
+      for (int j = 0; j < a.k; ++j) {
+        const int src = pos - (a.k - 1) + j;
+        if (src < 0) continue;
+        const uint16_t *row = a.raw + (t - pos + src) * a.stride;
+#pragma unroll
+        for (int part = 0; part < 3; ++part) {
+          const int64_t ch = part * W + (int64_t)h * a.Dl + c;
+          acc[part] += a.conv_w[ch * a.k + j] * bf16_bits_to_f32(row[ch]);
+        }
+      }
+      qv[r] = acc[0] * sigmoid_f32(acc[0]);
+      kv[r] = acc[1] * sigmoid_f32(acc[1]);
+      vv[r] = acc[2] * sigmoid_f32(acc[2]);
+      sq += qv[r] * qv[r];
+      sk += kv[r] * kv[r];
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    sq += __shfl_xor(sq, o);
+    sk += __shfl_xor(sk, o);
+  }
+  if (lane == 0) red[wv][0] = sq, red[wv][1] = sk;
+  __syncthreads();
+  const float qs = (1.0f / sqrtf(red[0][0] + red[1][0] + 1e-6f)) * a.q_scale;
+  const float ks = 1.0f / sqrtf(red[0][1] + red[1][1] + 1e-6f);
+  float *m = a.mixed + t * 3 * W + (int64_t)h * a.Dl;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = threadIdx.x + 128 * r;
+    if (c < a.Dl) {
+      m[c] = qv[r] * qs;
+      m[W + c] = kv[r] * ks;
+      m[2 * W + c] = vv[r];
+    }
+  }
+  if (threadIdx.x == 0) {
+    const uint16_t *row = a.raw + t * a.stride + 4 * W;
+    a.beta[t * a.Hl + h] = sigmoid_f32(bf16_bits_to_f32(row[h]));
+    const float x = bf16_bits_to_f32(row[a.Hl + h]) + a.dt_bias[h];
     const float sp = fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
-    p.g[e] = expf(sp * -expf(p.a_log[h]));
+    a.g[t * a.Hl + h] = expf(sp * -expf(a.a_log[h]));
   }
 }
 

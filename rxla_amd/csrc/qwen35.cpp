@@ -84,7 +84,7 @@ struct Q35FaPrepArgs {
   float eps;
 };
 struct Q35AttnArgs {
-  const float *q, *kc, *vc;
+  const float *q, *kc, *vc, *gate;
   float *out;
   int S, Hq, Hkv, Lmax, qtiles;
   float scale;
@@ -94,25 +94,15 @@ struct Q35MulArgs {
   const float *y;
   int64_t n;
 };
-struct Q35ConvArgs {
-  const uint16_t *x;
-  const float *w;
-  float *out;
-  int64_t T, C, x_stride;
-  int S, k;
-};
-struct Q35L2Args {
-  float *mixed;
-  int64_t T;
-  int Hl, Dl;
-  float q_scale;
-};
-struct Q35GateArgs {
-  const uint16_t *b, *a;
+struct Q35MixPrepArgs {
+  const uint16_t *raw;
+  const float *conv_w;
   const float *a_log, *dt_bias;
+  float *mixed;
   float *beta, *g;
-  int64_t n, stride;
-  int Hl;
+  int64_t stride;
+  int S, Hl, Dl, k;
+  float q_scale;
 };
 struct Q35DeltaArgs {
   const float *mixed, *beta, *g;
@@ -487,16 +477,12 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   int rc;
   // raw = xn [qkv; z; b; a]^T: columns [0, 3W) mixed, [3W, 4W) z, then b, a
   if ((rc = in_proj(m, L, T))) return rc;
-  const uint16_t *zp = m->raw + 3 * m->W, *bp = m->raw + 4 * m->W, *ap = bp + m->Hl;
-  Q35ConvArgs cv{m->raw, m->f32(L.conv), m->mixed, T, 3 * m->W, L.n_in, (int)S,
-                 (int)m->cfg.conv_kernel};
-  if ((rc = launch(rt, "rxw8_q35_conv_silu", dim3(grid_n(T * 3 * m->W)), dim3(256), cv))) return rc;
-  Q35L2Args l2{m->mixed, T, (int)m->Hl, (int)m->Dl, 1.0f / sqrtf((float)m->Dl)};
-  if ((rc = launch(rt, "rxw8_q35_qk_l2norm", dim3((unsigned)((T * 2 * m->Hl + 3) / 4)), dim3(256), l2)))
-    return rc;
-  Q35GateArgs ga{bp, ap, m->f32(L.a_log), m->f32(L.dt_bias), m->beta, m->g, T * m->Hl, L.n_in,
-                 (int)m->Hl};
-  if ((rc = launch(rt, "rxw8_q35_beta_decay", dim3(grid_n(T * m->Hl)), dim3(256), ga))) return rc;
+  const uint16_t *zp = m->raw + 3 * m->W;
+  // conv + SiLU, q / k L2 norms, beta and decay: one workgroup per (token, head)
+  Q35MixPrepArgs mp{m->raw, m->f32(L.conv), m->f32(L.a_log), m->f32(L.dt_bias), m->mixed, m->beta,
+                    m->g, L.n_in, (int)S, (int)m->Hl, (int)m->Dl, (int)m->cfg.conv_kernel,
+                    1.0f / sqrtf((float)m->Dl)};
+  if ((rc = launch(rt, "rxw8_q35_mix_prep", dim3((unsigned)(T * m->Hl)), dim3(128), mp))) return rc;
   Q35DeltaArgs da{m->mixed, m->beta, m->g, m->dout, (int)B, (int)S, (int)m->Hl};
   char kname[40];
   std::snprintf(kname, sizeof kname, "rxw8_q35_delta_rule_d%d", (int)m->Dl);
@@ -530,19 +516,20 @@ int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   if ((m->D == 64 || m->D == 128 || m->D == 256) && 4 % G == 0) {
     // f32 matrix-core flash attention: 4 waves per (sequence, kv head, query tile)
     const int64_t qtiles = (S + 16 * (4 / G) - 1) / (16 * (4 / G));
-    Q35AttnArgs at{m->q, m->kc, m->vc, m->att, (int)S, (int)m->Hq, (int)m->Hkv, (int)m->Smax,
-                   (int)qtiles, scale};
+    Q35AttnArgs at{m->q, m->kc, m->vc, m->gate, m->att, (int)S, (int)m->Hq, (int)m->Hkv,
+                   (int)m->Smax, (int)qtiles, scale};
     const size_t lds = (size_t)4 * 16 * (m->D + 4) * 4 + 4 * 16 * 20 * 4;
     char an[40];
     std::snprintf(an, sizeof an, "rxw8_q35_attention_d%d", (int)m->D);
-    rc = launch(rt, an, dim3((unsigned)(B * m->Hkv * qtiles)), dim3(256), at, lds);
+    // the kernel multiplies its output by the gate
+    if ((rc = launch(rt, an, dim3((unsigned)(B * m->Hkv * qtiles)), dim3(256), at, lds))) return rc;
   } else {
-    rc = attention_launch(rt, m->q, 1, m->kc, m->vc, 1, m->row_len, m->row_seq, nullptr, 0, 0,
-                          m->att, 1, T, m->Hq, m->Hkv, m->Smax, m->D, scale, nullptr);
+    if ((rc = attention_launch(rt, m->q, 1, m->kc, m->vc, 1, m->row_len, m->row_seq, nullptr, 0, 0,
+                               m->att, 1, T, m->Hq, m->Hkv, m->Smax, m->D, scale, nullptr)))
+      return rc;
+    Q35MulArgs mu{m->att, m->gate, T * m->Hq * m->D};
+    if ((rc = launch(rt, "rxw8_q35_mul", dim3(grid_n(T * m->Hq * m->D)), dim3(256), mu))) return rc;
   }
-  if (rc) return rc;
-  Q35MulArgs mu{m->att, m->gate, T * m->Hq * m->D};
-  if ((rc = launch(rt, "rxw8_q35_mul", dim3(grid_n(T * m->Hq * m->D)), dim3(256), mu))) return rc;
   return out_proj(m, L, L.o, m->att, 1, T);
 }
 
