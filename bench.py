@@ -419,6 +419,8 @@ def main():
     ap.add_argument("--skip-decoder", action="store_true")
     ap.add_argument("--skip-qwen35", action="store_true")
     ap.add_argument("--pmc-probe", choices=["gemv"], help="counter-collection program only")
+    ap.add_argument("--qwen35-only", action="store_true",
+                    help="(profiling) run only the Qwen3.5 leg and print its JSON")
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe(args.pmc_probe)
@@ -435,6 +437,9 @@ def main():
     info = rt.device_info()
     stream = torch.cuda.Stream()  # default priority
     rt.set_stream(stream.cuda_stream)
+    if args.qwen35_only:
+        print(json.dumps({"qwen35": bench_qwen35(rt, rx, torch, stream)}), flush=True)
+        return
     gen = torch.Generator(device="cuda").manual_seed(0)
     log(f"device {info}; allocating {args.copies} weight copies per N")
     with torch.cuda.stream(stream):
