@@ -99,6 +99,7 @@ struct LinearF32Args {
   float *y;            // [T, N]
   int T, N, K, G;
   int y_mode;          // 0: y = result; 1: y += result (f32 residual)
+  int tiles;           // channel tiles (16 WV channels each) per workgroup
 };
 
 template <int R, int WV>
@@ -112,8 +113,7 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
   uint16_t *al = ah + 16 * R * rowp;
   float *sc = (float *)(al + 16 * R * rowp);
   const int m0 = blockIdx.y * 16 * R;
-  const int n0 = blockIdx.x * 16 * WV;
-  // ---- stage x (split into hi / lo) and the scales
+  // ---- stage x (split into hi / lo) once for all of this workgroup's channel tiles
   for (int e = threadIdx.x * 4; e < 16 * R * K; e += blockDim.x * 4) {
     const int m = e / K, c = e - m * K;
     const int t = min(m0 + m, a.T - 1);
@@ -128,6 +128,11 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
     *(uint2 *)(ah + m * rowp + c) = uint2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
     *(uint2 *)(al + m * rowp + c) = uint2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
   }
+  const int col = lane & 15, part = lane >> 4;
+  for (int ct = 0; ct < a.tiles; ++ct) {
+  const int n0 = (blockIdx.x * a.tiles + ct) * 16 * WV;
+  if (n0 >= a.N) break;  // uniform
+  if (ct > 0) __syncthreads();  // every wave is done with the previous tile's scales
   for (int e = threadIdx.x; e < 16 * WV * ng; e += blockDim.x) {
     const int r = e / ng, g = e - r * ng;
     const int n = min(n0 + r, a.N - 1);
@@ -135,7 +140,6 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
   }
   __syncthreads();
   // ---- stream the weight rows
-  const int col = lane & 15, part = lane >> 4;
   const int nrow = min(n0 + 16 * wv + col, a.N - 1);
   const uint8_t *wp = a.w + (int64_t)nrow * K + 16 * part;
   const float *scl = sc + (16 * wv + col) * ng;
@@ -210,6 +214,7 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
         }
       }
   }
+  }  // channel tiles
 }
 
 #define RXW8_LINEAR_F32(R, WV)                                                          \

@@ -18,6 +18,13 @@ __device__ __forceinline__ float ld(const void *p, int64_t i, int f32) {
 }
 }  // namespace
 
+// One DPP move within a row of 16 lanes (CTRL: row_ror:n = 0x120 + n, or a
+// quad_perm pattern).
+template <int CTRL>
+__device__ __forceinline__ float dpp_rot(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
 // ---- W8 embedding: h[t, c] = (f32(u8[id, c]) - 128) * scale[id, c / G], ids
 // clamped to [0, V - 1] (mod.rs:134-157, indexing.rs:637-656); one workgroup
 // per token, which also writes the row's sum of squares (ss, optional) for the
@@ -181,10 +188,6 @@ struct Q35AttnArgs {
   float scale;
 };
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_rot(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
 __device__ __forceinline__ float row_max16(float v) {
   v = fmaxf(v, dpp_rot<0x128>(v));
   v = fmaxf(v, dpp_rot<0x124>(v));
@@ -493,6 +496,7 @@ __device__ void delta_rule(const Q35DeltaArgs &a) {
   }
 RXW8_Q35_DELTA(8)
 RXW8_Q35_DELTA(16)
+RXW8_Q35_DELTA(32)
 
 // Sum over the 16 lanes of a DPP row, the same bits in every lane (each
 // stage adds a lane's value to a rotation of the row: row_ror 8, row_ror 4,
@@ -507,78 +511,91 @@ __device__ __forceinline__ float row_sum16(float v) {
 
 // The same recurrence with each state column spread over the 16 lanes of a
 // DPP row: lane p of column j keeps S[i][j] for i = E p .. E p + E - 1
-// (E = DL / 16), so a position costs E-wide updates plus two row sums instead
-// of DL-long serial loops, and a (sequence, head) runs on DL / 16 workgroups of
-// 16 columns each (the columns of S evolve independently). The q / k slices,
-// v, beta and g of the next NPF positions are in flight while one is computed.
+// (E = DL / 16), and a (sequence, head) runs on DL / 16 workgroups of 16
+// columns each (the columns of S evolve independently). With S' the state
+// before position t, the step is evaluated as
+//   a_k = S'^T k,  a_q = S'^T q,  kq = k . q      (three sums, one DPP pass)
+//   pred = g a_k,  delta = (v - pred) beta,  o = g a_q + delta kq,
+//   S = g S' + k delta^T,
+// the same quantities as the reference's order (g S' first) with g factored
+// out of the sums, so one reduction round (not two) sits on the serial chain.
+// The inputs of the next NPF positions are in flight while one is computed;
+// beta and g of NPF positions come as one lane-indexed vector load (lane i of
+// the wave holds position t0 + i) and reach the step by v_readlane, so no
+// scalar-cache load (whose waits cannot be counted per load) sits in the loop.
 template <int DL>
 __device__ void delta_rule_rows(const Q35DeltaArgs &a) {
-  constexpr int E = DL / 16, NPF = 4, GROUPS = DL / 16;
+  constexpr int E = DL / 16, NPF = 8, GROUPS = DL / 16;
   const int lane = threadIdx.x & 63, p = lane & 15;
   const int bh = blockIdx.x / GROUPS, grp = blockIdx.x - bh * GROUPS;
   const int b = bh / a.Hl, h = bh - b * a.Hl;
   const int j = grp * 16 + (threadIdx.x >> 4);
   const int64_t W = (int64_t)a.Hl * DL;
   struct Vals {
-    float q[E], k[E], v, beta, g;
+    float q[E], k[E], v;
   };
   auto fetch = [&](int pos, Vals &o) {
     const int64_t row = (int64_t)b * a.S + pos;
     const float *m = a.mixed + row * 3 * W + (int64_t)h * DL;
-    if constexpr (E % 4 == 0) {
 #pragma unroll
-      for (int e = 0; e < E; e += 4) {
-        const float4 qq = *(const float4 *)(m + E * p + e);
-        const float4 kk = *(const float4 *)(m + W + E * p + e);
-        o.q[e] = qq.x, o.q[e + 1] = qq.y, o.q[e + 2] = qq.z, o.q[e + 3] = qq.w;
-        o.k[e] = kk.x, o.k[e + 1] = kk.y, o.k[e + 2] = kk.z, o.k[e + 3] = kk.w;
-      }
-    } else {
-      static_assert(E == 2, "DL in {32, 64, 128}");
-      const float2 qq = *(const float2 *)(m + E * p);
-      const float2 kk = *(const float2 *)(m + W + E * p);
-      o.q[0] = qq.x, o.q[1] = qq.y;
-      o.k[0] = kk.x, o.k[1] = kk.y;
+    for (int e = 0; e < E; e += 4) {
+      const float4 qq = *(const float4 *)(m + E * p + e);
+      const float4 kk = *(const float4 *)(m + W + E * p + e);
+      o.q[e] = qq.x, o.q[e + 1] = qq.y, o.q[e + 2] = qq.z, o.q[e + 3] = qq.w;
+      o.k[e] = kk.x, o.k[e + 1] = kk.y, o.k[e + 2] = kk.z, o.k[e + 3] = kk.w;
     }
     o.v = m[2 * W + j];
-    o.beta = a.beta[row * a.Hl + h];
-    o.g = a.g[row * a.Hl + h];
+  };
+  // beta, g of positions t0 .. t0 + NPF - 1 in lanes 0 .. NPF - 1
+  auto fetch_bg = [&](int t0, float &bb, float &gg) {
+    const int64_t row = (int64_t)b * a.S + min(t0 + (lane & (NPF - 1)), a.S - 1);
+    bb = a.beta[row * a.Hl + h];
+    gg = a.g[row * a.Hl + h];
   };
   float st[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) st[e] = 0.f;
-  auto step = [&](const Vals &c, int pos) {
-    float pp = 0.f;
+  auto step = [&](const Vals &c, float beta, float g, int pos) {
+    float ak[2] = {0.f, 0.f}, aq[2] = {0.f, 0.f}, kq[2] = {0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      st[e] *= c.g;
-      pp += st[e] * c.k[e];
+      ak[e & 1] += st[e] * c.k[e];
+      aq[e & 1] += st[e] * c.q[e];
+      kq[e & 1] += c.k[e] * c.q[e];
     }
-    const float delta = (c.v - row_sum16(pp)) * c.beta;
-    float po = 0.f;
+    float sk = ak[0] + ak[1], sq = aq[0] + aq[1], skq = kq[0] + kq[1];
+    sk += dpp_rot<0x128>(sk), sq += dpp_rot<0x128>(sq), skq += dpp_rot<0x128>(skq);
+    sk += dpp_rot<0x124>(sk), sq += dpp_rot<0x124>(sq), skq += dpp_rot<0x124>(skq);
+    sk += dpp_rot<0x4e>(sk), sq += dpp_rot<0x4e>(sq), skq += dpp_rot<0x4e>(skq);
+    sk += dpp_rot<0xb1>(sk), sq += dpp_rot<0xb1>(sq), skq += dpp_rot<0xb1>(skq);
+    const float delta = (c.v - g * sk) * beta;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      st[e] += c.k[e] * delta;
-      po += st[e] * c.q[e];
-    }
-    const float o = row_sum16(po);
-    if (p == 0) a.out[((int64_t)b * a.S + pos) * W + (int64_t)h * DL + j] = o;
+    for (int e = 0; e < E; ++e) st[e] = g * st[e] + c.k[e] * delta;
+    if (p == 0) a.out[((int64_t)b * a.S + pos) * W + (int64_t)h * DL + j] = g * sq + delta * skq;
+  };
+  auto lane_value = [](float v, int i) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), i));
   };
   Vals buf[NPF];
 #pragma unroll
   for (int i = 0; i < NPF; ++i) fetch(min(i, a.S - 1), buf[i]);
+  float bcur, gcur;
+  fetch_bg(0, bcur, gcur);
   int t0 = 0;
   for (; t0 + NPF <= a.S; t0 += NPF) {
+    float bnext, gnext;
+    fetch_bg(t0 + NPF, bnext, gnext);
 #pragma unroll
     for (int i = 0; i < NPF; ++i) {
       const Vals cur = buf[i];
       fetch(min(t0 + i + NPF, a.S - 1), buf[i]);
-      step(cur, t0 + i);
+      step(cur, lane_value(bcur, i), lane_value(gcur, i), t0 + i);
     }
+    bcur = bnext, gcur = gnext;
   }
 #pragma unroll
   for (int i = 0; i < NPF; ++i)
-    if (t0 + i < a.S) step(buf[i], t0 + i);
+    if (t0 + i < a.S) step(buf[i], lane_value(bcur, i), lane_value(gcur, i), t0 + i);
 }
 
 // 256 threads = 16 columns x 16 lanes; grid B * Hl * DL / 16.
@@ -586,7 +603,6 @@ __device__ void delta_rule_rows(const Q35DeltaArgs &a) {
   extern "C" __global__ void __launch_bounds__(256) rxw8_q35_delta_rule_d##DL(Q35DeltaArgs a) { \
     delta_rule_rows<DL>(a);                                                        \
   }
-RXW8_Q35_DELTA_ROWS(32)
 RXW8_Q35_DELTA_ROWS(64)
 RXW8_Q35_DELTA_ROWS(128)
 

@@ -100,6 +100,7 @@ struct LinearF32Args {
   float *y;
   int T, N, K, G;
   int y_mode;
+  int tiles;
 };
 
 struct KvUpdateArgs {
@@ -423,12 +424,16 @@ static int run_linear_f32(Runtime *rt, const float *x, const uint8_t *w, const f
   for (int R : {M > 16 ? 2 : 1, 1}) {
     const size_t lds = (size_t)2 * 16 * R * (K + 8) * 2 + (size_t)16 * WV * ng * 4;
     if (lds > rt->lds_max) continue;
-    LinearF32Args a{x, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode};
     const int64_t gy = (M + 16 * R - 1) / (16 * R);
     if (gy > 65535) return RXW8_UNIMPLEMENTED;
+    // several channel tiles per workgroup when there are many row tiles, so
+    // the staged rows of x are reused (about 2048 workgroups in all)
+    const int64_t ntiles = (N + 16 * WV - 1) / (16 * WV);
+    const int64_t per = std::max<int64_t>(1, std::min<int64_t>(16, ntiles * gy / 2048));
+    LinearF32Args a{x, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode, (int)per};
     char kname[40];
     std::snprintf(kname, sizeof kname, "rxw8_linear_f32_mfma_r%d_w%d", R, WV);
-    return launch(rt, kname, dim3((unsigned)((N + 16 * WV - 1) / (16 * WV)), (unsigned)gy),
+    return launch(rt, kname, dim3((unsigned)((ntiles + per - 1) / per), (unsigned)gy),
                   dim3(64 * WV), a, lds);
   }
   return RXW8_UNIMPLEMENTED;

@@ -486,9 +486,9 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   Q35DeltaArgs da{m->mixed, m->beta, m->g, m->dout, (int)B, (int)S, (int)m->Hl};
   char kname[40];
   std::snprintf(kname, sizeof kname, "rxw8_q35_delta_rule_d%d", (int)m->Dl);
-  // Dl <= 16: one workgroup of Dl threads per (sequence, head), one column per
-  // thread; Dl >= 32: 16 lanes per column, Dl / 16 workgroups of 256 threads
-  const bool rows = m->Dl >= 32;
+  // Dl <= 32: one workgroup of Dl threads per (sequence, head), one column per
+  // thread; Dl >= 64: 16 lanes per column, Dl / 16 workgroups of 256 threads
+  const bool rows = m->Dl >= 64;
   const dim3 grid((unsigned)(B * m->Hl * (rows ? m->Dl / 16 : 1)));
   if ((rc = launch(rt, kname, grid, dim3(rows ? 256u : (unsigned)m->Dl), da))) return rc;
   // gated RMSNorm over each (token, head) row of Dl: plain weight, times silu(z)
