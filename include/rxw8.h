@@ -334,6 +334,33 @@ int rxw8_qwen35_bind_parameter(rxw8_qwen35 *m, const char *path,
  * FAILED_PRECONDITION while a parameter is unbound. */
 int rxw8_qwen35_forward(rxw8_qwen35 *m, rxw8_buffer *ids, rxw8_buffer *logits);
 
+/* ---- XLA GPU custom-call handlers ------------------------------------------
+ * For a PJRT plugin's GPU custom-call registration
+ * (crates/rxla-pjrt/src/runtime.rs:380-428, GpuCustomCallApi::Legacy) of the
+ * calls the reference appends with CustomCall (crates/rxla-core/src/
+ * tensor_handle.rs:276-345, api_version 2 = status-returning). XLA's untyped
+ * GPU signature: `stream` is the hipStream_t of the call, `buffers` the
+ * operand device pointers in order and then the result's, `opaque` the
+ * backend_config text ("key=value;..."), `status` XLA's XlaCustomCallStatus*
+ * (failures are reported through XlaCustomCallStatusSetFailure when the
+ * process exports it, and always through rxw8_last_error; nothing launches).
+ * Each runs the matching `_into` entry point on the current device.
+ *   rxw8_quantized_linear: [x [m,k], weight U8 [n,k], scale F32 [n,k/g]] ->
+ *     y [m,n]; keys m, n, k, g, x, y (dtype names f32 / bf16), compute
+ *     (bf16 by default, or f32).
+ *   rxw8_gqa_decode: [q [b,hq,d], k_cache, v_cache [b,hkv,lmax,d], lens I32
+ *     [b]] -> out [b,hq,d]; keys b, hq, hkv, lmax, d, q, cache, out, scale
+ *     (optional; 1/sqrt(d) when absent).
+ *   rxw8_gqa_prefill: [q [b,s,hq,d], k_cache, v_cache BF16 [b,hkv,lmax,d],
+ *     starts I32 [b]] -> out [b,s,hq,d]; keys b, s, hq, hkv, lmax, d (128),
+ *     q, out, scale (optional). */
+void rxw8_xla_quantized_linear(void *stream, void **buffers, const char *opaque,
+                               size_t opaque_len, void *status);
+void rxw8_xla_gqa_decode(void *stream, void **buffers, const char *opaque,
+                         size_t opaque_len, void *status);
+void rxw8_xla_gqa_prefill(void *stream, void **buffers, const char *opaque,
+                          size_t opaque_len, void *status);
+
 #ifdef __cplusplus
 }
 #endif

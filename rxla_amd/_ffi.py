@@ -32,6 +32,7 @@ EXPORTS = [
     "rxw8_decoder_forward", "rxw8_decoder_generate", "rxw8_decoder_lens",
     "rxw8_qwen35_create", "rxw8_qwen35_destroy", "rxw8_qwen35_num_parameters",
     "rxw8_qwen35_parameter_info", "rxw8_qwen35_bind_parameter", "rxw8_qwen35_forward",
+    "rxw8_xla_quantized_linear", "rxw8_xla_gqa_decode", "rxw8_xla_gqa_prefill",
 ]
 
 
@@ -112,6 +113,9 @@ def _declare(L):
                                                i64p, POINTER(c_int)]),
         "rxw8_qwen35_bind_parameter": (c_int, [vp, c_char_p, vp]),
         "rxw8_qwen35_forward": (c_int, [vp, vp, vp]),
+        "rxw8_xla_quantized_linear": (None, [vp, POINTER(vp), c_char_p, c_size_t, vp]),
+        "rxw8_xla_gqa_decode": (None, [vp, POINTER(vp), c_char_p, c_size_t, vp]),
+        "rxw8_xla_gqa_prefill": (None, [vp, POINTER(vp), c_char_p, c_size_t, vp]),
     }
     for name, (res, args) in sigs.items():
         f = getattr(L, name)

@@ -266,15 +266,20 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
     if (t + 1 < ntiles) load_tile(t + 1);
     if (16 * t <= q0 + 15) {  // some key of the tile is visible to this wave's queries
       const float *kt = attn_lds + (2 * buf) * TILE + col * KS + DC * j;
-      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+      // four independent accumulators keep the MFMA pipe busy (no chain of
+      // D / 4 dependent MFMAs)
+      f32x4 s4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s4[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < DC; c += 4) {
         const float4 kk = *(const float4 *)(kt + c);
-        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c], kk.x, sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 1], kk.y, sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 2], kk.z, sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 3], kk.w, sc, 0, 0, 0);
+        s4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c], kk.x, s4[0], 0, 0, 0);
+        s4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 1], kk.y, s4[1], 0, 0, 0);
+        s4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 2], kk.z, s4[2], 0, 0, 0);
+        s4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qreg[c + 3], kk.w, s4[3], 0, 0, 0);
       }
+      const f32x4 sc = (s4[0] + s4[1]) + (s4[2] + s4[3]);
       const int key = 16 * t + col;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
