@@ -537,12 +537,16 @@ struct PrefillArgs {
 namespace {
 
 constexpr int PKB = 64;        // keys per block
-constexpr int VROW = PKB + 4;  // V^T row pitch (elements): 136 B, 8-byte aligned reads
+// V^T row pitch (elements): 144 B. A 4-key (8-byte) write per (d, key group)
+// puts 16 key groups of one d row in 128 contiguous bytes and the next d row
+// 32 banks further, so a half-wave of writes is conflict-free.
+constexpr int VROW = PKB + 8;
+// LDS bytes: K and V^T blocks, double-buffered
+constexpr int PREFILL_LDS = 2 * (PKB * D + D * VROW) * 2;
 
 template <int G>
 __device__ void attn_prefill(const PrefillArgs &a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[PKB * D];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VROW];
+  extern __shared__ __attribute__((aligned(16))) uint16_t pf_lds[];  // [2][K block | V^T block]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, g4 = lane >> 4;
   const int per_qb = a.B * a.Hkv;
@@ -598,41 +602,53 @@ __device__ void attn_prefill(const PrefillArgs &a) {
     for (int dt = 0; dt < 8; ++dt) o[h][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // block staging: thread chunk q = tid + 256 u is (key q / 16, 16-byte chunk q % 16)
+  // block staging. K: thread chunk q = tid + 256 u is (key q / 16, 16-byte
+  // chunk q % 16). V: thread t holds keys 4 (t % 16) .. + 3 of the 8 dims of
+  // chunk t / 16, written as one 8-byte V^T entry (4 keys) per dim.
   u32x4 kreg[4], vreg[4];
   auto gload = [&](int blk) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int qc = threadIdx.x + 256 * u;
       const int key = blk * PKB + (qc >> 4);
-      const int64_t off = kv_base + (int64_t)key * D + (qc & 15) * 8;
       const bool ok = key < kv_end;
-      kreg[u] = ok ? *(const u32x4 *)(a.kc + off) : u32x4{0, 0, 0, 0};
-      vreg[u] = ok ? *(const u32x4 *)(a.vc + off) : u32x4{0, 0, 0, 0};
+      kreg[u] = ok ? *(const u32x4 *)(a.kc + kv_base + (int64_t)key * D + (qc & 15) * 8)
+                   : u32x4{0, 0, 0, 0};
+      const int vkey = blk * PKB + 4 * (threadIdx.x & 15) + u;
+      vreg[u] = vkey < kv_end
+                    ? *(const u32x4 *)(a.vc + kv_base + (int64_t)vkey * D + (threadIdx.x >> 4) * 8)
+                    : u32x4{0, 0, 0, 0};
     }
   };
-  auto lds_store = [&]() {
+  auto lds_store = [&](int buf) {
+    uint16_t *ks_lds = pf_lds + buf * (PKB * D + D * VROW);
+    uint16_t *vt_lds = ks_lds + PKB * D;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int qc = threadIdx.x + 256 * u;
       const int r = qc >> 4, c = qc & 15;
       *(u32x4 *)(ks_lds + r * D + ((c ^ (r & 15)) << 3)) = kreg[u];
+    }
+    const int c = threadIdx.x >> 4, k4 = 4 * (threadIdx.x & 15);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt_lds[(8 * c + 2 * e) * VROW + r] = (uint16_t)(vreg[u][e] & 0xffffu);
-        vt_lds[(8 * c + 2 * e + 1) * VROW + r] = (uint16_t)(vreg[u][e] >> 16);
-      }
+    for (int e = 0; e < 8; ++e) {
+      const int sh = 16 * (e & 1);
+      const uint32_t k0 = (vreg[0][e >> 1] >> sh) & 0xffffu, k1 = (vreg[1][e >> 1] >> sh) & 0xffffu;
+      const uint32_t k2 = (vreg[2][e >> 1] >> sh) & 0xffffu, k3 = (vreg[3][e >> 1] >> sh) & 0xffffu;
+      *(uint2 *)(vt_lds + (8 * c + e) * VROW + k4) = uint2{k0 | (k1 << 16), k2 | (k3 << 16)};
     }
   };
 
   gload(0);
+  lds_store(0);
+  __syncthreads();
   for (int blk = 0; blk < nblk; ++blk) {
-    __syncthreads();  // every wave is done reading the previous block
-    lds_store();
-    __syncthreads();
-    if (blk + 1 < nblk) gload(blk + 1);
+    const int buf = blk & 1;
+    const uint16_t *ks_lds = pf_lds + buf * (PKB * D + D * VROW);
+    const uint16_t *vt_lds = ks_lds + PKB * D;
+    if (blk + 1 < nblk) gload(blk + 1);  // in flight while this block is used
     const int j0 = blk * PKB;
-    if (j0 > wave_last) continue;  // wave-uniform: every key of the block is in this wave's future
+    if (j0 <= wave_last) {  // wave-uniform: else every key of the block is in this wave's future
     // S^T tiles: s[h][kt] lane (key j0 + 16 kt + 4 g4 + i, row col)
     f32x4 s[G][4];
 #pragma unroll
@@ -701,6 +717,10 @@ __device__ void attn_prefill(const PrefillArgs &a) {
 #pragma unroll
         for (int h = 0; h < G; ++h) o[h][dt] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[h][ks]), o[h][dt]);
       }
+    }
+    // the other buffer was last read in the previous block, before the barrier
+    if (blk + 1 < nblk) lds_store(buf ^ 1);
+    __syncthreads();
   }
   if (i0 + col >= a.S) return;
 #pragma unroll

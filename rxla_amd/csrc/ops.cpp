@@ -765,7 +765,9 @@ int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t 
   a.out_f32 = out_f32;
   char kname[48];
   std::snprintf(kname, sizeof kname, "rxw8_gqa_prefill_d128_g%d", (int)(Hq / Hkv));
-  return launch(rt, kname, dim3((unsigned)(a.nqb * B * Hkv)), dim3(256), a);
+  // K and V^T blocks of 64 keys, double-buffered (2 x (64*128 + 128*72) bf16)
+  constexpr size_t lds = 2 * (64 * 128 + 128 * 72) * 2;
+  return launch(rt, kname, dim3((unsigned)(a.nqb * B * Hkv)), dim3(256), a, lds);
 }
 
 
