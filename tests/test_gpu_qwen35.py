@@ -202,6 +202,25 @@ def test_checkpoint_loads_verbatim(rt, tmp_path):
     assert "group_size" in str(e.value)
 
 
+def test_checkpoint_validation_happens_before_upload(rt, tmp_path):
+    r = rx()
+    cfg = CONFIGS["small"]
+    p = q35.random_params(cfg, seed=41)
+    pre = "model.language_model.layers."
+    ck = {k: ("U8" if v.dtype == np.uint8 else "F32", v) for k, v in p.items()}
+    del ck[pre + "1.self_attn.k_norm.weight"]
+    key = pre + "0.linear_attn.conv1d.weight"
+    ck[key] = ("F32", ck[key][1][:-1])  # one channel short
+    bad = tmp_path / "bad.safetensors"
+    stf.write(bad, ck)
+    m = r.Qwen35Model(rt, model_config(cfg)).compile()
+    with pytest.raises(r.Error) as e:
+        m.load_safetensors(bad)
+    assert e.value.code == r.Status.INVALID_ARGUMENT
+    assert "k_norm" in str(e.value) and "conv1d" in str(e.value)
+    assert m._bound == []  # nothing was uploaded or bound
+
+
 def test_error_contract(rt):
     r = rx()
     cfg = dict(CONFIGS["tiny"], max_positions=16)
