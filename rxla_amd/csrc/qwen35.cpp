@@ -471,6 +471,16 @@ int mlp(Qwen35 *m, const Layer &L, int64_t T) {
   return residual(m, L.down_pk, L.down, m->act, 0, T, m->ss_down);
 }
 
+// gated RMSNorm over each (token, head) row of Dl (plain weight, times
+// silu(z); row r = (t, head) takes z at raw + t * n_in + head * Dl), then out_proj.
+int finish_linear(Qwen35 *m, const Layer &L, int64_t T, const uint16_t *zp) {
+  int rc;
+  if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, false, zp, L.n_in,
+                 m->Hl)))
+    return rc;
+  return out_proj(m, L, L.out, m->gated, 0, T);
+}
+
 int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   Runtime *rt = m->rt;
   const int64_t T = B * S;
@@ -491,12 +501,7 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   const bool rows = m->Dl >= 64;
   const dim3 grid((unsigned)(B * m->Hl * (rows ? m->Dl / 16 : 1)));
   if ((rc = launch(rt, kname, grid, dim3(rows ? 256u : (unsigned)m->Dl), da))) return rc;
-  // gated RMSNorm over each (token, head) row of Dl: plain weight, times silu(z)
-  // row r = (t, head): z of token t at raw + t * n_in + head * Dl
-  if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, false, zp, L.n_in,
-                 m->Hl)))
-    return rc;
-  return out_proj(m, L, L.out, m->gated, 0, T);
+  return finish_linear(m, L, T, zp);
 }
 
 int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {

@@ -47,6 +47,8 @@ CONFIGS["mid"] = dict(q35.config(vocab=1000, hidden=512, intermediate=1024,
                                  group=128), max_batch=2, max_seq=64, std=0.03)
 CONFIGS["wide_linear"] = dict(CONFIGS["wide"], layers=[q35.LINEAR], max_seq=256)
 CONFIGS["small_mha"] = dict(CONFIGS["small"], kv_heads=4, layers=[q35.FULL, q35.LINEAR])  # G = 1
+# sequences of >= 128 positions take the chunked delta rule (Dl 64 and 128)
+CONFIGS["mid_long"] = dict(CONFIGS["mid"], layers=[q35.LINEAR, q35.FULL], max_seq=200)
 CONFIGS["wide_full"] = dict(CONFIGS["wide"], layers=[q35.FULL], max_seq=80)
 
 
@@ -80,6 +82,7 @@ def run(rt, m, ids):
                                       ("small", 1, 1), ("mid", 2, 37), ("mid", 1, 64),
                                       ("small_mha", 2, 45), ("wide_linear", 1, 16),
                                       ("wide_linear", 1, 203), ("wide_full", 1, 77),
+                                      ("mid_long", 2, 150), ("mid_long", 1, 200),
                                       ("wide_full", 1, 16), ("wide", 1, 16), ("wide", 1, 32)])
 def test_logits_match_the_oracle(rt, name, b, s):
     cfg = CONFIGS[name]
