@@ -184,7 +184,12 @@ struct Q35AttnArgs {
   const float *kc, *vc;  // [B, Hkv, Lmax, D]
   const float *gate;     // [T, Hq * D] output gate (layers.rs:93-94), multiplied in at the store
   float *out;            // [T, Hq * D]
-  int S, Hq, Hkv, Lmax, qtiles;
+  // nsplit > 1: each (sequence, kv head, query tile) is split into nsplit
+  // ranges of key tiles; every range writes its unnormalised rows
+  // [m, l, o[D]] to part[((t * Hq + h) * nsplit + split)] and
+  // rxw8_q35_attention_combine merges them (and applies the gate)
+  float *part;
+  int B, S, Hq, Hkv, Lmax, qtiles, nsplit;
   float scale;
 };
 
@@ -212,13 +217,18 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
   const int j = lane >> 4, col = lane & 15;
   const int G = a.Hq / a.Hkv, sub = 4 / G;
   int blk = blockIdx.x;
+  const int split = blk % a.nsplit;
+  blk /= a.nsplit;
   const int qt = a.qtiles - 1 - blk % a.qtiles;  // longest tiles first
   blk /= a.qtiles;
   const int hk = blk % a.Hkv, b = blk / a.Hkv;
   const int h = hk * G + wv % G;
   const int q0 = (qt * sub + wv / G) * 16;
   const int last_q = min(a.S, (qt + 1) * sub * 16) - 1;
-  const int ntiles = last_q / 16 + 1;
+  const int all_tiles = last_q / 16 + 1;
+  const int per = (all_tiles + a.nsplit - 1) / a.nsplit;
+  const int t_begin = split * per;
+  const int ntiles = min(all_tiles, t_begin + per);  // this split walks tiles [t_begin, ntiles)
   const float *kbase = a.kc + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
   const float *vbase = a.vc + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
   // q rows of this wave (clamped to S - 1 for loads; rows >= S are not stored)
@@ -258,11 +268,13 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) m[i] = -__builtin_huge_valf(), l[i] = 0.f;
   float *pw = plds + wv * 16 * PS;
-  load_tile(0);
-  store_tile(0);
+  if (t_begin < ntiles) {
+    load_tile(t_begin);
+    store_tile(0);
+  }
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
+  for (int t = t_begin; t < ntiles; ++t) {
+    const int buf = (t - t_begin) & 1;
     if (t + 1 < ntiles) load_tile(t + 1);
     if (16 * t <= q0 + 15) {  // some key of the tile is visible to this wave's queries
       const float *kt = attn_lds + (2 * buf) * TILE + col * KS + DC * j;
@@ -286,8 +298,9 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
         const int qpos = q0 + 4 * j + i;
         const float s_ = key <= qpos ? sc[i] * a.scale : -__builtin_huge_valf();
         const float mn = fmaxf(m[i], row_max16(s_));
-        const float alpha = __expf(m[i] - mn);
-        const float pv = __expf(s_ - mn);
+        // a split may start at tiles where a row sees no key yet (m, mn = -inf)
+        const float alpha = m[i] == -__builtin_huge_valf() ? 0.f : __expf(m[i] - mn);
+        const float pv = mn == -__builtin_huge_valf() ? 0.f : __expf(s_ - mn);
         l[i] = l[i] * alpha + row_add16(pv);
         m[i] = mn;
 #pragma unroll
@@ -310,6 +323,19 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
     if (t + 1 < ntiles) store_tile(buf ^ 1);
     __syncthreads();
   }
+  if (a.nsplit > 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qpos = q0 + 4 * j + i;
+      if (qpos < a.S) {
+        float *pp = a.part + ((((int64_t)b * a.S + qpos) * a.Hq + h) * a.nsplit + split) * (2 + D);
+        if (col == 0) pp[0] = m[i], pp[1] = l[i];
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) pp[2 + 16 * dt + col] = o[dt][i];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int qpos = q0 + 4 * j + i;
@@ -322,9 +348,38 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
   }
 }
 
+// Merge of the key-range splits of one (token, query head) row, split order:
+// out = gate * sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s. One wave per row.
+template <int D>
+__device__ void q35_attention_combine(const Q35AttnArgs &a) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // t * Hq + h
+  if (row >= (int64_t)a.B * a.S * a.Hq) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const float *pp = a.part + row * a.nsplit * (2 + D);
+  float M = -__builtin_huge_valf();
+  for (int sp = 0; sp < a.nsplit; ++sp) M = fmaxf(M, pp[sp * (2 + D)]);
+  float L = 0.f, o[D / 64];
+#pragma unroll
+  for (int e = 0; e < D / 64; ++e) o[e] = 0.f;
+  for (int sp = 0; sp < a.nsplit; ++sp) {
+    const float ms = pp[sp * (2 + D)];
+    const float f = ms == -__builtin_huge_valf() ? 0.f : __expf(ms - M);
+    L += f * pp[sp * (2 + D) + 1];
+#pragma unroll
+    for (int e = 0; e < D / 64; ++e) o[e] += f * pp[sp * (2 + D) + 2 + 64 * e + lane];
+  }
+  const float inv = 1.0f / L;
+  const int64_t off = row * D;  // [T, Hq * D] = row-major (t * Hq + h) * D
+#pragma unroll
+  for (int e = 0; e < D / 64; ++e) a.out[off + 64 * e + lane] = (o[e] * inv) * a.gate[off + 64 * e + lane];
+}
+
 #define RXW8_Q35_ATTN(D)                                                                    \
   extern "C" __global__ void __launch_bounds__(256) rxw8_q35_attention_d##D(Q35AttnArgs a) { \
     q35_attention<D>(a);                                                                    \
+  }                                                                                         \
+  extern "C" __global__ void __launch_bounds__(256) rxw8_q35_attention_combine_d##D(Q35AttnArgs a) { \
+    q35_attention_combine<D>(a);                                                            \
   }
 RXW8_Q35_ATTN(64)
 RXW8_Q35_ATTN(128)

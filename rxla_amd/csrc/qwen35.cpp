@@ -86,7 +86,8 @@ struct Q35FaPrepArgs {
 struct Q35AttnArgs {
   const float *q, *kc, *vc, *gate;
   float *out;
-  int S, Hq, Hkv, Lmax, qtiles;
+  float *part;
+  int B, S, Hq, Hkv, Lmax, qtiles, nsplit;
   float scale;
 };
 struct Q35MulArgs {
@@ -146,6 +147,8 @@ struct Q35LoraArgs {
   float alpha;      // y = x w^T (accumulate == 0) or y += alpha * x w^T
   int accumulate;
 };
+
+constexpr int kAttnMaxSplit = 4;  // key-range splits of the full attention (at most)
 
 unsigned grid_n(int64_t n, int64_t cap = 1 << 16) {
   int64_t g = (n + 255) / 256;
@@ -215,6 +218,7 @@ struct Qwen35 {
   float *mixed = nullptr, *beta = nullptr, *g = nullptr, *dout = nullptr;
   // full layers
   float *q = nullptr, *gate = nullptr, *att = nullptr, *kc = nullptr, *vc = nullptr;
+  float *attn_part = nullptr;  // key-range split partials [T, Hq, splits, 2 + D]
   // MLP: [gate | up] projection [T, 2I], SwiGLU output [T, I]
   uint16_t *gu = nullptr, *act = nullptr;
 
@@ -343,6 +347,7 @@ int allocate(Qwen35 *m) {
     c.add(&m->q, T * m->Hq * m->D);
     c.add(&m->gate, T * m->Hq * m->D);
     c.add(&m->att, T * m->Hq * m->D);
+    c.add(&m->attn_part, T * m->Hq * kAttnMaxSplit * (2 + m->D));
     c.add(&m->kc, m->Bmax * m->Hkv * m->Smax * m->D);
     c.add(&m->vc, m->Bmax * m->Hkv * m->Smax * m->D);
   }
@@ -521,13 +526,22 @@ int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   if ((m->D == 64 || m->D == 128 || m->D == 256) && 4 % G == 0) {
     // f32 matrix-core flash attention: 4 waves per (sequence, kv head, query tile)
     const int64_t qtiles = (S + 16 * (4 / G) - 1) / (16 * (4 / G));
-    Q35AttnArgs at{m->q, m->kc, m->vc, m->gate, m->att, (int)S, (int)m->Hq, (int)m->Hkv,
-                   (int)m->Smax, (int)qtiles, scale};
+    // key-range splits when the (sequence, kv head, query tile) workgroups
+    // alone leave CUs idle and the longest tile walks at least 8 key tiles
+    const int64_t base = B * m->Hkv * qtiles, longest = (S + 15) / 16;
+    int64_t nsplit = 1;
+    while (nsplit < kAttnMaxSplit && base * nsplit < 2 * rt->cus && longest >= 8 * nsplit) nsplit *= 2;
+    Q35AttnArgs at{m->q, m->kc, m->vc, m->gate, m->att, m->attn_part, (int)B, (int)S, (int)m->Hq,
+                   (int)m->Hkv, (int)m->Smax, (int)qtiles, (int)nsplit, scale};
     const size_t lds = (size_t)4 * 16 * (m->D + 4) * 4 + 4 * 16 * 20 * 4;
-    char an[40];
+    char an[48];
     std::snprintf(an, sizeof an, "rxw8_q35_attention_d%d", (int)m->D);
-    // the kernel multiplies its output by the gate
-    if ((rc = launch(rt, an, dim3((unsigned)(B * m->Hkv * qtiles)), dim3(256), at, lds))) return rc;
+    // the kernel (or the combine) multiplies the output by the gate
+    if ((rc = launch(rt, an, dim3((unsigned)(base * nsplit)), dim3(256), at, lds))) return rc;
+    if (nsplit > 1) {
+      std::snprintf(an, sizeof an, "rxw8_q35_attention_combine_d%d", (int)m->D);
+      if ((rc = launch(rt, an, dim3((unsigned)((T * m->Hq + 3) / 4)), dim3(256), at))) return rc;
+    }
   } else {
     if ((rc = attention_launch(rt, m->q, 1, m->kc, m->vc, 1, m->row_len, m->row_seq, nullptr, 0, 0,
                                m->att, 1, T, m->Hq, m->Hkv, m->Smax, m->D, scale, nullptr)))

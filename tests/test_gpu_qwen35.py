@@ -49,7 +49,7 @@ CONFIGS["wide_linear"] = dict(CONFIGS["wide"], layers=[q35.LINEAR], max_seq=256)
 CONFIGS["small_mha"] = dict(CONFIGS["small"], kv_heads=4, layers=[q35.FULL, q35.LINEAR])  # G = 1
 # sequences of >= 128 positions take the chunked delta rule (Dl 64 and 128)
 CONFIGS["mid_long"] = dict(CONFIGS["mid"], layers=[q35.LINEAR, q35.FULL], max_seq=200)
-CONFIGS["wide_full"] = dict(CONFIGS["wide"], layers=[q35.FULL], max_seq=80)
+CONFIGS["wide_full"] = dict(CONFIGS["wide"], layers=[q35.FULL], max_seq=160)
 
 
 def model_config(cfg):
@@ -82,6 +82,7 @@ def run(rt, m, ids):
                                       ("small", 1, 1), ("mid", 2, 37), ("mid", 1, 64),
                                       ("small_mha", 2, 45), ("wide_linear", 1, 16),
                                       ("wide_linear", 1, 203), ("wide_full", 1, 77),
+                                      ("wide_full", 1, 160),
                                       ("mid_long", 2, 150), ("mid_long", 1, 200),
                                       ("wide_full", 1, 16), ("wide", 1, 16), ("wide", 1, 32)])
 def test_logits_match_the_oracle(rt, name, b, s):
