@@ -19,7 +19,9 @@ roofline     = the GEMV kernel of the largest sweep shape, B=1 N=24576
                bytes per launch recorded in profiles/ by two rocprofv3 --pmc
                passes (FETCH_SIZE, WRITE_SIZE) over `bench.py --pmc-probe gemv`
 cpu_baseline = the CPU oracle (reference-order restatement, OpenMP) timed on
-               this host over a bounded sample of the same sweep
+               this host over a bounded sample of the same sweep; its
+               "decoder" entry times 8 full-size C5 decode steps (batch 8,
+               caches at 1024 positions) through the oracle decoder
 
 Algorithmic bytes per launch: N*K (u8 weights) + 4*N (f32 scales)
 + 2*B*K (bf16 x) + 2*B*N (bf16 y).
@@ -107,6 +109,54 @@ def cpu_baseline(budget_s=12.0):
             "sample": f"{passes} pass(es) of the 9-shape sweep (B in {list(BS)}, N in {list(NS)}, "
                       f"K={K}) through oracle.quantized_linear (bf16 compute, f32 accumulation), "
                       f"{total_t:.1f} s"}
+
+
+def cpu_decoder_baseline(steps=8, ctx=1024, batch=8, seed=11):
+    """C5 on the CPU: the oracle decoder (reference-order C restatement, OpenMP)
+    at full size, timing `steps` greedy decode steps (after one untimed step) of
+    `batch` sequences whose caches already hold `ctx` positions (zero K/V: the prompt's 8 x 1024 prefill
+    is 28 TFLOP, beyond a bounded CPU sample). Weights are random W8 codes and
+    scales and a random bf16 embedding (values do not change the work)."""
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    cfg = dict(layers=28, hidden=2048, q_heads=16, kv_heads=8, head_dim=128, intermediate=6144,
+               vocab=151936, max_seq=ctx + steps + 1, group=0, eps=1e-6, theta=1e6, qk_norm=True)
+    rng = np.random.default_rng(seed)
+    H, D, I, V = cfg["hidden"], cfg["head_dim"], cfg["intermediate"], cfg["vocab"]
+    qkv = (cfg["q_heads"] + 2 * cfg["kv_heads"]) * D
+
+    def codes(n, k):
+        return rng.integers(0, 256, (n, k), dtype=np.uint8)
+
+    def scales(n, k):
+        return (rng.random((n, 1), np.float32) * 1e-3 + 1e-4).astype(np.float32)
+
+    p = {"embed_tokens.weight": rng.integers(0x3C00, 0x4000, (V, H), dtype=np.uint16),
+         "norm.weight": np.ones(H, np.float32)}
+    for l in range(cfg["layers"]):
+        pre = f"layers.{l}."
+        p[pre + "input_layernorm.weight"] = np.ones(H, np.float32)
+        p[pre + "post_attention_layernorm.weight"] = np.ones(H, np.float32)
+        p[pre + "self_attn.q_norm.weight"] = np.ones(D, np.float32)
+        p[pre + "self_attn.k_norm.weight"] = np.ones(D, np.float32)
+        for name, n, k in (("self_attn.qkv_proj", qkv, H), ("self_attn.o_proj", H, H),
+                           ("mlp.gate_up_proj", 2 * I, H), ("mlp.down_proj", H, I)):
+            p[pre + name + ".weight"], p[pre + name + ".scale"] = codes(n, k), scales(n, k)
+    dec = oracle.Decoder(cfg, p, batch)
+    dec.lens[:] = ctx
+    ids = rng.integers(0, V, (batch, 1)).astype(np.int32)
+    _, nxt = dec.forward(ids, threads=threads)  # untimed: first touch of the caches
+    ids = nxt.reshape(batch, 1)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, nxt = dec.forward(ids, threads=threads)
+        ids = nxt.reshape(batch, 1)
+    dt = time.perf_counter() - t0
+    return {"decode_tokens_per_s": round(batch * steps / dt, 2), "ms_per_step": round(dt / steps * 1e3, 1),
+            "cores": threads, "kind": "port",
+            "sample": f"{steps} greedy decode steps of the 28-layer C5 decoder at full size, batch "
+                      f"{batch}, caches at {ctx} positions, through oracle.Decoder (C, OpenMP)"}
 
 
 def bench_gemm(rt, rx, torch, stream, reps=10):
@@ -614,6 +664,8 @@ def main():
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle) ...")
         out["cpu_baseline"] = cpu_baseline()
+        log("timing the CPU decoder baseline (oracle, C5 decode steps) ...")
+        out["cpu_baseline"]["decoder"] = cpu_decoder_baseline()
     print(json.dumps(out), flush=True)
 
 
