@@ -33,7 +33,7 @@ prefill_gemm  BASELINE configs[2]: x bf16 [M,4096] for M in {512, 2048, 8192}
               around back-to-back launches), roofline against dense bf16 MFMA
 decode_attention  BASELINE configs[3]: batch 8, 32/8 heads, D 128, lengths
               uniform in [512, 8192], bf16 cache; bytes = K and V rows read
-              (lens * 8 heads * 128 * 2 B * 2) + q + out, two cache copies
+              (lens * 8 heads * 128 * 2 B * 2) + q + out, three rotating cache copies
 prefill_attention  the C5 prompt's causal attention (8 x 1024 rows, 16/8
               heads, D 128) on rxw8_gqa_prefill: flops over HIP-event time,
               roofline against dense bf16 MFMA
@@ -109,6 +109,12 @@ def cpu_baseline(budget_s=12.0):
             "sample": f"{passes} pass(es) of the 9-shape sweep (B in {list(BS)}, N in {list(NS)}, "
                       f"K={K}) through oracle.quantized_linear (bf16 compute, f32 accumulation), "
                       f"{total_t:.1f} s"}
+
+
+SPIN_CYCLES = 2_000_000  # torch.cuda._sleep spacer, about 1 ms of shader clocks
+ROOF_CYCLES = 4          # passes over the weight copies per roofline event pair
+MALL_BYTES = 256 << 20   # MI355X last-level (Infinity) cache
+ATTN_COPIES = 3          # rotating KV caches of the C4 leg
 
 
 def cpu_decoder_baseline(steps=8, ctx=1024, batch=8, seed=11):
@@ -210,7 +216,7 @@ def bench_attention(rt, rx, torch, stream, reps=20):
     with torch.cuda.stream(stream):
         caches = [(torch.randn((B, HKV, LMAX, D), device="cuda", generator=gen).to(torch.bfloat16),
                    torch.randn((B, HKV, LMAX, D), device="cuda", generator=gen).to(torch.bfloat16))
-                  for _ in range(2)]
+                  for _ in range(ATTN_COPIES)]
         q = torch.randn((B, HQ, D), device="cuda", generator=gen).to(torch.bfloat16)
         o = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
         lt = torch.from_numpy(lens).to("cuda")
@@ -219,12 +225,14 @@ def bench_attention(rt, rx, torch, stream, reps=20):
     qb, ob, lb = rt.wrap_tensor(q), rt.wrap_tensor(o), rt.wrap_tensor(lt)
     nbytes = int(lens.sum()) * HKV * D * 2 * 2 + 2 * B * HQ * D * 2 + 4 * B
     for c in range(100):
-        rx.grouped_query_attention(rt, qb, cb[c % 2][0], cb[c % 2][1], lb, out=ob)
+        rx.grouped_query_attention(rt, qb, cb[c % ATTN_COPIES][0], cb[c % ATTN_COPIES][1], lb, out=ob)
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(SPIN_CYCLES)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for i in range(reps):
-        rx.grouped_query_attention(rt, qb, cb[i % 2][0], cb[i % 2][1], lb, out=ob)
+        rx.grouped_query_attention(rt, qb, cb[i % ATTN_COPIES][0], cb[i % ATTN_COPIES][1], lb, out=ob)
     e1.record(stream)
     torch.cuda.synchronize()
     t = e0.elapsed_time(e1) * 1e-3 / reps
@@ -233,7 +241,10 @@ def bench_attention(rt, rx, torch, stream, reps=20):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
             "kernels": "rxw8_gqa_decode_d128_g4 + rxw8_gqa_decode_combine_d128_g4",
             "us_per_call": round(t * 1e6, 2), "bytes_per_call": nbytes,
-            "lens": lens.tolist(), "timing": f"HIP events around {reps} calls, 2 cache copies"}
+            "lens": lens.tolist(),
+            "timing": f"HIP events around {reps} back-to-back calls after a spin kernel, "
+                      f"{ATTN_COPIES} rotating cache copies (each call reads ~207 MB, so a "
+                      "copy returns after 400+ MB: none is served from the 256 MB MALL)"}
 
 
 def bench_prefill_attention(rt, rx, torch, stream, reps=10):
@@ -418,10 +429,12 @@ def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, ite
                       f"mean of {iterations}"}
 
 
-def pmc_probe(kind, reps=30):
-    """A short fixed program for rocprofv3 --pmc passes: `reps` launches of one
-    roofline shape plus 4 plain 256 MiB device copies (torch) that calibrate
-    what FETCH_SIZE / WRITE_SIZE read for a known number of bytes."""
+def pmc_probe(kind, rounds=3):
+    """A short fixed program for rocprofv3 runs: the roofline shape launched as
+    the bench times it (`rounds` x [spin spacer, ROOF_CYCLES passes over 6
+    weight copies back to back]) plus 4 plain 256 MiB device copies (torch)
+    that calibrate what FETCH_SIZE / WRITE_SIZE read for a known number of
+    bytes."""
     import torch
     import rxla_amd as rx
 
@@ -444,8 +457,12 @@ def pmc_probe(kind, reps=30):
         wb = [(rx.pack_weight(rt, rt.wrap_tensor(u)), rt.wrap_tensor(s_)) for u, s_ in ws]
         rt.synchronize()
         xb, yb = rt.wrap_tensor(x), rt.wrap_tensor(y)
-        for i in range(reps):
-            rx.quantized_linear(rt, xb, wb[i % 6][0], wb[i % 6][1], rx.DType.BF16, out=yb)
+        for _ in range(rounds):
+            with torch.cuda.stream(stream):
+                torch.cuda._sleep(SPIN_CYCLES)
+            for i in range(ROOF_CYCLES * 6):
+                rx.quantized_linear(rt, xb, wb[i % 6][0], wb[i % 6][1], rx.DType.BF16, out=yb)
+        reps = rounds * ROOF_CYCLES * 6
         log(f"pmc probe gemv B={b} N={n} K={K}: {reps} launches, {gemv_bytes(b, n)} algorithmic B each")
     else:
         raise SystemExit(f"unknown --pmc-probe {kind}")
@@ -556,15 +573,19 @@ def main():
 
     # Kernel durations: per shape, one HIP event pair on the runtime stream
     # around `copies` back-to-back eager launches (one per weight copy), queued
-    # behind a 1 GiB fill so the host submits them all before the GPU reaches
-    # the first event; shapes interleave so no copy is reused from the MALL.
-    spacer = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    # behind a ~1 ms spin kernel (no memory traffic: a fill spacer would leave
+    # dirty cache lines whose write-back lands inside the timed launches) so
+    # the host submits them all before the GPU reaches the first event; shapes
+    # interleave so no copy is reused from the MALL.
+    def spacer():
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(SPIN_CYCLES)
+
     events = []
     rounds = max(3, args.steps // args.copies)
     for _ in range(rounds):
         for b, n in plan:
-            with torch.cuda.stream(stream):
-                spacer.zero_()
+            spacer()
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record(stream)
@@ -573,6 +594,23 @@ def main():
                 rx.quantized_linear(rt, xb[b], u, s, rx.DType.BF16, out=yb[(b, n)])
             e1.record(stream)
             events.append((b, n, e0, e1))
+    # The roofline shape: ROOF_CYCLES passes over the copies per event pair
+    # when each copy's 100 MB is read again only after the other copies have
+    # streamed at least 1.5x the 256 MB MALL (6 copies: 503 MB), so none is
+    # served from it; one pass otherwise.
+    roof_events = []
+    u_roof = [wb[24576][c] for c in range(args.copies)]
+    roof_cycles = ROOF_CYCLES if (args.copies - 1) * 24576 * K >= 1.5 * MALL_BYTES else 1
+    for _ in range(rounds):
+        spacer()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(roof_cycles * args.copies):
+            u, s = u_roof[i % args.copies]
+            rx.quantized_linear(rt, xb[1], u, s, rx.DType.BF16, out=yb[(1, 24576)])
+        e1.record(stream)
+        roof_events.append((e0, e1))
     torch.cuda.synchronize()
     per_launch = lambda e0, e1: e0.elapsed_time(e1) * 1e-3 / args.copies  # noqa: E731
 
@@ -589,7 +627,8 @@ def main():
     mean_bytes, mean_s = kernel_stats(lambda b: b <= 4)
     b16_bytes, b16_s = kernel_stats(lambda b: b > 4)
     # roofline shape: B=1, N=24576 (the largest decode GEMV of the sweep)
-    roof_s = float(np.median(per_shape[(1, 24576)]))
+    roof_s = float(np.median([e0.elapsed_time(e1) * 1e-3 / (roof_cycles * args.copies)
+                              for e0, e1 in roof_events]))
     roof_bytes = gemv_bytes(1, 24576)
     achieved = roof_bytes / roof_s / 1e9
     sweep = {f"B{b}_N{n}": {"us": round(float(np.median(v)) * 1e6, 2),
@@ -625,8 +664,10 @@ def main():
                      "shape": "B=1 N=24576 K=4096", "launch_us": round(roof_s * 1e6, 3),
                      "launch_bytes": roof_bytes,
                      "timing": "median of HIP event pairs on the runtime stream around "
-                               f"{args.copies} back-to-back launches of the shape, divided by "
-                               f"{args.copies} (includes the inter-kernel gaps)",
+                               f"{roof_cycles * args.copies} back-to-back launches of the shape "
+                               f"({roof_cycles} passes over the {args.copies} weight copies, "
+                               "after a spin kernel), divided by the launch count (includes "
+                               "the inter-kernel gaps)",
                      "traffic_source": "profiles/gemv_B1_N24576_traffic.txt (FETCH_SIZE + "
                                        "WRITE_SIZE per launch, copy-calibrated)",
                      "b_le_4_mean": {"achieved": round(mean_bytes / mean_s / 1e9, 2),
