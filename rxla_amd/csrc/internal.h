@@ -103,6 +103,7 @@ struct Runtime {
   Workspace scratch;   // general f32 scratch (attention split-K)
   Workspace xcast;     // bf16 copy of f32 activations ahead of the GEMM
   Workspace wdeq;      // bf16 dequantised weights ahead of the large-M GEMM
+  Workspace attn_counters;  // i32 split arrival counters of decode attention (zeroed once)
 
   hipFunction_t fn(const char *name);
 };

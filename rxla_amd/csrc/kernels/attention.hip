@@ -21,9 +21,12 @@
 // probabilities go through LDS, and P.V runs on the VALU in f32 with each lane
 // owning 8 dims of every fourth key (16-byte V loads, 1 KiB per wave load).
 // Waves merge (max, sum, acc) in LDS. With one split the workgroup writes the
-// output; otherwise every split writes (max, sum, acc) partials and
-// rxw8_gqa_decode_combine merges them in split order in a second launch
-// (deterministic; the kernel boundary makes the partials visible).
+// output; otherwise every split writes (max, sum, acc) partials, which are
+// merged in split order (deterministic) either by the last workgroup of the
+// (row, kv head) to arrive -- device-scope fences around an arrival counter
+// make the other splits' partials visible to it -- or, without counters, by
+// rxw8_gqa_decode_combine in a second launch (the kernel boundary makes the
+// partials visible). Both merges run the same code, so they agree bit for bit.
 #include "common.h"
 
 struct AttnArgs {
@@ -49,6 +52,10 @@ struct AttnArgs {
   const float *q_norm, *k_norm;  // [D] or null
   const float *rope;             // [Lmax, D] RoPE table: cos then sin per position
   float eps;
+  // [R * Hkv] arrival counters (zero between launches), or null: with S > 1
+  // splits the last workgroup of a (row, kv head) to finish merges the
+  // partials itself; null leaves that to rxw8_gqa_decode_combine.
+  int *counters;
 };
 
 namespace {
@@ -117,6 +124,87 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4 &r, float *x) {
   }
 }
 
+// Merge the S split partials of (row, kv head) bh in split order and write
+// the output rows of its G heads. Any workgroup size >= 64 (wave 0 takes the
+// statistics; lane c holds split c's (max, sum); the max and the weighted sum
+// use fixed butterflies, so the result does not depend on who runs it).
+// Split partials: device-coherent (write-through, sc1) stores and loads when
+// the last-arriving workgroup merges them within the launch, plain ones when
+// a second launch does (the kernel boundary then publishes them).
+__device__ __forceinline__ void store_part(float *p, float v, bool coherent) {
+  if (coherent)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *p = v;
+}
+template <bool COH>
+__device__ __forceinline__ float load_part(const float *p) {
+  if constexpr (COH)
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    return *p;
+}
+
+template <int G, bool COH>
+__device__ void combine_pair(const AttnArgs &a, int bh) {
+  constexpr int MAXC = 64;
+  __shared__ float fac[MAXC][G];  // exp(m_c - M) per chunk and head
+  __shared__ float inv_l[G];
+  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
+  const int nchunks = a.max_chunks;  // every split wrote a partial (empty: max -inf)
+  const float *base = a.ws + ((int64_t)bh * a.max_chunks) * G * (2 + D);
+  if (threadIdx.x < 64) {
+    const int c = threadIdx.x;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float *ph = base + ((int64_t)c * G + h) * (2 + D);
+      const float mc = c < nchunks ? load_part<COH>(ph) : kNegInf;
+      const float lc = c < nchunks ? load_part<COH>(ph + 1) : 0.f;
+      float M = mc;
+      for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+      const float f = mc == kNegInf ? 0.f : __expf(mc - M);
+      float L = f * lc;
+      for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
+      if (c < nchunks) fac[c][h] = f;
+      if (c == 0) inv_l[h] = L;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int h = idx / D, d = idx - h * D;
+    float O = 0.f;
+    for (int c = 0; c < nchunks; ++c)
+      O += fac[c][h] * load_part<COH>(base + ((int64_t)c * G + h) * (2 + D) + 2 + d);
+    const float r = O / inv_l[h];
+    const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
+    if (a.out_f32)
+      ((float *)a.out)[oi] = r;
+    else
+      ((uint16_t *)a.out)[oi] = f32_to_bf16_bits(r);
+  }
+}
+
+// After this workgroup stored its partials (device-coherent stores): wait
+// until every thread's stores completed, then count its arrival for (row, kv
+// head) bh; the workgroup that brings the count to S merges all S partials
+// with device-coherent loads (its increment follows every other split's
+// completed stores) and re-arms the counter for the next launch. No
+// device-scope fences: on this part a release fence writes back the whole L2
+// and costs ~100 us per launch. Uniform per workgroup.
+template <int G>
+__device__ void arrive_and_merge(const AttnArgs &a, int bh) {
+  __shared__ int is_last;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are done
+  __syncthreads();
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              a.max_chunks - 1;
+  __syncthreads();
+  if (!is_last) return;
+  combine_pair<G, true>(a, bh);
+  if (threadIdx.x == 0) __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Multi-pass variant: one workgroup of NP waves per (row, kv head, split).
 // Split s of a row covers keys [s * per, min(len, (s + 1) * per)), per =
 // ceil(len / S) rounded up to 64; the workgroup walks it in passes of NP * 64
@@ -146,7 +234,8 @@ __device__ void attn_pass(const AttnArgs &a) {
   float *part = a.ws + (((int64_t)bh * S + split) * G) * (2 + D);
   if (start >= end) {  // empty split (uniform per workgroup)
     for (int idx = threadIdx.x; idx < G * (2 + D); idx += blockDim.x)
-      part[idx] = (idx % (2 + D)) == 0 ? kNegInf : 0.f;
+      store_part(part + idx, (idx % (2 + D)) == 0 ? kNegInf : 0.f, a.counters != nullptr);
+    if (a.counters) arrive_and_merge<G>(a, bh);
     return;
   }
   const int seq = a.row_seq ? a.row_seq[b] : b;
@@ -211,6 +300,12 @@ __device__ void attn_pass(const AttnArgs &a) {
     }
   };
   const int first = start + wave * KW;
+  // Fused, G <= 2: the first block's K loads are in flight during the q
+  // prologue (norm + RoPE wait on q and the RoPE row); its V loads follow in
+  // the loop. (Issuing V here too, the next block at the end of each pass, or
+  // this hoist at G >= 4 keeps too many registers live and spills.)
+  constexpr bool kHoistK = FUSE && G <= 2;
+  if (kHoistK && first < end) load_k(first);
   float m_run = kNegInf, l_run = 0.f;  // per lane: head col (all g4 lanes agree)
   float o[G][8];
 #pragma unroll
@@ -239,7 +334,7 @@ __device__ void attn_pass(const AttnArgs &a) {
     stage = *(const u32x4 *)(src + (lane < 16 ? (a.Hq + kvh) * D + 8 * lane
                                               : (a.Hq + a.Hkv + kvh) * D + 8 * (lane - 16)));
   for (int j0 = first; j0 < end; j0 += NP * KW) {
-    load_k(j0);
+    if (!kHoistK || j0 != first) load_k(j0);
     load_v(j0);
     // q -> bf16 hi + lo after the block's loads are issued (q is in flight)
     u32x4 qhi[4], qlo[4];
@@ -428,58 +523,15 @@ __device__ void attn_pass(const AttnArgs &a) {
         ((uint16_t *)a.out)[oi] = f32_to_bf16_bits(r);
     } else {
       float *ph = part + h * (2 + D);
+      const bool coh = a.counters != nullptr;
       if (d == 0) {
-        ph[0] = M;
-        ph[1] = L;
+        store_part(ph, M, coh);
+        store_part(ph + 1, L, coh);
       }
-      ph[2 + d] = O;
+      store_part(ph + 2 + d, O, coh);
     }
   }
-}
-
-// Second launch: merge the chunk partials of rows with more than one chunk,
-// in chunk order. One workgroup per (row, kv head); thread = (head, dim).
-template <int G>
-__device__ void attn_combine(const AttnArgs &a) {
-  constexpr int MAXC = 64;
-  __shared__ float fac[MAXC][G];  // exp(m_c - M) per chunk and head
-  __shared__ float inv_l[G];
-  const int bh = blockIdx.x;
-  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
-  int len = a.lens[b];
-  len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
-  const int nchunks = a.max_chunks;  // every split wrote a partial (empty: max -inf)
-  const float *base = a.ws + ((int64_t)bh * a.max_chunks) * G * (2 + D);
-  // per-head statistics on wave 0: lane c holds chunk c's (max, sum); the
-  // max and the weighted sum use fixed butterflies (deterministic)
-  if (threadIdx.x < 64) {
-    const int c = threadIdx.x;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float *ph = base + ((int64_t)c * G + h) * (2 + D);
-      const float mc = c < nchunks ? ph[0] : kNegInf;
-      const float lc = c < nchunks ? ph[1] : 0.f;
-      float M = mc;
-      for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-      const float f = mc == kNegInf ? 0.f : __expf(mc - M);
-      float L = f * lc;
-      for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
-      if (c < nchunks) fac[c][h] = f;
-      if (c == 0) inv_l[h] = L;
-    }
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int h = idx / D, d = idx - h * D;
-    float O = 0.f;
-    for (int c = 0; c < nchunks; ++c) O += fac[c][h] * base[((int64_t)c * G + h) * (2 + D) + 2 + d];
-    const float r = O / inv_l[h];
-    const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
-    if (a.out_f32)
-      ((float *)a.out)[oi] = r;
-    else
-      ((uint16_t *)a.out)[oi] = f32_to_bf16_bits(r);
-  }
+  if (S > 1 && a.counters) arrive_and_merge<G>(a, bh);
 }
 
 }  // namespace
@@ -494,7 +546,7 @@ __device__ void attn_combine(const AttnArgs &a) {
   }                                                                                  \
   extern "C" __global__ void __launch_bounds__(256)                                  \
       rxw8_gqa_decode_combine_d128_g##G(AttnArgs a) {                                \
-    attn_combine<G>(a);                                                              \
+    combine_pair<G, false>(a, blockIdx.x);                                           \
   }
 RXW8_ATTN(1)
 RXW8_ATTN(2)

@@ -135,6 +135,7 @@ struct AttnArgs {
   const float *q_norm, *k_norm;
   const float *rope;
   float eps;
+  int *counters;
 };
 
 struct PrefillArgs {
@@ -657,21 +658,40 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
   if (rope && !fast) return fail(RXW8_INTERNAL, "fused RoPE attention needs the D = 128 kernel");
   if (fast) {
     // 8 waves walk a split of a row's keys in 512-key passes with an online
-    // softmax. S splits per (row, kv head): about one workgroup per CU, and at
-    // most ~1536 keys per workgroup; S = 1 (no combine launch) once the rows
-    // alone fill the GPU (prefill). The combine keeps at most 64 partials.
+    // softmax; one such workgroup fills a CU (VGPR-bound). S splits per (row,
+    // kv head) minimise rounds x (fixed cost + keys per split), with the fixed
+    // cost (launch, q set-up, wave merge, partial store) worth ~125 keys and
+    // Lmax standing in for the row lengths: whole rounds of workgroups win
+    // over a partial last round (64 pairs: S = 4 beats 6). S = 1 (no combine
+    // launch) once the rows alone fill the GPU (prefill). The combine keeps at
+    // most 64 partials, and every split holds at least 64 keys.
     const int forced = env_int("RXW8_ATTN_SPLITS", 0);
     const int64_t pairs = R * Hkv;
-    int64_t S = std::max<int64_t>((rt->cus + pairs - 1) / pairs, (Lmax + 1535) / 1536);
-    S = std::min<int64_t>(S, (Lmax + 63) / 64);
+    const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(64, (Lmax + 63) / 64));
+    int64_t S = 1;
+    double best = 0.0;
+    for (int64_t s = 1; s <= smax; ++s) {
+      const double rounds = (double)((pairs * s + rt->cus - 1) / rt->cus);
+      const double est = rounds * (125.0 + (double)Lmax / (double)s);
+      if (s == 1 || est < best) {
+        best = est;
+        S = s;
+      }
+    }
     if (forced > 0) S = forced;
     if (S > 64) S = 64;
     if (pairs >= 2 * rt->cus && !forced) S = 1;
     const int64_t max_chunks = S;
+    // Splits are merged by the last workgroup of each (row, kv head) to finish
+    // (arrival counters, zeroed once at allocation and re-armed by the kernel);
+    // RXW8_ATTN_TWO_PASS=1 uses the separate combine launch instead.
+    const bool two_pass = env_int("RXW8_ATTN_TWO_PASS", 0) != 0;
     if (max_chunks > 1) {
       int rc = ensure_workspace(rt, rt->scratch,
                                 (size_t)R * Hkv * max_chunks * G * (2 + D) * sizeof(float), false);
       if (rc) return rc;
+      if (!two_pass && (rc = ensure_workspace(rt, rt->attn_counters, (size_t)R * Hkv * sizeof(int), true)))
+        return rc;
     }
     AttnArgs a;
     a.q = q;
@@ -697,11 +717,12 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     a.k_norm = rope ? rope->k_norm : nullptr;
     a.rope = rope ? rope->table : nullptr;
     a.eps = rope ? rope->eps : 0.f;
+    a.counters = max_chunks > 1 && !two_pass ? (int *)rt->attn_counters.ptr : nullptr;
     char kname[64];
     std::snprintf(kname, sizeof kname, rope ? "rxw8_gqa_decode_rope_d128_g%d" : "rxw8_gqa_decode_d128_g%d",
                   (int)G);
     int rc = launch(rt, kname, dim3((unsigned)(R * Hkv * max_chunks)), dim3(512), a);
-    if (rc || max_chunks == 1) return rc;
+    if (rc || max_chunks == 1 || a.counters) return rc;
     std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_combine_d128_g%d", (int)G);
     return launch(rt, kname, dim3((unsigned)(R * Hkv)), dim3(256), a);
   }

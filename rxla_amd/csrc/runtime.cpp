@@ -204,7 +204,7 @@ int new_buffer(Runtime *rt, int dtype, const int64_t *dims, int rank, bool zero,
 static void runtime_free(Runtime *rt) {
   if (rt->stream) (void)hipStreamSynchronize(rt->stream);
   for (auto &kv : rt->free_blocks) (void)hipFree(kv.second);
-  for (Workspace *w : {&rt->partials, &rt->scratch, &rt->xcast, &rt->wdeq})
+  for (Workspace *w : {&rt->partials, &rt->scratch, &rt->xcast, &rt->wdeq, &rt->attn_counters})
     if (w->ptr) (void)hipFree(w->ptr);
   for (hipModule_t m : rt->modules) (void)hipModuleUnload(m);
   if (rt->own_stream) (void)hipStreamDestroy(rt->own_stream);

@@ -57,6 +57,31 @@ def test_edge_lengths_and_groups(rt, group, lens):
     assert rel_err(run_gqa(rt, q, kc, vc, lens), ref) <= 1e-4
 
 
+@pytest.mark.parametrize("splits", [2, 3, 4, 7, 16, 64])
+def test_in_kernel_split_merge_equals_combine_launch(rt, monkeypatch, splits):
+    # The last workgroup of a (row, kv head) merges the split partials itself
+    # (arrival counters); RXW8_ATTN_TWO_PASS=1 merges them in a second launch.
+    # Same code, same split order: bit-identical, on repeated calls (the
+    # counters re-arm) and with empty splits (64 splits of 100 keys).
+    r = rx()
+    rng = np.random.default_rng(300 + splits)
+    b, hq, hkv, lmax, d = 3, 8, 2, 2100, 128
+    lens = np.array([2100, 100, 1337], np.int32)
+    q = rng.standard_normal((b, hq, d)).astype(np.float32)
+    k_bits = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    v_bits = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    kc, vc = rt.buffer(k_bits, r.DType.BF16), rt.buffer(v_bits, r.DType.BF16)
+    qb, lb = rt.buffer(q), rt.buffer(lens)
+    monkeypatch.setenv("RXW8_ATTN_SPLITS", str(splits))
+    monkeypatch.setenv("RXW8_ATTN_TWO_PASS", "1")
+    want = r.grouped_query_attention(rt, qb, kc, vc, lb).to_numpy()
+    monkeypatch.delenv("RXW8_ATTN_TWO_PASS")
+    for _ in range(3):
+        got = r.grouped_query_attention(rt, qb, kc, vc, lb).to_numpy()
+        np.testing.assert_array_equal(got, want)
+    assert rel_err(want, oracle.gqa_decode_bf16cache(q, k_bits, v_bits, lens)) <= 1e-4
+
+
 def test_keys_beyond_length_are_never_read(rt):
     rng = np.random.default_rng(41)
     b, hq, hkv, lmax, d = 2, 8, 2, 600, 128
