@@ -124,10 +124,6 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4 &r, float *x) {
   }
 }
 
-// Merge the S split partials of (row, kv head) bh in split order and write
-// the output rows of its G heads. Any workgroup size >= 64 (wave 0 takes the
-// statistics; lane c holds split c's (max, sum); the max and the weighted sum
-// use fixed butterflies, so the result does not depend on who runs it).
 // Split partials: device-coherent (write-through, sc1) stores and loads when
 // the last-arriving workgroup merges them within the launch, plain ones when
 // a second launch does (the kernel boundary then publishes them).
@@ -145,37 +141,54 @@ __device__ __forceinline__ float load_part(const float *p) {
     return *p;
 }
 
+// Merge the S split partials of (row, kv head) bh in split order and write
+// the output rows of its G heads; any workgroup size. Thread (head, dim):
+// M = max_c m_c, then L = sum_c f_c l_c and O = sum_c f_c o_c in split order
+// with f_c = exp(m_c - M) (0 for empty splits). Up to 8 splits, all of an
+// output's partials are loaded first (one round trip), with the same
+// arithmetic order as the general loop.
 template <int G, bool COH>
 __device__ void combine_pair(const AttnArgs &a, int bh) {
-  constexpr int MAXC = 64;
-  __shared__ float fac[MAXC][G];  // exp(m_c - M) per chunk and head
-  __shared__ float inv_l[G];
+  constexpr int kFast = 8;
   const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
   const int nchunks = a.max_chunks;  // every split wrote a partial (empty: max -inf)
   const float *base = a.ws + ((int64_t)bh * a.max_chunks) * G * (2 + D);
-  if (threadIdx.x < 64) {
-    const int c = threadIdx.x;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float *ph = base + ((int64_t)c * G + h) * (2 + D);
-      const float mc = c < nchunks ? load_part<COH>(ph) : kNegInf;
-      const float lc = c < nchunks ? load_part<COH>(ph + 1) : 0.f;
-      float M = mc;
-      for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-      const float f = mc == kNegInf ? 0.f : __expf(mc - M);
-      float L = f * lc;
-      for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
-      if (c < nchunks) fac[c][h] = f;
-      if (c == 0) inv_l[h] = L;
-    }
-  }
-  __syncthreads();
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
-    float O = 0.f;
-    for (int c = 0; c < nchunks; ++c)
-      O += fac[c][h] * load_part<COH>(base + ((int64_t)c * G + h) * (2 + D) + 2 + d);
-    const float r = O / inv_l[h];
+    float M = kNegInf, L = 0.f, O = 0.f;
+    if (nchunks <= kFast) {
+      float mc[kFast], lc[kFast], oc[kFast];
+#pragma unroll
+      for (int c = 0; c < kFast; ++c) {
+        mc[c] = kNegInf;
+        lc[c] = 0.f;
+        oc[c] = 0.f;
+        if (c < nchunks) {
+          const float *ph = base + ((int64_t)c * G + h) * (2 + D);
+          mc[c] = load_part<COH>(ph);
+          lc[c] = load_part<COH>(ph + 1);
+          oc[c] = load_part<COH>(ph + 2 + d);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < kFast; ++c) M = fmaxf(M, mc[c]);
+#pragma unroll
+      for (int c = 0; c < kFast; ++c) {
+        const float f = mc[c] == kNegInf ? 0.f : __expf(mc[c] - M);
+        L += f * lc[c];
+        O += f * oc[c];
+      }
+    } else {
+      for (int c = 0; c < nchunks; ++c) M = fmaxf(M, load_part<COH>(base + ((int64_t)c * G + h) * (2 + D)));
+      for (int c = 0; c < nchunks; ++c) {
+        const float *ph = base + ((int64_t)c * G + h) * (2 + D);
+        const float mc = load_part<COH>(ph);
+        const float f = mc == kNegInf ? 0.f : __expf(mc - M);
+        L += f * load_part<COH>(ph + 1);
+        O += f * load_part<COH>(ph + 2 + d);
+      }
+    }
+    const float r = O / L;
     const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
     if (a.out_f32)
       ((float *)a.out)[oi] = r;
