@@ -61,7 +61,8 @@ struct AttnArgs {
 namespace {
 
 constexpr int D = 128;
-constexpr int KW = 64;            // keys per wave
+constexpr int KW = 64;            // split granularity (keys)
+constexpr int KT = 16;            // keys per wave tile
 constexpr float kNegInf = -__builtin_huge_valf();
 
 __device__ __forceinline__ float wave_max4(float v) {
@@ -229,7 +230,7 @@ __device__ void arrive_and_merge(const AttnArgs &a, int bh) {
 template <int G, int NP, bool FUSE>
 __device__ void attn_pass(const AttnArgs &a) {
   constexpr int GP = (G + 3) / 4 * 4;
-  __shared__ float p_lds[NP][KW][GP];
+  __shared__ float p_lds[NP][KT][GP];
   __shared__ float m_lds[NP][G], l_lds[NP][G];
   __shared__ float o_lds[NP][G][D];
 
@@ -288,37 +289,39 @@ __device__ void attn_pass(const AttnArgs &a) {
     }
   }
   }
-  // K fragments (A operand): lane (key = col, dgroup = g4); V rows: lane
-  // (kq = g4, dgroup = col) takes keys 4 * it + kq, dims 8 col .. +7
-  u32x4 kf[4][4], vf[16];
-  auto load_k = [&](int j0) {
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int key = j0 + 16 * kb + col;
+  // Tiles of KT = 16 keys per wave, double-buffered in registers: the loads of
+  // tile n+1 are in flight while tile n is scored and accumulated, so every
+  // wave keeps K and V streaming (a 64-key tile loaded and then consumed left
+  // the memory idle during each pass's compute; a 32-key pair of tiles spills).
+  // Wave w takes the tiles at first + 16 w + 128 n. K fragments (A operand):
+  // lane (key = col, dgroup = g4); V rows: lane (kq = g4, dgroup = col) takes
+  // keys 4 * it + kq, dims 8 col .. +7.
+  struct Tile {
+    u32x4 k[4], v[4];
+  };
+  auto load = [&](Tile &T, int j0) {
+    {
+      const int key = j0 + col;
       const bool valid = key < end;
       const uint16_t *krow = a.kc + (row_base + (valid ? key : 0)) * D + 8 * g4;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        kf[kb][t] = valid ? __builtin_nontemporal_load((const u32x4 *)(krow + 32 * t))
+        T.k[t] = valid ? __builtin_nontemporal_load((const u32x4 *)(krow + 32 * t)) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int key = j0 + 4 * it + g4;
+      T.v[it] = key < end ? __builtin_nontemporal_load(
+                                (const u32x4 *)(a.vc + (row_base + key) * D + 8 * col))
                           : u32x4{0, 0, 0, 0};
     }
   };
-  auto load_v = [&](int j0) {
-#pragma unroll
-    for (int it = 0; it < 16; ++it) {
-      const int key = j0 + 4 * it + g4;
-      vf[it] = key < end ? __builtin_nontemporal_load(
-                               (const u32x4 *)(a.vc + (row_base + key) * D + 8 * col))
-                         : u32x4{0, 0, 0, 0};
-    }
-  };
-  const int first = start + wave * KW;
-  // Fused, G <= 2: the first block's K loads are in flight during the q
-  // prologue (norm + RoPE wait on q and the RoPE row); its V loads follow in
-  // the loop. (Issuing V here too, the next block at the end of each pass, or
-  // this hoist at G >= 4 keeps too many registers live and spills.)
-  constexpr bool kHoistK = FUSE && G <= 2;
-  if (kHoistK && first < end) load_k(first);
+  const int first = start + wave * KT;
+  constexpr int kStep = NP * KT;
+  Tile ta, tb;
+  // The first tile is in flight during the q prologue (the fused norm + RoPE
+  // waits on q and the RoPE row).
+  load(ta, first);
   float m_run = kNegInf, l_run = 0.f;  // per lane: head col (all g4 lanes agree)
   float o[G][8];
 #pragma unroll
@@ -346,13 +349,10 @@ __device__ void attn_pass(const AttnArgs &a) {
   if (own_new && wave == 0 && lane < 32)
     stage = *(const u32x4 *)(src + (lane < 16 ? (a.Hq + kvh) * D + 8 * lane
                                               : (a.Hq + a.Hkv + kvh) * D + 8 * (lane - 16)));
-  for (int j0 = first; j0 < end; j0 += NP * KW) {
-    if (!kHoistK || j0 != first) load_k(j0);
-    load_v(j0);
-    // q -> bf16 hi + lo after the block's loads are issued (q is in flight)
-    u32x4 qhi[4], qlo[4];
+  // q -> bf16 hi + lo (B operand), once
+  u32x4 qhi[4], qlo[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < 4; ++t) {
       float qv[8];
       if (col < G) {
         if (FUSE || a.q_f32) {
@@ -374,54 +374,50 @@ __device__ void attn_pass(const AttnArgs &a) {
         qhi[t][e] = pack_bf16x2(h0, h1);
         qlo[t][e] = pack_bf16x2(qv[2 * e] - h0, qv[2 * e + 1] - h1);
       }
-    }
-    float s[4][4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+  }
+  // One online-softmax step over the tile at j0 (keys >= end score -inf and
+  // carry zero V rows).
+  auto consume = [&](const Tile &T, int j0) {
+    float s[4];
+    {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        acc = mfma16x16x32(as_bf16x8(kf[kb][t]), as_bf16x8(qhi[t]), acc);
-        acc = mfma16x16x32(as_bf16x8(kf[kb][t]), as_bf16x8(qlo[t]), acc);
+        acc = mfma16x16x32(as_bf16x8(T.k[t]), as_bf16x8(qhi[t]), acc);
+        acc = mfma16x16x32(as_bf16x8(T.k[t]), as_bf16x8(qlo[t]), acc);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int key = j0 + 16 * kb + 4 * g4 + i;
+        const int key = j0 + 4 * g4 + i;
         float v = kNegInf;
         if (key < end) {
           v = acc[i] * a.scale;
           if (a.mask && col < G)
             v += a.mask[(int64_t)b * a.mask_sb + (int64_t)(kvh * G + col) * a.mask_sh + key];
         }
-        s[kb][i] = v;
+        s[i] = v;
       }
     }
     float m_blk = kNegInf;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) m_blk = fmaxf(m_blk, s[kb][i]);
+    for (int i = 0; i < 4; ++i) m_blk = fmaxf(m_blk, s[i]);
     m_blk = wave_max4(m_blk);
     const float m_new = fmaxf(m_run, m_blk);
     const bool any = m_new != kNegInf;
     const float f_old = (m_run == kNegInf) ? 0.f : __expf(m_run - m_new);
     float l_blk = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = any ? __expf(s[kb][i] - m_new) : 0.f;
-        s[kb][i] = e;
-        l_blk += e;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const float e = any ? __expf(s[i] - m_new) : 0.f;
+      s[i] = e;
+      l_blk += e;
+    }
     l_blk = wave_sum4(l_blk);
     l_run = l_run * f_old + l_blk;
     m_run = m_new;
     if (col < G)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p_lds[wave][16 * kb + 4 * g4 + i][col] = s[kb][i];
+      for (int i = 0; i < 4; ++i) p_lds[wave][4 * g4 + i][col] = s[i];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -433,12 +429,12 @@ __device__ void attn_pass(const AttnArgs &a) {
       for (int e = 0; e < 8; ++e) o[h][e] *= fh;
     }
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < 4; ++it) {
       float v[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[2 * e] = bf16_bits_to_f32(vf[it][e] & 0xffffu);
-        v[2 * e + 1] = bf16_bits_to_f32(vf[it][e] >> 16);
+        v[2 * e] = bf16_bits_to_f32(T.v[it][e] & 0xffffu);
+        v[2 * e + 1] = bf16_bits_to_f32(T.v[it][e] >> 16);
       }
       const float *prow = p_lds[wave][4 * it + g4];
 #pragma unroll
@@ -448,10 +444,19 @@ __device__ void attn_pass(const AttnArgs &a) {
         for (int e = 0; e < 8; ++e) o[h][e] += p * v[e];
       }
     }
-    // p_lds[wave] is rewritten next pass only after every lane read it
+    // p_lds[wave] is rewritten next tile only after every lane read it
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  // A/B register sets: issue B, consume A, issue A', consume B. Loads past
+  // the split are masked per lane (no memory access); a B tile past the end
+  // is not consumed (uniform per wave).
+  for (int j0 = first; j0 < end; j0 += 2 * kStep) {
+    load(tb, j0 + kStep);
+    consume(ta, j0);
+    load(ta, j0 + 2 * kStep);
+    if (j0 + kStep < end) consume(tb, j0 + kStep);
   }
   if (own_new && wave == 0) {
     // the new key: k = bf16(RoPE(norm(raw k))), scored against q in f32, one
