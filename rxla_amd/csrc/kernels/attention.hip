@@ -56,6 +56,9 @@ struct AttnArgs {
   // splits the last workgroup of a (row, kv head) to finish merges the
   // partials itself; null leaves that to rxw8_gqa_decode_combine.
   int *counters;
+  // > 0: length-proportional splits, `units` workgroups per kv head shared by
+  // the R rows (row_units); 0: max_chunks splits for every row
+  int units;
 };
 
 namespace {
@@ -125,6 +128,36 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4 &r, float *x) {
   }
 }
 
+// Length-proportional splits: the `units` workgroups of a kv head go to the R
+// rows in proportion to their clamped lengths, at least one each: row b owns
+// units [u_b, u_{b+1}) with u_0 = 0 and u_{b+1} = clamp(round(C_{b+1} * units
+// / T), u_b + 1, units - (R - 1 - b)) (f32), C_b the lengths of rows < b and T their
+// total, so every workgroup walks about T / units keys. Returns row b's split
+// count; for unit u (>= 0), also the row and the split within it. Uniform per
+// workgroup; R < units (host-checked).
+__device__ __forceinline__ int row_units(const AttnArgs &a, int b, int u, int *row, int *split,
+                                         int *row_len = nullptr) {
+  int T = 0;  // R * Lmax < 2^31 (host-checked)
+  for (int r = 0; r < a.R; ++r) T += min(max(a.lens[r], 1), a.Lmax);
+  const float per_key = (float)a.units / (float)T;  // same value in every workgroup
+  int C = 0;
+  int ub = 0;  // u_r of the current row
+  for (int r = 0; r < a.R; ++r) {
+    const int len = min(max(a.lens[r], 1), a.Lmax);
+    C += len;
+    const int ideal = (int)((float)C * per_key + 0.5f);
+    const int un = min(max(ub + 1, ideal), a.units - (a.R - 1 - r));  // u_{r+1}
+    if ((u >= 0 && u < un) || (u < 0 && r == b)) {
+      if (row) *row = r;
+      if (split) *split = u - ub;
+      if (row_len) *row_len = len;
+      return un - ub;
+    }
+    ub = un;
+  }
+  return 1;
+}
+
 // Split partials: device-coherent (write-through, sc1) stores and loads when
 // the last-arriving workgroup merges them within the launch, plain ones when
 // a second launch does (the kernel boundary then publishes them).
@@ -149,10 +182,12 @@ __device__ __forceinline__ float load_part(const float *p) {
 // output's partials are loaded first (one round trip), with the same
 // arithmetic order as the general loop.
 template <int G, bool COH>
-__device__ void combine_pair(const AttnArgs &a, int bh) {
+__device__ void combine_pair(const AttnArgs &a, int bh, int nchunks = 0) {
   constexpr int kFast = 8;
   const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
-  const int nchunks = a.max_chunks;  // every split wrote a partial (empty: max -inf)
+  // every split of the row wrote a partial (empty: max -inf)
+  if (nchunks == 0) nchunks = a.units > 0 ? row_units(a, b, -1, nullptr, nullptr) : a.max_chunks;
+  if (nchunks == 1) return;  // a single split wrote the output itself
   const float *base = a.ws + ((int64_t)bh * a.max_chunks) * G * (2 + D);
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
@@ -206,16 +241,16 @@ __device__ void combine_pair(const AttnArgs &a, int bh) {
 // device-scope fences: on this part a release fence writes back the whole L2
 // and costs ~100 us per launch. Uniform per workgroup.
 template <int G>
-__device__ void arrive_and_merge(const AttnArgs &a, int bh) {
+__device__ void arrive_and_merge(const AttnArgs &a, int bh, int nsplit) {
   __shared__ int is_last;
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are done
   __syncthreads();
   if (threadIdx.x == 0)
     is_last = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-              a.max_chunks - 1;
+              nsplit - 1;
   __syncthreads();
   if (!is_last) return;
-  combine_pair<G, true>(a, bh);
+  combine_pair<G, true>(a, bh, nsplit);
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -236,20 +271,29 @@ __device__ void attn_pass(const AttnArgs &a) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int S = a.max_chunks;
-  const int split = blockIdx.x % S;
-  const int bh = blockIdx.x / S;  // row * Hkv + kvh
-  const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
-  int len = a.lens[b];
-  len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
-  const int per = ((len + S - 1) / S + KW - 1) / KW * KW;
+  const int S = a.max_chunks;  // partial slots per (row, kv head)
+  int split, b, kvh, nsplit;
+  int len;
+  if (a.units > 0) {  // length-proportional splits
+    kvh = blockIdx.x / a.units;
+    nsplit = row_units(a, 0, blockIdx.x - kvh * a.units, &b, &split, &len);
+  } else {
+    split = blockIdx.x % S;
+    b = (blockIdx.x / S) / a.Hkv;
+    kvh = (blockIdx.x / S) - b * a.Hkv;
+    nsplit = S;
+    len = a.lens[b];
+    len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
+  }
+  const int bh = b * a.Hkv + kvh;  // row * Hkv + kvh
+  const int per = ((len + nsplit - 1) / nsplit + KW - 1) / KW * KW;
   const int start = split * per;
   int end = min(len, start + per);
   float *part = a.ws + (((int64_t)bh * S + split) * G) * (2 + D);
   if (start >= end) {  // empty split (uniform per workgroup)
     for (int idx = threadIdx.x; idx < G * (2 + D); idx += blockDim.x)
       store_part(part + idx, (idx % (2 + D)) == 0 ? kNegInf : 0.f, a.counters != nullptr);
-    if (a.counters) arrive_and_merge<G>(a, bh);
+    if (a.counters) arrive_and_merge<G>(a, bh, nsplit);
     return;
   }
   const int seq = a.row_seq ? a.row_seq[b] : b;
@@ -532,7 +576,7 @@ __device__ void attn_pass(const AttnArgs &a) {
       L += f * l_lds[w][h];
       O += f * o_lds[w][h][d];
     }
-    if (S == 1) {
+    if (nsplit == 1) {
       const float r = O / L;
       const int64_t oi = ((int64_t)b * a.Hq + kvh * G + h) * D + d;
       if (a.out_f32)
@@ -549,7 +593,7 @@ __device__ void attn_pass(const AttnArgs &a) {
       store_part(ph + 2 + d, O, coh);
     }
   }
-  if (S > 1 && a.counters) arrive_and_merge<G>(a, bh);
+  if (nsplit > 1 && a.counters) arrive_and_merge<G>(a, bh, nsplit);
 }
 
 }  // namespace

@@ -136,6 +136,7 @@ struct AttnArgs {
   const float *rope;
   float eps;
   int *counters;
+  int units;
 };
 
 struct PrefillArgs {
@@ -681,6 +682,17 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     if (forced > 0) S = forced;
     if (S > 64) S = 64;
     if (pairs >= 2 * rt->cus && !forced) S = 1;
+    // Ragged rows: when splitting pays (S > 1), the rows fit one round and the
+    // cache is long (Lmax >= 2048: for short rows the apportioning pass costs
+    // more than the imbalance it removes), the kernel gives each row a share
+    // of cus / Hkv workgroups per kv head in proportion to its length
+    // (device-side, from lens), so no workgroup walks far more keys than the
+    // rest. RXW8_ATTN_SPLITS or RXW8_ATTN_UNIFORM=1 force uniform splits.
+    int64_t units = 0;
+    if (S > 1 && !forced && !env_int("RXW8_ATTN_UNIFORM", 0) && rt->cus / Hkv > R &&
+        Lmax >= 2048 && R * Lmax < (int64_t)1 << 30)
+      units = std::min<int64_t>(rt->cus / Hkv, R + 63);
+    if (units > 0) S = units - R + 1;  // partial slots: the most splits a row can get
     const int64_t max_chunks = S;
     // Splits are merged by the last workgroup of each (row, kv head) to finish
     // (arrival counters, zeroed once at allocation and re-armed by the kernel);
@@ -718,10 +730,12 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     a.rope = rope ? rope->table : nullptr;
     a.eps = rope ? rope->eps : 0.f;
     a.counters = max_chunks > 1 && !two_pass ? (int *)rt->attn_counters.ptr : nullptr;
+    a.units = (int)units;
     char kname[64];
     std::snprintf(kname, sizeof kname, rope ? "rxw8_gqa_decode_rope_d128_g%d" : "rxw8_gqa_decode_d128_g%d",
                   (int)G);
-    int rc = launch(rt, kname, dim3((unsigned)(R * Hkv * max_chunks)), dim3(512), a);
+    const int64_t grid = units > 0 ? Hkv * units : R * Hkv * max_chunks;
+    int rc = launch(rt, kname, dim3((unsigned)grid), dim3(512), a);
     if (rc || max_chunks == 1 || a.counters) return rc;
     std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_combine_d128_g%d", (int)G);
     return launch(rt, kname, dim3((unsigned)(R * Hkv)), dim3(256), a);

@@ -82,6 +82,32 @@ def test_in_kernel_split_merge_equals_combine_launch(rt, monkeypatch, splits):
     assert rel_err(want, oracle.gqa_decode_bf16cache(q, k_bits, v_bits, lens)) <= 1e-4
 
 
+@pytest.mark.parametrize("lens", [[8000, 100, 3000, 1], [6091, 7755, 7282, 4439, 7735, 8010, 7964, 1132],
+                                  [64, 64, 64, 8192]])
+def test_length_proportional_splits(rt, monkeypatch, lens):
+    # Few (row, kv head) pairs: each row gets workgroups in proportion to its
+    # length (the kernel apportions them from lens). Against the oracle, and
+    # the in-kernel merge against the combine launch bit for bit.
+    r = rx()
+    rng = np.random.default_rng(len(lens) * 31 + lens[0])
+    b, hq, hkv, lmax, d = len(lens), 32, 8, 8192, 128
+    lens = np.array(lens, np.int32)
+    q = rng.standard_normal((b, hq, d)).astype(np.float32)
+    k_bits = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    v_bits = oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32))
+    kc, vc = rt.buffer(k_bits, r.DType.BF16), rt.buffer(v_bits, r.DType.BF16)
+    qb, lb = rt.buffer(q), rt.buffer(lens)
+    got = [r.grouped_query_attention(rt, qb, kc, vc, lb).to_numpy() for _ in range(2)]
+    np.testing.assert_array_equal(got[0], got[1])
+    monkeypatch.setenv("RXW8_ATTN_TWO_PASS", "1")
+    np.testing.assert_array_equal(r.grouped_query_attention(rt, qb, kc, vc, lb).to_numpy(), got[0])
+    monkeypatch.delenv("RXW8_ATTN_TWO_PASS")
+    ref = oracle.gqa_decode_bf16cache(q, k_bits, v_bits, lens, threads=16)
+    assert rel_err(got[0], ref) <= 1e-4
+    monkeypatch.setenv("RXW8_ATTN_UNIFORM", "1")
+    assert rel_err(r.grouped_query_attention(rt, qb, kc, vc, lb).to_numpy(), ref) <= 1e-4
+
+
 def test_keys_beyond_length_are_never_read(rt):
     rng = np.random.default_rng(41)
     b, hq, hkv, lmax, d = 2, 8, 2, 600, 128
