@@ -178,12 +178,11 @@ __device__ __forceinline__ float load_part(const float *p) {
 // Merge the S split partials of (row, kv head) bh in split order and write
 // the output rows of its G heads; any workgroup size. Thread (head, dim):
 // M = max_c m_c, then L = sum_c f_c l_c and O = sum_c f_c o_c in split order
-// with f_c = exp(m_c - M) (0 for empty splits). Up to 8 splits, all of an
+// with f_c = exp(m_c - M) (0 for empty splits). Up to 32 splits, all of an
 // output's partials are loaded first (one round trip), with the same
-// arithmetic order as the general loop.
+// arithmetic order as the general loop (empty slots add exact zeros).
 template <int G, bool COH>
 __device__ void combine_pair(const AttnArgs &a, int bh, int nchunks = 0) {
-  constexpr int kFast = 8;
   const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
   // every split of the row wrote a partial (empty: max -inf)
   if (nchunks == 0) nchunks = a.units > 0 ? row_units(a, b, -1, nullptr, nullptr) : a.max_chunks;
@@ -192,10 +191,13 @@ __device__ void combine_pair(const AttnArgs &a, int bh, int nchunks = 0) {
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
     float M = kNegInf, L = 0.f, O = 0.f;
-    if (nchunks <= kFast) {
-      float mc[kFast], lc[kFast], oc[kFast];
+    // up to NC splits: every partial of this output is loaded before any
+    // arithmetic (one round trip); unused slots weigh 0
+    auto merge_upto = [&](auto nc) {
+      constexpr int NC = decltype(nc)::value;
+      float mc[NC], lc[NC], oc[NC];
 #pragma unroll
-      for (int c = 0; c < kFast; ++c) {
+      for (int c = 0; c < NC; ++c) {
         mc[c] = kNegInf;
         lc[c] = 0.f;
         oc[c] = 0.f;
@@ -207,13 +209,18 @@ __device__ void combine_pair(const AttnArgs &a, int bh, int nchunks = 0) {
         }
       }
 #pragma unroll
-      for (int c = 0; c < kFast; ++c) M = fmaxf(M, mc[c]);
+      for (int c = 0; c < NC; ++c) M = fmaxf(M, mc[c]);
 #pragma unroll
-      for (int c = 0; c < kFast; ++c) {
+      for (int c = 0; c < NC; ++c) {
         const float f = mc[c] == kNegInf ? 0.f : __expf(mc[c] - M);
         L += f * lc[c];
         O += f * oc[c];
       }
+    };
+    if (nchunks <= 8) {
+      merge_upto(std::integral_constant<int, 8>{});
+    } else if (nchunks <= 32) {
+      merge_upto(std::integral_constant<int, 32>{});
     } else {
       for (int c = 0; c < nchunks; ++c) M = fmaxf(M, load_part<COH>(base + ((int64_t)c * G + h) * (2 + D)));
       for (int c = 0; c < nchunks; ++c) {
