@@ -71,11 +71,11 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def recorded_traffic():
-    """HBM bytes per launch of the roofline GEMV from the committed counter
-    summary (two rocprofv3 --pmc passes, calibrated by a copy of known size);
-    None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "gemv_B1_N24576_traffic.txt")
+def recorded_traffic(name="gemv_B1_N24576_traffic.txt"):
+    """HBM bytes per launch (or per call) from a committed counter summary
+    (two rocprofv3 --pmc passes, calibrated by a copy of known size); None
+    when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
     try:
         for line in open(path):
             if line.startswith("TRAFFIC_BYTES_PER_LAUNCH="):
@@ -238,8 +238,11 @@ def bench_attention(rt, rx, torch, stream, reps=20):
     t = e0.elapsed_time(e1) * 1e-3 / reps
     gbs = nbytes / t / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernels": "rxw8_gqa_decode_d128_g4 + rxw8_gqa_decode_combine_d128_g4",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": recorded_traffic("attention_c4_traffic.txt"),
+            "traffic_source": "profiles/attention_c4_traffic.txt (FETCH_SIZE + WRITE_SIZE per call, "
+                              "copy-calibrated, bench.py --pmc-probe attention)",
+            "kernels": "rxw8_gqa_decode_d128_g4 (splits merged in-kernel)",
             "us_per_call": round(t * 1e6, 2), "bytes_per_call": nbytes,
             "lens": lens.tolist(),
             "timing": f"HIP events around {reps} back-to-back calls after a spin kernel, "
@@ -464,6 +467,27 @@ def pmc_probe(kind, rounds=3):
                 rx.quantized_linear(rt, xb, wb[i % 6][0], wb[i % 6][1], rx.DType.BF16, out=yb)
         reps = rounds * ROOF_CYCLES * 6
         log(f"pmc probe gemv B={b} N={n} K={K}: {reps} launches, {gemv_bytes(b, n)} algorithmic B each")
+    elif kind == "attention":  # C4, as bench_attention times it
+        B, HQ, HKV, D, LMAX = 8, 32, 8, 128, 8192
+        lens = np.random.default_rng(4).integers(512, 8193, B).astype(np.int32)
+        with torch.cuda.stream(stream):
+            caches = [(torch.randn((B, HKV, LMAX, D), device="cuda", generator=gen).to(torch.bfloat16),
+                       torch.randn((B, HKV, LMAX, D), device="cuda", generator=gen).to(torch.bfloat16))
+                      for _ in range(ATTN_COPIES)]
+            q = torch.randn((B, HQ, D), device="cuda", generator=gen).to(torch.bfloat16)
+            o = torch.empty((B, HQ, D), dtype=torch.bfloat16, device="cuda")
+            lt = torch.from_numpy(lens).to("cuda")
+        stream.synchronize()
+        cb = [(rt.wrap_tensor(k), rt.wrap_tensor(v)) for k, v in caches]
+        qb, ob, lb = rt.wrap_tensor(q), rt.wrap_tensor(o), rt.wrap_tensor(lt)
+        calls = 0
+        for _ in range(rounds):
+            with torch.cuda.stream(stream):
+                torch.cuda._sleep(SPIN_CYCLES)
+            for i in range(20):
+                rx.grouped_query_attention(rt, qb, cb[i % ATTN_COPIES][0], cb[i % ATTN_COPIES][1], lb, out=ob)
+                calls += 1
+        log(f"pmc probe attention C4 lens={lens.tolist()}: {calls} calls")
     else:
         raise SystemExit(f"unknown --pmc-probe {kind}")
     rt.synchronize()
@@ -485,7 +509,8 @@ def main():
     ap.add_argument("--skip-attention", action="store_true")
     ap.add_argument("--skip-decoder", action="store_true")
     ap.add_argument("--skip-qwen35", action="store_true")
-    ap.add_argument("--pmc-probe", choices=["gemv"], help="counter-collection program only")
+    ap.add_argument("--pmc-probe", choices=["gemv", "attention"],
+                    help="counter-collection program only")
     ap.add_argument("--qwen35-only", action="store_true",
                     help="(profiling) run only the Qwen3.5 leg and print its JSON")
     args = ap.parse_args()
