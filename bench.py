@@ -433,11 +433,12 @@ def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, ite
 
 
 def pmc_probe(kind, rounds=3):
-    """A short fixed program for rocprofv3 runs: the roofline shape launched as
-    the bench times it (`rounds` x [spin spacer, ROOF_CYCLES passes over 6
-    weight copies back to back]) plus 4 plain 256 MiB device copies (torch)
-    that calibrate what FETCH_SIZE / WRITE_SIZE read for a known number of
-    bytes."""
+    """A short fixed program for rocprofv3 runs: one roofline leg launched as
+    the bench times it (gemv: `rounds` x [spin spacer, ROOF_CYCLES passes over
+    6 weight copies back to back]; attention: `rounds` x [spin spacer, 20 C4
+    calls over the rotating caches]; gemm: 30 launches of the C3 roofline
+    shape) plus 4 plain 256 MiB device copies (torch) that calibrate what
+    FETCH_SIZE / WRITE_SIZE read for a known number of bytes."""
     import torch
     import rxla_amd as rx
 
@@ -467,6 +468,19 @@ def pmc_probe(kind, rounds=3):
                 rx.quantized_linear(rt, xb, wb[i % 6][0], wb[i % 6][1], rx.DType.BF16, out=yb)
         reps = rounds * ROOF_CYCLES * 6
         log(f"pmc probe gemv B={b} N={n} K={K}: {reps} launches, {gemv_bytes(b, n)} algorithmic B each")
+    elif kind == "gemm":  # C3 roofline shape M=8192 N=12288 K=4096, 10 launches after warm-up
+        m, n = 8192, 12288
+        with torch.cuda.stream(stream):
+            u = torch.randint(1, 256, (n, K), dtype=torch.uint8, device="cuda", generator=gen)
+            sc = torch.rand((n, 1), device="cuda", generator=gen) * 1e-3 + 1e-4
+            x = torch.randn((m, K), device="cuda", generator=gen).to(torch.bfloat16)
+            y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        stream.synchronize()
+        ub = rx.pack_weight(rt, rt.wrap_tensor(u))
+        xb, sb, yb = rt.wrap_tensor(x), rt.wrap_tensor(sc), rt.wrap_tensor(y)
+        for _ in range(30):
+            rx.quantized_linear(rt, xb, ub, sb, rx.DType.BF16, out=yb)
+        log(f"pmc probe gemm M={m} N={n} K={K}: 30 launches")
     elif kind == "attention":  # C4, as bench_attention times it
         B, HQ, HKV, D, LMAX = 8, 32, 8, 128, 8192
         lens = np.random.default_rng(4).integers(512, 8193, B).astype(np.int32)
@@ -509,7 +523,7 @@ def main():
     ap.add_argument("--skip-attention", action="store_true")
     ap.add_argument("--skip-decoder", action="store_true")
     ap.add_argument("--skip-qwen35", action="store_true")
-    ap.add_argument("--pmc-probe", choices=["gemv", "attention"],
+    ap.add_argument("--pmc-probe", choices=["gemv", "gemm", "attention"],
                     help="counter-collection program only")
     ap.add_argument("--qwen35-only", action="store_true",
                     help="(profiling) run only the Qwen3.5 leg and print its JSON")
