@@ -9,9 +9,10 @@
 // per prompt token in prefill), caches [Bc, Hkv, Lmax, D] bf16, out
 // [R, Hq, D] f32|bf16. Row r reads cache slot row_seq[r] (r when null) and
 // sees its first lens[r] keys. One workgroup (8 waves) handles one (row, kv
-// head, split) and walks the split in passes of 512 keys, 64 per wave, with an
-// online softmax per wave. The G = Hq/Hkv query heads of the kv head share
-// every K/V byte the workgroup loads.
+// head, split); each wave walks tiles of 16 keys (double-buffered in
+// registers) with its own online softmax. The G = Hq/Hkv query heads of the kv
+// head share every K/V byte the workgroup loads. Splits are uniform per row,
+// or, for few long ragged rows, apportioned by length on the device.
 //
 // QK^T runs on v_mfma_f32_16x16x32_bf16 with K as the A operand (16 keys x
 // 32 dims per fragment, 16-byte loads of contiguous K rows) and q^T as the B
@@ -23,8 +24,9 @@
 // Waves merge (max, sum, acc) in LDS. With one split the workgroup writes the
 // output; otherwise every split writes (max, sum, acc) partials, which are
 // merged in split order (deterministic) either by the last workgroup of the
-// (row, kv head) to arrive -- device-scope fences around an arrival counter
-// make the other splits' partials visible to it -- or, without counters, by
+// (row, kv head) to arrive -- device-coherent partial stores and loads around
+// an arrival counter make the other splits' partials visible to it -- or,
+// without counters, by
 // rxw8_gqa_decode_combine in a second launch (the kernel boundary makes the
 // partials visible). Both merges run the same code, so they agree bit for bit.
 #include "common.h"

@@ -658,7 +658,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
                     !env_int("RXW8_FORCE_GENERIC", 0);
   if (rope && !fast) return fail(RXW8_INTERNAL, "fused RoPE attention needs the D = 128 kernel");
   if (fast) {
-    // 8 waves walk a split of a row's keys in 512-key passes with an online
+    // 8 waves walk a split of a row's keys in 16-key tiles with an online
     // softmax; one such workgroup fills a CU (VGPR-bound). S splits per (row,
     // kv head) minimise rounds x (fixed cost + keys per split), with the fixed
     // cost (launch, q set-up, wave merge, partial store) worth ~125 keys and
