@@ -293,20 +293,38 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   // The first weight group is in flight while x and the scales are staged.
   load_group(bufA, 0);
 
-  // Grouped scales of this workgroup's rows and K-split, staged after x:
-  // ss[row_in_block * gps + g_local] (f32).
+  // One plain activation row with per-channel scales: every wave stages only
+  // its own K slice, in its own LDS region (stride Kw + kXPad), and starts its
+  // loop as soon as that slice is in -- no workgroup barrier before the
+  // weights stream. (Waves of different row groups stage the same slice.)
+  const bool wave_stage = a.x_mode == 0 && a.M == 1 && per_channel;
+  const uint16_t *xbase = xs;
+  int xld = ldx;
   const int gps = per_channel ? 0 : Kc / a.G;
   float *ss = (float *)(xs + a.M * ldx);
-  if (!per_channel) {
-    const int g0 = k0 / a.G;
-    for (int i = threadIdx.x; i < 16 * RW * gps; i += blockDim.x) {
-      const int rr = i / gps, gl = i - rr * gps;
-      const int n = rows0 + rr;
-      ss[i] = n < a.N ? a.scale[(int64_t)n * groups + g0 + gl] : 0.f;
+  if (wave_stage) {
+    uint16_t *xw = xs + wave * (Kw + kXPad);
+    for (int i = lane; i < Kw / 8; i += 64)
+      *(u32x4 *)(xw + 8 * i) = load_x8(a.x, (int64_t)a.x_off + k0 + kbase + 8 * i, a.x_f32 != 0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    xbase = xw - kbase;  // so that xbase + kbase is the slice start
+    xld = 0;
+  } else {
+    // Grouped scales of this workgroup's rows and K-split, staged after x:
+    // ss[row_in_block * gps + g_local] (f32).
+    if (!per_channel) {
+      const int g0 = k0 / a.G;
+      for (int i = threadIdx.x; i < 16 * RW * gps; i += blockDim.x) {
+        const int rr = i / gps, gl = i - rr * gps;
+        const int n = rows0 + rr;
+        ss[i] = n < a.N ? a.scale[(int64_t)n * groups + g0 + gl] : 0.f;
+      }
     }
+    stage_x(a, xs, k0, Kc);
+    __syncthreads();
   }
-  stage_x(a, xs, k0, Kc);
-  __syncthreads();
 
   f32x4 acc[MB], ones[MB], total[MB];
 #pragma unroll
@@ -320,7 +338,7 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int b = col + 16 * mb;
-    xrow[mb] = xs + (b < a.M ? b : a.M - 1) * ldx + kbase + j * 16;
+    xrow[mb] = xbase + (b < a.M ? b : a.M - 1) * xld + kbase + j * 16;
   }
   const u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
   const bf16x8 onesf = as_bf16x8(ones_bits);
