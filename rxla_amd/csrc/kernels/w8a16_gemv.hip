@@ -293,24 +293,29 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   // The first weight group is in flight while x and the scales are staged.
   load_group(bufA, 0);
 
-  // One plain activation row with per-channel scales: every wave stages only
-  // its own K slice, in its own LDS region (stride Kw + kXPad), and starts its
-  // loop as soon as that slice is in -- no workgroup barrier before the
+  // Plain activation rows with per-channel scales, one row (any tiling) or up
+  // to 4 rows with one row group: every wave stages only its own K slice of
+  // the rows, in its own LDS region (M rows of stride Kw + kXPad), and starts
+  // its loop as soon as that slice is in -- no workgroup barrier before the
   // weights stream. (Waves of different row groups stage the same slice.)
-  const bool wave_stage = a.x_mode == 0 && a.M == 1 && per_channel;
+  const bool wave_stage = a.x_mode == 0 && per_channel && (a.M == 1 || (RW == 1 && a.M <= 4));
   const uint16_t *xbase = xs;
   int xld = ldx;
   const int gps = per_channel ? 0 : Kc / a.G;
   float *ss = (float *)(xs + a.M * ldx);
   if (wave_stage) {
-    uint16_t *xw = xs + wave * (Kw + kXPad);
-    for (int i = lane; i < Kw / 8; i += 64)
-      *(u32x4 *)(xw + 8 * i) = load_x8(a.x, (int64_t)a.x_off + k0 + kbase + 8 * i, a.x_f32 != 0);
+    const int pieces = Kw / 8;  // 8 values per 16-byte piece
+    uint16_t *xw = xs + wave * a.M * (Kw + kXPad);
+    for (int i = lane; i < a.M * pieces; i += 64) {
+      const int b = i / pieces, p = i - b * pieces;
+      *(u32x4 *)(xw + b * (Kw + kXPad) + 8 * p) =
+          load_x8(a.x, (int64_t)b * a.x_stride + a.x_off + k0 + kbase + 8 * p, a.x_f32 != 0);
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    xbase = xw - kbase;  // so that xbase + kbase is the slice start
-    xld = 0;
+    xbase = xw - kbase;  // row b of the slice starts at xbase + b * xld + kbase
+    xld = Kw + kXPad;
   } else {
     // Grouped scales of this workgroup's rows and K-split, staged after x:
     // ss[row_in_block * gps + g_local] (f32).

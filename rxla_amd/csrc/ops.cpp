@@ -189,10 +189,11 @@ struct GemvPlan {
 static size_t gemv_lds(int64_t m, int64_t kc, int64_t k, int64_t g, int rw, int mb,
                        bool w_bf16, int nw = 4) {
   size_t stage = (size_t)m * (kc + 8) * 2 + (g == k ? 0 : (size_t)16 * rw * (kc / g) * 4);
-  // one row, per-channel scales: each of the nw waves may stage its own
-  // K slice (kc / (nw / rw) values) in a region of its own
-  if (m == 1 && g == k && !w_bf16) {
-    const size_t per_wave = (size_t)nw * (kc / (nw / rw) + 8) * 2;
+  // plain rows with per-channel scales (one row, or up to 4 with one row
+  // group): each of the nw waves may stage its own K slice (kc / (nw / rw)
+  // values) of the m rows in a region of its own
+  if ((m == 1 || (rw == 1 && m <= 4)) && g == k && !w_bf16) {
+    const size_t per_wave = (size_t)nw * m * (kc / (nw / rw) + 8) * 2;
     if (per_wave > stage) stage = per_wave;
   }
   const size_t red = (size_t)(nw / rw - 1) * rw * mb * 256 * 4;
