@@ -22,6 +22,7 @@
 //   norm.weight                                   F32 [H]
 // G = config.group, or each linear's input width when group == 0
 // (per-output-channel scales).
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -36,11 +37,6 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
                    int64_t G, int compute_bf16, int y_mode);
 int bf16_linear_launch(Runtime *rt, const void *x, int x_f32, const uint16_t *w, bool packed,
                        void *y, int y_f32, int64_t M, int64_t N, int64_t K);
-int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
-                     int cache_f32, const int32_t *lens, const int32_t *row_seq,
-                     const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
-                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
-                     const AttnRope *rope = nullptr);
 bool prefill_supported(int64_t Hq, int64_t Hkv, int64_t D, int cache_f32);
 bool gemm_eligible(int64_t M, int64_t N, int64_t K, int64_t G);
 int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t q_ss, int64_t q_sh,
@@ -174,11 +170,10 @@ struct Decoder {
   void *tail_block = nullptr;
   size_t tail_bytes = 0;
   int am_chunks = 64;  // argmax partials per row; <= 64 (one lane each in the final pass)
-  // decode-step graph for batch g_b
+  // decode-step graph and the values it bakes in (see graph_key)
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
-  int64_t g_b = -1;
-  void *g_out = nullptr;  // out_ids buffer the graph writes
+  int64_t g_key[10] = {-1};
 
   const ParamSpec &p(int layer, int kind) const {
     return params[by_layer_kind[(size_t)(layer < 0 ? 0 : layer) * 14 + kind]];
@@ -247,6 +242,17 @@ static int ensure_activations(Decoder *d, int64_t T) {
   d->cap_T = T;
   d->act_bytes = total;
   return RXW8_OK;
+}
+
+// What a captured decode step depends on beyond the decoder's fixed state.
+static void graph_key(const Decoder *d, int64_t b, int64_t ncols, const void *out, int64_t key[10]) {
+  const Runtime *rt = d->rt;
+  const void *ptrs[7] = {out, d->act_block, rt->partials.ptr, rt->scratch.ptr, rt->xcast.ptr,
+                         rt->wdeq.ptr, rt->attn_counters.ptr};
+  key[0] = b;
+  key[1] = ncols;
+  key[2] = d->cap_T;
+  for (int i = 0; i < 7; ++i) key[3 + i] = (int64_t)(intptr_t)ptrs[i];
 }
 
 static unsigned blocks(int64_t n, int per = 256) { return (unsigned)std::max<int64_t>(1, (n + per - 1) / per); }
@@ -702,7 +708,15 @@ int rxw8_decoder_generate(rxw8_decoder *d, rxw8_buffer *prompt, int64_t b, int64
   auto step = [&]() -> int { return enqueue_forward(d, d->next, b, 1, &rec); };
   int64_t done = 0;
   if (use_graph) {
-    if (d->g_b != b || d->g_out != out_ids->ptr || !d->gexec) {
+    // A captured step holds the batch, the out_ids row stride (steps + 1) and
+    // address, the activation block and every runtime workspace it used. Any
+    // of these can change between calls (a longer prompt regrows the
+    // activations; another op regrows a workspace; a freed out_ids block of
+    // the same rounded size is handed out again for another `steps`), so the
+    // graph is kept only while all of them match.
+    int64_t key[10];
+    graph_key(d, b, steps + 1, out_ids->ptr, key);
+    if (!d->gexec || !std::equal(key, key + 10, d->g_key)) {
       if ((rc = step())) return rc;  // eager step sizes every workspace first
       for (int64_t i = 0; i < b; ++i) d->h_lens[(size_t)i] += 1;
       done = 1;
@@ -710,7 +724,7 @@ int rxw8_decoder_generate(rxw8_decoder *d, rxw8_buffer *prompt, int64_t b, int64
       if (d->graph) (void)hipGraphDestroy(d->graph);
       d->gexec = nullptr;
       d->graph = nullptr;
-      d->g_b = -1;
+      d->g_key[0] = -1;
       RXW8_HIP(hipStreamBeginCapture(rt->stream, hipStreamCaptureModeThreadLocal));
       rc = step();
       hipGraph_t graph = nullptr;
@@ -726,8 +740,9 @@ int rxw8_decoder_generate(rxw8_decoder *d, rxw8_buffer *prompt, int64_t b, int64
         return hip_fail(e, "hipGraphInstantiate");
       }
       d->graph = graph;
-      d->g_b = b;
-      d->g_out = out_ids->ptr;
+      // the eager step above sized every workspace, so the key taken now is
+      // the one the capture used
+      graph_key(d, b, steps + 1, out_ids->ptr, d->g_key);
     }
     for (; done < steps; ++done) {
       RXW8_HIP(hipGraphLaunch(d->gexec, rt->stream));

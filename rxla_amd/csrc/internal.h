@@ -118,6 +118,29 @@ int gemv_launch(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf1
                 int y_mode, const GemvOptions &pro);
 
 
+// Caller-provided attention workspace (split partials and arrival counters)
+// used in place of the runtime's own, which would grow on demand. A launch
+// whose plan needs more than either capacity fails with RESOURCE_EXHAUSTED
+// and launches nothing. The counters must be zero before the first use; the
+// kernel re-arms each one it uses to zero.
+struct AttnWorkspace {
+  float *partials = nullptr;
+  size_t partial_bytes = 0;
+  int *counters = nullptr;
+  size_t counter_bytes = 0;
+};
+
+// Decode attention over a contiguous [R|B, Hkv, Lmax, D] cache (ops.cpp).
+int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
+                     int cache_f32, const int32_t *lens, const int32_t *row_seq,
+                     const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
+                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
+                     const AttnRope *rope = nullptr, const AttnWorkspace *ws = nullptr);
+
+// rxw8_gqa_decode_into with an optional caller workspace (ops.cpp).
+int gqa_decode_into(Runtime *rt, Buffer *q, Buffer *k_cache, Buffer *v_cache, Buffer *lens,
+                    Buffer *mask, float scale, Buffer *out, const AttnWorkspace *ws);
+
 // Device-side allocation through the runtime's cache.
 int rt_alloc(Runtime *rt, size_t bytes, void **out);
 void rt_free(Runtime *rt, void *ptr, size_t bytes);

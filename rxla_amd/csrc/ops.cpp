@@ -657,7 +657,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
                      int cache_f32, const int32_t *lens, const int32_t *row_seq,
                      const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
                      int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
-                     const AttnRope *rope) {
+                     const AttnRope *rope, const AttnWorkspace *ext) {
   if (R == 0) return RXW8_OK;
   const int64_t G = Hq / Hkv;
   const bool fast = !cache_f32 && D == 128 && (G == 1 || G == 2 || G == 4 || G == 8) &&
@@ -704,12 +704,27 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     // (arrival counters, zeroed once at allocation and re-armed by the kernel);
     // RXW8_ATTN_TWO_PASS=1 uses the separate combine launch instead.
     const bool two_pass = env_int("RXW8_ATTN_TWO_PASS", 0) != 0;
+    float *ws_partials = nullptr;
+    int *ws_counters = nullptr;
     if (max_chunks > 1) {
-      int rc = ensure_workspace(rt, rt->scratch,
-                                (size_t)R * Hkv * max_chunks * G * (2 + D) * sizeof(float), false);
-      if (rc) return rc;
-      if (!two_pass && (rc = ensure_workspace(rt, rt->attn_counters, (size_t)R * Hkv * sizeof(int), true)))
-        return rc;
+      const size_t need_p = (size_t)R * Hkv * max_chunks * G * (2 + D) * sizeof(float);
+      const size_t need_c = two_pass ? 0 : (size_t)R * Hkv * sizeof(int);
+      if (ext) {
+        if (need_p > ext->partial_bytes || need_c > ext->counter_bytes)
+          return fail(RXW8_RESOURCE_EXHAUSTED,
+                      "decode attention (B=%lld Hkv=%lld Lmax=%lld, %lld splits) needs %zu bytes of "
+                      "split partials and %zu of counters; the caller's workspace holds %zu and %zu",
+                      (long long)R, (long long)Hkv, (long long)Lmax, (long long)max_chunks, need_p,
+                      need_c, ext->partial_bytes, ext->counter_bytes);
+        ws_partials = ext->partials;
+        ws_counters = ext->counters;
+      } else {
+        int rc = ensure_workspace(rt, rt->scratch, need_p, false);
+        if (rc) return rc;
+        if (need_c && (rc = ensure_workspace(rt, rt->attn_counters, need_c, true))) return rc;
+        ws_partials = (float *)rt->scratch.ptr;
+        ws_counters = (int *)rt->attn_counters.ptr;
+      }
     }
     AttnArgs a;
     a.q = q;
@@ -719,7 +734,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     a.row_seq = row_seq;
     a.mask = mask;
     a.out = out;
-    a.ws = (float *)rt->scratch.ptr;
+    a.ws = ws_partials;
     a.mask_sb = mask_sb;
     a.mask_sh = mask_sh;
     a.R = (int)R;
@@ -735,7 +750,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     a.k_norm = rope ? rope->k_norm : nullptr;
     a.rope = rope ? rope->table : nullptr;
     a.eps = rope ? rope->eps : 0.f;
-    a.counters = max_chunks > 1 && !two_pass ? (int *)rt->attn_counters.ptr : nullptr;
+    a.counters = max_chunks > 1 && !two_pass ? ws_counters : nullptr;
     a.units = (int)units;
     char kname[64];
     std::snprintf(kname, sizeof kname, rope ? "rxw8_gqa_decode_rope_d128_g%d" : "rxw8_gqa_decode_d128_g%d",
@@ -1031,9 +1046,11 @@ static int check_gqa(const Buffer *q, const Buffer *k, const Buffer *v, const Bu
   return RXW8_OK;
 }
 
-int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
-                         rxw8_buffer *v_cache, rxw8_buffer *lens, rxw8_buffer *mask, float scale,
-                         rxw8_buffer *out) {
+}  // extern "C"
+
+namespace rxw8 {
+int gqa_decode_into(Runtime *rt, Buffer *q, Buffer *k_cache, Buffer *v_cache, Buffer *lens,
+                    Buffer *mask, float scale, Buffer *out, const AttnWorkspace *ws) {
   if (!rt || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
   int64_t sb, sh;
   int rc = check_gqa(q, k_cache, v_cache, lens, mask, &sb, &sh);
@@ -1049,7 +1066,16 @@ int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
                           k_cache->dtype == RXW8_F32, (const int32_t *)lens->ptr, nullptr,
                           mask ? (const float *)mask->ptr : nullptr, sb, sh, out->ptr,
                           out->dtype == RXW8_F32, q->dims[0], q->dims[1], k_cache->dims[1],
-                          k_cache->dims[2], D, scale, nullptr);
+                          k_cache->dims[2], D, scale, nullptr, ws);
+}
+}  // namespace rxw8
+
+extern "C" {
+
+int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
+                         rxw8_buffer *v_cache, rxw8_buffer *lens, rxw8_buffer *mask, float scale,
+                         rxw8_buffer *out) {
+  return rxw8::gqa_decode_into(rt, q, k_cache, v_cache, lens, mask, scale, out, nullptr);
 }
 
 int rxw8_gqa_decode(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache, rxw8_buffer *v_cache,

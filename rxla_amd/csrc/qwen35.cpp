@@ -45,11 +45,6 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
                    const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
                    int64_t G, int compute_bf16, int y_mode);
 bool gemm_eligible(int64_t M, int64_t N, int64_t K, int64_t G);
-int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, const void *vc,
-                     int cache_f32, const int32_t *lens, const int32_t *row_seq,
-                     const float *mask, int64_t mask_sb, int64_t mask_sh, void *out, int out_f32,
-                     int64_t R, int64_t Hq, int64_t Hkv, int64_t Lmax, int64_t D, float scale,
-                     const AttnRope *rope);
 
 namespace {
 

@@ -233,6 +233,33 @@ def test_generate_graph_matches_eager_and_oracle(rt):
     np.testing.assert_array_equal(outs[0][:, :3], want[:, :3])
 
 
+def test_generate_twice_on_one_model_rebuilds_the_graph(rt):
+    """A second generate on the same model with a longer prompt (the
+    activation block regrows) and another step count (the out_ids row stride
+    changes; at batch 2 an [2, 9] and an [2, 31] I32 buffer round to the same
+    cached block) must not replay the first call's graph."""
+    cfg = small_cfg(max_seq=48)
+    params = tiny_params(cfg, seed=63, std=0.05)
+    batch = 2
+    rng = np.random.default_rng(64)
+    runs = [(rng.integers(0, cfg["vocab"], (batch, 6)).astype(np.int32), 8),
+            (rng.integers(0, cfg["vocab"], (batch, 12)).astype(np.int32), 30),
+            (rng.integers(0, cfg["vocab"], (batch, 12)).astype(np.int32), 30)]
+    model = build(rt, cfg, params, batch)
+    got = []
+    for prompt, steps in runs:
+        model.reset()
+        out = model.generate(rt.buffer(prompt), steps, use_graph=True)
+        got.append(out.to_numpy())
+        del out  # its block returns to the cache and may be handed out again
+        np.testing.assert_array_equal(model.lens()[:batch], [prompt.shape[1] + steps] * batch)
+    eager = build(rt, cfg, params, batch)
+    for (prompt, steps), g in zip(runs, got):
+        eager.reset()
+        want = eager.generate(rt.buffer(prompt), steps, use_graph=False).to_numpy()
+        np.testing.assert_array_equal(g, want)
+
+
 def test_decoder_binding_and_capacity_errors(rt):
     r = rx()
     cfg = small_cfg(max_seq=8)
