@@ -119,6 +119,19 @@ int rxw8_buffer_device_ptr(const rxw8_buffer *buf, void **ptr);
  * caller buffer of the exact shape/dtype and allocate nothing per call
  * (split-K workspaces are runtime-owned, grown on first use). */
 
+/* The W8 encoder (benchmarks/quantize_qwen3_5_w8.py:27-44): for each row and
+ * group of group_size columns, s = max(amax, 1e-12) / 127 and
+ * u8 = clamp(rne(w / s), -127, 127) + 128, in f32 with a correctly rounded
+ * division, as the encoder's torch ops compute.
+ *   w F32|BF16 [N,K] (BF16 widens exactly, the encoder's value.float());
+ *   weight U8 [N,K] and scale F32 [N, K/group_size] are new buffers.
+ * group_size = K gives per-output-channel scales. INVALID_ARGUMENT for a
+ * non-positive group size or one that does not divide K (the encoder's
+ * ValueErrors). A group holding a NaN gets a NaN scale and code 128 (the
+ * encoder's codes there come from an unspecified NaN-to-uint8 cast). */
+int rxw8_quantize_w8(rxw8_runtime *rt, rxw8_buffer *w, int64_t group_size,
+                     rxw8_buffer **weight, rxw8_buffer **scale);
+
 /* W8 dequantisation (layers.rs:277-287): W = (f32(u8) - 128) * scale[n, k/G]
  * -> F32 (bit-exact) or BF16 (RNE of the f32 value). weight U8 [N,K],
  * scale F32 [N,K/G]. */
@@ -196,6 +209,15 @@ int rxw8_gqa_prefill(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache,
 int rxw8_gqa_prefill_into(rxw8_runtime *rt, rxw8_buffer *q,
                           rxw8_buffer *k_cache, rxw8_buffer *v_cache,
                           rxw8_buffer *starts, float scale, rxw8_buffer *out);
+
+/* Tensor::argmax(axis, keep_dims) (crates/rxla-core/src/indexing.rs:350-374):
+ * index of the first maximum along `axis` of an F32 tensor, as I32 with that
+ * axis removed (keep_dims: kept with length 1). Ties choose the lowest index;
+ * a NaN beats every number and the first NaN wins. INVALID_ARGUMENT unless
+ * 0 <= axis < rank and 0 < dims[axis] <= INT32_MAX; other empty axes give an
+ * empty result. The same two kernels end every decoder step (greedy ids). */
+int rxw8_argmax(rxw8_runtime *rt, rxw8_buffer *x, int axis, int keep_dims,
+                rxw8_buffer **out);
 
 /* KvCache::update_at / update_at_checked (kv_cache.rs:53-111): paired
  * dynamic_update_slice of k_update/v_update (equal shapes, rank = cache rank,
@@ -310,6 +332,12 @@ typedef struct rxw8_qwen35_config {
   int64_t lora_rank; /* 0 = no LoRA on the tied head */
   float lora_alpha;
   int64_t max_batch, max_seq; /* activation capacity of one forward */
+  /* Compute dtype of every projection: RXW8_F32 (also selected by 0), the
+   * reference's: qwen3_5/layers.rs:4-9 takes cx.layer_compute_dtype(), which
+   * qwen3_5() leaves at the Cx default F32 (rxla-nn lib.rs:432); activations
+   * stay f32 throughout. RXW8_BF16 is an opt-in (with_layer_compute_dtype):
+   * bf16(x) . bf16(W) rounded to bf16, on the packed W8A16 GEMV / GEMM. */
+  int32_t compute_dtype;
 } rxw8_qwen35_config;
 
 typedef struct rxw8_qwen35 rxw8_qwen35;

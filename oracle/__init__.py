@@ -302,7 +302,7 @@ class _Cfg(ctypes.Structure):
     _fields_ = [("layers", c_int64), ("hidden", c_int64), ("q_heads", c_int64),
                 ("kv_heads", c_int64), ("head_dim", c_int64), ("intermediate", c_int64),
                 ("vocab", c_int64), ("max_seq", c_int64), ("group", c_int64),
-                ("eps", c_float), ("theta", c_float), ("qk_norm", c_int32)]
+                ("eps", c_float), ("theta", c_float), ("qk_norm", c_int32), ("accum", c_int32)]
 
 
 class _Params(ctypes.Structure):
@@ -322,7 +322,7 @@ class Decoder:
         c = self.cfg
         self._c = _Cfg(c["layers"], c["hidden"], c["q_heads"], c["kv_heads"], c["head_dim"],
                        c["intermediate"], c["vocab"], c["max_seq"], c["group"], c["eps"],
-                       c["theta"], int(c.get("qk_norm", True)))
+                       c["theta"], int(c.get("qk_norm", True)), int(c.get("accum", ACCUM_F32)))
         nl = c["layers"]
         self._keep = []
 

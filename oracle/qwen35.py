@@ -1,12 +1,16 @@
 """Oracle for the hybrid Qwen3.5 W8 text model (TEST INFRASTRUCTURE ONLY:
 imported by tests/ as the checker, never by the product path).
 
-A numpy restatement, in float64 with the reference's bf16 cast points, of
+A numpy restatement, in float64 with the reference's cast points, of
 crates/rxla-models/src/qwen3_5/mod.rs:234-273 (model) and layers.rs (mixers):
   * W8 embedding gather: (f32(u8) - 128) * scale, rows clamped   mod.rs:158-179
   * zero-centred RMSNorm: x * rsqrt(mean(x^2) + eps) * (1 + w)    layers.rs(nn):459-491
-  * projections: bf16(x) . bf16((u8 - 128) * s)^T rounded to bf16,
-    returned as f32                                               rxla-nn layers.rs:257-298
+  * projections (rxla-nn layers.rs:257-298) at the layer compute dtype, which
+    qwen3_5() leaves at the Cx default F32 (rxla-nn lib.rs:432; qwen3_5/
+    layers.rs:4-9 reads cx.layer_compute_dtype()):
+      F32  (cfg compute "f32", the default): f32 x . ((u8 - 128) * s)^T in
+           f64, returned as f32 (dot_general at HIGHEST precision, emitter.rs:58)
+      BF16 (cfg compute "bf16", an opt-in): bf16(x) . bf16(W)^T rounded to bf16
   * full attention with output gate and partial RoPE              layers.rs:28-100
   * gated-delta linear attention (causal depthwise conv + SiLU,
     L2-normalised q/k, delta-rule recurrence, gated RMSNorm)      layers.rs:113-268
@@ -29,7 +33,7 @@ def config(**kw):
     widths the callers override."""
     c = dict(vocab=128, hidden=32, intermediate=64, layers=[LINEAR, FULL], heads=4, kv_heads=2,
              head_dim=8, linear_heads=4, linear_head_dim=8, conv_kernel=4, theta=1e7,
-             rotary_dim=4, eps=1e-6, group=8)
+             rotary_dim=4, eps=1e-6, group=8, compute="f32")
     c.update(kw)
     return c
 
@@ -48,8 +52,15 @@ def dequant(u8, scale):
     return (w * scale.astype(np.float32)[:, :, None]).reshape(n, k).astype(np.float32)
 
 
-def projection(x, u8, scale):
-    """compute dtype BF16: f32(bf16(bf16(x) . bf16(W)^T)) with f64 accumulation."""
+def projection(x, u8, scale, compute="f32"):
+    """QuantizedLinear::apply (layers.rs:257-298) with f64 accumulation.
+    compute "f32": f32(f32(x) . W^T), W = (f32(u8) - 128) * s in f32;
+    compute "bf16": f32(bf16(bf16(x) . bf16(W)^T))."""
+    if compute == "f32":
+        xf = np.asarray(x, np.float32).astype(np.float64)
+        return (xf @ dequant(u8, scale).astype(np.float64).T).astype(np.float32)
+    if compute != "bf16":
+        raise ValueError(f"compute dtype {compute!r}")
     xb = round_bf16(np.asarray(x, np.float32)).astype(np.float64)
     wb = round_bf16(dequant(u8, scale)).astype(np.float64)
     return round_bf16((xb @ wb.T).astype(np.float32))
@@ -133,21 +144,22 @@ def gated_delta(x, p, pre, cfg):
     b, s, _ = x.shape
     hl, dl = cfg["linear_heads"], cfg["linear_head_dim"]
     width = hl * dl
-    mixed = projection(x, p[pre + "in_proj_qkv.weight"], p[pre + "in_proj_qkv.scale"])
+    cd = cfg.get("compute", "f32")
+    mixed = projection(x, p[pre + "in_proj_qkv.weight"], p[pre + "in_proj_qkv.scale"], cd)
     conv_w = np.asarray(p[pre + "conv1d.weight"], np.float64).reshape(3 * width, -1)
     mixed = silu(depthwise_causal_conv(mixed.astype(np.float64), conv_w))
     q = l2_norm(mixed[..., :width].reshape(b, s, hl, dl)) * (1.0 / np.sqrt(np.float32(dl)))
     k = l2_norm(mixed[..., width:2 * width].reshape(b, s, hl, dl))
     v = mixed[..., 2 * width:].reshape(b, s, hl, dl)
-    z = projection(x, p[pre + "in_proj_z.weight"], p[pre + "in_proj_z.scale"]).reshape(b, s, hl, dl)
-    beta = sigmoid(projection(x, p[pre + "in_proj_b.weight"], p[pre + "in_proj_b.scale"]))
-    a = projection(x, p[pre + "in_proj_a.weight"], p[pre + "in_proj_a.scale"]).astype(np.float64)
+    z = projection(x, p[pre + "in_proj_z.weight"], p[pre + "in_proj_z.scale"], cd).reshape(b, s, hl, dl)
+    beta = sigmoid(projection(x, p[pre + "in_proj_b.weight"], p[pre + "in_proj_b.scale"], cd))
+    a = projection(x, p[pre + "in_proj_a.weight"], p[pre + "in_proj_a.scale"], cd).astype(np.float64)
     decay = softplus(a + np.asarray(p[pre + "dt_bias"], np.float64)) * \
         (-np.exp(np.asarray(p[pre + "A_log"], np.float64)))
     out = delta_rule(q, k, v, beta, np.exp(decay))
     o = rms_norm(out, p[pre + "norm.weight"], cfg["eps"], False) * silu(z)
     return projection(o.reshape(b, s, width).astype(np.float32), p[pre + "out_proj.weight"],
-                      p[pre + "out_proj.scale"])
+                      p[pre + "out_proj.scale"], cd)
 
 
 def full_attention(x, p, pre, cfg, angles):
@@ -155,12 +167,13 @@ def full_attention(x, p, pre, cfg, angles):
     causal GQA over the sequence."""
     b, s, _ = x.shape
     hq, hkv, d = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
-    qg = projection(x, p[pre + "q_proj.weight"], p[pre + "q_proj.scale"]).reshape(b, s, hq, 2 * d)
+    cd = cfg.get("compute", "f32")
+    qg = projection(x, p[pre + "q_proj.weight"], p[pre + "q_proj.scale"], cd).reshape(b, s, hq, 2 * d)
     query, gate = qg[..., :d].astype(np.float64), sigmoid(qg[..., d:].reshape(b, s, hq * d))
     query = rms_norm(query, p[pre + "q_norm.weight"], cfg["eps"], True).transpose(0, 2, 1, 3)
-    key = projection(x, p[pre + "k_proj.weight"], p[pre + "k_proj.scale"]).reshape(b, s, hkv, d)
+    key = projection(x, p[pre + "k_proj.weight"], p[pre + "k_proj.scale"], cd).reshape(b, s, hkv, d)
     key = rms_norm(key, p[pre + "k_norm.weight"], cfg["eps"], True).transpose(0, 2, 1, 3)
-    value = projection(x, p[pre + "v_proj.weight"], p[pre + "v_proj.scale"]).reshape(
+    value = projection(x, p[pre + "v_proj.weight"], p[pre + "v_proj.scale"], cd).reshape(
         b, s, hkv, d).astype(np.float64).transpose(0, 2, 1, 3)
     query = partial_rope(query, angles, cfg["rotary_dim"])
     key = partial_rope(key, angles, cfg["rotary_dim"])
@@ -172,14 +185,14 @@ def full_attention(x, p, pre, cfg, angles):
         sc = np.exp(sc - sc.max(axis=-1, keepdims=True))
         out[:, h] = np.einsum("bst,btd->bsd", sc / sc.sum(axis=-1, keepdims=True), value[:, h // g])
     att = out.transpose(0, 2, 1, 3).reshape(b, s, hq * d) * gate
-    return projection(att.astype(np.float32), p[pre + "o_proj.weight"], p[pre + "o_proj.scale"])
+    return projection(att.astype(np.float32), p[pre + "o_proj.weight"], p[pre + "o_proj.scale"], cd)
 
 
-def mlp(x, p, pre):
-    g = projection(x, p[pre + "gate_proj.weight"], p[pre + "gate_proj.scale"]).astype(np.float64)
-    u = projection(x, p[pre + "up_proj.weight"], p[pre + "up_proj.scale"]).astype(np.float64)
+def mlp(x, p, pre, compute="f32"):
+    g = projection(x, p[pre + "gate_proj.weight"], p[pre + "gate_proj.scale"], compute).astype(np.float64)
+    u = projection(x, p[pre + "up_proj.weight"], p[pre + "up_proj.scale"], compute).astype(np.float64)
     return projection((silu(g) * u).astype(np.float32), p[pre + "down_proj.weight"],
-                      p[pre + "down_proj.scale"])
+                      p[pre + "down_proj.scale"], compute)
 
 
 def forward(cfg, p, ids):
@@ -200,7 +213,7 @@ def forward(cfg, p, ids):
             mixed = full_attention(n, p, pre + "self_attn.", cfg, angles)
         h = h + mixed
         n = rms_norm(h, p[pre + "post_attention_layernorm.weight"], cfg["eps"], True).astype(np.float32)
-        h = h + mlp(n, p, pre + "mlp.")
+        h = h + mlp(n, p, pre + "mlp.", cfg.get("compute", "f32"))
     n = rms_norm(h, p[root + "norm.weight"], cfg["eps"], True)
     logits = n @ table.astype(np.float64).T
     rank = cfg.get("lora_rank", 0)

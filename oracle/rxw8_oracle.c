@@ -559,7 +559,7 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
     uint16_t *vcl = v_cache + l * b * HKV * L * D;
     rxo_rms_norm(h, T, H, p->in_norm[l], cfg->eps, 0, n);
     rc = rxo_quantized_linear(n, T, H, p->qkv_w[l], p->qkv_s[l], QKV, G_H,
-                              RXO_COMPUTE_BF16, RXO_ACCUM_F32, qkv, threads);
+                              RXO_COMPUTE_BF16, cfg->accum, qkv, threads);
     if (rc) goto done;
     for (int64_t r = 0; r < T; ++r) {
       memcpy(q + r * HQ * D, qkv + r * QKV, sizeof(float) * (size_t)(HQ * D));
@@ -594,17 +594,17 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
                                  1, 1, 1, L, D, scale, 0, att + (r * HQ + hh) * D, 1);
       }
     rc = rxo_quantized_linear(att, T, HQ * D, p->o_w[l], p->o_s[l], H, G_O,
-                              RXO_COMPUTE_BF16, RXO_ACCUM_F32, tmp, threads);
+                              RXO_COMPUTE_BF16, cfg->accum, tmp, threads);
     if (rc) goto done;
     for (int64_t i = 0; i < T * H; ++i) h[i] += tmp[i];
     rxo_rms_norm(h, T, H, p->post_norm[l], cfg->eps, 0, n);
     rc = rxo_quantized_linear(n, T, H, p->gu_w[l], p->gu_s[l], 2 * I, G_H,
-                              RXO_COMPUTE_BF16, RXO_ACCUM_F32, gu, threads);
+                              RXO_COMPUTE_BF16, cfg->accum, gu, threads);
     if (rc) goto done;
     for (int64_t r = 0; r < T; ++r)
       rxo_silu_mul(gu + r * 2 * I, gu + r * 2 * I + I, I, act + r * I);
     rc = rxo_quantized_linear(act, T, I, p->down_w[l], p->down_s[l], H, G_I,
-                              RXO_COMPUTE_BF16, RXO_ACCUM_F32, tmp, threads);
+                              RXO_COMPUTE_BF16, cfg->accum, tmp, threads);
     if (rc) goto done;
     for (int64_t i = 0; i < T * H; ++i) h[i] += tmp[i];
   }
@@ -612,7 +612,7 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
   for (int64_t bi = 0; bi < b; ++bi)
     memcpy(tmp + bi * H, h + (bi * s + s - 1) * H, sizeof(float) * (size_t)H);
   rxo_rms_norm(tmp, b, H, p->final_norm, cfg->eps, 0, n);
-  rc = rxo_linear_bf16w(n, b, H, p->embed, V, RXO_ACCUM_F32, logits, threads);
+  rc = rxo_linear_bf16w(n, b, H, p->embed, V, cfg->accum, logits, threads);
   if (rc) goto done;
   rxo_argmax_rows(logits, b, V, next_ids);
   for (int64_t bi = 0; bi < b; ++bi) lens[bi] += (int32_t)s;

@@ -149,6 +149,10 @@ typedef struct rxo_decoder_config {
   int64_t group;   /* W8 group size; 0 = per-output-channel (G = input width) */
   float eps, theta;
   int32_t qk_norm; /* per-head RMSNorm on q and k before RoPE */
+  int32_t accum;   /* RXO_ACCUM_F32 (sequential f32, the default) or RXO_ACCUM_F64
+                    * for every dot product: two summation orders of the same
+                    * cast points, to measure how far the reference's semantics
+                    * themselves move under a change of accumulation */
 } rxo_decoder_config;
 
 /* Parameters, per layer l (arrays of pointers, length `layers`):

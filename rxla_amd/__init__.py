@@ -224,6 +224,14 @@ def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
 
 # ---- ops ------------------------------------------------------------------------
 
+def quantize_w8(rt: Runtime, w: Buffer, group_size: int) -> tuple[Buffer, Buffer]:
+    """The W8 encoder (benchmarks/quantize_qwen3_5_w8.py:27-44) on the device:
+    F32|BF16 [N, K] -> (U8 [N, K] codes = int8 + 128, F32 [N, K/group] scales)."""
+    hw, hs = c_void_p(), c_void_p()
+    _check(_lib.rxw8_quantize_w8(rt.handle, w.handle, int(group_size), byref(hw), byref(hs)))
+    return Buffer(hw), Buffer(hs)
+
+
 def dequantize(rt: Runtime, weight: Buffer, scale: Buffer, out_dtype=DType.F32) -> Buffer:
     h = c_void_p()
     _check(_lib.rxw8_dequantize(rt.handle, weight.handle, scale.handle, int(out_dtype), byref(h)))
@@ -297,6 +305,14 @@ def grouped_query_attention(rt: Runtime, q: Buffer, k_cache: Buffer, v_cache: Bu
     h = c_void_p()
     _check(_lib.rxw8_gqa_decode(rt.handle, q.handle, k_cache.handle, v_cache.handle,
                                 lens.handle, m, ctypes.c_float(s), int(out_dtype), byref(h)))
+    return Buffer(h)
+
+
+def argmax(rt: Runtime, x: Buffer, axis: int, keep_dims: bool = False) -> Buffer:
+    """``Tensor::argmax`` (crates/rxla-core/src/indexing.rs:350-374): I32
+    index of the first maximum along ``axis``; the first NaN wins."""
+    h = c_void_p()
+    _check(_lib.rxw8_argmax(rt.handle, x.handle, int(axis), int(bool(keep_dims)), byref(h)))
     return Buffer(h)
 
 
@@ -419,8 +435,10 @@ class SafeTensors:
 
 from .model import DecoderConfig, DecoderModel, Qwen35Config, Qwen35Model  # noqa: E402
 
-__all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "dequantize", "pack_weight",
+__all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "quantize_w8", "dequantize",
+           "pack_weight",
            "quantized_linear",
            "linear_bf16", "QuantizedLinear", "grouped_query_attention",
-           "grouped_query_attention_prefill", "KvCache", "SafeTensors",
+           "grouped_query_attention_prefill", "argmax", "KvCache",
+           "SafeTensors",
            "DecoderConfig", "DecoderModel", "Qwen35Config", "Qwen35Model", "bf16_to_f32"]

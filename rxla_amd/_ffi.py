@@ -21,9 +21,9 @@ EXPORTS = [
     "rxw8_buffer_create", "rxw8_buffer_from_host", "rxw8_buffer_wrap", "rxw8_buffer_to_host",
     "rxw8_buffer_copy_from_host", "rxw8_buffer_retain", "rxw8_buffer_release",
     "rxw8_buffer_dtype", "rxw8_buffer_dims", "rxw8_buffer_device_ptr",
-    "rxw8_dequantize", "rxw8_pack_weight", "rxw8_quantized_linear", "rxw8_quantized_linear_into",
+    "rxw8_quantize_w8", "rxw8_dequantize", "rxw8_pack_weight", "rxw8_quantized_linear", "rxw8_quantized_linear_into",
     "rxw8_linear_bf16", "rxw8_linear_bf16_into", "rxw8_gqa_decode", "rxw8_gqa_decode_into",
-    "rxw8_gqa_prefill", "rxw8_gqa_prefill_into", "rxw8_kv_update_at",
+    "rxw8_gqa_prefill", "rxw8_gqa_prefill_into", "rxw8_kv_update_at", "rxw8_argmax",
     "rxw8_safetensors_open", "rxw8_safetensors_close", "rxw8_safetensors_num_tensors",
     "rxw8_safetensors_tensor_info", "rxw8_safetensors_find", "rxw8_safetensors_metadata",
     "rxw8_safetensors_upload",
@@ -52,7 +52,7 @@ class Qwen35Config(Structure):
                 ("group", c_int64), ("full_attention_interval", c_int64),
                 ("layer_kinds", POINTER(c_int32)), ("theta", c_float), ("eps", c_float),
                 ("lora_rank", c_int64), ("lora_alpha", c_float), ("max_batch", c_int64),
-                ("max_seq", c_int64)]
+                ("max_seq", c_int64), ("compute_dtype", c_int32)]
 
 
 def _declare(L):
@@ -77,6 +77,7 @@ def _declare(L):
         "rxw8_buffer_dtype": (c_int, [vp, POINTER(c_int)]),
         "rxw8_buffer_dims": (c_int, [vp, i64p, POINTER(c_int)]),
         "rxw8_buffer_device_ptr": (c_int, [vp, POINTER(vp)]),
+        "rxw8_quantize_w8": (c_int, [vp, vp, c_int64, POINTER(vp), POINTER(vp)]),
         "rxw8_dequantize": (c_int, [vp, vp, vp, c_int, POINTER(vp)]),
         "rxw8_pack_weight": (c_int, [vp, vp, POINTER(vp)]),
         "rxw8_quantized_linear": (c_int, [vp, vp, vp, vp, c_int, c_int, POINTER(vp)]),
@@ -88,6 +89,7 @@ def _declare(L):
         "rxw8_gqa_prefill": (c_int, [vp, vp, vp, vp, vp, c_float, c_int, POINTER(vp)]),
         "rxw8_gqa_prefill_into": (c_int, [vp, vp, vp, vp, vp, c_float, vp]),
         "rxw8_kv_update_at": (c_int, [vp, vp, vp, vp, vp, vp, c_int, vp]),
+        "rxw8_argmax": (c_int, [vp, vp, c_int, c_int, POINTER(vp)]),
         "rxw8_safetensors_open": (c_int, [c_char_p, POINTER(vp)]),
         "rxw8_safetensors_close": (c_int, [vp]),
         "rxw8_safetensors_num_tensors": (c_int, [vp, i64p]),

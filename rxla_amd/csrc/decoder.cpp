@@ -23,6 +23,7 @@
 // G = config.group, or each linear's input width when group == 0
 // (per-output-channel scales).
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -100,6 +101,7 @@ struct ArgmaxArgs {
   int32_t *out;
   int64_t cols;
   int rows, chunks;
+  int64_t inner;
 };
 struct PackArgs {
   const void *src;
@@ -425,7 +427,7 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
       return rc;
   }
   {
-    ArgmaxArgs a{d->logits, d->am_val, d->am_idx, d->next, d->V, (int)b, d->am_chunks};
+    ArgmaxArgs a{d->logits, d->am_val, d->am_idx, d->next, d->V, (int)b, d->am_chunks, 1};
     if ((rc = launch(rt, "rxw8_dec_argmax_partial", dim3((unsigned)(b * d->am_chunks)), dim3(256), a)))
       return rc;
     ArgmaxFinalArgs f{d->am_val, d->am_idx, d->next, d->d_lens, rec ? rec->out : nullptr,
@@ -682,6 +684,53 @@ int rxw8_decoder_forward(rxw8_decoder *d, rxw8_buffer *ids, int64_t b, int64_t s
     RXW8_HIP(hipMemcpyAsync(logits->ptr, d->logits, (size_t)b * d->V * 4, hipMemcpyDeviceToDevice,
                             d->rt->stream));
   for (int64_t i = 0; i < b; ++i) d->h_lens[(size_t)i] += (int32_t)s;
+  return RXW8_OK;
+}
+
+int rxw8_argmax(rxw8_runtime *rt, rxw8_buffer *x, int axis, int keep_dims, rxw8_buffer **out) {
+  if (!rt || !x || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if (x->dtype != RXW8_F32) return fail(RXW8_INVALID_ARGUMENT, "argmax: x must be F32");
+  if (axis < 0 || axis >= x->rank || x->dims[axis] <= 0 || x->dims[axis] > INT32_MAX)
+    return fail(RXW8_INVALID_ARGUMENT, "argmax requires a nonempty axis with I32-sized length");
+  int64_t outer = 1, inner = 1;
+  for (int i = 0; i < axis; ++i) outer *= x->dims[i];
+  for (int i = axis + 1; i < x->rank; ++i) inner *= x->dims[i];
+  const int64_t cols = x->dims[axis], rows = outer * inner;
+  // partials: up to 64 chunks of >= 2048 columns per row, one lane each in
+  // the final pass; the grid is rows x chunks workgroups
+  const int chunks = (int)std::min<int64_t>(64, std::max<int64_t>(1, cols / 2048));
+  if (rows > (int64_t)INT32_MAX / 64)
+    return fail(RXW8_UNIMPLEMENTED, "argmax: %lld rows exceed the kernel's grid", (long long)rows);
+  int64_t od[RXW8_MAX_RANK];
+  int orank = 0;
+  for (int i = 0; i < x->rank; ++i) {
+    if (i == axis && !keep_dims) continue;
+    od[orank++] = i == axis ? 1 : x->dims[i];
+  }
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  Buffer *o = nullptr;
+  int rc = new_buffer(rt, RXW8_I32, od, orank, false, &o);
+  if (rc) return rc;
+  if (rows > 0) {
+    void *part = nullptr;
+    const size_t pbytes = (size_t)rows * chunks * 8;
+    if ((rc = rt_alloc(rt, pbytes, &part))) {
+      rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+      return rc;
+    }
+    float *pval = (float *)part;
+    int32_t *pidx = (int32_t *)((char *)part + (size_t)rows * chunks * 4);
+    ArgmaxArgs a{(const float *)x->ptr, pval, pidx, nullptr, cols, (int)rows, chunks, inner};
+    rc = launch(rt, "rxw8_dec_argmax_partial", dim3((unsigned)(rows * chunks)), dim3(256), a);
+    ArgmaxFinalArgs f{pval, pidx, (int32_t *)o->ptr, nullptr, nullptr, nullptr, (int)rows, chunks, 0, 0};
+    if (!rc) rc = launch(rt, "rxw8_dec_argmax_final", dim3(1), dim3((unsigned)(64 * std::min<int64_t>(rows, 16))), f);
+    rt_free(rt, part, pbytes);
+    if (rc) {
+      rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+      return rc;
+    }
+  }
+  *out = static_cast<rxw8_buffer *>(o);
   return RXW8_OK;
 }
 

@@ -289,12 +289,13 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_silu_mul(SiluMulArgs 
 // every number and the first NaN wins. Pass 1: per-chunk partials; pass 2:
 // chunks in order.
 struct ArgmaxArgs {
-  const float *x;   // [rows, cols]
+  const float *x;   // [outer, cols, inner]; row r = (r / inner, :, r % inner)
   float *pval;      // [rows, chunks]
   int32_t *pidx;
   int32_t *out;     // [rows]
   int64_t cols;
   int rows, chunks;
+  int64_t inner;    // stride of the reduced axis (1: rows are contiguous)
 };
 
 __device__ __forceinline__ bool am_better(float a, int ia, float b, int ib) {
@@ -310,11 +311,13 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_argmax_partial(Argmax
   const int r = blockIdx.x / a.chunks, c = blockIdx.x - r * a.chunks;
   const int64_t per = (a.cols + a.chunks - 1) / a.chunks;
   const int64_t lo = c * per, hi = min(a.cols, lo + per);
+  const int64_t o = r / a.inner, j = r - o * a.inner;
+  const float *xr = a.x + o * a.cols * a.inner + j;
   float bv = -__builtin_huge_valf();
   int bi = (int)(lo < hi ? lo : 0);
   bool have = false;
   for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
-    const float v = a.x[(int64_t)r * a.cols + i];
+    const float v = xr[i * a.inner];
     if (!have || am_better(v, (int)i, bv, bi)) {
       bv = v;
       bi = (int)i;
@@ -352,7 +355,7 @@ struct ArgmaxFinalArgs {
   const float *pval;  // [rows, chunks]
   const int32_t *pidx;
   int32_t *next;      // [rows]
-  int32_t *lens;      // [rows] advanced by s
+  int32_t *lens;      // optional [rows] advanced by s
   int32_t *rec_out;   // optional [rows, ncols]
   int32_t *rec_step;  // device column counter (with rec_out)
   int rows, chunks, s, ncols;
@@ -381,7 +384,7 @@ extern "C" __global__ void __launch_bounds__(1024) rxw8_dec_argmax_final(ArgmaxF
     if (lane == 0) {
       const int id = bi == 0x7fffffff ? 0 : bi;
       a.next[r] = id;
-      a.lens[r] += a.s;
+      if (a.lens) a.lens[r] += a.s;
       if (a.rec_out && col < a.ncols) a.rec_out[r * a.ncols + col] = id;
     }
   }

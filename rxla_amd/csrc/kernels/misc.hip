@@ -27,6 +27,54 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dequant(DequantArgs a) {
   }
 }
 
+// ---- W8 encoder (benchmarks/quantize_qwen3_5_w8.py:27-44): per row and
+// group of G columns, s = max(amax, 1e-12) / 127 and
+// u8 = clamp(rne(w / s), -127, 127) + 128, all in f32 with a correctly rounded
+// division (not a reciprocal multiply), as the encoder's torch ops compute.
+// One wave per (row, group): lanes stride the group for the amax (a NaN makes
+// the scale NaN, as torch's amax propagates it), a butterfly reduces it, and
+// a second pass over the same (cache-resident) group writes the codes.
+// A group containing NaN gets code 128 throughout: the reference's codes for
+// it come from a NaN-to-uint8 cast, which torch leaves unspecified.
+struct QuantizeArgs {
+  const void *w;   // [n, k] f32 or bf16
+  uint8_t *u8;     // [n, k]
+  float *scale;    // [n, k / g]
+  int64_t n, k, g;
+  int w_bf16;
+};
+
+__device__ __forceinline__ float quant_load(const QuantizeArgs &a, int64_t i) {
+  return a.w_bf16 ? bf16_bits_to_f32(((const uint16_t *)a.w)[i]) : ((const float *)a.w)[i];
+}
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_quantize_w8(QuantizeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t groups = a.k / a.g;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= a.n * groups) return;  // whole waves only; no barriers below
+  const int64_t r = unit / groups, gi = unit - r * groups;
+  const int64_t base = r * a.k + gi * a.g;
+  float amax = 0.f;
+  int nan = 0;
+  for (int64_t i = lane; i < a.g; i += 64) {
+    const float v = fabsf(quant_load(a, base + i));
+    nan |= v != v;
+    amax = fmaxf(amax, v);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, o));
+    nan |= __shfl_xor(nan, o);
+  }
+  const float s = nan ? __builtin_nanf("") : (amax >= 1e-12f ? amax : 1e-12f) / 127.0f;
+  if (lane == 0) a.scale[r * groups + gi] = s;
+  for (int64_t i = lane; i < a.g; i += 64) {
+    const float qf = rintf(quant_load(a, base + i) / s);
+    const int code = nan ? 128 : (int)fminf(fmaxf(qf, -127.0f), 127.0f) + 128;
+    a.u8[base + i] = (uint8_t)code;
+  }
+}
+
 // ---- generic linear in reference order: one thread per output element.
 //   compute BF16: y = bf16( sum_k bf16(x) * bf16((u8 - 128) * s) )
 //   compute F32:  y = sum_k x * ((u8 - 128) * s)

@@ -102,9 +102,9 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a
 // the token's position. norm: zero-centred RMSNorm over D; RoPE: split-half
 // over the first rot channels with angle pos * freqs[i] (mod.rs:209-229).
 struct Q35FaPrepArgs {
-  const uint16_t *qg;    // [T, Hq * 2D] rows of `stride` elements
-  const uint16_t *kp;    // [T, Hkv * D] rows of `stride` elements
-  const uint16_t *vp;    // [T, Hkv * D] rows of `stride` elements
+  const void *qg;        // [T, Hq * 2D] rows of `stride` elements
+  const void *kp;        // [T, Hkv * D] rows of `stride` elements
+  const void *vp;        // [T, Hkv * D] rows of `stride` elements
   const float *q_norm, *k_norm;  // [D]
   const float *freqs;    // [rot / 2]
   float *q_out;          // [T, Hq, D]
@@ -112,6 +112,7 @@ struct Q35FaPrepArgs {
   float *kc, *vc;        // [B, Hkv, Lmax, D]
   int T, S, Hq, Hkv, D, rot, Lmax, stride;
   float eps;
+  int src_f32;           // projection rows in f32 (F32 compute) or bf16
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs a) {
@@ -124,12 +125,13 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
   const int bseq = t / a.S, pos = t - bseq * a.S;
   const int D = a.D;
   const bool is_q = h < a.Hq;
-  const uint16_t *src = is_q ? a.qg + (int64_t)t * a.stride + (int64_t)h * 2 * D
-                             : a.kp + (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
+  const int64_t src = is_q ? (int64_t)t * a.stride + (int64_t)h * 2 * D
+                            : (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
+  const void *sbase = is_q ? a.qg : a.kp;
   float *row = rowbuf[wv];
   float ss = 0.f;
   for (int i = lane; i < D; i += 64) {
-    const float v = bf16_bits_to_f32(src[i]);
+    const float v = ld(sbase, src + i, a.src_f32);
     row[i] = v;
     ss += v * v;
   }
@@ -155,11 +157,11 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
   }
   if (is_q) {
     for (int i = lane; i < D; i += 64)
-      a.gate_out[(int64_t)t * a.Hq * D + (int64_t)h * D + i] = sigmoid_f32(bf16_bits_to_f32(src[D + i]));
+      a.gate_out[(int64_t)t * a.Hq * D + (int64_t)h * D + i] = sigmoid_f32(ld(a.qg, src + D + i, a.src_f32));
   } else {
-    const uint16_t *vs = a.vp + (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
+    const int64_t vs = (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
     float *vd = a.vc + (((int64_t)bseq * a.Hkv + (h - a.Hq)) * a.Lmax + pos) * D;
-    for (int i = lane; i < D; i += 64) vd[i] = bf16_bits_to_f32(vs[i]);
+    for (int i = lane; i < D; i += 64) vd[i] = ld(a.vp, vs + i, a.src_f32);
   }
 }
 
@@ -422,7 +424,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_mul(Q35MulArgs a) {
 // The projection row of token t (bf16, `stride` elements) holds the conv
 // input channels [0, 3W), then z [3W, 4W), b [4W, 4W + Hl), a after b.
 struct Q35MixPrepArgs {
-  const uint16_t *raw;           // [T, stride]
+  const void *raw;               // [T, stride], f32 (F32 compute) or bf16
   const float *conv_w;           // [3W, k]
   const float *a_log, *dt_bias;  // [Hl]
   float *mixed;                  // [T, 3W]: q (normed, scaled), k (normed), v
@@ -430,6 +432,7 @@ struct Q35MixPrepArgs {
   int64_t stride;
   int S, Hl, Dl, k;
   float q_scale;
+  int raw_f32;
 };
 
 extern "C" __global__ void __launch_bounds__(128) rxw8_q35_mix_prep(Q35MixPrepArgs a) {
@@ -450,11 +453,11 @@ extern "C" __global__ void __launch_bounds__(128) rxw8_q35_mix_prep(Q35MixPrepAr
       for (int j = 0; j < a.k; ++j) {
         const int src = pos - (a.k - 1) + j;
         if (src < 0) continue;
-        const uint16_t *row = a.raw + (t - pos + src) * a.stride;
+        const int64_t row = (t - pos + src) * a.stride;
 #pragma unroll
         for (int part = 0; part < 3; ++part) {
           const int64_t ch = part * W + (int64_t)h * a.Dl + c;
-          acc[part] += a.conv_w[ch * a.k + j] * bf16_bits_to_f32(row[ch]);
+          acc[part] += a.conv_w[ch * a.k + j] * ld(a.raw, row + ch, a.raw_f32);
         }
       }
       qv[r] = acc[0] * sigmoid_f32(acc[0]);
@@ -483,9 +486,9 @@ extern "C" __global__ void __launch_bounds__(128) rxw8_q35_mix_prep(Q35MixPrepAr
     }
   }
   if (threadIdx.x == 0) {
-    const uint16_t *row = a.raw + t * a.stride + 4 * W;
-    a.beta[t * a.Hl + h] = sigmoid_f32(bf16_bits_to_f32(row[h]));
-    const float x = bf16_bits_to_f32(row[a.Hl + h]) + a.dt_bias[h];
+    const int64_t row = t * a.stride + 4 * W;
+    a.beta[t * a.Hl + h] = sigmoid_f32(ld(a.raw, row + h, a.raw_f32));
+    const float x = ld(a.raw, row + a.Hl + h, a.raw_f32) + a.dt_bias[h];
     const float sp = fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
     a.g[t * a.Hl + h] = expf(sp * -expf(a.a_log[h]));
   }
@@ -692,18 +695,23 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_lora(Q35LoraArgs a) {
 }
 
 // ---- SwiGLU of separate gate / up projections (layers.rs:270-293):
-// act = bf16(silu(g) * u) with g, u the bf16 projection outputs.
+// act = silu(g) * u with g, u the projection outputs: f32 throughout under F32
+// compute, else bf16 inputs and a bf16-rounded result.
 struct Q35SiluArgs {
-  const uint16_t *g, *u;  // [T, I] rows of `stride` elements
-  uint16_t *act;          // [T, I]
+  const void *g, *u;  // [T, I] rows of `stride` elements
+  void *act;          // [T, I]
   int64_t n, I, stride;
+  int f32;
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_q35_silu_mul(Q35SiluArgs a) {
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < a.n;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = e / a.I, c = e - t * a.I;
-    a.act[e] = f32_to_bf16_bits(silu_mul_f32(bf16_bits_to_f32(a.g[t * a.stride + c]),
-                                             bf16_bits_to_f32(a.u[t * a.stride + c])));
+    const float y = silu_mul_f32(ld(a.g, t * a.stride + c, a.f32), ld(a.u, t * a.stride + c, a.f32));
+    if (a.f32)
+      ((float *)a.act)[e] = y;
+    else
+      ((uint16_t *)a.act)[e] = f32_to_bf16_bits(y);
   }
 }

@@ -83,6 +83,14 @@ struct DequantArgs {
   int out_bf16;
 };
 
+struct QuantizeArgs {
+  const void *w;
+  uint8_t *u8;
+  float *scale;
+  int64_t n, k, g;
+  int w_bf16;
+};
+
 struct GenericLinearArgs {
   const void *x;
   const void *w;
@@ -861,6 +869,41 @@ int rxw8_dequantize(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer *scale, i
     return rc;
   }
   *out = static_cast<rxw8_buffer *>(o);
+  return RXW8_OK;
+}
+
+int rxw8_quantize_w8(rxw8_runtime *rt, rxw8_buffer *w, int64_t group_size, rxw8_buffer **weight,
+                     rxw8_buffer **scale) {
+  if (!rt || !w || !weight || !scale) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if ((w->dtype != RXW8_F32 && w->dtype != RXW8_BF16) || w->rank != 2)
+    return fail(RXW8_INVALID_ARGUMENT, "quantize_w8: weight must be F32 or BF16 [rows, columns]");
+  if (group_size <= 0) return fail(RXW8_INVALID_ARGUMENT, "group size must be positive");
+  const int64_t n = w->dims[0], k = w->dims[1];
+  if (n <= 0 || k <= 0) return fail(RXW8_INVALID_ARGUMENT, "quantize_w8: empty weight %s", dims_str(w).c_str());
+  if (k % group_size)
+    return fail(RXW8_INVALID_ARGUMENT, "quantize_w8: width %lld is not divisible by %lld",
+                (long long)k, (long long)group_size);
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  Buffer *u = nullptr, *sc = nullptr;
+  const int64_t sd[2] = {n, k / group_size};
+  int rc = new_buffer(rt, RXW8_U8, w->dims, 2, false, &u);
+  if (!rc) rc = new_buffer(rt, RXW8_F32, sd, 2, false, &sc);
+  if (!rc) {
+    QuantizeArgs a{w->ptr, (uint8_t *)u->ptr, (float *)sc->ptr, n, k, group_size,
+                   w->dtype == RXW8_BF16};
+    const int64_t units = n * (k / group_size);  // one wave each, 4 per workgroup
+    if (units / 4 >= (int64_t)1 << 31)
+      rc = fail(RXW8_UNIMPLEMENTED, "quantize_w8: %lld groups exceed the grid", (long long)units);
+    else
+      rc = launch(rt, "rxw8_quantize_w8", dim3((unsigned)((units + 3) / 4)), dim3(256), a);
+  }
+  if (rc) {
+    if (u) rxw8_buffer_release(static_cast<rxw8_buffer *>(u));
+    if (sc) rxw8_buffer_release(static_cast<rxw8_buffer *>(sc));
+    return rc;
+  }
+  *weight = static_cast<rxw8_buffer *>(u);
+  *scale = static_cast<rxw8_buffer *>(sc);
   return RXW8_OK;
 }
 

@@ -10,11 +10,15 @@
 // optional F32 LoRA update (mod.rs:158-195). Every sequence of the batch runs
 // from position 0 (mod.rs:211-229: positions iota, angles pos * theta^(-2i/r)).
 //
-// Projections are QuantizedLinear with compute dtype BF16 (bf16 x, bf16
-// dequantised weights, f32 accumulation, bf16-rounded result) on the shared
-// W8A16 GEMM / GEMV / generic paths; the LM head computes in F32 (a plain
-// linear against the f32 dequantised table). Token t = b * S + i is position
-// i of sequence b.
+// Projections are QuantizedLinear at the layer compute dtype
+// (qwen3_5/layers.rs:4-9 takes cx.layer_compute_dtype()). The default is the
+// reference's, F32 (rxla-nn lib.rs:432): f32 x against the f32 dequantised
+// weights on the F32 matrix-core linear, with every activation between
+// kernels in f32. The BF16 opt-in (bf16 x, bf16 dequantised weights, f32
+// accumulation, bf16-rounded result) runs on the packed W8A16 GEMV / GEMM with
+// bf16 activations. The LM head computes in F32 either way (a plain linear
+// against the f32 dequantised table). Token t = b * S + i is position i of
+// sequence b.
 //
 // Parameter schema (prefix P = "model.language_model."):
 //   P embed_tokens.{weight U8 [V, H], scale F32 [V, H/G]}        (tied head)
@@ -72,11 +76,12 @@ struct Q35NormArgs {
   int zero_centered, out_f32, z_f32;
 };
 struct Q35FaPrepArgs {
-  const uint16_t *qg, *kp, *vp;
+  const void *qg, *kp, *vp;
   const float *q_norm, *k_norm, *freqs;
   float *q_out, *gate_out, *kc, *vc;
   int T, S, Hq, Hkv, D, rot, Lmax, stride;
   float eps;
+  int src_f32;
 };
 struct Q35AttnArgs {
   const float *q, *kc, *vc, *gate;
@@ -91,7 +96,7 @@ struct Q35MulArgs {
   int64_t n;
 };
 struct Q35MixPrepArgs {
-  const uint16_t *raw;
+  const void *raw;
   const float *conv_w;
   const float *a_log, *dt_bias;
   float *mixed;
@@ -99,6 +104,7 @@ struct Q35MixPrepArgs {
   int64_t stride;
   int S, Hl, Dl, k;
   float q_scale;
+  int raw_f32;
 };
 struct Q35DeltaArgs {
   const float *mixed, *beta, *g;
@@ -106,9 +112,10 @@ struct Q35DeltaArgs {
   int B, S, Hl;
 };
 struct Q35SiluArgs {
-  const uint16_t *g, *u;
-  uint16_t *act;
+  const void *g, *u;
+  void *act;
   int64_t n, I, stride;
+  int f32;
 };
 struct PackArgs {
   const void *src;
@@ -195,7 +202,9 @@ struct Qwen35 {
   void *block = nullptr;
   void *fused = nullptr;
   int64_t n_in_max = 0;
-  bool packed = false;  // widths allow the tile layout (decided at create)
+  bool packed = false;  // BF16 compute and widths that allow the tile layout (decided at create)
+  bool f32c = true;     // projection compute dtype F32 (activations f32), else BF16
+  int64_t esz = 4;      // bytes per element of xn, raw, gated, gu, act (4: f32, 2: bf16)
   // row sums of squares of the residual h (<= 32 rows): embedding [T], residual
   // GEMV partials [H / 16][T]; ss_cur / ss_parts describe h's current state
   float *ss_embed = nullptr, *ss_o = nullptr, *ss_down = nullptr;
@@ -205,17 +214,17 @@ struct Qwen35 {
   float *freqs = nullptr;
   int32_t *zero_lens = nullptr, *pos = nullptr, *row_seq = nullptr, *row_len = nullptr;
   float *h = nullptr, *fin = nullptr, *lora_mid = nullptr;
-  uint16_t *xn = nullptr;
+  void *xn = nullptr;  // normed activations (f32 or bf16, per esz)
   // fused input projection output [T, n_in] (either layer kind)
-  uint16_t *raw = nullptr;
+  void *raw = nullptr;
   // linear layers
-  uint16_t *gated = nullptr;
+  void *gated = nullptr;
   float *mixed = nullptr, *beta = nullptr, *g = nullptr, *dout = nullptr;
   // full layers
   float *q = nullptr, *gate = nullptr, *att = nullptr, *kc = nullptr, *vc = nullptr;
   float *attn_part = nullptr;  // key-range split partials [T, Hq, splits, 2 + D]
   // MLP: [gate | up] projection [T, 2I], SwiGLU output [T, I]
-  uint16_t *gu = nullptr, *act = nullptr;
+  void *gu = nullptr, *act = nullptr;
 
   // forward graph: captured on the second consecutive call with the same
   // (batch, sequence, ids, logits), replayed while that key repeats
@@ -225,6 +234,8 @@ struct Qwen35 {
   int g_calls = 0;
 
   void *ptr(int i) const { return params[(size_t)i].bound->ptr; }
+  // element `e` of an activation buffer of element size esz
+  void *at(void *p, int64_t e) const { return (char *)p + e * esz; }
   const float *f32(int i) const { return (const float *)ptr(i); }
 };
 
@@ -304,6 +315,7 @@ struct Carver {
   void add(T **p, int64_t count) {
     items.push_back({(void **)p, (size_t)count * sizeof(T)});
   }
+  void add_bytes(void **p, int64_t bytes) { items.push_back({p, (size_t)bytes}); }
   size_t total() const {
     size_t o = 0;
     for (auto &it : items) o += (it.second + 255) & ~(size_t)255;
@@ -328,15 +340,15 @@ int allocate(Qwen35 *m) {
   c.add(&m->row_len, T);
   c.add(&m->h, T * m->H);
   c.add(&m->fin, T * m->H);
-  c.add(&m->xn, T * m->H);
+  c.add_bytes(&m->xn, T * std::max(m->H, m->I) * m->esz);
   if (m->cfg.lora_rank > 0) c.add(&m->lora_mid, T * m->cfg.lora_rank);
-  c.add(&m->raw, T * m->n_in_max);
+  c.add_bytes(&m->raw, T * m->n_in_max * m->esz);
   if (m->any_linear) {
     c.add(&m->mixed, T * 3 * m->W);
     c.add(&m->beta, T * m->Hl);
     c.add(&m->g, T * m->Hl);
     c.add(&m->dout, T * m->W);
-    c.add(&m->gated, T * m->W);
+    c.add_bytes(&m->gated, T * m->W * m->esz);
   }
   if (m->any_full) {
     c.add(&m->q, T * m->Hq * m->D);
@@ -346,11 +358,11 @@ int allocate(Qwen35 *m) {
     c.add(&m->kc, m->Bmax * m->Hkv * m->Smax * m->D);
     c.add(&m->vc, m->Bmax * m->Hkv * m->Smax * m->D);
   }
-  c.add(&m->gu, T * 2 * m->I);
+  c.add_bytes(&m->gu, T * 2 * m->I * m->esz);
   c.add(&m->ss_embed, 32);
   c.add(&m->ss_o, 32 * ((m->H + 15) / 16));
   c.add(&m->ss_down, 32 * ((m->H + 15) / 16));
-  c.add(&m->act, T * m->I);
+  c.add_bytes(&m->act, T * m->I * m->esz);
   const size_t bytes = c.total();
   hipError_t e = hipMalloc(&m->block, bytes);
   if (e != hipSuccess) {
@@ -369,25 +381,30 @@ int allocate(Qwen35 *m) {
   return RXW8_OK;
 }
 
-// QuantizedLinear with compute dtype BF16 on projection `p` (weight p, scale p + 1):
-// y bf16 [T, N], or (y_mode 1) the f32 residual [T, N] that receives y += result.
+// QuantizedLinear at the model's compute dtype on projection `p` (weight p,
+// scale p + 1): y [T, N] an activation (f32 under F32 compute, else bf16), or
+// (y_mode 1) the f32 residual [T, N] that receives y += result.
 int proj(Qwen35 *m, int p, const void *x, int x_f32, void *y, int y_mode, int64_t T) {
   const Param &w = m->params[(size_t)p];
   return qlinear_launch(m->rt, x, x_f32, (const uint8_t *)m->ptr(p), false, m->f32(p + 1), y,
-                        y_mode == 1 ? 1 : 0, T, w.dims[0], w.dims[1], m->G, 1, y_mode);
+                        y_mode == 1 || m->f32c ? 1 : 0, T, w.dims[0], w.dims[1], m->G,
+                        m->f32c ? 0 : 1, y_mode);
 }
 
-// The same on a fused weight of n rows.
+// The same on a fused (row-major) weight of n rows; x and y are activations.
 int proj_fused(Qwen35 *m, const uint8_t *w, const float *sc, int64_t n, const void *x, void *y,
                int64_t T) {
-  return qlinear_launch(m->rt, x, 0, w, false, sc, y, 0, T, n, m->H, m->G, 1, 0);
+  return qlinear_launch(m->rt, x, m->f32c, w, false, sc, y, m->f32c, T, n, m->H, m->G,
+                        m->f32c ? 0 : 1, 0);
 }
 
 int norm(Qwen35 *m, const float *x, const float *w, void *out, int64_t rows, int64_t L,
          bool zero_centered, bool out_f32, const void *z = nullptr, int64_t z_stride = 0,
          int64_t z_group = 1) {
+  // z (the output gate of the linear layers) is a projection output: f32
+  // under F32 compute, else bf16
   Q35NormArgs a{x, w, z, out, rows, L, L, L, z_stride, z_group, m->cfg.eps, zero_centered ? 1 : 0,
-                out_f32 ? 1 : 0, 0};
+                out_f32 ? 1 : 0, m->f32c ? 1 : 0};
   return launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)rows), dim3(256), a);
 }
 
@@ -403,9 +420,9 @@ int in_proj(Qwen35 *m, const Layer &L, int64_t T) {
                      0, o);
     if (rc != RXW8_UNIMPLEMENTED) return rc;
   }
-  if ((rc = norm(m, m->h, m->f32(L.in_norm), m->xn, T, m->H, true, false))) return rc;
-  return qlinear_launch(m->rt, m->xn, 0, L.in_w, m->packed, L.in_s, m->raw, 0, T, L.n_in, m->H,
-                        m->G, 1, 0);
+  if ((rc = norm(m, m->h, m->f32(L.in_norm), m->xn, T, m->H, true, m->f32c))) return rc;
+  return qlinear_launch(m->rt, m->xn, m->f32c, L.in_w, m->packed, L.in_s, m->raw, m->f32c, T,
+                        L.n_in, m->H, m->G, m->f32c ? 0 : 1, 0);
 }
 
 // h += x w^T for a residual projection (packed copy w_pk in packed mode). In
@@ -437,11 +454,11 @@ int mlp(Qwen35 *m, const Layer &L, int64_t T) {
   Runtime *rt = m->rt;
   int rc;
   if (!m->packed) {
-    if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, false))) return rc;
+    if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, m->f32c))) return rc;
     if ((rc = proj_fused(m, L.gu_w, L.gu_s, L.n_gu, m->xn, m->gu, T))) return rc;
-    Q35SiluArgs sa{m->gu, m->gu + m->I, m->act, T * m->I, m->I, L.n_gu};
+    Q35SiluArgs sa{m->gu, m->at(m->gu, m->I), m->act, T * m->I, m->I, L.n_gu, m->f32c ? 1 : 0};
     if ((rc = launch(rt, "rxw8_q35_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
-    return proj(m, L.down, m->act, 0, m->h, 1, T);
+    return proj(m, L.down, m->act, m->f32c, m->h, 1, T);
   }
   // gate|up rows in SwiGLU order: the GEMV (norm prologue) or GEMM epilogue
   // writes act = bf16(silu(gate) * up) directly
@@ -464,7 +481,7 @@ int mlp(Qwen35 *m, const Layer &L, int64_t T) {
       if ((rc = qlinear_launch(rt, m->xn, 0, L.gu_w, true, L.gu_s, m->gu, 0, T, 2 * m->I, m->H,
                                m->G, 1, 0)))
         return rc;
-      SiluMulArgs sa{m->gu, m->act, T, m->I, 1};
+      SiluMulArgs sa{(const uint16_t *)m->gu, (uint16_t *)m->act, T, m->I, 1};
       if ((rc = launch(rt, "rxw8_dec_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
     }
   }
@@ -473,12 +490,12 @@ int mlp(Qwen35 *m, const Layer &L, int64_t T) {
 
 // gated RMSNorm over each (token, head) row of Dl (plain weight, times
 // silu(z); row r = (t, head) takes z at raw + t * n_in + head * Dl), then out_proj.
-int finish_linear(Qwen35 *m, const Layer &L, int64_t T, const uint16_t *zp) {
+int finish_linear(Qwen35 *m, const Layer &L, int64_t T, const void *zp) {
   int rc;
-  if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, false, zp, L.n_in,
-                 m->Hl)))
+  if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, m->f32c, zp,
+                 L.n_in, m->Hl)))
     return rc;
-  return out_proj(m, L, L.out, m->gated, 0, T);
+  return out_proj(m, L, L.out, m->gated, m->f32c, T);
 }
 
 int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
@@ -487,11 +504,11 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   int rc;
   // raw = xn [qkv; z; b; a]^T: columns [0, 3W) mixed, [3W, 4W) z, then b, a
   if ((rc = in_proj(m, L, T))) return rc;
-  const uint16_t *zp = m->raw + 3 * m->W;
+  const void *zp = m->at(m->raw, 3 * m->W);
   // conv + SiLU, q / k L2 norms, beta and decay: one workgroup per (token, head)
   Q35MixPrepArgs mp{m->raw, m->f32(L.conv), m->f32(L.a_log), m->f32(L.dt_bias), m->mixed, m->beta,
                     m->g, L.n_in, (int)S, (int)m->Hl, (int)m->Dl, (int)m->cfg.conv_kernel,
-                    1.0f / sqrtf((float)m->Dl)};
+                    1.0f / sqrtf((float)m->Dl), m->f32c ? 1 : 0};
   if ((rc = launch(rt, "rxw8_q35_mix_prep", dim3((unsigned)(T * m->Hl)), dim3(128), mp))) return rc;
   Q35DeltaArgs da{m->mixed, m->beta, m->g, m->dout, (int)B, (int)S, (int)m->Hl};
   char kname[40];
@@ -510,10 +527,10 @@ int full_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   int rc;
   // raw = xn [q; k; v]^T
   if ((rc = in_proj(m, L, T))) return rc;
-  const uint16_t *kp = m->raw + 2 * m->Hq * m->D, *vp = kp + m->Hkv * m->D;
+  const void *kp = m->at(m->raw, 2 * m->Hq * m->D), *vp = m->at(m->raw, (2 * m->Hq + m->Hkv) * m->D);
   Q35FaPrepArgs fa{m->raw, kp, vp, m->f32(L.qn), m->f32(L.kn), m->freqs, m->q, m->gate,
                    m->kc, m->vc, (int)T, (int)S, (int)m->Hq, (int)m->Hkv, (int)m->D,
-                   (int)m->cfg.rotary_dim, (int)m->Smax, (int)L.n_in, m->cfg.eps};
+                   (int)m->cfg.rotary_dim, (int)m->Smax, (int)L.n_in, m->cfg.eps, m->f32c ? 1 : 0};
   const int64_t units = T * (m->Hq + m->Hkv);
   if ((rc = launch(rt, "rxw8_q35_fa_prep", dim3((unsigned)((units + 3) / 4)), dim3(256), fa))) return rc;
   const float scale = 1.0f / sqrtf((float)m->D);
@@ -801,8 +818,12 @@ int rxw8_qwen35_create(rxw8_runtime *rt, const rxw8_qwen35_config *cfg, rxw8_qwe
     return fail(RXW8_UNIMPLEMENTED, "qwen35: head_dim %lld (supported: even, <= 256)", (long long)q->D);
   if (q->any_full && q->Smax > 8192)
     return fail(RXW8_UNIMPLEMENTED, "qwen35: full-attention sequences of at most 8192 positions");
-  // tile layout: 16-row tiles, 64-byte k blocks, gate|up pairs of 8 rows
-  q->packed = c.hidden % 64 == 0 && c.intermediate % 64 == 0 &&
+  if (c.compute_dtype != 0 && c.compute_dtype != RXW8_F32 && c.compute_dtype != RXW8_BF16)
+    return fail(RXW8_INVALID_ARGUMENT, "qwen35: compute_dtype %d (F32 or BF16)", (int)c.compute_dtype);
+  q->f32c = c.compute_dtype != RXW8_BF16;
+  q->esz = q->f32c ? 4 : 2;
+  // tile layout (BF16 compute): 16-row tiles, 64-byte k blocks, gate|up pairs of 8 rows
+  q->packed = !q->f32c && c.hidden % 64 == 0 && c.intermediate % 64 == 0 &&
               (!q->any_linear || q->W % 64 == 0) && (!q->any_full || (c.heads * c.head_dim) % 64 == 0) &&
               !(std::getenv("RXW8_Q35_UNPACKED") && std::getenv("RXW8_Q35_UNPACKED")[0] == '1');
   const int64_t T = q->Bmax * q->Smax;

@@ -89,6 +89,7 @@ static int module_of(const char *kname) {
     int module;
   } routes[] = {{"rxw8_gemv_", 0},      {"rxw8_pack_tiles", 0},     {"rxw8_dequant", 1},
                 {"rxw8_linear_generic", 1}, {"rxw8_linear_f32_", 1}, {"rxw8_kv_update", 1},
+                {"rxw8_quantize_w8", 1},
                 {"rxw8_gqa_", 2},
                 {"rxw8_w8a16_gemm", 3}, {"rxw8_gemm_", 3},   {"rxw8_dec_", 4},
                 {"rxw8_q35_", 5}};

@@ -250,6 +250,14 @@ class DecoderModel(_CompiledPlan):
 LINEAR, FULL = 0, 1
 
 
+def _compute_dtype(name):
+    if name in ("f32", DType.F32):
+        return int(DType.F32)
+    if name in ("bf16", DType.BF16):
+        return int(DType.BF16)
+    raise ValueError(f"compute dtype must be 'f32' or 'bf16', not {name!r}")
+
+
 @dataclass
 class Qwen35Config:
     """Qwen3_5Config (crates/rxla-models/src/qwen3_5/mod.rs:16-33); defaults
@@ -276,6 +284,9 @@ class Qwen35Config:
     lora_alpha: float = 0.0
     max_batch: int = 1
     max_seq: int = 4096
+    # projection compute dtype: "f32", the reference's default (rxla-nn
+    # lib.rs:432), or the "bf16" opt-in (Cx::with_layer_compute_dtype)
+    compute: str = "f32"
 
     @classmethod
     def tiny(cls, **kw):
@@ -300,7 +311,8 @@ class Qwen35Config:
                               self.linear_head_dim, self.conv_kernel, self.max_positions,
                               self.rotary_dim, self.group, self.full_attention_interval,
                               ctypes.cast(arr, ctypes.POINTER(c_int32)), self.theta, self.eps,
-                              self.lora_rank, self.lora_alpha, self.max_batch, self.max_seq)
+                              self.lora_rank, self.lora_alpha, self.max_batch, self.max_seq,
+                              _compute_dtype(self.compute))
         c._kinds = arr  # the array must outlive the create call
         return c
 

@@ -32,6 +32,17 @@ def rel_err(actual, expected):
     return float(np.max(np.abs(a - e)) / (den if den > 0 else 1.0))
 
 
+def elem_rel_err(actual, expected, floor=1e-2):
+    """Per-element relative error: max_i |a_i - e_i| / max(|e_i|, floor * rms(e)).
+    Unlike the normwise metric it sees a corrupted small output; the floor
+    keeps outputs that cancel to ~0 from dividing by ~0."""
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    rms = float(np.sqrt(np.mean(e * e))) if e.size else 0.0
+    den = np.maximum(np.abs(e), floor * rms if rms > 0 else 1.0)
+    return float(np.max(np.abs(a - e) / den)) if e.size else 0.0
+
+
 @pytest.fixture(scope="session")
 def rt():
     """GPU runtime (only for tests marked gpu)."""

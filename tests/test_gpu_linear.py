@@ -8,11 +8,21 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import rel_err
+from conftest import elem_rel_err, rel_err
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
+# Per element (floor at 1% of the rms): within one bf16 ulp, whose relative
+# spacing is at most 2^-7. Against the exact product of the bf16 activations
+# and the integer weights (f64) the GEMV's single rounding of its f32 sum
+# stays within half of that; two independently rounded bf16 results (GPU and
+# the reference-order oracle) can be one ulp apart.
+ELEM_TOL = 2.0 ** -7
+
+
+def exact(x, u8, s):
+    return oracle.quantized_linear(x, u8, s, oracle.COMPUTE_F32, oracle.ACCUM_F64, threads=16)
 
 
 def rx():
@@ -43,8 +53,10 @@ def test_c1_single_linear_f32_boundary(rt):
     u8, s = quantized(rng, 1024, 1024, 1024)
     ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16)
     y = run_linear(rt, x, u8, s)
-    print(f"C1 rel_err={rel_err(y, ref):.3e}")
+    e_elem = elem_rel_err(y, exact(oracle.round_bf16(x), u8, s))
+    print(f"C1 rel_err={rel_err(y, ref):.3e} elem_rel_err(vs exact)={e_elem:.3e}")
     assert rel_err(y, ref) <= TOL
+    assert e_elem <= ELEM_TOL
     np.testing.assert_array_equal(oracle.round_bf16(y), y)  # bf16-valued, like the reference
 
 
@@ -57,8 +69,10 @@ def test_c2_decode_gemv_sweep(rt, b, n):
     ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16, threads=16)
     y = run_linear(rt, x, u8, s, x_dtype=rx().DType.BF16, out_dtype=rx().DType.BF16)
     err = rel_err(y, ref)
-    print(f"C2 B={b} N={n} rel_err={err:.3e}")
+    e_elem = elem_rel_err(y, exact(x, u8, s))
+    print(f"C2 B={b} N={n} rel_err={err:.3e} elem_rel_err(vs exact)={e_elem:.3e}")
     assert err <= TOL
+    assert e_elem <= ELEM_TOL
 
 
 @pytest.mark.parametrize("g", [64, 128, 512])
@@ -209,7 +223,11 @@ def test_bf16_weight_linear_lm_head(rt):
 
 @pytest.mark.parametrize("b,n,k,g", [(1, 4096, 4096, 4096), (16, 6144, 4096, 4096),
                                      (8, 2048, 2048, 128), (4, 1024, 6144, 6144),
-                                     (8, 2048, 6144, 2048)])  # 3-way k split
+                                     (8, 2048, 6144, 2048),  # 3-way k split
+                                     # the decoder's gate|up width and the bench's roofline
+                                     # kernel (rxw8_gemv_w8_pk_mb1_rw3_u4_w12 at B=1)
+                                     (1, 24576, 4096, 4096), (4, 24576, 4096, 4096),
+                                     (16, 24576, 4096, 4096)])
 def test_packed_weights_bit_identical(rt, b, n, k, g):
     """The tiled layout holds the same bytes: results equal the row-major path."""
     r = rx()
@@ -243,6 +261,27 @@ def test_packed_bf16_lm_head(rt):
     y_pk = r.linear_bf16(rt, rt.buffer(x), pk).to_numpy()
     np.testing.assert_array_equal(y_pk, y_row)
     assert rel_err(y_pk, oracle.linear_bf16w(x, e)) <= TOL
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_full_vocab_lm_head(rt, packed):
+    """The C5 head: bf16 embedding [151936, 2048] reused as lm_head at batch 8
+    (622 MB of weights; the decode step's largest GEMV), row-major and in the
+    decoder's packed layout."""
+    r = rx()
+    rng = np.random.default_rng(151936 + packed)
+    x = rng.standard_normal((8, 2048)).astype(np.float32)
+    e = oracle.bf16_bits((rng.standard_normal((151936, 2048)) * 0.02).astype(np.float32))
+    eb = rt.buffer(e, r.DType.BF16)
+    w = r.pack_weight(rt, eb) if packed else eb
+    y = r.linear_bf16(rt, rt.buffer(x), w).to_numpy()
+    ref = oracle.linear_bf16w(x, e, threads=16)
+    err = rel_err(y, ref)
+    e_elem = elem_rel_err(y, ref)
+    print(f"lm_head 8x2048x151936 packed={packed} rel_err={err:.3e} elem_rel_err={e_elem:.3e}")
+    assert err <= TOL
+    # both sides round the f32 sum of bf16(x) . W (exact products) to bf16
+    assert e_elem <= ELEM_TOL
 
 
 def test_pack_weight_validation(rt):

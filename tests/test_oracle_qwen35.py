@@ -94,7 +94,25 @@ def test_projection_and_dequant_against_the_c_oracle():
     u8, s = oracle.quantize_w8((rng.standard_normal((24, 64)) * 0.05).astype(np.float32), 16)
     np.testing.assert_array_equal(q35.dequant(u8, s), oracle.dequantize_w8(u8, s))
     want = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16, oracle.ACCUM_F64)
-    np.testing.assert_array_equal(q35.projection(x, u8, s), oracle.round_bf16(want))
+    np.testing.assert_array_equal(q35.projection(x, u8, s, "bf16"), oracle.round_bf16(want))
+    # the default compute dtype is F32 (rxla-nn lib.rs:432): f32 x against the
+    # f32 dequantised weights, accumulated in f64 on both sides
+    want = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_F32, oracle.ACCUM_F64)
+    np.testing.assert_array_equal(q35.projection(x, u8, s), want)
+    assert q35.config()["compute"] == "f32"
+
+
+def test_f32_projection_closed_form():
+    """Integer activations and codes with power-of-two scales: every product
+    and sum is exact, so the F32 projection equals the integer matrix product
+    (a dropped scale, a transposed operand or a bf16 cast of x fails this:
+    x holds 257, which bf16 cannot represent)."""
+    x = np.array([[257.0, -3.0, 1.0, 0.0], [2.0, 5.0, -7.0, 11.0]], np.float32)
+    codes = np.array([[1, 2, 3, 4], [-5, 6, -7, 8], [127, -127, 0, 1]])
+    s = np.array([[0.5], [0.25], [2.0]], np.float32)
+    y = q35.projection(x, (codes + 128).astype(np.uint8), s)
+    np.testing.assert_array_equal(y, (x.astype(np.float64) @ (codes * s).T).astype(np.float32))
+    assert y[0, 0] == np.float32((257 * 1 - 3 * 2 + 3) * 0.5)
 
 
 def test_forward_runs_and_the_first_row_ignores_the_future():
