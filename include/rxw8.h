@@ -191,6 +191,25 @@ int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q,
                          rxw8_buffer *lens, rxw8_buffer *mask, float scale,
                          rxw8_buffer *out);
 
+/* rxw8_gqa_decode_into that allocates nothing. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc).
+ * Same arguments, validation and results (bit for bit) as
+ * rxw8_gqa_decode_into. The split partials and arrival counters live in a
+ * fixed device array that each GPU holds for the life of the process
+ * (RXW8_NOALLOC_PARTIAL_BYTES + RXW8_NOALLOC_COUNTER_BYTES); a call whose plan
+ * needs more fails with RXW8_RESOURCE_EXHAUSTED before any launch (the split
+ * plans of the D = 128 kernel need at most about 9 MiB for Hq/Hkv <= 8).
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other streams, runtimes or threads) race and must be serialised by the
+ * caller. The device must have had a runtime created on it (set-up). */
+#define RXW8_NOALLOC_PARTIAL_BYTES ((size_t)16 << 20)
+#define RXW8_NOALLOC_COUNTER_BYTES ((size_t)64 << 10)
+int rxw8_gqa_decode_noalloc(rxw8_runtime *rt, rxw8_buffer *q,
+                            rxw8_buffer *k_cache, rxw8_buffer *v_cache,
+                            rxw8_buffer *lens, rxw8_buffer *mask, float scale,
+                            rxw8_buffer *out);
+
 /* Causal grouped-query prefill attention (attention.rs:83-135 + SDPA
  * :150-252 with the causal mask key_pos <= q_pos of attention.rs:14-32;
  * F32 softmax) for S new query rows per sequence whose keys and values are

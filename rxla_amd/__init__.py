@@ -316,6 +316,19 @@ def argmax(rt: Runtime, x: Buffer, axis: int, keep_dims: bool = False) -> Buffer
     return Buffer(h)
 
 
+def grouped_query_attention_noalloc(rt: Runtime, q: Buffer, k_cache: Buffer, v_cache: Buffer,
+                                    lens: Buffer, out: Buffer, mask: Buffer | None = None,
+                                    scale: float | None = None) -> Buffer:
+    """``grouped_query_attention`` into ``out`` without any device allocation:
+    the split workspace is the library's fixed per-GPU scratch array
+    (``rxw8_gqa_decode_noalloc``). Calls that overlap on one GPU race."""
+    s = 0.0 if scale is None else float(scale)
+    m = mask.handle if mask is not None else None
+    _check(_lib.rxw8_gqa_decode_noalloc(rt.handle, q.handle, k_cache.handle, v_cache.handle,
+                                        lens.handle, m, ctypes.c_float(s), out.handle))
+    return out
+
+
 def grouped_query_attention_prefill(rt: Runtime, q: Buffer, k_cache: Buffer, v_cache: Buffer,
                                     starts: Buffer, scale: float | None = None,
                                     out_dtype=DType.F32, out: Buffer | None = None) -> Buffer:
@@ -439,6 +452,6 @@ __all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "quantize_w8", "dequ
            "pack_weight",
            "quantized_linear",
            "linear_bf16", "QuantizedLinear", "grouped_query_attention",
-           "grouped_query_attention_prefill", "argmax", "KvCache",
+           "grouped_query_attention_prefill", "grouped_query_attention_noalloc", "argmax", "KvCache",
            "SafeTensors",
            "DecoderConfig", "DecoderModel", "Qwen35Config", "Qwen35Model", "bf16_to_f32"]

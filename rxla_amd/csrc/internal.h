@@ -141,6 +141,10 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
 int gqa_decode_into(Runtime *rt, Buffer *q, Buffer *k_cache, Buffer *v_cache, Buffer *lens,
                     Buffer *mask, float scale, Buffer *out, const AttnWorkspace *ws);
 
+// Takes the device address of the no-allocation scratch array on `device`
+// (current) and clears its counters; once per device (noalloc.hip).
+int noalloc_device_setup(int device);
+
 // Device-side allocation through the runtime's cache.
 int rt_alloc(Runtime *rt, size_t bytes, void **out);
 void rt_free(Runtime *rt, void *ptr, size_t bytes);

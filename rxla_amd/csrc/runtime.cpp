@@ -299,6 +299,12 @@ int rxw8_runtime_create(int device, rxw8_runtime **out) {
     return rc;
   }
   rt->stream = rt->own_stream;
+  if (int rc = noalloc_device_setup(device)) {
+    (void)hipStreamDestroy(rt->own_stream);
+    for (hipModule_t mm : rt->modules) (void)hipModuleUnload(mm);
+    delete rt;
+    return rc;
+  }
   *out = rt;
   return RXW8_OK;
 }
