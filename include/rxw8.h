@@ -191,6 +191,31 @@ int rxw8_gqa_decode_into(rxw8_runtime *rt, rxw8_buffer *q,
                          rxw8_buffer *lens, rxw8_buffer *mask, float scale,
                          rxw8_buffer *out);
 
+/* Tensor::grouped_query_attention(k, v, mask, scale) (attention.rs:83-135)
+ * with SDPA semantics (:150-252) for any query count:
+ *   q [..., Hq, Sq, D], k [..., Hkv, Sk, D], v [..., Hkv, Sk, Dv], all F32,
+ *   equal batch prefixes (up to 4 dims), Hq % Hkv == 0, Sk > 0;
+ *   mask: optional additive F32, broadcastable (right-aligned, size-1 dims)
+ *   to the scores [..., Hq, Sq, Sk] before grouping; NULL = none;
+ *   scale: NULL selects 1/sqrt(D), else it must be finite.
+ * Query head h reads kv head h / (Hq/Hkv); softmax over the keys in f32;
+ * out F32 [..., Hq, Sq, Dv]. A row whose keys are all masked is NaN, as in
+ * the reference. INVALID_ARGUMENT mirrors the reference's shape, dtype and
+ * scale errors; UNIMPLEMENTED beyond D 1024 / Dv 512. */
+int rxw8_gqa_attention(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k,
+                       rxw8_buffer *v, rxw8_buffer *mask, const float *scale,
+                       rxw8_buffer **out);
+int rxw8_gqa_attention_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k,
+                            rxw8_buffer *v, rxw8_buffer *mask,
+                            const float *scale, rxw8_buffer *out);
+
+/* Tensor::causal_attention_mask (attention.rs:14-32): from runtime query
+ * positions I32 [Q] and key positions I32 [K], the additive F32 mask [Q, K]
+ * whose (i, j) entry is 0 iff key_positions[j] <= query_positions[i] (signed
+ * I32 compare, exact at any I32 value), else -inf. */
+int rxw8_causal_attention_mask(rxw8_runtime *rt, rxw8_buffer *query_positions,
+                               rxw8_buffer *key_positions, rxw8_buffer **out);
+
 /* rxw8_gqa_decode_into that allocates nothing. It has no counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops and harnesses that forbid hipMalloc).

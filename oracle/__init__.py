@@ -194,6 +194,15 @@ def gqa_attention(q, k, v, mask=None, scale=None, precision=0, threads=0):
     return out
 
 
+def causal_attention_mask(query_positions, key_positions):
+    """Tensor::causal_attention_mask (crates/rxla-core/src/attention.rs:14-32):
+    [Q, K] f32, 0 where key_positions[j] <= query_positions[i] (signed I32
+    compare), else -inf."""
+    qp = np.asarray(query_positions, np.int32)
+    kp = np.asarray(key_positions, np.int32)
+    return np.where(kp[None, :] <= qp[:, None], np.float32(0.0), np.float32(-np.inf)).astype(np.float32)
+
+
 def gqa_decode_bf16cache(q, kc_bits, vc_bits, lens, scale=None, precision=0, threads=0):
     """q [B,Hq,D] f32; caches [B,Hkv,Lmax,D] bf16 bits; lens [B] int32."""
     q = _c(q, np.float32)

@@ -22,7 +22,7 @@ from __future__ import annotations
 import ctypes
 import enum
 import os
-from ctypes import POINTER, byref, c_int, c_int32, c_int64, c_void_p
+from ctypes import POINTER, byref, c_float, c_int, c_int32, c_int64, c_void_p
 
 import numpy as np
 
@@ -207,6 +207,11 @@ class Buffer:
         _check(_lib.rxw8_buffer_device_ptr(self._h, byref(p)))
         return p.value or 0
 
+    def _keep(self, *owners):
+        """Keep `owners` (the buffers a view's memory belongs to) alive with it."""
+        self._owners = owners
+        return self
+
     def to_numpy(self) -> np.ndarray:
         """Blocking download (Buffer::to_vec). BF16 comes back as uint16 bits."""
         out = np.empty(self.shape, _NP[self.dtype])
@@ -306,6 +311,60 @@ def grouped_query_attention(rt: Runtime, q: Buffer, k_cache: Buffer, v_cache: Bu
     _check(_lib.rxw8_gqa_decode(rt.handle, q.handle, k_cache.handle, v_cache.handle,
                                 lens.handle, m, ctypes.c_float(s), int(out_dtype), byref(h)))
     return Buffer(h)
+
+
+def gqa_attention(rt: Runtime, q: Buffer, k: Buffer, v: Buffer, mask: Buffer | None = None,
+                  scale: float | None = None, out: Buffer | None = None) -> Buffer:
+    """``Tensor::grouped_query_attention(k, v, mask, scale)`` (attention.rs:83-135)
+    for any query count: q [..., Hq, Sq, D], k/v [..., Hkv, Sk, D|Dv] F32, an
+    additive F32 mask broadcastable to [..., Hq, Sq, Sk]; F32 [..., Hq, Sq, Dv]."""
+    sp = byref(c_float(scale)) if scale is not None else None
+    m = mask.handle if mask is not None else None
+    if out is not None:
+        _check(_lib.rxw8_gqa_attention_into(rt.handle, q.handle, k.handle, v.handle, m, sp,
+                                            out.handle))
+        return out
+    h = c_void_p()
+    _check(_lib.rxw8_gqa_attention(rt.handle, q.handle, k.handle, v.handle, m, sp, byref(h)))
+    return Buffer(h)
+
+
+def scaled_dot_product_attention(rt: Runtime, q: Buffer, k: Buffer, v: Buffer,
+                                 mask: Buffer | None = None, scale: float | None = None) -> Buffer:
+    """``Tensor::scaled_dot_product_attention`` (attention.rs:150-252) on equal
+    batch prefixes: softmax(q k^T * scale + mask) v, as one-head GQA (q
+    [..., Sq, D], k [..., Sk, D], v [..., Sk, Dv], rank >= 2)."""
+    def with_head(b):
+        s = b.shape
+        return rt.wrap(b.ptr, s[:-2] + (1,) + s[-2:], b.dtype)
+    qh, kh, vh = with_head(q), with_head(k), with_head(v)
+    # a mask with batch dims gains the same head axis, so its batch dims stay aligned
+    mh = with_head(mask) if mask is not None and len(mask.shape) >= 3 else mask
+    o = gqa_attention(rt, qh, kh, vh, mh, scale)
+    return rt.wrap(o.ptr, q.shape[:-1] + (v.shape[-1],), o.dtype)._keep(o)
+
+
+def causal_attention_mask(rt: Runtime, query_positions: Buffer, key_positions: Buffer) -> Buffer:
+    """``Tensor::causal_attention_mask`` (attention.rs:14-32): F32 [Q, K], 0 iff
+    key_positions[j] <= query_positions[i] (signed I32), else -inf."""
+    h = c_void_p()
+    _check(_lib.rxw8_causal_attention_mask(rt.handle, query_positions.handle,
+                                           key_positions.handle, byref(h)))
+    return Buffer(h)
+
+
+def causal_attention_mask_static(rt: Runtime, queries: int, keys: int, query_offset: int) -> Buffer:
+    """``Graph::causal_attention_mask(queries, keys, query_offset)``
+    (attention.rs:45-67): key j visible to row i iff j <= query_offset + i;
+    counts and offset nonnegative and I32-representable, as the reference checks."""
+    imax = 2 ** 31 - 1
+    if (queries < 0 or keys < 0 or keys > imax + 1 or query_offset < 0 or query_offset > imax
+            or queries > imax + 1 - query_offset):
+        raise Error(Status.INVALID_ARGUMENT,
+                    "causal mask requires nonnegative I32-representable positions")
+    qpos = (np.arange(queries, dtype=np.int64) + query_offset).astype(np.int32)  # wraps like iota + offset
+    kpos = np.arange(keys, dtype=np.int64).astype(np.int32)
+    return causal_attention_mask(rt, rt.buffer(qpos), rt.buffer(kpos))
 
 
 def argmax(rt: Runtime, x: Buffer, axis: int, keep_dims: bool = False) -> Buffer:
@@ -452,6 +511,8 @@ __all__ = ["Runtime", "Buffer", "DType", "Status", "Error", "quantize_w8", "dequ
            "pack_weight",
            "quantized_linear",
            "linear_bf16", "QuantizedLinear", "grouped_query_attention",
-           "grouped_query_attention_prefill", "grouped_query_attention_noalloc", "argmax", "KvCache",
+           "grouped_query_attention_prefill", "grouped_query_attention_noalloc", "gqa_attention",
+           "scaled_dot_product_attention", "causal_attention_mask", "causal_attention_mask_static",
+           "argmax", "KvCache",
            "SafeTensors",
            "DecoderConfig", "DecoderModel", "Qwen35Config", "Qwen35Model", "bf16_to_f32"]

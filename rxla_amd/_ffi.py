@@ -23,7 +23,8 @@ EXPORTS = [
     "rxw8_buffer_dtype", "rxw8_buffer_dims", "rxw8_buffer_device_ptr",
     "rxw8_quantize_w8", "rxw8_dequantize", "rxw8_pack_weight", "rxw8_quantized_linear", "rxw8_quantized_linear_into",
     "rxw8_linear_bf16", "rxw8_linear_bf16_into", "rxw8_gqa_decode", "rxw8_gqa_decode_into",
-    "rxw8_gqa_decode_noalloc",
+    "rxw8_gqa_decode_noalloc", "rxw8_gqa_attention", "rxw8_gqa_attention_into",
+    "rxw8_causal_attention_mask",
     "rxw8_gqa_prefill", "rxw8_gqa_prefill_into", "rxw8_kv_update_at", "rxw8_argmax",
     "rxw8_safetensors_open", "rxw8_safetensors_close", "rxw8_safetensors_num_tensors",
     "rxw8_safetensors_tensor_info", "rxw8_safetensors_find", "rxw8_safetensors_metadata",
@@ -88,6 +89,9 @@ def _declare(L):
         "rxw8_gqa_decode": (c_int, [vp, vp, vp, vp, vp, vp, c_float, c_int, POINTER(vp)]),
         "rxw8_gqa_decode_into": (c_int, [vp, vp, vp, vp, vp, vp, c_float, vp]),
         "rxw8_gqa_decode_noalloc": (c_int, [vp, vp, vp, vp, vp, vp, c_float, vp]),
+        "rxw8_gqa_attention": (c_int, [vp, vp, vp, vp, vp, POINTER(c_float), POINTER(vp)]),
+        "rxw8_gqa_attention_into": (c_int, [vp, vp, vp, vp, vp, POINTER(c_float), vp]),
+        "rxw8_causal_attention_mask": (c_int, [vp, vp, vp, POINTER(vp)]),
         "rxw8_gqa_prefill": (c_int, [vp, vp, vp, vp, vp, c_float, c_int, POINTER(vp)]),
         "rxw8_gqa_prefill_into": (c_int, [vp, vp, vp, vp, vp, c_float, vp]),
         "rxw8_kv_update_at": (c_int, [vp, vp, vp, vp, vp, vp, c_int, vp]),

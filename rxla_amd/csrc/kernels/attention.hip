@@ -945,3 +945,130 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_decode_generic(AttnGe
       ((uint16_t *)a.out)[oi] = f32_to_bf16_bits(acc);
   }
 }
+
+// ---- general grouped-query attention (attention.rs:83-135 with SDPA
+// :150-252): q [NB, Hq, Sq, D], k [NB, Hkv, Sk, D], v [NB, Hkv, Sk, Dv], all
+// f32; query head h reads kv head h / (Hq / Hkv); scores q.k * scale + mask,
+// softmax over the Sk keys in f32, out [NB, Hq, Sq, Dv] f32. The additive
+// mask broadcasts to [..., Hq, Sq, Sk]: element (b, h, i, j) sits at
+// moff(b) + h * msh + i * msi + j * msj, where moff sums the batch index's
+// digits (bdim) times their mask strides (0 where the mask broadcasts).
+//
+// One wave per output row (b, h, i). The row's q sits in the wave's LDS
+// slice; keys go in chunks of 64 (lane = key: a sequential f32 dot product
+// over D), with an online softmax (running max m, sum l, accumulators rescaled
+// by exp(m_old - m_new)); P.V accumulates with lanes over the Dv outputs and
+// each chunk probability broadcast by a lane shuffle. A row whose keys are all
+// masked (-inf) ends as 0 / 0 = NaN, the reference's max-subtract softmax of
+// such a row. The reference orders the softmax as max, exp, sum, divide over
+// the whole row; the online form reassociates those sums (f32 rounding
+// differences only).
+struct GqaGeneralArgs {
+  const float *q, *k, *v;
+  const float *mask;        // or null
+  float *out;
+  int64_t bdim[4];          // batch prefix dims (innermost last), 1 where absent
+  int64_t mb[4];            // mask stride of each batch dim (0: broadcast)
+  int64_t msh, msi, msj;    // mask strides of head, query, key (0: broadcast)
+  int64_t rows;             // NB * Hq * Sq
+  int Hq, Hkv, Sq, Sk, D, Dv;
+  float scale;
+};
+
+constexpr int kGqaMaxD = 1024;   // q row staged in LDS
+constexpr int kGqaMaxDv = 512;   // 8 accumulators per lane
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_general(GqaGeneralArgs a) {
+  __shared__ float qrow[4][kGqaMaxD];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wv;
+  if (row >= a.rows) return;  // whole waves; no workgroup barrier below
+  const int i = (int)(row % a.Sq);
+  const int64_t bh = row / a.Sq;
+  const int h = (int)(bh % a.Hq);
+  const int64_t b = bh / a.Hq;
+  const int kvh = h / (a.Hq / a.Hkv);
+  const float *qp = a.q + row * a.D;
+  const float *kp = a.k + (b * a.Hkv + kvh) * (int64_t)a.Sk * a.D;
+  const float *vp = a.v + (b * a.Hkv + kvh) * (int64_t)a.Sk * a.Dv;
+  const float *mp = nullptr;
+  if (a.mask) {
+    int64_t off = 0, rest = b;
+    for (int t = 3; t >= 0; --t) {
+      const int64_t digit = rest % a.bdim[t];
+      rest /= a.bdim[t];
+      off += digit * a.mb[t];
+    }
+    mp = a.mask + off + (int64_t)h * a.msh + (int64_t)i * a.msi;
+  }
+  float *ql = qrow[wv];
+  for (int d = lane; d < a.D; d += 64) ql[d] = qp[d];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float ninf = -__builtin_huge_valf();
+  float m = ninf, l = 0.f;
+  float acc[kGqaMaxDv / 64];
+#pragma unroll
+  for (int r = 0; r < kGqaMaxDv / 64; ++r) acc[r] = 0.f;
+  for (int c0 = 0; c0 < a.Sk; c0 += 64) {
+    const int j = c0 + lane;
+    const bool valid = j < a.Sk;
+    float s = ninf;
+    if (valid) {
+      const float *kr = kp + (int64_t)j * a.D;
+      float dot = 0.f;
+      for (int d = 0; d < a.D; ++d) dot += ql[d] * kr[d];
+      s = dot * a.scale;
+      if (mp) s += mp[(int64_t)j * a.msj];
+    }
+    float cmax = valid ? s : ninf;
+    for (int o = 32; o > 0; o >>= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, o));
+    const float m_new = fmaxf(m, cmax);
+    if (m_new == ninf) continue;  // nothing visible yet: keep m = -inf, l = 0
+    const float alpha = expf(m - m_new);
+    const float p = valid ? expf(s - m_new) : 0.f;
+    float ps = p;
+    for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
+    l = l * alpha + ps;
+    const int nk = min(64, a.Sk - c0);
+#pragma unroll
+    for (int r = 0; r < kGqaMaxDv / 64; ++r) acc[r] *= alpha;
+    for (int jj = 0; jj < nk; ++jj) {
+      const float pj = __shfl(p, jj);
+      const float *vr = vp + (int64_t)(c0 + jj) * a.Dv;
+#pragma unroll
+      for (int r = 0; r < kGqaMaxDv / 64; ++r) {
+        const int d = lane + 64 * r;
+        if (d < a.Dv) acc[r] += pj * vr[d];
+      }
+    }
+    m = m_new;
+  }
+  // all keys masked: the reference's softmax of an all -inf row is NaN
+  const float inv = m == ninf ? __builtin_nanf("") : 1.0f / l;
+  float *op = a.out + row * a.Dv;
+#pragma unroll
+  for (int r = 0; r < kGqaMaxDv / 64; ++r) {
+    const int d = lane + 64 * r;
+    if (d < a.Dv) op[d] = m == ninf ? inv : acc[r] * inv;
+  }
+}
+
+// Tensor::causal_attention_mask (attention.rs:14-32): out [Q, K] f32, entry
+// (i, j) = 0 iff key_pos[j] <= query_pos[i] (signed I32 compare, no
+// subtraction or float conversion), else -inf.
+struct CausalMaskArgs {
+  const int32_t *qpos, *kpos;
+  float *out;
+  int64_t Q, K;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_causal_mask(CausalMaskArgs a) {
+  const int64_t n = a.Q * a.K;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / a.K, j = e - i * a.K;
+    a.out[e] = a.kpos[j] <= a.qpos[i] ? 0.0f : -__builtin_huge_valf();
+  }
+}

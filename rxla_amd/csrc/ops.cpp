@@ -4,6 +4,7 @@
 // BufferDType checks (crates/rxla-nn/src/layers.rs:258-274,
 // crates/rxla-nn/src/applied.rs:1274-1297, attention.rs:83-252,
 // kv_cache.rs:53-111); a rejected call launches nothing and mutates nothing.
+#include <climits>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -89,6 +90,24 @@ struct QuantizeArgs {
   float *scale;
   int64_t n, k, g;
   int w_bf16;
+};
+
+struct GqaGeneralArgs {
+  const float *q, *k, *v;
+  const float *mask;
+  float *out;
+  int64_t bdim[4];
+  int64_t mb[4];
+  int64_t msh, msi, msj;
+  int64_t rows;
+  int Hq, Hkv, Sq, Sk, D, Dv;
+  float scale;
+};
+
+struct CausalMaskArgs {
+  const int32_t *qpos, *kpos;
+  float *out;
+  int64_t Q, K;
 };
 
 struct GenericLinearArgs {
@@ -1086,6 +1105,128 @@ static int check_gqa(const Buffer *q, const Buffer *k, const Buffer *v, const Bu
     *mask_sh = mask->dims[1] == 1 ? 0 : L;
     *mask_sb = mask->dims[0] == 1 ? 0 : mask->dims[1] * L;
   }
+  return RXW8_OK;
+}
+
+int rxw8_causal_attention_mask(rxw8_runtime *rt, rxw8_buffer *query_positions,
+                               rxw8_buffer *key_positions, rxw8_buffer **out) {
+  if (!rt || !query_positions || !key_positions || !out)
+    return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if (query_positions->dtype != RXW8_I32 || key_positions->dtype != RXW8_I32)
+    return fail(RXW8_INVALID_ARGUMENT, "causal positions must be I32 tensors");
+  if (query_positions->rank != 1 || key_positions->rank != 1)
+    return fail(RXW8_INVALID_ARGUMENT, "causal positions must be rank-one I32 tensors");
+  const int64_t Q = query_positions->dims[0], K = key_positions->dims[0];
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  const int64_t od[2] = {Q, K};
+  Buffer *o = nullptr;
+  int rc = new_buffer(rt, RXW8_F32, od, 2, false, &o);
+  if (rc) return rc;
+  if (Q * K > 0) {
+    CausalMaskArgs a{(const int32_t *)query_positions->ptr, (const int32_t *)key_positions->ptr,
+                     (float *)o->ptr, Q, K};
+    rc = launch(rt, "rxw8_gqa_causal_mask", dim3(grid_for(Q * K, 256, 1 << 14)), dim3(256), a);
+    if (rc) {
+      rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+      return rc;
+    }
+  }
+  *out = static_cast<rxw8_buffer *>(o);
+  return RXW8_OK;
+}
+
+int rxw8_gqa_attention_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k, rxw8_buffer *v,
+                            rxw8_buffer *mask, const float *scale, rxw8_buffer *out) {
+  if (!rt || !q || !k || !v || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  const int r = q->rank;
+  if (r < 3 || k->rank != r || v->rank != r)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA requires matching ranks >= 3");
+  if (q->dtype != RXW8_F32 || k->dtype != RXW8_F32 || v->dtype != RXW8_F32 ||
+      (mask && mask->dtype != RXW8_F32))
+    return fail(RXW8_INVALID_ARGUMENT, "attention requires F32 Q/K/V and mask tensors");
+  const int hd = r - 3;
+  bool ok = q->dims[hd] > 0 && k->dims[hd] > 0 && v->dims[hd] == k->dims[hd] &&
+            q->dims[hd] % k->dims[hd] == 0;
+  for (int i = 0; ok && i < hd; ++i) ok = q->dims[i] == k->dims[i] && q->dims[i] == v->dims[i];
+  if (!ok)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA requires equal batch prefixes and divisible positive head counts");
+  const int64_t Hq = q->dims[hd], Hkv = k->dims[hd], Sq = q->dims[hd + 1], D = q->dims[hd + 2];
+  const int64_t Sk = k->dims[hd + 1], Dv = v->dims[hd + 2];
+  if (D <= 0 || k->dims[hd + 2] != D || Sk == 0 || v->dims[hd + 1] != Sk)
+    return fail(RXW8_INVALID_ARGUMENT, "attention requires matching positive Q/K depth and K/V length");
+  const float sc = scale ? *scale : 1.0f / std::sqrt((float)D);
+  if (!std::isfinite(sc)) return fail(RXW8_INVALID_ARGUMENT, "attention scale must be finite");
+  bool out_ok = out->dtype == RXW8_F32 && out->rank == r && out->dims[hd + 2] == Dv;
+  for (int i = 0; out_ok && i < hd + 2; ++i) out_ok = out->dims[i] == q->dims[i];
+  if (!out_ok) return fail(RXW8_INVALID_ARGUMENT, "GQA output must be F32 [..., Hq, Sq, Dv]");
+  if (hd > 4 || D > 1024 || Dv > 512)
+    return fail(RXW8_UNIMPLEMENTED,
+                "GQA: supported up to 4 batch dimensions, depth 1024 and value depth 512");
+  GqaGeneralArgs a{};
+  a.q = (const float *)q->ptr;
+  a.k = (const float *)k->ptr;
+  a.v = (const float *)v->ptr;
+  a.out = (float *)out->ptr;
+  for (int t = 0; t < 4; ++t) a.bdim[t] = 1, a.mb[t] = 0;
+  int64_t NB = 1;
+  for (int i = 0; i < hd; ++i) {
+    a.bdim[4 - hd + i] = q->dims[i];
+    NB *= q->dims[i];
+  }
+  if (mask) {
+    // right-aligned broadcast against the scores [..., Hq, Sq, Sk]
+    int64_t sd[RXW8_MAX_RANK];
+    for (int i = 0; i < hd + 2; ++i) sd[i] = q->dims[i];
+    sd[hd + 2] = Sk;
+    if (mask->rank > r)
+      return fail(RXW8_INVALID_ARGUMENT, "GQA mask %s cannot broadcast to the scores", dims_str(mask).c_str());
+    int64_t stride[RXW8_MAX_RANK] = {0}, st = 1;
+    for (int i = mask->rank - 1; i >= 0; --i) {
+      stride[i] = mask->dims[i] == 1 ? 0 : st;
+      st *= mask->dims[i];
+    }
+    int64_t ms[RXW8_MAX_RANK] = {0};
+    for (int t = 0; t < r; ++t) {
+      const int mt = t - (r - mask->rank);
+      if (mt < 0) continue;
+      if (mask->dims[mt] != 1 && mask->dims[mt] != sd[t])
+        return fail(RXW8_INVALID_ARGUMENT, "GQA mask %s cannot broadcast to the scores", dims_str(mask).c_str());
+      ms[t] = stride[mt];
+    }
+    for (int i = 0; i < hd; ++i) a.mb[4 - hd + i] = ms[i];
+    a.mask = (const float *)mask->ptr;
+    a.msh = ms[hd];
+    a.msi = ms[hd + 1];
+    a.msj = ms[hd + 2];
+  }
+  a.rows = NB * Hq * Sq;
+  a.Hq = (int)Hq, a.Hkv = (int)Hkv, a.Sq = (int)Sq, a.Sk = (int)Sk, a.D = (int)D, a.Dv = (int)Dv;
+  a.scale = sc;
+  if (a.rows == 0) return RXW8_OK;
+  if ((a.rows + 3) / 4 >= ((int64_t)1 << 31) || Sq > INT32_MAX || Sk > INT32_MAX)
+    return fail(RXW8_UNIMPLEMENTED, "GQA: %lld rows exceed the kernel's grid", (long long)a.rows);
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  return launch(rt, "rxw8_gqa_general", dim3((unsigned)((a.rows + 3) / 4)), dim3(256), a);
+}
+
+int rxw8_gqa_attention(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k, rxw8_buffer *v,
+                       rxw8_buffer *mask, const float *scale, rxw8_buffer **out) {
+  if (!rt || !q || !k || !v || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if (q->rank < 3 || v->rank != q->rank)
+    return fail(RXW8_INVALID_ARGUMENT, "GQA requires matching ranks >= 3");
+  int64_t od[RXW8_MAX_RANK];
+  for (int i = 0; i < q->rank; ++i) od[i] = q->dims[i];
+  od[q->rank - 1] = v->dims[v->rank - 1];
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  Buffer *o = nullptr;
+  int rc = new_buffer(rt, RXW8_F32, od, q->rank, false, &o);
+  if (rc) return rc;
+  rc = rxw8_gqa_attention_into(rt, q, k, v, mask, scale, static_cast<rxw8_buffer *>(o));
+  if (rc) {
+    rxw8_buffer_release(static_cast<rxw8_buffer *>(o));
+    return rc;
+  }
+  *out = static_cast<rxw8_buffer *>(o);
   return RXW8_OK;
 }
 

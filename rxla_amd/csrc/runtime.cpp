@@ -152,6 +152,19 @@ void rt_free(Runtime *rt, void *ptr, size_t bytes) {
 
 int ensure_workspace(Runtime *rt, Workspace &ws, size_t bytes, bool zero) {
   if (ws.bytes >= bytes) return RXW8_OK;
+  // Growing synchronizes the stream and reallocates: not possible inside a
+  // stream capture (an XLA command buffer, a caller's graph). Such callers
+  // run the call once outside capture first, which sizes the workspace.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(rt->stream, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    cs = hipStreamCaptureStatusNone;
+  }
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(RXW8_FAILED_PRECONDITION,
+                "a workspace of %zu bytes (now %zu) must grow while the stream is being captured; "
+                "run the call once outside the capture first",
+                bytes, ws.bytes);
   if (ws.ptr) {
     RXW8_HIP(hipStreamSynchronize(rt->stream));
     RXW8_HIP(hipFree(ws.ptr));

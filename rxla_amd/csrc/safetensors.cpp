@@ -30,6 +30,7 @@ struct TensorEntry {
   std::string st_dtype;  // safetensors dtype string
   int dtype = 0;         // rxw8 dtype, 0 when not representable
   std::vector<int64_t> shape;
+  int64_t numel = 0;            // validated: numel * element size <= INT64_MAX
   uint64_t begin = 0, end = 0;  // relative to the data section
 };
 
@@ -396,19 +397,34 @@ static int parse_header(const char *path, SafeTensors *st) {
     if (shape->arr.size() > RXW8_MAX_RANK)
       return fail(RXW8_UNIMPLEMENTED, "\"%s\": tensor \"%s\" has rank %zu > %d", path, kv.first.c_str(),
                   shape->arr.size(), RXW8_MAX_RANK);
-    unsigned __int128 numel = 1;
+    // element count with checked multiplication: any count whose bytes
+    // exceed INT64_MAX is rejected (it cannot match a data section anyway),
+    // so the product never wraps and later int64 arithmetic on it is exact
+    uint64_t numel = 1;
+    bool zero = false;
     for (const Json &d : shape->arr) {
       if (d.kind != Json::Num || d.neg_or_frac || d.num > (uint64_t)INT64_MAX)
         return fail(RXW8_DATA_LOSS, "\"%s\": tensor \"%s\" has a bad dimension", path, kv.first.c_str());
       t.shape.push_back((int64_t)d.num);
-      numel *= d.num;
+      zero = zero || d.num == 0;
     }
+    for (int64_t d : t.shape) {
+      if (zero) {
+        numel = 0;
+        break;
+      }
+      if (elem == 0 || (uint64_t)d > (uint64_t)INT64_MAX / elem / numel)
+        return fail(RXW8_DATA_LOSS, "\"%s\": tensor \"%s\" has more than INT64_MAX bytes", path,
+                    kv.first.c_str());
+      numel *= (uint64_t)d;
+    }
+    t.numel = (int64_t)numel;
     for (const Json &o : offs->arr)
       if (o.kind != Json::Num || o.neg_or_frac)
         return fail(RXW8_DATA_LOSS, "\"%s\": tensor \"%s\" has bad data_offsets", path, kv.first.c_str());
     t.begin = offs->arr[0].num;
     t.end = offs->arr[1].num;
-    if (t.begin > t.end || t.end > st->data_bytes || numel * elem != (unsigned __int128)(t.end - t.begin))
+    if (t.begin > t.end || t.end > st->data_bytes || numel * elem != t.end - t.begin)
       return fail(RXW8_DATA_LOSS, "\"%s\": tensor \"%s\": data_offsets [%llu, %llu) do not hold %s %s elements inside %llu bytes",
                   path, kv.first.c_str(), (unsigned long long)t.begin, (unsigned long long)t.end,
                   "its", dt->str.c_str(), (unsigned long long)st->data_bytes);
@@ -531,8 +547,7 @@ int rxw8_safetensors_upload(rxw8_safetensors *st, int64_t index, rxw8_buffer *ds
   if (index < 0 || index >= (int64_t)st->tensors.size())
     return fail(RXW8_OUT_OF_RANGE, "tensor index %lld out of range", (long long)index);
   const TensorEntry &t = st->tensors[(size_t)index];
-  int64_t numel = 1;
-  for (int64_t d : t.shape) numel *= d;
+  const int64_t numel = t.numel;
   const int ddt = dst->dtype;
   const bool floaty = [](int d) { return d == RXW8_F32 || d == RXW8_F16 || d == RXW8_BF16; }(ddt);
   const bool src_floaty = t.dtype == RXW8_F32 || t.dtype == RXW8_F16 || t.dtype == RXW8_BF16;

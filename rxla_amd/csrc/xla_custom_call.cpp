@@ -24,8 +24,10 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
+#include <utility>
 
 #include "internal.h"
 
@@ -33,27 +35,33 @@ using namespace rxw8;
 
 namespace {
 
-// One runtime per device, created on first use and kept for the process (XLA
-// handlers are process-lifetime).
-rxw8_runtime *device_runtime(int *rc) {
+// One runtime per (device, stream), created on first use and kept for the
+// process (XLA handlers are process-lifetime). Each runtime owns its
+// workspaces (split-K partials, attention split partials and arrival
+// counters), so handlers that XLA runs concurrently on different streams never
+// share them; calls on one stream are ordered by that stream.
+rxw8_runtime *stream_runtime(void *stream, int *rc) {
   static std::mutex mu;
-  static rxw8_runtime *rts[64] = {nullptr};
+  static std::map<std::pair<int, void *>, rxw8_runtime *> rts;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess || dev < 0 || dev >= 64) {
+  if (e != hipSuccess || dev < 0) {
     *rc = hip_fail(e == hipSuccess ? hipErrorInvalidDevice : e, "hipGetDevice");
     return nullptr;
   }
   std::lock_guard<std::mutex> g(mu);
-  if (!rts[dev]) {
-    *rc = rxw8_runtime_create(dev, &rts[dev]);
+  rxw8_runtime *&rt = rts[{dev, stream}];
+  if (!rt) {
+    *rc = rxw8_runtime_create(dev, &rt);
+    if (!*rc) *rc = rxw8_runtime_set_stream(rt, stream);  // for good: all its work runs there
     if (*rc) {
-      rts[dev] = nullptr;
+      if (rt) rxw8_runtime_destroy(rt);
+      rts.erase({dev, stream});
       return nullptr;
     }
   }
   *rc = RXW8_OK;
-  return rts[dev];
+  return rt;
 }
 
 struct Opaque {
@@ -128,17 +136,14 @@ struct Views {
   }
 };
 
-// Run `body` on the runtime of the current device with XLA's stream.
+// Run `body` on the runtime of (current device, XLA's stream).
 template <typename F>
 void run_on_stream(void *stream, const char *what, void *status, F body) {
   int rc = RXW8_OK;
-  rxw8_runtime *rt = device_runtime(&rc);
+  rxw8_runtime *rt = stream_runtime(stream, &rc);
   if (rt) {
     std::lock_guard<std::recursive_mutex> g(rt->mu);
-    void *prev = rt->stream;
-    rc = rxw8_runtime_set_stream(rt, stream);
-    if (!rc) rc = body(rt);
-    rt->stream = static_cast<hipStream_t>(prev);
+    rc = body(rt);
   }
   if (rc && status) {
     using SetFailure = void (*)(void *, const char *, size_t);

@@ -13,6 +13,7 @@ Fixtures (npz without pickles, or JSON):
 * kv_checked.json        crates/rxla-core/tests/kv_cache_checked.rs:3-101
 * argmax.npz             crates/rxla-core/tests/argmax.rs:30-110
 * rounding.npz           crates/rxla-core/tests/rounding.rs:23-102 (round_ties_even rows)
+* causal_attention.npz   crates/rxla-core/tests/causal_attention.rs:25-70,93-175
 """
 from __future__ import annotations
 
@@ -177,6 +178,43 @@ def rounding():
     return {"x": x, "expected": np.rint(x).astype(F32)}
 
 
+def causal_attention():
+    imax, imin = 2 ** 31 - 1, -2 ** 31
+    out = {}
+    # causal_attention.rs:35-56: q, k zero vectors (every score 0), scale 1,
+    # key positions [0, 1, 2, 3], values [10, 20, 30, 40]; with query positions
+    # [0, 2] the rows average values 0..0 and 0..2, with [1, 3] 0..1 and 0..3
+    out["rt_kpos"] = np.array([0, 1, 2, 3], np.int32)
+    out["rt_v"] = np.array([[10.0], [20.0], [30.0], [40.0]], F32)
+    out["rt_qpos"] = np.array([[0, 2], [1, 3]], np.int32)
+    out["rt_expected"] = np.array([[10.0, 20.0], [15.0, 25.0]], F32)
+    # causal_attention.rs:59-69: extreme I32 positions, mask [2, 4]
+    out["x_qpos"] = np.array([16_777_216, imax], np.int32)
+    out["x_kpos"] = np.array([16_777_216, 16_777_217, imax, imin], np.int32)
+    out["x_mask"] = np.array([[0.0, -np.inf, -np.inf, 0.0], [0.0, 0.0, 0.0, 0.0]], F32)
+    # causal_attention.rs:72-91: static masks; rows (queries, keys, offset)
+    out["static_bad"] = np.array([[-1, 2, 0], [2, -1, 0], [2, 2, -1], [2, 2, imax],
+                                  [1, 2 ** 63 - 1, 0]], np.int64)
+    out["static_ok"] = np.array([[0, 4, 0], [1, 1, imax]], np.int64)
+    out["static_241"] = np.array([[0.0, 0.0, -np.inf, -np.inf], [0.0, 0.0, 0.0, -np.inf]], F32)
+    # causal_attention.rs:93-175: q [5, 2], k [7, 2], v [7, 2], causal mask
+    # (5, 7, 0), scale 1; chunks (0, 2), (2, 5), (4, 5) with offset = start
+    # equal the full rows; row i = softmax over keys 0..i, in f64
+    qv = np.array([f32((i - 3.0) * 0.125) for i in range(10)], F32).reshape(5, 2)
+    kv = np.array([f32((i - 6.0) * 0.125) for i in range(14)], F32).reshape(7, 2)
+    vv = np.array([f32((i - 5.0) * 0.25) for i in range(14)], F32).reshape(7, 2)
+    full = np.zeros((5, 2))
+    for i in range(5):
+        sc = [math.exp(sum(float(qv[i, d]) * float(kv[j, d]) for d in range(2)))
+              for j in range(i + 1)]
+        tot = sum(sc)
+        for d in range(2):
+            full[i, d] = sum(sc[j] / tot * float(vv[j, d]) for j in range(i + 1))
+    out.update(full_q=qv, full_k=kv, full_v=vv, full_expected=full,
+               chunks=np.array([[0, 2], [2, 5], [4, 5]], np.int64))
+    return out
+
+
 def main():
     manifest = {}
 
@@ -198,6 +236,7 @@ def main():
     save_json("kv_checked.json", kv_checked())
     save_npz("argmax.npz", argmax())
     save_npz("rounding.npz", rounding())
+    save_npz("causal_attention.npz", causal_attention())
     with open(os.path.join(HERE, "MANIFEST.json"), "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)
     print(json.dumps(manifest, indent=1))

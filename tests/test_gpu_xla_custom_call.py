@@ -80,3 +80,50 @@ def test_bad_backend_config_launches_nothing(rt, opaque):
     call(rt, "rxw8_xla_quantized_linear", [xb, wb, sb, y], opaque)
     assert (y.to_numpy() == 7.0).all()
     assert "backend_config" in r._lib.rxw8_last_error().decode()
+
+
+def test_each_stream_has_its_own_workspaces_and_none_grows_in_a_capture(rt):
+    """The handlers keep one runtime per stream XLA passes. A call whose split
+    workspace would have to grow while its stream is being captured (an XLA
+    command buffer) fails with FAILED_PRECONDITION and records nothing; the
+    same call outside the capture sizes the workspace and matches the C ABI."""
+    import torch
+
+    r = rx()
+    rng = np.random.default_rng(4)
+
+    def decode_bufs(b, hkv, lmax, fill=None):
+        hq, d = 4 * hkv, 128
+        kc = rt.buffer(oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32)),
+                       r.DType.BF16)
+        vc = rt.buffer(oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32)),
+                       r.DType.BF16)
+        q = rt.buffer(rng.standard_normal((b, hq, d)).astype(np.float32))
+        lens = rt.buffer(np.full(b, lmax, np.int32))
+        out = rt.buffer(np.full((b, hq, d), 7.0, np.float32))
+        cfg = f"b={b};hq={hq};hkv={hkv};lmax={lmax};d={d};q=f32;cache=bf16;out=f32"
+        return [q, kc, vc, lens, out], cfg
+
+    small, small_cfg = decode_bufs(2, 2, 64)      # one split: no workspace
+    big, big_cfg = decode_bufs(2, 2, 4096)        # many splits: partials + counters
+    rt.synchronize()
+    s = torch.cuda.Stream()
+
+    def call_on(bufs, opaque):
+        ptrs = (ctypes.c_void_p * len(bufs))(*[b.ptr for b in bufs])
+        text = opaque.encode()
+        r._lib.rxw8_xla_gqa_decode(ctypes.c_void_p(s.cuda_stream), ptrs, text, len(text), None)
+
+    call_on(small, small_cfg)  # creates the stream's runtime
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+        call_on(big, big_cfg)
+    assert "captured" in r._lib.rxw8_last_error().decode()
+    g.replay()
+    torch.cuda.synchronize()
+    assert (big[4].to_numpy() == 7.0).all()
+    call_on(big, big_cfg)
+    s.synchronize()
+    want = r.grouped_query_attention(rt, *big[:4]).to_numpy()
+    np.testing.assert_array_equal(big[4].to_numpy(), want)

@@ -154,6 +154,37 @@ def test_gqa_reference_head_masks(kv_heads, precision):
     assert np.max(np.abs(out - g[f"expected{kv_heads}"])) < 2e-6  # tests/gqa.rs:95-99
 
 
+def test_causal_masks_reference_vectors():
+    """crates/rxla-core/tests/causal_attention.rs:59-69 (extreme I32 positions)
+    and :168-174 (the static (2, 4, 1) mask as positions offset + i)."""
+    g = golden_npz("causal_attention.npz")
+    np.testing.assert_array_equal(oracle.causal_attention_mask(g["x_qpos"], g["x_kpos"]), g["x_mask"])
+    np.testing.assert_array_equal(oracle.causal_attention_mask(np.arange(2) + 1, np.arange(4)),
+                                  g["static_241"])
+    # a subtraction-based mask would overflow on these positions
+    assert oracle.causal_attention_mask([np.iinfo(np.int32).max], [np.iinfo(np.int32).min])[0, 0] == 0
+
+
+def test_causal_sdpa_reference_vectors():
+    """causal_attention.rs:35-56 (runtime positions; zero scores average the
+    visible values) and :93-175 (full and chunked causal attention against
+    the test's f64 loop), through the oracle's f64 GQA with one head."""
+    g = golden_npz("causal_attention.npz")
+    for qpos, want in zip(g["rt_qpos"], g["rt_expected"]):
+        m = oracle.causal_attention_mask(qpos, g["rt_kpos"])
+        out = oracle.gqa_attention(np.zeros((1, 1, 2, 1), np.float32), np.zeros((1, 1, 4, 1), np.float32),
+                                   g["rt_v"][None, None], m, scale=1.0, precision=1)
+        np.testing.assert_allclose(out[0, 0, :, 0], want, atol=2e-5)
+    q, k, v = (g[n][None, None] for n in ("full_q", "full_k", "full_v"))
+    full = oracle.gqa_attention(q, k, v, oracle.causal_attention_mask(np.arange(5), np.arange(7)),
+                                scale=1.0, precision=1)[0, 0]
+    np.testing.assert_allclose(full, g["full_expected"], atol=2e-5)
+    for start, end in g["chunks"]:
+        m = oracle.causal_attention_mask(np.arange(start, end), np.arange(7))
+        part = oracle.gqa_attention(q[:, :, start:end], k, v, m, scale=1.0, precision=1)[0, 0]
+        np.testing.assert_allclose(part, full[start:end], atol=2e-5)
+
+
 def test_masked_decode_reference_steps():
     g = golden_npz("masked_decode.npz")
     kc = np.full((2, 4, 2), g["init_k"], np.float32)

@@ -76,7 +76,8 @@ def expect_error(r, path, code):
 @pytest.mark.parametrize("case", ["short_file", "header_too_long", "bad_json", "trailing",
                                   "not_object", "size_mismatch", "past_end", "overlap",
                                   "unknown_dtype", "bad_shape", "negative_offset", "duplicate",
-                                  "metadata_not_string", "missing_field"])
+                                  "metadata_not_string", "missing_field", "numel_wraps",
+                                  "bytes_overflow"])
 def test_malformed_headers(tmp_path, case):
     r = rx()
     p = tmp_path / f"{case}.safetensors"
@@ -111,6 +112,11 @@ def test_malformed_headers(tmp_path, case):
         stf.write_raw(p, {"a": ok, "__metadata__": {"group_size": 128}}, data)
     elif case == "missing_field":
         stf.write_raw(p, {"a": {"dtype": "U8", "shape": [4]}}, data)
+    elif case == "numel_wraps":  # 2^62 * 2^62 * 16 = 2^128 wraps a 128-bit count to 0
+        stf.write_raw(p, {"a": {"dtype": "U8", "shape": [2 ** 62, 2 ** 62, 16],
+                                "data_offsets": [0, 0]}}, data)
+    elif case == "bytes_overflow":  # 2^62 F32 elements: 2^64 bytes
+        stf.write_raw(p, {"a": {"dtype": "F32", "shape": [2 ** 62], "data_offsets": [0, 0]}}, data)
     msg = expect_error(r, p, r.Status.DATA_LOSS)
     assert str(p.name) in msg
 
