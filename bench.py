@@ -165,19 +165,30 @@ def cpu_decoder_baseline(steps=8, ctx=1024, batch=8, seed=11):
                       f"{batch}, caches at {ctx} positions, through oracle.Decoder (C, OpenMP)"}
 
 
+def c5_quantized(rt, rx, torch, stream, gen, n, k, std=0.02, group=None):
+    """BASELINE configs[1] weights: W ~ N(0, std) f32 [n, k] on the device,
+    encoded by rxw8_quantize_w8 (the reference encoder's arithmetic) per output
+    channel (group = k) or per group; returns (U8 [n, k], F32 scale) buffers."""
+    with torch.cuda.stream(stream):
+        w = torch.randn((n, k), device="cuda", generator=gen) * std
+    stream.synchronize()
+    u, s_ = rx.quantize_w8(rt, rt.wrap_tensor(w), group or k)
+    rt.synchronize()
+    del w
+    return u, s_
+
+
 def bench_gemm(rt, rx, torch, stream, reps=10):
     """C3 prefill dequant-GEMM shapes; returns per-shape TFLOP/s and the MFMA
     roofline of the largest one."""
     gen = torch.Generator(device="cuda").manual_seed(1)
     shapes = [(m, n, k) for m in (512, 2048, 8192) for n, k in ((12288, 4096), (4096, 12288))]
+    ws = {(n, k): c5_quantized(rt, rx, torch, stream, gen, n, k) for n, k in ((12288, 4096), (4096, 12288))}
     with torch.cuda.stream(stream):
-        ws = {(n, k): (torch.randint(1, 256, (n, k), dtype=torch.uint8, device="cuda", generator=gen),
-                       torch.rand((n, 1), device="cuda", generator=gen) * 1e-3 + 1e-4)
-              for n, k in ((12288, 4096), (4096, 12288))}
         xs = {(m, k): torch.randn((m, k), device="cuda", generator=gen).to(torch.bfloat16)
               for m in (512, 2048, 8192) for k in (4096, 12288)}
     stream.synchronize()
-    wb = {key: (rx.pack_weight(rt, rt.wrap_tensor(u)), rt.wrap_tensor(s_)) for key, (u, s_) in ws.items()}
+    wb = {key: (rx.pack_weight(rt, u), s_) for key, (u, s_) in ws.items()}
     rt.synchronize()
     out = {}
     for m, n, k in shapes:
@@ -392,12 +403,15 @@ def qwen35_weights(rt, rx, torch, stream, model, group, seed=7):
     return keep
 
 
-def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, iterations=10):
+def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, iterations=10,
+                 compute="f32"):
     """The reference's qwen3_5_bench workload (crates/rxla-safetensors/examples/
     qwen3_5_bench.rs:44-99) on the official 0.8B text topology with random
     weights: batch 1, token ids 1000 + i, full logits [1, S, 248320] per run;
-    tokens/s = S / mean run time."""
-    cfg = rx.Qwen35Config(max_batch=1, max_seq=max(sequences))
+    tokens/s = S / mean run time. compute "f32" is the reference's precision
+    (the example leaves the layer compute dtype at the Cx default F32);
+    "bf16" is the opt-in."""
+    cfg = rx.Qwen35Config(max_batch=1, max_seq=max(sequences), compute=compute)
     model = rx.Qwen35Model(rt, cfg).compile()
     keep = qwen35_weights(rt, rx, torch, stream, model, cfg.group)
     weight_bytes = sum(int(np.prod(sh)) * (1 if dt == rx.DType.U8 else 4)
@@ -425,9 +439,10 @@ def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, ite
                         "checksum": float(lg.astype(np.float64).sum())}
         del logits
     del keep, model
-    return {"runs": res, "weight_bytes": weight_bytes,
+    return {"runs": res, "weight_bytes": weight_bytes, "compute_dtype": compute,
             "config": "Qwen3.5-0.8B text topology (24 layers, 18 gated-delta + 6 full attention, "
-                      "hidden 1024, vocab 248320, G 128), batch 1, random W8 weights",
+                      "hidden 1024, vocab 248320, G 128), batch 1, random W8 weights, "
+                      f"projections computed in {compute}",
             "timing": f"wall clock around rxw8_qwen35_forward, synchronized; {warmup} warmup, "
                       f"mean of {iterations}"}
 
@@ -452,13 +467,12 @@ def pmc_probe(kind, rounds=3):
     stream.synchronize()
     if kind == "gemv":  # B=1, N=24576, K=4096, packed, 6 rotating copies
         n, b = 24576, 1
+        ws = [c5_quantized(rt, rx, torch, stream, gen, n, K) for _ in range(6)]
         with torch.cuda.stream(stream):
-            ws = [(torch.randint(1, 256, (n, K), dtype=torch.uint8, device="cuda", generator=gen),
-                   torch.rand((n, 1), device="cuda", generator=gen) * 1e-3) for _ in range(6)]
             x = torch.randn((b, K), device="cuda", generator=gen).to(torch.bfloat16)
             y = torch.empty((b, n), dtype=torch.bfloat16, device="cuda")
         stream.synchronize()
-        wb = [(rx.pack_weight(rt, rt.wrap_tensor(u)), rt.wrap_tensor(s_)) for u, s_ in ws]
+        wb = [(rx.pack_weight(rt, u), s_) for u, s_ in ws]
         rt.synchronize()
         xb, yb = rt.wrap_tensor(x), rt.wrap_tensor(y)
         for _ in range(rounds):
@@ -470,14 +484,13 @@ def pmc_probe(kind, rounds=3):
         log(f"pmc probe gemv B={b} N={n} K={K}: {reps} launches, {gemv_bytes(b, n)} algorithmic B each")
     elif kind == "gemm":  # C3 roofline shape M=8192 N=12288 K=4096, 10 launches after warm-up
         m, n = 8192, 12288
+        u, sb = c5_quantized(rt, rx, torch, stream, gen, n, K)
         with torch.cuda.stream(stream):
-            u = torch.randint(1, 256, (n, K), dtype=torch.uint8, device="cuda", generator=gen)
-            sc = torch.rand((n, 1), device="cuda", generator=gen) * 1e-3 + 1e-4
             x = torch.randn((m, K), device="cuda", generator=gen).to(torch.bfloat16)
             y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
         stream.synchronize()
-        ub = rx.pack_weight(rt, rt.wrap_tensor(u))
-        xb, sb, yb = rt.wrap_tensor(x), rt.wrap_tensor(sc), rt.wrap_tensor(y)
+        ub = rx.pack_weight(rt, u)
+        xb, yb = rt.wrap_tensor(x), rt.wrap_tensor(y)
         for _ in range(30):
             rx.quantized_linear(rt, xb, ub, sb, rx.DType.BF16, out=yb)
         log(f"pmc probe gemm M={m} N={n} K={K}: 30 launches")
@@ -547,29 +560,28 @@ def main():
         print(json.dumps({"qwen35": bench_qwen35(rt, rx, torch, stream)}), flush=True)
         return
     gen = torch.Generator(device="cuda").manual_seed(0)
-    log(f"device {info}; allocating {args.copies} weight copies per N")
+    log(f"device {info}; encoding {args.copies} weight copies per N from N(0, 0.02)")
+    weights = {n: [c5_quantized(rt, rx, torch, stream, gen, n, K) for _ in range(args.copies)]
+               for n in NS}
     with torch.cuda.stream(stream):
-        weights = {n: [(torch.randint(1, 256, (n, K), dtype=torch.uint8, device="cuda",
-                                      generator=gen),
-                        torch.rand((n, 1), dtype=torch.float32, device="cuda",
-                                   generator=gen) * 1e-3 + 1e-4)
-                       for _ in range(args.copies)] for n in NS}
         xs = {b: torch.randn((b, K), device="cuda", generator=gen).to(torch.bfloat16) for b in BS}
         ys = {(b, n): torch.empty((b, n), dtype=torch.bfloat16, device="cuda")
               for b in BS for n in NS}
     stream.synchronize()
     layout = os.environ.get("RXW8_BENCH_LAYOUT", "packed")
-    wb = {n: [((rx.pack_weight(rt, rt.wrap_tensor(u)) if layout == "packed" else rt.wrap_tensor(u)),
-               rt.wrap_tensor(s)) for u, s in weights[n]] for n in NS}
+    # the timed layout, and the reference's row-major U8 layout for the second leg
+    wb = {n: [((rx.pack_weight(rt, u) if layout == "packed" else u), s) for u, s in weights[n]]
+          for n in NS}
+    wb_row = {n: list(weights[n]) for n in NS}
     rt.synchronize()
     xb = {b: rt.wrap_tensor(xs[b]) for b in BS}
     yb = {k: rt.wrap_tensor(v) for k, v in ys.items()}
     plan = [(b, n) for n in NS for b in BS]
     step_bytes = sum(gemv_bytes(b, n) for b, n in plan)
 
-    def launch_all(copy, events=None):
+    def launch_all(copy, events=None, wts=None):
         for b, n in plan:
-            u, s = wb[n][copy]
+            u, s = (wts or wb)[n][copy]
             if events is not None:
                 e0 = torch.cuda.Event(enable_timing=True)
                 e1 = torch.cuda.Event(enable_timing=True)
@@ -609,6 +621,28 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     log(f"timed {args.steps} graph steps in {wall:.4f} s")
+
+    # The same sweep on the reference's row-major U8 weights (the layout the
+    # XLA handlers and direct QuantizedLinear::apply calls receive): graphs of
+    # the same 9 launches, same step count, timed the same way.
+    graphs_row = []
+    for c in range(args.copies):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            launch_all(c, wts=wb_row)
+        graphs_row.append(g)
+    for i in range(args.warmup):
+        graphs_row[i % args.copies].replay()
+    torch.cuda.synchronize()
+    assert all(torch.equal(ys[k], ref[k]) for k in ys) or layout != "packed", \
+        "row-major weights give other results than the packed layout"
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        graphs_row[i % args.copies].replay()
+    torch.cuda.synchronize()
+    wall_row = time.perf_counter() - t0
+    del graphs_row
+    log(f"timed {args.steps} row-major graph steps in {wall_row:.4f} s")
 
     # Kernel durations: per shape, one HIP event pair on the runtime stream
     # around `copies` back-to-back eager launches (one per weight copy), queued
@@ -688,8 +722,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (torch.randint u8 codes, uniform scales, randn bf16 activations; "
-                "seed 0)",
+        "data": "synthetic: W ~ N(0, 0.02) f32 encoded per output channel on the device by "
+                "rxw8_quantize_w8 (the reference encoder's arithmetic), x ~ N(0, 1) rounded to "
+                "bf16; torch generator seed 0",
         "config": {"workload": "decode dequant-GEMV sweep (BASELINE configs[1])",
                    "batch": list(BS), "out_features": list(NS), "in_features": K,
                    "scales": "per-output-channel f32", "weight_copies": args.copies,
@@ -719,6 +754,10 @@ def main():
                                     "rxw8_gemv_w8_pk_mb1_rw4_u4 + rxw8_gemv_splitk_reduce",
                          "mean_launch_us": round(b16_s * 1e6, 3)},
         "sweep": sweep,
+        "rowmajor": {"value": round(step_bytes * args.steps / wall_row / 1e9, 2), "unit": "GB/s",
+                     "ms_per_step": round(wall_row / args.steps * 1e3, 4),
+                     "weight_layout": "row-major U8 [N, K] (the reference's weight ABI)",
+                     "timing": "same sweep, step count and graph replays as `value`"},
         "device": info,
     }
     del graphs, weights, wb
@@ -741,6 +780,9 @@ def main():
         log("Qwen3.5-0.8B topology, full-sequence logits ...")
         out["qwen35"] = bench_qwen35(rt, rx, torch, stream)
         log(json.dumps(out["qwen35"]))
+        out["qwen35_bf16_opt_in"] = bench_qwen35(rt, rx, torch, stream, sequences=(16,),
+                                                 compute="bf16")
+        log(json.dumps(out["qwen35_bf16_opt_in"]))
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle) ...")
         out["cpu_baseline"] = cpu_baseline()

@@ -141,13 +141,14 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_linear_generic(GenericLin
 // in A and B). Rows of x >= T and channels >= N read clamped, valid addresses
 // and are never stored.
 struct LinearF32Args {
-  const float *x;      // [T, K]
-  const uint8_t *w;    // [N, K]
-  const float *scale;  // [N, K / G]
+  const float *x;      // [T, K] rows of ldx elements
+  const uint8_t *w;    // [N, K] rows of ldw bytes
+  const float *scale;  // [N, K / G] rows of ldsc elements
   float *y;            // [T, N]
   int T, N, K, G;
   int y_mode;          // 0: y = result; 1: y += result (f32 residual)
   int tiles;           // channel tiles (16 WV channels each) per workgroup
+  int64_t ldx, ldw, ldsc;  // row strides: a K-range of a wider product (host K chunks)
 };
 
 template <int R, int WV>
@@ -165,7 +166,7 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
   for (int e = threadIdx.x * 4; e < 16 * R * K; e += blockDim.x * 4) {
     const int m = e / K, c = e - m * K;
     const int t = min(m0 + m, a.T - 1);
-    const float4 v = *(const float4 *)(a.x + (int64_t)t * K + c);
+    const float4 v = *(const float4 *)(a.x + (int64_t)t * a.ldx + c);
     const float xs[4] = {v.x, v.y, v.z, v.w};
     uint32_t hb[4], lb[4];
 #pragma unroll
@@ -184,12 +185,12 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
   for (int e = threadIdx.x; e < 16 * WV * ng; e += blockDim.x) {
     const int r = e / ng, g = e - r * ng;
     const int n = min(n0 + r, a.N - 1);
-    sc[e] = a.scale[(int64_t)n * ng + g];
+    sc[e] = a.scale[(int64_t)n * a.ldsc + g];
   }
   __syncthreads();
   // ---- stream the weight rows
   const int nrow = min(n0 + 16 * wv + col, a.N - 1);
-  const uint8_t *wp = a.w + (int64_t)nrow * K + 16 * part;
+  const uint8_t *wp = a.w + (int64_t)nrow * a.ldw + 16 * part;
   const float *scl = sc + (16 * wv + col) * ng;
   f32x4 acc[R], accg[R];
 #pragma unroll

@@ -128,6 +128,7 @@ struct LinearF32Args {
   int T, N, K, G;
   int y_mode;
   int tiles;
+  int64_t ldx, ldw, ldsc;
 };
 
 struct KvUpdateArgs {
@@ -451,25 +452,53 @@ static int run_generic_linear(Runtime *rt, const void *x, int x_f32, const void 
 // rows of x within the LDS limit. Returns UNIMPLEMENTED otherwise.
 static int run_linear_f32(Runtime *rt, const float *x, const uint8_t *w, const float *scale,
                           float *y, int64_t M, int64_t N, int64_t K, int64_t G, int y_mode) {
-  if (K % 64 != 0 || G % 64 != 0 || K > (1 << 20) || N > (1LL << 30) || M > (1LL << 30) ||
+  if (K % 64 != 0 || G % 64 != 0 || K > (1 << 24) || N > (1LL << 30) || M > (1LL << 30) ||
       ((uintptr_t)x | (uintptr_t)w) % 16 != 0 || env_int("RXW8_FORCE_GENERIC", 0))
     return RXW8_UNIMPLEMENTED;
   constexpr int WV = 8;
-  const int64_t ng = K / G;
+  // x (hi and lo) of the workgroup's rows is staged in LDS for its K range:
+  // a K too wide for LDS runs as several launches over K ranges, each
+  // accumulating into y (the first one stores when y_mode is 0). Ranges hold
+  // whole scale groups, or, when one group is too wide, equal parts of every
+  // group (each part then scales its own partial sum). The group sums are
+  // reassociated across ranges: f32 rounding only.
+  auto lds_for = [&](int R, int64_t kc, int64_t g) {
+    return (size_t)2 * 16 * R * (kc + 8) * 2 + (size_t)16 * WV * (kc / g) * 4;
+  };
   for (int R : {M > 16 ? 2 : 1, 1}) {
-    const size_t lds = (size_t)2 * 16 * R * (K + 8) * 2 + (size_t)16 * WV * ng * 4;
-    if (lds > rt->lds_max) continue;
+    int64_t kc_max = 0, gk = G;
+    if (lds_for(R, K, G) <= rt->lds_max) {
+      kc_max = K;
+    } else if (lds_for(R, G, G) <= rt->lds_max) {
+      int64_t fit = G;
+      while (fit + G <= K && lds_for(R, fit + G, G) <= rt->lds_max) fit += G;
+      const int64_t chunks = (K + fit - 1) / fit;
+      kc_max = (K / G + chunks - 1) / chunks * G;
+    } else {
+      for (int64_t d = G; d >= 64; d -= 64)
+        if (G % d == 0 && lds_for(R, d, d) <= rt->lds_max) {
+          kc_max = gk = d;
+          break;
+        }
+    }
+    if (kc_max == 0) continue;
     const int64_t gy = (M + 16 * R - 1) / (16 * R);
     if (gy > 65535) return RXW8_UNIMPLEMENTED;
     // several channel tiles per workgroup when there are many row tiles, so
     // the staged rows of x are reused (about 2048 workgroups in all)
     const int64_t ntiles = (N + 16 * WV - 1) / (16 * WV);
     const int64_t per = std::max<int64_t>(1, std::min<int64_t>(16, ntiles * gy / 2048));
-    LinearF32Args a{x, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode, (int)per};
     char kname[40];
     std::snprintf(kname, sizeof kname, "rxw8_linear_f32_mfma_r%d_w%d", R, WV);
-    return launch(rt, kname, dim3((unsigned)((ntiles + per - 1) / per), (unsigned)gy),
-                  dim3(64 * WV), a, lds);
+    for (int64_t k0 = 0; k0 < K; k0 += kc_max) {
+      const int64_t kc = std::min(kc_max, K - k0);
+      LinearF32Args a{x + k0, w + k0, scale + k0 / G, y, (int)M, (int)N, (int)kc, (int)gk,
+                      k0 == 0 ? y_mode : 1, (int)per, K, K, K / G};
+      int rc = launch(rt, kname, dim3((unsigned)((ntiles + per - 1) / per), (unsigned)gy),
+                      dim3(64 * WV), a, lds_for(R, kc, gk));
+      if (rc) return rc;
+    }
+    return RXW8_OK;
   }
   return RXW8_UNIMPLEMENTED;
 }

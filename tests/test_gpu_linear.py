@@ -108,10 +108,15 @@ def test_f32_compute_path(rt):
 
 @pytest.mark.parametrize("m,n,k,g", [(1, 1000, 1024, 128), (16, 4096, 1024, 128),
                                      (33, 777, 512, 64), (100, 256, 2048, 2048),
-                                     (5, 96, 4096, 4096)])
+                                     (5, 96, 4096, 4096),
+                                     # K ranges of whole groups (the 0.8B down projection)
+                                     (16, 1024, 3584, 128), (40, 512, 8192, 2048),
+                                     # one group wider than LDS: equal parts of it
+                                     (3, 256, 12288, 12288)])
 def test_f32_compute_matrix_core_path(rt, m, n, k, g):
     """F32 compute on the matrix cores: x as bf16 hi + lo parts (16 significant
-    bits), exact codes, f32 accumulation; channel and row tails included."""
+    bits), exact codes, f32 accumulation; channel and row tails included, and
+    inputs too wide for one LDS staging (several launches over K ranges)."""
     rng = np.random.default_rng(m * 7 + n)
     x = rng.standard_normal((m, k)).astype(np.float32)
     u8, s = quantized(rng, n, k, g)
