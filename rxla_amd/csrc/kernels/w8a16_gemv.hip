@@ -64,6 +64,10 @@ struct GemvArgs {
   float eps;
   const float *ss_in;       // mode 3
   int ss_parts;
+  // plain rows (x_mode 0) with per-channel scales: every wave stages only its
+  // own K slice of the rows in an LDS region of its own and starts without a
+  // workgroup barrier (host-chosen; the LDS holds NW regions of M rows)
+  int wave_stage;
 };
 
 struct SplitkReduceArgs {
@@ -249,7 +253,13 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 // NW: waves per workgroup (4, or 8 / 16 for the wide decode variants that
 // give one workgroup more loads in flight instead of splitting K over
 // workgroups).
-template <int MB, int RW, int U, bool PK, int NW = 4>
+// XG: bf16 activation rows (x_mode 0, per-channel scales) are read as MFMA B
+// fragments straight from global memory -- the rows are tiny next to the
+// weights and shared by every workgroup, so they stay in L2 -- and prefetched
+// with the weights in the same double-buffered groups: no LDS staging, no
+// barrier before the stream, and LDS only for the cross-wave reduction (so it
+// does not limit how many workgroups a CU holds).
+template <int MB, int RW, int U, bool PK, int NW = 4, bool XG = false>
 __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   constexpr int KW = NW / RW;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -284,26 +294,48 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
     wstep = 64;
   }
   const int last = chunks - 1;
+  // B-operand rows: batch column col + 16*mb, clamped to a valid row (LDS
+  // rows are set after staging; XG reads the global rows)
+  const uint16_t *xrow[MB];
+  if (XG)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int b = col + 16 * mb;
+      xrow[mb] = (const uint16_t *)a.x + (int64_t)(b < a.M ? b : a.M - 1) * a.x_stride + a.x_off +
+                 k0 + kbase + j * 16;
+    }
   u32x4 bufA[U], bufB[U];
-  auto load_group = [&](u32x4(&wb)[U], int c0) {
+  u32x4 xgA[XG ? U : 1][MB][2], xgB[XG ? U : 1][MB][2];
+  auto load_group = [&](u32x4(&wb)[U], u32x4(&xg)[XG ? U : 1][MB][2], int c0) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
       wb[u] = __builtin_nontemporal_load((const u32x4 *)(wp + (int64_t)min(c0 + u, last) * wstep));
+    if (XG)
+#pragma unroll
+      for (int u = 0; u < (XG ? U : 1); ++u)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const u32x4 *xp = (const u32x4 *)(xrow[mb] + (int64_t)min(c0 + u, last) * 64);
+          xg[u][mb][0] = xp[0];
+          xg[u][mb][1] = xp[1];
+        }
   };
   // The first weight group is in flight while x and the scales are staged.
-  load_group(bufA, 0);
+  load_group(bufA, xgA, 0);
 
-  // Plain activation rows with per-channel scales, one row (any tiling) or up
-  // to 4 rows with one row group: every wave stages only its own K slice of
-  // the rows, in its own LDS region (M rows of stride Kw + kXPad), and starts
-  // its loop as soon as that slice is in -- no workgroup barrier before the
-  // weights stream. (Waves of different row groups stage the same slice.)
-  const bool wave_stage = a.x_mode == 0 && per_channel && (a.M == 1 || (RW == 1 && a.M <= 4));
+  // Plain activation rows with per-channel scales (when the host chose it):
+  // every wave stages only its own K slice of the rows, in its own LDS region
+  // (M rows of stride Kw + kXPad), and starts its loop as soon as that slice
+  // is in -- no workgroup barrier before the weights stream. (Waves of
+  // different row groups stage the same slice.)
+  const bool wave_stage = a.wave_stage && a.x_mode == 0 && per_channel;
   const uint16_t *xbase = xs;
   int xld = ldx;
   const int gps = per_channel ? 0 : Kc / a.G;
   float *ss = (float *)(xs + a.M * ldx);
-  if (wave_stage) {
+  if (XG) {
+    // nothing to stage: per-channel scales are read in the epilogue
+  } else if (wave_stage) {
     const int pieces = Kw / 8;  // 8 values per 16-byte piece
     uint16_t *xw = xs + wave * a.M * (Kw + kXPad);
     for (int i = lane; i < a.M * pieces; i += 64) {
@@ -338,25 +370,25 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
     ones[mb] = acc[mb];
     total[mb] = acc[mb];
   }
-  // B-operand rows: batch column col + 16*mb, clamped to a valid staged row.
-  const uint16_t *xrow[MB];
+  if (!XG)
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int b = col + 16 * mb;
-    xrow[mb] = xbase + (b < a.M ? b : a.M - 1) * xld + kbase + j * 16;
-  }
+    for (int mb = 0; mb < MB; ++mb) {
+      const int b = col + 16 * mb;
+      xrow[mb] = xbase + (b < a.M ? b : a.M - 1) * xld + kbase + j * 16;
+    }
   const u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
   const bf16x8 onesf = as_bf16x8(ones_bits);
 
-  // Process one 64-k chunk c (of this wave's slice) held in register slice w.
-  auto process = [&](const u32x4 w, const int c) {
+  // Process one 64-k chunk c (of this wave's slice) held in register slice w
+  // (XG: with its activation fragments xg).
+  auto process = [&](const u32x4 w, const u32x4(&xg)[MB][2], const int c) {
     const uint2 p0 = u8x4_to_bf16x4(w[0]), p1 = u8x4_to_bf16x4(w[1]);
     const uint2 p2 = u8x4_to_bf16x4(w[2]), p3 = u8x4_to_bf16x4(w[3]);
     const u32x4 a0 = {p0.x, p0.y, p1.x, p1.y}, a1 = {p2.x, p2.y, p3.x, p3.y};
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const u32x4 *xp = (const u32x4 *)(xrow[mb] + c * 64);
-      const bf16x8 x0 = as_bf16x8(xp[0]), x1 = as_bf16x8(xp[1]);
+      const bf16x8 x0 = as_bf16x8(XG ? xg[mb][0] : xp[0]), x1 = as_bf16x8(XG ? xg[mb][1] : xp[1]);
       acc[mb] = mfma16x16x32(as_bf16x8(a0), x0, acc[mb]);
       acc[mb] = mfma16x16x32(as_bf16x8(a1), x1, acc[mb]);
       ones[mb] = mfma16x16x32(onesf, x0, ones[mb]);
@@ -378,12 +410,12 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   // A/B double buffer: issue B, consume A, issue A', consume B.
   // chunks % (2U) == 0 (host); loads past the last chunk are clamped to it.
   for (int c0 = 0; c0 < chunks; c0 += 2 * U) {
-    load_group(bufB, c0 + U);
+    load_group(bufB, xgB, c0 + U);
 #pragma unroll
-    for (int u = 0; u < U; ++u) process(bufA[u], c0 + u);
-    load_group(bufA, c0 + 2 * U);
+    for (int u = 0; u < U; ++u) process(bufA[u], xgA[XG ? u : 0], c0 + u);
+    load_group(bufA, xgA, c0 + 2 * U);
 #pragma unroll
-    for (int u = 0; u < U; ++u) process(bufB[u], c0 + U + u);
+    for (int u = 0; u < U; ++u) process(bufB[u], xgB[XG ? u : 0], c0 + U + u);
   }
   if (per_channel)
 #pragma unroll
@@ -523,12 +555,40 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(Splitk
   RXW8_GEMV_WIDE_U(MB, 1, NW)     \
   RXW8_GEMV_WIDE_U(MB, 2, NW)     \
   RXW8_GEMV_WIDE_U(MB, 4, NW)
+// XG: activations from global memory (bf16 rows, per-channel scales, M <= 16)
+#define RXW8_GEMV_XG(RW, U, NW)                                                 \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                         \
+      rxw8_gemv_w8_mb1_rw##RW##_u##U##_w##NW##_xg(GemvArgs a) {                 \
+    gemv_w8<1, RW, U, false, NW, true>(a);                                      \
+  }                                                                             \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                         \
+      rxw8_gemv_w8_pk_mb1_rw##RW##_u##U##_w##NW##_xg(GemvArgs a) {              \
+    gemv_w8<1, RW, U, true, NW, true>(a);                                       \
+  }
+#define RXW8_GEMV_XG_U(RW, NW) \
+  RXW8_GEMV_XG(RW, 4, NW)      \
+  RXW8_GEMV_XG(RW, 3, NW)      \
+  RXW8_GEMV_XG(RW, 2, NW)      \
+  RXW8_GEMV_XG(RW, 1, NW)
+RXW8_GEMV_XG_U(1, 4)
+RXW8_GEMV_XG_U(4, 4)
+RXW8_GEMV_XG_U(1, 8)
+RXW8_GEMV_XG_U(2, 8)
+RXW8_GEMV_XG_U(4, 8)
+RXW8_GEMV_XG_U(3, 12)
+RXW8_GEMV_XG_U(1, 16)
+RXW8_GEMV_XG_U(2, 16)
+RXW8_GEMV_XG_U(4, 16)
+RXW8_GEMV_XG_U(1, 14)
 RXW8_GEMV_WIDE_RW(1, 8)
 RXW8_GEMV_WIDE_RW(1, 16)
 RXW8_GEMV_WIDE_RW(2, 8)
 RXW8_GEMV_WIDE_RW(2, 16)
 RXW8_GEMV_WIDE_U(1, 3, 12)
 RXW8_GEMV_WIDE_U(2, 3, 12)
+// 12 waves as 6 row groups x 2 k slices: 96-row tiles stage x once per 96
+// rows (many activation rows, e.g. N = 24576 in 256 workgroups)
+RXW8_GEMV_WIDE_U(1, 6, 12)
 // 14 waves over K (K = 14 x 256, e.g. 3584) for narrow N in one launch
 RXW8_GEMV_WIDE_U(1, 1, 14)
 RXW8_GEMV_WIDE_U(2, 1, 14)

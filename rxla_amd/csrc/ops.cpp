@@ -31,6 +31,7 @@ struct GemvArgs {
   float eps;
   const float *ss_in;
   int ss_parts;
+  int wave_stage;
 };
 
 struct PackArgs {
@@ -211,16 +212,26 @@ struct GemvPlan {
   size_t lds = 0;
 };
 
+// Whether plain rows (x_mode 0) are staged per wave (each wave its own K
+// slice, no workgroup barrier): per-channel u8 weights with one row, or up to
+// RXW8_GEMV_WAVE_M rows (default 4) with one row group per workgroup.
+static bool gemv_wave_stage(int64_t m, int64_t k, int64_t g, int rw, bool w_bf16) {
+  static const int max_m = [] {
+    const char *v = std::getenv("RXW8_GEMV_WAVE_M");
+    return v && *v ? std::atoi(v) : 4;
+  }();
+  return g == k && !w_bf16 && (m == 1 || (rw == 1 && m <= max_m));
+}
+
 // LDS of one GEMV workgroup: the [m, kc] bf16 activation slice (rows padded by
 // 8), the grouped-scale tile [16*rw, kc/g] f32, and the cross-wave reduction
 // area (reused after the loop) of (4/rw - 1) * rw * mb f32 tiles of 16x16.
 static size_t gemv_lds(int64_t m, int64_t kc, int64_t k, int64_t g, int rw, int mb,
                        bool w_bf16, int nw = 4) {
   size_t stage = (size_t)m * (kc + 8) * 2 + (g == k ? 0 : (size_t)16 * rw * (kc / g) * 4);
-  // plain rows with per-channel scales (one row, or up to 4 with one row
-  // group): each of the nw waves may stage its own K slice (kc / (nw / rw)
-  // values) of the m rows in a region of its own
-  if ((m == 1 || (rw == 1 && m <= 4)) && g == k && !w_bf16) {
+  // per-wave staging: each of the nw waves stages its own K slice
+  // (kc / (nw / rw) values) of the m rows in a region of its own
+  if (gemv_wave_stage(m, k, g, rw, w_bf16)) {
     const size_t per_wave = (size_t)nw * m * (kc / (nw / rw) + 8) * 2;
     if (per_wave > stage) stage = per_wave;
   }
@@ -251,10 +262,21 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
   // divides the wave's slices into A/B groups.
   if (prefer_ks1 && allow_wide && !w_bf16 && forced_rw == 0) {
     const int forced_nw = env_int("RXW8_GEMV_NW", 0);
-    static const int shapes[][2] = {{16, 4}, {12, 3}, {16, 2}, {16, 1}, {14, 1}, {8, 4}, {8, 2}, {8, 1}};
+    // Many activation rows (m > 4) make staging the cost per weight byte:
+    // 96-row tiles (12 waves as 6 row groups) come first there, and 8-wave
+    // workgroups before 16-wave ones (half the cross-wave reduction per tile;
+    // measured at 8 and 16 rows, e.g. 8 x 4096 x 2048: 4.8 vs 4.8 us, 16 x
+    // 4096 x 4096: 9.2 vs 10.4 us).
+    static const int shapes_few[][2] = {{16, 4}, {12, 3}, {16, 2}, {16, 1}, {14, 1},
+                                        {8, 4}, {8, 2}, {8, 1}, {12, 6}};
+    static const int shapes_many[][2] = {{12, 6}, {12, 3}, {8, 4}, {8, 2}, {8, 1},
+                                         {16, 4}, {16, 2}, {16, 1}, {14, 1}};
+    const auto &shapes = m > 4 ? shapes_many : shapes_few;
+    const int forced_rw6 = env_int("RXW8_GEMV_RW6", -1);
     for (int pass = 0; pass < 2; ++pass) {
       for (const auto &sh : shapes) {
         const int nw = sh[0], rw = sh[1];
+        if (rw == 6 && (p.mb != 1 || pass == 1 || !(forced_rw6 >= 0 ? forced_rw6 : m > 4))) continue;
         if (forced_nw && forced_nw != nw) continue;
         const int kw = nw / rw;
         const int64_t tiles = (n + 16 * rw - 1) / (16 * rw);
@@ -262,7 +284,9 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
         if (pass == 1 && rw > 1 && tiles < rt->cus) continue;
         if (pass == 1 && rw == 3) continue;
         if (k % kw || (k / kw) % (2 * slice)) continue;
-        if (!per_channel && k % g) continue;
+        // grouped scales: every wave's K slice holds whole groups (the kernel
+        // folds a group's sum within one wave)
+        if (!per_channel && (k / kw) % g) continue;
         const size_t lds = gemv_lds(m, k, k, g, rw, p.mb, w_bf16, nw);
         if (lds + 256 > rt->lds_max) continue;
         p.nw = nw;
@@ -277,12 +301,14 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
     }
   }
   // 4-wave plans: rw = 1 splits K over the 4 waves, so K per split must hold
-  // 4 waves x an even number of slices; narrow K (e.g. 256) falls back to
-  // rw = 4 (one wave per 16-row group, the whole split each)
+  // 4 waves x an even number of slices (and whole scale groups per wave);
+  // otherwise (narrow K such as 256, wide groups) rw = 4 (one wave per
+  // 16-row group, the whole split each)
   if (forced_rw == 0 && p.rw == 1) {
     bool any = false;
     for (int ks = 1; ks <= 64 && !any; ++ks)
-      any = k % ks == 0 && (k / ks) % 4 == 0 && (k / ks / 4) % (2 * slice) == 0;
+      any = k % ks == 0 && (k / ks) % 4 == 0 && (k / ks / 4) % (2 * slice) == 0 &&
+            (per_channel || (k / ks / 4) % g == 0);
     if (!any) p.rw = 4;
   }
   const int kw = 4 / p.rw;
@@ -300,7 +326,7 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
       if (k % ks) continue;
       const int64_t kc = k / ks;
       if (kc % kw || (kc / kw) % (2 * slice)) continue;  // even slices per wave
-      if (!per_channel && kc % g) continue;
+      if (!per_channel && (kc / kw) % g) continue;         // whole groups per wave
       if (gemv_lds(m, kc, k, g, p.rw, p.mb, w_bf16) + 256 > cap) continue;
       valid[nvalid++] = ks;
     }
@@ -341,12 +367,21 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
                     int64_t K, int64_t G, int y_mode = 0, const GemvOptions *pro = nullptr) {
   // Plain calls take the wide single-launch tilings when even 64-row tiles
   // give every CU a workgroup (e.g. N = 24576): x is then staged once per 64
-  // rows and no split-K reduce runs. Smaller N keep the 4-wave plans, which
-  // fill the CUs with more, narrower tiles.
+  // rows and no split-K reduce runs; so do 8 or more rows over at most 17 MB
+  // of weights (one launch beats a split plus its reduce there). Other shapes
+  // keep the 4-wave plans, which fill the CUs with more, narrower tiles.
   GemvOptions plain;
   const int wide_env = env_int("RXW8_GEMV_PREFER_WIDE", -1);
-  plain.prefer_ks1 = wide_env >= 0 ? wide_env != 0 : (!w_bf16 && N / 64 >= rt->cus);
+  plain.prefer_ks1 = wide_env >= 0 ? wide_env != 0
+                                    : (!w_bf16 && (N / 64 >= rt->cus || (M >= 8 && N * K <= 17000000)));
   if (!pro) pro = &plain;
+  // activations as MFMA fragments from global memory (XG) pay off when the
+  // weights are small next to the staging each workgroup would do: up to 8
+  // rows and 17 MB of weights (measured: 8 x 4096 x 2048 5.6 -> 4.8 us;
+  // 25 MB and more, or 16 rows, stream slower because the fragment reads load
+  // L2). RXW8_GEMV_XG=0 / 1 forces it off / on (where it applies).
+  static const int xg_env = env_int("RXW8_GEMV_XG", -1);
+  const int xg_mode = xg_env >= 0 ? xg_env : (M <= 8 && N * K <= 17000000);
   const int64_t mchunk = M <= 16 ? 16 : 32;
   GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16, pro->prefer_ks1,
                          pro->mode != 1);
@@ -388,14 +423,24 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     a.x_f32 = x_f32;
     a.y_f32 = y_f32;
     a.y_mode = pro->swiglu ? 2 : y_mode;
+    a.wave_stage = pro->mode == 0 && gemv_wave_stage(mm, K, G, p.rw, w_bf16);
     const int mb = mm <= 16 ? 1 : 2;
+    // bf16 activation rows with per-channel u8 weights: the variant that reads
+    // them as MFMA fragments from global memory (no LDS staging)
+    const bool xg = xg_mode != 0 && pro->mode == 0 && !x_f32 && !w_bf16 && G == K && mb == 1 &&
+                    (p.nw != 4 || p.rw == 1 || p.rw == 4);
+    const int u = xg && p.u > 4 ? 4 : p.u;
     char kname[64];
-    char wide[8] = "";
-    if (p.nw != 4) std::snprintf(wide, sizeof wide, "_w%d", p.nw);
+    char wide[12] = "";
+    if (xg)
+      std::snprintf(wide, sizeof wide, "_w%d_xg", p.nw);
+    else if (p.nw != 4)
+      std::snprintf(wide, sizeof wide, "_w%d", p.nw);
     std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s_mb%d_rw%d_u%d%s", w_bf16 ? "bf16" : "w8",
-                  packed ? "_pk" : "", mb, p.rw, p.u, wide);
-    int rc = launch(rt, kname, dim3((unsigned)(tiles * p.ks)), dim3(64 * p.nw), a,
-                    gemv_lds(mm, K / p.ks, K, G, p.rw, mb, w_bf16, p.nw));
+                  packed ? "_pk" : "", mb, p.rw, u, wide);
+    const size_t lds = xg ? (size_t)(p.nw / p.rw - 1) * p.rw * mb * 256 * 4 + 16
+                          : gemv_lds(mm, K / p.ks, K, G, p.rw, mb, w_bf16, p.nw);
+    int rc = launch(rt, kname, dim3((unsigned)(tiles * p.ks)), dim3(64 * p.nw), a, lds);
     if (rc) return rc;
     if (p.ks > 1) {
       SplitkReduceArgs r;

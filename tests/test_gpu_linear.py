@@ -75,11 +75,13 @@ def test_c2_decode_gemv_sweep(rt, b, n):
     assert e_elem <= ELEM_TOL
 
 
-@pytest.mark.parametrize("g", [64, 128, 512])
-def test_grouped_scales(rt, g):
-    rng = np.random.default_rng(g)
-    x = rng.standard_normal((8, 2048)).astype(np.float32)
-    u8, s = quantized(rng, 1024, 2048, g)
+@pytest.mark.parametrize("m,k,g", [(8, 2048, 64), (8, 2048, 128), (8, 2048, 512),
+                                   # groups wider than a wave's K slice at 1 and 4 rows
+                                   (1, 4096, 2048), (4, 4096, 1024), (16, 4096, 2048)])
+def test_grouped_scales(rt, m, k, g):
+    rng = np.random.default_rng(g + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    u8, s = quantized(rng, 1024, k, g)
     ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16)
     err = rel_err(run_linear(rt, x, u8, s), ref)
     print(f"G={g} rel_err={err:.3e}")
