@@ -540,6 +540,8 @@ def main():
                     help="counter-collection program only")
     ap.add_argument("--qwen35-only", action="store_true",
                     help="(profiling) run only the Qwen3.5 leg and print its JSON")
+    ap.add_argument("--decoder-only", action="store_true",
+                    help="(profiling) run only the C5 decoder leg and print its JSON")
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe(args.pmc_probe)
@@ -558,6 +560,9 @@ def main():
     rt.set_stream(stream.cuda_stream)
     if args.qwen35_only:
         print(json.dumps({"qwen35": bench_qwen35(rt, rx, torch, stream)}), flush=True)
+        return
+    if args.decoder_only:
+        print(json.dumps({"decoder": bench_decoder(rt, rx, torch, stream)}), flush=True)
         return
     gen = torch.Generator(device="cuda").manual_seed(0)
     log(f"device {info}; encoding {args.copies} weight copies per N from N(0, 0.02)")

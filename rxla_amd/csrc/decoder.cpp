@@ -47,17 +47,15 @@ int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t 
                    float scale);
 
 // Kernel argument structs (match kernels/decoder.hip and w8a16_gemv.hip).
-struct DecPosArgs {
-  const int32_t *lens;
-  int32_t *pos, *row_seq, *row_len;
-  int b, s;
-};
 struct EmbedArgs {
   const int32_t *ids;
   const uint16_t *table;
   float *h;
   float *ss;
   int64_t T, V, H;
+  const int32_t *lens;
+  int32_t *pos, *row_seq, *row_len;
+  int s;
 };
 struct InterleaveArgs {
   const float *src;
@@ -267,10 +265,6 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
   Runtime *rt = d->rt;
   const int64_t T = b * s;
   int rc;
-  {
-    DecPosArgs a{d->d_lens, d->pos, d->row_seq, d->row_len, (int)b, (int)s};
-    if ((rc = launch(rt, "rxw8_dec_positions", dim3(blocks(T)), dim3(256), a))) return rc;
-  }
   // Decode-sized steps run the fused schedule, 7 launches per layer: the
   // residual-writing GEMVs (o_proj, down) also emit per-16-channel sums of
   // squares of the new residual rows, from which the next projection (QKV,
@@ -299,8 +293,9 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
                           !(unfused_rope && *unfused_rope == '1');
   {
     const ParamSpec &e = d->p(-1, P_EMBED);
+    // the embedding launch also writes the token positions
     EmbedArgs a{ids, (const uint16_t *)e.bound->ptr, d->h, fused ? d->ss_embed : nullptr, T, d->V,
-                d->H};
+                d->H, d->d_lens, d->pos, d->row_seq, d->row_len, (int)s};
     if ((rc = launch(rt, "rxw8_dec_embed", dim3((unsigned)T), dim3(256), a))) return rc;
   }
   const size_t layer_cache = (size_t)d->Bmax * d->Hkv * d->Lmax * d->D;

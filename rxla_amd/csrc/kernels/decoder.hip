@@ -29,17 +29,30 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_positions(DecPosArgs 
 
 
 // ---- embedding: h[t] = f32(E[clamp(ids[t], 0, V-1)]) (indexing.rs:637-656) ----
+// Also the token positions (when lens is set): token t = (b, i) sits at
+// pos = lens[b] + i, in cache slot b, and sees pos + 1 keys. With ss the
+// row's sum of squares.
 struct EmbedArgs {
   const int32_t *ids;
   const uint16_t *table;  // [V, H] bf16
   float *h;               // [T, H]
   float *ss;              // optional [T]: sum of squares of each written row
   int64_t T, V, H;
+  const int32_t *lens;    // optional [B]: write the positions below
+  int32_t *pos, *row_seq, *row_len;  // [T]
+  int s;                  // tokens per sequence
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_dec_embed(EmbedArgs a) {
   __shared__ float red[4];
   const int64_t t = blockIdx.x;
+  if (a.lens && threadIdx.x == 0) {
+    const int bi = (int)(t / a.s);
+    const int p = a.lens[bi] + (int)(t - (int64_t)bi * a.s);
+    a.pos[t] = p;
+    a.row_seq[t] = bi;
+    a.row_len[t] = p + 1;
+  }
   int64_t id = a.ids[t];
   id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
   const uint16_t *src = a.table + id * a.H;
