@@ -240,7 +240,9 @@ int rxw8_gqa_decode_noalloc(rxw8_runtime *rt, rxw8_buffer *q,
  * F32 softmax) for S new query rows per sequence whose keys and values are
  * already in the cache:
  *   q [B,S,Hq,D] F32|BF16 (token-major, the layout of the projection output);
- *   k_cache/v_cache [B,Hkv,Lmax,D] BF16 with D = 128 and Hq/Hkv in {1,2,4};
+ *   k_cache/v_cache [B,Hkv,Lmax,D] BF16, Hq % Hkv == 0, D <= 512 (D = 128
+ *   with Hq/Hkv in {1,2,4} runs on the matrix-core flash kernel, other
+ *   shapes on the general GQA kernel with f32 probabilities);
  *   starts I32 [B] (device): row i of sequence b sits at position
  *   starts[b] + i and sees keys 0 .. starts[b] + i; entries are clamped by
  *   the kernel into [0, Lmax - S]; S <= Lmax;

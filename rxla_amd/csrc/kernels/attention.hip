@@ -947,12 +947,19 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_decode_generic(AttnGe
 }
 
 // ---- general grouped-query attention (attention.rs:83-135 with SDPA
-// :150-252): q [NB, Hq, Sq, D], k [NB, Hkv, Sk, D], v [NB, Hkv, Sk, Dv], all
-// f32; query head h reads kv head h / (Hq / Hkv); scores q.k * scale + mask,
-// softmax over the Sk keys in f32, out [NB, Hq, Sq, Dv] f32. The additive
-// mask broadcasts to [..., Hq, Sq, Sk]: element (b, h, i, j) sits at
-// moff(b) + h * msh + i * msi + j * msj, where moff sums the batch index's
-// digits (bdim) times their mask strides (0 where the mask broadcasts).
+// :150-252): query row (b, h, i) with i < Sq, keys j < Sk of kv head
+// h / (Hq / Hkv); scores q.k * scale + mask, softmax over the keys in f32,
+// out (b, h, i, :) = sum_j p_j v_j. Element strides (batch b, head, row) for
+// q, out, k and v (rows of D, resp. Dv, contiguous), so one kernel serves
+// head-major [..., H, S, D] tensors and the token-major [B, S, Hq, D] prefill
+// queries over a [B, Hkv, Lmax, D] cache. q, k, v are f32 or bf16 (widened
+// exactly), out f32 or bf16. The additive mask broadcasts to [..., Hq, Sq,
+// Sk]: element (b, h, i, j) sits at moff(b) + h * msh + i * msi + j * msj,
+// moff summing the batch index's digits (bdim) times their mask strides (0
+// where the mask broadcasts). With starts (causal prefill), row i of batch b
+// sees keys 0 .. st + i only, st = clamp(starts[b], 0, Sk - Sq) (the
+// reference's causal mask key_pos <= q_pos for rows at positions st + i;
+// the keys past it are skipped, which adds exactly nothing to the softmax).
 //
 // One wave per output row (b, h, i). The row's q sits in the wave's LDS
 // slice; keys go in chunks of 64 (lane = key: a sequential f32 dot product
@@ -964,19 +971,29 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_decode_generic(AttnGe
 // the whole row; the online form reassociates those sums (f32 rounding
 // differences only).
 struct GqaGeneralArgs {
-  const float *q, *k, *v;
+  const void *q, *k, *v;
   const float *mask;        // or null
-  float *out;
+  void *out;
   int64_t bdim[4];          // batch prefix dims (innermost last), 1 where absent
   int64_t mb[4];            // mask stride of each batch dim (0: broadcast)
   int64_t msh, msi, msj;    // mask strides of head, query, key (0: broadcast)
   int64_t rows;             // NB * Hq * Sq
   int Hq, Hkv, Sq, Sk, D, Dv;
   float scale;
+  int64_t q_sb, q_sh, q_si;  // element strides of q (batch, head, row)
+  int64_t o_sb, o_sh, o_si;  // of out
+  int64_t k_sb, k_sh;        // of k (rows of D), v: v_sb, v_sh (rows of Dv)
+  int64_t v_sb, v_sh;
+  int q_bf16, kv_bf16, out_bf16;
+  const int32_t *starts;     // [NB] causal prefill starts, or null
 };
 
 constexpr int kGqaMaxD = 1024;   // q row staged in LDS
 constexpr int kGqaMaxDv = 512;   // 8 accumulators per lane
+
+__device__ __forceinline__ float gqa_ld(const void *p, int64_t i, int bf16) {
+  return bf16 ? bf16_bits_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+}
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_general(GqaGeneralArgs a) {
   __shared__ float qrow[4][kGqaMaxD];
@@ -988,9 +1005,14 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_general(GqaGeneralArg
   const int h = (int)(bh % a.Hq);
   const int64_t b = bh / a.Hq;
   const int kvh = h / (a.Hq / a.Hkv);
-  const float *qp = a.q + row * a.D;
-  const float *kp = a.k + (b * a.Hkv + kvh) * (int64_t)a.Sk * a.D;
-  const float *vp = a.v + (b * a.Hkv + kvh) * (int64_t)a.Sk * a.Dv;
+  const int64_t qo = b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)i * a.q_si;
+  const int64_t ko = b * a.k_sb + (int64_t)kvh * a.k_sh;
+  const int64_t vo = b * a.v_sb + (int64_t)kvh * a.v_sh;
+  int nkeys = a.Sk;
+  if (a.starts) {
+    const int st = min(max(a.starts[b], 0), a.Sk - a.Sq);
+    nkeys = st + i + 1;
+  }
   const float *mp = nullptr;
   if (a.mask) {
     int64_t off = 0, rest = b;
@@ -1002,7 +1024,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_general(GqaGeneralArg
     mp = a.mask + off + (int64_t)h * a.msh + (int64_t)i * a.msi;
   }
   float *ql = qrow[wv];
-  for (int d = lane; d < a.D; d += 64) ql[d] = qp[d];
+  for (int d = lane; d < a.D; d += 64) ql[d] = gqa_ld(a.q, qo + d, a.q_bf16);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1011,14 +1033,14 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_general(GqaGeneralArg
   float acc[kGqaMaxDv / 64];
 #pragma unroll
   for (int r = 0; r < kGqaMaxDv / 64; ++r) acc[r] = 0.f;
-  for (int c0 = 0; c0 < a.Sk; c0 += 64) {
+  for (int c0 = 0; c0 < nkeys; c0 += 64) {
     const int j = c0 + lane;
-    const bool valid = j < a.Sk;
+    const bool valid = j < nkeys;
     float s = ninf;
     if (valid) {
-      const float *kr = kp + (int64_t)j * a.D;
+      const int64_t kr = ko + (int64_t)j * a.D;
       float dot = 0.f;
-      for (int d = 0; d < a.D; ++d) dot += ql[d] * kr[d];
+      for (int d = 0; d < a.D; ++d) dot += ql[d] * gqa_ld(a.k, kr + d, a.kv_bf16);
       s = dot * a.scale;
       if (mp) s += mp[(int64_t)j * a.msj];
     }
@@ -1031,27 +1053,33 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_general(GqaGeneralArg
     float ps = p;
     for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
     l = l * alpha + ps;
-    const int nk = min(64, a.Sk - c0);
+    const int nk = min(64, nkeys - c0);
 #pragma unroll
     for (int r = 0; r < kGqaMaxDv / 64; ++r) acc[r] *= alpha;
     for (int jj = 0; jj < nk; ++jj) {
       const float pj = __shfl(p, jj);
-      const float *vr = vp + (int64_t)(c0 + jj) * a.Dv;
+      const int64_t vr = vo + (int64_t)(c0 + jj) * a.Dv;
 #pragma unroll
       for (int r = 0; r < kGqaMaxDv / 64; ++r) {
         const int d = lane + 64 * r;
-        if (d < a.Dv) acc[r] += pj * vr[d];
+        if (d < a.Dv) acc[r] += pj * gqa_ld(a.v, vr + d, a.kv_bf16);
       }
     }
     m = m_new;
   }
   // all keys masked: the reference's softmax of an all -inf row is NaN
   const float inv = m == ninf ? __builtin_nanf("") : 1.0f / l;
-  float *op = a.out + row * a.Dv;
+  const int64_t oo = b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)i * a.o_si;
 #pragma unroll
   for (int r = 0; r < kGqaMaxDv / 64; ++r) {
     const int d = lane + 64 * r;
-    if (d < a.Dv) op[d] = m == ninf ? inv : acc[r] * inv;
+    if (d < a.Dv) {
+      const float y = m == ninf ? inv : acc[r] * inv;
+      if (a.out_bf16)
+        ((uint16_t *)a.out)[oo + d] = f32_to_bf16_bits(y);
+      else
+        ((float *)a.out)[oo + d] = y;
+    }
   }
 }
 

@@ -94,15 +94,21 @@ struct QuantizeArgs {
 };
 
 struct GqaGeneralArgs {
-  const float *q, *k, *v;
+  const void *q, *k, *v;
   const float *mask;
-  float *out;
+  void *out;
   int64_t bdim[4];
   int64_t mb[4];
   int64_t msh, msi, msj;
   int64_t rows;
   int Hq, Hkv, Sq, Sk, D, Dv;
   float scale;
+  int64_t q_sb, q_sh, q_si;
+  int64_t o_sb, o_sh, o_si;
+  int64_t k_sb, k_sh;
+  int64_t v_sb, v_sh;
+  int q_bf16, kv_bf16, out_bf16;
+  const int32_t *starts;
 };
 
 struct CausalMaskArgs {
@@ -894,14 +900,51 @@ bool prefill_supported(int64_t Hq, int64_t Hkv, int64_t D, int cache_f32) {
   return !cache_f32 && D == 128 && Hkv > 0 && Hq % Hkv == 0 && (G == 1 || G == 2 || G == 4);
 }
 
+// Causal prefill on the general GQA kernel: q / out element (b, i, h, d) at
+// b*sb + i*ss + h*sh + d, bf16 cache [B, Hkv, Lmax, D], row i of sequence b
+// seeing keys 0 .. clamp(starts[b], 0, Lmax - S) + i. Any head dim up to 512
+// and any group size.
+static int prefill_general(Runtime *rt, const void *q, int q_bf16, int64_t q_sb, int64_t q_ss,
+                           int64_t q_sh, const uint16_t *kc, const uint16_t *vc,
+                           const int32_t *starts, void *out, int out_bf16, int64_t o_sb,
+                           int64_t o_ss, int64_t o_sh, int64_t B, int64_t S, int64_t Hq,
+                           int64_t Hkv, int64_t Lmax, int64_t D, float scale) {
+  if (D > 512) return fail(RXW8_UNIMPLEMENTED, "prefill attention: head dim %lld > 512", (long long)D);
+  GqaGeneralArgs a{};
+  a.q = q, a.k = kc, a.v = vc, a.out = out;
+  for (int t = 0; t < 4; ++t) a.bdim[t] = 1, a.mb[t] = 0;
+  a.bdim[3] = B;
+  a.rows = B * Hq * S;
+  a.Hq = (int)Hq, a.Hkv = (int)Hkv, a.Sq = (int)S, a.Sk = (int)Lmax, a.D = (int)D, a.Dv = (int)D;
+  a.scale = scale;
+  a.q_sb = q_sb, a.q_sh = q_sh, a.q_si = q_ss;
+  a.o_sb = o_sb, a.o_sh = o_sh, a.o_si = o_ss;
+  a.k_sb = a.v_sb = Hkv * Lmax * D;
+  a.k_sh = a.v_sh = Lmax * D;
+  a.q_bf16 = q_bf16, a.kv_bf16 = 1, a.out_bf16 = out_bf16;
+  a.starts = starts;
+  if ((a.rows + 3) / 4 >= ((int64_t)1 << 31))
+    return fail(RXW8_UNIMPLEMENTED, "prefill attention: %lld rows exceed the grid", (long long)a.rows);
+  return launch(rt, "rxw8_gqa_general", dim3((unsigned)((a.rows + 3) / 4)), dim3(256), a);
+}
+
 int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                    const uint16_t *kc, const uint16_t *vc, const int32_t *starts,
                    const int32_t *slots, void *out, int out_f32, int64_t o_sb, int64_t o_ss,
                    int64_t o_sh, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t Lmax,
                    float scale) {
   if (B == 0 || S == 0) return RXW8_OK;
-  if (!prefill_supported(Hq, Hkv, 128, 0) || S > Lmax)
-    return fail(RXW8_UNIMPLEMENTED, "prefill attention: needs D = 128, Hq/Hkv in {1,2,4}, S <= Lmax");
+  if (S > Lmax) return fail(RXW8_INVALID_ARGUMENT, "prefill attention: S %lld > Lmax %lld",
+                            (long long)S, (long long)Lmax);
+  if (!prefill_supported(Hq, Hkv, 128, 0)) {
+    // other group sizes: the general GQA kernel with the same causal-from-
+    // starts rule (one wave per query row; D = 128 here)
+    if (slots || Hkv <= 0 || Hq % Hkv)
+      return fail(RXW8_UNIMPLEMENTED, "prefill attention: no kernel for Hq=%lld Hkv=%lld",
+                  (long long)Hq, (long long)Hkv);
+    return prefill_general(rt, q, !q_f32, q_sb, q_ss, q_sh, kc, vc, starts, out, !out_f32, o_sb,
+                           o_ss, o_sh, B, S, Hq, Hkv, Lmax, 128, scale);
+  }
   PrefillArgs a;
   a.q = q;
   a.kc = kc;
@@ -1146,8 +1189,10 @@ static int check_prefill(const Buffer *q, const Buffer *k, const Buffer *v, cons
   const int64_t B = q->dims[0], S = q->dims[1], Hq = q->dims[2], D = q->dims[3];
   if (k->dims[0] != B || k->dims[3] != D || S < 1 || S > k->dims[2])
     return fail(RXW8_INVALID_ARGUMENT, "GQA prefill: batch/dim mismatch or S outside [1, Lmax]");
-  if (!prefill_supported(Hq, k->dims[1], D, 0))
-    return fail(RXW8_UNIMPLEMENTED, "GQA prefill: needs D = 128 and Hq/Hkv in {1, 2, 4}");
+  if (Hq <= 0 || k->dims[1] <= 0 || Hq % k->dims[1] != 0)
+    return fail(RXW8_INVALID_ARGUMENT,
+                "GQA requires equal batch prefixes and divisible positive head counts");
+  if (D > 512) return fail(RXW8_UNIMPLEMENTED, "GQA prefill: head dim %lld > 512", (long long)D);
   if (starts->dtype != RXW8_I32 || starts->rank != 1 || starts->dims[0] != B)
     return fail(RXW8_INVALID_ARGUMENT, "GQA prefill: starts must be I32 [B]");
   return RXW8_OK;
@@ -1237,10 +1282,15 @@ int rxw8_gqa_attention_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k, rx
     return fail(RXW8_UNIMPLEMENTED,
                 "GQA: supported up to 4 batch dimensions, depth 1024 and value depth 512");
   GqaGeneralArgs a{};
-  a.q = (const float *)q->ptr;
-  a.k = (const float *)k->ptr;
-  a.v = (const float *)v->ptr;
-  a.out = (float *)out->ptr;
+  a.q = q->ptr;
+  a.k = k->ptr;
+  a.v = v->ptr;
+  a.out = out->ptr;
+  // contiguous [NB, H, S, D] operands
+  a.q_si = D, a.q_sh = Sq * D, a.q_sb = Hq * Sq * D;
+  a.o_si = Dv, a.o_sh = Sq * Dv, a.o_sb = Hq * Sq * Dv;
+  a.k_sh = Sk * D, a.k_sb = Hkv * Sk * D;
+  a.v_sh = Sk * Dv, a.v_sb = Hkv * Sk * Dv;
   for (int t = 0; t < 4; ++t) a.bdim[t] = 1, a.mb[t] = 0;
   int64_t NB = 1;
   for (int i = 0; i < hd; ++i) {
@@ -1372,6 +1422,12 @@ int rxw8_gqa_prefill_into(rxw8_runtime *rt, rxw8_buffer *q, rxw8_buffer *k_cache
   const int64_t B = q->dims[0], S = q->dims[1], Hq = q->dims[2], D = q->dims[3];
   if (scale <= 0.f) scale = 1.0f / std::sqrt((float)D);
   std::lock_guard<std::recursive_mutex> g(rt->mu);
+  if (!prefill_supported(Hq, k_cache->dims[1], D, 0))
+    return prefill_general(rt, q->ptr, q->dtype != RXW8_F32, S * Hq * D, Hq * D, D,
+                           (const uint16_t *)k_cache->ptr, (const uint16_t *)v_cache->ptr,
+                           (const int32_t *)starts->ptr, out->ptr, out->dtype != RXW8_F32,
+                           S * Hq * D, Hq * D, D, B, S, Hq, k_cache->dims[1], k_cache->dims[2], D,
+                           scale);
   return prefill_launch(rt, q->ptr, q->dtype == RXW8_F32, S * Hq * D, Hq * D, D,
                         (const uint16_t *)k_cache->ptr, (const uint16_t *)v_cache->ptr,
                         (const int32_t *)starts->ptr, nullptr, out->ptr, out->dtype == RXW8_F32,

@@ -115,18 +115,38 @@ def test_prefill_starts_are_clamped(rt):
     assert rel_err(out, ref) <= TIGHT
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(16, 2, 128), (8, 1, 64), (6, 3, 96), (4, 4, 256),
+                                       (5, 1, 32)])
+def test_any_group_and_head_dim(rt, hq, hkv, d):
+    """Group sizes and head dims outside the MFMA kernel (D = 128, Hq/Hkv in
+    {1, 2, 4}) run on the general GQA kernel with the same causal-from-starts
+    rule: f32 scores and probabilities, so it matches the f32 oracle closely."""
+    rng = np.random.default_rng(hq * 100 + d)
+    s, lmax = 37, 150
+    q, kc, vc = make(rng, 2, s, hq, hkv, lmax, d=d)
+    starts = [0, 90]
+    out = run_prefill(rt, q, kc, vc, starts)
+    ref = oracle_prefill(q, kc, vc, np.array(starts))
+    err = rel_err(out, ref)
+    print(f"prefill Hq={hq} Hkv={hkv} D={d}: rel_err {err:.2e}")
+    assert err <= 1e-5
+    out16 = run_prefill(rt, q, kc, vc, [500, -3], out_bf16=True, q_bf16=True)  # clamped starts
+    ref16 = oracle_prefill(oracle.round_bf16(q), kc, vc, np.array([lmax - s, 0]))
+    assert rel_err(out16, ref16) <= TIGHT
+
+
 def test_prefill_errors(rt):
     r = rx()
     rng = np.random.default_rng(9)
-    q, kc, vc = make(rng, 2, 8, 16, 2, 64)  # group 8: not supported by this kernel
-    with pytest.raises(r.Error) as e:
-        run_prefill(rt, q, kc, vc, [0, 0])
-    assert e.value.code == r.Status.UNIMPLEMENTED
     q, kc, vc = make(rng, 2, 80, 4, 2, 64)  # S > Lmax
     with pytest.raises(r.Error) as e:
         run_prefill(rt, q, kc, vc, [0, 0])
     assert e.value.code == r.Status.INVALID_ARGUMENT
-    q, kc, vc = make(rng, 2, 8, 4, 2, 64, d=64)  # D != 128
+    q, kc, vc = make(rng, 2, 8, 6, 4, 64)  # 6 query heads over 4 kv heads
     with pytest.raises(r.Error) as e:
         run_prefill(rt, q, kc, vc, [0, 0])
+    assert e.value.code == r.Status.INVALID_ARGUMENT
+    q, kc, vc = make(rng, 1, 8, 2, 1, 64, d=640)  # head dim beyond the general kernel
+    with pytest.raises(r.Error) as e:
+        run_prefill(rt, q, kc, vc, [0])
     assert e.value.code == r.Status.UNIMPLEMENTED
