@@ -83,12 +83,13 @@ namespace {
 
 constexpr int kXPad = 8;  // bf16 elements of padding per staged activation row
 
-// Returns the squared norm of the updated residual values (y_mode 1), else 0.
+// Returns the squared norm of the updated residual values (y_mode 1, with h0
+// the residual values loaded earlier), else 0.
 __device__ __forceinline__ float store_out(void *y, int y_f32, int y_mode, int64_t N, int b, int n,
-                                           f32x4 v) {
+                                           f32x4 v, float4 h0) {
   if (y_mode == 1) {  // residual: h += f32(bf16(result)) (layers.rs:295-296 + add)
     float4 *h = (float4 *)((float *)y + (int64_t)b * N + n);
-    float4 o = *h;
+    float4 o = h0;
     o.x += round_bf16(v[0]);
     o.y += round_bf16(v[1]);
     o.z += round_bf16(v[2]);
@@ -105,24 +106,136 @@ __device__ __forceinline__ float store_out(void *y, int y_f32, int y_mode, int64
   return 0.f;
 }
 
+// 16-byte bf16 pieces per thread whose global loads the staging loops issue
+// before storing any of them: one round trip per batch (a load-then-store loop
+// waits for every load in turn). Sized so staging needs no more registers than
+// the streaming loop (every path's peak sets the kernel's occupancy).
+constexpr int kStageBatch = 4;
+
+// Copy rows [0, M) x pieces [0, per_row) of 8 activations (row m at x + m *
+// stride + off; bf16, or f32 rounded to bf16) into LDS rows of stride ld.
+// The caller's thread t0 of nt takes pieces t0, t0 + nt, ..., loading
+// kStageBatch (f32: half as many) of them before storing any.
+__device__ __forceinline__ void stage_rows(const void *x, bool x_f32, int64_t stride, int64_t off,
+                                           int M, int per_row, uint16_t *dst, int ld, int t0, int nt) {
+  const int total = M * per_row;
+  if (x_f32) {
+    constexpr int SB = kStageBatch / 2;
+    for (int i0 = t0; i0 < total; i0 += SB * nt) {
+      float4 v[SB][2];
+#pragma unroll
+      for (int s = 0; s < SB; ++s) {
+        const int i = i0 + s * nt;
+        if (i < total) {
+          const int b = i / per_row, kk = (i - b * per_row) * 8;
+          const float4 *p = (const float4 *)((const float *)x + b * stride + off + kk);
+          v[s][0] = p[0];
+          v[s][1] = p[1];
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < SB; ++s) {
+        const int i = i0 + s * nt;
+        if (i < total) {
+          const int b = i / per_row, kk = (i - b * per_row) * 8;
+          u32x4 r;
+          r[0] = pack_bf16x2(v[s][0].x, v[s][0].y);
+          r[1] = pack_bf16x2(v[s][0].z, v[s][0].w);
+          r[2] = pack_bf16x2(v[s][1].x, v[s][1].y);
+          r[3] = pack_bf16x2(v[s][1].z, v[s][1].w);
+          *(u32x4 *)(dst + b * ld + kk) = r;
+        }
+      }
+    }
+    return;
+  }
+  constexpr int SB = kStageBatch;
+  for (int i0 = t0; i0 < total; i0 += SB * nt) {
+    u32x4 v[SB];
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+      const int i = i0 + s * nt;
+      if (i < total) {
+        const int b = i / per_row, kk = (i - b * per_row) * 8;
+        v[s] = *(const u32x4 *)((const uint16_t *)x + b * stride + off + kk);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+      const int i = i0 + s * nt;
+      if (i < total) {
+        const int b = i / per_row, kk = (i - b * per_row) * 8;
+        *(u32x4 *)(dst + b * ld + kk) = v[s];
+      }
+    }
+  }
+}
+
 // Stage x[0:M, k0:k0+Kc] as bf16 into LDS rows of stride Kc + kXPad, applying
 // the activation prologue (x_mode). Mode 1 sums each full row first with the
 // same thread stride and block reduction as rxw8_dec_rmsnorm, so the staged
-// bits equal that kernel's output.
+// bits equal that kernel's output. Row pieces of the norm modes are staged one
+// per round trip (a piece pairs 8 row values with 8 norm weights; a batch of
+// them would raise the kernel's register peak).
 __device__ __forceinline__ void stage_x(const GemvArgs &a, uint16_t *xs, int k0, int Kc) {
   const int ldx = Kc + kXPad;
   const int per_row = Kc / 8;
   const int total = a.M * per_row;
+  const int nt = blockDim.x;
   if (a.x_mode == 1 || a.x_mode == 3) {
     __shared__ float red[4];
     __shared__ float row_scale[32];
+    constexpr int SB = 1;
+    float4 hv[SB][2], wv[SB][2];
+    auto fetch = [&](int i0) {
+#pragma unroll
+      for (int s = 0; s < SB; ++s) {
+        const int i = i0 + s * nt;
+        if (i < total) {
+          const int b = i / per_row, kk = (i - b * per_row) * 8;
+          const float *h = (const float *)a.x + b * a.x_stride + a.x_off + k0 + kk;
+          hv[s][0] = *(const float4 *)h;
+          hv[s][1] = *(const float4 *)(h + 4);
+          wv[s][0] = *(const float4 *)(a.norm_w + k0 + kk);
+          wv[s][1] = *(const float4 *)(a.norm_w + k0 + kk + 4);
+        }
+      }
+    };
+    auto put = [&](int i0) {
+#pragma unroll
+      for (int s = 0; s < SB; ++s) {
+        const int i = i0 + s * nt;
+        if (i < total) {
+          const int b = i / per_row, kk = (i - b * per_row) * 8;
+          const float sc = row_scale[b];
+          const float4 h0 = hv[s][0], h1 = hv[s][1], w0 = wv[s][0], w1 = wv[s][1];
+          u32x4 v;
+          v[0] = pack_bf16x2((h0.x * sc) * w0.x, (h0.y * sc) * w0.y);
+          v[1] = pack_bf16x2((h0.z * sc) * w0.z, (h0.w * sc) * w0.w);
+          v[2] = pack_bf16x2((h1.x * sc) * w1.x, (h1.y * sc) * w1.y);
+          v[3] = pack_bf16x2((h1.z * sc) * w1.z, (h1.w * sc) * w1.w);
+          *(u32x4 *)(xs + b * ldx + kk) = v;
+        }
+      }
+    };
     if (a.x_mode == 3) {
       // sums of squares from the producer's partials: one wave per row, lane
-      // l adds partials l, l + 64, ..., then a fixed butterfly (deterministic)
-      const int lane = threadIdx.x & 63, nwaves = blockDim.x >> 6;
+      // l adds partials l, l + 64, ... in that order (loads issued in batches
+      // of 4), then a fixed butterfly (deterministic)
+      const int lane = threadIdx.x & 63, nwaves = nt >> 6;
       for (int b = threadIdx.x >> 6; b < a.M; b += nwaves) {
         float ss = 0.f;
-        for (int p = lane; p < a.ss_parts; p += 64) ss += a.ss_in[(int64_t)p * a.M + b];
+        for (int p0 = lane; p0 < a.ss_parts; p0 += 256) {
+          float t[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int p = p0 + 64 * s;
+            t[s] = p < a.ss_parts ? a.ss_in[(int64_t)p * a.M + b] : 0.f;
+          }
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            if (p0 + 64 * s < a.ss_parts) ss += t[s];
+        }
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
         if (lane == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
       }
@@ -130,49 +243,51 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, uint16_t *xs, int k0,
       for (int b = 0; b < a.M; ++b) {
         const float *h = (const float *)a.x + b * a.x_stride + a.x_off;
         float ss = 0.f;
-        for (int i = threadIdx.x; i < a.K; i += blockDim.x) ss += h[i] * h[i];
+        for (int i = threadIdx.x; i < a.K; i += nt) ss += h[i] * h[i];
         ss = block_sum_256(ss, red);
         if (threadIdx.x == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
       }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < total; i += blockDim.x) {
-      const int b = i / per_row, kk = (i - b * per_row) * 8;
-      const float *h = (const float *)a.x + b * a.x_stride + a.x_off + k0 + kk;
-      const float sc = row_scale[b];
-      const float4 h0 = *(const float4 *)h, h1 = *(const float4 *)(h + 4);
-      const float4 w0 = *(const float4 *)(a.norm_w + k0 + kk), w1 = *(const float4 *)(a.norm_w + k0 + kk + 4);
-      u32x4 v;
-      v[0] = pack_bf16x2((h0.x * sc) * w0.x, (h0.y * sc) * w0.y);
-      v[1] = pack_bf16x2((h0.z * sc) * w0.z, (h0.w * sc) * w0.w);
-      v[2] = pack_bf16x2((h1.x * sc) * w1.x, (h1.y * sc) * w1.y);
-      v[3] = pack_bf16x2((h1.z * sc) * w1.z, (h1.w * sc) * w1.w);
-      *(u32x4 *)(xs + b * ldx + kk) = v;
+    for (int i0 = threadIdx.x; i0 < total; i0 += SB * nt) {
+      fetch(i0);
+      put(i0);
     }
     return;
   }
   if (a.x_mode == 2) {
-    for (int i = threadIdx.x; i < total; i += blockDim.x) {
-      const int b = i / per_row, kk = (i - b * per_row) * 8;
-      const uint16_t *row = (const uint16_t *)a.x + b * a.x_stride;
-      const u32x4 g8 = *(const u32x4 *)(row + k0 + kk);
-      const u32x4 u8_ = *(const u32x4 *)(row + a.K + k0 + kk);
-      u32x4 v;
+    constexpr int SB = kStageBatch / 2;
+    for (int i0 = threadIdx.x; i0 < total; i0 += SB * nt) {
+      u32x4 gv[SB], uv[SB];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float g0 = bf16_bits_to_f32(g8[e] & 0xffffu), g1 = bf16_bits_to_f32(g8[e] >> 16);
-        const float u0 = bf16_bits_to_f32(u8_[e] & 0xffffu), u1 = bf16_bits_to_f32(u8_[e] >> 16);
-        v[e] = pack_bf16x2(silu_mul_f32(g0, u0), silu_mul_f32(g1, u1));
+      for (int s = 0; s < SB; ++s) {
+        const int i = i0 + s * nt;
+        if (i < total) {
+          const int b = i / per_row, kk = (i - b * per_row) * 8;
+          const uint16_t *row = (const uint16_t *)a.x + b * a.x_stride;
+          gv[s] = *(const u32x4 *)(row + k0 + kk);
+          uv[s] = *(const u32x4 *)(row + a.K + k0 + kk);
+        }
       }
-      *(u32x4 *)(xs + b * ldx + kk) = v;
+#pragma unroll
+      for (int s = 0; s < SB; ++s) {
+        const int i = i0 + s * nt;
+        if (i < total) {
+          const int b = i / per_row, kk = (i - b * per_row) * 8;
+          u32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float g0 = bf16_bits_to_f32(gv[s][e] & 0xffffu), g1 = bf16_bits_to_f32(gv[s][e] >> 16);
+            const float u0 = bf16_bits_to_f32(uv[s][e] & 0xffffu), u1 = bf16_bits_to_f32(uv[s][e] >> 16);
+            v[e] = pack_bf16x2(silu_mul_f32(g0, u0), silu_mul_f32(g1, u1));
+          }
+          *(u32x4 *)(xs + b * ldx + kk) = v;
+        }
+      }
     }
     return;
   }
-  for (int i = threadIdx.x; i < total; i += blockDim.x) {
-    const int b = i / per_row, kk = (i - b * per_row) * 8;
-    const int64_t off = (int64_t)b * a.x_stride + a.x_off + k0 + kk;
-    *(u32x4 *)(xs + b * ldx + kk) = load_x8(a.x, off, a.x_f32 != 0);
-  }
+  stage_rows(a.x, a.x_f32 != 0, a.x_stride, a.x_off + k0, a.M, per_row, xs, ldx, threadIdx.x, nt);
 }
 
 // Reduce the KW k-slices of each row group through LDS (slice order), then
@@ -237,7 +352,10 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int b = col + 16 * mb;
-    float ss = b < a.M ? store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, total[mb] * sc) : 0.f;
+    float ss = b < a.M ? store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, total[mb] * sc,
+                                   a.y_mode == 1 ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
+                                                 : float4{0.f, 0.f, 0.f, 0.f})
+                       : 0.f;
     if (a.ss_out) {  // 4 lanes (j) hold the group's 16 channels of row b
       ss += __shfl_xor(ss, 16);
       ss += __shfl_xor(ss, 32);
@@ -336,13 +454,9 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   if (XG) {
     // nothing to stage: per-channel scales are read in the epilogue
   } else if (wave_stage) {
-    const int pieces = Kw / 8;  // 8 values per 16-byte piece
     uint16_t *xw = xs + wave * a.M * (Kw + kXPad);
-    for (int i = lane; i < a.M * pieces; i += 64) {
-      const int b = i / pieces, p = i - b * pieces;
-      *(u32x4 *)(xw + b * (Kw + kXPad) + 8 * p) =
-          load_x8(a.x, (int64_t)b * a.x_stride + a.x_off + k0 + kbase + 8 * p, a.x_f32 != 0);
-    }
+    stage_rows(a.x, a.x_f32 != 0, a.x_stride, a.x_off + k0 + kbase, a.M, Kw / 8, xw, Kw + kXPad,
+               lane, 64);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -508,16 +622,22 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(Splitk
        qd += (int64_t)gridDim.x * blockDim.x) {
     const int64_t e = qd * 4;
     const int b = (int)(e / a.N), n = (int)(e - (int64_t)b * a.N);
+    // residual and scale loads go out with the first batch of partials
+    const float4 h0 = a.y_mode == 1 ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
+                                    : float4{0.f, 0.f, 0.f, 0.f};
+    const float4 s4 = a.scale ? *(const float4 *)(a.scale + n) : float4{1.f, 1.f, 1.f, 1.f};
     f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.ksplit; ++s) {
-      const float4 p = *(const float4 *)(a.ws + ((int64_t)s * a.M + b) * a.N + n);
-      sum += f32x4{p.x, p.y, p.z, p.w};
+    for (int s0 = 0; s0 < a.ksplit; s0 += 4) {  // 4 partial loads in flight, summed in split order
+      float4 p[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (s0 + t < a.ksplit) p[t] = *(const float4 *)(a.ws + ((int64_t)(s0 + t) * a.M + b) * a.N + n);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (s0 + t < a.ksplit) sum += f32x4{p[t].x, p[t].y, p[t].z, p[t].w};
     }
-    if (a.scale) {
-      const float4 s4 = *(const float4 *)(a.scale + n);
-      sum *= f32x4{s4.x, s4.y, s4.z, s4.w};
-    }
-    store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, sum);
+    if (a.scale) sum *= f32x4{s4.x, s4.y, s4.z, s4.w};
+    store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, sum, h0);
   }
 }
 
