@@ -117,6 +117,11 @@ struct ArgmaxFinalArgs {
   int32_t *rec_out;
   int32_t *rec_step;
   int rows, chunks, s, ncols;
+  const uint16_t *table = nullptr;  // optional: embed the winners (generate)
+  float *h = nullptr;
+  float *ss = nullptr;
+  int32_t *pos = nullptr, *row_seq = nullptr, *row_len = nullptr;
+  int64_t V = 0, H = 0;
 };
 struct RecordArgs {
   const int32_t *next;
@@ -260,8 +265,13 @@ static unsigned blocks(int64_t n, int per = 256) { return (unsigned)std::max<int
 // Enqueue one forward pass over ids[b, s] (device) starting at the current
 // lengths; writes next ids and logits of the last position; advances lengths.
 // rec (generate): also store the chosen ids in column *rec->step of rec->out.
+// embedded: h, the positions and (fused) ss_embed already hold this step's
+// input rows -- written by the previous step's argmax launch, which embeds
+// its winners when embed_next is set (generate's decode steps: ids == next,
+// s == 1 for the following step).
 static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
-                           const RecordArgs *rec = nullptr) {
+                           const RecordArgs *rec = nullptr, bool embedded = false,
+                           bool embed_next = false) {
   Runtime *rt = d->rt;
   const int64_t T = b * s;
   int rc;
@@ -291,7 +301,7 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
                           (d->Hq / d->Hkv == 1 || d->Hq / d->Hkv == 2 || d->Hq / d->Hkv == 4 ||
                            d->Hq / d->Hkv == 8) &&
                           !(unfused_rope && *unfused_rope == '1');
-  {
+  if (!embedded) {
     const ParamSpec &e = d->p(-1, P_EMBED);
     // the embedding launch also writes the token positions
     EmbedArgs a{ids, (const uint16_t *)e.bound->ptr, d->h, fused ? d->ss_embed : nullptr, T, d->V,
@@ -409,17 +419,14 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
       return rc;
   }
   // final norm on the last position of each sequence, tied bf16 lm_head, argmax
+  const ParamSpec &e = d->p(-1, P_EMBED);
+  const bool pk = e.packed != nullptr;
+  const uint16_t *ew = (const uint16_t *)(pk ? e.packed->ptr : e.bound->ptr);
+  const float *final_norm = (const float *)d->p(-1, P_FINAL_NORM).bound->ptr;
   {
-    RmsNormArgs a{d->h, (const float *)d->p(-1, P_FINAL_NORM).bound->ptr, d->xl, nullptr, d->H,
-                  (int)b, (int)s, (int)s - 1, d->cfg.eps};
+    RmsNormArgs a{d->h, final_norm, d->xl, nullptr, d->H, (int)b, (int)s, (int)s - 1, d->cfg.eps};
     if ((rc = launch(rt, "rxw8_dec_rmsnorm", dim3((unsigned)b), dim3(256), a))) return rc;
-  }
-  {
-    const ParamSpec &e = d->p(-1, P_EMBED);
-    const bool pk = e.packed != nullptr;
-    if ((rc = bf16_linear_launch(rt, d->xl, 0, (const uint16_t *)(pk ? e.packed->ptr : e.bound->ptr),
-                                 pk, d->logits, 1, b, d->V, d->H)))
-      return rc;
+    if ((rc = bf16_linear_launch(rt, d->xl, 0, ew, pk, d->logits, 1, b, d->V, d->H))) return rc;
   }
   {
     ArgmaxArgs a{d->logits, d->am_val, d->am_idx, d->next, d->V, (int)b, d->am_chunks, 1};
@@ -427,7 +434,14 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
       return rc;
     ArgmaxFinalArgs f{d->am_val, d->am_idx, d->next, d->d_lens, rec ? rec->out : nullptr,
                       rec ? rec->step : nullptr, (int)b, d->am_chunks, (int)s, rec ? rec->ncols : 0};
-    const unsigned threads = 64u * (unsigned)std::min<int64_t>(b, 16);
+    unsigned threads = 64u * (unsigned)std::min<int64_t>(b, 16);
+    if (embed_next) {
+      // the next step's input rows (its fused QKV prologue reads ss_embed,
+      // sized for the 32 rows a fused step takes)
+      f.table = (const uint16_t *)e.bound->ptr, f.h = d->h, f.ss = b <= 32 ? d->ss_embed : nullptr;
+      f.pos = d->pos, f.row_seq = d->row_seq, f.row_len = d->row_len, f.V = d->V, f.H = d->H;
+      threads = 1024;
+    }
     if ((rc = launch(rt, "rxw8_dec_argmax_final", dim3(1), dim3(threads), f))) return rc;
   }
   return RXW8_OK;
@@ -745,11 +759,14 @@ int rxw8_decoder_generate(rxw8_decoder *d, rxw8_buffer *prompt, int64_t b, int64
   if ((rc = ensure_activations(d, b * s))) return rc;
   RXW8_HIP(hipMemsetAsync(d->d_step, 0, 4, rt->stream));
   RecordArgs rec{d->next, (int32_t *)out_ids->ptr, d->d_step, (int)b, (int)(steps + 1)};
-  if ((rc = enqueue_forward(d, (const int32_t *)prompt->ptr, b, s, &rec))) return rc;
+  // With decode steps to follow, every forward's argmax launch also embeds
+  // its winners as the next step's input rows (one launch fewer per step).
+  if ((rc = enqueue_forward(d, (const int32_t *)prompt->ptr, b, s, &rec, false, steps > 0)))
+    return rc;
   for (int64_t i = 0; i < b; ++i) d->h_lens[(size_t)i] += (int32_t)s;
   if (steps == 0) return RXW8_OK;
-  // One decode step: consume the previous argmax (d->next) as the ids.
-  auto step = [&]() -> int { return enqueue_forward(d, d->next, b, 1, &rec); };
+  // One decode step: its input rows (the previous argmax, d->next) are embedded.
+  auto step = [&]() -> int { return enqueue_forward(d, d->next, b, 1, &rec, true, true); };
   int64_t done = 0;
   if (use_graph) {
     // A captured step holds the batch, the out_ids row stride (steps + 1) and

@@ -32,6 +32,47 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_positions(DecPosArgs 
 // Also the token positions (when lens is set): token t = (b, i) sits at
 // pos = lens[b] + i, in cache slot b, and sees pos + 1 keys. With ss the
 // row's sum of squares.
+//
+// One row by a 256-thread slice (thread t of it): with H % 8 == 0 (and
+// 16-byte aligned rows), 16-byte
+// pieces p = t, t + 256, ... of 8 values (loads issued 4 at a time), each
+// thread summing its squares in element order; otherwise elements t, t + 256,
+// .... Returns the thread's partial sum (the caller adds the slice's partials
+// in block_sum_256 order).
+__device__ __forceinline__ float embed_row(const uint16_t *src, float *dst, int64_t H, int t) {
+  float ss = 0.f;
+  if (H % 8 || ((uintptr_t)src | (uintptr_t)dst) % 16) {
+    for (int64_t i = t; i < H; i += 256) {
+      const float v = bf16_bits_to_f32(src[i]);
+      dst[i] = v;
+      ss += v * v;
+    }
+    return ss;
+  }
+  const int64_t pieces = H / 8;
+  for (int64_t p0 = t; p0 < pieces; p0 += 4 * 256) {
+    u32x4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (p0 + 256 * q < pieces) v[q] = *(const u32x4 *)(src + 8 * (p0 + 256 * q));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (p0 + 256 * q >= pieces) break;
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[2 * e] = bf16_bits_to_f32(v[q][e] & 0xffffu);
+        f[2 * e + 1] = bf16_bits_to_f32(v[q][e] >> 16);
+      }
+      float4 *d = (float4 *)(dst + 8 * (p0 + 256 * q));
+      d[0] = float4{f[0], f[1], f[2], f[3]};
+      d[1] = float4{f[4], f[5], f[6], f[7]};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+    }
+  }
+  return ss;
+}
 struct EmbedArgs {
   const int32_t *ids;
   const uint16_t *table;  // [V, H] bf16
@@ -55,14 +96,7 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_embed(EmbedArgs a) {
   }
   int64_t id = a.ids[t];
   id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
-  const uint16_t *src = a.table + id * a.H;
-  float *dst = a.h + t * a.H;
-  float ss = 0.f;
-  for (int64_t i = threadIdx.x; i < a.H; i += blockDim.x) {
-    const float v = bf16_bits_to_f32(src[i]);
-    dst[i] = v;
-    ss += v * v;
-  }
+  float ss = embed_row(a.table + id * a.H, a.h + t * a.H, a.H, threadIdx.x);
   if (a.ss) {
     ss = block_sum_256(ss, red);
     if (threadIdx.x == 0) a.ss[t] = ss;
@@ -363,7 +397,12 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_argmax_partial(Argmax
 // am_better is a total order, so the butterfly returns the same winner as a
 // sequential scan), writes next[r] and advances lens[r] by s; with `rec_out`
 // (generate) it also stores next[r] in column *step of rec_out and then
-// advances *step. One workgroup of 64 * min(rows, 16) threads.
+// advances *step. With `table` (generate) it then does the work of the next
+// single-token step's rxw8_dec_embed: row r of h = f32(E[next[r]]) with its
+// sum of squares (each 256-thread slice of the workgroup takes one row through
+// embed_row, as that kernel does, so the bits agree) and the positions
+// pos[r] = lens[r], row_seq[r] = r, row_len[r] = lens[r] + 1. One workgroup
+// of 64 * min(rows, 16) threads, or 1024 with `table`.
 struct ArgmaxFinalArgs {
   const float *pval;  // [rows, chunks]
   const int32_t *pidx;
@@ -372,6 +411,11 @@ struct ArgmaxFinalArgs {
   int32_t *rec_out;   // optional [rows, ncols]
   int32_t *rec_step;  // device column counter (with rec_out)
   int rows, chunks, s, ncols;
+  const uint16_t *table;  // optional [V, H] bf16 embedding (needs lens)
+  float *h;               // [rows, H]
+  float *ss;              // optional [rows]
+  int32_t *pos, *row_seq, *row_len;  // [rows]
+  int64_t V, H;
 };
 
 extern "C" __global__ void __launch_bounds__(1024) rxw8_dec_argmax_final(ArgmaxFinalArgs a) {
@@ -403,5 +447,30 @@ extern "C" __global__ void __launch_bounds__(1024) rxw8_dec_argmax_final(ArgmaxF
   }
   __syncthreads();
   if (a.rec_out && threadIdx.x == 0) *a.rec_step = col + 1;
+  if (!a.table) return;
+  __shared__ float red[16];
+  const int groups = blockDim.x >> 8, g = threadIdx.x >> 8, t = threadIdx.x & 255;
+  for (int r0 = 0; r0 < a.rows; r0 += groups) {  // uniform trip count (barriers inside)
+    const int r = r0 + g;
+    float ss = 0.f;
+    if (r < a.rows) {
+      int64_t id = a.next[r];
+      id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
+      ss = embed_row(a.table + id * a.H, a.h + (int64_t)r * a.H, a.H, t);
+      if (t == 0) {
+        const int p = a.lens[r];
+        a.pos[r] = p;
+        a.row_seq[r] = r;
+        a.row_len[r] = p + 1;
+      }
+    }
+    // block_sum_256 of the slice: wave butterfly, then its 4 wave sums in order
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    __syncthreads();
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    if (a.ss && r < a.rows && t == 0)
+      a.ss[r] = (red[4 * g] + red[4 * g + 1]) + (red[4 * g + 2] + red[4 * g + 3]);
+  }
 }
 
