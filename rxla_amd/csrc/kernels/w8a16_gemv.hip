@@ -68,6 +68,11 @@ struct GemvArgs {
   // own K slice of the rows in an LDS region of its own and starts without a
   // workgroup barrier (host-chosen; the LDS holds NW regions of M rows)
   int wave_stage;
+  // bf16 rows (x_mode 0, Kc % 512 == 0, 16-byte aligned; host-checked) are
+  // staged by LDS DMA: global_load_lds_dwordx4 copies 16 bytes per lane
+  // straight into LDS -- no registers, every copy of the workgroup in flight
+  // at once
+  int lds_dma;
 };
 
 struct SplitkReduceArgs {
@@ -171,6 +176,15 @@ __device__ __forceinline__ void stage_rows(const void *x, bool x_f32, int64_t st
   }
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One LDS DMA instruction of the wave: lane l copies 16 bytes from g (its own
+// address) to LDS at l_base + 16 l (l_base wave-uniform). Completion is
+// counted by vmcnt.
+__device__ __forceinline__ void lds_dma16(const void *g, void *l_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void *)l_base, 16, 0, 0);
+}
+
 // Stage x[0:M, k0:k0+Kc] as bf16 into LDS rows of stride Kc + kXPad, applying
 // the activation prologue (x_mode). Mode 1 sums each full row first with the
 // same thread stride and block reduction as rxw8_dec_rmsnorm, so the staged
@@ -182,6 +196,16 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, uint16_t *xs, int k0,
   const int per_row = Kc / 8;
   const int total = a.M * per_row;
   const int nt = blockDim.x;
+  if (a.lds_dma) {  // x_mode 0 bf16 rows: one instruction = 64 pieces of one row
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = nt >> 6;
+    for (int t = wave; t < total / 64; t += nwaves) {
+      const int q0 = 64 * t, b = q0 / per_row, kk0 = (q0 - b * per_row) * 8;
+      lds_dma16((const uint16_t *)a.x + b * a.x_stride + a.x_off + k0 + kk0 + 8 * lane,
+                xs + b * ldx + kk0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the caller's barrier publishes the rows
+    return;
+  }
   if (a.x_mode == 1 || a.x_mode == 3) {
     __shared__ float red[4];
     __shared__ float row_scale[32];
