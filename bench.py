@@ -10,7 +10,10 @@ Every launch reads its own copy of the int8 weights (copies rotate,
 weight bytes and the figure is HBM bandwidth.
 
 value        = sweep algorithmic bytes / wall time of the timed steps (GB/s);
-               each step is one HIP-graph replay of the 9 launches
+               each step is the 9 launches, replayed from HIP graphs that
+               hold one step per weight copy in turn (a graph boundary idles
+               the GPU for ~8 us; the remainder of K steps replays one-step
+               graphs)
 roofline     = the GEMV kernel of the largest sweep shape, B=1 N=24576
                (rxw8_gemv_w8_pk_mb1_rw3_u4_w12: 12 waves, 48-row tiles, 512
                workgroups = 2 whole rounds): algorithmic bytes per launch /
@@ -528,7 +531,7 @@ def pmc_probe(kind, rounds=3):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--copies", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -596,20 +599,39 @@ def main():
                 e1.record(stream)
                 events.append((b, n, e0, e1))
 
-    # Eager warmup (sizes workspaces, resolves kernels), then one HIP graph per
-    # weight copy holding the 9 launches of a step.
+    # Eager warmup (sizes workspaces, resolves kernels), then HIP graphs of
+    # the 9 launches of a step: one per weight copy, and one holding a step
+    # per copy in turn (`copies` steps: a replay boundary costs ~8 us of idle
+    # GPU, so the timed steps replay the multi-step graph and the one-step
+    # graphs only for the remainder).
     for i in range(args.warmup):
         launch_all(i % args.copies)
     torch.cuda.synchronize()
     eager = {k: v.clone() for k, v in ys.items()}
-    graphs = []
-    for c in range(args.copies):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            launch_all(c)
-        graphs.append(g)
+
+    def step_graphs(wts=None):
+        singles = []
+        for c in range(args.copies):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                launch_all(c, wts=wts)
+            singles.append(g)
+        multi = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(multi, stream=stream):
+            for c in range(args.copies):
+                launch_all(c, wts=wts)
+        return singles, multi
+
+    def run_steps(singles, multi, steps):
+        for _ in range(steps // args.copies):
+            multi.replay()
+        for c in range(steps % args.copies):
+            singles[c].replay()
+
+    graphs, graph_multi = step_graphs()
     for i in range(args.warmup):
         graphs[i % args.copies].replay()
+    graph_multi.replay()
     torch.cuda.synchronize()
     launch_all((args.warmup - 1) % args.copies)  # eager result of the last graph's copy
     torch.cuda.synchronize()
@@ -617,12 +639,18 @@ def main():
     graphs[(args.warmup - 1) % args.copies].replay()
     torch.cuda.synchronize()
     assert all(torch.equal(ys[k], ref[k]) for k in ys), "graph replay differs from eager launch"
+    launch_all(args.copies - 1)  # the multi-step graph ends with the last copy's step
+    torch.cuda.synchronize()
+    ref = {k: v.clone() for k, v in ys.items()}
+    graph_multi.replay()
+    torch.cuda.synchronize()
+    assert all(torch.equal(ys[k], ref[k]) for k in ys), "multi-step replay differs from eager launch"
 
-    # Timed region: K steps = K graph replays, synchronized on both sides.
+    # Timed region: exactly K steps (multi-step replays + the remainder),
+    # synchronized on both sides.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        graphs[i % args.copies].replay()
+    run_steps(graphs, graph_multi, args.steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     log(f"timed {args.steps} graph steps in {wall:.4f} s")
@@ -674,21 +702,16 @@ def main():
     # The same sweep on the reference's row-major U8 weights (the layout the
     # XLA handlers and direct QuantizedLinear::apply calls receive): graphs of
     # the same 9 launches, same step count, timed the same way.
-    graphs_row = []
-    for c in range(args.copies):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            launch_all(c, wts=wb_row)
-        graphs_row.append(g)
+    graphs_row, multi_row = step_graphs(wb_row)
     for i in range(args.warmup):
         graphs_row[i % args.copies].replay()
+    multi_row.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        graphs_row[i % args.copies].replay()
+    run_steps(graphs_row, multi_row, args.steps)
     torch.cuda.synchronize()
     wall_row = time.perf_counter() - t0
-    del graphs_row
+    del graphs_row, multi_row
     log(f"timed {args.steps} row-major graph steps in {wall_row:.4f} s")
 
     per_shape = {}
@@ -733,7 +756,8 @@ def main():
                    "batch": list(BS), "out_features": list(NS), "in_features": K,
                    "scales": "per-output-channel f32", "weight_copies": args.copies,
                    "weight_layout": layout,
-                   "launches_per_step": len(plan), "bytes_per_step": step_bytes},
+                   "launches_per_step": len(plan), "bytes_per_step": step_bytes,
+                   "steps_per_graph_replay": args.copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": recorded_traffic() if layout == "packed" else None,
@@ -764,7 +788,7 @@ def main():
                      "timing": "same sweep, step count and graph replays as `value`"},
         "device": info,
     }
-    del graphs, weights, wb
+    del graphs, graph_multi, weights, wb
     torch.cuda.synchronize()
     if not args.skip_gemm:
         log("prefill GEMM shapes ...")
