@@ -292,7 +292,7 @@ def bench_prefill_attention(rt, rx, torch, stream, reps=10):
     tf = flops / t / 1e12
     return {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-            "kernel": "rxw8_gqa_prefill_d128_g2", "us_per_call": round(t * 1e6, 1),
+            "kernel": "rxw8_gqa_prefill_r2_d128_g2", "us_per_call": round(t * 1e6, 1),
             "flops_per_call": flops, "shape": "B=8 S=1024 Hq=16 Hkv=8 D=128, causal from 0",
             "note": "flops count the visible (causal) keys once; q enters as bf16 hi + lo, "
                     "so the MFMA work is 1.5x this count",

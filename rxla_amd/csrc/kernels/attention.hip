@@ -70,15 +70,29 @@ constexpr int KW = 64;            // split granularity (keys)
 constexpr int KT = 16;            // keys per wave tile
 constexpr float kNegInf = -__builtin_huge_valf();
 
+// The values of lanes l and l ^ 16 (resp. l ^ 32), in some order, through
+// v_permlane16_swap / v_permlane32_swap with both operands v: a VALU exchange
+// instead of an LDS round trip (ds_bpermute). Callers combine the pair with a
+// commutative operation, so the result equals v op v[l ^ 16] bit for bit.
+__device__ __forceinline__ uint2 pair_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return uint2{r[0], r[1]};
+}
+__device__ __forceinline__ uint2 pair_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return uint2{r[0], r[1]};
+}
 __device__ __forceinline__ float wave_max4(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  uint2 p = pair_xor16(v);
+  v = fmaxf(__uint_as_float(p.x), __uint_as_float(p.y));
+  p = pair_xor32(v);
+  return fmaxf(__uint_as_float(p.x), __uint_as_float(p.y));
 }
 __device__ __forceinline__ float wave_sum4(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  uint2 p = pair_xor16(v);
+  v = __uint_as_float(p.x) + __uint_as_float(p.y);
+  p = pair_xor32(v);
+  return __uint_as_float(p.x) + __uint_as_float(p.y);
 }
 
 // Per-head RMSNorm (when nw is set) and split-half RoPE of one head held by
@@ -474,10 +488,11 @@ __device__ void attn_pass(const AttnArgs &a) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // rescale the running P.V of head h by head h's factor (held by lane h)
+    // rescale the running P.V of head h by head h's factor (held by lane h;
+    // v_readlane, no LDS round trip)
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float fh = __shfl(f_old, h);
+      const float fh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f_old), h));
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[h][e] *= fh;
     }
@@ -548,7 +563,8 @@ __device__ void attn_pass(const AttnArgs &a) {
     unpack_bf16x8(vraw, v);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float fh = __shfl(f_old, h), ph = g4 == 0 ? __shfl(pe, h) : 0.f;
+      const float fh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f_old), h));
+      const float ph = g4 == 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), h)) : 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * fh + ph * v[e];
     }
@@ -864,9 +880,445 @@ __device__ void attn_prefill(const PrefillArgs &a) {
 
 }  // namespace
 
+// One head per wave: a workgroup of 4 G waves takes 64 query rows of one
+// (sequence, kv head); wave w computes query head kvh * G + w / 4 for rows
+// 16 (w % 4) .. + 15. The K and V^T blocks staged in LDS serve the waves of
+// all G heads, while a wave's registers hold one head (q hi + lo, O, softmax
+// state): twice the waves of attn_prefill per CU hide the LDS, softmax and
+// load latencies between MFMAs. Same arithmetic per (row, head) as
+// attn_prefill, so the outputs agree bit for bit.
+template <int G>
+__device__ void attn_prefill_wh(const PrefillArgs &a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t pf_lds[];  // [2][K block | V^T block]
+  constexpr int NT = 256 * G;
+  constexpr int KU = 4 / G;  // 16-byte K chunks per thread per block
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, g4 = lane >> 4;
+  const int head = wave >> 2, rg = wave & 3;
+  const int per_qb = a.B * a.Hkv;
+  const int qb = a.nqb - 1 - (int)(blockIdx.x / per_qb);
+  const int rem = blockIdx.x - (a.nqb - 1 - qb) * per_qb;
+  const int b = rem / a.Hkv, kvh = rem - (rem / a.Hkv) * a.Hkv;
+  int start = a.starts[b];  // clamped so rows sit in [0, Lmax) (host: S <= Lmax)
+  start = start < 0 ? 0 : (start > a.Lmax - a.S ? a.Lmax - a.S : start);
+  const int slot = a.slots ? a.slots[b] : b;
+  const int64_t kv_base = ((int64_t)slot * a.Hkv + kvh) * a.Lmax * D;
+  const int i0 = qb * 64 + rg * 16;
+  const int kv_end = min(start + min(a.S, qb * 64 + 64), a.Lmax);  // keys the workgroup reads
+  const int nblk = (kv_end + PKB - 1) / PKB;
+  const int my_i = min(i0 + col, a.S - 1);
+  const int my_pos = start + my_i;  // last visible key of this lane's row
+  const int wave_last = start + min(i0 + 15, a.S - 1);
+  const int hq = kvh * G + head;
+
+  // q^T fragments: lane (row col, dims 32 t + 8 g4 ..), bf16 hi + lo
+  u32x4 qhi[4], qlo[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t off = (int64_t)b * a.q_sb + (int64_t)my_i * a.q_ss + (int64_t)hq * a.q_sh + 32 * t + 8 * g4;
+    float v[8];
+    if (a.q_f32) {
+      const f32x4 lo = *(const f32x4 *)((const float *)a.q + off);
+      const f32x4 hi = *(const f32x4 *)((const float *)a.q + off + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = lo[e];
+        v[4 + e] = hi[e];
+      }
+    } else {
+      unpack_bf16x8(*(const u32x4 *)((const uint16_t *)a.q + off), v);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float h0 = round_bf16(v[2 * e]), h1 = round_bf16(v[2 * e + 1]);
+      qhi[t][e] = pack_bf16x2(h0, h1);
+      qlo[t][e] = pack_bf16x2(v[2 * e] - h0, v[2 * e + 1] - h1);
+    }
+  }
+
+  f32x4 o[8];
+  float m_run = kNegInf, l_run = 0.f;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // block staging. K: thread chunk q = tid + NT u is (key q / 16, 16-byte
+  // chunk q % 16). V (threads < 256): thread t holds keys 4 (t % 16) .. + 3 of
+  // the 8 dims of chunk t / 16, written as one 8-byte V^T entry (4 keys) per dim.
+  u32x4 kreg[KU], vreg[4];
+  const bool vthread = threadIdx.x < 256;
+  auto gload = [&](int blk) {
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int qc = threadIdx.x + NT * u;
+      const int key = blk * PKB + (qc >> 4);
+      kreg[u] = key < kv_end ? *(const u32x4 *)(a.kc + kv_base + (int64_t)key * D + (qc & 15) * 8)
+                             : u32x4{0, 0, 0, 0};
+    }
+    if (vthread)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int vkey = blk * PKB + 4 * (threadIdx.x & 15) + u;
+        vreg[u] = vkey < kv_end
+                      ? *(const u32x4 *)(a.vc + kv_base + (int64_t)vkey * D + (threadIdx.x >> 4) * 8)
+                      : u32x4{0, 0, 0, 0};
+      }
+  };
+  auto lds_store = [&](int buf) {
+    uint16_t *ks_lds = pf_lds + buf * (PKB * D + D * VROW);
+    uint16_t *vt_lds = ks_lds + PKB * D;
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int qc = threadIdx.x + NT * u;
+      const int r = qc >> 4, c = qc & 15;
+      *(u32x4 *)(ks_lds + r * D + ((c ^ (r & 15)) << 3)) = kreg[u];
+    }
+    if (vthread) {
+      const int c = threadIdx.x >> 4, k4 = 4 * (threadIdx.x & 15);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int sh = 16 * (e & 1);
+        const uint32_t k0 = (vreg[0][e >> 1] >> sh) & 0xffffu, k1 = (vreg[1][e >> 1] >> sh) & 0xffffu;
+        const uint32_t k2 = (vreg[2][e >> 1] >> sh) & 0xffffu, k3 = (vreg[3][e >> 1] >> sh) & 0xffffu;
+        *(uint2 *)(vt_lds + (8 * c + e) * VROW + k4) = uint2{k0 | (k1 << 16), k2 | (k3 << 16)};
+      }
+    }
+  };
+
+  gload(0);
+  lds_store(0);
+  __syncthreads();
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int buf = blk & 1;
+    const uint16_t *ks_lds = pf_lds + buf * (PKB * D + D * VROW);
+    const uint16_t *vt_lds = ks_lds + PKB * D;
+    if (blk + 1 < nblk) gload(blk + 1);  // in flight while this block is used
+    const int j0 = blk * PKB;
+    if (j0 <= wave_last) {  // wave-uniform: else every key of the block is in this wave's future
+      // S^T tiles: s[kt] lane (key j0 + 16 kt + 4 g4 + i, row col)
+      f32x4 s[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const int r = kt * 16 + col;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4 kf = *(const u32x4 *)(ks_lds + r * D + (((4 * t + g4) ^ col) << 3));
+          acc = mfma16x16x32(as_bf16x8(kf), as_bf16x8(qhi[t]), acc);
+          acc = mfma16x16x32(as_bf16x8(kf), as_bf16x8(qlo[t]), acc);
+        }
+        s[kt] = acc;
+      }
+      float mb = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = j0 + 16 * kt + 4 * g4 + i;
+          const float v = key <= my_pos ? s[kt][i] * a.scale : kNegInf;
+          s[kt][i] = v;
+          mb = fmaxf(mb, v);
+        }
+      mb = wave_max4(mb);
+      // key 0 is visible to every row and block 0 is never skipped, so m_new
+      // is finite from the first block on
+      const float m_new = fmaxf(m_run, mb);
+      const float f = m_run == kNegInf ? 0.f : __expf(m_run - m_new);
+      float ls = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = __expf(s[kt][i] - m_new);
+          s[kt][i] = e;
+          ls += e;
+        }
+      l_run = l_run * f + wave_sum4(ls);
+      m_run = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt] *= f;
+      u32x4 pb[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        pb[ks] = u32x4{pack_bf16x2(s[2 * ks][0], s[2 * ks][1]), pack_bf16x2(s[2 * ks][2], s[2 * ks][3]),
+                       pack_bf16x2(s[2 * ks + 1][0], s[2 * ks + 1][1]),
+                       pack_bf16x2(s[2 * ks + 1][2], s[2 * ks + 1][3])};
+      // O^T += V^T P^T: the V^T operand in the key order of pb
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const uint16_t *vrow = vt_lds + (dt * 16 + col) * VROW + 32 * ks + 4 * g4;
+          const uint2 lo = *(const uint2 *)vrow, hi = *(const uint2 *)(vrow + 16);
+          const u32x4 va = {lo.x, lo.y, hi.x, hi.y};
+          o[dt] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[ks]), o[dt]);
+        }
+    }
+    // the other buffer was last read in the previous block, before the barrier
+    if (blk + 1 < nblk) lds_store(buf ^ 1);
+    __syncthreads();
+  }
+  if (i0 + col >= a.S) return;
+  const float inv = 1.0f / l_run;
+  const int64_t ob = (int64_t)b * a.o_sb + (int64_t)(i0 + col) * a.o_ss + (int64_t)hq * a.o_sh;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    const f32x4 r = o[dt] * inv;
+    const int64_t oi = ob + dt * 16 + 4 * g4;
+    if (a.out_f32)
+      *(f32x4 *)((float *)a.out + oi) = r;
+    else
+      *(uint2 *)((uint16_t *)a.out + oi) = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+  }
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One LDS DMA instruction of the wave: lane l copies 16 bytes from g (its own
+// address) to LDS at l_base + 16 l (l_base wave-uniform); completion is
+// counted by vmcnt.
+__device__ __forceinline__ void lds_dma16(const void *g, void *l_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void *)l_base, 16, 0, 0);
+}
+
+// R row tiles per wave: as attn_prefill_wh, but wave w owns rows
+// 16 R (w % 4) .. + 16 R - 1 of a workgroup's 64 R query rows, as R 16-row
+// tiles of one head. Every K and V^T fragment read from LDS then feeds R
+// tiles' MFMAs (the LDS reads per block per wave stay 32 KiB, the matrix work
+// grows R-fold), and each staged K/V block serves 64 R rows. Same arithmetic
+// per (row, head) as attn_prefill.
+template <int G, int R>
+__device__ void attn_prefill_rt(const PrefillArgs &a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t pf_lds[];  // [2][K block | V^T block]
+  constexpr int QROWS = 64 * R;   // query rows per workgroup
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, g4 = lane >> 4;
+  const int head = wave >> 2, rg = wave & 3;
+  const int per_qb = a.B * a.Hkv;
+  const int qb = a.nqb - 1 - (int)(blockIdx.x / per_qb);
+  const int rem = blockIdx.x - (a.nqb - 1 - qb) * per_qb;
+  const int b = rem / a.Hkv, kvh = rem - (rem / a.Hkv) * a.Hkv;
+  int start = a.starts[b];  // clamped so rows sit in [0, Lmax) (host: S <= Lmax)
+  start = start < 0 ? 0 : (start > a.Lmax - a.S ? a.Lmax - a.S : start);
+  const int slot = a.slots ? a.slots[b] : b;
+  const int64_t kv_base = ((int64_t)slot * a.Hkv + kvh) * a.Lmax * D;
+  const int i0 = qb * QROWS + rg * 16 * R;  // the wave's first row
+  const int kv_end = min(start + min(a.S, qb * QROWS + QROWS), a.Lmax);  // keys the workgroup reads
+  const int nblk = (kv_end + PKB - 1) / PKB;
+  int my_pos[R];  // last visible key of this lane's row in tile r
+#pragma unroll
+  for (int r = 0; r < R; ++r) my_pos[r] = start + min(i0 + 16 * r + col, a.S - 1);
+  const int wave_last = start + min(i0 + 16 * R - 1, a.S - 1);
+  const int hq = kvh * G + head;
+  const float c_exp = a.scale * 1.4426950408889634f;  // scale * log2(e)
+
+  // q^T fragments: lane (row col of tile r, dims 32 t + 8 g4 ..), bf16 hi + lo
+  u32x4 qhi[R][4], qlo[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int my_i = min(i0 + 16 * r + col, a.S - 1);
+      const int64_t off = (int64_t)b * a.q_sb + (int64_t)my_i * a.q_ss + (int64_t)hq * a.q_sh + 32 * t + 8 * g4;
+      float v[8];
+      if (a.q_f32) {
+        const f32x4 lo = *(const f32x4 *)((const float *)a.q + off);
+        const f32x4 hi = *(const f32x4 *)((const float *)a.q + off + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = lo[e];
+          v[4 + e] = hi[e];
+        }
+      } else {
+        unpack_bf16x8(*(const u32x4 *)((const uint16_t *)a.q + off), v);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float h0 = round_bf16(v[2 * e]), h1 = round_bf16(v[2 * e + 1]);
+        qhi[r][t][e] = pack_bf16x2(h0, h1);
+        qlo[r][t][e] = pack_bf16x2(v[2 * e] - h0, v[2 * e + 1] - h1);
+      }
+    }
+
+  f32x4 o[R][8];
+  float m_run[R], l_run[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    m_run[r] = kNegInf;
+    l_run[r] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[r][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Block staging by LDS DMA (no registers held across the block): K into
+  // two buffers, row-major with 16-byte chunks XOR-swizzled by row (the lane
+  // writing LDS chunk slot c' of row r fetches global chunk c' ^ (r & 15));
+  // V row-major into one staging block, transposed to V^T by an LDS pass.
+  // Lanes past kv_end copy nothing: their K scores are masked to -inf and
+  // the transpose writes zero V rows for them.
+  uint16_t *k_lds0 = pf_lds;                 // [2][64 keys][128] swizzled
+  uint16_t *v_raw = pf_lds + 2 * PKB * D;    // [64 keys][128]
+  uint16_t *vt_lds = v_raw + PKB * D;        // [128 dims][VROW]
+  auto dma_block = [&](int blk) {
+    uint16_t *kb = k_lds0 + (blk & 1) * PKB * D;
+    // 2 x 16 instructions of 64 lanes (K, then V), spread over the waves
+    for (int ins = wave; ins < 32; ins += 4 * G) {
+      const int gidx = 64 * (ins & 15) + lane;  // 16-byte granule of the block
+      const int r = gidx >> 4, c = gidx & 15;
+      const int key = blk * PKB + r;
+      if (key < kv_end) {
+        if (ins < 16)
+          lds_dma16(a.kc + kv_base + (int64_t)key * D + ((c ^ (r & 15)) << 3), kb + 64 * 8 * (ins & 15));
+        else
+          lds_dma16(a.vc + kv_base + (int64_t)key * D + (c << 3), v_raw + 64 * 8 * (ins & 15));
+      }
+    }
+  };
+  // threads < 256: keys 4 (t % 16) .. + 3 of dims 8 (t / 16) .. + 7 -> V^T.
+  // A V^T row holds the block's keys in the order the P operand takes them:
+  // key 16 kt + 4 g + i at 32 (kt / 2) + 8 g + 4 (kt % 2) + i, so a lane's
+  // 8 keys of one step (two 16-key tiles, 4 keys each) are 16 contiguous bytes.
+  auto transpose_v = [&](int blk) {
+    if (threadIdx.x >= 256) return;
+    const int c = threadIdx.x >> 4, k4 = 4 * (threadIdx.x & 15);
+    const int kt = k4 >> 4, g = (k4 >> 2) & 3;
+    const int kpos = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1);
+    u32x4 vr[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      vr[u] = blk * PKB + k4 + u < kv_end ? *(const u32x4 *)(v_raw + (k4 + u) * D + 8 * c)
+                                          : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sh = 16 * (e & 1);
+      const uint32_t k0 = (vr[0][e >> 1] >> sh) & 0xffffu, k1 = (vr[1][e >> 1] >> sh) & 0xffffu;
+      const uint32_t k2 = (vr[2][e >> 1] >> sh) & 0xffffu, k3 = (vr[3][e >> 1] >> sh) & 0xffffu;
+      *(uint2 *)(vt_lds + (8 * c + e) * VROW + kpos) = uint2{k0 | (k1 << 16), k2 | (k3 << 16)};
+    }
+  };
+
+  dma_block(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  transpose_v(0);
+  __syncthreads();
+  for (int blk = 0; blk < nblk; ++blk) {
+    const uint16_t *ks_lds = k_lds0 + (blk & 1) * PKB * D;
+    if (blk + 1 < nblk) dma_block(blk + 1);  // in flight while this block is used
+    const int j0 = blk * PKB;
+    if (j0 <= wave_last) {  // wave-uniform: else every key of the block is in this wave's future
+      // S^T tiles: s[r][kt] lane (key j0 + 16 kt + 4 g4 + i, row col of tile r)
+      f32x4 s[R][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const int kr = kt * 16 + col;
+        f32x4 acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4 kf = *(const u32x4 *)(ks_lds + kr * D + (((4 * t + g4) ^ col) << 3));
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            acc[r] = mfma16x16x32(as_bf16x8(kf), as_bf16x8(qhi[r][t]), acc[r]);
+            acc[r] = mfma16x16x32(as_bf16x8(kf), as_bf16x8(qlo[r][t]), acc[r]);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) s[r][kt] = acc[r];
+      }
+      u32x4 pb[R][2];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        // Raw scores (the scale is folded into the exponent below); the
+        // causal mask only where some key of the block lies past the tile's
+        // first row (wave-uniform).
+        if (j0 + PKB - 1 > start + i0 + 16 * r) {
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (j0 + 16 * kt + 4 * g4 + i > my_pos[r]) s[r][kt][i] = kNegInf;
+        }
+        float mb = kNegInf;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mb = fmaxf(mb, s[r][kt][i]);
+        mb = wave_max4(mb);
+        // key 0 is visible to every row and block 0 is never skipped, so
+        // m_new is finite from the first block on.
+        // p = exp(scale (s - m)) = exp2(c s - c m), c = scale * log2(e), on
+        // v_exp_f32 (terms below 2^-126 of the row maximum flush to zero)
+        const float m_new = fmaxf(m_run[r], mb);
+        const float cm = c_exp * m_new;
+        const float f = m_run[r] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(c_exp * m_run[r] - cm);
+        float ls = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float e = __builtin_amdgcn_exp2f(fmaf(c_exp, s[r][kt][i], -cm));
+            s[r][kt][i] = e;
+            ls += e;
+          }
+        l_run[r] = l_run[r] * f + wave_sum4(ls);
+        m_run[r] = m_new;
+        if (__ballot(f != 1.f))  // no row's maximum moved: nothing to rescale
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) o[r][dt] *= f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          pb[r][ks] = u32x4{pack_bf16x2(s[r][2 * ks][0], s[r][2 * ks][1]),
+                            pack_bf16x2(s[r][2 * ks][2], s[r][2 * ks][3]),
+                            pack_bf16x2(s[r][2 * ks + 1][0], s[r][2 * ks + 1][1]),
+                            pack_bf16x2(s[r][2 * ks + 1][2], s[r][2 * ks + 1][3])};
+      }
+      // O^T += V^T P^T: the V^T operand in the key order of pb
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const u32x4 va = *(const u32x4 *)(vt_lds + (dt * 16 + col) * VROW + 32 * ks + 8 * g4);
+#pragma unroll
+          for (int r = 0; r < R; ++r) o[r][dt] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[r][ks]), o[r][dt]);
+        }
+    }
+    // the next block's copies are in; every wave is done with V^T and this K
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (blk + 1 < nblk) {
+      transpose_v(blk + 1);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (i0 + 16 * r + col >= a.S) continue;
+    const float inv = 1.0f / l_run[r];
+    const int64_t ob = (int64_t)b * a.o_sb + (int64_t)(i0 + 16 * r + col) * a.o_ss + (int64_t)hq * a.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const f32x4 v = o[r][dt] * inv;
+      const int64_t oi = ob + dt * 16 + 4 * g4;
+      if (a.out_f32)
+        *(f32x4 *)((float *)a.out + oi) = v;
+      else
+        *(uint2 *)((uint16_t *)a.out + oi) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  }
+}
+
 #define RXW8_PREFILL(G)                                                              \
   extern "C" __global__ void __launch_bounds__(256) rxw8_gqa_prefill_d128_g##G(PrefillArgs a) { \
     attn_prefill<G>(a);                                                              \
+  }                                                                                  \
+  extern "C" __global__ void __launch_bounds__(256 * G)                              \
+      rxw8_gqa_prefill_wh_d128_g##G(PrefillArgs a) {                                 \
+    attn_prefill_wh<G>(a);                                                           \
+  }                                                                                  \
+  extern "C" __global__ void __launch_bounds__(256 * G)                              \
+      __attribute__((amdgpu_waves_per_eu(2))) rxw8_gqa_prefill_r2_d128_g##G(PrefillArgs a) { \
+    attn_prefill_rt<G, 2>(a);                                                        \
   }
 RXW8_PREFILL(1)
 RXW8_PREFILL(2)

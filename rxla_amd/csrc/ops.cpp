@@ -972,10 +972,25 @@ int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t 
   a.q_f32 = q_f32;
   a.out_f32 = out_f32;
   char kname[48];
-  std::snprintf(kname, sizeof kname, "rxw8_gqa_prefill_d128_g%d", (int)(Hq / Hkv));
+  const int G = (int)(Hq / Hkv);
+  // G <= 2: one query head per wave (4 G waves per workgroup), two 16-row
+  // tiles per wave (128 query rows per workgroup) and LDS-DMA staging: at the
+  // C5 prompt shape 82.7 us against 94.3 (one tile) and 120.5 (all heads per
+  // wave, one wave per SIMD). G = 4 keeps the all-heads kernel (the per-head
+  // variants would spill at 1024 threads). RXW8_PREFILL_R2=0 selects the
+  // one-tile kernel, RXW8_PREFILL_R2=0 RXW8_PREFILL_WH=0 the all-heads one.
+  static const int wh_env = env_int("RXW8_PREFILL_WH", 1);
+  static const int r2_env = env_int("RXW8_PREFILL_R2", 1);
+  const bool r2 = r2_env && G <= 2;
+  const bool wh = wh_env && G <= 2;
+  if (r2) a.nqb = (int)((S + 127) / 128);
+  std::snprintf(kname, sizeof kname,
+                r2 ? "rxw8_gqa_prefill_r2_d128_g%d"
+                   : (wh ? "rxw8_gqa_prefill_wh_d128_g%d" : "rxw8_gqa_prefill_d128_g%d"),
+                G);
   // K and V^T blocks of 64 keys, double-buffered (2 x (64*128 + 128*72) bf16)
   constexpr size_t lds = 2 * (64 * 128 + 128 * 72) * 2;
-  return launch(rt, kname, dim3((unsigned)(a.nqb * B * Hkv)), dim3(256), a, lds);
+  return launch(rt, kname, dim3((unsigned)(a.nqb * B * Hkv)), dim3(wh || r2 ? 256 * G : 256), a, lds);
 }
 
 
