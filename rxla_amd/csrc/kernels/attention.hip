@@ -70,18 +70,6 @@ constexpr int KW = 64;            // split granularity (keys)
 constexpr int KT = 16;            // keys per wave tile
 constexpr float kNegInf = -__builtin_huge_valf();
 
-// The values of lanes l and l ^ 16 (resp. l ^ 32), in some order, through
-// v_permlane16_swap / v_permlane32_swap with both operands v: a VALU exchange
-// instead of an LDS round trip (ds_bpermute). Callers combine the pair with a
-// commutative operation, so the result equals v op v[l ^ 16] bit for bit.
-__device__ __forceinline__ uint2 pair_xor16(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return uint2{r[0], r[1]};
-}
-__device__ __forceinline__ uint2 pair_xor32(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return uint2{r[0], r[1]};
-}
 __device__ __forceinline__ float wave_max4(float v) {
   uint2 p = pair_xor16(v);
   v = fmaxf(__uint_as_float(p.x), __uint_as_float(p.y));

@@ -44,6 +44,41 @@ __device__ __forceinline__ uint2 u8x4_to_bf16x4(uint32_t w) {
   return uint2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
 }
 
+// The values of lanes l and l ^ 16 (resp. l ^ 32), in some order, through
+// v_permlane16_swap / v_permlane32_swap with both operands v: a VALU exchange
+// instead of an LDS round trip (ds_bpermute). Combined with a commutative
+// operation the result equals v op v[l ^ 16] bit for bit.
+__device__ __forceinline__ uint2 pair_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return uint2{r[0], r[1]};
+}
+__device__ __forceinline__ uint2 pair_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return uint2{r[0], r[1]};
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const uint2 p = pair_xor16(v);
+  return __uint_as_float(p.x) + __uint_as_float(p.y);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const uint2 p = pair_xor32(v);
+  return __uint_as_float(p.x) + __uint_as_float(p.y);
+}
+// v of lane l ^ 32 (the member of the pair that is not this lane's bits; equal
+// bits make either the answer)
+__device__ __forceinline__ float value_xor32(float v) {
+  const uint2 p = pair_xor32(v);
+  return __uint_as_float(p.x == __float_as_uint(v) ? p.y : p.x);
+}
+// Sum over the 64 lanes, butterfly order 32, 16, 8, 4, 2, 1 (the first two
+// steps on the VALU exchanges)
+__device__ __forceinline__ float wave_sum64(float v) {
+  v = sum_xor32(v);
+  v = sum_xor16(v);
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {

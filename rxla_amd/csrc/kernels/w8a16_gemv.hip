@@ -260,7 +260,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, uint16_t *xs, int k0,
           for (int s = 0; s < 4; ++s)
             if (p0 + 64 * s < a.ss_parts) ss += t[s];
         }
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        ss = wave_sum64(ss);
         if (lane == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
       }
     } else {  // mode 1: 256-thread workgroups only (host-checked)
@@ -360,7 +360,7 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
       const f32x4 v = total[mb] * sc;
       f32x4 up;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(v[i], 32);
+      for (int i = 0; i < 4; ++i) up[i] = value_xor32(v[i]);
       const int b = col + 16 * mb;
       if (j < 2 && b < a.M) {
         const int c = (rows0 + rg * 16) / 2 + 4 * j;  // first of 4 output channels
@@ -381,8 +381,8 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
                                                  : float4{0.f, 0.f, 0.f, 0.f})
                        : 0.f;
     if (a.ss_out) {  // 4 lanes (j) hold the group's 16 channels of row b
-      ss += __shfl_xor(ss, 16);
-      ss += __shfl_xor(ss, 32);
+      ss = sum_xor16(ss);
+      ss = sum_xor32(ss);
       if (j == 0 && b < a.M) a.ss_out[(int64_t)((rows0 + rg * 16) / 16) * a.M + b] = ss;
     }
   }
