@@ -215,7 +215,10 @@ def bench_gemm(rt, rx, torch, stream, reps=10):
     big = out["M8192_N12288_K4096"]
     return out, {"bound": "mfma", "achieved": big["TFLOPs"], "peak": MFMA_BF16_PEAK_TFLOPS,
                  "unit": "TFLOP/s", "frac": round(big["TFLOPs"] / MFMA_BF16_PEAK_TFLOPS, 4),
-                 "traffic": None,
+                 "traffic": recorded_traffic("gemm_M8192_N12288_K4096_traffic.txt"),
+                 "traffic_source": "profiles/gemm_M8192_N12288_K4096_traffic.txt (FETCH_SIZE + "
+                                   "WRITE_SIZE per call of both kernels, copy-calibrated, "
+                                   "bench.py --pmc-probe gemm)",
                  "kernel": "rxw8_gemm_dequant_w + rxw8_w8a16_gemm_bf16w_t256 (M >= 4096 path)",
                  "shape": "M=8192 N=12288 K=4096", "mean_launch_us": big["us"],
                  "timing": f"HIP events around {reps} back-to-back launches after ~60 ms "
@@ -452,11 +455,13 @@ def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, ite
 
 def pmc_probe(kind, rounds=3):
     """A short fixed program for rocprofv3 runs: one roofline leg launched as
-    the bench times it (gemv: `rounds` x [spin spacer, ROOF_CYCLES passes over
-    6 weight copies back to back]; attention: `rounds` x [spin spacer, 20 C4
-    calls over the rotating caches]; gemm: 30 launches of the C3 roofline
-    shape) plus 4 plain 256 MiB device copies (torch) that calibrate what
-    FETCH_SIZE / WRITE_SIZE read for a known number of bytes."""
+    the bench times it (gemv / gemv16: `rounds` x [spin spacer, ROOF_CYCLES
+    passes over 6 weight copies back to back] at B = 1 / 16; attention:
+    `rounds` x [spin spacer, 20 C4 calls over the rotating caches]; gemm: 30
+    launches of the C3 roofline shape; decoder: the C5 leg with 16 decode
+    steps; prefill: the prefill-attention leg) plus 4 plain 256 MiB device
+    copies (torch) that calibrate what FETCH_SIZE / WRITE_SIZE read for a
+    known number of bytes."""
     import torch
     import rxla_amd as rx
 
@@ -468,8 +473,8 @@ def pmc_probe(kind, rounds=3):
         src = torch.randn(1 << 26, device="cuda", generator=gen)  # 256 MiB
         dst = torch.empty_like(src)
     stream.synchronize()
-    if kind == "gemv":  # B=1, N=24576, K=4096, packed, 6 rotating copies
-        n, b = 24576, 1
+    if kind in ("gemv", "gemv16"):  # B=1 (or 16), N=24576, K=4096, packed, 6 rotating copies
+        n, b = 24576, (16 if kind == "gemv16" else 1)
         ws = [c5_quantized(rt, rx, torch, stream, gen, n, K) for _ in range(6)]
         with torch.cuda.stream(stream):
             x = torch.randn((b, K), device="cuda", generator=gen).to(torch.bfloat16)
@@ -518,6 +523,12 @@ def pmc_probe(kind, rounds=3):
                 rx.grouped_query_attention(rt, qb, cb[i % ATTN_COPIES][0], cb[i % ATTN_COPIES][1], lb, out=ob)
                 calls += 1
         log(f"pmc probe attention C4 lens={lens.tolist()}: {calls} calls")
+    elif kind == "decoder":  # C5: prompt 1024, 16 greedy steps (generate run 3 times)
+        r = bench_decoder(rt, rx, torch, stream, steps=16)
+        log(f"pmc probe decoder C5: 16 decode steps per generate, {r['ms_per_decode_step']} ms/step")
+    elif kind == "prefill":  # the C5 prompt's causal attention, as bench_prefill_attention times it
+        r = bench_prefill_attention(rt, rx, torch, stream)
+        log(f"pmc probe prefill attention: {r['us_per_call']} us/call")
     else:
         raise SystemExit(f"unknown --pmc-probe {kind}")
     rt.synchronize()
@@ -539,7 +550,7 @@ def main():
     ap.add_argument("--skip-attention", action="store_true")
     ap.add_argument("--skip-decoder", action="store_true")
     ap.add_argument("--skip-qwen35", action="store_true")
-    ap.add_argument("--pmc-probe", choices=["gemv", "gemm", "attention"],
+    ap.add_argument("--pmc-probe", choices=["gemv", "gemv16", "gemm", "attention", "decoder", "prefill"],
                     help="counter-collection program only")
     ap.add_argument("--qwen35-only", action="store_true",
                     help="(profiling) run only the Qwen3.5 leg and print its JSON")
