@@ -233,6 +233,32 @@ def test_generate_graph_matches_eager_and_oracle(rt):
     np.testing.assert_array_equal(outs[0][:, :3], want[:, :3])
 
 
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_generate_equals_stepwise_forward(rt, use_graph):
+    """generate's decode steps take their input rows from the argmax launch,
+    which embeds its winners (and their sum-of-squares partials) for the next
+    step; forward embeds its ids with the separate embedding launch. Both must
+    give the same greedy ids at every step."""
+    cfg = small_cfg()
+    params = tiny_params(cfg, seed=65, std=0.05)
+    batch, s, steps = 3, 7, 12
+    rng = np.random.default_rng(66)
+    prompt = rng.integers(0, cfg["vocab"], (batch, s)).astype(np.int32)
+    got = build(rt, cfg, params, batch).generate(rt.buffer(prompt), steps,
+                                                 use_graph=use_graph).to_numpy()
+    model = build(rt, cfg, params, batch)
+    nxt = model.forward(rt.buffer(prompt)).to_numpy().reshape(batch)
+    want = [nxt]
+    for _ in range(steps):
+        nxt = model.forward(rt.buffer(nxt.reshape(batch, 1).astype(np.int32))).to_numpy()
+        nxt = nxt.reshape(batch)
+        want.append(nxt)
+    want = np.stack(want, axis=1)
+    assert got.shape == want.shape
+    assert len(np.unique(want)) > steps  # the ids vary, so a wrong row would show
+    np.testing.assert_array_equal(got, want)
+
+
 def test_generate_twice_on_one_model_rebuilds_the_graph(rt):
     """A second generate on the same model with a longer prompt (the
     activation block regrows) and another step count (the out_ids row stride
