@@ -238,9 +238,11 @@ def test_generate_equals_stepwise_forward(rt, use_graph):
     """generate's decode steps take their input rows from the argmax launch,
     which embeds its winners (and their sum-of-squares partials) for the next
     step; forward embeds its ids with the separate embedding launch. Both must
-    give the same greedy ids at every step."""
+    give the same greedy ids at every step. (At std 0.05 the tied embedding
+    dominates and every sequence repeats one id; at 0.3 the oracle's greedy
+    ids for this seed take 37 values over the 3 x 13 steps.)"""
     cfg = small_cfg()
-    params = tiny_params(cfg, seed=65, std=0.05)
+    params = tiny_params(cfg, seed=65, std=0.3)
     batch, s, steps = 3, 7, 12
     rng = np.random.default_rng(66)
     prompt = rng.integers(0, cfg["vocab"], (batch, s)).astype(np.int32)
