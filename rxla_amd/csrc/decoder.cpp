@@ -56,6 +56,8 @@ struct EmbedArgs {
   const int32_t *lens;
   int32_t *pos, *row_seq, *row_len;
   int s;
+  const float *xw_norm = nullptr;
+  uint16_t *xw = nullptr;
 };
 struct InterleaveArgs {
   const float *src;
@@ -122,6 +124,8 @@ struct ArgmaxFinalArgs {
   float *ss = nullptr;
   int32_t *pos = nullptr, *row_seq = nullptr, *row_len = nullptr;
   int64_t V = 0, H = 0;
+  const float *xw_norm = nullptr;
+  uint16_t *xw = nullptr;
 };
 struct RecordArgs {
   const int32_t *next;
@@ -260,6 +264,15 @@ static void graph_key(const Decoder *d, int64_t b, int64_t ncols, const void *ou
   for (int i = 0; i < 7; ++i) key[3 + i] = (int64_t)(intptr_t)ptrs[i];
 }
 
+// Whether a fused step of T rows applies the RMSNorms after the projections:
+// the row-norm GEMV kernels take packed weights, up to 16 rows and at most
+// 256 sum-of-squares partials per row (H <= 4096).
+static bool row_norm_enabled(const Decoder *d, int64_t T) {
+  const char *env = std::getenv("RXW8_DEC_ROW_NORM");
+  return !(env && *env == '0') && T <= 16 && d->H % 16 == 0 && d->H / 16 <= 256 &&
+         d->p(0, P_QKV_W).packed && d->p(0, P_GU_W).packed;
+}
+
 static unsigned blocks(int64_t n, int per = 256) { return (unsigned)std::max<int64_t>(1, (n + per - 1) / per); }
 
 // Enqueue one forward pass over ids[b, s] (device) starting at the current
@@ -301,11 +314,20 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
                           (d->Hq / d->Hkv == 1 || d->Hq / d->Hkv == 2 || d->Hq / d->Hkv == 4 ||
                            d->Hq / d->Hkv == 8) &&
                           !(unfused_rope && *unfused_rope == '1');
+  // Fused steps apply each RMSNorm after its projection: the producer of the
+  // residual rows (embedding, o_proj, down) also writes bf16(h * norm weight)
+  // into xn, and the next projection's GEMV reads those rows and multiplies
+  // each row's result by 1/sqrt(mean(h^2) + eps), formed from the producer's
+  // sum-of-squares partials. Off the critical path of the weight stream,
+  // unlike normalising the rows while staging them (RXW8_DEC_ROW_NORM=0).
+  const bool rn = fused && row_norm_enabled(d, T);
+  const float *in_norm0 = (const float *)d->p(0, P_IN_NORM).bound->ptr;
   if (!embedded) {
     const ParamSpec &e = d->p(-1, P_EMBED);
     // the embedding launch also writes the token positions
     EmbedArgs a{ids, (const uint16_t *)e.bound->ptr, d->h, fused ? d->ss_embed : nullptr, T, d->V,
                 d->H, d->d_lens, d->pos, d->row_seq, d->row_len, (int)s};
+    if (rn) a.xw_norm = in_norm0, a.xw = d->xn;
     if ((rc = launch(rt, "rxw8_dec_embed", dim3((unsigned)T), dim3(256), a))) return rc;
   }
   const size_t layer_cache = (size_t)d->Bmax * d->Hkv * d->Lmax * d->D;
@@ -324,11 +346,13 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
     // into the GEMV's activation staging (one launch instead of two).
     if (fused) {
       GemvOptions o;
-      o.mode = 3, o.norm_w = fptr(P_IN_NORM), o.eps = d->cfg.eps, o.prefer_ks1 = true;
+      o.mode = rn ? 0 : 3, o.row_norm = rn, o.norm_w = fptr(P_IN_NORM), o.eps = d->cfg.eps;
+      o.prefer_ks1 = true;
       o.ss_in = l == 0 ? d->ss_embed : d->ss_down;
       o.ss_parts = l == 0 ? 1 : (int)(d->H / 16);
-      if ((rc = gemv_launch(rt, d->h, 1, wptr(P_QKV_W), false, packed(P_QKV_W), fptr(P_QKV_S),
-                            d->qkv, 0, T, d->QKV, d->H, d->group_for(d->H), 0, o)))
+      if ((rc = gemv_launch(rt, rn ? (const void *)d->xn : (const void *)d->h, rn ? 0 : 1,
+                            wptr(P_QKV_W), false, packed(P_QKV_W), fptr(P_QKV_S), d->qkv, 0, T,
+                            d->QKV, d->H, d->group_for(d->H), 0, o)))
         return rc;
     } else {
       RmsNormArgs a{d->h, fptr(P_IN_NORM), d->xn, nullptr, d->H, (int)T, 1, 0, d->cfg.eps};
@@ -378,17 +402,24 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
     if (fused) {
       GemvOptions o;
       o.prefer_ks1 = true, o.ss_out = d->ss_o;
+      if (rn) o.xw_norm = fptr(P_POST_NORM), o.xw_out = d->xn;
       if ((rc = gemv_launch(rt, d->attn, 0, wptr(P_O_W), false, packed(P_O_W), fptr(P_O_S), d->h, 1,
                             T, d->H, d->Hq * d->D, d->group_for(d->Hq * d->D), 1, o)))
         return rc;
       GemvOptions g;
-      g.mode = 3, g.norm_w = fptr(P_POST_NORM), g.eps = d->cfg.eps;
+      g.mode = rn ? 0 : 3, g.row_norm = rn, g.norm_w = fptr(P_POST_NORM), g.eps = d->cfg.eps;
       g.ss_in = d->ss_o, g.ss_parts = (int)(d->H / 16), g.prefer_ks1 = true, g.swiglu = true;
-      if ((rc = gemv_launch(rt, d->h, 1, wptr(P_GU_W), false, packed(P_GU_W), fptr(P_GU_S), d->act,
-                            0, T, 2 * d->I, d->H, d->group_for(d->H), 0, g)))
+      if ((rc = gemv_launch(rt, rn ? (const void *)d->xn : (const void *)d->h, rn ? 0 : 1,
+                            wptr(P_GU_W), false, packed(P_GU_W), fptr(P_GU_S), d->act, 0, T,
+                            2 * d->I, d->H, d->group_for(d->H), 0, g)))
         return rc;
       GemvOptions dn;
       dn.prefer_ks1 = true, dn.ss_out = d->ss_down;
+      if (rn) {  // the next layer's input norm, or the final norm after the last layer
+        dn.xw_norm = l + 1 < d->L ? (const float *)d->p(l + 1, P_IN_NORM).bound->ptr
+                                  : (const float *)d->p(-1, P_FINAL_NORM).bound->ptr;
+        dn.xw_out = d->xn;
+      }
       if ((rc = gemv_launch(rt, d->act, 0, wptr(P_DOWN_W), false, packed(P_DOWN_W), fptr(P_DOWN_S),
                             d->h, 1, T, d->H, d->I, d->group_for(d->I), 1, dn)))
         return rc;
@@ -423,7 +454,16 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
   const bool pk = e.packed != nullptr;
   const uint16_t *ew = (const uint16_t *)(pk ? e.packed->ptr : e.bound->ptr);
   const float *final_norm = (const float *)d->p(-1, P_FINAL_NORM).bound->ptr;
-  {
+  // single-token steps: every row is a last position, and the lm_head GEMV
+  // applies the final norm to the rows the last down projection wrote
+  rc = RXW8_UNIMPLEMENTED;
+  if (rn && s == 1) {
+    GemvOptions o;
+    o.row_norm = true, o.ss_in = d->ss_down, o.ss_parts = (int)(d->H / 16), o.eps = d->cfg.eps;
+    rc = gemv_launch(rt, d->xn, 0, ew, true, pk, nullptr, d->logits, 1, b, d->V, d->H, d->H, 0, o);
+    if (rc && rc != RXW8_UNIMPLEMENTED) return rc;
+  }
+  if (rc == RXW8_UNIMPLEMENTED) {
     RmsNormArgs a{d->h, final_norm, d->xl, nullptr, d->H, (int)b, (int)s, (int)s - 1, d->cfg.eps};
     if ((rc = launch(rt, "rxw8_dec_rmsnorm", dim3((unsigned)b), dim3(256), a))) return rc;
     if ((rc = bf16_linear_launch(rt, d->xl, 0, ew, pk, d->logits, 1, b, d->V, d->H))) return rc;
@@ -440,6 +480,7 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
       // sized for the 32 rows a fused step takes)
       f.table = (const uint16_t *)e.bound->ptr, f.h = d->h, f.ss = b <= 32 ? d->ss_embed : nullptr;
       f.pos = d->pos, f.row_seq = d->row_seq, f.row_len = d->row_len, f.V = d->V, f.H = d->H;
+      if (row_norm_enabled(d, b)) f.xw_norm = in_norm0, f.xw = d->xn;
       threads = 1024;
     }
     if ((rc = launch(rt, "rxw8_dec_argmax_final", dim3(1), dim3(threads), f))) return rc;

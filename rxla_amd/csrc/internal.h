@@ -34,6 +34,12 @@ struct GemvOptions {
   bool prefer_ks1 = false;
   bool swiglu = false;
   float *ss_out = nullptr;
+  // mode 0 with bf16 rows x = bf16(h * norm weight): multiply row b's result
+  // by 1/sqrt(sum_p ss_in[p * M + b] / K + eps) (ss_in, ss_parts, eps above)
+  bool row_norm = false;
+  // y_mode 1 with ss_out: also write xw_out[b, n] = bf16(h_new[b, n] * xw_norm[n])
+  const float *xw_norm = nullptr;
+  uint16_t *xw_out = nullptr;
 };
 
 // Records the thread-local error message and returns `code`.

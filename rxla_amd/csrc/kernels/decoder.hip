@@ -38,13 +38,16 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_positions(DecPosArgs 
 // pieces p = t, t + 256, ... of 8 values (loads issued 4 at a time), each
 // thread summing its squares in element order; otherwise elements t, t + 256,
 // .... Returns the thread's partial sum (the caller adds the slice's partials
-// in block_sum_256 order).
-__device__ __forceinline__ float embed_row(const uint16_t *src, float *dst, int64_t H, int t) {
+// in block_sum_256 order). With xw, also writes xw[i] = bf16(dst[i] *
+// xw_norm[i]) (the first layer's RMSNorm rows before the row factor).
+__device__ __forceinline__ float embed_row(const uint16_t *src, float *dst, int64_t H, int t,
+                                           const float *xw_norm = nullptr, uint16_t *xw = nullptr) {
   float ss = 0.f;
-  if (H % 8 || ((uintptr_t)src | (uintptr_t)dst) % 16) {
+  if (H % 8 || ((uintptr_t)src | (uintptr_t)dst | (uintptr_t)xw | (uintptr_t)xw_norm) % 16) {
     for (int64_t i = t; i < H; i += 256) {
       const float v = bf16_bits_to_f32(src[i]);
       dst[i] = v;
+      if (xw) xw[i] = f32_to_bf16_bits(v * xw_norm[i]);
       ss += v * v;
     }
     return ss;
@@ -67,6 +70,13 @@ __device__ __forceinline__ float embed_row(const uint16_t *src, float *dst, int6
       float4 *d = (float4 *)(dst + 8 * (p0 + 256 * q));
       d[0] = float4{f[0], f[1], f[2], f[3]};
       d[1] = float4{f[4], f[5], f[6], f[7]};
+      if (xw) {
+        const float4 *wn = (const float4 *)(xw_norm + 8 * (p0 + 256 * q));
+        const float4 w0 = wn[0], w1 = wn[1];
+        *(u32x4 *)(xw + 8 * (p0 + 256 * q)) =
+            u32x4{pack_bf16x2(f[0] * w0.x, f[1] * w0.y), pack_bf16x2(f[2] * w0.z, f[3] * w0.w),
+                  pack_bf16x2(f[4] * w1.x, f[5] * w1.y), pack_bf16x2(f[6] * w1.z, f[7] * w1.w)};
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
     }
@@ -82,6 +92,8 @@ struct EmbedArgs {
   const int32_t *lens;    // optional [B]: write the positions below
   int32_t *pos, *row_seq, *row_len;  // [T]
   int s;                  // tokens per sequence
+  const float *xw_norm;   // optional [H]: also write xw [T, H] = bf16(row * xw_norm)
+  uint16_t *xw;
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_dec_embed(EmbedArgs a) {
@@ -96,7 +108,8 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_embed(EmbedArgs a) {
   }
   int64_t id = a.ids[t];
   id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
-  float ss = embed_row(a.table + id * a.H, a.h + t * a.H, a.H, threadIdx.x);
+  float ss = embed_row(a.table + id * a.H, a.h + t * a.H, a.H, threadIdx.x, a.xw_norm,
+                       a.xw ? a.xw + t * a.H : nullptr);
   if (a.ss) {
     ss = block_sum_256(ss, red);
     if (threadIdx.x == 0) a.ss[t] = ss;
@@ -416,6 +429,8 @@ struct ArgmaxFinalArgs {
   float *ss;              // optional [rows]
   int32_t *pos, *row_seq, *row_len;  // [rows]
   int64_t V, H;
+  const float *xw_norm;   // optional [H]: also write xw [rows, H] = bf16(row * xw_norm)
+  uint16_t *xw;
 };
 
 extern "C" __global__ void __launch_bounds__(1024) rxw8_dec_argmax_final(ArgmaxFinalArgs a) {
@@ -456,7 +471,8 @@ extern "C" __global__ void __launch_bounds__(1024) rxw8_dec_argmax_final(ArgmaxF
     if (r < a.rows) {
       int64_t id = a.next[r];
       id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
-      ss = embed_row(a.table + id * a.H, a.h + (int64_t)r * a.H, a.H, t);
+      ss = embed_row(a.table + id * a.H, a.h + (int64_t)r * a.H, a.H, t, a.xw_norm,
+                     a.xw ? a.xw + (int64_t)r * a.H : nullptr);
       if (t == 0) {
         const int p = a.lens[r];
         a.pos[r] = p;

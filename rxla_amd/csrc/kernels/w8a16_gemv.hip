@@ -73,6 +73,17 @@ struct GemvArgs {
   // straight into LDS -- no registers, every copy of the workgroup in flight
   // at once
   int lds_dma;
+  // RMSNorm applied after the product (x_mode 0, ksplit 1, ss_parts <= 256;
+  // host-checked): the rows of x hold
+  // bf16(h * norm_w) and row b's result is multiplied by
+  // 1/sqrt(sum_p ss_in[p * M + b] / K + eps) before the scale and epilogue.
+  // The factors live in LDS at byte offset rs_off.
+  int row_norm;
+  int rs_off;
+  // y_mode 1 with ss_out (optional): also write xw_out[b * N + n] =
+  // bf16(h_new * xw_norm[n]), the next RMSNorm's weighted rows
+  const float *xw_norm;
+  uint16_t *xw_out;
 };
 
 struct SplitkReduceArgs {
@@ -89,9 +100,11 @@ namespace {
 constexpr int kXPad = 8;  // bf16 elements of padding per staged activation row
 
 // Returns the squared norm of the updated residual values (y_mode 1, with h0
-// the residual values loaded earlier), else 0.
+// the residual values loaded earlier), else 0. With xw_out (y_mode 1), also
+// writes the updated values times the next RMSNorm's weights as bf16.
 __device__ __forceinline__ float store_out(void *y, int y_f32, int y_mode, int64_t N, int b, int n,
-                                           f32x4 v, float4 h0) {
+                                           f32x4 v, float4 h0, const float *xw_norm = nullptr,
+                                           uint16_t *xw_out = nullptr) {
   if (y_mode == 1) {  // residual: h += f32(bf16(result)) (layers.rs:295-296 + add)
     float4 *h = (float4 *)((float *)y + (int64_t)b * N + n);
     float4 o = h0;
@@ -100,6 +113,11 @@ __device__ __forceinline__ float store_out(void *y, int y_f32, int y_mode, int64
     o.z += round_bf16(v[2]);
     o.w += round_bf16(v[3]);
     *h = o;
+    if (xw_out) {
+      const float4 w = *(const float4 *)(xw_norm + n);
+      *(uint2 *)(xw_out + (int64_t)b * N + n) =
+          uint2{pack_bf16x2(o.x * w.x, o.y * w.y), pack_bf16x2(o.z * w.z, o.w * w.w)};
+    }
     return ((o.x * o.x + o.y * o.y) + o.z * o.z) + o.w * o.w;
   } else if (y_f32) {
     float4 o = {round_bf16(v[0]), round_bf16(v[1]), round_bf16(v[2]), round_bf16(v[3])};
@@ -314,15 +332,39 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, uint16_t *xs, int k0,
   stage_rows(a.x, a.x_f32 != 0, a.x_stride, a.x_off + k0, a.M, per_row, xs, ldx, threadIdx.x, nt);
 }
 
+// row_norm: the wave loads row b's partial sums of squares, lane l taking
+// partials l, l + 64, l + 128, l + 192 (ss_parts <= 256); rows b >= M load
+// nothing.
+__device__ __forceinline__ void row_norm_load(const GemvArgs &a, int b, float (&v)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int p = lane + 64 * s;
+    v[s] = b < a.M && p < a.ss_parts ? a.ss_in[(int64_t)p * a.M + b] : 0.f;
+  }
+}
+
+// Sums them (the order of the x_mode 3 prologue, so the factor has the same
+// bits) and stores row b's factor 1/sqrt(mean + eps) in LDS at rs_off.
+__device__ __forceinline__ void row_norm_store(const GemvArgs &a, int b, const float (&v)[4],
+                                               void *lds) {
+  const float ss = wave_sum64(((v[0] + v[1]) + v[2]) + v[3]);
+  if ((threadIdx.x & 63) == 0 && b < a.M)
+    ((float *)((char *)lds + a.rs_off))[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+}
+
 // Reduce the KW k-slices of each row group through LDS (slice order), then
 // write the tile (ksplit == 1, scaled here when per-channel) or its partial.
-template <int MB, int RW, int NW = 4>
+// With row_norm, every wave of the workgroup calls this after storing its
+// rows' factors in LDS (at rs_off); the first barrier here publishes them.
+template <int MB, int RW, int NW = 4, bool RN = false>
 __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int rows0, int sp,
                                             f32x4 (&total)[MB], bool scale_here) {
   constexpr int KW = NW / RW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int rg = wave % RW, kq = wave / RW;
+  if (KW == 1 && RN) __syncthreads();
   if (KW > 1) {
     __syncthreads();  // staged x/scales are no longer read; reuse LDS
     if (kq > 0)
@@ -338,6 +380,11 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
         total[mb] += *(const f32x4 *)(red + (((q - 1) * RW + rg) * MB + mb) * 256 + lane * 4);
   }
   const int j = lane >> 4, col = lane & 15;
+  if (RN) {
+    const float *rs = (const float *)((const char *)red + a.rs_off);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) total[mb] *= rs[min(col + 16 * mb, a.M - 1)];
+  }
   const int n = rows0 + rg * 16 + 4 * j;
   if (n >= a.N) return;  // uniform per wave when N % 16 == 0 (the only case modes 2 and ss use)
   if (a.ksplit > 1) {
@@ -378,7 +425,8 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
     const int b = col + 16 * mb;
     float ss = b < a.M ? store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, total[mb] * sc,
                                    a.y_mode == 1 ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
-                                                 : float4{0.f, 0.f, 0.f, 0.f})
+                                                 : float4{0.f, 0.f, 0.f, 0.f},
+                                   a.xw_norm, a.xw_out)
                        : 0.f;
     if (a.ss_out) {  // 4 lanes (j) hold the group's 16 channels of row b
       ss = sum_xor16(ss);
@@ -401,7 +449,8 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 // with the weights in the same double-buffered groups: no LDS staging, no
 // barrier before the stream, and LDS only for the cross-wave reduction (so it
 // does not limit how many workgroups a CU holds).
-template <int MB, int RW, int U, bool PK, int NW = 4, bool XG = false>
+// RN: row_norm (the _rn kernels; the host sets a.row_norm for them only).
+template <int MB, int RW, int U, bool PK, int NW = 4, bool XG = false, bool RN = false>
 __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   constexpr int KW = NW / RW;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -464,6 +513,11 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   };
   // The first weight group is in flight while x and the scales are staged.
   load_group(bufA, xgA, 0);
+  // row_norm: the partials arrive during the stream and are reduced after it
+  // (KW > 1: finish_tile's first barrier publishes the factors)
+  // (wave w: row w; rows past the wave count are loaded after the stream)
+  float rnv[4];
+  if (RN) row_norm_load(a, wave, rnv);
 
   // Plain activation rows with per-channel scales (when the host chose it):
   // every wave stages only its own K slice of the rows, in its own LDS region
@@ -558,13 +612,20 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   if (per_channel)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) total[mb] = acc[mb] - 128.f * ones[mb];
-  finish_tile<MB, RW, NW>(a, (float *)xs, rows0, sp, total, per_channel);
+  if (RN) {
+    row_norm_store(a, wave, rnv, xs);
+    for (int b = wave + NW; b < a.M; b += NW) {  // rows beyond the wave count
+      row_norm_load(a, b, rnv);
+      row_norm_store(a, b, rnv, xs);
+    }
+  }
+  finish_tile<MB, RW, NW, RN>(a, (float *)xs, rows0, sp, total, per_channel);
 }
 
 // Dense bf16 weights (lm_head): one 16-byte slice = one MFMA A-fragment.
 // PK: tiled layout [N/16][K/32][64 lanes][16 B], lane l holding
 // W[16t + l%16][32c + 8(l/16) .. +8] (rxw8_pack_bf16 builds it).
-template <int MB, int RW, int U, bool PK>
+template <int MB, int RW, int U, bool PK, bool RN = false>
 __device__ __forceinline__ void gemv_bf16(const GemvArgs &a) {
   constexpr int KW = 4 / RW;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -600,7 +661,19 @@ __device__ __forceinline__ void gemv_bf16(const GemvArgs &a) {
 #pragma unroll
   for (int u = 0; u < U; ++u)
     bufA[u] = __builtin_nontemporal_load((const u32x4 *)(wrow + (int64_t)min(u, last) * wstep));
+  // row_norm: the factors are published by the staging barrier (KW may be
+  // 1); wave w takes rows w, w + 4, ... (the first row's partials load
+  // while x is staged)
+  float rnv[4];
+  if (RN) row_norm_load(a, wave, rnv);
   stage_x(a, xs, k0, Kc);
+  if (RN) {
+    row_norm_store(a, wave, rnv, xs);
+    for (int b = wave + 4; b < a.M; b += 4) {
+      row_norm_load(a, b, rnv);
+      row_norm_store(a, b, rnv, xs);
+    }
+  }
   __syncthreads();
 
   f32x4 total[MB];
@@ -633,7 +706,7 @@ __device__ __forceinline__ void gemv_bf16(const GemvArgs &a) {
       for (int u = 0; u < U; ++u) process(bufB[u], c0 + U + u);
     }
   }
-  finish_tile<MB, RW>(a, (float *)xs, rows0, sp, total, false);
+  finish_tile<MB, RW, 4, RN>(a, (float *)xs, rows0, sp, total, false);
 }
 
 }  // namespace
@@ -736,6 +809,65 @@ RXW8_GEMV_WIDE_U(1, 6, 12)
 // 14 waves over K (K = 14 x 256, e.g. 3584) for narrow N in one launch
 RXW8_GEMV_WIDE_U(1, 1, 14)
 RXW8_GEMV_WIDE_U(2, 1, 14)
+
+// Row-norm variants (packed weights, up to 16 rows): the decoder's projections
+// whose rows are bf16(h * norm weight), and its bf16 lm_head. Names: the
+// plain kernel's name + "_rn".
+#define RXW8_GEMV_XG_RN(RW, U, NW)                                              \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                         \
+      rxw8_gemv_w8_pk_mb1_rw##RW##_u##U##_w##NW##_xg_rn(GemvArgs a) {           \
+    gemv_w8<1, RW, U, true, NW, true, true>(a);                                 \
+  }
+#define RXW8_GEMV_WIDE_RN(RW, U, NW)                                            \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                         \
+      rxw8_gemv_w8_pk_mb1_rw##RW##_u##U##_w##NW##_rn(GemvArgs a) {              \
+    gemv_w8<1, RW, U, true, NW, false, true>(a);                                \
+  }                                                                             \
+  RXW8_GEMV_XG_RN(RW, U, NW)
+#define RXW8_GEMV_WIDE_RN_U(RW, NW) \
+  RXW8_GEMV_WIDE_RN(RW, 4, NW)      \
+  RXW8_GEMV_WIDE_RN(RW, 3, NW)      \
+  RXW8_GEMV_WIDE_RN(RW, 2, NW)      \
+  RXW8_GEMV_WIDE_RN(RW, 1, NW)
+RXW8_GEMV_WIDE_RN_U(1, 8)
+RXW8_GEMV_WIDE_RN_U(2, 8)
+RXW8_GEMV_WIDE_RN_U(4, 8)
+RXW8_GEMV_WIDE_RN_U(3, 12)
+RXW8_GEMV_WIDE_RN_U(6, 12)
+RXW8_GEMV_WIDE_RN_U(1, 16)
+RXW8_GEMV_WIDE_RN_U(2, 16)
+RXW8_GEMV_WIDE_RN_U(4, 16)
+RXW8_GEMV_WIDE_RN_U(1, 14)
+// 4-wave plans: the staged kernels (U up to 8) and the XG ones (U up to 4)
+#define RXW8_GEMV_RN4(RW, U)                                                    \
+  extern "C" __global__ void __launch_bounds__(256)                             \
+      rxw8_gemv_w8_pk_mb1_rw##RW##_u##U##_rn(GemvArgs a) {                      \
+    gemv_w8<1, RW, U, true, 4, false, true>(a);                                 \
+  }
+#define RXW8_GEMV_RN4_U(RW) \
+  RXW8_GEMV_RN4(RW, 8)      \
+  RXW8_GEMV_RN4(RW, 4)      \
+  RXW8_GEMV_RN4(RW, 2)      \
+  RXW8_GEMV_RN4(RW, 1)      \
+  RXW8_GEMV_XG_RN(RW, 4, 4) \
+  RXW8_GEMV_XG_RN(RW, 3, 4) \
+  RXW8_GEMV_XG_RN(RW, 2, 4) \
+  RXW8_GEMV_XG_RN(RW, 1, 4)
+RXW8_GEMV_RN4_U(1)
+RXW8_GEMV_RN4_U(4)
+#define RXW8_GEMV_BF16_RN(RW, U)                                                \
+  extern "C" __global__ void __launch_bounds__(256)                             \
+      rxw8_gemv_bf16_pk_mb1_rw##RW##_u##U##_rn(GemvArgs a) {                    \
+    gemv_bf16<1, RW, U, true, true>(a);                                         \
+  }
+RXW8_GEMV_BF16_RN(1, 8)
+RXW8_GEMV_BF16_RN(1, 4)
+RXW8_GEMV_BF16_RN(1, 2)
+RXW8_GEMV_BF16_RN(1, 1)
+RXW8_GEMV_BF16_RN(4, 8)
+RXW8_GEMV_BF16_RN(4, 4)
+RXW8_GEMV_BF16_RN(4, 2)
+RXW8_GEMV_BF16_RN(4, 1)
 
 #define RXW8_GEMV_ALL(KIND) \
   RXW8_GEMV_U(KIND, 1, 1)   \

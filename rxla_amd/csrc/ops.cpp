@@ -33,6 +33,10 @@ struct GemvArgs {
   int ss_parts;
   int wave_stage;
   int lds_dma;  // bf16 rows staged by LDS DMA
+  int row_norm;  // RMSNorm factor applied after the product (x = bf16(h * w))
+  int rs_off;    // LDS byte offset of the row factors
+  const float *xw_norm;
+  uint16_t *xw_out;
 };
 
 struct PackArgs {
@@ -397,6 +401,13 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
   // 16-channel groups; one chunk of rows keeps the partial layout [g][M]
   if ((pro->swiglu || pro->ss_out) && (p.ks != 1 || N % 16 || M > mchunk)) return RXW8_UNIMPLEMENTED;
   if (pro->mode == 3 && M > mchunk) return RXW8_UNIMPLEMENTED;
+  // the post-product RMSNorm reads its rows' partials (one chunk of rows,
+  // at most 256 partials per row) and needs the whole sum in one launch
+  // (kernels for packed weights and up to 16 rows)
+  if (pro->row_norm && (pro->mode != 0 || x_f32 || !pro->ss_in || pro->ss_parts < 1 ||
+                        pro->ss_parts > 256 || M > 16 || p.ks != 1 || !packed))
+    return RXW8_UNIMPLEMENTED;
+  if (pro->xw_out && (y_mode != 1 || p.ks != 1 || M > mchunk || N % 4)) return RXW8_UNIMPLEMENTED;
   const int64_t tiles = (N + 16 * p.rw - 1) / (16 * p.rw);
   const size_t xe = x_f32 ? 4 : 2, ye = y_f32 ? 4 : 2;
   if (p.ks > 1) {
@@ -443,10 +454,19 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
       std::snprintf(wide, sizeof wide, "_w%d_xg", p.nw);
     else if (p.nw != 4)
       std::snprintf(wide, sizeof wide, "_w%d", p.nw);
-    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s_mb%d_rw%d_u%d%s", w_bf16 ? "bf16" : "w8",
-                  packed ? "_pk" : "", mb, p.rw, u, wide);
-    const size_t lds = xg ? (size_t)(p.nw / p.rw - 1) * p.rw * mb * 256 * 4 + 16
-                          : gemv_lds(mm, K / p.ks, K, G, p.rw, mb, w_bf16, p.nw);
+    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s_mb%d_rw%d_u%d%s%s", w_bf16 ? "bf16" : "w8",
+                  packed ? "_pk" : "", mb, p.rw, u, wide, pro->row_norm ? "_rn" : "");
+    size_t lds = xg ? (size_t)(p.nw / p.rw - 1) * p.rw * mb * 256 * 4 + 16
+                    : gemv_lds(mm, K / p.ks, K, G, p.rw, mb, w_bf16, p.nw);
+    a.row_norm = pro->row_norm ? 1 : 0;
+    a.rs_off = 0;
+    if (pro->row_norm) {  // the row factors follow everything else in LDS
+      lds = (lds + 15) / 16 * 16;
+      a.rs_off = (int)lds;
+      lds += 32 * sizeof(float);
+    }
+    a.xw_norm = pro->xw_norm;
+    a.xw_out = pro->xw_out;
     // bf16 rows whose split is whole 512-element runs, 16-byte aligned, are
     // staged by LDS DMA (B = 16, K = 4096: 8.9 -> 7.4 us for N = 4096).
     // RXW8_GEMV_LDS_DMA=0 turns it off.

@@ -180,6 +180,43 @@ def test_rope_kv_kernels_agree(rt, monkeypatch, qk_norm):
         assert err <= 1e-2
 
 
+@pytest.mark.parametrize("group,batch", [(0, 3), (128, 3), (0, 16)])
+def test_post_product_norm_matches_staged_norm(rt, monkeypatch, group, batch):
+    """Fused steps apply the input, post-attention and final RMSNorms after
+    their projections (the producers write bf16(h * w), the consumer GEMV
+    multiplies each row's result by 1/sqrt(mean(h^2) + eps)); RXW8_DEC_ROW_NORM=0
+    normalises the rows while staging them instead. Both against the oracle,
+    over a prompt and 4 decode steps; batch 16 has more rows than the 8-wave
+    kernels have waves, grouped scales take the staged (non-XG) kernels."""
+    cfg = small_cfg(group=group)
+    params = tiny_params(cfg, seed=97 + group + batch, std=0.05)
+    rng = np.random.default_rng(98)
+    prompt = rng.integers(0, cfg["vocab"], (batch, 1 if batch > 3 else 5)).astype(np.int32)
+    dec = oracle.Decoder(cfg, params, batch)
+    ids, want, feeds = prompt, [], [prompt]
+    for _ in range(5):  # every side takes the oracle's greedy ids
+        lg, nxt = dec.forward(ids)
+        want.append(lg)
+        ids = nxt.reshape(batch, 1).astype(np.int32)
+        feeds.append(ids)
+    got = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("RXW8_DEC_ROW_NORM", mode)
+        model = build(rt, cfg, params, batch)
+        seq = []
+        for step in range(5):
+            out = rt.zeros((batch, cfg["vocab"]), rx().DType.F32)
+            model.forward(rt.buffer(feeds[step]), logits=out)
+            seq.append(out.to_numpy())
+            err = rel_err(seq[-1], want[step])
+            print(f"row_norm={mode} group={group} batch={batch} step {step} rel_err={err:.3e}")
+            assert err <= 1e-2
+        got[mode] = np.stack(seq)
+    err = rel_err(got["1"], got["0"])
+    print(f"row_norm on vs off: rel_err={err:.3e}")
+    assert err <= 1e-2
+
+
 def test_decoder_prefill_kernel_matches_rowwise(rt, monkeypatch):
     """Prompts of >= 16 rows take the causal prefill kernel; the row-wise
     decode kernel (RXW8_DEC_ROWWISE_PREFILL=1) must give the same logits, for
