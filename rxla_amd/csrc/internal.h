@@ -40,6 +40,10 @@ struct GemvOptions {
   // y_mode 1 with ss_out: also write xw_out[b, n] = bf16(h_new[b, n] * xw_norm[n])
   const float *xw_norm = nullptr;
   uint16_t *xw_out = nullptr;
+  // compute dtype F32 (packed weights): f32 x rows split into bf16 hi + lo
+  // parts, exact codes u - 128, f32 results without bf16 rounding (modes 0,
+  // 1, 3; y_mode 0 / 1 and swiglu; no row_norm / xw_out)
+  bool f32c = false;
 };
 
 // Records the thread-local error message and returns `code`.

@@ -44,6 +44,16 @@ __device__ __forceinline__ uint2 u8x4_to_bf16x4(uint32_t w) {
   return uint2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
 }
 
+// Four u8 codes of one dword -> two dwords of the bf16 pairs of u - 128
+// (exact: -128..127 fit bf16's 8 significant bits).
+__device__ __forceinline__ uint2 u8x4_to_signed_bf16x4(uint32_t w) {
+  float f0 = (float)(w & 0xffu) - 128.f;
+  float f1 = (float)((w >> 8) & 0xffu) - 128.f;
+  float f2 = (float)((w >> 16) & 0xffu) - 128.f;
+  float f3 = (float)(w >> 24) - 128.f;
+  return uint2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
+}
+
 // The values of lanes l and l ^ 16 (resp. l ^ 32), in some order, through
 // v_permlane16_swap / v_permlane32_swap with both operands v: a VALU exchange
 // instead of an LDS round trip (ds_bpermute). Combined with a commutative

@@ -55,9 +55,16 @@ __device__ __forceinline__ float embed_row(const uint16_t *src, float *dst, int6
   const int64_t pieces = H / 8;
   for (int64_t p0 = t; p0 < pieces; p0 += 4 * 256) {
     u32x4 v[4];
+    float4 wn[4][2];  // the norm weights load with the row (not after the stores)
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (p0 + 256 * q < pieces) v[q] = *(const u32x4 *)(src + 8 * (p0 + 256 * q));
+      if (p0 + 256 * q < pieces) {
+        v[q] = *(const u32x4 *)(src + 8 * (p0 + 256 * q));
+        if (xw) {
+          wn[q][0] = *(const float4 *)(xw_norm + 8 * (p0 + 256 * q));
+          wn[q][1] = *(const float4 *)(xw_norm + 8 * (p0 + 256 * q) + 4);
+        }
+      }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if (p0 + 256 * q >= pieces) break;
@@ -71,8 +78,7 @@ __device__ __forceinline__ float embed_row(const uint16_t *src, float *dst, int6
       d[0] = float4{f[0], f[1], f[2], f[3]};
       d[1] = float4{f[4], f[5], f[6], f[7]};
       if (xw) {
-        const float4 *wn = (const float4 *)(xw_norm + 8 * (p0 + 256 * q));
-        const float4 w0 = wn[0], w1 = wn[1];
+        const float4 w0 = wn[q][0], w1 = wn[q][1];
         *(u32x4 *)(xw + 8 * (p0 + 256 * q)) =
             u32x4{pack_bf16x2(f[0] * w0.x, f[1] * w0.y), pack_bf16x2(f[2] * w0.z, f[3] * w0.w),
                   pack_bf16x2(f[4] * w1.x, f[5] * w1.y), pack_bf16x2(f[6] * w1.z, f[7] * w1.w)};

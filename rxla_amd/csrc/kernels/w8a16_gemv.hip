@@ -84,6 +84,10 @@ struct GemvArgs {
   // bf16(h_new * xw_norm[n]), the next RMSNorm's weighted rows
   const float *xw_norm;
   uint16_t *xw_out;
+  // row stride of the sum-of-squares partials (ss_in[p * ss_ld + b],
+  // ss_out[g * ss_ld + b]): the rows of the whole product when the host runs
+  // it in chunks of rows (the pointers then start at the chunk)
+  int ss_ld;
 };
 
 struct SplitkReduceArgs {
@@ -102,9 +106,11 @@ constexpr int kXPad = 8;  // bf16 elements of padding per staged activation row
 // Returns the squared norm of the updated residual values (y_mode 1, with h0
 // the residual values loaded earlier), else 0. With xw_out (y_mode 1), also
 // writes the updated values times the next RMSNorm's weights as bf16.
+// (The caller loads h0 and w together: a load placed after the store of h
+// could alias it and would wait for that store.)
 __device__ __forceinline__ float store_out(void *y, int y_f32, int y_mode, int64_t N, int b, int n,
-                                           f32x4 v, float4 h0, const float *xw_norm = nullptr,
-                                           uint16_t *xw_out = nullptr) {
+                                           f32x4 v, float4 h0, uint16_t *xw_out = nullptr,
+                                           float4 w = float4{0.f, 0.f, 0.f, 0.f}) {
   if (y_mode == 1) {  // residual: h += f32(bf16(result)) (layers.rs:295-296 + add)
     float4 *h = (float4 *)((float *)y + (int64_t)b * N + n);
     float4 o = h0;
@@ -113,11 +119,9 @@ __device__ __forceinline__ float store_out(void *y, int y_f32, int y_mode, int64
     o.z += round_bf16(v[2]);
     o.w += round_bf16(v[3]);
     *h = o;
-    if (xw_out) {
-      const float4 w = *(const float4 *)(xw_norm + n);
+    if (xw_out)
       *(uint2 *)(xw_out + (int64_t)b * N + n) =
           uint2{pack_bf16x2(o.x * w.x, o.y * w.y), pack_bf16x2(o.z * w.z, o.w * w.w)};
-    }
     return ((o.x * o.x + o.y * o.y) + o.z * o.z) + o.w * o.w;
   } else if (y_f32) {
     float4 o = {round_bf16(v[0]), round_bf16(v[1]), round_bf16(v[2]), round_bf16(v[3])};
@@ -203,6 +207,107 @@ __device__ __forceinline__ void lds_dma16(const void *g, void *l_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void *)l_base, 16, 0, 0);
 }
 
+// FC (compute dtype F32): stage f32 rows x[0:M, k0:k0+Kc] as their bf16
+// parts, hi = bf16(v) in LDS row b and lo = bf16(v - hi) in row LO + b
+// (|v - hi - lo| <= 2^-17 |v|), with v the row value (x_mode 0) or its
+// RMSNorm (h * factor) * w (modes 1, 3, the f32 value the reference's norm
+// produces). Pieces of 8 values, SB of them loaded before any is stored.
+__device__ __forceinline__ void norm_row_scales(const GemvArgs &a, float *row_scale, float *red);
+__device__ __forceinline__ void stage_x_fc(const GemvArgs &a, uint16_t *xs, int k0, int Kc, int LO) {
+  const int ldx = Kc + kXPad;
+  const int per_row = Kc / 8;
+  const int total = a.M * per_row;
+  const int nt = blockDim.x;
+  const bool norm = a.x_mode == 1 || a.x_mode == 3;
+  __shared__ float red[4];
+  __shared__ float row_scale[16];
+  if (norm) {
+    norm_row_scales(a, row_scale, red);
+    __syncthreads();
+  }
+  constexpr int SB = 2;
+  for (int i0 = threadIdx.x; i0 < total; i0 += SB * nt) {
+    float4 hv[SB][2], wv[SB][2];
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+      const int i = i0 + s * nt;
+      if (i < total) {
+        const int b = i / per_row, kk = (i - b * per_row) * 8;
+        const float *h = (const float *)a.x + b * a.x_stride + a.x_off + k0 + kk;
+        hv[s][0] = *(const float4 *)h;
+        hv[s][1] = *(const float4 *)(h + 4);
+        if (norm) {
+          wv[s][0] = *(const float4 *)(a.norm_w + k0 + kk);
+          wv[s][1] = *(const float4 *)(a.norm_w + k0 + kk + 4);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < SB; ++s) {
+      const int i = i0 + s * nt;
+      if (i < total) {
+        const int b = i / per_row, kk = (i - b * per_row) * 8;
+        float v[8] = {hv[s][0].x, hv[s][0].y, hv[s][0].z, hv[s][0].w,
+                      hv[s][1].x, hv[s][1].y, hv[s][1].z, hv[s][1].w};
+        if (norm) {
+          const float sc = row_scale[b];
+          const float w[8] = {wv[s][0].x, wv[s][0].y, wv[s][0].z, wv[s][0].w,
+                              wv[s][1].x, wv[s][1].y, wv[s][1].z, wv[s][1].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (v[e] * sc) * w[e];
+        }
+        u32x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float h0 = round_bf16(v[2 * e]), h1 = round_bf16(v[2 * e + 1]);
+          hi[e] = pack_bf16x2(h0, h1);
+          lo[e] = pack_bf16x2(v[2 * e] - h0, v[2 * e + 1] - h1);
+        }
+        *(u32x4 *)(xs + b * ldx + kk) = hi;
+        *(u32x4 *)(xs + (LO + b) * ldx + kk) = lo;
+      }
+    }
+  }
+}
+
+// RMSNorm factors 1/sqrt(mean(h^2) + eps) of rows [0, M) into row_scale
+// (LDS; the caller's barrier publishes them). Mode 3: the sums of squares
+// from the producer's partials, one wave per row, lane l adding partials l,
+// l + 64, ... in that order (loads issued in batches of 4), then a fixed
+// butterfly (deterministic). Mode 1: each row summed with the thread stride
+// and block reduction of rxw8_dec_rmsnorm (256-thread workgroups only,
+// host-checked).
+__device__ __forceinline__ void norm_row_scales(const GemvArgs &a, float *row_scale, float *red) {
+  const int nt = blockDim.x;
+  if (a.x_mode == 3) {
+    const int lane = threadIdx.x & 63, nwaves = nt >> 6;
+    for (int b = threadIdx.x >> 6; b < a.M; b += nwaves) {
+      float ss = 0.f;
+      for (int p0 = lane; p0 < a.ss_parts; p0 += 256) {
+        float t[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int p = p0 + 64 * s;
+          t[s] = p < a.ss_parts ? a.ss_in[(int64_t)p * a.ss_ld + b] : 0.f;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          if (p0 + 64 * s < a.ss_parts) ss += t[s];
+      }
+      ss = wave_sum64(ss);
+      if (lane == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+    }
+  } else {
+    for (int b = 0; b < a.M; ++b) {
+      const float *h = (const float *)a.x + b * a.x_stride + a.x_off;
+      float ss = 0.f;
+      for (int i = threadIdx.x; i < a.K; i += nt) ss += h[i] * h[i];
+      ss = block_sum_256(ss, red);
+      if (threadIdx.x == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+    }
+  }
+}
+
 // Stage x[0:M, k0:k0+Kc] as bf16 into LDS rows of stride Kc + kXPad, applying
 // the activation prologue (x_mode). Mode 1 sums each full row first with the
 // same thread stride and block reduction as rxw8_dec_rmsnorm, so the staged
@@ -260,36 +365,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, uint16_t *xs, int k0,
         }
       }
     };
-    if (a.x_mode == 3) {
-      // sums of squares from the producer's partials: one wave per row, lane
-      // l adds partials l, l + 64, ... in that order (loads issued in batches
-      // of 4), then a fixed butterfly (deterministic)
-      const int lane = threadIdx.x & 63, nwaves = nt >> 6;
-      for (int b = threadIdx.x >> 6; b < a.M; b += nwaves) {
-        float ss = 0.f;
-        for (int p0 = lane; p0 < a.ss_parts; p0 += 256) {
-          float t[4];
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const int p = p0 + 64 * s;
-            t[s] = p < a.ss_parts ? a.ss_in[(int64_t)p * a.M + b] : 0.f;
-          }
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            if (p0 + 64 * s < a.ss_parts) ss += t[s];
-        }
-        ss = wave_sum64(ss);
-        if (lane == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-      }
-    } else {  // mode 1: 256-thread workgroups only (host-checked)
-      for (int b = 0; b < a.M; ++b) {
-        const float *h = (const float *)a.x + b * a.x_stride + a.x_off;
-        float ss = 0.f;
-        for (int i = threadIdx.x; i < a.K; i += nt) ss += h[i] * h[i];
-        ss = block_sum_256(ss, red);
-        if (threadIdx.x == 0) row_scale[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-      }
-    }
+    norm_row_scales(a, row_scale, red);
     __syncthreads();
     for (int i0 = threadIdx.x; i0 < total; i0 += SB * nt) {
       fetch(i0);
@@ -340,7 +416,7 @@ __device__ __forceinline__ void row_norm_load(const GemvArgs &a, int b, float (&
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int p = lane + 64 * s;
-    v[s] = b < a.M && p < a.ss_parts ? a.ss_in[(int64_t)p * a.M + b] : 0.f;
+    v[s] = b < a.M && p < a.ss_parts ? a.ss_in[(int64_t)p * a.ss_ld + b] : 0.f;
   }
 }
 
@@ -353,11 +429,66 @@ __device__ __forceinline__ void row_norm_store(const GemvArgs &a, int b, const f
     ((float *)((char *)lds + a.rs_off))[b] = 1.0f / sqrtf(ss / (float)a.K + a.eps);
 }
 
+// FC epilogue (ksplit 1, N % 16 == 0): the hi and lo sums of row t (batch
+// columns t and LO + t: the same lane for MB == 2, lanes col and col ^ 8 for
+// MB == 1) are added, scaled (per-channel) and stored as f32 without bf16
+// rounding: y_mode 0 y[t, n] = v; 1 h[t, n] += v (with ss_out); 2 (SwiGLU
+// tiles) y[t, c] = silu(gate) * up.
+template <int MB>
+__device__ __forceinline__ void finish_fc(const GemvArgs &a, int rows0, int rg, f32x4 (&total)[MB],
+                                          bool scale_here) {
+  const int lane = threadIdx.x & 63, j = lane >> 4, col = lane & 15;
+  f32x4 v;
+  if (MB == 2) {
+    v = total[0] + total[MB - 1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = total[0][i] + __shfl_xor(total[0][i], 8);
+  }
+  const int t = col;
+  const bool valid = (MB == 2 || col < 8) && t < a.M;
+  const int n = rows0 + rg * 16 + 4 * j;
+  if (n >= a.N) return;  // uniform per wave (N % 16 == 0)
+  if (scale_here) {
+    const float4 s4 = *(const float4 *)(a.scale + n);
+    v *= f32x4{s4.x, s4.y, s4.z, s4.w};
+  }
+  if (a.y_mode == 2) {  // gate values in lanes j < 2, the matching up values 32 lanes higher
+    f32x4 up;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) up[i] = value_xor32(v[i]);
+    if (j < 2 && valid) {
+      const int c = (rows0 + rg * 16) / 2 + 4 * j;
+      *(float4 *)((float *)a.y + (int64_t)t * (a.N / 2) + c) =
+          float4{silu_mul_f32(v[0], up[0]), silu_mul_f32(v[1], up[1]), silu_mul_f32(v[2], up[2]),
+                 silu_mul_f32(v[3], up[3])};
+    }
+    return;
+  }
+  float ss = 0.f;
+  if (valid) {
+    float4 *yp = (float4 *)((float *)a.y + (int64_t)t * a.N + n);
+    if (a.y_mode == 1) {  // f32 residual: h += result
+      float4 o = *yp;
+      o.x += v[0], o.y += v[1], o.z += v[2], o.w += v[3];
+      *yp = o;
+      ss = ((o.x * o.x + o.y * o.y) + o.z * o.z) + o.w * o.w;
+    } else {
+      *yp = float4{v[0], v[1], v[2], v[3]};
+    }
+  }
+  if (a.ss_out) {  // 4 lanes (j) hold the group's 16 channels of row t
+    ss = sum_xor16(ss);
+    ss = sum_xor32(ss);
+    if (j == 0 && valid) a.ss_out[(int64_t)((rows0 + rg * 16) / 16) * a.ss_ld + t] = ss;
+  }
+}
+
 // Reduce the KW k-slices of each row group through LDS (slice order), then
 // write the tile (ksplit == 1, scaled here when per-channel) or its partial.
 // With row_norm, every wave of the workgroup calls this after storing its
 // rows' factors in LDS (at rs_off); the first barrier here publishes them.
-template <int MB, int RW, int NW = 4, bool RN = false>
+template <int MB, int RW, int NW = 4, bool RN = false, bool FC = false>
 __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int rows0, int sp,
                                             f32x4 (&total)[MB], bool scale_here) {
   constexpr int KW = NW / RW;
@@ -378,6 +509,10 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
         total[mb] += *(const f32x4 *)(red + (((q - 1) * RW + rg) * MB + mb) * 256 + lane * 4);
+  }
+  if (FC) {
+    finish_fc<MB>(a, rows0, rg, total, scale_here);
+    return;
   }
   const int j = lane >> 4, col = lane & 15;
   if (RN) {
@@ -420,18 +555,19 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
     }
     return;
   }
+  const float4 xw_w = a.xw_out ? *(const float4 *)(a.xw_norm + n) : float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int b = col + 16 * mb;
     float ss = b < a.M ? store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, total[mb] * sc,
                                    a.y_mode == 1 ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
                                                  : float4{0.f, 0.f, 0.f, 0.f},
-                                   a.xw_norm, a.xw_out)
+                                   a.xw_out, xw_w)
                        : 0.f;
     if (a.ss_out) {  // 4 lanes (j) hold the group's 16 channels of row b
       ss = sum_xor16(ss);
       ss = sum_xor32(ss);
-      if (j == 0 && b < a.M) a.ss_out[(int64_t)((rows0 + rg * 16) / 16) * a.M + b] = ss;
+      if (j == 0 && b < a.M) a.ss_out[(int64_t)((rows0 + rg * 16) / 16) * a.ss_ld + b] = ss;
     }
   }
 }
@@ -450,8 +586,13 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 // barrier before the stream, and LDS only for the cross-wave reduction (so it
 // does not limit how many workgroups a CU holds).
 // RN: row_norm (the _rn kernels; the host sets a.row_norm for them only).
-template <int MB, int RW, int U, bool PK, int NW = 4, bool XG = false, bool RN = false>
+// FC: compute dtype F32 (the _fc kernels): f32 rows staged as bf16 hi / lo
+// parts (stage_x_fc; rows b and LO + b, LO = 8 MB), the codes as the exact
+// bf16 values u - 128 (no all-ones correction), f32 results (finish_fc).
+template <int MB, int RW, int U, bool PK, int NW = 4, bool XG = false, bool RN = false,
+          bool FC = false>
 __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
+  constexpr int LO = 8 * MB;  // FC: staged row of the lo part of row 0
   constexpr int KW = NW / RW;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & 63;
@@ -528,7 +669,7 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   const uint16_t *xbase = xs;
   int xld = ldx;
   const int gps = per_channel ? 0 : Kc / a.G;
-  float *ss = (float *)(xs + a.M * ldx);
+  float *ss = (float *)(xs + (FC ? 2 * LO : a.M) * ldx);
   if (XG) {
     // nothing to stage: per-channel scales are read in the epilogue
   } else if (wave_stage) {
@@ -551,7 +692,10 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
         ss[i] = n < a.N ? a.scale[(int64_t)n * groups + g0 + gl] : 0.f;
       }
     }
-    stage_x(a, xs, k0, Kc);
+    if (FC)
+      stage_x_fc(a, xs, k0, Kc, LO);
+    else
+      stage_x(a, xs, k0, Kc);
     __syncthreads();
   }
 
@@ -566,7 +710,11 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const int b = col + 16 * mb;
-      xrow[mb] = xbase + (b < a.M ? b : a.M - 1) * xld + kbase + j * 16;
+      // FC: column b < LO reads the hi part of row b, column LO + t the lo
+      // part of row t (rows clamped to M - 1, never stored)
+      const int row = FC ? (b >= LO ? LO : 0) + min(b >= LO ? b - LO : b, a.M - 1)
+                         : (b < a.M ? b : a.M - 1);
+      xrow[mb] = xbase + row * xld + kbase + j * 16;
     }
   const u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
   const bf16x8 onesf = as_bf16x8(ones_bits);
@@ -574,8 +722,14 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   // Process one 64-k chunk c (of this wave's slice) held in register slice w
   // (XG: with its activation fragments xg).
   auto process = [&](const u32x4 w, const u32x4(&xg)[MB][2], const int c) {
-    const uint2 p0 = u8x4_to_bf16x4(w[0]), p1 = u8x4_to_bf16x4(w[1]);
-    const uint2 p2 = u8x4_to_bf16x4(w[2]), p3 = u8x4_to_bf16x4(w[3]);
+    uint2 p0, p1, p2, p3;
+    if (FC) {
+      p0 = u8x4_to_signed_bf16x4(w[0]), p1 = u8x4_to_signed_bf16x4(w[1]);
+      p2 = u8x4_to_signed_bf16x4(w[2]), p3 = u8x4_to_signed_bf16x4(w[3]);
+    } else {
+      p0 = u8x4_to_bf16x4(w[0]), p1 = u8x4_to_bf16x4(w[1]);
+      p2 = u8x4_to_bf16x4(w[2]), p3 = u8x4_to_bf16x4(w[3]);
+    }
     const u32x4 a0 = {p0.x, p0.y, p1.x, p1.y}, a1 = {p2.x, p2.y, p3.x, p3.y};
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -583,17 +737,19 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
       const bf16x8 x0 = as_bf16x8(XG ? xg[mb][0] : xp[0]), x1 = as_bf16x8(XG ? xg[mb][1] : xp[1]);
       acc[mb] = mfma16x16x32(as_bf16x8(a0), x0, acc[mb]);
       acc[mb] = mfma16x16x32(as_bf16x8(a1), x1, acc[mb]);
-      ones[mb] = mfma16x16x32(onesf, x0, ones[mb]);
-      ones[mb] = mfma16x16x32(onesf, x1, ones[mb]);
+      if (!FC) {
+        ones[mb] = mfma16x16x32(onesf, x0, ones[mb]);
+        ones[mb] = mfma16x16x32(onesf, x1, ones[mb]);
+      }
     }
     if (!per_channel && ((c + 1) % chunks_per_group) == 0) {
-      // fold one scale group: total += s[n, g] * (acc - 128 * ones)
+      // fold one scale group: total += s[n, g] * (acc - 128 * ones) (FC: acc)
       const int gl = (kbase + c * 64) / a.G;
       const float *srow = ss + (rg * 16 + 4 * j) * gps + gl;
       const f32x4 sc = {srow[0], srow[gps], srow[2 * gps], srow[3 * gps]};
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        total[mb] += sc * (acc[mb] - 128.f * ones[mb]);
+        total[mb] += sc * (FC ? acc[mb] : acc[mb] - 128.f * ones[mb]);
         acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
         ones[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
@@ -611,7 +767,7 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   }
   if (per_channel)
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) total[mb] = acc[mb] - 128.f * ones[mb];
+    for (int mb = 0; mb < MB; ++mb) total[mb] = FC ? acc[mb] : acc[mb] - 128.f * ones[mb];
   if (RN) {
     row_norm_store(a, wave, rnv, xs);
     for (int b = wave + NW; b < a.M; b += NW) {  // rows beyond the wave count
@@ -619,7 +775,7 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
       row_norm_store(a, b, rnv, xs);
     }
   }
-  finish_tile<MB, RW, NW, RN>(a, (float *)xs, rows0, sp, total, per_channel);
+  finish_tile<MB, RW, NW, RN, FC>(a, (float *)xs, rows0, sp, total, per_channel);
 }
 
 // Dense bf16 weights (lm_head): one 16-byte slice = one MFMA A-fragment.
@@ -868,6 +1024,44 @@ RXW8_GEMV_BF16_RN(4, 8)
 RXW8_GEMV_BF16_RN(4, 4)
 RXW8_GEMV_BF16_RN(4, 2)
 RXW8_GEMV_BF16_RN(4, 1)
+
+// F32-compute variants (packed weights, up to 16 rows as 2 x 16 staged
+// rows, MB = 2; up to 8 rows as 2 x 8, MB = 1). Names: plain name + "_fc".
+#define RXW8_GEMV_FC_WIDE(MB, RW, U, NW)                                        \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                         \
+      rxw8_gemv_w8_pk_mb##MB##_rw##RW##_u##U##_w##NW##_fc(GemvArgs a) {         \
+    gemv_w8<MB, RW, U, true, NW, false, false, true>(a);                        \
+  }
+#define RXW8_GEMV_FC_WIDE_U(MB, RW, NW) \
+  RXW8_GEMV_FC_WIDE(MB, RW, 4, NW)      \
+  RXW8_GEMV_FC_WIDE(MB, RW, 3, NW)      \
+  RXW8_GEMV_FC_WIDE(MB, RW, 2, NW)      \
+  RXW8_GEMV_FC_WIDE(MB, RW, 1, NW)
+#define RXW8_GEMV_FC4(MB, RW, U)                                                \
+  extern "C" __global__ void __launch_bounds__(256)                             \
+      rxw8_gemv_w8_pk_mb##MB##_rw##RW##_u##U##_fc(GemvArgs a) {                 \
+    gemv_w8<MB, RW, U, true, 4, false, false, true>(a);                         \
+  }
+#define RXW8_GEMV_FC_MB(MB)      \
+  RXW8_GEMV_FC4(MB, 1, 8)        \
+  RXW8_GEMV_FC4(MB, 1, 4)        \
+  RXW8_GEMV_FC4(MB, 1, 2)        \
+  RXW8_GEMV_FC4(MB, 1, 1)        \
+  RXW8_GEMV_FC4(MB, 4, 8)        \
+  RXW8_GEMV_FC4(MB, 4, 4)        \
+  RXW8_GEMV_FC4(MB, 4, 2)        \
+  RXW8_GEMV_FC4(MB, 4, 1)        \
+  RXW8_GEMV_FC_WIDE_U(MB, 1, 8)  \
+  RXW8_GEMV_FC_WIDE_U(MB, 2, 8)  \
+  RXW8_GEMV_FC_WIDE_U(MB, 4, 8)  \
+  RXW8_GEMV_FC_WIDE_U(MB, 1, 16) \
+  RXW8_GEMV_FC_WIDE_U(MB, 2, 16) \
+  RXW8_GEMV_FC_WIDE_U(MB, 4, 16) \
+  RXW8_GEMV_FC_WIDE_U(MB, 3, 12) \
+  RXW8_GEMV_FC_WIDE_U(MB, 1, 14)
+RXW8_GEMV_FC_MB(1)
+RXW8_GEMV_FC_MB(2)
+RXW8_GEMV_FC_WIDE_U(1, 6, 12)
 
 #define RXW8_GEMV_ALL(KIND) \
   RXW8_GEMV_U(KIND, 1, 1)   \

@@ -37,6 +37,7 @@ struct GemvArgs {
   int rs_off;    // LDS byte offset of the row factors
   const float *xw_norm;
   uint16_t *xw_out;
+  int ss_ld;  // row stride of the sum-of-squares partials
 };
 
 struct PackArgs {
@@ -467,6 +468,7 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     }
     a.xw_norm = pro->xw_norm;
     a.xw_out = pro->xw_out;
+    a.ss_ld = (int)M;  // (ss modes run as one chunk of rows)
     // bf16 rows whose split is whole 512-element runs, 16-byte aligned, are
     // staged by LDS DMA (B = 16, K = 4096: 8.9 -> 7.4 us for N = 4096).
     // RXW8_GEMV_LDS_DMA=0 turns it off.
@@ -494,6 +496,71 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
   return RXW8_OK;
 }
 
+// F32-compute GEMV (the _fc kernels): f32 rows x (x_mode 0, or the RMSNorm
+// prologues 1 / 3), packed u8 weights, f32 y (y_mode 0), f32 residual
+// (y_mode 1, optional ss_out) or f32 SwiGLU activation (y_mode 2, interleaved
+// gate|up tiles). Each f32 row is staged as two bf16 rows (hi, lo), so a
+// launch takes up to 16 rows (2 x 16 staged rows), or 8 when 32 staged rows
+// of K do not fit in LDS; longer inputs run in chunks of rows (the ss
+// partials then carry the whole product's row stride). UNIMPLEMENTED (nothing
+// launched) when no single-launch plan fits.
+static int run_gemv_fc(Runtime *rt, const float *x, const uint8_t *w, const float *scale, float *y,
+                       int64_t M, int64_t N, int64_t K, int64_t G, int y_mode, const GemvOptions *pro) {
+  GemvOptions plain;
+  if (!pro) pro = &plain;
+  if (M < 1 || N % 16 || K % 64 || (G != K && G % 64) || M > (1 << 30) || N > (1 << 30) ||
+      pro->mode == 2 || pro->row_norm || pro->xw_out || (pro->swiglu && y_mode != 0) ||
+      (pro->mode == 3 && !pro->ss_in))
+    return RXW8_UNIMPLEMENTED;
+  const bool allow_wide = pro->mode != 1;  // mode 1 sums rows with 256-thread reductions
+  GemvPlan p;
+  int rows = 0;  // staged rows per launch: 2 x 16 or 2 x 8
+  for (int r : {M > 8 ? 32 : 16, 16}) {
+    GemvPlan q = plan_gemv(rt, r, N, K, G, false, true, allow_wide);
+    if (q.ks == 1 && q.lds + 256 <= rt->lds_max) {
+      p = q;
+      rows = r;
+      break;
+    }
+  }
+  if (!rows) return RXW8_UNIMPLEMENTED;
+  const int64_t mchunk = rows / 2, mb = rows / 16;
+  char kname[64], wide[8] = "";
+  if (p.nw != 4) std::snprintf(wide, sizeof wide, "_w%d", p.nw);
+  std::snprintf(kname, sizeof kname, "rxw8_gemv_w8_pk_mb%d_rw%d_u%d%s_fc", (int)mb, p.rw, p.u, wide);
+  const int64_t xstride = pro->stride > 0 ? pro->stride : K;
+  const int64_t ycols = pro->swiglu ? N / 2 : N;
+  for (int64_t m0 = 0; m0 < M; m0 += mchunk) {
+    const int64_t mm = std::min(mchunk, M - m0);
+    GemvArgs a{};
+    a.x = x + m0 * xstride;
+    a.w = w;
+    a.scale = scale;
+    a.y = y + m0 * ycols;
+    a.M = (int)mm;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.G = (int)G;
+    a.ksplit = 1;
+    a.x_f32 = 1;
+    a.y_f32 = 1;
+    a.y_mode = pro->swiglu ? 2 : y_mode;
+    a.ss_out = pro->ss_out ? pro->ss_out + m0 : nullptr;
+    a.x_mode = pro->mode;
+    a.x_stride = xstride;
+    a.x_off = pro->off;
+    a.norm_w = pro->norm_w;
+    a.eps = pro->eps;
+    a.ss_in = pro->ss_in ? pro->ss_in + m0 : nullptr;
+    a.ss_parts = pro->ss_parts;
+    a.ss_ld = (int)M;
+    const size_t lds = gemv_lds(rows, K, K, G, p.rw, (int)mb, false, p.nw);
+    int rc = launch(rt, kname, dim3((unsigned)((N + 16 * p.rw - 1) / (16 * p.rw))), dim3(64 * p.nw), a, lds);
+    if (rc) return rc;
+  }
+  return RXW8_OK;
+}
+
 bool gemv_single_launch(const Runtime *rt, int64_t M, int64_t N, int64_t K, int64_t G) {
   return M <= 32 && N % 16 == 0 && plan_gemv(rt, M, N, K, G, false, true).ks == 1;
 }
@@ -502,6 +569,11 @@ int gemv_launch(Runtime *rt, const void *x, int x_f32, const void *w, bool w_bf1
                 const float *scale, void *y, int y_f32, int64_t M, int64_t N, int64_t K, int64_t G,
                 int y_mode, const GemvOptions &pro) {
   if (M == 0) return RXW8_OK;
+  if (pro.f32c) {
+    if (!x_f32 || !(y_f32 || y_mode == 1) || w_bf16 || !packed) return RXW8_UNIMPLEMENTED;
+    return run_gemv_fc(rt, (const float *)x, (const uint8_t *)w, scale, (float *)y, M, N, K, G,
+                       y_mode, &pro);
+  }
   return run_gemv(rt, x, x_f32, w, w_bf16, packed, scale, y, y_f32, M, N, K, G, y_mode, &pro);
 }
 
@@ -749,11 +821,15 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
   if (packed) {
     if (compute_bf16 && gemm_eligible(M, N, K, G))
       return run_gemm(rt, x, x_f32, w, true, s, y, y_f32, M, N, K, G, y_mode);
+    // F32 compute on packed weights: the _fc GEMV in chunks of rows
     int rc = compute_bf16 ? run_gemv(rt, x, x_f32, w, false, true, s, y, y_f32, M, N, K, G, y_mode)
-                          : (int)RXW8_UNIMPLEMENTED;
+             : x_f32 && y_f32
+                 ? run_gemv_fc(rt, (const float *)x, w, s, (float *)y, M, N, K, G, y_mode, nullptr)
+                 : (int)RXW8_UNIMPLEMENTED;
     if (rc == RXW8_UNIMPLEMENTED)
       return fail(RXW8_UNIMPLEMENTED,
-                  "packed W8 weights need BF16 compute and a GEMV tiling for N=%lld K=%lld G=%lld",
+                  "packed W8 weights need a GEMV tiling for N=%lld K=%lld G=%lld (F32 compute: "
+                  "N %% 16 == 0)",
                   (long long)N, (long long)K, (long long)G);
     return rc;
   }

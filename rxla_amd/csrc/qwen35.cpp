@@ -183,6 +183,11 @@ struct Layer {
   // packed copies, and the zero-centred norm weights as 1 + w
   uint8_t *out_pk = nullptr, *down_pk = nullptr;
   float *in_nw = nullptr, *post_nw = nullptr;
+  // the tile-layout copies the chained GEMVs read: in packed mode in_w / gu_w
+  // / gu_s themselves; under F32 compute (fc) extra packed copies beside the
+  // row-major ones
+  uint8_t *in_pk = nullptr, *gu_pk = nullptr;
+  float *gu_spk = nullptr;
 };
 
 }  // namespace
@@ -203,6 +208,9 @@ struct Qwen35 {
   void *fused = nullptr;
   int64_t n_in_max = 0;
   bool packed = false;  // BF16 compute and widths that allow the tile layout (decided at create)
+  // F32 compute and widths that allow the tile layout: packed copies beside
+  // the row-major weights, for the chained F32 GEMVs of short inputs
+  bool fc = false;
   bool f32c = true;     // projection compute dtype F32 (activations f32), else BF16
   int64_t esz = 4;      // bytes per element of xn, raw, gated, gu, act (4: f32, 2: bf16)
   // row sums of squares of the residual h (<= 32 rows): embedding [T], residual
@@ -381,6 +389,12 @@ int allocate(Qwen35 *m) {
   return RXW8_OK;
 }
 
+// Whether the environment switch `name` is set to 0.
+bool env_off(const char *name) {
+  const char *v = std::getenv(name);
+  return v && v[0] == '0';
+}
+
 // QuantizedLinear at the model's compute dtype on projection `p` (weight p,
 // scale p + 1): y [T, N] an activation (f32 under F32 compute, else bf16), or
 // (y_mode 1) the f32 residual [T, N] that receives y += result.
@@ -415,9 +429,9 @@ int in_proj(Qwen35 *m, const Layer &L, int64_t T) {
   if (m->chain && m->ss_cur) {
     GemvOptions o;
     o.mode = 3, o.norm_w = L.in_nw, o.eps = m->cfg.eps, o.ss_in = m->ss_cur, o.ss_parts = m->ss_parts;
-    o.prefer_ks1 = true;
-    rc = gemv_launch(m->rt, m->h, 1, L.in_w, false, true, L.in_s, m->raw, 0, T, L.n_in, m->H, m->G,
-                     0, o);
+    o.prefer_ks1 = true, o.f32c = m->f32c;
+    rc = gemv_launch(m->rt, m->h, 1, L.in_pk, false, true, L.in_s, m->raw, m->f32c ? 1 : 0, T, L.n_in,
+                     m->H, m->G, 0, o);
     if (rc != RXW8_UNIMPLEMENTED) return rc;
   }
   if ((rc = norm(m, m->h, m->f32(L.in_norm), m->xn, T, m->H, true, m->f32c))) return rc;
@@ -428,11 +442,10 @@ int in_proj(Qwen35 *m, const Layer &L, int64_t T) {
 // h += x w^T for a residual projection (packed copy w_pk in packed mode). In
 // the chained mode the GEMV also writes h's new row sums of squares to ss.
 int residual(Qwen35 *m, const uint8_t *w_pk, int p, const void *x, int x_f32, int64_t T, float *ss) {
-  if (!m->packed) return proj(m, p, x, x_f32, m->h, 1, T);
   const Param &w = m->params[(size_t)p];
   if (m->chain) {
     GemvOptions o;
-    o.prefer_ks1 = true, o.ss_out = ss;
+    o.prefer_ks1 = true, o.ss_out = ss, o.f32c = m->f32c;
     const int rc = gemv_launch(m->rt, x, x_f32, w_pk, false, true, m->f32(p + 1), m->h, 1, T,
                                w.dims[0], w.dims[1], m->G, 1, o);
     if (rc != RXW8_UNIMPLEMENTED) {
@@ -441,6 +454,7 @@ int residual(Qwen35 *m, const uint8_t *w_pk, int p, const void *x, int x_f32, in
     }
   }
   m->ss_cur = nullptr;
+  if (!m->packed) return proj(m, p, x, x_f32, m->h, 1, T);
   return qlinear_launch(m->rt, x, x_f32, w_pk, true, m->f32(p + 1), m->h, 1, T, w.dims[0],
                         w.dims[1], m->G, 1, 1);
 }
@@ -452,24 +466,24 @@ int out_proj(Qwen35 *m, const Layer &L, int p, const void *x, int x_f32, int64_t
 // h += down(silu(gate(x)) * up(x)), x = norm_post(h).
 int mlp(Qwen35 *m, const Layer &L, int64_t T) {
   Runtime *rt = m->rt;
-  int rc;
-  if (!m->packed) {
+  int rc = RXW8_UNIMPLEMENTED;
+  // chained GEMV: gate|up rows in SwiGLU order, the norm in the prologue, act
+  // = silu(gate) * up (bf16, or f32 under F32 compute) from the epilogue
+  if (m->chain && m->ss_cur) {
+    GemvOptions o;
+    o.mode = 3, o.norm_w = L.post_nw, o.eps = m->cfg.eps, o.ss_in = m->ss_cur;
+    o.ss_parts = m->ss_parts, o.swiglu = true, o.prefer_ks1 = true, o.f32c = m->f32c;
+    rc = gemv_launch(rt, m->h, 1, L.gu_pk, false, true, L.gu_spk, m->act, m->f32c ? 1 : 0, T,
+                     2 * m->I, m->H, m->G, 0, o);
+    if (rc != RXW8_UNIMPLEMENTED && rc) return rc;
+  }
+  if (rc == RXW8_UNIMPLEMENTED && !m->packed) {
     if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, m->f32c))) return rc;
     if ((rc = proj_fused(m, L.gu_w, L.gu_s, L.n_gu, m->xn, m->gu, T))) return rc;
     Q35SiluArgs sa{m->gu, m->at(m->gu, m->I), m->act, T * m->I, m->I, L.n_gu, m->f32c ? 1 : 0};
     if ((rc = launch(rt, "rxw8_q35_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
+    m->ss_cur = nullptr;
     return proj(m, L.down, m->act, m->f32c, m->h, 1, T);
-  }
-  // gate|up rows in SwiGLU order: the GEMV (norm prologue) or GEMM epilogue
-  // writes act = bf16(silu(gate) * up) directly
-  rc = RXW8_UNIMPLEMENTED;
-  if (m->chain && m->ss_cur) {
-    GemvOptions o;
-    o.mode = 3, o.norm_w = L.post_nw, o.eps = m->cfg.eps, o.ss_in = m->ss_cur;
-    o.ss_parts = m->ss_parts, o.swiglu = true, o.prefer_ks1 = true;
-    rc = gemv_launch(rt, m->h, 1, L.gu_w, false, true, L.gu_s, m->act, 0, T, 2 * m->I, m->H, m->G,
-                     0, o);
-    if (rc != RXW8_UNIMPLEMENTED && rc) return rc;
   }
   if (rc == RXW8_UNIMPLEMENTED) {
     if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, false))) return rc;
@@ -485,7 +499,7 @@ int mlp(Qwen35 *m, const Layer &L, int64_t T) {
       if ((rc = launch(rt, "rxw8_dec_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
     }
   }
-  return residual(m, L.down_pk, L.down, m->act, 0, T, m->ss_down);
+  return residual(m, L.down_pk, L.down, m->act, m->f32c ? 1 : 0, T, m->ss_down);
 }
 
 // gated RMSNorm over each (token, head) row of Dl (plain weight, times
@@ -573,7 +587,9 @@ int enqueue_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int
   // packed mode up to 32 rows: the residual's row sums of squares travel with
   // it (embedding, then the residual GEMVs' per-16-channel partials), so the
   // projections after each RMSNorm take it in their prologue (GEMV mode 3)
-  m->chain = m->packed && T <= 32 && m->H % 16 == 0;
+  // (F32 compute: up to 16 rows, two bf16 parts each, on the packed copies)
+  m->chain = ((m->packed && T <= 32) || (m->fc && T <= 16 && !env_off("RXW8_Q35_FC"))) &&
+             m->H % 16 == 0;
   Q35EmbedArgs ea{ids, (const uint8_t *)m->ptr(m->embed), m->f32(m->embed + 1), m->h,
                   m->chain ? m->ss_embed : nullptr, T, m->V, m->H, m->G};
   if ((rc = launch(rt, "rxw8_q35_embed", dim3((unsigned)T), dim3(256), ea))) return rc;
@@ -615,12 +631,14 @@ int prepare(Qwen35 *m) {
   for (const Layer &L : m->layers) {
     total += al((size_t)L.n_in * m->H) + al((size_t)L.n_in * ng * 4) + al((size_t)L.n_gu * m->H) +
              al((size_t)L.n_gu * ng * 4);
-    if (m->packed) {
+    if (m->packed || m->fc) {
       const int64_t ko = L.full ? m->Hq * m->D : m->W;
       total += al((size_t)m->H * ko) + al((size_t)m->H * m->I) + 2 * al((size_t)m->H * 4);
       stage = std::max(stage, al((size_t)std::max(L.n_in, L.n_gu) * m->H) +
                                   al((size_t)L.n_gu * ng * 4));
     }
+    if (m->fc)  // packed copies of the fused input projections and gate|up (+ scales)
+      total += al((size_t)L.n_in * m->H) + al((size_t)2 * m->I * m->H) + al((size_t)2 * m->I * ng * 4);
   }
   hipError_t e = hipMalloc(&m->fused, total);
   void *tmp = nullptr;
@@ -673,15 +691,26 @@ int prepare(Qwen35 *m) {
     if (!m->packed) {
       if ((rc = stack(in, L.n_in, L.in_w, L.in_s))) break;
       if ((rc = stack({L.gate, L.up}, L.n_gu, L.gu_w, L.gu_s))) break;
-      continue;
+      if (!m->fc) continue;
+      // F32 compute: tile-layout copies of the stacked rows (gate|up: its
+      // first 2 I rows in SwiGLU order, scale rows to match)
+      L.in_pk = (uint8_t *)take((size_t)L.n_in * m->H);
+      if ((rc = pack(L.in_w, L.in_pk, L.n_in, m->H, 0))) break;
+      L.gu_pk = (uint8_t *)take((size_t)2 * m->I * m->H);
+      if ((rc = pack(L.gu_w, L.gu_pk, 2 * m->I, m->H, m->I))) break;
+      L.gu_spk = (float *)take((size_t)2 * m->I * ng * 4);
+      InterleaveArgs il{L.gu_s, L.gu_spk, m->I, ng};
+      if ((rc = launch(rt, "rxw8_dec_interleave_rows", dim3(grid_n(2 * m->I * ng)), dim3(256), il))) break;
+    } else {
+      tmp_s = (float *)((char *)tmp + al((size_t)std::max(L.n_in, L.n_gu) * m->H));
+      if ((rc = stack(in, L.n_in, tmp_w, L.in_s))) break;
+      if ((rc = pack(tmp_w, L.in_w, L.n_in, m->H, 0))) break;
+      if ((rc = stack({L.gate, L.up}, L.n_gu, tmp_w, tmp_s))) break;
+      if ((rc = pack(tmp_w, L.gu_w, L.n_gu, m->H, m->I))) break;
+      InterleaveArgs il{tmp_s, L.gu_s, m->I, ng};
+      if ((rc = launch(rt, "rxw8_dec_interleave_rows", dim3(grid_n(2 * m->I * ng)), dim3(256), il))) break;
+      L.in_pk = L.in_w, L.gu_pk = L.gu_w, L.gu_spk = L.gu_s;
     }
-    tmp_s = (float *)((char *)tmp + al((size_t)std::max(L.n_in, L.n_gu) * m->H));
-    if ((rc = stack(in, L.n_in, tmp_w, L.in_s))) break;
-    if ((rc = pack(tmp_w, L.in_w, L.n_in, m->H, 0))) break;
-    if ((rc = stack({L.gate, L.up}, L.n_gu, tmp_w, tmp_s))) break;
-    if ((rc = pack(tmp_w, L.gu_w, L.n_gu, m->H, m->I))) break;
-    InterleaveArgs il{tmp_s, L.gu_s, m->I, ng};
-    if ((rc = launch(rt, "rxw8_dec_interleave_rows", dim3(grid_n(2 * m->I * ng)), dim3(256), il))) break;
     const int o = L.full ? L.o : L.out;
     const int64_t ko = m->params[(size_t)o].dims[1];
     L.out_pk = (uint8_t *)take((size_t)m->H * ko);
@@ -823,9 +852,11 @@ int rxw8_qwen35_create(rxw8_runtime *rt, const rxw8_qwen35_config *cfg, rxw8_qwe
   q->f32c = c.compute_dtype != RXW8_BF16;
   q->esz = q->f32c ? 4 : 2;
   // tile layout (BF16 compute): 16-row tiles, 64-byte k blocks, gate|up pairs of 8 rows
-  q->packed = !q->f32c && c.hidden % 64 == 0 && c.intermediate % 64 == 0 &&
-              (!q->any_linear || q->W % 64 == 0) && (!q->any_full || (c.heads * c.head_dim) % 64 == 0) &&
-              !(std::getenv("RXW8_Q35_UNPACKED") && std::getenv("RXW8_Q35_UNPACKED")[0] == '1');
+  const bool tiles = c.hidden % 64 == 0 && c.intermediate % 64 == 0 &&
+                     (!q->any_linear || q->W % 64 == 0) && (!q->any_full || (c.heads * c.head_dim) % 64 == 0) &&
+                     !(std::getenv("RXW8_Q35_UNPACKED") && std::getenv("RXW8_Q35_UNPACKED")[0] == '1');
+  q->packed = !q->f32c && tiles;
+  q->fc = q->f32c && tiles && c.hidden % 16 == 0;
   const int64_t T = q->Bmax * q->Smax;
   if (T > (1LL << 31) / std::max<int64_t>({q->H, 3 * q->W, q->I, 2 * q->Hq * q->D}))
     return fail(RXW8_INVALID_ARGUMENT, "qwen35: max_batch * max_seq too large");

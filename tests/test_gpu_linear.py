@@ -147,6 +147,49 @@ def test_f32_compute_exact_on_integer_inputs(rt):
     np.testing.assert_array_equal(y, want)
 
 
+def run_linear_packed_f32(rt, x, u8, s):
+    r = rx()
+    packed = r.pack_weight(rt, rt.buffer(u8, r.DType.U8))
+    return r.quantized_linear(rt, rt.buffer(x), packed, rt.buffer(s, r.DType.F32),
+                              r.DType.F32, r.DType.F32).to_numpy()
+
+
+@pytest.mark.parametrize("m,n,k,g", [(1, 1024, 1024, 128), (5, 4096, 1024, 128), (8, 256, 2048, 2048),
+                                     (9, 7168, 1024, 128), (16, 1024, 2048, 128),
+                                     # 32 staged rows of K do not fit: launches of 8 rows
+                                     (16, 1024, 3584, 128),
+                                     # chunks of 16 rows
+                                     (37, 512, 1024, 64)])
+def test_f32_compute_packed_gemv(rt, m, n, k, g):
+    """F32 compute on packed weights: the GEMV stages each f32 row as bf16
+    hi and lo rows (batch columns t and 8 / 16 + t), multiplies the exact
+    codes u - 128 and adds the two parts in f32 (no bf16 rounding)."""
+    rng = np.random.default_rng(m * 11 + n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    u8, s = quantized(rng, n, k, g)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_F32, oracle.ACCUM_F64)
+    y = run_linear_packed_f32(rt, x, u8, s)
+    err = rel_err(y, ref)
+    print(f"F32 compute packed m={m} n={n} k={k} g={g} rel_err={err:.3e}")
+    assert err < 1e-5
+
+
+def test_f32_compute_packed_exact_on_integer_inputs(rt):
+    """The packed F32 GEMV on the integer case of the row-major path above:
+    bit for bit, including the row whose value needs the lo part."""
+    k = np.arange(1024)
+    codes = ((k[None, :] + 4 * np.arange(160)[:, None]) % 256).astype(np.uint8)
+    s = np.ones((160, 8), np.float32)
+    x = np.zeros((12, 1024), np.float32)
+    for r in range(4):
+        x[r, r] = 1.0
+    x[4:] = np.random.default_rng(3).integers(-3, 4, (8, 1024))
+    x[5] = 0.0
+    x[5, 7], x[5, 9] = 1.0 + 2.0 ** -12, 2.0
+    want = (x.astype(np.float64) @ (codes.astype(np.float64) - 128).T).astype(np.float32)
+    np.testing.assert_array_equal(run_linear_packed_f32(rt, x, codes, s), want)
+
+
 def test_rank3_input_and_empty_batch(rt):
     r = rx()
     rng = np.random.default_rng(4)
