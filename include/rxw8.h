@@ -152,7 +152,8 @@ int rxw8_pack_weight(rxw8_runtime *rt, rxw8_buffer *weight, rxw8_buffer **packed
  *   x [..., K] F32 or BF16; weight U8 [N,K] (int8 + 128), or its packed form
  *   U8 [N/16, K/64, 1024] (rxw8_pack_weight); scale F32 [N,K/G];
  *   compute_dtype BF16 (W8A16: bf16(x) . bf16 weights, f32 accumulation,
- *   bf16-rounded result) or F32 (f32 x, f32 dequantised weights).
+ *   bf16-rounded result) or F32 (f32 x, f32 dequantised weights; with the
+ *   packed form, N % 16 == 0).
  *   y [..., N] of out_dtype F32 or BF16 (same values: the BF16 compute result
  *   is bf16-valued; F32 compute requires F32 out).
  * Errors (before launch): INVALID_ARGUMENT for rank 0, non-positive widths,
