@@ -322,8 +322,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a) {
 // 8 x 4 accumulators, 12 fragment reads per 32 MFMAs. Two LDS stages of
 // [bf16 weight tile 32 KB | bf16 activation tile 32 KB]; activations are DMA'd
 // one k tile ahead, weights loaded two ahead into two register sets.
+// TNB: weight rows per tile, 256 or 192 (wave w then owns weight rows
+// [TNB/2 (w & 1), +TNB/2): FI = TNB / 32 weight fragments; at 192 the 768
+// weight slices of a k tile leave threads 256-511 one slice each, their second
+// load re-reading a valid row that is never stored, so every wave issues the
+// same loads and the wait counts stay exact).
+template <int TNB>
 __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
-  constexpr int TNB = 256, TMB = 256;
+  constexpr int TMB = 256;
+  constexpr int FI = TNB / 32;        // weight fragments per wave
+  constexpr int SLICES = TNB * 4;     // 16-code weight slices per k tile
   constexpr int W_BYTES = TNB * BK * 2, X_BYTES = TMB * BK * 2, STAGE = W_BYTES + X_BYTES;
   constexpr int X_DMA = TMB * BK * 2 / 1024 / 8;  // 4 LDS-DMA instructions per wave per k tile
   const int tid = threadIdx.x, lane = tid & 63;
@@ -365,12 +373,13 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
             lds_addr(smem + stage * STAGE + W_BYTES + (wave * X_DMA + i) * 1024));
   };
 
-  // weights: 1024 slices of 16 codes per k tile, 2 per thread (row = id / 4, kq = id % 4)
+  // weights: SLICES slices of 16 codes per k tile, 2 per thread (row = id / 4, kq = id % 4)
   const int kstride = a.w_packed ? 1024 : BK;
   uint32_t woff[2], soff[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const int id = tid + 512 * p, row = id >> 2, kq = id & 3;
+    const int id = SLICES == 1024 ? tid + 512 * p : min(tid + 512 * p, SLICES - 1);
+    const int row = id >> 2, kq = id & 3;
     const int n = n0 + row;
     woff[p] = a.w_packed
                   ? ((uint32_t)(n >> 4) * (uint32_t)KTall * 1024u + (uint32_t)((row & 15) + 16 * kq) * 16u)
@@ -392,6 +401,7 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
   uint32_t hq[8];
   auto dequant_piece = [&](const WSet &ws, int piece, int stage) {
     const int p = piece >> 2, e = piece & 3;
+    if (SLICES < 1024 && tid + 512 * p >= SLICES) return;  // a re-read slice (uniform per wave)
     const float sc = ws.s[p], o = -128.0f * sc;
     const uint32_t w4 = ws.w[p][e];
     const float f0 = __builtin_fmaf((float)(w4 & 0xffu), sc, o);
@@ -408,14 +418,14 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
     }
   };
 
-  f32x4 acc[8][4];
+  f32x4 acc[FI][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int r16 = lane & 15, kg = lane >> 4;
   auto frag_a = [&](int stage, int i, int ks) {
-    return as_bf16x8(*(const u32x4 *)(smem + stage * STAGE + swz(wn * 128 + 16 * i + r16, ks * 4 + kg)));
+    return as_bf16x8(*(const u32x4 *)(smem + stage * STAGE + swz(wn * (TNB / 2) + 16 * i + r16, ks * 4 + kg)));
   };
   auto frag_b = [&](int stage, int j, int ks) {
     return as_bf16x8(
@@ -435,9 +445,12 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
   for (int piece = 0; piece < 8; ++piece) dequant_piece(w0, piece, 0);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  // 16 groups per k tile, g = 8 ks + i: the 4 MFMAs of weight fragment (ks, i);
-  // fragment reads run PREFETCH groups ahead (a ring of PREFETCH + 1 weight
-  // fragments), the activation fragments of ks = 1 two groups before use.
+  // 2 FI groups per k tile, g = FI ks + i: the 4 MFMAs of weight fragment
+  // (ks, i); fragment reads run PREFETCH groups ahead (a ring of PREFETCH + 1
+  // weight fragments), the activation fragments of ks = 1 two groups before
+  // use; the 8 dequantisation pieces of the next tile spread over the ks = 1
+  // groups (at FI = 6 the last two groups take two each, a slice's e = 3
+  // piece, which stores it, last).
   constexpr int PREFETCH = RXW8_GEMM_PREFETCH;
   auto step = [&](int kt, auto xs, WSet &load_set, const WSet &deq_set) {
     constexpr int cur = decltype(xs)::value, nxt = cur ^ 1;
@@ -448,21 +461,25 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) bf[j] = frag_b(cur, j, 0);
 #pragma unroll
-    for (int g = 0; g < PREFETCH; ++g) af[g] = frag_a(cur, g & 7, g >> 3);
+    for (int g = 0; g < PREFETCH; ++g) af[g] = frag_a(cur, g % FI, g / FI);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      const int i = g & 7, ks = g >> 3;
-      if (g + PREFETCH < 16) af[(g + PREFETCH) % (PREFETCH + 1)] = frag_a(cur, (g + PREFETCH) & 7, (g + PREFETCH) >> 3);
-      if (g == 6)
+    for (int g = 0; g < 2 * FI; ++g) {
+      const int i = g % FI, ks = g / FI;
+      if (g + PREFETCH < 2 * FI)
+        af[(g + PREFETCH) % (PREFETCH + 1)] = frag_a(cur, (g + PREFETCH) % FI, (g + PREFETCH) / FI);
+      if (g == FI - 2)
 #pragma unroll
         for (int j = 0; j < 4; ++j) bn[j] = frag_b(cur, j, 1);
       // weights of tile kt+1 were loaded last k tile: this tile's 8 loads are younger
-      if (g == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      if (g == FI) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         acc[i][j] = mfma16x16x32(af[g % (PREFETCH + 1)], ks ? bn[j] : bf[j], acc[i][j]);
-      if (ks) dequant_piece(deq_set, i, nxt);
+      if (ks) {
+        dequant_piece(deq_set, i, nxt);
+        if (FI == 6 && i >= 4) dequant_piece(deq_set, i + 2, nxt);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     // activation tile kt+1 (this tile's DMAs) is older than this tile's 4 weight loads
@@ -479,20 +496,21 @@ __device__ __forceinline__ void gemm_tile_big(const GemmArgs &a) {
 
   if (S > 1) {  // raw f32 partials; rxw8_gemv_splitk_reduce sums them in split order
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < FI; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int m = m0 + wm * 64 + 16 * j + r16;
         if (m < a.M)
-          *(f32x4 *)(a.ws + ((int64_t)split * a.M + m) * a.N + n0 + wn * 128 + 16 * i + 4 * kg) = acc[i][j];
+          *(f32x4 *)(a.ws + ((int64_t)split * a.M + m) * a.N + n0 + wn * (TNB / 2) + 16 * i + 4 * kg) =
+              acc[i][j];
       }
     return;
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      gemm_store(a, m0 + wm * 64 + 16 * j + r16, n0 + wn * 128 + 16 * i + 4 * kg, acc[i][j]);
+      gemm_store(a, m0 + wm * 64 + 16 * j + r16, n0 + wn * (TNB / 2) + 16 * i + 4 * kg, acc[i][j]);
 }
 
 // 256 x 256 tiles over weights already dequantised to bf16 (row-major
@@ -553,7 +571,7 @@ __device__ __forceinline__ void gemm_tile_bf16w(const GemmArgs &a) {
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int r16 = lane & 15, kg = lane >> 4;
   auto frag_a = [&](int stage, int i, int ks) {
-    return as_bf16x8(*(const u32x4 *)(smem + stage * STAGE + swz(wn * 128 + 16 * i + r16, ks * 4 + kg)));
+    return as_bf16x8(*(const u32x4 *)(smem + stage * STAGE + swz(wn * (TNB / 2) + 16 * i + r16, ks * 4 + kg)));
   };
   auto frag_b = [&](int stage, int j, int ks) {
     return as_bf16x8(
@@ -657,7 +675,10 @@ extern "C" __global__ void __launch_bounds__(512) rxw8_w8a16_gemm_bf16w_t256(Gem
 // G % 64 == 0 and K % G == 0, M >= 1, M * K * 2 < 2^31 and the weight bytes
 // < 2^32; grid = 8 * ceil(tiles / 8) workgroups.
 extern "C" __global__ void __launch_bounds__(512) rxw8_w8a16_gemm_t256(GemmArgs a) {
-  gemm_tile_big(a);
+  gemm_tile_big<256>(a);
+}
+extern "C" __global__ void __launch_bounds__(512) rxw8_w8a16_gemm_t192(GemmArgs a) {
+  gemm_tile_big<192>(a);
 }
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_w8a16_gemm_m256(GemmArgs a) {

@@ -749,10 +749,15 @@ static int run_gemm(Runtime *rt, const void *x, int x_f32, const uint8_t *w, boo
     int tm, tn, threads;
     double eff;
   };
+  // 256 x 192 (the 8-wave kernel with 6 weight fragments per wave) fills
+  // whole rounds where 256-wide tiles leave half a round, e.g. M = 2048,
+  // N = 12288: 512 tiles instead of 384.
   static const Tiling tilings[] = {{"rxw8_w8a16_gemm_t256", 256, 256, 512, 0.50},
+                                   {"rxw8_w8a16_gemm_t192", 256, 192, 512, 0.44},
                                    {"rxw8_w8a16_gemm_m256", 256, 128, 256, 0.36},
                                    {"rxw8_w8a16_gemm_m128", 128, 128, 256, 0.30}};
-  const int forced = env_int("RXW8_GEMM_TILE", 0);  // 256x256 = 256, 256x128 = 2, 128x128 = 128
+  // RXW8_GEMM_TILE: 256x256 = 256, 256x192 = 192, 256x128 = 2, 128x128 = 128
+  const int forced = env_int("RXW8_GEMM_TILE", 0);
   const int forced_ks = env_int("RXW8_GEMM_KSPLIT", 0);
   const double cu_flops = 2.5e15 / 256.0, hbm = 4.0e12;  // per-CU bf16 MFMA peak, B/s
   const Tiling *best = nullptr;
@@ -760,7 +765,7 @@ static int run_gemm(Runtime *rt, const void *x, int x_f32, const uint8_t *w, boo
   double best_t = 1e30;
   for (const Tiling &tl : tilings) {
     if (N % tl.tn) continue;
-    const int code = tl.tn == 256 ? 256 : (tl.tm == 256 ? 2 : 128);
+    const int code = tl.tn == 256 || tl.tn == 192 ? tl.tn : (tl.tm == 256 ? 2 : 128);
     if (forced && forced != code) continue;
     const int64_t tiles = (M + tl.tm - 1) / tl.tm * (N / tl.tn);
     for (int ks : {1, 2, 3, 4, 6, 8}) {

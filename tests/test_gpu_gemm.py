@@ -145,3 +145,13 @@ def test_gemm_tile_kernels(rt, monkeypatch, tile, m, n, k, g):
     np.testing.assert_array_equal(y_pk, y)
     err, eq = check(y, ref)
     print(f"tile={tile} M={m} N={n} K={k} G={g} rel_err={err:.3e} equal={eq:.4f}")
+
+
+@pytest.mark.parametrize("m,n,k,g", [(65, 384, 64, 64), (300, 768, 256, 128), (513, 1152, 640, 640),
+                                     (256, 1536, 1024, 128)])
+def test_gemm_256x192_tiles(rt, monkeypatch, m, n, k, g):
+    """The 256 x 192 tiling (the 8-wave kernel with 6 weight fragments per
+    wave; threads 256-511 load one weight slice per k tile and re-read a
+    second that is never stored): ragged M, single- and odd-count k tiles,
+    packed and row-major, against the oracle."""
+    test_gemm_tile_kernels(rt, monkeypatch, 192, m, n, k, g)
