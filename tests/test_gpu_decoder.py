@@ -8,10 +8,15 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import rel_err
+from conftest import elem_rel_err, rel_err
 from decoder_fixtures import tiny_config, tiny_params
 
 pytestmark = pytest.mark.gpu
+
+# per-logit error bound: elem_rel_err with the floor at the logits' rms
+# (observed 2.7e-2 - 4.2e-2 from bf16 roundings upstream; a corrupted logit
+# or channel is off by O(1) of the rms)
+ELEM_TOL = 1e-1
 
 
 def rx():
@@ -64,15 +69,21 @@ def test_decoder_prefill_and_decode_match_oracle(rt, group):
     ids = rng.integers(0, cfg["vocab"], (batch, 7)).astype(np.int32)
     lg, nxt, rlg, rnxt = step_both(rt, model, dec, ids)
     err = rel_err(lg, rlg)
-    print(f"prefill group={group} logits rel_err={err:.3e}")
+    # per logit, floored at the logits' rms (logits near 0 carry absolute
+    # error of the same size as large ones)
+    e_elem = elem_rel_err(lg, rlg, floor=1.0)
+    print(f"prefill group={group} logits rel_err={err:.3e} elem_rel_err={e_elem:.3e}")
     assert err <= 1e-2
+    assert e_elem <= ELEM_TOL
     np.testing.assert_array_equal(model.lens()[:batch], [7, 7])
     for step in range(5):
         ids = rnxt.reshape(batch, 1).astype(np.int32)
         lg, nxt, rlg, rnxt = step_both(rt, model, dec, ids)
         err = rel_err(lg, rlg)
-        print(f"decode step {step} rel_err={err:.3e}")
+        e_elem = elem_rel_err(lg, rlg, floor=1.0)
+        print(f"decode step {step} rel_err={err:.3e} elem_rel_err={e_elem:.3e}")
         assert err <= 1e-2
+        assert e_elem <= ELEM_TOL
         top2 = np.sort(rlg, axis=1)[:, -2:]
         clear = (top2[:, 1] - top2[:, 0]) > 0.05 * np.abs(top2[:, 1]).max()
         np.testing.assert_array_equal(nxt[clear], rnxt[clear])
@@ -119,8 +130,10 @@ def test_decoder_c5_widths_match_oracle(rt, inter):
     for step in range(4):
         lg, nxt, rlg, rnxt = step_both(rt, model, dec, rnxt.reshape(batch, 1).astype(np.int32))
         err = rel_err(lg, rlg)
-        print(f"C5-width decode step {step} rel_err={err:.3e}")
+        e_elem = elem_rel_err(lg, rlg, floor=1.0)
+        print(f"C5-width decode step {step} rel_err={err:.3e} elem_rel_err={e_elem:.3e}")
         assert err <= 1e-2
+        assert e_elem <= ELEM_TOL
 
 
 @pytest.mark.parametrize("qk_norm", [True, False])
