@@ -208,11 +208,25 @@ __device__ __forceinline__ float row_add16(float v) {
   return v + dpp_rot<0xb1>(v);
 }
 
+// global -> LDS DMA of 16 bytes per active lane (global_load_lds_dwordx4:
+// lane l writes LDS bytes [lds + 16 l, +16)), from inline asm so the compiler
+// does not answer later LDS reads with waits on it (the caller waits).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void q35_dma16(const void *base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, %2"
+               :: "v"(voff), "s"(lds), "s"(base) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t q35_lds_addr(const float *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
+}
+
 template <int D>
 __device__ void q35_attention(const Q35AttnArgs &a) {
   constexpr int DC = D / 4, DT = D / 16, KS = D + 4, PS = 20;
   constexpr int TILE = 16 * KS;                  // floats of one K (or V) tile
-  constexpr int LD = 2 * 16 * D / 4 / 256;       // float4 loads per thread per tile (K and V)
   extern __shared__ __attribute__((aligned(16))) float attn_lds[];
   float *plds = attn_lds + 4 * TILE;             // [4 waves][16 q][PS]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -244,23 +258,22 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
       qreg[c] = v.x, qreg[c + 1] = v.y, qreg[c + 2] = v.z, qreg[c + 3] = v.w;
     }
   }
-  float4 stage[LD];
-  auto load_tile = [&](int t) {
+  // K/V rows go global -> LDS by LDS DMA, 8 of a tile's 32 rows (16 K, 16
+  // V) per wave, one instruction per row with lanes [0, D/4) active (lane l
+  // copies d 4l..4l+3 into the padded row; masked lanes write nothing). No
+  // registers hold a tile in flight, so tile t + 1 loads while tile t is
+  // used; the loop waits for the DMAs itself before each barrier. Keys past
+  // S repeat row S - 1 (never visible).
+  const int wvu = __builtin_amdgcn_readfirstlane(wv);
+  auto issue_tile = [&](int t, int buf) {
+    if (lane < D / 4) {
 #pragma unroll
-    for (int r = 0; r < LD; ++r) {
-      const int f = threadIdx.x + 256 * r;     // float4 index in [K tile | V tile]
-      const int kv = f / (16 * D / 4), g = f - kv * (16 * D / 4);
-      const int key = min(16 * t + g / (D / 4), a.S - 1), d4 = g % (D / 4);
-      stage[r] = *(const float4 *)((kv ? vbase : kbase) + (int64_t)key * D + 4 * d4);
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int r = 0; r < LD; ++r) {
-      const int f = threadIdx.x + 256 * r;
-      const int kv = f / (16 * D / 4), g = f - kv * (16 * D / 4);
-      const int key = g / (D / 4), d4 = g % (D / 4);
-      *(float4 *)(attn_lds + (2 * buf + kv) * TILE + key * KS + 4 * d4) = stage[r];
+      for (int i = 0; i < 8; ++i) {
+        const int row = wvu * 8 + i, kv = row >> 4, kr = row & 15;
+        const int key = min(16 * t + kr, a.S - 1);
+        q35_dma16(kv ? vbase : kbase, (uint32_t)(key * D + 4 * lane) * 4u,
+                  q35_lds_addr(attn_lds + (2 * buf + kv) * TILE + kr * KS));
+      }
     }
   };
   f32x4 o[DT];
@@ -270,14 +283,12 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) m[i] = -__builtin_huge_valf(), l[i] = 0.f;
   float *pw = plds + wv * 16 * PS;
-  if (t_begin < ntiles) {
-    load_tile(t_begin);
-    store_tile(0);
-  }
+  if (t_begin < ntiles) issue_tile(t_begin, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   for (int t = t_begin; t < ntiles; ++t) {
     const int buf = (t - t_begin) & 1;
-    if (t + 1 < ntiles) load_tile(t + 1);
+    if (t + 1 < ntiles) issue_tile(t + 1, buf ^ 1);  // that buffer's tile was used before the last barrier
     if (16 * t <= q0 + 15) {  // some key of the tile is visible to this wave's queries
       const float *kt = attn_lds + (2 * buf) * TILE + col * KS + DC * j;
       // four independent accumulators keep the MFMA pipe busy (no chain of
@@ -322,7 +333,7 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.w, vt[3 * KS + 16 * dt], o[dt], 0, 0, 0);
       }
     }
-    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next tile's DMAs
     __syncthreads();
   }
   if (a.nsplit > 1) {
