@@ -157,17 +157,43 @@ struct RmsNormArgs {
   float eps;
 };
 
+// Thread t sums elements t, t + 256, ... in that order, then block_sum_256
+// (the fused GEMV's x_mode 1 prologue repeats this order). Rows of up to
+// 16 x 256 elements are read once: all of a thread's x and weight loads are
+// issued before any is used, and the write reuses them.
 extern "C" __global__ void __launch_bounds__(256) rxw8_dec_rmsnorm(RmsNormArgs a) {
   __shared__ float red[4];
   const int r = blockIdx.x;
   const int64_t src = a.src_row ? a.src_row[r] : (int64_t)r * a.src_stride + a.src_offset;
   const float *x = a.x + src * a.H;
+  uint16_t *y = a.y + (int64_t)r * a.H;
+  const int t = threadIdx.x;
+  constexpr int R = 16;
+  if (a.H <= 256 * R) {
+    float v[R], w[R];
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const int64_t i = t + 256 * s;
+      v[s] = i < a.H ? x[i] : 0.f;
+      w[s] = i < a.H ? a.w[i] : 0.f;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < R; ++s) ss += v[s] * v[s];  // zeros past H add nothing
+    ss = block_sum_256(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const int64_t i = t + 256 * s;
+      if (i < a.H) y[i] = f32_to_bf16_bits((v[s] * scale) * w[s]);
+    }
+    return;
+  }
   float ss = 0.f;
-  for (int64_t i = threadIdx.x; i < a.H; i += blockDim.x) ss += x[i] * x[i];
+  for (int64_t i = t; i < a.H; i += blockDim.x) ss += x[i] * x[i];
   ss = block_sum_256(ss, red);
   const float scale = 1.0f / sqrtf(ss / (float)a.H + a.eps);
-  uint16_t *y = a.y + (int64_t)r * a.H;
-  for (int64_t i = threadIdx.x; i < a.H; i += blockDim.x)
+  for (int64_t i = t; i < a.H; i += blockDim.x)
     y[i] = f32_to_bf16_bits((x[i] * scale) * a.w[i]);
 }
 
