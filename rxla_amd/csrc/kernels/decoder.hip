@@ -318,6 +318,21 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_qk_rope_kv_d128(QkRop
   }
   const bool is_q = h < a.Hq;
   const float *nw = is_q ? a.q_norm : a.k_norm;
+  // norm weights and the position's RoPE row, 16-byte loads issued before
+  // the reduction that precedes their use
+  const float *rope = a.rope + (int64_t)p * D;
+  float w0[8], w1[8], cs[8], sn[8];
+#pragma unroll
+  for (int c = 0; c < 8; c += 4) {
+    const float4 a4 = *(const float4 *)(rope + i0 + c), b4 = *(const float4 *)(rope + HALF + i0 + c);
+    cs[c] = a4.x, cs[c + 1] = a4.y, cs[c + 2] = a4.z, cs[c + 3] = a4.w;
+    sn[c] = b4.x, sn[c + 1] = b4.y, sn[c + 2] = b4.z, sn[c + 3] = b4.w;
+    if (nw) {
+      const float4 c4 = *(const float4 *)(nw + i0 + c), d4 = *(const float4 *)(nw + HALF + i0 + c);
+      w0[c] = c4.x, w0[c + 1] = c4.y, w0[c + 2] = c4.z, w0[c + 3] = c4.w;
+      w1[c] = d4.x, w1[c + 1] = d4.y, w1[c + 2] = d4.z, w1[c + 3] = d4.w;
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += x0[e] * x0[e] + x1[e] * x1[e];
@@ -328,17 +343,15 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_qk_rope_kv_d128(QkRop
     const float sc = 1.0f / sqrtf(ss / (float)D + a.eps);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      x0[e] = (x0[e] * sc) * nw[i0 + e];
-      x1[e] = (x1[e] * sc) * nw[HALF + i0 + e];
+      x0[e] = (x0[e] * sc) * w0[e];
+      x1[e] = (x1[e] * sc) * w1[e];
     }
   }
-  const float *rope = a.rope + (int64_t)p * D;
   float r0[8], r1[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float cs = rope[i0 + e], sn = rope[HALF + i0 + e];
-    r0[e] = x0[e] * cs - x1[e] * sn;
-    r1[e] = x1[e] * cs + x0[e] * sn;
+    r0[e] = x0[e] * cs[e] - x1[e] * sn[e];
+    r1[e] = x1[e] * cs[e] + x0[e] * sn[e];
   }
   if (!live) return;
   if (is_q) {
