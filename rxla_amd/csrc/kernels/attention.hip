@@ -1076,7 +1076,7 @@ __device__ __forceinline__ void lds_dma16(const void *g, void *l_base) {
 // per (row, head) as attn_prefill.
 template <int G, int R>
 __device__ void attn_prefill_rt(const PrefillArgs &a) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t pf_lds[];  // [2][K block | V^T block]
+  extern __shared__ __attribute__((aligned(16))) uint16_t pf_lds[];  // [2][K block] [2][V block]
   constexpr int QROWS = 64 * R;   // query rows per workgroup
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, g4 = lane >> 4;
@@ -1137,60 +1137,64 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
     for (int dt = 0; dt < 8; ++dt) o[r][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Block staging by LDS DMA (no registers held across the block): K into
-  // two buffers, row-major with 16-byte chunks XOR-swizzled by row (the lane
-  // writing LDS chunk slot c' of row r fetches global chunk c' ^ (r & 15));
-  // V row-major into one staging block, transposed to V^T by an LDS pass.
-  // Lanes past kv_end copy nothing: their K scores are masked to -inf and
-  // the transpose writes zero V rows for them.
+  // Block staging by LDS DMA (no registers held across the block), both
+  // operands double-buffered and row-major with 16-byte chunks XOR-swizzled
+  // by row (the lane writing LDS chunk slot c' of row r fetches global chunk
+  // c' ^ f(r)): K with f(r) = r & 15 (conflict-free fragment reads of 16 rows
+  // of one chunk), V with f(r) = 2 (r & 7), whose transposing reads (below)
+  // then hit 16 distinct slots per half wave. K rows past kv_end are not
+  // copied (their scores are masked to -inf); V rows past kv_end repeat key
+  // kv_end - 1, so whatever P multiplies there is finite (and P is 0).
   uint16_t *k_lds0 = pf_lds;                 // [2][64 keys][128] swizzled
-  uint16_t *v_raw = pf_lds + 2 * PKB * D;    // [64 keys][128]
-  uint16_t *vt_lds = v_raw + PKB * D;        // [128 dims][VROW]
+  uint16_t *v_lds0 = pf_lds + 2 * PKB * D;   // [2][64 keys][128] swizzled
   auto dma_block = [&](int blk) {
     uint16_t *kb = k_lds0 + (blk & 1) * PKB * D;
+    uint16_t *vb = v_lds0 + (blk & 1) * PKB * D;
     // 2 x 16 instructions of 64 lanes (K, then V), spread over the waves
     for (int ins = wave; ins < 32; ins += 4 * G) {
       const int gidx = 64 * (ins & 15) + lane;  // 16-byte granule of the block
       const int r = gidx >> 4, c = gidx & 15;
       const int key = blk * PKB + r;
-      if (key < kv_end) {
-        if (ins < 16)
+      if (ins < 16) {
+        if (key < kv_end)
           lds_dma16(a.kc + kv_base + (int64_t)key * D + ((c ^ (r & 15)) << 3), kb + 64 * 8 * (ins & 15));
-        else
-          lds_dma16(a.vc + kv_base + (int64_t)key * D + (c << 3), v_raw + 64 * 8 * (ins & 15));
+      } else {
+        lds_dma16(a.vc + kv_base + (int64_t)min(key, kv_end - 1) * D + ((c ^ (2 * (r & 7))) << 3),
+                  vb + 64 * 8 * (ins & 15));
       }
     }
   };
-  // threads < 256: keys 4 (t % 16) .. + 3 of dims 8 (t / 16) .. + 7 -> V^T.
-  // A V^T row holds the block's keys in the order the P operand takes them:
-  // key 16 kt + 4 g + i at 32 (kt / 2) + 8 g + 4 (kt % 2) + i, so a lane's
-  // 8 keys of one step (two 16-key tiles, 4 keys each) are 16 contiguous bytes.
-  auto transpose_v = [&](int blk) {
-    if (threadIdx.x >= 256) return;
-    const int c = threadIdx.x >> 4, k4 = 4 * (threadIdx.x & 15);
-    const int kt = k4 >> 4, g = (k4 >> 2) & 3;
-    const int kpos = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1);
-    u32x4 vr[4];
+  // The V^T operand of O^T += V^T P^T straight from row-major V by
+  // ds_read_b64_tr_b16: in each 16-lane group, lane 4j + q reads the 4
+  // values d0 + 4q .. + 3 of key row k_j, and lane i receives the values at
+  // d = d0 + i of rows k_0 .. k_3. Lane (col, g4) needs, for step ks, keys
+  // 32 ks + 4 g4 + 0..3 and 32 ks + 16 + 4 g4 + 0..3 (the key order of its P
+  // operand) at d = 16 dt + col: two reads.
+  const int tr_j = col >> 2, tr_q = col & 3;
+  auto v_frag = [&](const uint16_t *vb, int ks, int dt) {
+    u32x4 va;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      vr[u] = blk * PKB + k4 + u < kv_end ? *(const u32x4 *)(v_raw + (k4 + u) * D + 8 * c)
-                                          : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int sh = 16 * (e & 1);
-      const uint32_t k0 = (vr[0][e >> 1] >> sh) & 0xffffu, k1 = (vr[1][e >> 1] >> sh) & 0xffffu;
-      const uint32_t k2 = (vr[2][e >> 1] >> sh) & 0xffffu, k3 = (vr[3][e >> 1] >> sh) & 0xffffu;
-      *(uint2 *)(vt_lds + (8 * c + e) * VROW + kpos) = uint2{k0 | (k1 << 16), k2 | (k3 << 16)};
+    for (int h = 0; h < 2; ++h) {
+      const int row = 32 * ks + 16 * h + 4 * g4 + tr_j;
+      const int d0 = 16 * dt + 4 * tr_q;
+      const int slot = (d0 >> 3) ^ (2 * (row & 7));
+      const uint16_t *src = vb + row * D + slot * 8 + (d0 & 7);
+      typedef short v4i16 __attribute__((ext_vector_type(4)));
+      const v4i16 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4i16 *)(src));
+      const uint2 u = __builtin_bit_cast(uint2, t);
+      va[2 * h] = u.x;
+      va[2 * h + 1] = u.y;
     }
+    return va;
   };
 
   dma_block(0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  transpose_v(0);
-  __syncthreads();
   for (int blk = 0; blk < nblk; ++blk) {
     const uint16_t *ks_lds = k_lds0 + (blk & 1) * PKB * D;
+    const uint16_t *vs_lds = v_lds0 + (blk & 1) * PKB * D;
     if (blk + 1 < nblk) dma_block(blk + 1);  // in flight while this block is used
     const int j0 = blk * PKB;
     if (j0 <= wave_last) {  // wave-uniform: else every key of the block is in this wave's future
@@ -1266,18 +1270,14 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-          const u32x4 va = *(const u32x4 *)(vt_lds + (dt * 16 + col) * VROW + 32 * ks + 8 * g4);
+          const u32x4 va = v_frag(vs_lds, ks, dt);
 #pragma unroll
           for (int r = 0; r < R; ++r) o[r][dt] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[r][ks]), o[r][dt]);
         }
     }
-    // the next block's copies are in; every wave is done with V^T and this K
+    // the next block's copies are in; every wave is done with this block
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (blk + 1 < nblk) {
-      transpose_v(blk + 1);
-      __syncthreads();
-    }
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
