@@ -1068,6 +1068,22 @@ __device__ __forceinline__ void lds_dma16(const void *g, void *l_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void *)l_base, 16, 0, 0);
 }
 
+// The same copy from inline asm, base + voff (base wave-uniform in SGPRs, byte
+// offset per lane) into LDS at lds + 16 l: the compiler then does not answer
+// LDS reads of the other buffer with waits on the copy (the caller waits
+// before the barrier that publishes it).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16_asm(const void *base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, %2"
+               :: "v"(voff), "s"(lds), "s"(base) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_u32(const uint16_t *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t *)p;
+}
+
 // R row tiles per wave: as attn_prefill_wh, but wave w owns rows
 // 16 R (w % 4) .. + 16 R - 1 of a workgroup's 64 R query rows, as R 16-row
 // tiles of one head. Every K and V^T fragment read from LDS then feeds R
@@ -1151,16 +1167,17 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
     uint16_t *kb = k_lds0 + (blk & 1) * PKB * D;
     uint16_t *vb = v_lds0 + (blk & 1) * PKB * D;
     // 2 x 16 instructions of 64 lanes (K, then V), spread over the waves
-    for (int ins = wave; ins < 32; ins += 4 * G) {
+    for (int ins = __builtin_amdgcn_readfirstlane(wave); ins < 32; ins += 4 * G) {
       const int gidx = 64 * (ins & 15) + lane;  // 16-byte granule of the block
       const int r = gidx >> 4, c = gidx & 15;
       const int key = blk * PKB + r;
       if (ins < 16) {
         if (key < kv_end)
-          lds_dma16(a.kc + kv_base + (int64_t)key * D + ((c ^ (r & 15)) << 3), kb + 64 * 8 * (ins & 15));
+          lds_dma16_asm(a.kc + kv_base, (uint32_t)(key * D + ((c ^ (r & 15)) << 3)) * 2u,
+                        lds_u32(kb + 64 * 8 * (ins & 15)));
       } else {
-        lds_dma16(a.vc + kv_base + (int64_t)min(key, kv_end - 1) * D + ((c ^ (2 * (r & 7))) << 3),
-                  vb + 64 * 8 * (ins & 15));
+        lds_dma16_asm(a.vc + kv_base, (uint32_t)(min(key, kv_end - 1) * D + ((c ^ (2 * (r & 7))) << 3)) * 2u,
+                      lds_u32(vb + 64 * 8 * (ins & 15)));
       }
     }
   };

@@ -1082,7 +1082,8 @@ int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t 
   // one-tile kernel, RXW8_PREFILL_R2=0 RXW8_PREFILL_WH=0 the all-heads one.
   static const int wh_env = env_int("RXW8_PREFILL_WH", 1);
   static const int r2_env = env_int("RXW8_PREFILL_R2", 1);
-  const bool r2 = r2_env && G <= 2;
+  // (the two-tile kernel addresses a cache plane with 32-bit byte offsets)
+  const bool r2 = r2_env && G <= 2 && Lmax <= ((int64_t)1 << 22);
   const bool wh = wh_env && G <= 2;
   if (r2) a.nqb = (int)((S + 127) / 128);
   std::snprintf(kname, sizeof kname,
