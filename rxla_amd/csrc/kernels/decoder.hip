@@ -410,10 +410,71 @@ __device__ __forceinline__ bool am_better(float a, int ia, float b, int ib) {
   return a > b || (a == b && ia < ib);
 }
 
+// (value, index) pair of a wave with the lowest index on ties (am_better is a
+// total order, so any reduction order returns the same winner); index
+// 0x7fffffff marks "no element".
+__device__ __forceinline__ void am_wave_reduce(float &bv, int &bi) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (oi != 0x7fffffff && (bi == 0x7fffffff || am_better(ov, oi, bv, bi))) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+}
+
 extern "C" __global__ void __launch_bounds__(256) rxw8_dec_argmax_partial(ArgmaxArgs a) {
   __shared__ float sv[256];
   __shared__ int si[256];
   const int r = blockIdx.x / a.chunks, c = blockIdx.x - r * a.chunks;
+  if (a.inner == 1 && (a.cols & 3) == 0 && ((uintptr_t)a.x & 15) == 0) {
+    // contiguous rows of whole float4s: chunks of whole float4s, each
+    // thread's loads issued together, wave butterflies, then the 4 waves
+    const int64_t q4 = a.cols >> 2, per4 = (q4 + a.chunks - 1) / a.chunks;
+    const int64_t lo4 = c * per4, hi4 = min(q4, lo4 + per4);
+    const float4 *xr = (const float4 *)(a.x + (int64_t)r * a.cols);
+    float bv = -__builtin_huge_valf();
+    int bi = 0x7fffffff;
+    for (int64_t q0 = lo4 + threadIdx.x; q0 < hi4; q0 += 4 * 256) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (q0 + 256 * u < hi4) v[u] = xr[q0 + 256 * u];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t q = q0 + 256 * u;
+        if (q < hi4) {
+          const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int i = (int)(4 * q + k);
+            if (bi == 0x7fffffff || am_better(e[k], i, bv, bi)) {
+              bv = e[k];
+              bi = i;
+            }
+          }
+        }
+      }
+    }
+    am_wave_reduce(bv, bi);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+      sv[wave] = bv;
+      si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < 4; ++w)
+        if (si[w] != 0x7fffffff && (bi == 0x7fffffff || am_better(sv[w], si[w], bv, bi))) {
+          bv = sv[w];
+          bi = si[w];
+        }
+      a.pval[blockIdx.x] = bv;
+      a.pidx[blockIdx.x] = bi;
+    }
+    return;
+  }
   const int64_t per = (a.cols + a.chunks - 1) / a.chunks;
   const int64_t lo = c * per, hi = min(a.cols, lo + per);
   const int64_t o = r / a.inner, j = r - o * a.inner;
@@ -480,26 +541,21 @@ struct ArgmaxFinalArgs {
 
 extern "C" __global__ void __launch_bounds__(1024) rxw8_dec_argmax_final(ArgmaxFinalArgs a) {
   __shared__ int col;
+  __shared__ int ids[256];  // the winners of rows < 256 for the embedding pass
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   if (threadIdx.x == 0) col = a.rec_out ? *a.rec_step : 0;
   __syncthreads();
   for (int r = wave; r < a.rows; r += nwaves) {
     float bv = -__builtin_huge_valf();
     int bi = 0x7fffffff;
-    if (lane < a.chunks) {
+    if (lane < a.chunks) {  // both loads in flight (the value is unused for an empty chunk)
       bi = a.pidx[r * a.chunks + lane];
-      if (bi != 0x7fffffff) bv = a.pval[r * a.chunks + lane];
+      bv = a.pval[r * a.chunks + lane];
     }
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (oi != 0x7fffffff && (bi == 0x7fffffff || am_better(ov, oi, bv, bi))) {
-        bv = ov;
-        bi = oi;
-      }
-    }
+    am_wave_reduce(bv, bi);
     if (lane == 0) {
       const int id = bi == 0x7fffffff ? 0 : bi;
+      if (r < 256) ids[r] = id;
       a.next[r] = id;
       if (a.lens) a.lens[r] += a.s;
       if (a.rec_out && col < a.ncols) a.rec_out[r * a.ncols + col] = id;
@@ -514,7 +570,7 @@ extern "C" __global__ void __launch_bounds__(1024) rxw8_dec_argmax_final(ArgmaxF
     const int r = r0 + g;
     float ss = 0.f;
     if (r < a.rows) {
-      int64_t id = a.next[r];
+      int64_t id = r < 256 ? ids[r] : a.next[r];
       id = id < 0 ? 0 : (id > a.V - 1 ? a.V - 1 : id);
       ss = embed_row(a.table + id * a.H, a.h + (int64_t)r * a.H, a.H, t, a.xw_norm,
                      a.xw ? a.xw + (int64_t)r * a.H : nullptr);
