@@ -1096,10 +1096,14 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
   constexpr int QROWS = 64 * R;   // query rows per workgroup
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, g4 = lane >> 4;
+  // HW = min(G, 2) query heads per workgroup (4 HW waves): G = 4 runs two
+  // workgroups per (sequence, kv head, query block), heads 2 hp and 2 hp + 1
+  constexpr int HW = G < 2 ? G : 2, HP = G / HW;
   const int head = wave >> 2, rg = wave & 3;
-  const int per_qb = a.B * a.Hkv;
+  const int per_qb = a.B * a.Hkv * HP;
   const int qb = a.nqb - 1 - (int)(blockIdx.x / per_qb);
-  const int rem = blockIdx.x - (a.nqb - 1 - qb) * per_qb;
+  const int rem3 = blockIdx.x - (a.nqb - 1 - qb) * per_qb;
+  const int hp = HP > 1 ? rem3 % HP : 0, rem = HP > 1 ? rem3 / HP : rem3;
   const int b = rem / a.Hkv, kvh = rem - (rem / a.Hkv) * a.Hkv;
   int start = a.starts[b];  // clamped so rows sit in [0, Lmax) (host: S <= Lmax)
   start = start < 0 ? 0 : (start > a.Lmax - a.S ? a.Lmax - a.S : start);
@@ -1112,7 +1116,7 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
 #pragma unroll
   for (int r = 0; r < R; ++r) my_pos[r] = start + min(i0 + 16 * r + col, a.S - 1);
   const int wave_last = start + min(i0 + 16 * R - 1, a.S - 1);
-  const int hq = kvh * G + head;
+  const int hq = kvh * G + hp * HW + head;
   const float c_exp = a.scale * 1.4426950408889634f;  // scale * log2(e)
 
   // q^T fragments: lane (row col of tile r, dims 32 t + 8 g4 ..), bf16 hi + lo
@@ -1167,7 +1171,7 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
     uint16_t *kb = k_lds0 + (blk & 1) * PKB * D;
     uint16_t *vb = v_lds0 + (blk & 1) * PKB * D;
     // 2 x 16 instructions of 64 lanes (K, then V), spread over the waves
-    for (int ins = __builtin_amdgcn_readfirstlane(wave); ins < 32; ins += 4 * G) {
+    for (int ins = __builtin_amdgcn_readfirstlane(wave); ins < 32; ins += 4 * HW) {
       const int gidx = 64 * (ins & 15) + lane;  // 16-byte granule of the block
       const int r = gidx >> 4, c = gidx & 15;
       const int key = blk * PKB + r;
@@ -1255,18 +1259,18 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
           for (int i = 0; i < 4; ++i) mb = fmaxf(mb, s[r][kt][i]);
         mb = wave_max4(mb);
         // key 0 is visible to every row and block 0 is never skipped, so
-        // m_new is finite from the first block on.
-        // p = exp(scale (s - m)) = exp2(c s - c m), c = scale * log2(e), on
-        // v_exp_f32 (terms below 2^-126 of the row maximum flush to zero)
+        // m_new is finite from the first block on (f = exp2(-inf) = 0 there).
+        // p = exp(scale (s - m)) = exp2(c (s - m)), c = scale * log2(e), on
+        // v_exp_f32 (terms below 2^-126 of the row maximum flush to zero):
+        // exactly 1 at the maximum, and f exactly 1 while the maximum stays
         const float m_new = fmaxf(m_run[r], mb);
-        const float cm = c_exp * m_new;
-        const float f = m_run[r] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(c_exp * m_run[r] - cm);
+        const float f = __builtin_amdgcn_exp2f(c_exp * (m_run[r] - m_new));
         float ls = 0.f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(fmaf(c_exp, s[r][kt][i], -cm));
+            const float e = __builtin_amdgcn_exp2f(c_exp * (s[r][kt][i] - m_new));
             s[r][kt][i] = e;
             ls += e;
           }
@@ -1321,7 +1325,7 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
       rxw8_gqa_prefill_wh_d128_g##G(PrefillArgs a) {                                 \
     attn_prefill_wh<G>(a);                                                           \
   }                                                                                  \
-  extern "C" __global__ void __launch_bounds__(256 * G)                              \
+  extern "C" __global__ void __launch_bounds__(256 * (G < 2 ? G : 2))                \
       __attribute__((amdgpu_waves_per_eu(2))) rxw8_gqa_prefill_r2_d128_g##G(PrefillArgs a) { \
     attn_prefill_rt<G, 2>(a);                                                        \
   }

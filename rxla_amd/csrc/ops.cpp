@@ -1074,16 +1074,17 @@ int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t 
   a.out_f32 = out_f32;
   char kname[48];
   const int G = (int)(Hq / Hkv);
-  // G <= 2: one query head per wave (4 G waves per workgroup), two 16-row
-  // tiles per wave (128 query rows per workgroup) and LDS-DMA staging: at the
-  // C5 prompt shape 82.7 us against 94.3 (one tile) and 120.5 (all heads per
-  // wave, one wave per SIMD). G = 4 keeps the all-heads kernel (the per-head
-  // variants would spill at 1024 threads). RXW8_PREFILL_R2=0 selects the
-  // one-tile kernel, RXW8_PREFILL_R2=0 RXW8_PREFILL_WH=0 the all-heads one.
+  // The two-tile kernel: one query head per wave, min(G, 2) heads per
+  // workgroup (4 waves each; G = 4 takes two workgroups per kv head), two
+  // 16-row tiles per wave (128 query rows per workgroup), K and V by LDS
+  // DMA: at the C5 prompt shape 72.8 us against 94.3 (one tile) and 120.5
+  // (all heads per wave, one wave per SIMD). RXW8_PREFILL_R2=0 selects the
+  // one-tile kernel for G <= 2 and the all-heads one for G = 4;
+  // RXW8_PREFILL_R2=0 RXW8_PREFILL_WH=0 the all-heads one for every G.
   static const int wh_env = env_int("RXW8_PREFILL_WH", 1);
   static const int r2_env = env_int("RXW8_PREFILL_R2", 1);
   // (the two-tile kernel addresses a cache plane with 32-bit byte offsets)
-  const bool r2 = r2_env && G <= 2 && Lmax <= ((int64_t)1 << 22);
+  const bool r2 = r2_env && G <= 4 && Lmax <= ((int64_t)1 << 22);
   const bool wh = wh_env && G <= 2;
   if (r2) a.nqb = (int)((S + 127) / 128);
   std::snprintf(kname, sizeof kname,
@@ -1092,7 +1093,11 @@ int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t 
                 G);
   // K and V^T blocks of 64 keys, double-buffered (2 x (64*128 + 128*72) bf16)
   constexpr size_t lds = 2 * (64 * 128 + 128 * 72) * 2;
-  return launch(rt, kname, dim3((unsigned)(a.nqb * B * Hkv)), dim3(wh || r2 ? 256 * G : 256), a, lds);
+  // the two-tile kernel: min(G, 2) heads per workgroup, G / min(G, 2) workgroups per kv head
+  const int hw = G < 2 ? G : 2;
+  if (r2)
+    return launch(rt, kname, dim3((unsigned)(a.nqb * B * Hkv * (G / hw))), dim3(256 * hw), a, lds);
+  return launch(rt, kname, dim3((unsigned)(a.nqb * B * Hkv)), dim3(wh ? 256 * G : 256), a, lds);
 }
 
 
