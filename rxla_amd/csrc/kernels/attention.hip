@@ -1332,6 +1332,12 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
 RXW8_PREFILL(1)
 RXW8_PREFILL(2)
 RXW8_PREFILL(4)
+// 8 query heads per kv head: the two-tile kernel only (four workgroups of
+// two heads per kv head)
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+rxw8_gqa_prefill_r2_d128_g8(PrefillArgs a) {
+  attn_prefill_rt<8, 2>(a);
+}
 
 // ---- generic decode attention (any D <= 256, any group, f32 or bf16 cache):
 // one workgroup per (b, query head); scores staged in LDS (Lmax <= 8192).

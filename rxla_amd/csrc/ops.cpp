@@ -1006,7 +1006,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
 // into [0, Lmax - S]). D = 128, bf16 caches, Hq / Hkv in {1, 2, 4}.
 bool prefill_supported(int64_t Hq, int64_t Hkv, int64_t D, int cache_f32) {
   const int64_t G = Hkv > 0 ? Hq / Hkv : 0;
-  return !cache_f32 && D == 128 && Hkv > 0 && Hq % Hkv == 0 && (G == 1 || G == 2 || G == 4);
+  return !cache_f32 && D == 128 && Hkv > 0 && Hq % Hkv == 0 && (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
 // Causal prefill on the general GQA kernel: q / out element (b, i, h, d) at
@@ -1084,8 +1084,15 @@ int prefill_launch(Runtime *rt, const void *q, int q_f32, int64_t q_sb, int64_t 
   static const int wh_env = env_int("RXW8_PREFILL_WH", 1);
   static const int r2_env = env_int("RXW8_PREFILL_R2", 1);
   // (the two-tile kernel addresses a cache plane with 32-bit byte offsets)
-  const bool r2 = r2_env && G <= 4 && Lmax <= ((int64_t)1 << 22);
+  const bool r2 = r2_env && (G <= 4 || G == 8) && Lmax <= ((int64_t)1 << 22);
   const bool wh = wh_env && G <= 2;
+  if (G == 8 && !r2) {  // no all-heads kernel for 8 heads: the general GQA kernel
+    if (slots)
+      return fail(RXW8_UNIMPLEMENTED, "prefill attention: 8 heads per kv head with cache slots "
+                                      "needs the two-tile kernel (Lmax <= 2^22)");
+    return prefill_general(rt, q, !q_f32, q_sb, q_ss, q_sh, kc, vc, starts, out, !out_f32, o_sb,
+                           o_ss, o_sh, B, S, Hq, Hkv, Lmax, 128, scale);
+  }
   if (r2) a.nqb = (int)((S + 127) / 128);
   std::snprintf(kname, sizeof kname,
                 r2 ? "rxw8_gqa_prefill_r2_d128_g%d"
