@@ -1120,6 +1120,7 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
   const float c_exp = a.scale * 1.4426950408889634f;  // scale * log2(e)
 
   // q^T fragments: lane (row col of tile r, dims 32 t + 8 g4 ..), bf16 hi + lo
+  // of c q in f32, so the scores come out as c s (c = scale * log2(e))
   u32x4 qhi[R][4], qlo[R][4];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -1139,6 +1140,8 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
       } else {
         unpack_bf16x8(*(const u32x4 *)((const uint16_t *)a.q + off), v);
       }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] *= c_exp;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float h0 = round_bf16(v[2 * e]), h1 = round_bf16(v[2 * e + 1]);
@@ -1242,9 +1245,9 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
       u32x4 pb[R][2];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        // Raw scores (the scale is folded into the exponent below); the
-        // causal mask only where some key of the block lies past the tile's
-        // first row (wave-uniform).
+        // Scores c s (the scale and log2(e) are folded into q); the causal
+        // mask only where some key of the block lies past the tile's first
+        // row (wave-uniform).
         if (j0 + PKB - 1 > start + i0 + 16 * r) {
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt)
@@ -1260,17 +1263,17 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
         mb = wave_max4(mb);
         // key 0 is visible to every row and block 0 is never skipped, so
         // m_new is finite from the first block on (f = exp2(-inf) = 0 there).
-        // p = exp(scale (s - m)) = exp2(c (s - m)), c = scale * log2(e), on
-        // v_exp_f32 (terms below 2^-126 of the row maximum flush to zero):
-        // exactly 1 at the maximum, and f exactly 1 while the maximum stays
+        // p = exp(scale (s - m)) = exp2(c s - c m) on v_exp_f32 (terms below
+        // 2^-126 of the row maximum flush to zero): exactly 1 at the maximum,
+        // and f exactly 1 while the maximum stays
         const float m_new = fmaxf(m_run[r], mb);
-        const float f = __builtin_amdgcn_exp2f(c_exp * (m_run[r] - m_new));
+        const float f = __builtin_amdgcn_exp2f(m_run[r] - m_new);
         float ls = 0.f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(c_exp * (s[r][kt][i] - m_new));
+            const float e = __builtin_amdgcn_exp2f(s[r][kt][i] - m_new);
             s[r][kt][i] = e;
             ls += e;
           }
