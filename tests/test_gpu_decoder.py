@@ -111,6 +111,29 @@ def test_decoder_long_prefill_matches_oracle(rt):
     np.testing.assert_array_equal(model.lens()[:batch], [43, 43])
 
 
+@pytest.mark.parametrize("q_heads,kv_heads", [(8, 2), (16, 2)])
+def test_decoder_prefill_wide_groups_match_oracle(rt, q_heads, kv_heads):
+    """4 and 8 query heads per kv head: the prompt's attention runs on the
+    two-tile prefill kernel as two / four workgroups of two heads per kv head
+    (cache slots, rows from position 0), then decode steps; against the
+    oracle decoder."""
+    cfg = small_cfg(q_heads=q_heads, kv_heads=kv_heads, hidden=128 * q_heads, max_seq=48)
+    params = tiny_params(cfg, seed=95 + q_heads, std=0.03)
+    batch = 2
+    model = build(rt, cfg, params, batch)
+    dec = oracle.Decoder(cfg, params, batch)
+    ids = np.random.default_rng(96).integers(0, cfg["vocab"], (batch, 24)).astype(np.int32)
+    lg, nxt, rlg, rnxt = step_both(rt, model, dec, ids)
+    err = rel_err(lg, rlg)
+    print(f"G={q_heads // kv_heads} prefill logits rel_err={err:.3e}")
+    assert err <= 1e-2
+    for step in range(2):
+        lg, nxt, rlg, rnxt = step_both(rt, model, dec, rnxt.reshape(batch, 1).astype(np.int32))
+        err = rel_err(lg, rlg)
+        print(f"G={q_heads // kv_heads} decode step {step} rel_err={err:.3e}")
+        assert err <= 1e-2
+
+
 @pytest.mark.parametrize("inter", [2048, 6144])
 def test_decoder_c5_widths_match_oracle(rt, inter):
     """Hidden 2048 / 16 q heads / 8 kv heads and intermediate 6144 (the C5
