@@ -92,15 +92,18 @@ def test_prefill_c5_shape(rt):
         assert err <= TIGHT
 
 
-def test_prefill_bf16_q_and_first_row_is_value_row(rt):
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_prefill_bf16_q_and_first_row_is_value_row(rt, group):
     """Row 0 at position 0 sees key 0 alone: its output is exactly v[0]
-    (softmax of one key), which pins the mask edge and the V^T indexing."""
-    rng = np.random.default_rng(7)
-    q, kc, vc = make(rng, 2, 70, 8, 2, 128)
+    (softmax of one key: probability exactly 1), which pins the mask edge,
+    the V^T indexing and each head's kv head for every group size."""
+    rng = np.random.default_rng(7 + group)
+    hq = 2 * group
+    q, kc, vc = make(rng, 2, 70, hq, 2, 128)
     out = run_prefill(rt, q, kc, vc, [0, 0], q_bf16=True)
     v0 = oracle.bf16_to_f32(vc[:, :, 0, :])  # [B, Hkv, D]
-    for h in range(8):
-        np.testing.assert_allclose(out[:, 0, h], v0[:, h // 4], rtol=0, atol=0)
+    for h in range(hq):
+        np.testing.assert_allclose(out[:, 0, h], v0[:, h // group], rtol=0, atol=0)
     ref = oracle_prefill(oracle.round_bf16(q), kc, vc, np.array([0, 0]))
     assert rel_err(out, ref) <= TIGHT
 
