@@ -363,8 +363,11 @@ static GemvPlan plan_gemv(const Runtime *rt, int64_t m, int64_t n, int64_t k, in
   p.ks = pick;
   p.lds = gemv_lds(m, k / pick, k, g, p.rw, p.mb, w_bf16);
   const int64_t chunks = k / pick / kw / slice;
+  // bf16 weights: 2-deep groups (48-54 VGPRs, 8 waves per SIMD) stream
+  // faster than 4-deep (74-76, 6 waves): the lm_head's 622 MB (8 rows x
+  // 2048 x 151936) in 101.5 against 104.6-105.0 us
   const int forced_u = env_int("RXW8_GEMV_U", 0);
-  p.u = forced_u == 8 || forced_u == 2 || forced_u == 1 ? forced_u : 4;
+  p.u = forced_u == 8 || forced_u == 4 || forced_u == 2 || forced_u == 1 ? forced_u : (w_bf16 ? 2 : 4);
   while (chunks % (2 * p.u)) p.u /= 2;
   return p;
 }
