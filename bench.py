@@ -5,17 +5,19 @@ One step = one pass of the decode dequant-GEMV over the whole sweep
 B in {1, 4, 16} x N in {4096, 6144, 24576}, K = 4096, per-output-channel
 scales (9 launches). Weights are in the tiled layout of rxw8_pack_weight
 (packed once, outside the timed region; same bytes as the row-major U8).
-Every launch reads its own copy of the int8 weights (copies rotate,
->= 6 x 143 MB of distinct weights), so the 256 MB MALL holds no reusable
-weight bytes and the figure is HBM bandwidth.
+Every launch reads a copy of the int8 weights of its own: each N has a pool
+of 48 / 36 / 12 copies and launch (b, n) of step t reads copy
+(3 t + index of b) mod pool size, so a copy is read again only after at
+least 790 MB of other weights of that N (3 x the 256 MB MALL): no weight byte
+is served from the MALL and the figure is HBM bandwidth.
 
 value        = sweep algorithmic bytes / wall time of the timed steps (GB/s);
-               each step is the 9 launches, replayed from HIP graphs that
-               hold one step per weight copy in turn (a graph boundary idles
-               the GPU for ~8 us; the remainder of K steps replays one-step
-               graphs)
+               each step is the 9 launches, replayed from HIP graphs: one of
+               48 consecutive steps (every pool turns over a whole number of
+               times in it) replayed K // 48 times, then one of the first
+               K % 48 steps (a graph boundary idles the GPU for ~8 us)
 roofline     = the GEMV kernel of the largest sweep shape, B=1 N=24576
-               (rxw8_gemv_w8_pk_mb1_rw3_u4_w12: 12 waves, 48-row tiles, 512
+               (rxw8_gemv_rc_w8_pk_mb1_rw3_u4_w12: 12 waves, 48-row tiles, 512
                workgroups = 2 whole rounds): algorithmic bytes per launch /
                launch duration, from HIP events on the runtime's stream around
                runs of back-to-back launches of the shape; traffic = the HBM
@@ -115,8 +117,15 @@ def cpu_baseline(budget_s=12.0):
 
 
 SPIN_CYCLES = 2_000_000  # torch.cuda._sleep spacer, about 1 ms of shader clocks
-ROOF_CYCLES = 4          # passes over the weight copies per roofline event pair
+ROOF_CYCLES = 2          # passes over the weight copies per roofline event pair
 MALL_BYTES = 256 << 20   # MI355X last-level (Infinity) cache
+# Weight copies per N of the sweep: (copies - 1) x N x K >= 790 MB (3 x the
+# MALL) of other weights of that N stream between two reads of one copy.
+# Multiples of 3 (the three batch sizes of a step) whose turns all fit
+# GRAPH_STEPS steps a whole number of times: 48 steps x 3 launches per N =
+# 3 x 48 = 4 x 36 = 12 x 12.
+POOL = {4096: 48, 6144: 36, 24576: 12}
+GRAPH_STEPS = 48
 ATTN_COPIES = 3          # rotating KV caches of the C4 leg
 
 
@@ -166,6 +175,47 @@ def cpu_decoder_baseline(steps=8, ctx=1024, batch=8, seed=11):
             "cores": threads, "kind": "port",
             "sample": f"{steps} greedy decode steps of the 28-layer C5 decoder at full size, batch "
                       f"{batch}, caches at {ctx} positions, through oracle.Decoder (C, OpenMP)"}
+
+
+class SweepPools:
+    """The sweep's operands: POOL[n] weight copies per N (row-major U8 as
+    encoded, and the packed copies the timed legs read), bf16 x [B, K] and
+    bf16 y [B, N]. Launch (b, n) of step t reads copy (3 t + index of b) mod
+    POOL[n]; launch_next continues a per-N cursor for the per-shape timing."""
+
+    def __init__(self, rt, rx, torch, stream, gen):
+        self.rt, self.rx, self.torch = rt, rx, torch
+        log(f"encoding {sum(POOL.values())} weight copies ({POOL}) from N(0, 0.02)")
+        self.rowmajor = {n: [c5_quantized(rt, rx, torch, stream, gen, n, K) for _ in range(POOL[n])]
+                         for n in NS}
+        self.packed = {n: [(rx.pack_weight(rt, u), s) for u, s in self.rowmajor[n]] for n in NS}
+        with torch.cuda.stream(stream):
+            self.xs = {b: torch.randn((b, K), device="cuda", generator=gen).to(torch.bfloat16)
+                       for b in BS}
+            self.ys = {(b, n): torch.empty((b, n), dtype=torch.bfloat16, device="cuda")
+                       for b in BS for n in NS}
+        stream.synchronize()
+        rt.synchronize()
+        self.xb = {b: rt.wrap_tensor(self.xs[b]) for b in BS}
+        self.yb = {k: rt.wrap_tensor(v) for k, v in self.ys.items()}
+        self.plan = [(b, n) for n in NS for b in BS]
+        self.cursor = {n: 0 for n in NS}
+
+    def launch(self, b, n, copy, wts):
+        u, s = wts[n][copy % POOL[n]]
+        self.rx.quantized_linear(self.rt, self.xb[b], u, s, self.rx.DType.BF16,
+                                 out=self.yb[(b, n)])
+
+    def launch_step(self, step, wts):
+        for b, n in self.plan:
+            self.launch(b, n, 3 * step + BS.index(b), wts)
+
+    def launch_next(self, b, n, wts):
+        self.launch(b, n, self.cursor[n], wts)
+        self.cursor[n] += 1
+
+    def release(self):
+        self.rowmajor = self.packed = None
 
 
 def c5_quantized(rt, rx, torch, stream, gen, n, k, std=0.02, group=None):
@@ -409,7 +459,12 @@ def qwen35_weights(rt, rx, torch, stream, model, group, seed=7):
     return keep
 
 
-def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, iterations=10,
+# The reference's own published W8 runs of this workload (RTX 5080, JAX CUDA 13
+# PJRT plugin; docs/QWEN3.5-BENCHMARK.md:68-80): mean ms per run by sequence.
+QWEN35_REFERENCE_MS = {1: 2.393, 16: 10.535}
+
+
+def bench_qwen35(rt, rx, torch, stream, sequences=(1, 16, 256, 1024), warmup=2, iterations=10,
                  compute="f32"):
     """The reference's qwen3_5_bench workload (crates/rxla-safetensors/examples/
     qwen3_5_bench.rs:44-99) on the official 0.8B text topology with random
@@ -443,6 +498,8 @@ def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, ite
                         "weight_GBs": round(weight_bytes / mean / 1e9, 1),
                         "finite": bool(np.isfinite(lg).all()),
                         "checksum": float(lg.astype(np.float64).sum())}
+        if S in QWEN35_REFERENCE_MS:
+            res[f"S{S}"]["reference_ms_rtx5080"] = QWEN35_REFERENCE_MS[S]
         del logits
     del keep, model
     return {"runs": res, "weight_bytes": weight_bytes, "compute_dtype": compute,
@@ -456,7 +513,9 @@ def bench_qwen35(rt, rx, torch, stream, sequences=(16, 256, 1024), warmup=2, ite
 def pmc_probe(kind, rounds=3):
     """A short fixed program for rocprofv3 runs: one roofline leg launched as
     the bench times it (gemv / gemv16: `rounds` x [spin spacer, ROOF_CYCLES
-    passes over 6 weight copies back to back] at B = 1 / 16; attention:
+    passes over the 12 weight copies of N = 24576 back to back] at B = 1 / 16;
+    sweep: 2 x 48 whole steps of the sweep, eager, with the bench's copy
+    rotation (counters summed over a step's 9 launches); attention:
     `rounds` x [spin spacer, 20 C4 calls over the rotating caches]; gemm: 30
     launches of the C3 roofline shape; decoder: the C5 leg with 16 decode
     steps; prefill: the prefill-attention leg) plus 4 plain 256 MiB device
@@ -473,9 +532,9 @@ def pmc_probe(kind, rounds=3):
         src = torch.randn(1 << 26, device="cuda", generator=gen)  # 256 MiB
         dst = torch.empty_like(src)
     stream.synchronize()
-    if kind in ("gemv", "gemv16"):  # B=1 (or 16), N=24576, K=4096, packed, 6 rotating copies
+    if kind in ("gemv", "gemv16"):  # B=1 (or 16), N=24576, K=4096, packed, its 12 rotating copies
         n, b = 24576, (16 if kind == "gemv16" else 1)
-        ws = [c5_quantized(rt, rx, torch, stream, gen, n, K) for _ in range(6)]
+        ws = [c5_quantized(rt, rx, torch, stream, gen, n, K) for _ in range(POOL[n])]
         with torch.cuda.stream(stream):
             x = torch.randn((b, K), device="cuda", generator=gen).to(torch.bfloat16)
             y = torch.empty((b, n), dtype=torch.bfloat16, device="cuda")
@@ -486,10 +545,18 @@ def pmc_probe(kind, rounds=3):
         for _ in range(rounds):
             with torch.cuda.stream(stream):
                 torch.cuda._sleep(SPIN_CYCLES)
-            for i in range(ROOF_CYCLES * 6):
-                rx.quantized_linear(rt, xb, wb[i % 6][0], wb[i % 6][1], rx.DType.BF16, out=yb)
-        reps = rounds * ROOF_CYCLES * 6
+            for i in range(ROOF_CYCLES * POOL[n]):
+                u, s_ = wb[i % POOL[n]]
+                rx.quantized_linear(rt, xb, u, s_, rx.DType.BF16, out=yb)
+        reps = rounds * ROOF_CYCLES * POOL[n]
         log(f"pmc probe gemv B={b} N={n} K={K}: {reps} launches, {gemv_bytes(b, n)} algorithmic B each")
+    elif kind == "sweep":  # whole sweep steps with the bench's rotation, eager
+        pools = SweepPools(rt, rx, torch, stream, gen)
+        for st in range(2 * GRAPH_STEPS):
+            pools.launch_step(st, pools.packed)
+        step_bytes = sum(gemv_bytes(b, n) for b, n in pools.plan)
+        log(f"pmc probe sweep: {2 * GRAPH_STEPS} steps of {len(pools.plan)} launches, "
+            f"{step_bytes} algorithmic B per step")
     elif kind == "gemm":  # C3 roofline shape M=8192 N=12288 K=4096, 10 launches after warm-up
         m, n = 8192, 12288
         u, sb = c5_quantized(rt, rx, torch, stream, gen, n, K)
@@ -544,13 +611,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--copies", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-gemm", action="store_true")
     ap.add_argument("--skip-attention", action="store_true")
     ap.add_argument("--skip-decoder", action="store_true")
     ap.add_argument("--skip-qwen35", action="store_true")
-    ap.add_argument("--pmc-probe", choices=["gemv", "gemv16", "gemm", "attention", "decoder", "prefill"],
+    ap.add_argument("--pmc-probe", choices=["gemv", "gemv16", "sweep", "gemm", "attention", "decoder",
+                                            "prefill"],
                     help="counter-collection program only")
     ap.add_argument("--qwen35-only", action="store_true",
                     help="(profiling) run only the Qwen3.5 leg and print its JSON")
@@ -579,172 +646,136 @@ def main():
         print(json.dumps({"decoder": bench_decoder(rt, rx, torch, stream)}), flush=True)
         return
     gen = torch.Generator(device="cuda").manual_seed(0)
-    log(f"device {info}; encoding {args.copies} weight copies per N from N(0, 0.02)")
-    weights = {n: [c5_quantized(rt, rx, torch, stream, gen, n, K) for _ in range(args.copies)]
-               for n in NS}
-    with torch.cuda.stream(stream):
-        xs = {b: torch.randn((b, K), device="cuda", generator=gen).to(torch.bfloat16) for b in BS}
-        ys = {(b, n): torch.empty((b, n), dtype=torch.bfloat16, device="cuda")
-              for b in BS for n in NS}
-    stream.synchronize()
-    layout = os.environ.get("RXW8_BENCH_LAYOUT", "packed")
-    # the timed layout, and the reference's row-major U8 layout for the second leg
-    wb = {n: [((rx.pack_weight(rt, u) if layout == "packed" else u), s) for u, s in weights[n]]
-          for n in NS}
-    wb_row = {n: list(weights[n]) for n in NS}
-    rt.synchronize()
-    xb = {b: rt.wrap_tensor(xs[b]) for b in BS}
-    yb = {k: rt.wrap_tensor(v) for k, v in ys.items()}
-    plan = [(b, n) for n in NS for b in BS]
+    pools = SweepPools(rt, rx, torch, stream, gen)
+    xb, yb, ys = pools.xb, pools.yb, pools.ys
+    wb, wb_row = pools.packed, pools.rowmajor
+    plan = pools.plan
     step_bytes = sum(gemv_bytes(b, n) for b, n in plan)
 
-    def launch_all(copy, events=None, wts=None):
-        for b, n in plan:
-            u, s = (wts or wb)[n][copy]
-            if events is not None:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-            rx.quantized_linear(rt, xb[b], u, s, rx.DType.BF16, out=yb[(b, n)])
-            if events is not None:
-                e1.record(stream)
-                events.append((b, n, e0, e1))
+    def launch_all(step, events=None, wts=None):
+        pools.launch_step(step, wts or wb)
 
-    # Eager warmup (sizes workspaces, resolves kernels), then HIP graphs of
-    # the 9 launches of a step: one per weight copy, and one holding a step
-    # per copy in turn (`copies` steps: a replay boundary costs ~8 us of idle
-    # GPU, so the timed steps replay the multi-step graph and the one-step
-    # graphs only for the remainder).
+    # Eager warmup (sizes workspaces, resolves kernels), then HIP graphs: one
+    # holding GRAPH_STEPS consecutive steps (every pool turns over a whole
+    # number of times in it, so replays follow each other seamlessly) and one
+    # holding the first K % GRAPH_STEPS steps; the timed region replays the
+    # first K // GRAPH_STEPS times, then the second once (a graph boundary
+    # idles the GPU for ~8 us).
     for i in range(args.warmup):
-        launch_all(i % args.copies)
+        launch_all(GRAPH_STEPS - args.warmup + i)
     torch.cuda.synchronize()
-    eager = {k: v.clone() for k, v in ys.items()}
 
-    def step_graphs(wts=None):
-        singles = []
-        for c in range(args.copies):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                launch_all(c, wts=wts)
-            singles.append(g)
-        multi = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(multi, stream=stream):
-            for c in range(args.copies):
-                launch_all(c, wts=wts)
-        return singles, multi
+    def step_graph(first, count, wts=None):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for st in range(first, first + count):
+                launch_all(st, wts=wts)
+        return g
 
-    def run_steps(singles, multi, steps):
-        for _ in range(steps // args.copies):
-            multi.replay()
-        for c in range(steps % args.copies):
-            singles[c].replay()
+    def timed_graphs(wts=None):
+        full = step_graph(0, GRAPH_STEPS, wts) if args.steps >= GRAPH_STEPS else None
+        rem = step_graph(0, args.steps % GRAPH_STEPS, wts) if args.steps % GRAPH_STEPS else None
+        return full, rem
 
-    graphs, graph_multi = step_graphs()
-    for i in range(args.warmup):
-        graphs[i % args.copies].replay()
-    graph_multi.replay()
-    torch.cuda.synchronize()
-    launch_all((args.warmup - 1) % args.copies)  # eager result of the last graph's copy
-    torch.cuda.synchronize()
-    ref = {k: v.clone() for k, v in ys.items()}
-    graphs[(args.warmup - 1) % args.copies].replay()
-    torch.cuda.synchronize()
-    assert all(torch.equal(ys[k], ref[k]) for k in ys), "graph replay differs from eager launch"
-    launch_all(args.copies - 1)  # the multi-step graph ends with the last copy's step
-    torch.cuda.synchronize()
-    ref = {k: v.clone() for k, v in ys.items()}
-    graph_multi.replay()
-    torch.cuda.synchronize()
-    assert all(torch.equal(ys[k], ref[k]) for k in ys), "multi-step replay differs from eager launch"
+    def run_steps(full, rem, steps):
+        for _ in range(steps // GRAPH_STEPS):
+            full.replay()
+        if rem is not None:
+            rem.replay()
 
-    # Timed region: exactly K steps (multi-step replays + the remainder),
-    # synchronized on both sides.
+    graph_full, graph_rem = timed_graphs()
+    # replays equal eager launches: after a graph of steps [0, n) every output
+    # holds step n - 1's result
+    for g, last in ((graph_full, GRAPH_STEPS - 1), (graph_rem, args.steps % GRAPH_STEPS - 1)):
+        if g is None:
+            continue
+        launch_all(last)
+        torch.cuda.synchronize()
+        ref = {k: v.clone() for k, v in ys.items()}
+        g.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(ys[k], ref[k]) for k in ys), "graph replay differs from eager launch"
+    # warm the timed graphs; the last warm step is GRAPH_STEPS - 1, so the
+    # timed step 0 reads copies last read a whole pool turn ago
+    if graph_full is not None:
+        graph_full.replay()
+    else:
+        for st in range(GRAPH_STEPS):
+            launch_all(st)
+
+    # Timed region: exactly K steps, synchronized on both sides.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    run_steps(graphs, graph_multi, args.steps)
+    run_steps(graph_full, graph_rem, args.steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     log(f"timed {args.steps} graph steps in {wall:.4f} s")
 
-
     # Kernel durations: per shape, one HIP event pair on the runtime stream
-    # around `copies` back-to-back eager launches (one per weight copy), queued
-    # behind a ~1 ms spin kernel (no memory traffic: a fill spacer would leave
-    # dirty cache lines whose write-back lands inside the timed launches) so
-    # the host submits them all before the GPU reaches the first event; shapes
-    # interleave so no copy is reused from the MALL.
+    # around one pass over that N's pool (one launch per copy, the pool's
+    # cursor continuing across shapes), queued behind a ~1 ms spin kernel (no
+    # memory traffic: a fill spacer would leave dirty cache lines whose
+    # write-back lands inside the timed launches) so the host submits them all
+    # before the GPU reaches the first event. Every copy is read again only
+    # after at least 512 MB of other weights: none comes from the MALL.
     def spacer():
         with torch.cuda.stream(stream):
             torch.cuda._sleep(SPIN_CYCLES)
 
-    # A shape whose other copies stream at least 1.5x the MALL before one is
-    # read again gets ROOF_CYCLES passes per event pair (the roofline's rule:
-    # the pair's fixed cost then spreads over more launches); others one pass.
-    def cycles_for(n):
-        return ROOF_CYCLES if (args.copies - 1) * n * K >= 1.5 * MALL_BYTES else 1
-
     events = []
-    rounds = max(3, args.steps // args.copies)
+    rounds = 3
     for _ in range(rounds):
         for b, n in plan:
             spacer()
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            for c in range(cycles_for(n) * args.copies):
-                u, s = wb[n][c % args.copies]
-                rx.quantized_linear(rt, xb[b], u, s, rx.DType.BF16, out=yb[(b, n)])
+            for _c in range(POOL[n]):
+                pools.launch_next(b, n, wb)
             e1.record(stream)
             events.append((b, n, e0, e1))
-    # The roofline shape: ROOF_CYCLES passes over the copies per event pair
-    # when each copy's 100 MB is read again only after the other copies have
-    # streamed at least 1.5x the 256 MB MALL (6 copies: 503 MB), so none is
-    # served from it; one pass otherwise.
+    # The roofline shape (B=1, N=24576): ROOF_CYCLES passes over its pool of
+    # 12 copies per event pair (1.2 GB between reuses of a copy).
     roof_events = []
-    u_roof = [wb[24576][c] for c in range(args.copies)]
-    roof_cycles = ROOF_CYCLES if (args.copies - 1) * 24576 * K >= 1.5 * MALL_BYTES else 1
     for _ in range(rounds):
         spacer()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for i in range(roof_cycles * args.copies):
-            u, s = u_roof[i % args.copies]
-            rx.quantized_linear(rt, xb[1], u, s, rx.DType.BF16, out=yb[(1, 24576)])
+        for _c in range(ROOF_CYCLES * POOL[24576]):
+            pools.launch_next(1, 24576, wb)
         e1.record(stream)
         roof_events.append((e0, e1))
     torch.cuda.synchronize()
-    per_launch = lambda e0, e1: e0.elapsed_time(e1) * 1e-3 / args.copies  # noqa: E731
 
     # The same sweep on the reference's row-major U8 weights (the layout the
     # XLA handlers and direct QuantizedLinear::apply calls receive): graphs of
-    # the same 9 launches, same step count, timed the same way.
-    graphs_row, multi_row = step_graphs(wb_row)
-    for i in range(args.warmup):
-        graphs_row[i % args.copies].replay()
-    multi_row.replay()
+    # the same launches, same step count, timed the same way.
+    row_full, row_rem = timed_graphs(wb_row)
+    if row_full is not None:
+        row_full.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    run_steps(graphs_row, multi_row, args.steps)
+    run_steps(row_full, row_rem, args.steps)
     torch.cuda.synchronize()
     wall_row = time.perf_counter() - t0
-    del graphs_row, multi_row
+    del row_full, row_rem
     log(f"timed {args.steps} row-major graph steps in {wall_row:.4f} s")
 
     per_shape = {}
     for b, n, e0, e1 in events:
-        per_shape.setdefault((b, n), []).append(per_launch(e0, e1) / cycles_for(n))
+        per_shape.setdefault((b, n), []).append(e0.elapsed_time(e1) * 1e-3 / POOL[n])
 
     def kernel_stats(sel):
         ev = [(b, n, e0, e1) for b, n, e0, e1 in events if sel(b)]
         mb = float(np.mean([gemv_bytes(b, n) for b, n, _, _ in ev]))
-        ms = float(np.mean([per_launch(e0, e1) / cycles_for(n) for b, n, e0, e1 in ev]))
+        ms = float(np.mean([e0.elapsed_time(e1) * 1e-3 / POOL[n] for b, n, e0, e1 in ev]))
         return mb, ms
 
     mean_bytes, mean_s = kernel_stats(lambda b: b <= 4)
     b16_bytes, b16_s = kernel_stats(lambda b: b > 4)
     # roofline shape: B=1, N=24576 (the largest decode GEMV of the sweep)
-    roof_s = float(np.median([e0.elapsed_time(e1) * 1e-3 / (roof_cycles * args.copies)
+    roof_s = float(np.median([e0.elapsed_time(e1) * 1e-3 / (ROOF_CYCLES * POOL[24576])
                               for e0, e1 in roof_events]))
     roof_bytes = gemv_bytes(1, 24576)
     achieved = roof_bytes / roof_s / 1e9
@@ -771,20 +802,23 @@ def main():
                 "bf16; torch generator seed 0",
         "config": {"workload": "decode dequant-GEMV sweep (BASELINE configs[1])",
                    "batch": list(BS), "out_features": list(NS), "in_features": K,
-                   "scales": "per-output-channel f32", "weight_copies": args.copies,
-                   "weight_layout": layout,
+                   "scales": "per-output-channel f32",
+                   "weight_copies": {str(n): POOL[n] for n in NS},
+                   "weight_layout": "packed",
                    "launches_per_step": len(plan), "bytes_per_step": step_bytes,
-                   "steps_per_graph_replay": args.copies},
+                   "steps_per_graph_replay": GRAPH_STEPS,
+                   "copy_rotation": "launch (b, n) of step t reads copy (3 t + index of b) mod "
+                                    "copies[n]: a copy is read again after >= 790 MB of other "
+                                    "weights (>= 3 x the 256 MB MALL)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": recorded_traffic() if layout == "packed" else None,
-                     "kernel": "rxw8_gemv_w8_pk_mb1_rw3_u4_w12" if layout == "packed"
-                     else "rxw8_gemv_w8_mb1_rw3_u4_w12",
+                     "traffic": recorded_traffic(),
+                     "kernel": "rxw8_gemv_rc_w8_pk_mb1_rw3_u4_w12",
                      "shape": "B=1 N=24576 K=4096", "launch_us": round(roof_s * 1e6, 3),
                      "launch_bytes": roof_bytes,
                      "timing": "median of HIP event pairs on the runtime stream around "
-                               f"{roof_cycles * args.copies} back-to-back launches of the shape "
-                               f"({roof_cycles} passes over the {args.copies} weight copies, "
+                               f"{ROOF_CYCLES * POOL[24576]} back-to-back launches of the shape "
+                               f"({ROOF_CYCLES} passes over its {POOL[24576]} weight copies, "
                                "after a spin kernel), divided by the launch count (includes "
                                "the inter-kernel gaps)",
                      "traffic_source": "profiles/gemv_B1_N24576_traffic.txt (FETCH_SIZE + "
@@ -795,22 +829,22 @@ def main():
         "roofline_b16": {"bound": "hbm", "achieved": round(b16_bytes / b16_s / 1e9, 2),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(b16_bytes / b16_s / 1e9 / HBM_PEAK_GBS, 4),
-                         "kernels": "N=24576: rxw8_gemv_w8_pk_mb1_rw6_u4_w12 (96-row tiles, LDS-DMA "
-                                    "staging); N=4096 / 6144: the per-shape plans (8-wave 16-row "
-                                    "tiles; 4-wave split-K + rxw8_gemv_splitk_reduce)",
+                         "kernels": "N=24576: rxw8_gemv_rc_w8_pk_mb1_rw6_u4_w12 (96-row tiles, "
+                                    "LDS-DMA staging); N=4096 / 6144: the per-shape plans (8-wave "
+                                    "16-row tiles; 4-wave split-K + rxw8_gemv_splitk_reduce)",
                          "mean_launch_us": round(b16_s * 1e6, 3)},
         "sweep": sweep,
-        "sweep_timing": "per shape, the median over HIP event pairs around back-to-back launches "
-                        "over the 6 weight copies after a spin kernel (N = 24576: 4 passes per pair, "
-                        "as for the roofline; smaller N: one pass, as a repeat would come from the "
-                        "MALL), divided by the launch count",
+        "sweep_timing": "per shape, the median over HIP event pairs around one pass over that "
+                        "N's weight copies (48 / 36 / 12 launches, each copy read again only after "
+                        ">= 790 MB of other weights) after a spin kernel, divided by the launch count",
         "rowmajor": {"value": round(step_bytes * args.steps / wall_row / 1e9, 2), "unit": "GB/s",
                      "ms_per_step": round(wall_row / args.steps * 1e3, 4),
                      "weight_layout": "row-major U8 [N, K] (the reference's weight ABI)",
                      "timing": "same sweep, step count and graph replays as `value`"},
         "device": info,
     }
-    del graphs, graph_multi, weights, wb
+    del graph_full, graph_rem
+    pools.release()
     torch.cuda.synchronize()
     if not args.skip_gemm:
         log("prefill GEMM shapes ...")

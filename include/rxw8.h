@@ -224,8 +224,11 @@ int rxw8_causal_attention_mask(rxw8_runtime *rt, rxw8_buffer *query_positions,
  * rxw8_gqa_decode_into. The split partials and arrival counters live in a
  * fixed device array that each GPU holds for the life of the process
  * (RXW8_NOALLOC_PARTIAL_BYTES + RXW8_NOALLOC_COUNTER_BYTES); a call whose plan
- * needs more fails with RXW8_RESOURCE_EXHAUSTED before any launch (the split
- * plans of the D = 128 kernel need at most about 9 MiB for Hq/Hkv <= 8).
+ * needs more fails with RXW8_RESOURCE_EXHAUSTED before any launch. The split
+ * plans of the D = 128 kernel (Hq/Hkv in {1, 2, 4, 8}) use at most 4 x CUs
+ * partial slots of Hq/Hkv x 130 floats -- 4.1 MiB on 256 CUs -- and the
+ * general kernel none, so on MI355X that happens only for a counter need
+ * (rows x kv heads) above 16384.
  * Every call on one GPU shares that array: calls that overlap on one GPU
  * (other streams, runtimes or threads) race and must be serialised by the
  * caller. The device must have had a runtime created on it (set-up). */
@@ -346,6 +349,22 @@ int rxw8_decoder_reset(rxw8_decoder *dec);
  * logits; logits (optional, device F32 [b, vocab]) receives those logits. */
 int rxw8_decoder_forward(rxw8_decoder *dec, rxw8_buffer *ids, int64_t b,
                          int64_t s, rxw8_buffer *next_ids, rxw8_buffer *logits);
+/* Teacher forcing, for parity tests that isolate each layer's own error (no
+ * counterpart in the reference, whose compiled model runs whole): layers
+ * [first, last) of one forward step of s tokens for b sequences, run as
+ * rxw8_decoder_forward runs them, with the residual stream entering layer
+ * `first` read from hidden_in (device F32 [b, s, hidden]) instead of the
+ * embedding. The tokens sit at each sequence's current length; every layer
+ * run appends its k/v there. hidden_out (device F32 [b, s, hidden]) receives
+ * the residual stream leaving layer last - 1. With logits (device F32
+ * [b, vocab]; needs last == layers) the step's tail runs too: final norm of
+ * the last position and lm_head. commit != 0 advances every length by s (once
+ * per step, with its last layer). INVALID_ARGUMENT unless 0 <= first < last
+ * <= layers and the shapes match; otherwise as rxw8_decoder_forward. */
+int rxw8_decoder_forward_layers(rxw8_decoder *dec, rxw8_buffer *hidden_in,
+                                int64_t b, int64_t s, int64_t first,
+                                int64_t last, rxw8_buffer *hidden_out,
+                                rxw8_buffer *logits, int commit);
 /* Prefill `prompt` (device I32 [b, s]) then `steps` greedy decode steps;
  * out_ids (device I32 [b, steps + 1]) receives the token chosen after the
  * prompt followed by one token per decode step. With use_graph != 0 the

@@ -85,6 +85,10 @@ def _declare(L):
     L.rxo_decoder_forward.restype = c_int
     L.rxo_decoder_forward.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int]
+    L.rxo_decoder_forward_trace.restype = c_int
+    L.rxo_decoder_forward_trace.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                                            c_int, c_void_p]
 
 
 def _c(a, dtype):
@@ -369,15 +373,21 @@ class Decoder:
         self.v_cache = np.zeros(shape, np.uint16)
         self.lens = np.zeros(batch, np.int32)
 
-    def forward(self, ids, threads=0):
+    def forward(self, ids, threads=0, trace=False):
+        """Runs ids [b, s] from the current lengths; returns (logits [b, V],
+        next ids [b]) and, with trace, also the residual stream [layers + 1,
+        b, s, H]: entry l is the input of layer l, the last the output of the
+        final layer (before the final norm)."""
         ids = _c(ids, np.int32)
         b, s = ids.shape
         assert b == self.batch
         logits = np.empty((b, self.cfg["vocab"]), np.float32)
         nxt = np.empty(b, np.int32)
-        rc = lib().rxo_decoder_forward(ctypes.byref(self._c), ctypes.byref(self._p),
-                                       _p(self.k_cache), _p(self.v_cache), _p(self.lens), b, s,
-                                       _p(ids), _p(logits), _p(nxt), threads)
+        hs = np.empty((self.cfg["layers"] + 1, b, s, self.cfg["hidden"]), np.float32) if trace else None
+        rc = lib().rxo_decoder_forward_trace(ctypes.byref(self._c), ctypes.byref(self._p),
+                                             _p(self.k_cache), _p(self.v_cache), _p(self.lens),
+                                             b, s, _p(ids), _p(logits), _p(nxt), threads,
+                                             _p(hs) if trace else None)
         if rc:
             raise ValueError(f"decoder_forward failed ({rc})")
-        return logits, nxt
+        return (logits, nxt, hs) if trace else (logits, nxt)

@@ -519,6 +519,15 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
                         uint16_t *v_cache, int32_t *lens, int64_t b, int64_t s,
                         const int32_t *ids, float *logits, int32_t *next_ids,
                         int threads) {
+  return rxo_decoder_forward_trace(cfg, p, k_cache, v_cache, lens, b, s, ids,
+                                   logits, next_ids, threads, NULL);
+}
+
+int rxo_decoder_forward_trace(const rxo_decoder_config *cfg,
+                              const rxo_decoder_params *p, uint16_t *k_cache,
+                              uint16_t *v_cache, int32_t *lens, int64_t b,
+                              int64_t s, const int32_t *ids, float *logits,
+                              int32_t *next_ids, int threads, float *trace) {
   const int64_t H = cfg->hidden, HQ = cfg->q_heads, HKV = cfg->kv_heads;
   const int64_t D = cfg->head_dim, I = cfg->intermediate, V = cfg->vocab;
   const int64_t L = cfg->max_seq, G = cfg->group;
@@ -555,6 +564,7 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
 
   const float scale = 1.0f / sqrtf((float)D);
   for (int64_t l = 0; l < cfg->layers; ++l) {
+    if (trace) memcpy(trace + l * T * H, h, sizeof(float) * (size_t)(T * H));
     uint16_t *kcl = k_cache + l * b * HKV * L * D;
     uint16_t *vcl = v_cache + l * b * HKV * L * D;
     rxo_rms_norm(h, T, H, p->in_norm[l], cfg->eps, 0, n);
@@ -608,6 +618,7 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
     if (rc) goto done;
     for (int64_t i = 0; i < T * H; ++i) h[i] += tmp[i];
   }
+  if (trace) memcpy(trace + cfg->layers * T * H, h, sizeof(float) * (size_t)(T * H));
   /* final norm + tied bf16 lm_head on the last new position of each sequence */
   for (int64_t bi = 0; bi < b; ++bi)
     memcpy(tmp + bi * H, h + (bi * s + s - 1) * H, sizeof(float) * (size_t)H);

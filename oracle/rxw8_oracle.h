@@ -184,6 +184,15 @@ int rxo_decoder_forward(const rxo_decoder_config *cfg,
                         const int32_t *ids, float *logits, int32_t *next_ids,
                         int threads);
 
+/* rxo_decoder_forward that also records the residual stream: trace
+ * [layers + 1, b * s, H] f32 receives the input of every layer (row bi * s + t)
+ * and, last, the output of the final layer (before the final norm). */
+int rxo_decoder_forward_trace(const rxo_decoder_config *cfg,
+                              const rxo_decoder_params *p, uint16_t *k_cache,
+                              uint16_t *v_cache, int32_t *lens, int64_t b,
+                              int64_t s, const int32_t *ids, float *logits,
+                              int32_t *next_ids, int threads, float *trace);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,7 +31,8 @@ EXPORTS = [
     "rxw8_safetensors_upload",
     "rxw8_decoder_create", "rxw8_decoder_destroy", "rxw8_decoder_num_parameters",
     "rxw8_decoder_parameter_info", "rxw8_decoder_bind_parameter", "rxw8_decoder_reset",
-    "rxw8_decoder_forward", "rxw8_decoder_generate", "rxw8_decoder_lens",
+    "rxw8_decoder_forward", "rxw8_decoder_forward_layers", "rxw8_decoder_generate",
+    "rxw8_decoder_lens",
     "rxw8_qwen35_create", "rxw8_qwen35_destroy", "rxw8_qwen35_num_parameters",
     "rxw8_qwen35_parameter_info", "rxw8_qwen35_bind_parameter", "rxw8_qwen35_forward",
     "rxw8_xla_quantized_linear", "rxw8_xla_gqa_decode", "rxw8_xla_gqa_prefill",
@@ -112,6 +113,8 @@ def _declare(L):
         "rxw8_decoder_bind_parameter": (c_int, [vp, c_char_p, vp]),
         "rxw8_decoder_reset": (c_int, [vp]),
         "rxw8_decoder_forward": (c_int, [vp, vp, c_int64, c_int64, vp, vp]),
+        "rxw8_decoder_forward_layers": (c_int, [vp, vp, c_int64, c_int64, c_int64, c_int64, vp,
+                                                vp, c_int]),
         "rxw8_decoder_generate": (c_int, [vp, vp, c_int64, c_int64, c_int64, vp, c_int]),
         "rxw8_decoder_lens": (c_int, [vp, POINTER(c_int32), c_int64]),
         "rxw8_qwen35_create": (c_int, [vp, POINTER(Qwen35Config), POINTER(vp)]),

@@ -59,6 +59,17 @@ struct EmbedArgs {
   const float *xw_norm = nullptr;
   uint16_t *xw = nullptr;
 };
+struct LoadRowsArgs {
+  const float *h_in;
+  float *h;
+  float *ss;
+  int64_t H;
+  const int32_t *lens;
+  int32_t *pos, *row_seq, *row_len;
+  int s;
+  const float *xw_norm;
+  uint16_t *xw;
+};
 struct InterleaveArgs {
   const float *src;
   float *dst;
@@ -275,6 +286,17 @@ static bool row_norm_enabled(const Decoder *d, int64_t T) {
 
 static unsigned blocks(int64_t n, int per = 256) { return (unsigned)std::max<int64_t>(1, (n + per - 1) / per); }
 
+// Part of a forward step run by the teacher-forcing entry point: the residual
+// rows entering layer `first` come from h_in (instead of the embedding),
+// layers [first, last) run, and the tail (final norm, lm_head, argmax) runs
+// only with `tail` (last == layers), advancing the device lengths only with
+// `advance`.
+struct LayerRange {
+  const float *h_in = nullptr;
+  int first = 0, last = 0;
+  bool tail = false, advance = false;
+};
+
 // Enqueue one forward pass over ids[b, s] (device) starting at the current
 // lengths; writes next ids and logits of the last position; advances lengths.
 // rec (generate): also store the chosen ids in column *rec->step of rec->out.
@@ -284,9 +306,10 @@ static unsigned blocks(int64_t n, int per = 256) { return (unsigned)std::max<int
 // s == 1 for the following step).
 static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
                            const RecordArgs *rec = nullptr, bool embedded = false,
-                           bool embed_next = false) {
+                           bool embed_next = false, const LayerRange *range = nullptr) {
   Runtime *rt = d->rt;
   const int64_t T = b * s;
+  const int l_first = range ? range->first : 0, l_end = range ? range->last : (int)d->L;
   int rc;
   // Decode-sized steps run the fused schedule, 7 launches per layer: the
   // residual-writing GEMVs (o_proj, down) also emit per-16-channel sums of
@@ -322,7 +345,13 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
   // unlike normalising the rows while staging them (RXW8_DEC_ROW_NORM=0).
   const bool rn = fused && row_norm_enabled(d, T);
   const float *in_norm0 = (const float *)d->p(0, P_IN_NORM).bound->ptr;
-  if (!embedded) {
+  if (range) {
+    // the caller's residual rows enter layer l_first (positions as embedded)
+    LoadRowsArgs a{range->h_in, d->h, fused ? d->ss_embed : nullptr, d->H, d->d_lens, d->pos,
+                   d->row_seq, d->row_len, (int)s, nullptr, nullptr};
+    if (rn) a.xw_norm = (const float *)d->p(l_first, P_IN_NORM).bound->ptr, a.xw = d->xn;
+    if ((rc = launch(rt, "rxw8_dec_load_rows", dim3((unsigned)T), dim3(256), a))) return rc;
+  } else if (!embedded) {
     const ParamSpec &e = d->p(-1, P_EMBED);
     // the embedding launch also writes the token positions
     EmbedArgs a{ids, (const uint16_t *)e.bound->ptr, d->h, fused ? d->ss_embed : nullptr, T, d->V,
@@ -332,7 +361,7 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
   }
   const size_t layer_cache = (size_t)d->Bmax * d->Hkv * d->Lmax * d->D;
   const float scale = 1.0f / std::sqrt((float)d->D);
-  for (int l = 0; l < d->L; ++l) {
+  for (int l = l_first; l < l_end; ++l) {
     auto wptr = [&](int kind) -> const uint8_t * {
       const ParamSpec &ps = d->p(l, kind);
       return (const uint8_t *)(ps.packed ? ps.packed->ptr : ps.bound->ptr);
@@ -348,8 +377,8 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
       GemvOptions o;
       o.mode = rn ? 0 : 3, o.row_norm = rn, o.norm_w = fptr(P_IN_NORM), o.eps = d->cfg.eps;
       o.prefer_ks1 = true;
-      o.ss_in = l == 0 ? d->ss_embed : d->ss_down;
-      o.ss_parts = l == 0 ? 1 : (int)(d->H / 16);
+      o.ss_in = l == l_first ? d->ss_embed : d->ss_down;
+      o.ss_parts = l == l_first ? 1 : (int)(d->H / 16);
       if ((rc = gemv_launch(rt, rn ? (const void *)d->xn : (const void *)d->h, rn ? 0 : 1,
                             wptr(P_QKV_W), false, packed(P_QKV_W), fptr(P_QKV_S), d->qkv, 0, T,
                             d->QKV, d->H, d->group_for(d->H), 0, o)))
@@ -449,6 +478,7 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
                              1, T, d->H, d->I, d->group_for(d->I), 1, 1)))
       return rc;
   }
+  if (range && !range->tail) return RXW8_OK;
   // final norm on the last position of each sequence, tied bf16 lm_head, argmax
   const ParamSpec &e = d->p(-1, P_EMBED);
   const bool pk = e.packed != nullptr;
@@ -472,7 +502,8 @@ static int enqueue_forward(Decoder *d, const int32_t *ids, int64_t b, int64_t s,
     ArgmaxArgs a{d->logits, d->am_val, d->am_idx, d->next, d->V, (int)b, d->am_chunks, 1};
     if ((rc = launch(rt, "rxw8_dec_argmax_partial", dim3((unsigned)(b * d->am_chunks)), dim3(256), a)))
       return rc;
-    ArgmaxFinalArgs f{d->am_val, d->am_idx, d->next, d->d_lens, rec ? rec->out : nullptr,
+    ArgmaxFinalArgs f{d->am_val, d->am_idx, d->next, range && !range->advance ? nullptr : d->d_lens,
+                      rec ? rec->out : nullptr,
                       rec ? rec->step : nullptr, (int)b, d->am_chunks, (int)s, rec ? rec->ncols : 0};
     unsigned threads = 64u * (unsigned)std::min<int64_t>(b, 16);
     if (embed_next) {
@@ -734,6 +765,48 @@ int rxw8_decoder_forward(rxw8_decoder *d, rxw8_buffer *ids, int64_t b, int64_t s
     RXW8_HIP(hipMemcpyAsync(logits->ptr, d->logits, (size_t)b * d->V * 4, hipMemcpyDeviceToDevice,
                             d->rt->stream));
   for (int64_t i = 0; i < b; ++i) d->h_lens[(size_t)i] += (int32_t)s;
+  return RXW8_OK;
+}
+
+int rxw8_decoder_forward_layers(rxw8_decoder *d, rxw8_buffer *hidden_in, int64_t b, int64_t s,
+                                int64_t first, int64_t last, rxw8_buffer *hidden_out,
+                                rxw8_buffer *logits, int commit) {
+  if (!d || !hidden_in || !hidden_out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if (first < 0 || last <= first || last > d->L)
+    return fail(RXW8_INVALID_ARGUMENT, "layer range [%lld, %lld) outside [0, %lld]", (long long)first,
+                (long long)last, (long long)d->L);
+  if (b < 1 || s < 1 || b > d->Bmax || s > d->Lmax)
+    return fail(RXW8_INVALID_ARGUMENT, "b and s must lie in [1, max_batch] and [1, max_seq]");
+  for (rxw8_buffer *hb : {hidden_in, hidden_out})
+    if (hb->dtype != RXW8_F32 || hb->numel() != b * s * d->H || hb->rt != d->rt)
+      return fail(RXW8_INVALID_ARGUMENT, "hidden_in / hidden_out must be F32 [b, s, hidden] of this runtime");
+  if (logits && (last != d->L || logits->dtype != RXW8_F32 || logits->numel() != b * d->V))
+    return fail(RXW8_INVALID_ARGUMENT, "logits need last == layers and F32 [b, vocab]");
+  std::lock_guard<std::recursive_mutex> g(d->rt->mu);
+  int rc = check_ready(d, b, s);
+  if (rc) return rc;
+  if ((rc = ensure_activations(d, b * s))) return rc;
+  LayerRange range;
+  range.h_in = (const float *)hidden_in->ptr;
+  range.first = (int)first;
+  range.last = (int)last;
+  range.tail = logits != nullptr;
+  range.advance = logits && commit;
+  if ((rc = enqueue_forward(d, nullptr, b, s, nullptr, false, false, &range))) return rc;
+  Runtime *rt = d->rt;
+  RXW8_HIP(hipMemcpyAsync(hidden_out->ptr, d->h, (size_t)(b * s * d->H) * 4,
+                          hipMemcpyDeviceToDevice, rt->stream));
+  if (logits)
+    RXW8_HIP(hipMemcpyAsync(logits->ptr, d->logits, (size_t)b * d->V * 4, hipMemcpyDeviceToDevice,
+                            rt->stream));
+  if (commit) {
+    for (int64_t i = 0; i < b; ++i) d->h_lens[(size_t)i] += (int32_t)s;
+    if (!logits) {  // no argmax pass to advance the device lengths
+      RXW8_HIP(hipMemcpyAsync(d->d_lens, d->h_lens.data(), (size_t)b * 4, hipMemcpyHostToDevice,
+                              rt->stream));
+      RXW8_HIP(hipStreamSynchronize(rt->stream));
+    }
+  }
   return RXW8_OK;
 }
 

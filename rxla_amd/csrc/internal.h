@@ -80,6 +80,7 @@ struct Buffer {
   bool owned = true;
   std::atomic<int> refs{1};
 
+  // (buffer_extent admitted the shape: the product fits int64)
   int64_t numel() const {
     int64_t n = 1;
     for (int i = 0; i < rank; ++i) n *= dims[i];
@@ -152,13 +153,18 @@ int gqa_decode_into(Runtime *rt, Buffer *q, Buffer *k_cache, Buffer *v_cache, Bu
                     Buffer *mask, float scale, Buffer *out, const AttnWorkspace *ws);
 
 // Takes the device address of the no-allocation scratch array on `device`
-// (current) and clears its counters; once per device (noalloc.hip).
-int noalloc_device_setup(int device);
+// (current) and clears its counters on `stream`; once per device (noalloc.hip).
+int noalloc_device_setup(int device, hipStream_t stream);
 
 // Device-side allocation through the runtime's cache.
 int rt_alloc(Runtime *rt, size_t bytes, void **out);
 void rt_free(Runtime *rt, void *ptr, size_t bytes);
 int ensure_workspace(Runtime *rt, Workspace &ws, size_t bytes, bool zero);
+// Validates a buffer shape (known dtype, rank <= RXW8_MAX_RANK, dims >= 0,
+// element count and byte size within int64 by checked products) and returns
+// its byte size; INVALID_ARGUMENT otherwise. Every buffer is created through
+// it, so Buffer::numel cannot overflow.
+int buffer_extent(int dtype, const int64_t *dims, int rank, size_t *bytes);
 // New owned buffer (uninitialised contents unless zero).
 int new_buffer(Runtime *rt, int dtype, const int64_t *dims, int rank, bool zero,
                Buffer **out);

@@ -39,7 +39,10 @@ struct AttnArgs {
   const int32_t *row_seq;  // [R] cache slot of row r, or null (slot r)
   const float *mask;       // additive, mask[r * mask_sb + h * mask_sh + j], or null
   void *out;               // [R, Hq, D]
-  float *ws;               // partials [R, Hkv, max_chunks, G, 2 + D]
+  // split partials, (G, 2 + D) floats per slot: slot bh * max_chunks + split
+  // for uniform splits; slot kvh * units + u (one per workgroup) for
+  // length-proportional ones
+  float *ws;
   int64_t mask_sb, mask_sh;
   int R, Hq, Hkv, Lmax, max_chunks;
   float scale;
@@ -137,10 +140,11 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4 &r, float *x) {
 // units [u_b, u_{b+1}) with u_0 = 0 and u_{b+1} = clamp(round(C_{b+1} * units
 // / T), u_b + 1, units - (R - 1 - b)) (f32), C_b the lengths of rows < b and T their
 // total, so every workgroup walks about T / units keys. Returns row b's split
-// count; for unit u (>= 0), also the row and the split within it. Uniform per
-// workgroup; R < units (host-checked).
+// count; for unit u (>= 0), also the row and the split within it, and the
+// row's first unit u_r (unit0). Uniform per workgroup; R < units
+// (host-checked).
 __device__ __forceinline__ int row_units(const AttnArgs &a, int b, int u, int *row, int *split,
-                                         int *row_len = nullptr) {
+                                         int *row_len = nullptr, int *unit0 = nullptr) {
   int T = 0;  // R * Lmax < 2^31 (host-checked)
   for (int r = 0; r < a.R; ++r) T += min(max(a.lens[r], 1), a.Lmax);
   const float per_key = (float)a.units / (float)T;  // same value in every workgroup
@@ -155,6 +159,7 @@ __device__ __forceinline__ int row_units(const AttnArgs &a, int b, int u, int *r
       if (row) *row = r;
       if (split) *split = u - ub;
       if (row_len) *row_len = len;
+      if (unit0) *unit0 = ub;
       return un - ub;
     }
     ub = un;
@@ -180,18 +185,27 @@ __device__ __forceinline__ float load_part(const float *p) {
 }
 
 // Merge the S split partials of (row, kv head) bh in split order and write
-// the output rows of its G heads; any workgroup size. Thread (head, dim):
+// the output rows of its G heads; any workgroup size. slot0: the partial slot
+// of the row's split 0 (-1: found here). Thread (head, dim):
 // M = max_c m_c, then L = sum_c f_c l_c and O = sum_c f_c o_c in split order
 // with f_c = exp(m_c - M) (0 for empty splits). Up to 32 splits, all of an
 // output's partials are loaded first (one round trip), with the same
 // arithmetic order as the general loop (empty slots add exact zeros).
 template <int G, bool COH>
-__device__ void combine_pair(const AttnArgs &a, int bh, int nchunks = 0) {
+__device__ void combine_pair(const AttnArgs &a, int bh, int nchunks = 0, int slot0 = -1) {
   const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
   // every split of the row wrote a partial (empty: max -inf)
-  if (nchunks == 0) nchunks = a.units > 0 ? row_units(a, b, -1, nullptr, nullptr) : a.max_chunks;
+  if (a.units > 0) {
+    int u0 = 0;
+    const int n = row_units(a, b, -1, nullptr, nullptr, nullptr, &u0);
+    if (nchunks == 0) nchunks = n;
+    if (slot0 < 0) slot0 = kvh * a.units + u0;
+  } else {
+    if (nchunks == 0) nchunks = a.max_chunks;
+    if (slot0 < 0) slot0 = bh * a.max_chunks;
+  }
   if (nchunks == 1) return;  // a single split wrote the output itself
-  const float *base = a.ws + ((int64_t)bh * a.max_chunks) * G * (2 + D);
+  const float *base = a.ws + (int64_t)slot0 * G * (2 + D);
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx - h * D;
     float M = kNegInf, L = 0.f, O = 0.f;
@@ -252,7 +266,7 @@ __device__ void combine_pair(const AttnArgs &a, int bh, int nchunks = 0) {
 // device-scope fences: on this part a release fence writes back the whole L2
 // and costs ~100 us per launch. Uniform per workgroup.
 template <int G>
-__device__ void arrive_and_merge(const AttnArgs &a, int bh, int nsplit) {
+__device__ void arrive_and_merge(const AttnArgs &a, int bh, int nsplit, int slot0) {
   __shared__ int is_last;
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are done
   __syncthreads();
@@ -261,7 +275,7 @@ __device__ void arrive_and_merge(const AttnArgs &a, int bh, int nsplit) {
               nsplit - 1;
   __syncthreads();
   if (!is_last) return;
-  combine_pair<G, true>(a, bh, nsplit);
+  combine_pair<G, true>(a, bh, nsplit, slot0);
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -285,9 +299,12 @@ __device__ void attn_pass(const AttnArgs &a) {
   const int S = a.max_chunks;  // partial slots per (row, kv head)
   int split, b, kvh, nsplit;
   int len;
+  int slot0;  // partial slot of the row's split 0 (this workgroup's: slot0 + split)
   if (a.units > 0) {  // length-proportional splits
     kvh = blockIdx.x / a.units;
-    nsplit = row_units(a, 0, blockIdx.x - kvh * a.units, &b, &split, &len);
+    const int u = blockIdx.x - kvh * a.units;
+    nsplit = row_units(a, 0, u, &b, &split, &len);
+    slot0 = kvh * a.units + u - split;
   } else {
     split = blockIdx.x % S;
     b = (blockIdx.x / S) / a.Hkv;
@@ -295,16 +312,17 @@ __device__ void attn_pass(const AttnArgs &a) {
     nsplit = S;
     len = a.lens[b];
     len = len < 1 ? 1 : (len > a.Lmax ? a.Lmax : len);
+    slot0 = (b * a.Hkv + kvh) * S;
   }
   const int bh = b * a.Hkv + kvh;  // row * Hkv + kvh
   const int per = ((len + nsplit - 1) / nsplit + KW - 1) / KW * KW;
   const int start = split * per;
   int end = min(len, start + per);
-  float *part = a.ws + (((int64_t)bh * S + split) * G) * (2 + D);
+  float *part = a.ws + ((int64_t)(slot0 + split) * G) * (2 + D);
   if (start >= end) {  // empty split (uniform per workgroup)
     for (int idx = threadIdx.x; idx < G * (2 + D); idx += blockDim.x)
       store_part(part + idx, (idx % (2 + D)) == 0 ? kNegInf : 0.f, a.counters != nullptr);
-    if (a.counters) arrive_and_merge<G>(a, bh, nsplit);
+    if (a.counters) arrive_and_merge<G>(a, bh, nsplit, slot0);
     return;
   }
   const int seq = a.row_seq ? a.row_seq[b] : b;
@@ -606,7 +624,7 @@ __device__ void attn_pass(const AttnArgs &a) {
       store_part(ph + 2 + d, O, coh);
     }
   }
-  if (nsplit > 1 && a.counters) arrive_and_merge<G>(a, bh, nsplit);
+  if (nsplit > 1 && a.counters) arrive_and_merge<G>(a, bh, nsplit, slot0);
 }
 
 }  // namespace

@@ -54,6 +54,20 @@ __device__ __forceinline__ uint2 u8x4_to_signed_bf16x4(uint32_t w) {
   return uint2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
 }
 
+// Four u8 codes of one dword -> two dwords of bf16 pairs of the dequantised
+// weights bf16((u - 128) * s), round to nearest even: the reference's
+// dequantise-then-cast order (crates/rxla-nn/src/layers.rs:277-296). The f32
+// product (u - 128) * s is formed as fma(u, s, ms) with ms = -128 s: -128 s is
+// exact (a power-of-two multiple), so the fma's single rounding of
+// u s - 128 s gives the correctly rounded product.
+__device__ __forceinline__ uint2 u8x4_to_dq_bf16x4(uint32_t w, float s, float ms) {
+  const float f0 = fmaf((float)(w & 0xffu), s, ms);
+  const float f1 = fmaf((float)((w >> 8) & 0xffu), s, ms);
+  const float f2 = fmaf((float)((w >> 16) & 0xffu), s, ms);
+  const float f3 = fmaf((float)(w >> 24), s, ms);
+  return uint2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
+}
+
 // The values of lanes l and l ^ 16 (resp. l ^ 32), in some order, through
 // v_permlane16_swap / v_permlane32_swap with both operands v: a VALU exchange
 // instead of an LDS round trip (ds_bpermute). Combined with a commutative

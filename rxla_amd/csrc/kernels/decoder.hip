@@ -122,6 +122,47 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_dec_embed(EmbedArgs a) {
   }
 }
 
+// ---- residual rows from the caller: h[t] = h_in[t] -----------------------------
+// The input of a layer run by the teacher-forcing entry point
+// (rxw8_decoder_forward_layers): writes what rxw8_dec_embed writes for a row
+// -- the positions, the f32 row, its sum of squares and the first layer's
+// weighted bf16 row -- from an f32 row instead of an embedding row. One
+// workgroup of 256 threads per row, thread t taking elements t, t + 256, ...
+struct LoadRowsArgs {
+  const float *h_in;      // [T, H]
+  float *h;               // [T, H]
+  float *ss;              // optional [T]
+  int64_t H;
+  const int32_t *lens;    // [B]
+  int32_t *pos, *row_seq, *row_len;  // [T]
+  int s;
+  const float *xw_norm;   // optional [H]: also write xw [T, H] = bf16(row * xw_norm)
+  uint16_t *xw;
+};
+
+extern "C" __global__ void __launch_bounds__(256) rxw8_dec_load_rows(LoadRowsArgs a) {
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x;
+  if (threadIdx.x == 0) {
+    const int bi = (int)(t / a.s);
+    const int p = a.lens[bi] + (int)(t - (int64_t)bi * a.s);
+    a.pos[t] = p;
+    a.row_seq[t] = bi;
+    a.row_len[t] = p + 1;
+  }
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < a.H; i += 256) {
+    const float v = a.h_in[t * a.H + i];
+    a.h[t * a.H + i] = v;
+    if (a.xw) a.xw[t * a.H + i] = f32_to_bf16_bits(v * a.xw_norm[i]);
+    ss += v * v;
+  }
+  if (a.ss) {
+    ss = block_sum_256(ss, red);
+    if (threadIdx.x == 0) a.ss[t] = ss;
+  }
+}
+
 // Row permutation of the fused gate|up projection used by the SwiGLU GEMV
 // epilogue: output row R takes input row (R % 16 < 8 ? 8 (R / 16) + R % 16
 // : half + 8 (R / 16) + R % 16 - 8), i.e. 16-row tiles of 8 gate rows then the

@@ -1,5 +1,9 @@
 // K1: W8A16 decode GEMV / skinny GEMM on gfx950 MFMA.
 //
+// The default (gemv_rc, RC) form is the reference's product
+// (crates/rxla-nn/src/layers.rs:277-296):
+//   y[m, n] = bf16( sum_k bf16(x[m, k]) * bf16((u8[n, k] - 128) * s[n, k / G]) )
+// The exact-code form (gemv, RXW8_GEMV_REF_CAST=0) moves the scale after the sum:
 //   y[m, n] = bf16( sum_g s[n, g] * sum_{k in g} bf16(x[m, k]) * (u8[n, k] - 128) )
 //
 // Layout: u8 weights [N, K] row-major (RXLA's U8 = int8 + 128 storage,
@@ -589,8 +593,14 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 // FC: compute dtype F32 (the _fc kernels): f32 rows staged as bf16 hi / lo
 // parts (stage_x_fc; rows b and LO + b, LO = 8 MB), the codes as the exact
 // bf16 values u - 128 (no all-ones correction), f32 results (finish_fc).
+// RC: the reference's cast point (the _rc kernels, layers.rs:277-296): each
+// A-fragment element is the dequantised weight rounded to bf16,
+// bf16((u - 128) * s[n, k / G]), so the product is
+// sum_k bf16(x) * bf16(dequant(W)) in f32, with no all-ones correction and no
+// scale after the sum. Lane l's row n takes its scale from global memory once
+// (per-channel) or from the staged scale tile per 64-k chunk (grouped).
 template <int MB, int RW, int U, bool PK, int NW = 4, bool XG = false, bool RN = false,
-          bool FC = false>
+          bool FC = false, bool RC = false>
 __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   constexpr int LO = 8 * MB;  // FC: staged row of the lo part of row 0
   constexpr int KW = NW / RW;
@@ -718,12 +728,21 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
     }
   const u32x4 ones_bits = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
   const bf16x8 onesf = as_bf16x8(ones_bits);
+  // RC with per-channel scales: lane l's row scale (rows of inactive groups
+  // repeat the tile's first rows, as their weights do)
+  float s_lane = 0.f;
+  if (RC && per_channel) s_lane = a.scale[(int64_t)wrow16 * 16 + r];
 
   // Process one 64-k chunk c (of this wave's slice) held in register slice w
   // (XG: with its activation fragments xg).
   auto process = [&](const u32x4 w, const u32x4(&xg)[MB][2], const int c) {
     uint2 p0, p1, p2, p3;
-    if (FC) {
+    if (RC) {
+      const float s = per_channel ? s_lane : ss[(rg * 16 + r) * gps + (kbase + c * 64) / a.G];
+      const float ms = -128.f * s;
+      p0 = u8x4_to_dq_bf16x4(w[0], s, ms), p1 = u8x4_to_dq_bf16x4(w[1], s, ms);
+      p2 = u8x4_to_dq_bf16x4(w[2], s, ms), p3 = u8x4_to_dq_bf16x4(w[3], s, ms);
+    } else if (FC) {
       p0 = u8x4_to_signed_bf16x4(w[0]), p1 = u8x4_to_signed_bf16x4(w[1]);
       p2 = u8x4_to_signed_bf16x4(w[2]), p3 = u8x4_to_signed_bf16x4(w[3]);
     } else {
@@ -737,12 +756,12 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
       const bf16x8 x0 = as_bf16x8(XG ? xg[mb][0] : xp[0]), x1 = as_bf16x8(XG ? xg[mb][1] : xp[1]);
       acc[mb] = mfma16x16x32(as_bf16x8(a0), x0, acc[mb]);
       acc[mb] = mfma16x16x32(as_bf16x8(a1), x1, acc[mb]);
-      if (!FC) {
+      if (!FC && !RC) {
         ones[mb] = mfma16x16x32(onesf, x0, ones[mb]);
         ones[mb] = mfma16x16x32(onesf, x1, ones[mb]);
       }
     }
-    if (!per_channel && ((c + 1) % chunks_per_group) == 0) {
+    if (!RC && !per_channel && ((c + 1) % chunks_per_group) == 0) {
       // fold one scale group: total += s[n, g] * (acc - 128 * ones) (FC: acc)
       const int gl = (kbase + c * 64) / a.G;
       const float *srow = ss + (rg * 16 + 4 * j) * gps + gl;
@@ -765,9 +784,9 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) process(bufB[u], xgB[XG ? u : 0], c0 + U + u);
   }
-  if (per_channel)
+  if (per_channel || RC)
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) total[mb] = FC ? acc[mb] : acc[mb] - 128.f * ones[mb];
+    for (int mb = 0; mb < MB; ++mb) total[mb] = (FC || RC) ? acc[mb] : acc[mb] - 128.f * ones[mb];
   if (RN) {
     row_norm_store(a, wave, rnv, xs);
     for (int b = wave + NW; b < a.M; b += NW) {  // rows beyond the wave count
@@ -775,7 +794,7 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
       row_norm_store(a, b, rnv, xs);
     }
   }
-  finish_tile<MB, RW, NW, RN, FC>(a, (float *)xs, rows0, sp, total, per_channel);
+  finish_tile<MB, RW, NW, RN, FC>(a, (float *)xs, rows0, sp, total, per_channel && !RC);
 }
 
 // Dense bf16 weights (lm_head): one 16-byte slice = one MFMA A-fragment.
@@ -867,57 +886,43 @@ __device__ __forceinline__ void gemv_bf16(const GemvArgs &a) {
 
 }  // namespace
 
-// Second launch of a split GEMV: y[b, n] = s[n] * sum_sp ws[sp, b, n] (split
-// order), rounded to bf16. One thread per 4 consecutive outputs.
-extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(SplitkReduceArgs a) {
-  const int64_t quads = (int64_t)a.M * a.N / 4;
-  for (int64_t qd = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; qd < quads;
-       qd += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t e = qd * 4;
-    const int b = (int)(e / a.N), n = (int)(e - (int64_t)b * a.N);
-    // residual and scale loads go out with the first batch of partials
-    const float4 h0 = a.y_mode == 1 ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
-                                    : float4{0.f, 0.f, 0.f, 0.f};
-    const float4 s4 = a.scale ? *(const float4 *)(a.scale + n) : float4{1.f, 1.f, 1.f, 1.f};
-    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < a.ksplit; s0 += 4) {  // 4 partial loads in flight, summed in split order
-      float4 p[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        if (s0 + t < a.ksplit) p[t] = *(const float4 *)(a.ws + ((int64_t)(s0 + t) * a.M + b) * a.N + n);
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        if (s0 + t < a.ksplit) sum += f32x4{p[t].x, p[t].y, p[t].z, p[t].w};
-    }
-    if (a.scale) sum *= f32x4{s4.x, s4.y, s4.z, s4.w};
-    store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, sum, h0);
-  }
-}
+// Kernel instances. The file is compiled twice: as the gemv code object
+// (names rxw8_gemv_*, the exact-code products) and, with RXW8_GEMV_RC defined
+// (kernels/w8a16_gemv_rc.hip), as the gemv_rc code object: the same u8 tilings
+// with the reference's cast point (template flag RC, names rxw8_gemv_rc_*).
+// Building them as two objects keeps each compile at the size of one.
+#ifdef RXW8_GEMV_RC
+#define RXW8_RC true
+#define RXW8_KN(rest) rxw8_gemv_rc_##rest
+#else
+#define RXW8_RC false
+#define RXW8_KN(rest) rxw8_gemv_##rest
+#endif
 
-#define RXW8_GEMV(KIND, MB, RW, U)                                              \
+#define RXW8_GEMV_W8(MB, RW, U)                                                 \
   extern "C" __global__ void __launch_bounds__(256)                             \
-      rxw8_gemv_##KIND##_mb##MB##_rw##RW##_u##U(GemvArgs a) {                   \
-    gemv_##KIND<MB, RW, U, false>(a);                                           \
+      RXW8_KN(w8_mb##MB##_rw##RW##_u##U)(GemvArgs a) {                          \
+    gemv_w8<MB, RW, U, false, 4, false, false, false, RXW8_RC>(a);              \
   }                                                                             \
   extern "C" __global__ void __launch_bounds__(256)                             \
-      rxw8_gemv_##KIND##_pk_mb##MB##_rw##RW##_u##U(GemvArgs a) {                \
-    gemv_##KIND<MB, RW, U, true>(a);                                            \
+      RXW8_KN(w8_pk_mb##MB##_rw##RW##_u##U)(GemvArgs a) {                       \
+    gemv_w8<MB, RW, U, true, 4, false, false, false, RXW8_RC>(a);               \
   }
-#define RXW8_GEMV_U(KIND, MB, RW) \
-  RXW8_GEMV(KIND, MB, RW, 8)      \
-  RXW8_GEMV(KIND, MB, RW, 4)      \
-  RXW8_GEMV(KIND, MB, RW, 2)      \
-  RXW8_GEMV(KIND, MB, RW, 1)
+#define RXW8_GEMV_W8_U(MB, RW) \
+  RXW8_GEMV_W8(MB, RW, 8)      \
+  RXW8_GEMV_W8(MB, RW, 4)      \
+  RXW8_GEMV_W8(MB, RW, 2)      \
+  RXW8_GEMV_W8(MB, RW, 1)
 // Wide variants: 8, 12, 14 or 16 waves per workgroup = RW row groups x NW/RW k
 // slices (12 waves: 3 row groups of 4, e.g. N = 12288 in 256 workgroups).
 #define RXW8_GEMV_WIDE(MB, RW, U, NW)                                           \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
-      rxw8_gemv_w8_mb##MB##_rw##RW##_u##U##_w##NW(GemvArgs a) {                 \
-    gemv_w8<MB, RW, U, false, NW>(a);                                           \
+      RXW8_KN(w8_mb##MB##_rw##RW##_u##U##_w##NW)(GemvArgs a) {                  \
+    gemv_w8<MB, RW, U, false, NW, false, false, false, RXW8_RC>(a);             \
   }                                                                             \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
-      rxw8_gemv_w8_pk_mb##MB##_rw##RW##_u##U##_w##NW(GemvArgs a) {              \
-    gemv_w8<MB, RW, U, true, NW>(a);                                            \
+      RXW8_KN(w8_pk_mb##MB##_rw##RW##_u##U##_w##NW)(GemvArgs a) {               \
+    gemv_w8<MB, RW, U, true, NW, false, false, false, RXW8_RC>(a);              \
   }
 #define RXW8_GEMV_WIDE_U(MB, RW, NW) \
   RXW8_GEMV_WIDE(MB, RW, 4, NW)      \
@@ -931,12 +936,12 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(Splitk
 // XG: activations from global memory (bf16 rows, per-channel scales, M <= 16)
 #define RXW8_GEMV_XG(RW, U, NW)                                                 \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
-      rxw8_gemv_w8_mb1_rw##RW##_u##U##_w##NW##_xg(GemvArgs a) {                 \
-    gemv_w8<1, RW, U, false, NW, true>(a);                                      \
+      RXW8_KN(w8_mb1_rw##RW##_u##U##_w##NW##_xg)(GemvArgs a) {                  \
+    gemv_w8<1, RW, U, false, NW, true, false, false, RXW8_RC>(a);               \
   }                                                                             \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
-      rxw8_gemv_w8_pk_mb1_rw##RW##_u##U##_w##NW##_xg(GemvArgs a) {              \
-    gemv_w8<1, RW, U, true, NW, true>(a);                                       \
+      RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_w##NW##_xg)(GemvArgs a) {               \
+    gemv_w8<1, RW, U, true, NW, true, false, false, RXW8_RC>(a);                \
   }
 #define RXW8_GEMV_XG_U(RW, NW) \
   RXW8_GEMV_XG(RW, 4, NW)      \
@@ -971,13 +976,13 @@ RXW8_GEMV_WIDE_U(2, 1, 14)
 // plain kernel's name + "_rn".
 #define RXW8_GEMV_XG_RN(RW, U, NW)                                              \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
-      rxw8_gemv_w8_pk_mb1_rw##RW##_u##U##_w##NW##_xg_rn(GemvArgs a) {           \
-    gemv_w8<1, RW, U, true, NW, true, true>(a);                                 \
+      RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_w##NW##_xg_rn)(GemvArgs a) {            \
+    gemv_w8<1, RW, U, true, NW, true, true, false, RXW8_RC>(a);                 \
   }
 #define RXW8_GEMV_WIDE_RN(RW, U, NW)                                            \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
-      rxw8_gemv_w8_pk_mb1_rw##RW##_u##U##_w##NW##_rn(GemvArgs a) {              \
-    gemv_w8<1, RW, U, true, NW, false, true>(a);                                \
+      RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_w##NW##_rn)(GemvArgs a) {               \
+    gemv_w8<1, RW, U, true, NW, false, true, false, RXW8_RC>(a);                \
   }                                                                             \
   RXW8_GEMV_XG_RN(RW, U, NW)
 #define RXW8_GEMV_WIDE_RN_U(RW, NW) \
@@ -997,8 +1002,8 @@ RXW8_GEMV_WIDE_RN_U(1, 14)
 // 4-wave plans: the staged kernels (U up to 8) and the XG ones (U up to 4)
 #define RXW8_GEMV_RN4(RW, U)                                                    \
   extern "C" __global__ void __launch_bounds__(256)                             \
-      rxw8_gemv_w8_pk_mb1_rw##RW##_u##U##_rn(GemvArgs a) {                      \
-    gemv_w8<1, RW, U, true, 4, false, true>(a);                                 \
+      RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_rn)(GemvArgs a) {                       \
+    gemv_w8<1, RW, U, true, 4, false, true, false, RXW8_RC>(a);                 \
   }
 #define RXW8_GEMV_RN4_U(RW) \
   RXW8_GEMV_RN4(RW, 8)      \
@@ -1011,6 +1016,32 @@ RXW8_GEMV_WIDE_RN_U(1, 14)
   RXW8_GEMV_XG_RN(RW, 1, 4)
 RXW8_GEMV_RN4_U(1)
 RXW8_GEMV_RN4_U(4)
+
+RXW8_GEMV_W8_U(1, 1)
+RXW8_GEMV_W8_U(1, 4)
+RXW8_GEMV_W8_U(2, 1)
+RXW8_GEMV_W8_U(2, 4)
+
+#ifndef RXW8_GEMV_RC
+// Dense bf16 weights and the F32-compute kernels exist once (no RC form).
+#define RXW8_GEMV_BF16(MB, RW, U)                                               \
+  extern "C" __global__ void __launch_bounds__(256)                             \
+      rxw8_gemv_bf16_mb##MB##_rw##RW##_u##U(GemvArgs a) {                       \
+    gemv_bf16<MB, RW, U, false>(a);                                             \
+  }                                                                             \
+  extern "C" __global__ void __launch_bounds__(256)                             \
+      rxw8_gemv_bf16_pk_mb##MB##_rw##RW##_u##U(GemvArgs a) {                    \
+    gemv_bf16<MB, RW, U, true>(a);                                              \
+  }
+#define RXW8_GEMV_BF16_U(MB, RW) \
+  RXW8_GEMV_BF16(MB, RW, 8)      \
+  RXW8_GEMV_BF16(MB, RW, 4)      \
+  RXW8_GEMV_BF16(MB, RW, 2)      \
+  RXW8_GEMV_BF16(MB, RW, 1)
+RXW8_GEMV_BF16_U(1, 1)
+RXW8_GEMV_BF16_U(1, 4)
+RXW8_GEMV_BF16_U(2, 1)
+RXW8_GEMV_BF16_U(2, 4)
 #define RXW8_GEMV_BF16_RN(RW, U)                                                \
   extern "C" __global__ void __launch_bounds__(256)                             \
       rxw8_gemv_bf16_pk_mb1_rw##RW##_u##U##_rn(GemvArgs a) {                    \
@@ -1063,14 +1094,33 @@ RXW8_GEMV_FC_MB(1)
 RXW8_GEMV_FC_MB(2)
 RXW8_GEMV_FC_WIDE_U(1, 6, 12)
 
-#define RXW8_GEMV_ALL(KIND) \
-  RXW8_GEMV_U(KIND, 1, 1)   \
-  RXW8_GEMV_U(KIND, 1, 4)   \
-  RXW8_GEMV_U(KIND, 2, 1)   \
-  RXW8_GEMV_U(KIND, 2, 4)
+// Second launch of a split GEMV: y[b, n] = s[n] * sum_sp ws[sp, b, n] (split
+// order), rounded to bf16. One thread per 4 consecutive outputs.
+extern "C" __global__ void __launch_bounds__(256) rxw8_gemv_splitk_reduce(SplitkReduceArgs a) {
+  const int64_t quads = (int64_t)a.M * a.N / 4;
+  for (int64_t qd = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; qd < quads;
+       qd += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e = qd * 4;
+    const int b = (int)(e / a.N), n = (int)(e - (int64_t)b * a.N);
+    // residual and scale loads go out with the first batch of partials
+    const float4 h0 = a.y_mode == 1 ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
+                                    : float4{0.f, 0.f, 0.f, 0.f};
+    const float4 s4 = a.scale ? *(const float4 *)(a.scale + n) : float4{1.f, 1.f, 1.f, 1.f};
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < a.ksplit; s0 += 4) {  // 4 partial loads in flight, summed in split order
+      float4 p[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (s0 + t < a.ksplit) p[t] = *(const float4 *)(a.ws + ((int64_t)(s0 + t) * a.M + b) * a.N + n);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (s0 + t < a.ksplit) sum += f32x4{p[t].x, p[t].y, p[t].z, p[t].w};
+    }
+    if (a.scale) sum *= f32x4{s4.x, s4.y, s4.z, s4.w};
+    store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, sum, h0);
+  }
+}
 
-RXW8_GEMV_ALL(w8)
-RXW8_GEMV_ALL(bf16)
 
 // Tiled weight layouts for the packed GEMV kernels. One thread moves one
 // 16-byte lane slice: dst block (t, c), lane l <- src row 16t + l%16.
@@ -1100,3 +1150,4 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_pack_tiles(PackArgs a) {
     *(u32x4 *)((char *)a.dst + i * 16) = v;
   }
 }
+#endif  // !RXW8_GEMV_RC

@@ -42,8 +42,10 @@ void *g_ptr[kMaxDevices] = {nullptr};  // device address of `scratch`, per devic
 namespace rxw8 {
 
 // Once per device, with that device current: the device address of `scratch`
-// and a cleared counter region.
-int noalloc_device_setup(int device) {
+// and a cleared counter region (cleared on `stream`, the creating runtime's
+// own new stream, and waited for there: no device-wide synchronisation, which
+// would stall other streams and break a capture in progress elsewhere).
+int noalloc_device_setup(int device, hipStream_t stream) {
   if (device < 0 || device >= kMaxDevices)
     return fail(RXW8_INVALID_ARGUMENT, "device %d outside [0, %d) for the no-allocation scratch",
                 device, kMaxDevices);
@@ -52,10 +54,10 @@ int noalloc_device_setup(int device) {
   void *ptr = nullptr;
   hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !ptr) return hip_fail(e, "hipGetSymbolAddress(scratch)");
-  e = hipMemset(ptr, 0, kCounterBytes);
-  if (e != hipSuccess) return hip_fail(e, "hipMemset(scratch counters)");
-  e = hipDeviceSynchronize();
-  if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+  e = hipMemsetAsync(ptr, 0, kCounterBytes, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync(scratch counters)");
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   g_ptr[device] = ptr;
   return RXW8_OK;
 }

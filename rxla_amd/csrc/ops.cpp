@@ -401,6 +401,11 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
   GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16, pro->prefer_ks1,
                          pro->mode != 1);
   if (p.ks == 0 || N % 4) return RXW8_UNIMPLEMENTED;
+  // u8 weights enter the product at the reference's cast point, each weight
+  // bf16((u - 128) * s) (the gemv_rc kernels); RXW8_GEMV_REF_CAST=0 selects
+  // the exact codes u - 128 with the scale applied after the f32 sum instead
+  const char *rc_env = std::getenv("RXW8_GEMV_REF_CAST");
+  const bool ref_cast = !w_bf16 && !(rc_env && *rc_env == '0');
   // the fused epilogues need the whole reduction in one launch and whole
   // 16-channel groups; one chunk of rows keeps the partial layout [g][M]
   if ((pro->swiglu || pro->ss_out) && (p.ks != 1 || N % 16 || M > mchunk)) return RXW8_UNIMPLEMENTED;
@@ -458,8 +463,9 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
       std::snprintf(wide, sizeof wide, "_w%d_xg", p.nw);
     else if (p.nw != 4)
       std::snprintf(wide, sizeof wide, "_w%d", p.nw);
-    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s_mb%d_rw%d_u%d%s%s", w_bf16 ? "bf16" : "w8",
-                  packed ? "_pk" : "", mb, p.rw, u, wide, pro->row_norm ? "_rn" : "");
+    std::snprintf(kname, sizeof kname, "rxw8_gemv_%s%s%s_mb%d_rw%d_u%d%s%s", ref_cast ? "rc_" : "",
+                  w_bf16 ? "bf16" : "w8", packed ? "_pk" : "", mb, p.rw, u, wide,
+                  pro->row_norm ? "_rn" : "");
     size_t lds = xg ? (size_t)(p.nw / p.rw - 1) * p.rw * mb * 256 * 4 + 16
                     : gemv_lds(mm, K / p.ks, K, G, p.rw, mb, w_bf16, p.nw);
     a.row_norm = pro->row_norm ? 1 : 0;
@@ -484,7 +490,8 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     if (p.ks > 1) {
       SplitkReduceArgs r;
       r.ws = (const float *)rt->partials.ptr;
-      r.scale = (!w_bf16 && G == K) ? scale : nullptr;
+      // (the reference-cast partials already hold the dequantised products)
+      r.scale = (!w_bf16 && G == K && !ref_cast) ? scale : nullptr;
       r.y = a.y;
       r.M = (int)mm;
       r.N = (int)N;
@@ -896,7 +903,11 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(64, (Lmax + 63) / 64));
     int64_t S = 1;
     double best = 0.0;
-    for (int64_t s = 1; s <= smax; ++s) {
+    // At most 4 x cus split workgroups (partial slots): beyond that the
+    // estimate is flat (rounds x keys per split stays ~pairs x Lmax / cus),
+    // and the bound keeps every plan's partials within cus x 4 x G (2 + D)
+    // floats (4.1 MiB at G = 8 on 256 CUs).
+    for (int64_t s = 1; s <= smax && (s == 1 || pairs * s <= 4 * (int64_t)rt->cus); ++s) {
       const double rounds = (double)((pairs * s + rt->cus - 1) / rt->cus);
       const double est = rounds * (125.0 + (double)Lmax / (double)s);
       if (s == 1 || est < best) {
@@ -917,7 +928,7 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     if (S > 1 && !forced && !env_int("RXW8_ATTN_UNIFORM", 0) && rt->cus / Hkv > R &&
         Lmax >= 2048 && R * Lmax < (int64_t)1 << 30)
       units = std::min<int64_t>(rt->cus / Hkv, R + 63);
-    if (units > 0) S = units - R + 1;  // partial slots: the most splits a row can get
+    if (units > 0) S = units - R + 1;  // the most splits a row can get (> 1: a split plan)
     const int64_t max_chunks = S;
     // Splits are merged by the last workgroup of each (row, kv head) to finish
     // (arrival counters, zeroed once at allocation and re-armed by the kernel);
@@ -926,7 +937,10 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     float *ws_partials = nullptr;
     int *ws_counters = nullptr;
     if (max_chunks > 1) {
-      const size_t need_p = (size_t)R * Hkv * max_chunks * G * (2 + D) * sizeof(float);
+      // one partial slot per workgroup: Hkv x units (length-proportional) or
+      // R x Hkv x S (uniform splits)
+      const size_t slots = units > 0 ? (size_t)Hkv * units : (size_t)R * Hkv * max_chunks;
+      const size_t need_p = slots * G * (2 + D) * sizeof(float);
       const size_t need_c = two_pass ? 0 : (size_t)R * Hkv * sizeof(int);
       if (ext) {
         if (need_p > ext->partial_bytes || need_c > ext->counter_bytes)

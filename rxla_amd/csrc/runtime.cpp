@@ -15,6 +15,7 @@
 // Code objects embedded by kernels_blob.S (.incbin of the gfx950 .hsaco files).
 extern "C" {
 extern const unsigned char rxw8_co_gemv[], rxw8_co_gemv_end[];
+extern const unsigned char rxw8_co_gemv_rc[], rxw8_co_gemv_rc_end[];
 extern const unsigned char rxw8_co_misc[], rxw8_co_misc_end[];
 extern const unsigned char rxw8_co_attention[], rxw8_co_attention_end[];
 extern const unsigned char rxw8_co_gemm[], rxw8_co_gemm_end[];
@@ -87,7 +88,7 @@ static int module_of(const char *kname) {
   static const struct {
     const char *prefix;
     int module;
-  } routes[] = {{"rxw8_gemv_", 0},      {"rxw8_pack_tiles", 0},     {"rxw8_dequant", 1},
+  } routes[] = {{"rxw8_gemv_rc_", 6}, {"rxw8_gemv_", 0},      {"rxw8_pack_tiles", 0},     {"rxw8_dequant", 1},
                 {"rxw8_linear_generic", 1}, {"rxw8_linear_f32_", 1}, {"rxw8_kv_update", 1},
                 {"rxw8_quantize_w8", 1},
                 {"rxw8_gqa_", 2},
@@ -181,22 +182,39 @@ int ensure_workspace(Runtime *rt, Workspace &ws, size_t bytes, bool zero) {
   return RXW8_OK;
 }
 
-int new_buffer(Runtime *rt, int dtype, const int64_t *dims, int rank, bool zero,
-               Buffer **out) {
-  if (dtype_size(dtype) == 0) return fail(RXW8_INVALID_ARGUMENT, "unsupported dtype %d", dtype);
+int buffer_extent(int dtype, const int64_t *dims, int rank, size_t *bytes) {
+  const size_t esz = dtype_size(dtype);
+  if (esz == 0) return fail(RXW8_INVALID_ARGUMENT, "unsupported dtype %d", dtype);
   if (rank < 0 || rank > RXW8_MAX_RANK)
     return fail(RXW8_INVALID_ARGUMENT, "rank %d outside [0, %d]", rank, RXW8_MAX_RANK);
-  int64_t n = 1;
+  if (rank > 0 && !dims) return fail(RXW8_INVALID_ARGUMENT, "dims is NULL");
+  bool empty = false;
   for (int i = 0; i < rank; ++i) {
     if (dims[i] < 0) return fail(RXW8_INVALID_ARGUMENT, "negative dimension %lld", (long long)dims[i]);
-    n *= dims[i];
+    empty = empty || dims[i] == 0;
   }
+  // checked products: the element count and the byte size must fit int64
+  int64_t n = 1;
+  for (int i = 0; i < rank && !empty; ++i)
+    if (__builtin_mul_overflow(n, dims[i], &n))
+      return fail(RXW8_INVALID_ARGUMENT, "shape overflows a 64-bit element count");
+  int64_t total = 0;
+  if (!empty && __builtin_mul_overflow(n, (int64_t)esz, &total))
+    return fail(RXW8_INVALID_ARGUMENT, "shape overflows a 64-bit byte size");
+  *bytes = (size_t)total;
+  return RXW8_OK;
+}
+
+int new_buffer(Runtime *rt, int dtype, const int64_t *dims, int rank, bool zero,
+               Buffer **out) {
+  size_t bytes = 0;
+  if (int rc = buffer_extent(dtype, dims, rank, &bytes)) return rc;
   auto *b = new rxw8_buffer();
   b->rt = rt;
   b->dtype = dtype;
   b->rank = rank;
   for (int i = 0; i < rank; ++i) b->dims[i] = dims[i];
-  b->bytes = (size_t)n * dtype_size(dtype);
+  b->bytes = bytes;
   int rc = rt_alloc(rt, b->bytes, &b->ptr);
   if (rc) {
     delete b;
@@ -275,10 +293,8 @@ int rxw8_runtime_create(int device, rxw8_runtime **out) {
                {"attention", rxw8_co_attention, rxw8_co_attention_end},
                {"gemm", rxw8_co_gemm, rxw8_co_gemm_end},
                {"decoder", rxw8_co_decoder, rxw8_co_decoder_end},
-               {"qwen35", rxw8_co_qwen35, rxw8_co_qwen35_end}};
-  // Development hook: RXW8_CODE_OBJECT_DIR=<dir> loads <dir>/<name>.hsaco in
-  // place of the embedded code object of that name when the file exists.
-  const char *override_dir = std::getenv("RXW8_CODE_OBJECT_DIR");
+               {"qwen35", rxw8_co_qwen35, rxw8_co_qwen35_end},
+               {"gemv_rc", rxw8_co_gemv_rc, rxw8_co_gemv_rc_end}};
   for (auto &blob : blobs) {  // order = module indices of module_of()
     if (blob.end - blob.begin <= 0) {
       for (hipModule_t mm : rt->modules) (void)hipModuleUnload(mm);
@@ -286,16 +302,7 @@ int rxw8_runtime_create(int device, rxw8_runtime **out) {
       return fail(RXW8_INTERNAL, "embedded code object %s is empty", blob.name);
     }
     hipModule_t m = nullptr;
-    std::string path;
-    if (override_dir && *override_dir) {
-      path = std::string(override_dir) + "/" + blob.name + ".hsaco";
-      if (FILE *f = std::fopen(path.c_str(), "rb")) {
-        std::fclose(f);
-      } else {
-        path.clear();
-      }
-    }
-    e = path.empty() ? hipModuleLoadData(&m, blob.begin) : hipModuleLoad(&m, path.c_str());
+    e = hipModuleLoadData(&m, blob.begin);
     if (e != hipSuccess) {
       int rc = hip_fail(e, "hipModuleLoadData");
       for (hipModule_t mm : rt->modules) (void)hipModuleUnload(mm);
@@ -312,7 +319,7 @@ int rxw8_runtime_create(int device, rxw8_runtime **out) {
     return rc;
   }
   rt->stream = rt->own_stream;
-  if (int rc = noalloc_device_setup(device)) {
+  if (int rc = noalloc_device_setup(device, rt->own_stream)) {
     (void)hipStreamDestroy(rt->own_stream);
     for (hipModule_t mm : rt->modules) (void)hipModuleUnload(mm);
     delete rt;
@@ -370,7 +377,9 @@ int rxw8_runtime_device_info(rxw8_runtime *rt, int *compute_units, char *name,
 
 int rxw8_buffer_create(rxw8_runtime *rt, int dtype, const int64_t *dims, int rank,
                        rxw8_buffer **out) {
-  if (!rt || !out || (rank > 0 && !dims)) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  size_t bytes = 0;  // the shape is validated before anything else
+  if (int rc = buffer_extent(dtype, dims, rank, &bytes)) return rc;
+  if (!rt || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
   std::lock_guard<std::recursive_mutex> g(rt->mu);
   Buffer *b = nullptr;
   int rc = new_buffer(rt, dtype, dims, rank, true, &b);
@@ -381,7 +390,9 @@ int rxw8_buffer_create(rxw8_runtime *rt, int dtype, const int64_t *dims, int ran
 
 int rxw8_buffer_from_host(rxw8_runtime *rt, int dtype, const int64_t *dims, int rank,
                           const void *data, rxw8_buffer **out) {
-  if (!rt || !out || (rank > 0 && !dims)) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  size_t bytes = 0;
+  if (int rc = buffer_extent(dtype, dims, rank, &bytes)) return rc;
+  if (!rt || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
   std::lock_guard<std::recursive_mutex> g(rt->mu);
   Buffer *b = nullptr;
   int rc = new_buffer(rt, dtype, dims, rank, false, &b);
@@ -404,22 +415,17 @@ int rxw8_buffer_from_host(rxw8_runtime *rt, int dtype, const int64_t *dims, int 
 
 int rxw8_buffer_wrap(rxw8_runtime *rt, int dtype, const int64_t *dims, int rank,
                      void *device_ptr, rxw8_buffer **out) {
-  if (!rt || !out || (rank > 0 && !dims)) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
-  if (dtype_size(dtype) == 0) return fail(RXW8_INVALID_ARGUMENT, "unsupported dtype %d", dtype);
-  if (rank < 0 || rank > RXW8_MAX_RANK) return fail(RXW8_INVALID_ARGUMENT, "bad rank %d", rank);
-  int64_t n = 1;
-  for (int i = 0; i < rank; ++i) {
-    if (dims[i] < 0) return fail(RXW8_INVALID_ARGUMENT, "negative dimension");
-    n *= dims[i];
-  }
-  if (n > 0 && !device_ptr) return fail(RXW8_INVALID_ARGUMENT, "device_ptr is NULL");
+  size_t bytes = 0;
+  if (int rc = buffer_extent(dtype, dims, rank, &bytes)) return rc;
+  if (!rt || !out) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if (bytes > 0 && !device_ptr) return fail(RXW8_INVALID_ARGUMENT, "device_ptr is NULL");
   std::lock_guard<std::recursive_mutex> g(rt->mu);
   auto *b = new rxw8_buffer();
   b->rt = rt;
   b->dtype = dtype;
   b->rank = rank;
   for (int i = 0; i < rank; ++i) b->dims[i] = dims[i];
-  b->bytes = (size_t)n * dtype_size(dtype);
+  b->bytes = bytes;
   b->ptr = device_ptr;
   b->owned = false;
   rt->refs.fetch_add(1);

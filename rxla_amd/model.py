@@ -238,6 +238,19 @@ class DecoderModel(_CompiledPlan):
                                          logits.handle if logits is not None else None))
         return nxt
 
+    def forward_layers(self, hidden_in: Buffer, first: int, last: int,
+                       hidden_out: Buffer | None = None, logits: Buffer | None = None,
+                       commit: bool = False) -> Buffer:
+        """Teacher forcing: layers [first, last) of one step from the F32
+        residual rows ``hidden_in`` [b, s, hidden] (rxw8_decoder_forward_layers).
+        Returns the residual rows leaving layer last - 1."""
+        b, s, _ = hidden_in.shape
+        out = hidden_out if hidden_out is not None else self.rt.zeros(hidden_in.shape, DType.F32)
+        _check(_lib.rxw8_decoder_forward_layers(
+            self._h, hidden_in.handle, b, s, first, last, out.handle,
+            logits.handle if logits is not None else None, int(commit)))
+        return out
+
     def generate(self, prompt: Buffer, steps: int, out_ids: Buffer | None = None,
                  use_graph: bool = True) -> Buffer:
         b, s = prompt.shape

@@ -71,6 +71,32 @@ def test_status_codes_and_errors_without_gpu():
     assert lib.rxw8_quantized_linear(None, None, None, None, 4, 5, None) == rx.Status.INVALID_ARGUMENT
 
 
+def test_buffer_shapes_are_checked_before_anything_else():
+    """Buffer shapes whose element count or byte size overflows int64 are
+    rejected with INVALID_ARGUMENT before any handle or device is touched (the
+    shape is checked first, so a NULL runtime still reports the shape)."""
+    _ensure_built()
+    import rxla_amd as rx
+
+    lib = rx._lib
+    I64 = ctypes.c_int64
+    out = ctypes.c_void_p()
+    cases = [((1 << 40, 1 << 30, 1 << 2), b"element count"),  # 2^72 elements
+             ((1 << 61, 1), b"byte size"),                      # 2^61 elements x 4 bytes
+             ((-1, 4), b"negative")]
+    for dims, what in cases:
+        d = (I64 * len(dims))(*dims)
+        for call in (lambda: lib.rxw8_buffer_create(None, int(rx.DType.F32), d, len(dims), out),
+                     lambda: lib.rxw8_buffer_from_host(None, int(rx.DType.F32), d, len(dims), None, out),
+                     lambda: lib.rxw8_buffer_wrap(None, int(rx.DType.F32), d, len(dims), None, out)):
+            assert call() == rx.Status.INVALID_ARGUMENT
+            assert what in lib.rxw8_last_error(), (dims, lib.rxw8_last_error())
+    # an empty shape never overflows: its other dims are not multiplied
+    d = (I64 * 3)(0, 1 << 62, 1 << 62)
+    assert lib.rxw8_buffer_create(None, int(rx.DType.F32), d, 3, out) == rx.Status.INVALID_ARGUMENT
+    assert b"NULL" in lib.rxw8_last_error()
+
+
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is present")
 def test_runtime_create_without_device_is_failed_precondition():
     _ensure_built()
@@ -133,4 +159,5 @@ def test_every_kernel_routes_to_its_code_object():
             continue  # formatted names, checked by prefix below
         assert module_of(name) is not None, name
     assert module_of("rxw8_gemv_w8_pk_mb1_rw1_u4") == "gemv"
+    assert module_of("rxw8_gemv_rc_w8_pk_mb1_rw1_u4_w16_xg_rn") == "gemv_rc"
     assert seen > 10

@@ -14,15 +14,17 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
 # Per element (floor at 1% of the rms): within one bf16 ulp, whose relative
-# spacing is at most 2^-7. Against the exact product of the bf16 activations
-# and the integer weights (f64) the GEMV's single rounding of its f32 sum
-# stays within half of that; two independently rounded bf16 results (GPU and
-# the reference-order oracle) can be one ulp apart.
+# spacing is at most 2^-7. The GEMV forms the reference's product, the f32 sum
+# of bf16(x) * bf16(dequantised W), and rounds it to bf16; against the same
+# cast points with exact (f64) accumulation only the summation order differs,
+# so two independently rounded bf16 results can be one ulp apart.
 ELEM_TOL = 2.0 ** -7
 
 
 def exact(x, u8, s):
-    return oracle.quantized_linear(x, u8, s, oracle.COMPUTE_F32, oracle.ACCUM_F64, threads=16)
+    """The reference's cast points (bf16 x, bf16 dequantised W, bf16 result)
+    with exact accumulation."""
+    return oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16, oracle.ACCUM_F64, threads=16)
 
 
 def rx():
@@ -339,3 +341,44 @@ def test_pack_weight_validation(rt):
     with pytest.raises(r.Error) as e:
         r.pack_weight(rt, rt.buffer(np.zeros((24, 64), np.uint8)))  # 24 % 16 != 0
     assert e.value.code == r.Status.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("m,n,k,g,packed", [
+    (1, 4096, 4096, 4096, False), (4, 6144, 4096, 4096, True), (16, 24576, 4096, 4096, False),
+    (8, 2048, 2048, 2048, True), (8, 12288, 2048, 2048, True),
+    # grouped scales (the scale tile staged per workgroup), row-major and packed
+    (8, 4096, 2048, 128, True), (8, 2048, 6144, 64, False), (1, 1024, 4096, 2048, False)])
+def test_reference_cast_point_gemv(rt, monkeypatch, m, n, k, g, packed):
+    """The GEMV casts every dequantised weight to bf16 before the product,
+    bf16((u - 128) * s) (crates/rxla-nn/src/layers.rs:288-297), and applies no
+    scale after the sum. Against the oracle with the same cast points and
+    exact (f64) accumulation, only the f32 summation of the kernel and the
+    final bf16 rounding differ: each output within one bf16 ulp (2^-7
+    relative, floor at 1% of the rms), and closer to that oracle than the
+    exact-code product with the scale after the sum (RXW8_GEMV_REF_CAST=0)."""
+    r = rx()
+    rng = np.random.default_rng(m * 7 + n + g)
+    x = oracle.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    u8, s = quantized(rng, n, k, g)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_BF16, oracle.ACCUM_F64, threads=16)
+
+    def run():
+        w = rt.buffer(u8, r.DType.U8)
+        if packed:
+            w = r.pack_weight(rt, w)
+        y = r.quantized_linear(rt, rt.buffer(oracle.bf16_bits(x), r.DType.BF16), w,
+                               rt.buffer(s, r.DType.F32), r.DType.BF16, r.DType.F32)
+        return y.to_numpy()
+
+    monkeypatch.setenv("RXW8_GEMV_REF_CAST", "0")
+    y_exact = run()
+    monkeypatch.delenv("RXW8_GEMV_REF_CAST")
+    y_rc = run()
+    e_rc, e_exact = elem_rel_err(y_rc, ref), elem_rel_err(y_exact, ref)
+    same = float(np.mean(y_rc == ref))
+    print(f"ref-cast m={m} n={n} k={k} g={g} packed={packed}: elem_rel_err {e_rc:.3e} "
+          f"(exact-code {e_exact:.3e}); bit-equal {same:.4f}; normwise {rel_err(y_rc, ref):.3e} "
+          f"(exact-code {rel_err(y_exact, ref):.3e})")
+    np.testing.assert_array_equal(oracle.round_bf16(y_rc), y_rc)
+    assert e_rc <= ELEM_TOL
+    assert rel_err(y_rc, ref) <= rel_err(y_exact, ref)

@@ -53,6 +53,22 @@ def test_noalloc_equals_allocating_entry_point_on_two_calls(rt):
     assert rel_err(both(rt, c4)[0], oracle.gqa_decode_bf16cache(q, kc, vc, lens, threads=16)) <= 1e-4
 
 
+@pytest.mark.parametrize("b,hq,hkv", [(64, 8, 2), (128, 8, 1)])
+def test_noalloc_length_proportional_plans(rt, b, hq, hkv):
+    """Ragged rows on the length-proportional split plan (units workgroups per
+    kv head shared by the rows): one partial slot per workgroup, so these fit
+    the scratch (B = 64, Hkv = 2 and B = 128, Hkv = 1 at Lmax 4096), bit for
+    bit equal to the allocating entry point and within 1e-4 of the oracle."""
+    lens = np.random.default_rng(b + hkv).integers(1, 4097, b)
+    case = make_case(85 + b, b, hq, hkv, 4096, lens)
+    got, want = both(rt, case)
+    np.testing.assert_array_equal(got, want)
+    q, kc, vc, lens, _ = case
+    err = rel_err(got, oracle.gqa_decode_bf16cache(q, kc, vc, lens, threads=16))
+    print(f"noalloc B={b} Hq={hq} Hkv={hkv}: rel_err vs oracle {err:.3e}", flush=True)
+    assert err <= 1e-4
+
+
 def test_noalloc_rejects_a_plan_beyond_its_scratch(rt, monkeypatch):
     r = rx()
     # 64 forced splits of 8 x 8 (row, kv head) pairs at G = 8 need 17.0 MB of
