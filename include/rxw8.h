@@ -455,6 +455,30 @@ void rxw8_xla_gqa_decode(void *stream, void **buffers, const char *opaque,
 void rxw8_xla_gqa_prefill(void *stream, void **buffers, const char *opaque,
                           size_t opaque_len, void *status);
 
+/* ---- XLA typed-FFI handlers (HLO api_version 4) ----------------------------
+ * The same three calls for the reference's default custom-call form,
+ * CustomCall::typed_ffi (crates/rxla-core/src/tensor_handle.rs:278-300,
+ * api_version 4), registered as GpuCustomCallApi::TypedFfi with an execute
+ * handler (crates/rxla-pjrt/src/runtime.rs:265-308,395-428). Each is an
+ * XLA_FFI_Handler of XLA's FFI C API 0.1 (xla/ffi/api/c_api.h): call_frame is
+ * an XLA_FFI_CallFrame*, and the return value NULL or an XLA_FFI_Error* made
+ * with the frame's api->XLA_FFI_Error_Create (code = the rxw8_status, which is
+ * XLA's numbering). A frame carrying the metadata extension is answered with
+ * API version 0.1 and no traits; stages other than execute do nothing. Shapes
+ * and dtypes come from the buffers (XLA_FFI_DataType S32, U8, F16, F32, BF16),
+ * the stream from api->XLA_FFI_Stream_Get, options from the backend_config
+ * dictionary's attributes. Malformed frames (operand count, non-buffer
+ * operands, other dtypes, attribute kinds) fail before any device work.
+ *   rxw8_xla_ffi_quantized_linear: x [..., k], weight U8 [n, k] or packed,
+ *     scale F32 [n, k/g] -> y [..., n]; compute = "bf16" (default) | "f32".
+ *   rxw8_xla_ffi_gqa_decode: q [b, hq, d], k_cache, v_cache [b, hkv, lmax, d],
+ *     lens S32 [b] -> out [b, hq, d]; scale (optional f32 / f64 scalar).
+ *   rxw8_xla_ffi_gqa_prefill: q [b, s, hq, d], k_cache, v_cache BF16, starts
+ *     S32 [b] -> out [b, s, hq, d]; scale (optional). */
+void *rxw8_xla_ffi_quantized_linear(void *call_frame);
+void *rxw8_xla_ffi_gqa_decode(void *call_frame);
+void *rxw8_xla_ffi_gqa_prefill(void *call_frame);
+
 #ifdef __cplusplus
 }
 #endif

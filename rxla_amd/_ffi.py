@@ -36,6 +36,7 @@ EXPORTS = [
     "rxw8_qwen35_create", "rxw8_qwen35_destroy", "rxw8_qwen35_num_parameters",
     "rxw8_qwen35_parameter_info", "rxw8_qwen35_bind_parameter", "rxw8_qwen35_forward",
     "rxw8_xla_quantized_linear", "rxw8_xla_gqa_decode", "rxw8_xla_gqa_prefill",
+    "rxw8_xla_ffi_quantized_linear", "rxw8_xla_ffi_gqa_decode", "rxw8_xla_ffi_gqa_prefill",
 ]
 
 
@@ -126,6 +127,9 @@ def _declare(L):
         "rxw8_qwen35_forward": (c_int, [vp, vp, vp]),
         "rxw8_xla_quantized_linear": (None, [vp, POINTER(vp), c_char_p, c_size_t, vp]),
         "rxw8_xla_gqa_decode": (None, [vp, POINTER(vp), c_char_p, c_size_t, vp]),
+        "rxw8_xla_ffi_quantized_linear": (vp, [vp]),
+        "rxw8_xla_ffi_gqa_decode": (vp, [vp]),
+        "rxw8_xla_ffi_gqa_prefill": (vp, [vp]),
         "rxw8_xla_gqa_prefill": (None, [vp, POINTER(vp), c_char_p, c_size_t, vp]),
     }
     for name, (res, args) in sigs.items():

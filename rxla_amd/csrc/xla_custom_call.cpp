@@ -19,9 +19,18 @@
 // shapes the entry point rejects) launches nothing; it is reported through
 // XlaCustomCallStatusSetFailure when the hosting process exports it (every XLA
 // runtime does), and always through rxw8_last_error().
+//
+// The typed-FFI handlers (rxw8_xla_ffi_*, HLO api_version 4, the reference's
+// default for CustomCall::typed_ffi, registered as GpuCustomCallApi::TypedFfi)
+// are XLA_FFI_Handler functions: they receive XLA's call frame -- operand and
+// result buffers with their dtypes and dims, the backend_config dictionary as
+// typed attributes, the execution context that yields the stream -- and return
+// NULL or an error made by the frame's own API table. They run the same `_into`
+// entry points as the untyped handlers.
 #include <dlfcn.h>
 
 #include <cmath>
+#include <cstddef>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -156,6 +165,241 @@ void run_on_stream(void *stream, const char *what, void *status, F body) {
   }
 }
 
+// ---- XLA FFI C ABI --------------------------------------------------------
+// The subset of XLA's public FFI C API (xla/ffi/api/c_api.h, FFI API version
+// 0.1, the API of XLA releases that ship PJRT C API 0.115, the version the
+// reference vendors) that the handlers read: the layouts must match XLA's, so
+// the structs and enum values follow that header; the names carry an Xf
+// prefix here. Every struct starts with struct_size and an extension chain.
+struct XfExtensionBase {
+  size_t struct_size;
+  int type;  // XLA_FFI_Extension_Type; 1 = XLA_FFI_Extension_Metadata
+  XfExtensionBase *next;
+};
+struct XfApiVersion {
+  size_t struct_size;
+  XfExtensionBase *extension_start;
+  int major_version, minor_version;
+};
+struct XfErrorCreateArgs {
+  size_t struct_size;
+  XfExtensionBase *extension_start;
+  const char *message;
+  int errc;  // XLA_FFI_Error_Code: the absl::StatusCode numbering (= rxw8_status)
+};
+struct XfStreamGetArgs {
+  size_t struct_size;
+  XfExtensionBase *extension_start;
+  void *ctx;     // XLA_FFI_ExecutionContext*
+  void *stream;  // out: the platform stream (hipStream_t)
+};
+typedef void *(*XfErrorCreate)(XfErrorCreateArgs *);
+typedef void *(*XfStreamGet)(XfStreamGetArgs *);
+struct XfApi {
+  size_t struct_size;
+  XfExtensionBase *extension_start;
+  XfApiVersion api_version;
+  void *internal_api;
+  XfErrorCreate error_create;  // XLA_FFI_Error_Create
+  void *error_get_message;     // XLA_FFI_Error_GetMessage
+  void *error_destroy;         // XLA_FFI_Error_Destroy
+  void *handler_register;      // XLA_FFI_Handler_Register
+  XfStreamGet stream_get;      // XLA_FFI_Stream_Get
+};
+struct XfBuffer {
+  size_t struct_size;
+  XfExtensionBase *extension_start;
+  int dtype;  // XLA_FFI_DataType
+  void *data;
+  int64_t rank;
+  int64_t *dims;
+};
+struct XfArgs {  // XLA_FFI_Args and XLA_FFI_Rets share this layout
+  size_t struct_size;
+  XfExtensionBase *extension_start;
+  int64_t size;
+  int *types;  // XLA_FFI_ArgType / XLA_FFI_RetType: 1 = buffer
+  void **args;
+};
+struct XfByteSpan {
+  const char *ptr;
+  size_t len;
+};
+struct XfScalar {
+  int dtype;
+  void *value;
+};
+struct XfAttrs {
+  size_t struct_size;
+  XfExtensionBase *extension_start;
+  int64_t size;
+  int *types;  // XLA_FFI_AttrType: 1 array, 2 dictionary, 3 scalar, 4 string
+  XfByteSpan **names;
+  void **attrs;
+};
+struct XfCallFrame {
+  size_t struct_size;
+  XfExtensionBase *extension_start;
+  const XfApi *api;
+  void *ctx;
+  int stage;  // XLA_FFI_ExecutionStage: 3 = execute
+  XfArgs args;
+  XfArgs rets;
+  XfAttrs attrs;
+};
+struct XfMetadata {
+  size_t struct_size;
+  XfApiVersion api_version;
+  uint32_t traits;  // XLA_FFI_Handler_Traits (0: not command-buffer compatible)
+};
+struct XfMetadataExtension {
+  XfExtensionBase extension_base;
+  XfMetadata *metadata;
+};
+constexpr int kXfMetadataExtension = 1;
+constexpr int kXfStageExecute = 3;
+constexpr int kXfBuffer = 1;
+constexpr int kXfAttrScalar = 3, kXfAttrString = 4;
+constexpr int kXfApiMajor = 0, kXfApiMinor = 1;
+// XLA_FFI_DataType (= xla::PrimitiveType, the reference's vendored
+// xla_data.proto) -> rxw8 dtype; 0 for types no handler takes
+int xf_dtype(int t) {
+  switch (t) {
+    case 4: return RXW8_I32;    // S32
+    case 6: return RXW8_U8;     // U8
+    case 10: return RXW8_F16;   // F16
+    case 11: return RXW8_F32;   // F32
+    case 16: return RXW8_BF16;  // BF16
+    default: return 0;
+  }
+}
+
+// A typed call's operands (n_args buffers then n_rets) as rxw8 views, and its
+// attributes by name. check() validates the frame's structure before anything
+// touches a device, so malformed frames fail without a GPU.
+struct XfCall {
+  const XfCallFrame *f;
+  const char *what;
+  const XfBuffer *buf[8] = {nullptr};
+  int n = 0;
+
+  int check(int n_args, int n_rets) {
+    if (f->struct_size < offsetof(XfCallFrame, attrs) + sizeof(XfAttrs))
+      return fail(RXW8_INVALID_ARGUMENT, "%s: XLA FFI call frame of %zu bytes is too small", what,
+                  f->struct_size);
+    if (f->args.size != n_args || f->rets.size != n_rets)
+      return fail(RXW8_INVALID_ARGUMENT, "%s: expects %d operands and %d result, got %lld and %lld",
+                  what, n_args, n_rets, (long long)f->args.size, (long long)f->rets.size);
+    for (int i = 0; i < n_args + n_rets; ++i) {
+      const XfArgs &a = i < n_args ? f->args : f->rets;
+      const int j = i < n_args ? i : i - n_args;
+      if (a.types[j] != kXfBuffer || !a.args[j])
+        return fail(RXW8_INVALID_ARGUMENT, "%s: operand %d is not a buffer", what, i);
+      buf[n] = static_cast<const XfBuffer *>(a.args[j]);
+      if (xf_dtype(buf[n]->dtype) == 0 || buf[n]->rank < 0 || buf[n]->rank > RXW8_MAX_RANK)
+        return fail(RXW8_INVALID_ARGUMENT, "%s: operand %d has XLA dtype %d and rank %lld", what, i,
+                    buf[n]->dtype, (long long)buf[n]->rank);
+      ++n;
+    }
+    return RXW8_OK;
+  }
+  // attribute `name` of the given kind, or null when absent
+  const void *attr(const char *name, int kind) const {
+    const size_t len = std::strlen(name);
+    for (int64_t i = 0; i < f->attrs.size; ++i) {
+      const XfByteSpan *nm = f->attrs.names[i];
+      if (nm && nm->len == len && std::memcmp(nm->ptr, name, len) == 0)
+        return f->attrs.types[i] == kind ? f->attrs.attrs[i] : nullptr;
+    }
+    return nullptr;
+  }
+  bool has(const char *name) const {
+    const size_t len = std::strlen(name);
+    for (int64_t i = 0; i < f->attrs.size; ++i)
+      if (f->attrs.names[i] && f->attrs.names[i]->len == len &&
+          std::memcmp(f->attrs.names[i]->ptr, name, len) == 0)
+        return true;
+    return false;
+  }
+  // f32 / f64 scalar attribute
+  int scale(float *out) const {
+    if (!has("scale")) return RXW8_OK;
+    const XfScalar *sc = static_cast<const XfScalar *>(attr("scale", kXfAttrScalar));
+    if (sc && sc->dtype == 11) *out = *static_cast<const float *>(sc->value);
+    else if (sc && sc->dtype == 12) *out = (float)*static_cast<const double *>(sc->value);
+    else return fail(RXW8_INVALID_ARGUMENT, "%s: attribute scale must be an f32 or f64 scalar", what);
+    return RXW8_OK;
+  }
+  // string attribute naming a dtype (f32 / bf16)
+  int dtype_attr(const char *name, int *out) const {
+    if (!has(name)) return RXW8_OK;
+    const XfByteSpan *sp = static_cast<const XfByteSpan *>(attr(name, kXfAttrString));
+    const std::string v = sp ? std::string(sp->ptr, sp->len) : std::string();
+    if (v == "bf16") *out = RXW8_BF16;
+    else if (v == "f32") *out = RXW8_F32;
+    else return fail(RXW8_INVALID_ARGUMENT, "%s: attribute %s must be the string bf16 or f32", what, name);
+    return RXW8_OK;
+  }
+  int view(Views &v, rxw8_runtime *rt, int i, rxw8_buffer **out) const {
+    const XfBuffer *b = buf[i];
+    const int rc = rxw8_buffer_wrap(rt, xf_dtype(b->dtype), b->dims, (int)b->rank, b->data, &v.b[v.n]);
+    if (rc) return rc;
+    *out = v.b[v.n++];
+    return RXW8_OK;
+  }
+};
+
+// Options a typed call reads from its attributes.
+struct XfOptions {
+  int compute = RXW8_BF16;
+  float scale = 0.f;
+};
+
+// Runs a typed call: the metadata query (the frame carries
+// XLA_FFI_Metadata_Extension: report API 0.1, no traits), stages other than
+// execute (nothing to do), then the frame's structure and attributes
+// (`parse`, before any device work), and `body` on the runtime of the
+// context's stream; a failure becomes the frame's XLA_FFI_Error.
+template <typename P, typename F>
+void *run_typed(void *frame, const char *what, int n_args, int n_rets, P parse, F body) {
+  XfCallFrame *f = static_cast<XfCallFrame *>(frame);
+  if (!f) {
+    fail(RXW8_INVALID_ARGUMENT, "%s: call frame is NULL", what);
+    return nullptr;  // no API table to report through
+  }
+  if (f->extension_start && f->extension_start->type == kXfMetadataExtension) {
+    XfMetadata *m = reinterpret_cast<XfMetadataExtension *>(f->extension_start)->metadata;
+    if (m) {
+      m->api_version.major_version = kXfApiMajor;
+      m->api_version.minor_version = kXfApiMinor;
+      m->traits = 0;
+    }
+    return nullptr;
+  }
+  if (f->stage != kXfStageExecute) return nullptr;
+  XfCall call{f, what};
+  XfOptions opt;
+  int rc = call.check(n_args, n_rets);
+  if (!rc) rc = parse(call, opt);
+  if (!rc) {
+    XfStreamGetArgs sa{sizeof(XfStreamGetArgs), nullptr, f->ctx, nullptr};
+    void *err = f->api && f->api->stream_get ? f->api->stream_get(&sa) : nullptr;
+    if (err) return err;  // XLA's own error, passed through
+    if (!f->api || !f->api->stream_get)
+      rc = fail(RXW8_INVALID_ARGUMENT, "%s: XLA FFI API table has no stream getter", what);
+    rxw8_runtime *rt = rc ? nullptr : stream_runtime(sa.stream, &rc);
+    if (rt) {
+      std::lock_guard<std::recursive_mutex> g(rt->mu);
+      rc = body(rt, call, opt);
+    }
+  }
+  if (!rc) return nullptr;
+  if (!f->api || !f->api->error_create) return nullptr;
+  std::string msg = std::string(what) + ": " + rxw8_last_error();
+  XfErrorCreateArgs ea{sizeof(XfErrorCreateArgs), nullptr, msg.c_str(), rc};
+  return f->api->error_create(&ea);
+}
+
 int bad_opaque(const char *what) {
   return fail(RXW8_INVALID_ARGUMENT, "%s: backend_config is missing a key or has a malformed value",
               what);
@@ -235,6 +479,59 @@ void rxw8_xla_gqa_prefill(void *stream, void **buffers, const char *opaque, size
       return rc;
     return rxw8_gqa_prefill_into(rt, q, kc, vc, starts, scale, out);
   });
+}
+
+// ---- typed FFI (api_version 4) ---------------------------------------------
+
+void *rxw8_xla_ffi_quantized_linear(void *call_frame) {
+  // operands x [..., k], weight U8 [n, k] (or packed), scale F32 [n, k/g];
+  // result y [..., n]; attribute compute = "bf16" (default) or "f32"
+  return run_typed(
+      call_frame, "rxw8_quantized_linear", 3, 1,
+      [](const XfCall &c, XfOptions &o) { return c.dtype_attr("compute", &o.compute); },
+      [](rxw8_runtime *rt, const XfCall &c, const XfOptions &o) {
+        Views v;
+        rxw8_buffer *x, *w, *s, *y;
+        int rc;
+        if ((rc = c.view(v, rt, 0, &x)) || (rc = c.view(v, rt, 1, &w)) || (rc = c.view(v, rt, 2, &s)) ||
+            (rc = c.view(v, rt, 3, &y)))
+          return rc;
+        return rxw8_quantized_linear_into(rt, x, w, s, o.compute, y);
+      });
+}
+
+void *rxw8_xla_ffi_gqa_decode(void *call_frame) {
+  // operands q [b, hq, d], k_cache, v_cache [b, hkv, lmax, d], lens S32 [b];
+  // result out [b, hq, d]; attribute scale (optional f32 / f64)
+  return run_typed(
+      call_frame, "rxw8_gqa_decode", 4, 1,
+      [](const XfCall &c, XfOptions &o) { return c.scale(&o.scale); },
+      [](rxw8_runtime *rt, const XfCall &c, const XfOptions &o) {
+        Views v;
+        rxw8_buffer *q, *kc, *vc, *lens, *out;
+        int rc;
+        if ((rc = c.view(v, rt, 0, &q)) || (rc = c.view(v, rt, 1, &kc)) || (rc = c.view(v, rt, 2, &vc)) ||
+            (rc = c.view(v, rt, 3, &lens)) || (rc = c.view(v, rt, 4, &out)))
+          return rc;
+        return rxw8_gqa_decode_into(rt, q, kc, vc, lens, nullptr, o.scale, out);
+      });
+}
+
+void *rxw8_xla_ffi_gqa_prefill(void *call_frame) {
+  // operands q [b, s, hq, d], k_cache, v_cache BF16 [b, hkv, lmax, d], starts
+  // S32 [b]; result out [b, s, hq, d]; attribute scale (optional)
+  return run_typed(
+      call_frame, "rxw8_gqa_prefill", 4, 1,
+      [](const XfCall &c, XfOptions &o) { return c.scale(&o.scale); },
+      [](rxw8_runtime *rt, const XfCall &c, const XfOptions &o) {
+        Views v;
+        rxw8_buffer *q, *kc, *vc, *starts, *out;
+        int rc;
+        if ((rc = c.view(v, rt, 0, &q)) || (rc = c.view(v, rt, 1, &kc)) || (rc = c.view(v, rt, 2, &vc)) ||
+            (rc = c.view(v, rt, 3, &starts)) || (rc = c.view(v, rt, 4, &out)))
+          return rc;
+        return rxw8_gqa_prefill_into(rt, q, kc, vc, starts, o.scale, out);
+      });
 }
 
 }  // extern "C"

@@ -127,3 +127,77 @@ def test_each_stream_has_its_own_workspaces_and_none_grows_in_a_capture(rt):
     s.synchronize()
     want = r.grouped_query_attention(rt, *big[:4]).to_numpy()
     np.testing.assert_array_equal(big[4].to_numpy(), want)
+
+
+# ---- typed FFI (api_version 4): XLA's call frame, stream from the API table
+
+def ffi_call(rt, name, operands, results, attrs=None):
+    import xla_ffi_frames as xf
+    api = xf.FakeApi(stream=rt.stream())
+    fr = xf.Frame(api, operands, results, attrs)
+    err = getattr(rx()._lib, name)(fr.ptr())
+    return err, api
+
+
+def fbuf(b):
+    import xla_ffi_frames as xf
+    r = rx()
+    code = {r.DType.F32: xf.F32, r.DType.BF16: xf.BF16, r.DType.U8: xf.U8, r.DType.I32: xf.S32}
+    return (code[b.dtype], list(b.shape), b.ptr)
+
+
+@pytest.mark.parametrize("xd,compute", [("f32", "bf16"), ("bf16", "bf16"), ("f32", "f32")])
+def test_typed_ffi_quantized_linear_matches_the_c_abi(rt, xd, compute):
+    r = rx()
+    dt = {"f32": r.DType.F32, "bf16": r.DType.BF16}
+    rng = np.random.default_rng(11)
+    m, n, k, g = 8, 640, 1024, 128
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    u8, s = oracle.quantize_w8((rng.standard_normal((n, k)) * 0.02).astype(np.float32), g)
+    xb = rt.buffer(oracle.bf16_bits(x), r.DType.BF16) if xd == "bf16" else rt.buffer(x)
+    wb, sb = rt.buffer(u8), rt.buffer(s)
+    want = r.quantized_linear(rt, xb, wb, sb, dt[compute], r.DType.F32).to_numpy()
+    y = rt.zeros((m, n), r.DType.F32)
+    err, api = ffi_call(rt, "rxw8_xla_ffi_quantized_linear", [fbuf(xb), fbuf(wb), fbuf(sb)],
+                        [fbuf(y)], {"compute": compute})
+    assert err is None and api.errors == [] and api.stream_calls == 1
+    np.testing.assert_array_equal(y.to_numpy(), want)
+
+
+def test_typed_ffi_attention_matches_the_c_abi(rt):
+    r = rx()
+    rng = np.random.default_rng(12)
+    b, hq, hkv, lmax, d, s = 2, 8, 2, 96, 128, 20
+    kc = rt.buffer(oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32)),
+                   r.DType.BF16)
+    vc = rt.buffer(oracle.bf16_bits(rng.standard_normal((b, hkv, lmax, d)).astype(np.float32)),
+                   r.DType.BF16)
+    q = rt.buffer(oracle.bf16_bits(rng.standard_normal((b, hq, d)).astype(np.float32)), r.DType.BF16)
+    lens = rt.buffer(np.array([37, 96], np.int32))
+    want = r.grouped_query_attention(rt, q, kc, vc, lens, scale=0.1).to_numpy()
+    out = rt.zeros((b, hq, d), r.DType.F32)
+    err, api = ffi_call(rt, "rxw8_xla_ffi_gqa_decode", [fbuf(q), fbuf(kc), fbuf(vc), fbuf(lens)],
+                        [fbuf(out)], {"scale": 0.1})
+    assert err is None and api.errors == []
+    np.testing.assert_array_equal(out.to_numpy(), want)
+    qp = rt.buffer(oracle.bf16_bits(rng.standard_normal((b, s, hq, d)).astype(np.float32)),
+                   r.DType.BF16)
+    starts = rt.buffer(np.array([0, 40], np.int32))
+    want = r.grouped_query_attention_prefill(rt, qp, kc, vc, starts).to_numpy()
+    outp = rt.zeros((b, s, hq, d), r.DType.F32)
+    err, api = ffi_call(rt, "rxw8_xla_ffi_gqa_prefill", [fbuf(qp), fbuf(kc), fbuf(vc), fbuf(starts)],
+                        [fbuf(outp)])
+    assert err is None and api.errors == []
+    np.testing.assert_array_equal(outp.to_numpy(), want)
+
+
+def test_typed_ffi_shape_error_leaves_the_result_untouched(rt):
+    r = rx()
+    x = rt.buffer(np.ones((4, 64), np.float32))
+    w = rt.buffer(np.full((32, 64), 130, np.uint8))
+    s = rt.buffer(np.ones((32, 1), np.float32))
+    y = rt.buffer(np.full((4, 33), 7.0, np.float32))  # N mismatch
+    err, api = ffi_call(rt, "rxw8_xla_ffi_quantized_linear", [fbuf(x), fbuf(w), fbuf(s)], [fbuf(y)])
+    assert err is not None and api.errors and api.errors[0][0] == int(r.Status.INVALID_ARGUMENT)
+    rt.synchronize()
+    np.testing.assert_array_equal(y.to_numpy(), 7.0)
