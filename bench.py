@@ -12,10 +12,14 @@ least 790 MB of other weights of that N (3 x the 256 MB MALL): no weight byte
 is served from the MALL and the figure is HBM bandwidth.
 
 value        = sweep algorithmic bytes / wall time of the timed steps (GB/s);
-               each step is the 9 launches, replayed from HIP graphs: one of
-               48 consecutive steps (every pool turns over a whole number of
-               times in it) replayed K // 48 times, then one of the first
-               K % 48 steps (a graph boundary idles the GPU for ~8 us)
+               each step is the 9 products in one rxw8_quantized_linear_group
+               call (two grouped launches: B 1 and 4, then B 16; every
+               product on the 12-wave 48-row tiling), replayed from HIP
+               graphs: one of 48 consecutive steps (every pool turns over a
+               whole number of times in it) replayed K // 48 times, then one
+               of the first K % 48 steps (a graph boundary idles the GPU for
+               ~8 us); single_launches times the same steps as 9
+               rxw8_quantized_linear_into calls (the per-shape plans)
 roofline     = the GEMV kernel of the largest sweep shape, B=1 N=24576
                (rxw8_gemv_rc_w8_pk_mb1_rw3_u4_w12: 12 waves, 48-row tiles, 512
                workgroups = 2 whole rounds): algorithmic bytes per launch /
@@ -209,6 +213,15 @@ class SweepPools:
     def launch_step(self, step, wts):
         for b, n in self.plan:
             self.launch(b, n, 3 * step + BS.index(b), wts)
+
+    def launch_step_grouped(self, step, wts):
+        """The step's nine products in one rxw8_quantized_linear_group call
+        (two launches: B 1 and 4, then B 16)."""
+        xs, ws, ss, ys = [], [], [], []
+        for b, n in self.plan:
+            u, s = wts[n][(3 * step + BS.index(b)) % POOL[n]]
+            xs.append(self.xb[b]), ws.append(u), ss.append(s), ys.append(self.yb[(b, n)])
+        self.rx.quantized_linear_group(self.rt, xs, ws, ss, ys)
 
     def launch_next(self, b, n, wts):
         self.launch(b, n, self.cursor[n], wts)
@@ -652,8 +665,11 @@ def main():
     plan = pools.plan
     step_bytes = sum(gemv_bytes(b, n) for b, n in plan)
 
-    def launch_all(step, events=None, wts=None):
-        pools.launch_step(step, wts or wb)
+    def launch_all(step, events=None, wts=None, grouped=True):
+        if grouped:
+            pools.launch_step_grouped(step, wts or wb)
+        else:
+            pools.launch_step(step, wts or wb)
 
     # Eager warmup (sizes workspaces, resolves kernels), then HIP graphs: one
     # holding GRAPH_STEPS consecutive steps (every pool turns over a whole
@@ -665,16 +681,17 @@ def main():
         launch_all(GRAPH_STEPS - args.warmup + i)
     torch.cuda.synchronize()
 
-    def step_graph(first, count, wts=None):
+    def step_graph(first, count, wts=None, grouped=True):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
             for st in range(first, first + count):
-                launch_all(st, wts=wts)
+                launch_all(st, wts=wts, grouped=grouped)
         return g
 
-    def timed_graphs(wts=None):
-        full = step_graph(0, GRAPH_STEPS, wts) if args.steps >= GRAPH_STEPS else None
-        rem = step_graph(0, args.steps % GRAPH_STEPS, wts) if args.steps % GRAPH_STEPS else None
+    def timed_graphs(wts=None, grouped=True):
+        full = (step_graph(0, GRAPH_STEPS, wts, grouped) if args.steps >= GRAPH_STEPS else None)
+        rem = (step_graph(0, args.steps % GRAPH_STEPS, wts, grouped)
+               if args.steps % GRAPH_STEPS else None)
         return full, rem
 
     def run_steps(full, rem, steps):
@@ -748,19 +765,27 @@ def main():
         roof_events.append((e0, e1))
     torch.cuda.synchronize()
 
+    def timed_variant(wts, grouped):
+        full, rem = timed_graphs(wts, grouped)
+        if full is not None:
+            full.replay()
+        else:
+            for st in range(GRAPH_STEPS):
+                launch_all(st, wts=wts, grouped=grouped)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run_steps(full, rem, args.steps)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
     # The same sweep on the reference's row-major U8 weights (the layout the
-    # XLA handlers and direct QuantizedLinear::apply calls receive): graphs of
-    # the same launches, same step count, timed the same way.
-    row_full, row_rem = timed_graphs(wb_row)
-    if row_full is not None:
-        row_full.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    run_steps(row_full, row_rem, args.steps)
-    torch.cuda.synchronize()
-    wall_row = time.perf_counter() - t0
-    del row_full, row_rem
+    # XLA handlers and direct QuantizedLinear::apply calls receive), and as
+    # nine single launches per step (one rxw8_quantized_linear_into each):
+    # graphs of the same steps, same step count, timed the same way.
+    wall_row = timed_variant(wb_row, True)
     log(f"timed {args.steps} row-major graph steps in {wall_row:.4f} s")
+    wall_single = timed_variant(wb, False)
+    log(f"timed {args.steps} single-launch graph steps in {wall_single:.4f} s")
 
     per_shape = {}
     for b, n, e0, e1 in events:
@@ -805,7 +830,9 @@ def main():
                    "scales": "per-output-channel f32",
                    "weight_copies": {str(n): POOL[n] for n in NS},
                    "weight_layout": "packed",
-                   "launches_per_step": len(plan), "bytes_per_step": step_bytes,
+                   "products_per_step": len(plan),
+                   "launches_per_step": "2 (rxw8_quantized_linear_group: B 1 and 4, then B 16)",
+                   "bytes_per_step": step_bytes,
                    "steps_per_graph_replay": GRAPH_STEPS,
                    "copy_rotation": "launch (b, n) of step t reads copy (3 t + index of b) mod "
                                     "copies[n]: a copy is read again after >= 790 MB of other "
@@ -841,6 +868,12 @@ def main():
                      "ms_per_step": round(wall_row / args.steps * 1e3, 4),
                      "weight_layout": "row-major U8 [N, K] (the reference's weight ABI)",
                      "timing": "same sweep, step count and graph replays as `value`"},
+        "single_launches": {"value": round(step_bytes * args.steps / wall_single / 1e9, 2),
+                            "unit": "GB/s", "ms_per_step": round(wall_single / args.steps * 1e3, 4),
+                            "launches_per_step": len(plan) + 1,
+                            "timing": "the same steps as nine rxw8_quantized_linear_into calls "
+                                      "each (per-shape plans; one splits K and adds a reduce "
+                                      "launch), same step count and graph replays as `value`"},
         "device": info,
     }
     del graph_full, graph_rem

@@ -262,6 +262,19 @@ def quantized_linear(rt: Runtime, x: Buffer, weight: Buffer, scale: Buffer,
     return Buffer(h)
 
 
+def quantized_linear_group(rt: Runtime, xs, weights, scales, outs):
+    """Independent W8A16 linears (BF16 compute) in one grouped launch per class
+    of rows: outs[i] receives quantized_linear(xs[i], weights[i], scales[i])
+    (rxw8_quantized_linear_group)."""
+    n = len(xs)
+    if not (len(weights) == len(scales) == len(outs) == n):
+        raise ValueError("quantized_linear_group: xs, weights, scales and outs differ in length")
+    arr = lambda bufs: (c_void_p * n)(*[b.handle for b in bufs])  # noqa: E731
+    _check(_lib.rxw8_quantized_linear_group(rt.handle, n, arr(xs), arr(weights), arr(scales),
+                                            arr(outs)))
+    return outs
+
+
 def linear_bf16(rt: Runtime, x: Buffer, weight: Buffer, out_dtype=DType.F32,
                 out: Buffer | None = None):
     if out is not None:

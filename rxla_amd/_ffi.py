@@ -22,7 +22,8 @@ EXPORTS = [
     "rxw8_buffer_copy_from_host", "rxw8_buffer_retain", "rxw8_buffer_release",
     "rxw8_buffer_dtype", "rxw8_buffer_dims", "rxw8_buffer_device_ptr",
     "rxw8_quantize_w8", "rxw8_dequantize", "rxw8_pack_weight", "rxw8_quantized_linear", "rxw8_quantized_linear_into",
-    "rxw8_linear_bf16", "rxw8_linear_bf16_into", "rxw8_gqa_decode", "rxw8_gqa_decode_into",
+    "rxw8_quantized_linear_group", "rxw8_linear_bf16", "rxw8_linear_bf16_into",
+    "rxw8_gqa_decode", "rxw8_gqa_decode_into",
     "rxw8_gqa_decode_noalloc", "rxw8_gqa_attention", "rxw8_gqa_attention_into",
     "rxw8_causal_attention_mask",
     "rxw8_gqa_prefill", "rxw8_gqa_prefill_into", "rxw8_kv_update_at", "rxw8_argmax",
@@ -86,6 +87,8 @@ def _declare(L):
         "rxw8_pack_weight": (c_int, [vp, vp, POINTER(vp)]),
         "rxw8_quantized_linear": (c_int, [vp, vp, vp, vp, c_int, c_int, POINTER(vp)]),
         "rxw8_quantized_linear_into": (c_int, [vp, vp, vp, vp, c_int, vp]),
+        "rxw8_quantized_linear_group": (c_int, [vp, c_int, POINTER(vp), POINTER(vp), POINTER(vp),
+                                                POINTER(vp)]),
         "rxw8_linear_bf16": (c_int, [vp, vp, vp, c_int, POINTER(vp)]),
         "rxw8_linear_bf16_into": (c_int, [vp, vp, vp, vp]),
         "rxw8_gqa_decode": (c_int, [vp, vp, vp, vp, vp, vp, c_float, c_int, POINTER(vp)]),

@@ -94,6 +94,26 @@ struct GemvArgs {
   int ss_ld;
 };
 
+// Grouped launch: several independent products, each with its own operands
+// and shape, in one grid; problem p owns workgroups [tile_begin, next
+// problem's tile_begin). Every problem runs the same tiling (the kernel's
+// template) with its own staging flags.
+struct GemvProblem {
+  const void *x;
+  const void *w;
+  const float *scale;
+  void *y;
+  int M, N, K, G;
+  int tile_begin;
+  int x_f32, y_f32, lds_dma, wave_stage;
+};
+constexpr int kGemvGroupMax = 16;
+struct GemvGroupArgs {
+  GemvArgs base;  // settings shared by every problem (plain rows, plain stores, no split)
+  int count;
+  GemvProblem p[kGemvGroupMax];
+};
+
 struct SplitkReduceArgs {
   const float *ws;    // [ksplit, M, N]
   const float *scale; // [N] per-channel scale or null
@@ -599,17 +619,19 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
 // sum_k bf16(x) * bf16(dequant(W)) in f32, with no all-ones correction and no
 // scale after the sum. Lane l's row n takes its scale from global memory once
 // (per-channel) or from the staged scale tile per 64-k chunk (grouped).
+// blk: the workgroup's tile (x split) index, blockIdx.x except in grouped
+// launches.
 template <int MB, int RW, int U, bool PK, int NW = 4, bool XG = false, bool RN = false,
           bool FC = false, bool RC = false>
-__device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
+__device__ __forceinline__ void gemv_w8(const GemvArgs &a, const int blk) {
   constexpr int LO = 8 * MB;  // FC: staged row of the lo part of row 0
   constexpr int KW = NW / RW;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int rg = wave % RW, kq = wave / RW;
-  const int tile = blockIdx.x / a.ksplit;
-  const int sp = blockIdx.x - tile * a.ksplit;
+  const int tile = blk / a.ksplit;
+  const int sp = blk - tile * a.ksplit;
   const int Kc = a.K / a.ksplit;
   const int k0 = sp * Kc;
   const int Kw = Kc / KW;                   // this wave's slice of the split
@@ -797,6 +819,31 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a) {
   finish_tile<MB, RW, NW, RN, FC>(a, (float *)xs, rows0, sp, total, per_channel && !RC);
 }
 
+// One workgroup of a grouped launch: find its problem (uniform scan of the
+// problem table), then run that problem's tile with the problem's operands.
+template <int RW, int U, bool PK, int NW, bool RC>
+__device__ __forceinline__ void gemv_group(const GemvGroupArgs &g) {
+  int p = 0;
+  while (p + 1 < g.count && (int)blockIdx.x >= g.p[p + 1].tile_begin) ++p;
+  const GemvProblem &q = g.p[p];
+  GemvArgs a = g.base;
+  a.x = q.x;
+  a.w = q.w;
+  a.scale = q.scale;
+  a.y = q.y;
+  a.M = q.M;
+  a.N = q.N;
+  a.K = q.K;
+  a.G = q.G;
+  a.x_f32 = q.x_f32;
+  a.y_f32 = q.y_f32;
+  a.lds_dma = q.lds_dma;
+  a.wave_stage = q.wave_stage;
+  a.x_stride = q.K;
+  a.ss_ld = q.M;
+  gemv_w8<1, RW, U, PK, NW, false, false, false, RC>(a, (int)blockIdx.x - q.tile_begin);
+}
+
 // Dense bf16 weights (lm_head): one 16-byte slice = one MFMA A-fragment.
 // PK: tiled layout [N/16][K/32][64 lanes][16 B], lane l holding
 // W[16t + l%16][32c + 8(l/16) .. +8] (rxw8_pack_bf16 builds it).
@@ -902,11 +949,11 @@ __device__ __forceinline__ void gemv_bf16(const GemvArgs &a) {
 #define RXW8_GEMV_W8(MB, RW, U)                                                 \
   extern "C" __global__ void __launch_bounds__(256)                             \
       RXW8_KN(w8_mb##MB##_rw##RW##_u##U)(GemvArgs a) {                          \
-    gemv_w8<MB, RW, U, false, 4, false, false, false, RXW8_RC>(a);              \
+    gemv_w8<MB, RW, U, false, 4, false, false, false, RXW8_RC>(a, blockIdx.x);              \
   }                                                                             \
   extern "C" __global__ void __launch_bounds__(256)                             \
       RXW8_KN(w8_pk_mb##MB##_rw##RW##_u##U)(GemvArgs a) {                       \
-    gemv_w8<MB, RW, U, true, 4, false, false, false, RXW8_RC>(a);               \
+    gemv_w8<MB, RW, U, true, 4, false, false, false, RXW8_RC>(a, blockIdx.x);               \
   }
 #define RXW8_GEMV_W8_U(MB, RW) \
   RXW8_GEMV_W8(MB, RW, 8)      \
@@ -918,11 +965,11 @@ __device__ __forceinline__ void gemv_bf16(const GemvArgs &a) {
 #define RXW8_GEMV_WIDE(MB, RW, U, NW)                                           \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       RXW8_KN(w8_mb##MB##_rw##RW##_u##U##_w##NW)(GemvArgs a) {                  \
-    gemv_w8<MB, RW, U, false, NW, false, false, false, RXW8_RC>(a);             \
+    gemv_w8<MB, RW, U, false, NW, false, false, false, RXW8_RC>(a, blockIdx.x);             \
   }                                                                             \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       RXW8_KN(w8_pk_mb##MB##_rw##RW##_u##U##_w##NW)(GemvArgs a) {               \
-    gemv_w8<MB, RW, U, true, NW, false, false, false, RXW8_RC>(a);              \
+    gemv_w8<MB, RW, U, true, NW, false, false, false, RXW8_RC>(a, blockIdx.x);              \
   }
 #define RXW8_GEMV_WIDE_U(MB, RW, NW) \
   RXW8_GEMV_WIDE(MB, RW, 4, NW)      \
@@ -937,11 +984,11 @@ __device__ __forceinline__ void gemv_bf16(const GemvArgs &a) {
 #define RXW8_GEMV_XG(RW, U, NW)                                                 \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       RXW8_KN(w8_mb1_rw##RW##_u##U##_w##NW##_xg)(GemvArgs a) {                  \
-    gemv_w8<1, RW, U, false, NW, true, false, false, RXW8_RC>(a);               \
+    gemv_w8<1, RW, U, false, NW, true, false, false, RXW8_RC>(a, blockIdx.x);               \
   }                                                                             \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_w##NW##_xg)(GemvArgs a) {               \
-    gemv_w8<1, RW, U, true, NW, true, false, false, RXW8_RC>(a);                \
+    gemv_w8<1, RW, U, true, NW, true, false, false, RXW8_RC>(a, blockIdx.x);                \
   }
 #define RXW8_GEMV_XG_U(RW, NW) \
   RXW8_GEMV_XG(RW, 4, NW)      \
@@ -977,12 +1024,12 @@ RXW8_GEMV_WIDE_U(2, 1, 14)
 #define RXW8_GEMV_XG_RN(RW, U, NW)                                              \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_w##NW##_xg_rn)(GemvArgs a) {            \
-    gemv_w8<1, RW, U, true, NW, true, true, false, RXW8_RC>(a);                 \
+    gemv_w8<1, RW, U, true, NW, true, true, false, RXW8_RC>(a, blockIdx.x);                 \
   }
 #define RXW8_GEMV_WIDE_RN(RW, U, NW)                                            \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_w##NW##_rn)(GemvArgs a) {               \
-    gemv_w8<1, RW, U, true, NW, false, true, false, RXW8_RC>(a);                \
+    gemv_w8<1, RW, U, true, NW, false, true, false, RXW8_RC>(a, blockIdx.x);                \
   }                                                                             \
   RXW8_GEMV_XG_RN(RW, U, NW)
 #define RXW8_GEMV_WIDE_RN_U(RW, NW) \
@@ -1003,7 +1050,7 @@ RXW8_GEMV_WIDE_RN_U(1, 14)
 #define RXW8_GEMV_RN4(RW, U)                                                    \
   extern "C" __global__ void __launch_bounds__(256)                             \
       RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_rn)(GemvArgs a) {                       \
-    gemv_w8<1, RW, U, true, 4, false, true, false, RXW8_RC>(a);                 \
+    gemv_w8<1, RW, U, true, 4, false, true, false, RXW8_RC>(a, blockIdx.x);                 \
   }
 #define RXW8_GEMV_RN4_U(RW) \
   RXW8_GEMV_RN4(RW, 8)      \
@@ -1021,6 +1068,25 @@ RXW8_GEMV_W8_U(1, 1)
 RXW8_GEMV_W8_U(1, 4)
 RXW8_GEMV_W8_U(2, 1)
 RXW8_GEMV_W8_U(2, 4)
+
+// Grouped launches (rxw8_quantized_linear_group): 12 waves, staged x, up to
+// 16 activation rows; RW = 3 (48-row tiles x 4 k slices) for up to 4 rows,
+// RW = 6 (96-row tiles x 2 k slices: x staged once per 96 weight rows) beyond.
+#define RXW8_GEMV_GRP(RW, U)                                                    \
+  extern "C" __global__ void __launch_bounds__(768)                             \
+      RXW8_KN(w8_mb1_rw##RW##_u##U##_w12_grp)(GemvGroupArgs g) {                \
+    gemv_group<RW, U, false, 12, RXW8_RC>(g);                                   \
+  }                                                                             \
+  extern "C" __global__ void __launch_bounds__(768)                             \
+      RXW8_KN(w8_pk_mb1_rw##RW##_u##U##_w12_grp)(GemvGroupArgs g) {             \
+    gemv_group<RW, U, true, 12, RXW8_RC>(g);                                    \
+  }
+RXW8_GEMV_GRP(3, 4)
+RXW8_GEMV_GRP(3, 2)
+RXW8_GEMV_GRP(3, 1)
+RXW8_GEMV_GRP(6, 4)
+RXW8_GEMV_GRP(6, 2)
+RXW8_GEMV_GRP(6, 1)
 
 #ifndef RXW8_GEMV_RC
 // Dense bf16 weights and the F32-compute kernels exist once (no RC form).
@@ -1061,7 +1127,7 @@ RXW8_GEMV_BF16_RN(4, 1)
 #define RXW8_GEMV_FC_WIDE(MB, RW, U, NW)                                        \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       rxw8_gemv_w8_pk_mb##MB##_rw##RW##_u##U##_w##NW##_fc(GemvArgs a) {         \
-    gemv_w8<MB, RW, U, true, NW, false, false, true>(a);                        \
+    gemv_w8<MB, RW, U, true, NW, false, false, true>(a, blockIdx.x);                        \
   }
 #define RXW8_GEMV_FC_WIDE_U(MB, RW, NW) \
   RXW8_GEMV_FC_WIDE(MB, RW, 4, NW)      \
@@ -1071,7 +1137,7 @@ RXW8_GEMV_BF16_RN(4, 1)
 #define RXW8_GEMV_FC4(MB, RW, U)                                                \
   extern "C" __global__ void __launch_bounds__(256)                             \
       rxw8_gemv_w8_pk_mb##MB##_rw##RW##_u##U##_fc(GemvArgs a) {                 \
-    gemv_w8<MB, RW, U, true, 4, false, false, true>(a);                         \
+    gemv_w8<MB, RW, U, true, 4, false, false, true>(a, blockIdx.x);                         \
   }
 #define RXW8_GEMV_FC_MB(MB)      \
   RXW8_GEMV_FC4(MB, 1, 8)        \

@@ -49,6 +49,23 @@ struct PackArgs {
   int64_t ilv_half;
 };
 
+// Grouped GEMV launch (matches kernels/w8a16_gemv.hip).
+struct GemvProblem {
+  const void *x;
+  const void *w;
+  const float *scale;
+  void *y;
+  int M, N, K, G;
+  int tile_begin;
+  int x_f32, y_f32, lds_dma, wave_stage;
+};
+constexpr int kGemvGroupMax = 16;
+struct GemvGroupArgs {
+  GemvArgs base;
+  int count;
+  GemvProblem p[kGemvGroupMax];
+};
+
 struct SplitkReduceArgs {
   const float *ws;
   const float *scale;
@@ -1247,6 +1264,93 @@ int rxw8_quantized_linear_into(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *we
   return qlinear_launch(rt, x->ptr, x->dtype == RXW8_F32, (const uint8_t *)weight->ptr,
                         weight->rank == 3, (const float *)scale->ptr, y->ptr,
                         y->dtype == RXW8_F32, M, N, K, G, compute_dtype == RXW8_BF16);
+}
+
+int rxw8_quantized_linear_group(rxw8_runtime *rt, int count, rxw8_buffer *const *x,
+                                rxw8_buffer *const *weight, rxw8_buffer *const *scale,
+                                rxw8_buffer *const *y) {
+  if (!rt || !x || !weight || !scale || !y) return fail(RXW8_INVALID_ARGUMENT, "NULL argument");
+  if (count < 1 || count > kGemvGroupMax)
+    return fail(RXW8_INVALID_ARGUMENT, "group of %d linears outside [1, %d]", count, kGemvGroupMax);
+  // Every product runs a 12-wave tiling with the whole K in one workgroup and
+  // staged activations: 3 row groups of 16 rows (48-row tiles) x 4 k slices
+  // for up to 4 rows; 6 row groups (96-row tiles) x 2 k slices beyond, where
+  // staging is paid once per 96 weight rows.
+  constexpr int kNw = 12;
+  auto rw_for = [](int64_t m) { return m > 4 ? 6 : 3; };
+  struct Item {
+    int64_t M, N, K, G;
+    size_t lds;
+    bool wave_stage;
+  } it[kGemvGroupMax];
+  bool packed = false;
+  for (int i = 0; i < count; ++i) {
+    if (!y[i]) return fail(RXW8_INVALID_ARGUMENT, "group linear %d: NULL output", i);
+    Item &t = it[i];
+    int rc = check_qlinear(x[i], weight[i], scale[i], RXW8_BF16, &t.M, &t.N, &t.K, &t.G);
+    if (rc) return fail(rc, "group linear %d: %s", i, std::string(rxw8_last_error()).c_str());
+    if (x[i]->rt != rt) return fail(RXW8_INVALID_ARGUMENT, "group linear %d: buffers of another runtime", i);
+    bool shape_ok = is_f(y[i]->dtype) && y[i]->rank == x[i]->rank && y[i]->dims[y[i]->rank - 1] == t.N;
+    for (int d = 0; shape_ok && d < x[i]->rank - 1; ++d) shape_ok = y[i]->dims[d] == x[i]->dims[d];
+    if (!shape_ok)
+      return fail(RXW8_INVALID_ARGUMENT, "group linear %d: output %s does not match", i,
+                  dims_str(y[i]).c_str());
+    if (i == 0) packed = weight[0]->rank == 3;
+    if ((weight[i]->rank == 3) != packed)
+      return fail(RXW8_INVALID_ARGUMENT, "group linears must all take packed or all row-major weights");
+    if (t.M < 1 || t.M > 16 || t.N % 16 || t.K % 512 || (t.G != t.K && (t.K / 4) % t.G))
+      return fail(RXW8_UNIMPLEMENTED,
+                  "group linear %d: needs 1..16 rows, N %% 16 == 0, K %% 512 == 0 and whole scale "
+                  "groups per quarter of K (M=%lld N=%lld K=%lld G=%lld)",
+                  i, (long long)t.M, (long long)t.N, (long long)t.K, (long long)t.G);
+    const int rw = rw_for(t.M);
+    t.wave_stage = gemv_wave_stage(t.M, t.K, t.G, rw, false);
+    t.lds = gemv_lds(t.M, t.K, t.K, t.G, rw, 1, false, kNw);
+    if (t.lds + 256 > rt->lds_max)
+      return fail(RXW8_UNIMPLEMENTED, "group linear %d: staged rows need %zu bytes of LDS", i, t.lds);
+  }
+  std::lock_guard<std::recursive_mutex> g(rt->mu);
+  const char *rc_env = std::getenv("RXW8_GEMV_REF_CAST");
+  const bool ref_cast = !(rc_env && *rc_env == '0');
+  // One launch per class of staged rows: up to 4 rows need at most 33 KB of
+  // LDS per workgroup (K = 4096), 16 rows 131 KB (one workgroup per CU); a
+  // launch's LDS is its largest problem's.
+  for (int cls = 0; cls < 2; ++cls) {
+    GemvGroupArgs a{};
+    a.base.ksplit = 1;
+    a.base.y_mode = 0;
+    a.base.x_mode = 0;
+    size_t lds = 0;
+    int tiles = 0, u = 4;
+    const int rw = cls == 1 ? 6 : 3;
+    for (int i = 0; i < count; ++i) {
+      if ((it[i].M > 4) != (cls == 1)) continue;
+      GemvProblem &q = a.p[a.count++];
+      q.x = x[i]->ptr;
+      q.w = weight[i]->ptr;
+      q.scale = (const float *)scale[i]->ptr;
+      q.y = y[i]->ptr;
+      q.M = (int)it[i].M;
+      q.N = (int)it[i].N;
+      q.K = (int)it[i].K;
+      q.G = (int)it[i].G;
+      q.tile_begin = tiles;
+      q.x_f32 = x[i]->dtype == RXW8_F32;
+      q.y_f32 = y[i]->dtype == RXW8_F32;
+      q.wave_stage = it[i].wave_stage;
+      q.lds_dma = !q.x_f32 && !q.wave_stage && (uintptr_t)q.x % 16 == 0;
+      tiles += (int)((it[i].N + 16 * rw - 1) / (16 * rw));
+      lds = std::max(lds, it[i].lds);
+      const int64_t chunks = it[i].K / (kNw / rw) / 64;
+      while (chunks % (2 * u)) u /= 2;
+    }
+    if (a.count == 0) continue;
+    char kname[64];
+    std::snprintf(kname, sizeof kname, "rxw8_gemv_%sw8%s_mb1_rw%d_u%d_w12_grp", ref_cast ? "rc_" : "",
+                  packed ? "_pk" : "", rw, u);
+    if (int rc = launch(rt, kname, dim3((unsigned)tiles), dim3(64 * kNw), a, lds)) return rc;
+  }
+  return RXW8_OK;
 }
 
 int rxw8_quantized_linear(rxw8_runtime *rt, rxw8_buffer *x, rxw8_buffer *weight,

@@ -382,3 +382,58 @@ def test_reference_cast_point_gemv(rt, monkeypatch, m, n, k, g, packed):
     np.testing.assert_array_equal(oracle.round_bf16(y_rc), y_rc)
     assert e_rc <= ELEM_TOL
     assert rel_err(y_rc, ref) <= rel_err(y_exact, ref)
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_quantized_linear_group_sweep(rt, packed):
+    """The nine decode shapes of BASELINE configs[1] (B 1/4/16 x N 4096/6144/
+    24576, K 4096) in one rxw8_quantized_linear_group call (two launches: up to
+    4 rows, 16 rows), plus a grouped-scale product with f32 input and output:
+    every output within one bf16 ulp of the reference-order oracle, and bit
+    for bit the single call's where that picks the same tiling (N 24576:
+    48-row tiles at B 1 and 4, 96-row tiles at B 16)."""
+    r = rx()
+    rng = np.random.default_rng(4096 + packed)
+    probs = [(b, n, 4096, 4096, r.DType.BF16) for n in (4096, 6144, 24576) for b in (1, 4, 16)]
+    probs.append((8, 1024, 2048, 128, r.DType.F32))
+    xs, ws, ss, ys, refs, singles = [], [], [], [], [], []
+    for b, n, k, g, dt in probs:
+        x = oracle.round_bf16(rng.standard_normal((b, k)).astype(np.float32))
+        u8, s = quantized(rng, n, k, g)
+        xb = rt.buffer(oracle.bf16_bits(x), r.DType.BF16) if dt == r.DType.BF16 else rt.buffer(x)
+        wb = rt.buffer(u8, r.DType.U8)
+        if packed:
+            wb = r.pack_weight(rt, wb)
+        sb = rt.buffer(s, r.DType.F32)
+        xs.append(xb), ws.append(wb), ss.append(sb)
+        ys.append(rt.buffer(np.full((b, n), np.nan, np.float32)))
+        refs.append(exact(x, u8, s))
+        singles.append(r.quantized_linear(rt, xb, wb, sb, r.DType.BF16, r.DType.F32).to_numpy())
+    r.quantized_linear_group(rt, xs, ws, ss, ys)
+    for (b, n, k, g, _), y, ref, single in zip(probs, ys, refs, singles):
+        got = y.to_numpy()
+        e = elem_rel_err(got, ref)
+        print(f"group B={b} N={n} K={k} G={g} packed={packed}: elem_rel_err {e:.3e}, "
+              f"equal to the single call {float(np.mean(got == single)):.4f}")
+        assert e <= ELEM_TOL
+        if n == 24576:
+            np.testing.assert_array_equal(got, single)
+
+
+def test_quantized_linear_group_validation(rt):
+    r = rx()
+    x = rt.buffer(np.zeros((4, 512), np.float32))
+    w = rt.buffer(np.full((32, 512), 128, np.uint8))
+    s = rt.buffer(np.ones((32, 1), np.float32))
+    y = rt.buffer(np.full((4, 32), 7.0, np.float32))
+    wp = r.pack_weight(rt, w)
+    x17 = rt.buffer(np.zeros((17, 512), np.float32))
+    y17 = rt.buffer(np.zeros((17, 32), np.float32))
+    for args, code in ((([x, x], [w, wp], [s, s], [y, y]), r.Status.INVALID_ARGUMENT),
+                       (([x17], [w], [s], [y17]), r.Status.UNIMPLEMENTED),
+                       (([x], [w], [s], [y17]), r.Status.INVALID_ARGUMENT)):
+        with pytest.raises(r.Error) as e:
+            r.quantized_linear_group(rt, *args)
+        assert e.value.code == code
+    rt.synchronize()
+    np.testing.assert_array_equal(y.to_numpy(), 7.0)
