@@ -512,9 +512,21 @@ __device__ __forceinline__ void finish_fc(const GemvArgs &a, int rows0, int rg, 
 // write the tile (ksplit == 1, scaled here when per-channel) or its partial.
 // With row_norm, every wave of the workgroup calls this after storing its
 // rows' factors in LDS (at rs_off); the first barrier here publishes them.
+// Residual operands of the epilogue (y_mode 1, one split) that the kernel
+// loaded at its start, beside its first weight group: row b = col + 16 mb's
+// values h[b, n .. n + 3] and the next norm's weights (with xw_out), so the
+// epilogue waits on no memory round trip of its own.
+template <int MB>
+struct ResidualPrefetch {
+  bool valid = false;
+  float4 h[MB];
+  float4 w;
+};
+
 template <int MB, int RW, int NW = 4, bool RN = false, bool FC = false>
 __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int rows0, int sp,
-                                            f32x4 (&total)[MB], bool scale_here) {
+                                            f32x4 (&total)[MB], bool scale_here,
+                                            const ResidualPrefetch<MB> *pre = nullptr) {
   constexpr int KW = NW / RW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -579,13 +591,16 @@ __device__ __forceinline__ void finish_tile(const GemvArgs &a, float *red, int r
     }
     return;
   }
-  const float4 xw_w = a.xw_out ? *(const float4 *)(a.xw_norm + n) : float4{0.f, 0.f, 0.f, 0.f};
+  const bool have_pre = pre && pre->valid;
+  const float4 xw_w = have_pre ? pre->w
+                      : a.xw_out ? *(const float4 *)(a.xw_norm + n) : float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int b = col + 16 * mb;
     float ss = b < a.M ? store_out(a.y, a.y_f32, a.y_mode, a.N, b, n, total[mb] * sc,
-                                   a.y_mode == 1 ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
-                                                 : float4{0.f, 0.f, 0.f, 0.f},
+                                   have_pre ? pre->h[mb]
+                                   : a.y_mode == 1 ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
+                                                   : float4{0.f, 0.f, 0.f, 0.f},
                                    a.xw_out, xw_w)
                        : 0.f;
     if (a.ss_out) {  // 4 lanes (j) hold the group's 16 channels of row b
@@ -686,6 +701,20 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a, const int blk) {
   };
   // The first weight group is in flight while x and the scales are staged.
   load_group(bufA, xgA, 0);
+  // Residual epilogue in this launch (the waves that run it): its h values
+  // and next-norm weights load now, with the first weights.
+  ResidualPrefetch<MB> pre;
+  if (!FC && a.y_mode == 1 && a.ksplit == 1 && kq == 0 && active) {
+    const int n = row0 + 4 * j;
+    pre.valid = true;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int b = col + 16 * mb;
+      pre.h[mb] = b < a.M ? *(const float4 *)((const float *)a.y + (int64_t)b * a.N + n)
+                          : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    pre.w = a.xw_out ? *(const float4 *)(a.xw_norm + n) : float4{0.f, 0.f, 0.f, 0.f};
+  }
   // row_norm: the partials arrive during the stream and are reduced after it
   // (KW > 1: finish_tile's first barrier publishes the factors)
   // (wave w: row w; rows past the wave count are loaded after the stream)
@@ -816,7 +845,7 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a, const int blk) {
       row_norm_store(a, b, rnv, xs);
     }
   }
-  finish_tile<MB, RW, NW, RN, FC>(a, (float *)xs, rows0, sp, total, per_channel && !RC);
+  finish_tile<MB, RW, NW, RN, FC>(a, (float *)xs, rows0, sp, total, per_channel && !RC, &pre);
 }
 
 // One workgroup of a grouped launch: find its problem (uniform scan of the

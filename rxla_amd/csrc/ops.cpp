@@ -407,22 +407,26 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
   plain.prefer_ks1 = wide_env >= 0 ? wide_env != 0
                                     : (!w_bf16 && (N / 64 >= rt->cus || (M >= 8 && N * K <= 17000000)));
   if (!pro) pro = &plain;
-  // activations as MFMA fragments from global memory (XG) pay off when the
-  // weights are small next to the staging each workgroup would do: up to 8
-  // rows and 17 MB of weights (measured: 8 x 4096 x 2048 5.6 -> 4.8 us;
-  // 25 MB and more, or 16 rows, stream slower because the fragment reads load
-  // L2). RXW8_GEMV_XG=0 / 1 forces it off / on (where it applies).
-  static const int xg_env = env_int("RXW8_GEMV_XG", -1);
-  const int xg_mode = xg_env >= 0 ? xg_env : (M <= 8 && N * K <= 17000000);
-  const int64_t mchunk = M <= 16 ? 16 : 32;
-  GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16, pro->prefer_ks1,
-                         pro->mode != 1);
-  if (p.ks == 0 || N % 4) return RXW8_UNIMPLEMENTED;
   // u8 weights enter the product at the reference's cast point, each weight
   // bf16((u - 128) * s) (the gemv_rc kernels); RXW8_GEMV_REF_CAST=0 selects
   // the exact codes u - 128 with the scale applied after the f32 sum instead
   const char *rc_env = std::getenv("RXW8_GEMV_REF_CAST");
   const bool ref_cast = !w_bf16 && !(rc_env && *rc_env == '0');
+  // Activations as MFMA fragments from global memory (XG) paid off for the
+  // exact-code kernels when the weights are small next to the staging each
+  // workgroup would do: up to 8 rows and 17 MB of weights (8 x 4096 x 2048
+  // 5.6 -> 4.8 us; 25 MB and more, or 16 rows, stream slower because the
+  // fragment reads load L2). With the reference cast point (16 more VALU ops
+  // per 16 bytes of weights) staged rows are faster from 8 rows on: the C5
+  // decode step's o_proj 4.84 -> 4.48 us, down 8.12 -> 7.32, QKV 5.96 ->
+  // 5.80; up to 4 rows XG still wins (4 x 4096 x 4096: 6.0 against 6.8 us).
+  // RXW8_GEMV_XG=0 / 1 forces it off / on (where it applies).
+  static const int xg_env = env_int("RXW8_GEMV_XG", -1);
+  const int xg_mode = xg_env >= 0 ? xg_env : (M <= (ref_cast ? 4 : 8) && N * K <= 17000000);
+  const int64_t mchunk = M <= 16 ? 16 : 32;
+  GemvPlan p = plan_gemv(rt, M < mchunk ? M : mchunk, N, K, G, w_bf16, pro->prefer_ks1,
+                         pro->mode != 1);
+  if (p.ks == 0 || N % 4) return RXW8_UNIMPLEMENTED;
   // the fused epilogues need the whole reduction in one launch and whole
   // 16-channel groups; one chunk of rows keeps the partial layout [g][M]
   if ((pro->swiglu || pro->ss_out) && (p.ks != 1 || N % 16 || M > mchunk)) return RXW8_UNIMPLEMENTED;
@@ -471,8 +475,9 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     const int mb = mm <= 16 ? 1 : 2;
     // bf16 activation rows with per-channel u8 weights: the variant that reads
     // them as MFMA fragments from global memory (no LDS staging)
+    // (XG kernels exist for every wide tiling but the 96-row one)
     const bool xg = xg_mode != 0 && pro->mode == 0 && !x_f32 && !w_bf16 && G == K && mb == 1 &&
-                    (p.nw != 4 || p.rw == 1 || p.rw == 4);
+                    (p.nw != 4 || p.rw == 1 || p.rw == 4) && p.rw != 6;
     const int u = xg && p.u > 4 ? 4 : p.u;
     char kname[64];
     char wide[12] = "";
