@@ -13,8 +13,8 @@ is served from the MALL and the figure is HBM bandwidth.
 
 value        = sweep algorithmic bytes / wall time of the timed steps (GB/s);
                each step is the 9 products in one rxw8_quantized_linear_group
-               call (two grouped launches: B 1 and 4, then B 16; every
-               product on the 12-wave 48-row tiling), replayed from HIP
+               call (two grouped launches: B 1 and 4 on 96-row tiles, then
+               B 16 on 192-row tiles), replayed from HIP
                graphs: one of 48 consecutive steps (every pool turns over a
                whole number of times in it) replayed K // 48 times, then one
                of the first K % 48 steps (a graph boundary idles the GPU for

@@ -170,14 +170,14 @@ int rxw8_quantized_linear_into(rxw8_runtime *rt, rxw8_buffer *x,
  * grouped launch (no counterpart in the reference, which compiles each linear
  * into its own XLA op): for i < count, y[i] = the product rxw8_quantized_linear_into
  * computes for (x[i], weight[i], scale[i]). One launch per class of rows
- * (<= 4: 48-row tiles; 5..16: 96-row tiles) runs every product of the class
+ * (<= 4: 96-row tiles; 5..16: 192-row tiles) runs every product of the class
  * on one tiling, so the per-launch cost is paid once per class instead of
  * once per product.
  * Requirements beyond rxw8_quantized_linear_into's: count in [1, 16];
  * 1..16 rows (the product of x's leading dims) per product; N % 16 == 0,
  * K % 512 == 0, per-channel scales or groups that divide K/4; all weights
  * row-major or all packed. Results agree with the single call within one
- * bf16 ulp (bit for bit where the single call picks the same tiling).
+ * bf16 ulp (the tilings, and so the f32 summation order, may differ).
  * INVALID_ARGUMENT / UNIMPLEMENTED before any launch. */
 int rxw8_quantized_linear_group(rxw8_runtime *rt, int count, rxw8_buffer *const *x,
                                 rxw8_buffer *const *weight, rxw8_buffer *const *scale,

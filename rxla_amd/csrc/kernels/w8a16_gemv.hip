@@ -1099,8 +1099,8 @@ RXW8_GEMV_W8_U(2, 1)
 RXW8_GEMV_W8_U(2, 4)
 
 // Grouped launches (rxw8_quantized_linear_group): 12 waves, staged x, up to
-// 16 activation rows; RW = 3 (48-row tiles x 4 k slices) for up to 4 rows,
-// RW = 6 (96-row tiles x 2 k slices: x staged once per 96 weight rows) beyond.
+// 16 activation rows, RW row groups of 16 rows x 12 / RW k slices (the host
+// picks 6 up to 4 rows, 12 beyond: x staged once per 96 / 192 weight rows).
 #define RXW8_GEMV_GRP(RW, U)                                                    \
   extern "C" __global__ void __launch_bounds__(768)                             \
       RXW8_KN(w8_mb1_rw##RW##_u##U##_w12_grp)(GemvGroupArgs g) {                \
@@ -1116,6 +1116,9 @@ RXW8_GEMV_GRP(3, 1)
 RXW8_GEMV_GRP(6, 4)
 RXW8_GEMV_GRP(6, 2)
 RXW8_GEMV_GRP(6, 1)
+RXW8_GEMV_GRP(12, 4)
+RXW8_GEMV_GRP(12, 2)
+RXW8_GEMV_GRP(12, 1)
 
 #ifndef RXW8_GEMV_RC
 // Dense bf16 weights and the F32-compute kernels exist once (no RC form).

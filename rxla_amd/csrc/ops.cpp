@@ -1278,11 +1278,21 @@ int rxw8_quantized_linear_group(rxw8_runtime *rt, int count, rxw8_buffer *const 
   if (count < 1 || count > kGemvGroupMax)
     return fail(RXW8_INVALID_ARGUMENT, "group of %d linears outside [1, %d]", count, kGemvGroupMax);
   // Every product runs a 12-wave tiling with the whole K in one workgroup and
-  // staged activations: 3 row groups of 16 rows (48-row tiles) x 4 k slices
-  // for up to 4 rows; 6 row groups (96-row tiles) x 2 k slices beyond, where
-  // staging is paid once per 96 weight rows.
+  // staged activations: up to 4 rows, 6 row groups of 16 rows (96-row tiles)
+  // x 2 k slices; beyond, 12 row groups (192-row tiles), each wave the whole
+  // K of its 16 rows. The 5-16-row class holds one workgroup per CU (131 KB
+  // of staged rows at K = 4096): 192-row tiles fit the sweep's B = 16 shapes
+  // in one round (182 workgroups) where 96-row tiles take 1.4 (sweep 4.80 ->
+  // 5.00 TB/s); up to 4 rows, 96-row tiles measured 2% above 48-row ones and
+  // 4% above 192-row ones. RXW8_GEMV_GRP_RW_FEW / _RW override (3, 6 or 12).
   constexpr int kNw = 12;
-  auto rw_for = [](int64_t m) { return m > 4 ? 6 : 3; };
+  auto rw_env = [](const char *name, int dflt) {
+    const int v = env_int(name, dflt);
+    return v == 3 || v == 6 || v == 12 ? v : dflt;
+  };
+  static const int rw_many = rw_env("RXW8_GEMV_GRP_RW", 12);
+  static const int rw_few = rw_env("RXW8_GEMV_GRP_RW_FEW", 6);
+  auto rw_for = [](int64_t m) { return m > 4 ? rw_many : rw_few; };
   struct Item {
     int64_t M, N, K, G;
     size_t lds;
@@ -1318,8 +1328,8 @@ int rxw8_quantized_linear_group(rxw8_runtime *rt, int count, rxw8_buffer *const 
   const char *rc_env = std::getenv("RXW8_GEMV_REF_CAST");
   const bool ref_cast = !(rc_env && *rc_env == '0');
   // One launch per class of staged rows: up to 4 rows need at most 33 KB of
-  // LDS per workgroup (K = 4096), 16 rows 131 KB (one workgroup per CU); a
-  // launch's LDS is its largest problem's.
+  // LDS per workgroup (K = 4096), 16 rows 131 KB; a launch's LDS is its
+  // largest problem's.
   for (int cls = 0; cls < 2; ++cls) {
     GemvGroupArgs a{};
     a.base.ksplit = 1;
@@ -1327,7 +1337,7 @@ int rxw8_quantized_linear_group(rxw8_runtime *rt, int count, rxw8_buffer *const 
     a.base.x_mode = 0;
     size_t lds = 0;
     int tiles = 0, u = 4;
-    const int rw = cls == 1 ? 6 : 3;
+    const int rw = cls == 1 ? rw_many : rw_few;
     for (int i = 0; i < count; ++i) {
       if ((it[i].M > 4) != (cls == 1)) continue;
       GemvProblem &q = a.p[a.count++];

@@ -389,9 +389,9 @@ def test_quantized_linear_group_sweep(rt, packed):
     """The nine decode shapes of BASELINE configs[1] (B 1/4/16 x N 4096/6144/
     24576, K 4096) in one rxw8_quantized_linear_group call (two launches: up to
     4 rows, 16 rows), plus a grouped-scale product with f32 input and output:
-    every output within one bf16 ulp of the reference-order oracle, and bit
-    for bit the single call's where that picks the same tiling (N 24576:
-    48-row tiles at B 1 and 4, 96-row tiles at B 16)."""
+    every output within one bf16 ulp of the reference-order oracle and of
+    the single call (the grouped launch runs its own tilings, 96-row tiles up
+    to 4 rows and 192-row tiles beyond, so summation order may differ)."""
     r = rx()
     rng = np.random.default_rng(4096 + packed)
     probs = [(b, n, 4096, 4096, r.DType.BF16) for n in (4096, 6144, 24576) for b in (1, 4, 16)]
@@ -416,8 +416,7 @@ def test_quantized_linear_group_sweep(rt, packed):
         print(f"group B={b} N={n} K={k} G={g} packed={packed}: elem_rel_err {e:.3e}, "
               f"equal to the single call {float(np.mean(got == single)):.4f}")
         assert e <= ELEM_TOL
-        if n == 24576:
-            np.testing.assert_array_equal(got, single)
+        assert elem_rel_err(got, single) <= ELEM_TOL
 
 
 def test_quantized_linear_group_validation(rt):
