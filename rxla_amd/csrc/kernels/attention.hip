@@ -629,13 +629,20 @@ __device__ void attn_pass(const AttnArgs &a) {
 
 }  // namespace
 
+// NP = 8 waves per workgroup (512 threads) for G <= 4. G = 8 holds 64 f32
+// P.V accumulators per lane: at 8 waves (2 per SIMD, at most 256 registers)
+// it spilled 116 / 276 bytes per lane to scratch, so it runs 4 waves (256
+// threads, one per SIMD), which keeps the overflow in AGPRs: 78.0 -> 60.2 us
+// for B 8, 64 / 8 heads, lengths 512-8192.
+#define RXW8_ATTN_NP(G) ((G) == 8 ? 4 : 8)
 #define RXW8_ATTN(G)                                                                 \
-  extern "C" __global__ void __launch_bounds__(512) rxw8_gqa_decode_d128_g##G(AttnArgs a) { \
-    attn_pass<G, 8, false>(a);                                                       \
+  extern "C" __global__ void __launch_bounds__(RXW8_ATTN_NP(G) * 64)                 \
+      rxw8_gqa_decode_d128_g##G(AttnArgs a) {                                        \
+    attn_pass<G, RXW8_ATTN_NP(G), false>(a);                                         \
   }                                                                                  \
-  extern "C" __global__ void __launch_bounds__(512)                                  \
+  extern "C" __global__ void __launch_bounds__(RXW8_ATTN_NP(G) * 64)                 \
       rxw8_gqa_decode_rope_d128_g##G(AttnArgs a) {                                   \
-    attn_pass<G, 8, true>(a);                                                        \
+    attn_pass<G, RXW8_ATTN_NP(G), true>(a);                                          \
   }                                                                                  \
   extern "C" __global__ void __launch_bounds__(256)                                  \
       rxw8_gqa_decode_combine_d128_g##G(AttnArgs a) {                                \

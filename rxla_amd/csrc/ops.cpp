@@ -1008,10 +1008,12 @@ int attention_launch(Runtime *rt, const void *q, int q_f32, const void *kc, cons
     a.counters = max_chunks > 1 && !two_pass ? ws_counters : nullptr;
     a.units = (int)units;
     char kname[64];
+    // G = 8 runs 4-wave workgroups (no register spills); the others 8 waves
+    const unsigned threads = G == 8 ? 256 : 512;
     std::snprintf(kname, sizeof kname, rope ? "rxw8_gqa_decode_rope_d128_g%d" : "rxw8_gqa_decode_d128_g%d",
                   (int)G);
     const int64_t grid = units > 0 ? Hkv * units : R * Hkv * max_chunks;
-    int rc = launch(rt, kname, dim3((unsigned)grid), dim3(512), a);
+    int rc = launch(rt, kname, dim3((unsigned)grid), dim3(threads), a);
     if (rc || max_chunks == 1 || a.counters) return rc;
     std::snprintf(kname, sizeof kname, "rxw8_gqa_decode_combine_d128_g%d", (int)G);
     return launch(rt, kname, dim3((unsigned)(R * Hkv)), dim3(256), a);
