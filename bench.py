@@ -472,6 +472,59 @@ def qwen35_weights(rt, rx, torch, stream, model, group, seed=7):
     return keep
 
 
+def bench_f32_linear(rt, rx, torch, stream, reps=10, n=248320, k=1024, g=128):
+    """The F32-compute W8 linear (rxw8_linear_f32_mfma_*: f32 x split into bf16
+    hi + lo, exact codes, f32 results), the Qwen3.5 default compute, at its
+    largest product, the tied LM head W [248320, 1024] U8 with G = 128
+    scales: S = 16 rows is bound by the weight stream (bytes N K + 4 N K / G
+    + 4 S K + 4 S N), S = 1024 by the matrix cores (2 S N K flops; the hi / lo
+    parts make the MFMA work twice that). Two weight copies (254 MB each)
+    alternate so neither is read from the MALL; HIP events around `reps`
+    back-to-back calls after a spin kernel."""
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    ws = [c5_quantized(rt, rx, torch, stream, gen, n, k, group=g) for _ in range(2)]
+    out = {}
+    for S in (16, 1024):
+        with torch.cuda.stream(stream):
+            x = torch.randn((S, k), device="cuda", generator=gen)
+            y = torch.empty((S, n), dtype=torch.float32, device="cuda")
+        stream.synchronize()
+        xb, yb = rt.wrap_tensor(x), rt.wrap_tensor(y)
+        for i in range(4):
+            rx.quantized_linear(rt, xb, ws[i % 2][0], ws[i % 2][1], rx.DType.F32, out=yb)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(SPIN_CYCLES)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            rx.quantized_linear(rt, xb, ws[i % 2][0], ws[i % 2][1], rx.DType.F32, out=yb)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / reps
+        if S == 16:
+            nbytes = n * k + 4 * n * (k // g) + 4 * S * k + 4 * S * n
+            gbs = nbytes / sec / 1e9
+            out[f"S{S}"] = {"bound": "hbm", "us": round(sec * 1e6, 2), "achieved": round(gbs, 1),
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                            "bytes": nbytes}
+        else:
+            tf = 2.0 * S * n * k / sec / 1e12
+            out[f"S{S}"] = {"bound": "mfma", "us": round(sec * 1e6, 2), "achieved": round(tf, 1),
+                            "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                            "mfma_frac": round(2 * tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                            "flops": 2 * S * n * k}
+        del x, y
+    del ws
+    return {"kernel": "rxw8_linear_f32_mfma_r1_w8 (S 16) / _r2_w8 (S 1024)",
+            "shape": f"W [{n}, {k}] U8, G {g} (the Qwen3.5-0.8B tied LM head), x F32 [S, {k}]",
+            "runs": out,
+            "note": "mfma_frac counts the hi and lo MFMAs (twice the algorithmic flops)",
+            "timing": f"HIP events around {reps} back-to-back calls over 2 alternating weight "
+                      "copies after a spin kernel"}
+
+
 # The reference's own published W8 runs of this workload (RTX 5080, JAX CUDA 13
 # PJRT plugin; docs/QWEN3.5-BENCHMARK.md:68-80): mean ms per run by sequence.
 QWEN35_REFERENCE_MS = {1: 2.393, 16: 10.535}
@@ -894,6 +947,9 @@ def main():
         out["decoder"] = bench_decoder(rt, rx, torch, stream)
         log(json.dumps(out["decoder"]))
     if not args.skip_qwen35:
+        log("F32-compute W8 linear at the Qwen3.5 LM head ...")
+        out["roofline_f32_linear"] = bench_f32_linear(rt, rx, torch, stream)
+        log(json.dumps(out["roofline_f32_linear"]))
         log("Qwen3.5-0.8B topology, full-sequence logits ...")
         out["qwen35"] = bench_qwen35(rt, rx, torch, stream)
         log(json.dumps(out["qwen35"]))
