@@ -21,8 +21,8 @@ value        = sweep algorithmic bytes / wall time of the timed steps (GB/s);
                ~8 us); single_launches times the same steps as 9
                rxw8_quantized_linear_into calls (the per-shape plans)
 roofline     = the GEMV kernel of the largest sweep shape, B=1 N=24576
-               (rxw8_gemv_rc_w8_pk_mb1_rw3_u4_w12: 12 waves, 48-row tiles, 512
-               workgroups = 2 whole rounds): algorithmic bytes per launch /
+               (rxw8_gemv_rc_w8_pk_mb1_rw1_u4: 4 waves splitting K, 16-row
+               tiles, 1536 workgroups): algorithmic bytes per launch /
                launch duration, from HIP events on the runtime's stream around
                runs of back-to-back launches of the shape; traffic = the HBM
                bytes per launch recorded in profiles/ by two rocprofv3 --pmc
@@ -893,7 +893,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": recorded_traffic(),
-                     "kernel": "rxw8_gemv_rc_w8_pk_mb1_rw3_u4_w12",
+                     "kernel": "rxw8_gemv_rc_w8_pk_mb1_rw1_u4",
                      "shape": "B=1 N=24576 K=4096", "launch_us": round(roof_s * 1e6, 3),
                      "launch_bytes": roof_bytes,
                      "timing": "median of HIP event pairs on the runtime stream around "

@@ -398,20 +398,26 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
                     bool packed, const float *scale, void *y, int y_f32, int64_t M, int64_t N,
                     int64_t K, int64_t G, int y_mode = 0, const GemvOptions *pro = nullptr) {
   // Plain calls take the wide single-launch tilings when even 64-row tiles
-  // give every CU a workgroup (e.g. N = 24576): x is then staged once per 64
-  // rows and no split-K reduce runs; so do 8 or more rows over at most 17 MB
-  // of weights (one launch beats a split plus its reduce there). Other shapes
-  // keep the 4-wave plans, which fill the CUs with more, narrower tiles.
-  GemvOptions plain;
-  const int wide_env = env_int("RXW8_GEMV_PREFER_WIDE", -1);
-  plain.prefer_ks1 = wide_env >= 0 ? wide_env != 0
-                                    : (!w_bf16 && (N / 64 >= rt->cus || (M >= 8 && N * K <= 17000000)));
-  if (!pro) pro = &plain;
+  // give every CU a workgroup (e.g. N = 24576) and there are several rows: x
+  // is then staged once per 64 rows and no split-K reduce runs; so do 8 or
+  // more rows over at most 17 MB of weights (one launch beats a split plus
+  // its reduce there). Other shapes keep the 4-wave plans, which fill the CUs
+  // with more, narrower tiles.
   // u8 weights enter the product at the reference's cast point, each weight
   // bf16((u - 128) * s) (the gemv_rc kernels); RXW8_GEMV_REF_CAST=0 selects
   // the exact codes u - 128 with the scale applied after the f32 sum instead
   const char *rc_env = std::getenv("RXW8_GEMV_REF_CAST");
   const bool ref_cast = !w_bf16 && !(rc_env && *rc_env == '0');
+  // (one row at the reference's cast point: the 4-wave plan, 1536 workgroups
+  // of 16 rows for N = 24576, streams faster than the wide tiles, 18.4
+  // against 18.8 us; from 4 rows on the wide tiles win)
+  GemvOptions plain;
+  const int wide_env = env_int("RXW8_GEMV_PREFER_WIDE", -1);
+  plain.prefer_ks1 =
+      wide_env >= 0 ? wide_env != 0
+                    : (!w_bf16 && ((N / 64 >= rt->cus && !(ref_cast && M == 1)) ||
+                                   (M >= 8 && N * K <= 17000000)));
+  if (!pro) pro = &plain;
   // Activations as MFMA fragments from global memory (XG) paid off for the
   // exact-code kernels when the weights are small next to the staging each
   // workgroup would do: up to 8 rows and 17 MB of weights (8 x 4096 x 2048

@@ -159,12 +159,15 @@ def test_decoder_c5_widths_match_oracle(rt, inter):
         assert e_elem <= ELEM_TOL
 
 
+@pytest.mark.parametrize("max_seq", [1100, 2200])
 @pytest.mark.parametrize("qk_norm", [True, False])
-def test_decode_fused_rope_matches_separate_kernel(rt, monkeypatch, qk_norm):
+def test_decode_fused_rope_matches_separate_kernel(rt, monkeypatch, qk_norm, max_seq):
     """Decode steps fold q/k norm + RoPE + the KV append into the attention
     launch; the separate RoPE/KV kernel (RXW8_DEC_UNFUSED_ROPE=1) must give
-    the same logits, caches and next ids, across splits of several sizes."""
-    cfg = small_cfg(max_seq=1100, qk_norm=qk_norm)
+    the same logits, caches and next ids, across splits of several sizes.
+    max_seq 2200 (Lmax >= 2048) takes the length-proportional split plan,
+    whose last workgroup of each row appends that row's new key."""
+    cfg = small_cfg(max_seq=max_seq, qk_norm=qk_norm)
     params = tiny_params(cfg, seed=95, std=0.05)
     batch = 3
     rng = np.random.default_rng(96)
