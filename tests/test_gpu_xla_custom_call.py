@@ -82,6 +82,8 @@ def test_bad_backend_config_launches_nothing(rt, opaque):
     assert "backend_config" in r._lib.rxw8_last_error().decode()
 
 
+# the refused call records nothing, so torch reports the captured graph as empty
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
 def test_each_stream_has_its_own_workspaces_and_none_grows_in_a_capture(rt):
     """The handlers keep one runtime per stream XLA passes. A call whose split
     workspace would have to grow while its stream is being captured (an XLA
