@@ -583,7 +583,8 @@ def pmc_probe(kind, rounds=3):
     sweep: 2 x 48 whole steps of the sweep, eager, with the bench's copy
     rotation (counters summed over a step's 9 launches); attention:
     `rounds` x [spin spacer, 20 C4 calls over the rotating caches]; gemm: 30
-    launches of the C3 roofline shape; decoder: the C5 leg with 16 decode
+    launches of the C3 roofline shape; gemm_all: 20 launches of each of the
+    six C3 shapes; decoder: the C5 leg with 16 decode
     steps; prefill: the prefill-attention leg) plus 4 plain 256 MiB device
     copies (torch) that calibrate what FETCH_SIZE / WRITE_SIZE read for a
     known number of bytes."""
@@ -635,6 +636,24 @@ def pmc_probe(kind, rounds=3):
         for _ in range(30):
             rx.quantized_linear(rt, xb, ub, sb, rx.DType.BF16, out=yb)
         log(f"pmc probe gemm M={m} N={n} K={K}: 30 launches")
+    elif kind == "gemm_all":  # every C3 shape, 20 launches each, in the order of bench_gemm
+        ws = {}
+        for n_, k_ in ((12288, 4096), (4096, 12288)):
+            u, sb = c5_quantized(rt, rx, torch, stream, gen, n_, k_)
+            ws[(n_, k_)] = (rx.pack_weight(rt, u), sb)
+        rt.synchronize()
+        for m in (512, 2048, 8192):
+            for (n_, k_), (ub, sb) in ws.items():
+                with torch.cuda.stream(stream):
+                    x = torch.randn((m, k_), device="cuda", generator=gen).to(torch.bfloat16)
+                    y = torch.empty((m, n_), dtype=torch.bfloat16, device="cuda")
+                stream.synchronize()
+                xb, yb = rt.wrap_tensor(x), rt.wrap_tensor(y)
+                for _ in range(20):
+                    rx.quantized_linear(rt, xb, ub, sb, rx.DType.BF16, out=yb)
+                rt.synchronize()
+                log(f"pmc probe gemm_all M={m} N={n_} K={k_}: 20 launches")
+                del x, y
     elif kind == "attention":  # C4, as bench_attention times it
         B, HQ, HKV, D, LMAX = 8, 32, 8, 128, 8192
         lens = np.random.default_rng(4).integers(512, 8193, B).astype(np.int32)
@@ -682,7 +701,7 @@ def main():
     ap.add_argument("--skip-attention", action="store_true")
     ap.add_argument("--skip-decoder", action="store_true")
     ap.add_argument("--skip-qwen35", action="store_true")
-    ap.add_argument("--pmc-probe", choices=["gemv", "gemv16", "sweep", "gemm", "attention", "decoder",
+    ap.add_argument("--pmc-probe", choices=["gemv", "gemv16", "sweep", "gemm", "gemm_all", "attention", "decoder",
                                             "prefill"],
                     help="counter-collection program only")
     ap.add_argument("--qwen35-only", action="store_true",
