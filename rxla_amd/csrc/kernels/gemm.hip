@@ -621,6 +621,188 @@ __device__ __forceinline__ void gemm_tile_bf16w(const GemmArgs &a) {
       gemm_store(a, m0 + wm * 64 + 16 * j + r16, n0 + wn * 128 + 16 * i + 4 * kg, acc[i][j]);
 }
 
+// ---- W8 linear with compute dtype F32 for long inputs (Qwen3.5 prefill,
+// the tied LM head; layers.rs:277-298 with an f32 compute dtype):
+//   y[m, n] = sum_g s[n, g] * sum_{k in g} (xh[m, k] + xl[m, k]) * (u8[n, k] - 128)
+// with x = xh + xl + r split into bf16 parts (rxw8_gemm_split_x; |r| <= 2^-17
+// |x|) and the codes u - 128 exact in bf16, so every MFMA product is exact and
+// accumulates in f32; each scale group's f32 sum is then scaled into the
+// total, the arithmetic of rxw8_linear_f32_mfma (a reassociation of the
+// reference's x . (q s): both are f32 sums of the same terms).
+//
+// 256 (weight rows n) x 128 (activation rows m) output tiles, 8 waves of 64 x
+// 64 (4 along n, 2 along m), k tiles of 64 in two LDS stages of [bf16 codes
+// 256 x 64 | xh 128 x 64 | xl 128 x 64]. The codes go global -> VGPRs ->
+// (u - 128 as bf16) -> LDS once per workgroup, loaded a tile ahead; xh / xl
+// go global -> LDS by LDS DMA, a tile ahead. The tile's scales sit in LDS as
+// [group][256 rows] (K / G <= 32). Per k tile a wave issues 64 MFMAs (hi and
+// lo for each of its 4 x 4 fragment pairs and both k halves), so the weights
+// are read once per 128 rows of x instead of once per 32.
+struct LinearF32GemmArgs {
+  const uint16_t *xh, *xl;  // [M, K] bf16 hi / lo parts of x
+  const uint8_t *w;         // [N, K] u8 codes, or packed [N/16, K/64, 1024]
+  const float *scale;       // [N, K / G]
+  float *y;                 // [M, N]
+  int M, N, K, G;
+  int y_mode;               // 0: y = result; 1: y += result
+  int w_packed;
+};
+
+__device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a) {
+  constexpr int TNB = 256, TMB = 128;
+  constexpr int W_BYTES = TNB * BK * 2, X_BYTES = TMB * BK * 2;
+  constexpr int STAGE = W_BYTES + 2 * X_BYTES;  // 64 KiB
+  constexpr int XDMA = X_BYTES / 1024 / 8;       // 2 LDS-DMA instructions per wave per part
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 3, wm = wave >> 2;
+
+  const int tiles_m = (a.M + TMB - 1) / TMB, tiles_n = (a.N + TNB - 1) / TNB;
+  const int ntiles = tiles_m * tiles_n;
+  const int per_xcd = (ntiles + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t >= ntiles) return;
+  constexpr int GN = 4;  // n tiles per tile-order group
+  const int group = t / (GN * tiles_m);
+  const int first_n = group * GN;
+  const int gw = min(GN, tiles_n - first_n);
+  const int r = t - group * GN * tiles_m;
+  const int n0 = (first_n + r % gw) * TNB, m0 = (r / gw) * TMB;
+  const int KT = a.K / BK, ng = a.K / a.G, tpg = a.G / BK;  // k tiles per scale group
+
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+  __shared__ float sc[32 * TNB];  // [group][row]
+
+  // rows past N (the last n tile of N % 256 == 128) repeat row N - 1 and are not stored
+  for (int e = tid; e < ng * TNB; e += 512) {
+    const int g = e / TNB, row = e - g * TNB;
+    sc[e] = a.scale[(int64_t)min(n0 + row, a.N - 1) * ng + g];
+  }
+  // activation DMA: instruction i of this wave fills rows 8 (2 wave + i) .. + 8
+  uint32_t xoff[XDMA];
+#pragma unroll
+  for (int i = 0; i < XDMA; ++i) {
+    const int row = (wave * XDMA + i) * 8 + (lane >> 3);
+    const int m = min(m0 + row, a.M - 1);  // rows past M repeat the last row (not stored)
+    xoff[i] = (uint32_t)m * (uint32_t)a.K * 2u + ((uint32_t)((lane & 7) ^ (row & 7)) << 4);
+  }
+  auto issue_x = [&](int kt, int stage) {
+#pragma unroll
+    for (int i = 0; i < XDMA; ++i) {
+      const uint32_t l = lds_addr(smem + stage * STAGE + W_BYTES + (wave * XDMA + i) * 1024);
+      dma16(a.xh, xoff[i] + (uint32_t)(kt * (BK * 2)), l);
+      dma16(a.xl, xoff[i] + (uint32_t)(kt * (BK * 2)), l + X_BYTES);
+    }
+  };
+  // codes: 1024 slices of 16 per k tile, 2 per thread (row = id / 4, kq = id % 4)
+  const int kstride = a.w_packed ? 1024 : BK;
+  uint32_t woff[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int id = tid + 512 * p, row = id >> 2, kq = id & 3;
+    const int n = min(n0 + row, a.N - 1);
+    woff[p] = a.w_packed ? ((uint32_t)(n >> 4) * (uint32_t)KT * 1024u + (uint32_t)((n & 15) + 16 * kq) * 16u)
+                         : (uint32_t)n * (uint32_t)a.K + (uint32_t)kq * 16u;
+  }
+  u32x4 wr[2];
+  auto load_w = [&](int kt) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) wr[p] = *(const u32x4 *)(a.w + woff[p] + (uint32_t)(kt * kstride));
+  };
+  auto store_w = [&](int stage) {  // u - 128, exact in bf16
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int id = tid + 512 * p, row = id >> 2, kq = id & 3;
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t q = wr[p][e];
+        h[2 * e] = pack_bf16x2((float)(q & 0xffu) - 128.f, (float)((q >> 8) & 0xffu) - 128.f);
+        h[2 * e + 1] = pack_bf16x2((float)((q >> 16) & 0xffu) - 128.f, (float)(q >> 24) - 128.f);
+      }
+      char *dst = smem + stage * STAGE;
+      *(u32x4 *)(dst + swz(row, 2 * kq)) = u32x4{h[0], h[1], h[2], h[3]};
+      *(u32x4 *)(dst + swz(row, 2 * kq + 1)) = u32x4{h[4], h[5], h[6], h[7]};
+    }
+  };
+
+  f32x4 acc[4][4], tot[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      tot[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  const int r16 = lane & 15, kg = lane >> 4;
+
+  load_w(0);
+  issue_x(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  store_w(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1, nxt = cur ^ 1;
+    const bool more = kt + 1 < KT;  // uniform
+    if (more) {
+      load_w(kt + 1);     // 2 loads, then 4 DMAs: vmcnt(4) waits for the loads alone
+      issue_x(kt + 1, nxt);
+    }
+    const char *st = smem + cur * STAGE;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 fa[4], fh[4], fl[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        fa[i] = as_bf16x8(*(const u32x4 *)(st + swz(wn * 64 + 16 * i + r16, ks * 4 + kg)));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        fh[j] = as_bf16x8(*(const u32x4 *)(st + W_BYTES + swz(wm * 64 + 16 * j + r16, ks * 4 + kg)));
+        fl[j] = as_bf16x8(*(const u32x4 *)(st + W_BYTES + X_BYTES + swz(wm * 64 + 16 * j + r16, ks * 4 + kg)));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[i][j] = mfma16x16x32(fa[i], fh[j], acc[i][j]);
+          acc[i][j] = mfma16x16x32(fa[i], fl[j], acc[i][j]);
+        }
+    }
+    if ((kt + 1) % tpg == 0) {  // the end of a scale group: tot += s[n, g] * acc
+      const int g = kt / tpg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 sv = *(const f32x4 *)(sc + g * TNB + wn * 64 + 16 * i + 4 * kg);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          tot[i][j] += sv * acc[i][j];
+          acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+    if (more) {
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      store_w(nxt);  // stage nxt was last read in step kt - 1, before the barrier
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+
+  // lane holds D[n = 16 i + 4 kg + e][m = 16 j + r16]
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = m0 + wm * 64 + 16 * j + r16;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = n0 + wn * 64 + 16 * i + 4 * kg;
+      if (n >= a.N) continue;  // (N % 128 == 0: a lane's 4 channels are all in or all out)
+      f32x4 *yp = (f32x4 *)(a.y + (int64_t)m * a.N + n);
+      *yp = a.y_mode == 1 ? *yp + tot[i][j] : tot[i][j];
+    }
+  }
+}
+
 }  // namespace
 
 // Exact dequantisation into a bf16 [N, K] row-major workspace, the input of
@@ -700,4 +882,28 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemm_cast_x(CastArgs a) {
   const int64_t tail = a.n - 4 * n4;
   if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail)
     a.y[4 * n4 + threadIdx.x] = f32_to_bf16_bits(a.x[4 * n4 + threadIdx.x]);
+}
+
+// Launch contract (checked by the host): N % 128 == 0, K % 64 == 0, G % 64
+// == 0, K % G == 0, K / G <= 32, M >= 1, M * K * 2 < 2^31, N * K < 2^32;
+// grid = 8 * ceil(tiles / 8) workgroups of 512 threads.
+extern "C" __global__ void __launch_bounds__(512) rxw8_gemm_f32c(LinearF32GemmArgs a) {
+  linear_f32_gemm_tile(a);
+}
+
+// f32 rows -> their bf16 parts hi = bf16(x), lo = bf16(x - hi) (RNE both), the
+// operand split of rxw8_gemm_f32c.
+struct SplitXArgs {
+  const float *x;
+  uint16_t *hi, *lo;
+  int64_t n;
+};
+extern "C" __global__ void __launch_bounds__(256) rxw8_gemm_split_x(SplitXArgs a) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = a.x[i];
+    const uint16_t h = f32_to_bf16_bits(v);
+    a.hi[i] = h;
+    a.lo[i] = f32_to_bf16_bits(v - bf16_bits_to_f32(h));
+  }
 }

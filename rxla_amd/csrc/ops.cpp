@@ -635,12 +635,55 @@ static int run_generic_linear(Runtime *rt, const void *x, int x_f32, const void 
   return launch(rt, "rxw8_linear_generic", dim3(grid_for(M * N)), dim3(256), a);
 }
 
+struct LinearF32GemmArgs {
+  const uint16_t *xh, *xl;
+  const uint8_t *w;
+  const float *scale;
+  float *y;
+  int M, N, K, G;
+  int y_mode, w_packed;
+};
+struct SplitXArgs {
+  const float *x;
+  uint16_t *hi, *lo;
+  int64_t n;
+};
+
+// F32-compute W8 linear for long inputs on the GEMM tiles
+// (rxw8_gemm_f32c): x split into bf16 hi / lo parts in the runtime's
+// staging buffer, then 256 x 128 output tiles that read each weight tile
+// once per 128 rows of x. Taken from 128 rows on when those tiles give the
+// CUs at least half a round (RXW8_F32_GEMM=0 / 1 forces it off / on where it
+// applies); UNIMPLEMENTED (nothing launched) when the shape or the 16-byte
+// alignment of the weights and y does not fit its contract.
+static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bool packed,
+                               const float *scale, float *y, int64_t M, int64_t N, int64_t K,
+                               int64_t G, int y_mode) {
+  const int env = env_int("RXW8_F32_GEMM", -1);
+  const int64_t tiles = (M + 127) / 128 * ((N + 255) / 256);
+  if (env == 0 || N % 128 || K % 64 || G % 64 || K % G || K / G > 32 || M * K * 2 >= (1LL << 31) ||
+      N * K >= (1LL << 32) || ((uintptr_t)w | (uintptr_t)y) % 16 != 0 ||
+      (env < 0 && (M < 128 || 2 * tiles < rt->cus)))
+    return RXW8_UNIMPLEMENTED;
+  int rc = ensure_workspace(rt, rt->xcast, (size_t)(M * K) * 4, false);
+  if (rc) return rc;
+  uint16_t *xh = (uint16_t *)rt->xcast.ptr, *xl = xh + M * K;
+  SplitXArgs sx{x, xh, xl, M * K};
+  if ((rc = launch(rt, "rxw8_gemm_split_x", dim3(grid_for(M * K, 256, 4096)), dim3(256), sx))) return rc;
+  LinearF32GemmArgs a{xh, xl, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode, packed ? 1 : 0};
+  return launch(rt, "rxw8_gemm_f32c", dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(512), a);
+}
+
 // QuantizedLinear with compute dtype F32 on the matrix cores (x split into
 // bf16 hi + lo parts, exact codes, f32 accumulation): f32 x, row-major U8
 // weights, K and G multiples of 64, 16-byte aligned operands and the staged
 // rows of x within the LDS limit. Returns UNIMPLEMENTED otherwise.
 static int run_linear_f32(Runtime *rt, const float *x, const uint8_t *w, const float *scale,
                           float *y, int64_t M, int64_t N, int64_t K, int64_t G, int y_mode) {
+  {
+    const int rc = run_linear_f32_gemm(rt, x, w, false, scale, y, M, N, K, G, y_mode);
+    if (rc != RXW8_UNIMPLEMENTED) return rc;
+  }
   if (K % 64 != 0 || G % 64 != 0 || K > (1 << 24) || N > (1LL << 30) || M > (1LL << 30) ||
       ((uintptr_t)x | (uintptr_t)w) % 16 != 0 || env_int("RXW8_FORCE_GENERIC", 0))
     return RXW8_UNIMPLEMENTED;
@@ -864,7 +907,12 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
   if (packed) {
     if (compute_bf16 && gemm_eligible(M, N, K, G))
       return run_gemm(rt, x, x_f32, w, true, s, y, y_f32, M, N, K, G, y_mode);
-    // F32 compute on packed weights: the _fc GEMV in chunks of rows
+    // F32 compute on packed weights: the GEMM tiles for long inputs, else the
+    // _fc GEMV in chunks of rows
+    if (!compute_bf16 && x_f32 && y_f32) {
+      const int rc = run_linear_f32_gemm(rt, (const float *)x, w, true, s, (float *)y, M, N, K, G, y_mode);
+      if (rc != RXW8_UNIMPLEMENTED) return rc;
+    }
     int rc = compute_bf16 ? run_gemv(rt, x, x_f32, w, false, true, s, y, y_f32, M, N, K, G, y_mode)
              : x_f32 && y_f32
                  ? run_gemv_fc(rt, (const float *)x, w, s, (float *)y, M, N, K, G, y_mode, nullptr)
