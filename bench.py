@@ -517,7 +517,8 @@ def bench_f32_linear(rt, rx, torch, stream, reps=10, n=248320, k=1024, g=128):
                             "flops": 2 * S * n * k}
         del x, y
     del ws
-    return {"kernel": "rxw8_linear_f32_mfma_r1_w8 (S 16) / _r2_w8 (S 1024)",
+    return {"kernel": "rxw8_linear_f32_mfma_r1_w8 (S 16) / rxw8_gemm_split_x + rxw8_gemm_f32c "
+                      "(S 1024)",
             "shape": f"W [{n}, {k}] U8, G {g} (the Qwen3.5-0.8B tied LM head), x F32 [S, {k}]",
             "runs": out,
             "note": "mfma_frac counts the hi and lo MFMAs (twice the algorithmic flops)",
