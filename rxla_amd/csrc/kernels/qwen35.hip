@@ -680,6 +680,196 @@ __device__ void delta_rule_rows(const Q35DeltaArgs &a) {
 RXW8_Q35_DELTA_ROWS(64)
 RXW8_Q35_DELTA_ROWS(128)
 
+// ---- the gated-delta mixer of a short sequence in one launch: one workgroup
+// of 512 threads per (sequence, head) forms, for the token rows of the
+// sequence in chunks of CH positions,
+//   (A) the causal conv (kernel 4) + SiLU of the head's q, k and v channels,
+//       the q / k L2 norms, beta and g (the arithmetic of rxw8_q35_mix_prep);
+//       thread c < 3 DL owns channel c and all CH positions of the chunk, so
+//       the chunk's inputs are one round of loads and the convolution needs
+//       no neighbours;
+//   (B) the delta-rule recurrence over the chunk's positions, as
+//       rxw8_q35_delta_rule_d* evaluates it (S = g S' + k delta^T,
+//       o = g S'^T q + delta (k . q), delta = (v - g S'^T k) beta), column j of
+//       the state on the LPC = 512 / DL lanes LPC j.. (E = DL / LPC rows
+//       each): the columns evolve independently, so this walk has no barrier;
+//   (C) the gated RMSNorm o * rsqrt(mean(o^2) + eps) * w * silu(z) of
+//       rxw8_q35_rmsnorm for every position of the chunk
+// (layers.rs:131-259). Replaces three launches for short sequences; on long
+// ones the token-parallel prologue and the 16-lane recurrence are faster
+// (here each position's k and q reach all DL columns from one CU's LDS).
+struct Q35ShortMixArgs {
+  const void *raw;               // [T, stride]: conv channels [0, 3W), z [3W, 4W), b, a
+  const float *conv_w;           // [3W, 4]
+  const float *a_log, *dt_bias;  // [Hl]
+  const float *norm_w;           // [DL] gated-norm weight (applied as given)
+  void *out;                     // [T, Hl * DL] gated rows (f32 or bf16)
+  int64_t stride;
+  int S, Hl, k;                  // k = 4 (the host checks)
+  float q_scale, eps;
+  int raw_f32, out_f32;
+};
+
+template <int DL>
+__device__ void linear_short(const Q35ShortMixArgs &a) {
+  constexpr int NT = 512, LPC = NT / DL, E = DL / LPC, CH = 16, C3 = 3 * DL, WPP = DL / 64, K = 4;
+  static_assert(E % 4 == 0 && C3 <= NT && DL % 64 == 0 && (LPC == 4 || LPC == 8), "layout");
+  __shared__ __attribute__((aligned(16))) float qn[CH][DL], kn[CH][DL];
+  __shared__ float vn[CH][DL], on[CH][DL], red[CH][8], bb[CH], gg[CH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.x, b = bh / a.Hl, h = bh - b * a.Hl;
+  const int64_t W = (int64_t)a.Hl * DL;
+  // (A) roles: channel threads (waves of one part each), then beta / g threads
+  const bool chan = tid < C3;
+  const int part = tid / DL, c = tid - part * DL;
+  const int64_t col = (int64_t)part * W + (int64_t)h * DL + c;
+  float cw[K] = {0.f, 0.f, 0.f, 0.f};
+  if (chan)
+#pragma unroll
+    for (int jj = 0; jj < K; ++jj) cw[jj] = a.conv_w[col * K + jj];
+  float hist[K - 1] = {0.f, 0.f, 0.f};  // x at the 3 positions before the chunk (0 before 0)
+  const float nw = tid < DL ? a.norm_w[tid] : 0.f;
+  // (B) roles
+  const int j = tid / LPC, p = tid - j * LPC;
+  float st[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) st[e] = 0.f;
+  // sum over the wave (every lane gets the same bits): lanes l ^ 32, l ^ 16
+  // by the VALU exchanges, then within each row of 16
+  auto wave_sum = [](float v) {
+    v = sum_xor32(v);
+    v = sum_xor16(v);
+    return row_sum16(v);
+  };
+  // sum over the LPC lanes of a column (quads, then the half-row mirror)
+  auto col_sum = [](float v) {
+    v += dpp_rot<0xb1>(v);
+    v += dpp_rot<0x4e>(v);
+    if (LPC == 8) v += dpp_rot<0x141>(v);
+    return v;
+  };
+  for (int p0 = 0; p0 < a.S; p0 += CH) {
+    const int n = min(CH, a.S - p0);
+    const int64_t row0 = (int64_t)b * a.S + p0;
+    float xv[CH], zv[CH];
+#pragma unroll
+    for (int r = 0; r < CH; ++r) {  // (the branches on r < n are uniform)
+      const int64_t row = (row0 + r) * a.stride;
+      xv[r] = chan && r < n ? ld(a.raw, row + col, a.raw_f32) : 0.f;
+      zv[r] = tid < DL && r < n ? ld(a.raw, row + 3 * W + (int64_t)h * DL + tid, a.raw_f32) : 0.f;
+    }
+    if (tid >= C3 && tid - C3 < n) {
+      const int r = tid - C3;
+      const int64_t row = (row0 + r) * a.stride + 4 * W;
+      bb[r] = sigmoid_f32(ld(a.raw, row + h, a.raw_f32));
+      const float xg = ld(a.raw, row + a.Hl + h, a.raw_f32) + a.dt_bias[h];
+      const float sp = fmaxf(xg, 0.f) + log1pf(expf(-fabsf(xg)));
+      gg[r] = expf(sp * -expf(a.a_log[h]));
+    }
+    float y[CH];
+#pragma unroll
+    for (int r = 0; r < CH; ++r) {
+      y[r] = 0.f;
+      if (r >= n) continue;
+      float acc = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < K; ++jj) {
+        const int src = r - (K - 1) + jj;
+        acc += cw[jj] * (src >= 0 ? xv[src] : hist[K - 1 + src]);
+      }
+      y[r] = acc * sigmoid_f32(acc);
+    }
+    if (n == CH) hist[0] = xv[CH - 3], hist[1] = xv[CH - 2], hist[2] = xv[CH - 1];
+    if (chan && part < 2)
+#pragma unroll
+      for (int r = 0; r < CH; ++r) {
+        if (r >= n) continue;
+        const float sq = wave_sum(y[r] * y[r]);
+        if (lane == 0) red[r][wave] = sq;
+      }
+    __syncthreads();
+    if (chan)
+#pragma unroll
+      for (int r = 0; r < CH; ++r) {
+        if (r >= n) continue;
+        if (part == 2) {
+          vn[r][c] = y[r];
+          continue;
+        }
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPP; ++w) tot += red[r][part * WPP + w];
+        if (part == 0)
+          qn[r][c] = y[r] * ((1.0f / sqrtf(tot + 1e-6f)) * a.q_scale);
+        else
+          kn[r][c] = y[r] * (1.0f / sqrtf(tot + 1e-6f));
+      }
+    __syncthreads();
+    // (B)
+    for (int r = 0; r < n; ++r) {
+      const float beta = bb[r], g = gg[r], v = vn[r][j];
+      float ak[2] = {0.f, 0.f}, aq[2] = {0.f, 0.f}, kq[2] = {0.f, 0.f};
+      float kk[E];
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        const float4 k4 = *(const float4 *)(&kn[r][E * p + e]);
+        const float4 q4 = *(const float4 *)(&qn[r][E * p + e]);
+        kk[e] = k4.x, kk[e + 1] = k4.y, kk[e + 2] = k4.z, kk[e + 3] = k4.w;
+        const float qq[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          ak[u & 1] += st[e + u] * kk[e + u];
+          aq[u & 1] += st[e + u] * qq[u];
+          kq[u & 1] += kk[e + u] * qq[u];
+        }
+      }
+      const float sk = col_sum(ak[0] + ak[1]), sqq = col_sum(aq[0] + aq[1]), skq = col_sum(kq[0] + kq[1]);
+      const float delta = (v - g * sk) * beta;
+#pragma unroll
+      for (int e = 0; e < E; ++e) st[e] = g * st[e] + kk[e] * delta;
+      if (p == 0) on[r][j] = g * sqq + delta * skq;
+    }
+    __syncthreads();
+    // (C)
+    float o[CH];
+    if (tid < DL)
+#pragma unroll
+      for (int r = 0; r < CH; ++r) {
+        o[r] = 0.f;
+        if (r >= n) continue;
+        o[r] = on[r][tid];
+        const float so = wave_sum(o[r] * o[r]);
+        if (lane == 0) red[r][wave] = so;
+      }
+    __syncthreads();
+    if (tid < DL)
+#pragma unroll
+      for (int r = 0; r < CH; ++r) {
+        if (r >= n) continue;
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPP; ++w) tot += red[r][w];
+        const float sc = 1.0f / sqrtf(tot / (float)DL + a.eps);
+        float res = (o[r] * sc) * nw;
+        res *= zv[r] * sigmoid_f32(zv[r]);
+        const int64_t at = (row0 + r) * W + (int64_t)h * DL + tid;
+        if (a.out_f32)
+          ((float *)a.out)[at] = res;
+        else
+          ((uint16_t *)a.out)[at] = f32_to_bf16_bits(res);
+      }
+    __syncthreads();  // the next chunk reuses red, qn .. on
+  }
+}
+
+// 512 threads; grid B * Hl.
+#define RXW8_Q35_SHORT(DL)                                                         \
+  extern "C" __global__ void __launch_bounds__(512) rxw8_q35_linear_short_d##DL(Q35ShortMixArgs a) { \
+    linear_short<DL>(a);                                                           \
+  }
+RXW8_Q35_SHORT(64)
+RXW8_Q35_SHORT(128)
+
 // ---- F32 LoRA on the tied head (mod.rs:174-195): down = x A^T, then
 // logits += (alpha / rank) * down B^T. One thread per output element.
 struct Q35LoraArgs {

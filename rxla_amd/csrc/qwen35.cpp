@@ -111,6 +111,17 @@ struct Q35DeltaArgs {
   float *out;
   int B, S, Hl;
 };
+struct Q35ShortMixArgs {
+  const void *raw;
+  const float *conv_w;
+  const float *a_log, *dt_bias;
+  const float *norm_w;
+  void *out;
+  int64_t stride;
+  int S, Hl, k;
+  float q_scale, eps;
+  int raw_f32, out_f32;
+};
 struct Q35SiluArgs {
   const void *g, *u;
   void *act;
@@ -519,13 +530,30 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   // raw = xn [qkv; z; b; a]^T: columns [0, 3W) mixed, [3W, 4W) z, then b, a
   if ((rc = in_proj(m, L, T))) return rc;
   const void *zp = m->at(m->raw, 3 * m->W);
+  char kname[40];
+  // Short sequences (up to 4 positions; RXW8_Q35_SHORT=0 / 1 forces it off /
+  // on at any length): the prologue, the recurrence and the gated norm in one
+  // launch of a workgroup per (sequence, head). Its recurrence walks a
+  // position in ~1 us (every state column reads all of k and q from one CU's
+  // LDS), the 16-lane kernel spread over DL / 16 CUs per head in ~0.15 us, so
+  // from ~8 positions on the three launches are faster.
+  const char *short_env = std::getenv("RXW8_Q35_SHORT");
+  const int short_mode = short_env && short_env[0] ? (short_env[0] == '1' ? 1 : 0) : -1;
+  if ((m->Dl == 64 || m->Dl == 128) && m->cfg.conv_kernel == 4 &&
+      (short_mode == 1 || (short_mode < 0 && S <= 4))) {
+    Q35ShortMixArgs sa{m->raw, m->f32(L.conv), m->f32(L.a_log), m->f32(L.dt_bias), m->f32(L.lnorm),
+                       m->gated, L.n_in, (int)S, (int)m->Hl, (int)m->cfg.conv_kernel,
+                       1.0f / sqrtf((float)m->Dl), m->cfg.eps, m->f32c ? 1 : 0, m->f32c ? 1 : 0};
+    std::snprintf(kname, sizeof kname, "rxw8_q35_linear_short_d%d", (int)m->Dl);
+    if ((rc = launch(rt, kname, dim3((unsigned)(B * m->Hl)), dim3(512), sa))) return rc;
+    return out_proj(m, L, L.out, m->gated, m->f32c, T);
+  }
   // conv + SiLU, q / k L2 norms, beta and decay: one workgroup per (token, head)
   Q35MixPrepArgs mp{m->raw, m->f32(L.conv), m->f32(L.a_log), m->f32(L.dt_bias), m->mixed, m->beta,
                     m->g, L.n_in, (int)S, (int)m->Hl, (int)m->Dl, (int)m->cfg.conv_kernel,
                     1.0f / sqrtf((float)m->Dl), m->f32c ? 1 : 0};
   if ((rc = launch(rt, "rxw8_q35_mix_prep", dim3((unsigned)(T * m->Hl)), dim3(128), mp))) return rc;
   Q35DeltaArgs da{m->mixed, m->beta, m->g, m->dout, (int)B, (int)S, (int)m->Hl};
-  char kname[40];
   std::snprintf(kname, sizeof kname, "rxw8_q35_delta_rule_d%d", (int)m->Dl);
   // Dl <= 32: one workgroup of Dl threads per (sequence, head), one column per
   // thread; Dl >= 64: 16 lanes per column, Dl / 16 workgroups of 256 threads

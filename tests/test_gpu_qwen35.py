@@ -46,7 +46,7 @@ CONFIGS["mid"] = dict(q35.config(vocab=1000, hidden=512, intermediate=1024,
                                  group=128), max_batch=2, max_seq=64)
 CONFIGS["wide_linear"] = dict(CONFIGS["wide"], layers=[q35.LINEAR], max_seq=256)
 CONFIGS["small_mha"] = dict(CONFIGS["small"], kv_heads=4, layers=[q35.FULL, q35.LINEAR])  # G = 1
-# sequences of >= 128 positions take the chunked delta rule (Dl 64 and 128)
+# sequences of >= 128 positions (Dl 64 and 128)
 CONFIGS["mid_long"] = dict(CONFIGS["mid"], layers=[q35.LINEAR, q35.FULL], max_seq=200)
 CONFIGS["wide_full"] = dict(CONFIGS["wide"], layers=[q35.FULL], max_seq=160)
 
@@ -98,6 +98,31 @@ def test_logits_match_the_oracle(rt, name, b, s):
     top2 = np.sort(want, axis=-1)[..., -2:]
     clear = (top2[..., 1] - top2[..., 0]) > 0.05 * np.abs(want).max()
     np.testing.assert_array_equal(got.argmax(-1)[clear], want.argmax(-1)[clear])
+
+
+@pytest.mark.parametrize("name,b,s", [("mid", 2, 1), ("mid", 2, 9), ("mid", 1, 16), ("mid", 2, 37),
+                                      ("wide_linear", 1, 1), ("wide_linear", 1, 7),
+                                      ("wide_linear", 1, 16)])
+def test_short_sequence_mixer(rt, monkeypatch, name, b, s):
+    """The gated-delta mixer in one launch per (sequence, head)
+    (rxw8_q35_linear_short_d64 / _d128: conv + SiLU, L2 norms, beta / g, the
+    recurrence and the gated RMSNorm), forced on at every length here (the
+    default takes it up to 4 positions), and the three-launch path forced
+    on: both within TOL of the oracle, and within 1e-5 of each other (the
+    same arithmetic; only the partition of the state's column sums differs)."""
+    cfg = CONFIGS[name]
+    p = q35.random_params(cfg, seed=21, std=0.05)
+    ids = np.random.default_rng(22).integers(0, cfg["vocab"], (b, s))
+    want = q35.forward(cfg, p, ids)
+    monkeypatch.setenv("RXW8_Q35_SHORT", "1")
+    fused = run(rt, build(rt, cfg, p), ids)
+    monkeypatch.setenv("RXW8_Q35_SHORT", "0")
+    split = run(rt, build(rt, cfg, p), ids)
+    e_fused, e_split, e_pair = rel_err(fused, want), rel_err(split, want), rel_err(fused, split)
+    print(f"qwen35 short mixer {name} b={b} s={s}: fused {e_fused:.2e}, three launches "
+          f"{e_split:.2e}, between {e_pair:.2e}")
+    assert e_fused <= TOL and e_split <= TOL
+    assert e_pair <= 1e-5
 
 
 @pytest.mark.parametrize("name,b,s,std", [("tiny", 2, 13, 0.05), ("small", 2, 13, 0.05),
