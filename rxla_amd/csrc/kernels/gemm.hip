@@ -638,6 +638,12 @@ __device__ __forceinline__ void gemm_tile_bf16w(const GemmArgs &a) {
 // [group][256 rows] (K / G <= 32). Per k tile a wave issues 64 MFMAs (hi and
 // lo for each of its 4 x 4 fragment pairs and both k halves), so the weights
 // are read once per 128 rows of x instead of once per 32.
+//
+// Split K (ksplit > 1, for shapes with too few tiles to fill the CUs): work
+// item (split, tile) covers split's share of the scale groups (of the k tiles
+// when there is one group), scales its group sums into an f32 partial tile
+// written to ws[split], and rxw8_gemm_f32c_reduce adds the partials in split
+// order into y.
 struct LinearF32GemmArgs {
   const uint16_t *xh, *xl;  // [M, K] bf16 hi / lo parts of x
   const uint8_t *w;         // [N, K] u8 codes, or packed [N/16, K/64, 1024]
@@ -646,6 +652,8 @@ struct LinearF32GemmArgs {
   int M, N, K, G;
   int y_mode;               // 0: y = result; 1: y += result
   int w_packed;
+  int ksplit;               // 1, or the number of K splits
+  float *ws;                // [ksplit, M, N] f32 partials when ksplit > 1
 };
 
 __device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a) {
@@ -659,9 +667,11 @@ __device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a)
 
   const int tiles_m = (a.M + TMB - 1) / TMB, tiles_n = (a.N + TNB - 1) / TNB;
   const int ntiles = tiles_m * tiles_n;
-  const int per_xcd = (ntiles + 7) / 8;
-  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-  if (t >= ntiles) return;
+  const int S = a.ksplit > 1 ? a.ksplit : 1;  // split = the slowest index of the work
+  const int per_xcd = (ntiles * S + 7) / 8;
+  const int t_all = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t_all >= ntiles * S) return;
+  const int split = t_all / ntiles, t = t_all - split * ntiles;
   constexpr int GN = 4;  // n tiles per tile-order group
   const int group = t / (GN * tiles_m);
   const int first_n = group * GN;
@@ -669,6 +679,9 @@ __device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a)
   const int r = t - group * GN * tiles_m;
   const int n0 = (first_n + r % gw) * TNB, m0 = (r / gw) * TMB;
   const int KT = a.K / BK, ng = a.K / a.G, tpg = a.G / BK;  // k tiles per scale group
+  // k tiles [kb, ke) of this split: whole scale groups, or k tiles of the one group
+  const int units = ng > 1 ? ng : KT, upt = ng > 1 ? tpg : 1;
+  const int kb = split * units / S * upt, ke = (split + 1) * units / S * upt;
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
   __shared__ float sc[32 * TNB];  // [group][row]
@@ -736,15 +749,15 @@ __device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a)
     }
   const int r16 = lane & 15, kg = lane >> 4;
 
-  load_w(0);
-  issue_x(0, 0);
+  load_w(kb);
+  issue_x(kb, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   store_w(0);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1, nxt = cur ^ 1;
-    const bool more = kt + 1 < KT;  // uniform
+  for (int kt = kb; kt < ke; ++kt) {
+    const int cur = (kt - kb) & 1, nxt = cur ^ 1;
+    const bool more = kt + 1 < ke;  // uniform
     if (more) {
       load_w(kt + 1);     // 2 loads, then 4 DMAs: vmcnt(4) waits for the loads alone
       issue_x(kt + 1, nxt);
@@ -769,7 +782,7 @@ __device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a)
           acc[i][j] = mfma16x16x32(fa[i], fl[j], acc[i][j]);
         }
     }
-    if ((kt + 1) % tpg == 0) {  // the end of a scale group: tot += s[n, g] * acc
+    if ((kt + 1) % tpg == 0 || kt + 1 == ke) {  // a scale group's end (or the split's): tot += s[n, g] * acc
       const int g = kt / tpg;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -796,9 +809,13 @@ __device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int n = n0 + wn * 64 + 16 * i + 4 * kg;
-      if (n >= a.N) continue;  // (N % 128 == 0: a lane's 4 channels are all in or all out)
-      f32x4 *yp = (f32x4 *)(a.y + (int64_t)m * a.N + n);
-      *yp = a.y_mode == 1 ? *yp + tot[i][j] : tot[i][j];
+      if (n >= a.N) continue;  // (N % 16 == 0: a lane's 4 channels are all in or all out)
+      if (S > 1) {
+        *(f32x4 *)(a.ws + ((int64_t)split * a.M + m) * a.N + n) = tot[i][j];
+      } else {
+        f32x4 *yp = (f32x4 *)(a.y + (int64_t)m * a.N + n);
+        *yp = a.y_mode == 1 ? *yp + tot[i][j] : tot[i][j];
+      }
     }
   }
 }
@@ -884,11 +901,30 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemm_cast_x(CastArgs a) {
     a.y[4 * n4 + threadIdx.x] = f32_to_bf16_bits(a.x[4 * n4 + threadIdx.x]);
 }
 
-// Launch contract (checked by the host): N % 128 == 0, K % 64 == 0, G % 64
-// == 0, K % G == 0, K / G <= 32, M >= 1, M * K * 2 < 2^31, N * K < 2^32;
-// grid = 8 * ceil(tiles / 8) workgroups of 512 threads.
+// Launch contract (checked by the host): N % 16 == 0, K % 64 == 0, G % 64
+// == 0, K % G == 0, K / G <= 32, M >= 1, M * K * 2 < 2^31, N * K < 2^32,
+// ksplit <= the split units; grid = 8 * ceil(tiles * ksplit / 8) workgroups
+// of 512 threads.
 extern "C" __global__ void __launch_bounds__(512) rxw8_gemm_f32c(LinearF32GemmArgs a) {
   linear_f32_gemm_tile(a);
+}
+
+// y = (or +=) the sum of the split partials of rxw8_gemm_f32c in split order.
+struct F32ReduceArgs {
+  const float *ws;  // [ksplit, M * N]
+  float *y;         // [M * N]
+  int64_t mn;       // M * N (a multiple of 4)
+  int ksplit, y_mode;
+};
+extern "C" __global__ void __launch_bounds__(256) rxw8_gemm_f32c_reduce(F32ReduceArgs a) {
+  const int64_t q4 = a.mn / 4;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < q4;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const f32x4 h = a.y_mode == 1 ? ((const f32x4 *)a.y)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 sum = ((const f32x4 *)a.ws)[i];
+    for (int s = 1; s < a.ksplit; ++s) sum += ((const f32x4 *)(a.ws + (int64_t)s * a.mn))[i];
+    ((f32x4 *)a.y)[i] = a.y_mode == 1 ? h + sum : sum;
+  }
 }
 
 // f32 rows -> their bf16 parts hi = bf16(x), lo = bf16(x - hi) (RNE both), the

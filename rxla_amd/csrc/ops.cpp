@@ -642,6 +642,14 @@ struct LinearF32GemmArgs {
   float *y;
   int M, N, K, G;
   int y_mode, w_packed;
+  int ksplit;
+  float *ws;
+};
+struct F32ReduceArgs {
+  const float *ws;
+  float *y;
+  int64_t mn;
+  int ksplit, y_mode;
 };
 struct SplitXArgs {
   const float *x;
@@ -652,26 +660,51 @@ struct SplitXArgs {
 // F32-compute W8 linear for long inputs on the GEMM tiles
 // (rxw8_gemm_f32c): x split into bf16 hi / lo parts in the runtime's
 // staging buffer, then 256 x 128 output tiles that read each weight tile
-// once per 128 rows of x. Taken from 128 rows on when those tiles give the
-// CUs at least half a round (RXW8_F32_GEMM=0 / 1 forces it off / on where it
-// applies); UNIMPLEMENTED (nothing launched) when the shape or the 16-byte
-// alignment of the weights and y does not fit its contract.
+// once per 128 rows of x. Shapes with fewer tiles than half a round of CUs
+// split K (at scale-group boundaries, at least 4 k tiles per split, up to 8
+// splits) toward a round of work items, and a reduce launch adds the
+// partials in split order. Taken from 128 rows on (RXW8_F32_GEMM=0 / 1
+// forces it off / on where it applies; RXW8_F32_GEMM_KSPLIT=n forces n
+// splits): even at 32-64 work items (Qwen3.5's 1024-channel projections at
+// 256 rows) it beats the row kernels, which read the weights once per 32
+// rows and cut K into LDS-sized launches. UNIMPLEMENTED (nothing launched)
+// when the shape or the 16-byte alignment of the weights and y does not fit
+// its contract.
 static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bool packed,
                                const float *scale, float *y, int64_t M, int64_t N, int64_t K,
                                int64_t G, int y_mode) {
   const int env = env_int("RXW8_F32_GEMM", -1);
-  const int64_t tiles = (M + 127) / 128 * ((N + 255) / 256);
-  if (env == 0 || N % 128 || K % 64 || G % 64 || K % G || K / G > 32 || M * K * 2 >= (1LL << 31) ||
-      N * K >= (1LL << 32) || ((uintptr_t)w | (uintptr_t)y) % 16 != 0 ||
-      (env < 0 && (M < 128 || 2 * tiles < rt->cus)))
+  if (env == 0 || N % 16 || K % 64 || G % 64 || K % G || K / G > 32 || M * K * 2 >= (1LL << 31) ||
+      N * K >= (1LL << 32) || ((uintptr_t)w | (uintptr_t)y) % 16 != 0)
     return RXW8_UNIMPLEMENTED;
+  const int64_t tiles = (M + 127) / 128 * ((N + 255) / 256);
+  // split units: scale groups, or the k tiles of a single group
+  const int64_t ng = K / G, units = ng > 1 ? ng : K / 64, upt = ng > 1 ? G / 64 : 1;
+  const int ks_env = env_int("RXW8_F32_GEMM_KSPLIT", 0);
+  int64_t ks = 1;
+  if (ks_env > 0) {
+    ks = std::min<int64_t>(ks_env, units);
+  } else if (2 * tiles < rt->cus) {
+    for (int c : {2, 3, 4, 6, 8}) {
+      if (units / c * upt < 4) break;
+      ks = c;
+      if (tiles * c >= rt->cus) break;
+    }
+  }
+  if (env < 0 && M < 128) return RXW8_UNIMPLEMENTED;
   int rc = ensure_workspace(rt, rt->xcast, (size_t)(M * K) * 4, false);
   if (rc) return rc;
+  if (ks > 1 && (rc = ensure_workspace(rt, rt->partials, (size_t)(ks * M * N) * 4, false))) return rc;
   uint16_t *xh = (uint16_t *)rt->xcast.ptr, *xl = xh + M * K;
   SplitXArgs sx{x, xh, xl, M * K};
   if ((rc = launch(rt, "rxw8_gemm_split_x", dim3(grid_for(M * K, 256, 4096)), dim3(256), sx))) return rc;
-  LinearF32GemmArgs a{xh, xl, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode, packed ? 1 : 0};
-  return launch(rt, "rxw8_gemm_f32c", dim3((unsigned)((tiles + 7) / 8 * 8)), dim3(512), a);
+  LinearF32GemmArgs a{xh, xl, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode, packed ? 1 : 0,
+                      (int)ks, ks > 1 ? (float *)rt->partials.ptr : nullptr};
+  if ((rc = launch(rt, "rxw8_gemm_f32c", dim3((unsigned)((tiles * ks + 7) / 8 * 8)), dim3(512), a)))
+    return rc;
+  if (ks == 1) return RXW8_OK;
+  F32ReduceArgs r{(const float *)rt->partials.ptr, y, M * N, (int)ks, y_mode};
+  return launch(rt, "rxw8_gemm_f32c_reduce", dim3(grid_for(M * N / 4, 256, 4096)), dim3(256), r);
 }
 
 // QuantizedLinear with compute dtype F32 on the matrix cores (x split into

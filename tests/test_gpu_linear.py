@@ -131,16 +131,21 @@ def test_f32_compute_matrix_core_path(rt, m, n, k, g):
     assert err < 1e-5
 
 
+@pytest.mark.parametrize("ksplit", ["1", "3"])
 @pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("m,n,k,g", [(1, 256, 64, 64), (130, 512, 256, 128), (300, 1024, 1024, 128),
                                      (257, 768, 3584, 128), (129, 256, 2048, 2048),
-                                     (1024, 4096, 1024, 64), (200, 640, 512, 128), (64, 128, 1024, 128)])
-def test_f32_compute_gemm_tiles(rt, monkeypatch, m, n, k, g, packed):
+                                     (1024, 4096, 1024, 64), (200, 640, 512, 128), (64, 128, 1024, 128),
+                                     (150, 1040, 1024, 128)])
+def test_f32_compute_gemm_tiles(rt, monkeypatch, m, n, k, g, packed, ksplit):
     """F32 compute on the GEMM tiles for long inputs (rxw8_gemm_f32c,
     forced here at every size): x split into bf16 hi + lo, exact codes, group
-    sums scaled in f32; ragged M, a half n tile (N % 256 == 128), one k tile,
-    28 scale groups, per-channel scales; row-major and packed weights. Within 1e-5 of the f64 oracle (on
+    sums scaled in f32; ragged M, a half n tile (N % 256 == 128), N % 256 ==
+    16, one k tile, 28 scale groups, per-channel scales; row-major and packed
+    weights; whole K, or 3 K splits (scale groups, or k tiles of the one
+    group) summed by rxw8_gemm_f32c_reduce. Within 1e-5 of the f64 oracle (on
     sampled rows at M = 1024) and of the row-tile kernel."""
+    monkeypatch.setenv("RXW8_F32_GEMM_KSPLIT", ksplit)
     r = rx()
     rng = np.random.default_rng(m * 3 + n + k)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -151,13 +156,14 @@ def test_f32_compute_gemm_tiles(rt, monkeypatch, m, n, k, g, packed):
     monkeypatch.setenv("RXW8_F32_GEMM", "1")
     y = run(rt, x, u8, s)
     monkeypatch.setenv("RXW8_F32_GEMM", "0")
+    monkeypatch.delenv("RXW8_F32_GEMM_KSPLIT")
     try:
         y_rows = run(rt, x, u8, s)
     except r.Error as e:  # the packed GEMV has no tiling for K = 64
         assert e.code == r.Status.UNIMPLEMENTED and packed and k == 64
         y_rows = y
     err = rel_err(y[rows], ref)
-    print(f"F32 GEMM m={m} n={n} k={k} g={g} packed={packed}: rel_err={err:.3e}, "
+    print(f"F32 GEMM m={m} n={n} k={k} g={g} packed={packed} ksplit={ksplit}: rel_err={err:.3e}, "
           f"vs row tiles {rel_err(y, y_rows):.3e}")
     assert err < 1e-5
     assert rel_err(y, y_rows) < 1e-5

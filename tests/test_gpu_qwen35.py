@@ -125,6 +125,27 @@ def test_short_sequence_mixer(rt, monkeypatch, name, b, s):
     assert e_pair <= 1e-5
 
 
+@pytest.mark.parametrize("name,b,s", [("mid_long", 2, 150), ("wide_full", 1, 160)])
+def test_f32_gemm_split_k_residuals(rt, monkeypatch, name, b, s):
+    """Every F32 projection that fits the GEMM tiles forced onto them
+    (rxw8_gemm_f32c) with 3 K splits, the residual projections included (the
+    reduce launch adds the partials to the f32 residual stream): within TOL of
+    the oracle and within 1e-5 of the default plan."""
+    cfg = CONFIGS[name]
+    p = q35.random_params(cfg, seed=51, std=0.05)
+    ids = np.random.default_rng(52).integers(0, cfg["vocab"], (b, s))
+    want = q35.forward(cfg, p, ids)
+    base = run(rt, build(rt, cfg, p), ids)
+    monkeypatch.setenv("RXW8_F32_GEMM", "1")
+    monkeypatch.setenv("RXW8_F32_GEMM_KSPLIT", "3")
+    got = run(rt, build(rt, cfg, p), ids)
+    e_got, e_base, e_pair = rel_err(got, want), rel_err(base, want), rel_err(got, base)
+    print(f"qwen35 split-K F32 GEMM {name} b={b} s={s}: forced {e_got:.2e}, default {e_base:.2e}, "
+          f"between {e_pair:.2e}")
+    assert e_got <= TOL and e_base <= TOL
+    assert e_pair <= 1e-5
+
+
 @pytest.mark.parametrize("name,b,s,std", [("tiny", 2, 13, 0.05), ("small", 2, 13, 0.05),
                                           ("small", 2, 70, 0.05), ("mid", 2, 37, 0.03),
                                           ("wide", 1, 16, 0.02), ("wide_full", 1, 77, 0.02)])
