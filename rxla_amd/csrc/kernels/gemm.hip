@@ -934,9 +934,23 @@ struct SplitXArgs {
   uint16_t *hi, *lo;
   int64_t n;
 };
+// Four values per thread (a 16-byte load, two 8-byte stores) when x is
+// 16-byte aligned (n is a multiple of 64: K % 64 == 0), else one.
 extern "C" __global__ void __launch_bounds__(256) rxw8_gemm_split_x(SplitXArgs a) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n;
-       i += (int64_t)gridDim.x * blockDim.x) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  if (((uintptr_t)a.x & 15) == 0) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n / 4; i += stride) {
+      const float4 v = ((const float4 *)a.x)[i];
+      const uint32_t h01 = pack_bf16x2(v.x, v.y), h23 = pack_bf16x2(v.z, v.w);
+      ((uint2 *)a.hi)[i] = uint2{h01, h23};
+      ((uint2 *)a.lo)[i] = uint2{pack_bf16x2(v.x - bf16_bits_to_f32((uint16_t)h01),
+                                             v.y - bf16_bits_to_f32((uint16_t)(h01 >> 16))),
+                                 pack_bf16x2(v.z - bf16_bits_to_f32((uint16_t)h23),
+                                             v.w - bf16_bits_to_f32((uint16_t)(h23 >> 16)))};
+    }
+    return;
+  }
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
     const float v = a.x[i];
     const uint16_t h = f32_to_bf16_bits(v);
     a.hi[i] = h;

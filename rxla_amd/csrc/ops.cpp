@@ -697,7 +697,8 @@ static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bo
   if (ks > 1 && (rc = ensure_workspace(rt, rt->partials, (size_t)(ks * M * N) * 4, false))) return rc;
   uint16_t *xh = (uint16_t *)rt->xcast.ptr, *xl = xh + M * K;
   SplitXArgs sx{x, xh, xl, M * K};
-  if ((rc = launch(rt, "rxw8_gemm_split_x", dim3(grid_for(M * K, 256, 4096)), dim3(256), sx))) return rc;
+  if ((rc = launch(rt, "rxw8_gemm_split_x", dim3(grid_for(M * K / 4, 256, 4096)), dim3(256), sx)))
+    return rc;
   LinearF32GemmArgs a{xh, xl, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode, packed ? 1 : 0,
                       (int)ks, ks > 1 ? (float *)rt->partials.ptr : nullptr};
   if ((rc = launch(rt, "rxw8_gemm_f32c", dim3((unsigned)((tiles * ks + 7) / 8 * 8)), dim3(512), a)))
