@@ -556,9 +556,11 @@ int linear_mixer(Qwen35 *m, const Layer &L, int64_t B, int64_t S) {
   Q35DeltaArgs da{m->mixed, m->beta, m->g, m->dout, (int)B, (int)S, (int)m->Hl};
   std::snprintf(kname, sizeof kname, "rxw8_q35_delta_rule_d%d", (int)m->Dl);
   // Dl <= 32: one workgroup of Dl threads per (sequence, head), one column per
-  // thread; Dl >= 64: 16 lanes per column, Dl / 16 workgroups of 256 threads
+  // thread; Dl >= 64: lpc lanes per column (16 at Dl 64, 32 at Dl 128),
+  // workgroups of 256 threads (256 / lpc columns each)
   const bool rows = m->Dl >= 64;
-  const dim3 grid((unsigned)(B * m->Hl * (rows ? m->Dl / 16 : 1)));
+  const int lpc = m->Dl >= 128 ? 32 : 16;
+  const dim3 grid((unsigned)(B * m->Hl * (rows ? m->Dl / (256 / lpc) : 1)));
   if ((rc = launch(rt, kname, grid, dim3(rows ? 256u : (unsigned)m->Dl), da))) return rc;
   return finish_linear(m, L, T, zp);
 }
