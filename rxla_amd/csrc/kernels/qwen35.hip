@@ -598,10 +598,10 @@ __device__ __forceinline__ float row_sum16(float v) {
 // beta and g of NPF positions come as one lane-indexed vector load (lane i of
 // the wave holds position t0 + i) and reach the step by v_readlane, so no
 // scalar-cache load (whose waits cannot be counted per load) sits in the loop.
-template <int DL, int LPC = 16, int NWV = 4>
+template <int DL, int LPC = 16, int NWV = 4, int NPF = 16>
 __device__ void delta_rule_rows(const Q35DeltaArgs &a) {
-  // LPC lanes per column (16 or 32), NWV waves per workgroup
-  constexpr int E = DL / LPC, NPF = 8, CPG = 64 / LPC * NWV, GROUPS = DL / CPG;
+  // LPC lanes per column (16 or 32), NWV waves per workgroup, NPF positions in flight
+  constexpr int E = DL / LPC, CPG = 64 / LPC * NWV, GROUPS = DL / CPG;
   static_assert((LPC == 16 || LPC == 32) && E % 4 == 0 && DL % CPG == 0, "layout");
   const int lane = threadIdx.x & 63, p = lane & (LPC - 1);
   const int bh = blockIdx.x / GROUPS, grp = blockIdx.x - bh * GROUPS;
@@ -680,7 +680,10 @@ __device__ void delta_rule_rows(const Q35DeltaArgs &a) {
 // threads = 8 columns x 32 lanes (4 rows per lane), grid B * Hl * 16, which
 // measured 3% faster per forward than 16 lanes (0.8B model, S = 1024:
 // 11.85 against 12.15-12.29 ms); 8-wave workgroups (two waves per SIMD) were
-// slower with either width.
+// slower with either width. 16 positions in flight instead of 8: 11.38
+// against 12.14 ms (the loads of position t + 8 had not landed by its turn).
+// (Two positions per reduction round, with the second position's sums
+// regrouped, measured no faster than this.)
 extern "C" __global__ void __launch_bounds__(256) rxw8_q35_delta_rule_d64(Q35DeltaArgs a) {
   delta_rule_rows<64, 16, 4>(a);
 }
