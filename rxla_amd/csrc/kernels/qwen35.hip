@@ -440,6 +440,7 @@ struct Q35MixPrepArgs {
   const float *a_log, *dt_bias;  // [Hl]
   float *mixed;                  // [T, 3W]: q (normed, scaled), k (normed), v
   float *beta, *g;               // [T, Hl]
+  float *lg;                     // [T, Hl] log g (the chunked recurrence's decays), or null
   int64_t stride;
   int S, Hl, Dl, k;
   float q_scale;
@@ -501,7 +502,9 @@ extern "C" __global__ void __launch_bounds__(128) rxw8_q35_mix_prep(Q35MixPrepAr
     a.beta[t * a.Hl + h] = sigmoid_f32(ld(a.raw, row + h, a.raw_f32));
     const float x = ld(a.raw, row + a.Hl + h, a.raw_f32) + a.dt_bias[h];
     const float sp = fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
-    a.g[t * a.Hl + h] = expf(sp * -expf(a.a_log[h]));
+    const float lgv = sp * -expf(a.a_log[h]);
+    a.g[t * a.Hl + h] = expf(lgv);
+    if (a.lg) a.lg[t * a.Hl + h] = lgv;
   }
 }
 
@@ -675,6 +678,306 @@ __device__ void delta_rule_rows(const Q35DeltaArgs &a) {
   for (int i = 0; i < NPF; ++i)
     if (t0 + i < a.S) step(buf[i], lane_value(bcur, i), lane_value(gcur, i), t0 + i);
 }
+
+// ---- chunked delta rule (layers.rs:197-234, the same recurrence in chunks of
+// C = 64 positions). With S0 the state before a chunk, Gamma_t = prod_{u<=t}
+// g_u = exp(gam_t) (gam the inclusive cumulative log decay, so every ratio
+// Gamma_t / Gamma_s with s <= t is exp(gam_t - gam_s) <= 1), unrolling
+// S_t = g_t S_{t-1} + k_t delta_t^T gives
+//   (I + A) Delta = diag(beta) (V - diag(Gamma) K S0),
+//     A_ts = beta_t (Gamma_t / Gamma_s) k_t . k_s  (s < t),
+//   O = diag(Gamma) Q S0 + P Delta,  P_ts = (Gamma_t / Gamma_s) q_t . k_s (s <= t),
+//   S_end = Gamma_end S0 + sum_s (Gamma_end / Gamma_s) k_s Delta_s^T.
+// With U = (I + A)^-1 diag(beta) V and W = (I + A)^-1 diag(beta Gamma) K,
+// Delta = U - W S0. rxw8_q35_delta_chunk_d* forms, for every chunk in
+// parallel, U, W, P, Qg = diag(Gamma) Q, KdT = (diag(Gamma_end / Gamma) K)^T
+// (state rows major, so the walk reads it in 16-byte pieces) and gam;
+// rxw8_q35_delta_scan_d* walks the chunks in order with the state on the
+// matrix cores. Rows past the sequence are zero (beta = 0, k = q = v = 0,
+// lg = 0), so every chunk is processed as 64 rows.
+struct Q35ChunkArgs {
+  const float *mixed;        // [T, 3W]: q, k, v
+  const float *beta, *lg;    // [T, Hl]
+  // per chunk of each (sequence, head): [64][DL], [64][DL], [64][64], [64],
+  // [64][DL], [DL][64]
+  float *u, *wm, *pm, *gam, *qg, *kdt;
+  float *out;                // [T, W] (the scan)
+  int S, Hl, NC;
+};
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// One chunk of one (sequence, head): 256 threads (4 waves).
+template <int DL>
+__device__ void delta_chunk(const Q35ChunkArgs &a) {
+  constexpr int C = 64, KP = DL + 4, KQ = DL / 4;
+  __shared__ __attribute__((aligned(16))) float ks[C][KP], qs[C][KP];
+  __shared__ __attribute__((aligned(16))) float as[C][C + 4];
+  __shared__ float bs[C], gs[C];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t ch = blockIdx.x;
+  const int bh = (int)(ch / a.NC), c = (int)(ch - (int64_t)bh * a.NC);
+  const int b = bh / a.Hl, h = bh - b * a.Hl;
+  const int t0 = c * C, n = min(C, a.S - t0);
+  const int64_t W = (int64_t)a.Hl * DL;
+  const int64_t row0 = (int64_t)b * a.S + t0;
+  // the v column of the U half of the solve, loaded first (thread = column)
+  float x[C];
+#pragma unroll
+  for (int t = 0; t < C; ++t)
+    x[t] = tid < DL && t < n ? a.mixed[(row0 + t) * 3 * W + 2 * W + (int64_t)h * DL + tid] : 0.f;
+  // k and q rows of the chunk (rows past the sequence zero)
+  for (int e = tid; e < C * KQ; e += 256) {
+    const int t = e / KQ, d4 = e - t * KQ;
+    float4 qv = {0.f, 0.f, 0.f, 0.f}, kv = qv;
+    if (t < n) {
+      const float *m = a.mixed + (row0 + t) * 3 * W + (int64_t)h * DL + 4 * d4;
+      qv = *(const float4 *)m;
+      kv = *(const float4 *)(m + W);
+    }
+    *(float4 *)&qs[t][4 * d4] = qv;
+    *(float4 *)&ks[t][4 * d4] = kv;
+  }
+  if (wave == 0) {  // inclusive scan of the log decays; beta
+    float x = lane < n ? a.lg[(row0 + lane) * a.Hl + h] : 0.f;
+    for (int o = 1; o < 64; o <<= 1) {
+      const float y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    gs[lane] = x;
+    bs[lane] = lane < n ? a.beta[(row0 + lane) * a.Hl + h] : 0.f;
+  }
+  __syncthreads();
+  // Qg = diag(Gamma) Q; KdT[i][s] = (Gamma_end / Gamma_s) k_s[i]
+  {
+    float *qg = a.qg + ch * C * DL, *kdt = a.kdt + ch * C * DL;
+    const float gend = gs[C - 1];
+    for (int e = tid; e < C * KQ; e += 256) {
+      const int t = e / KQ, d4 = e - t * KQ;
+      const float f = expf(gs[t]);
+      const float4 q4 = *(const float4 *)&qs[t][4 * d4];
+      *(float4 *)(qg + t * DL + 4 * d4) = float4{f * q4.x, f * q4.y, f * q4.z, f * q4.w};
+    }
+    for (int e = tid; e < DL * (C / 4); e += 256) {
+      const int i = e / (C / 4), s4 = 4 * (e - i * (C / 4));
+      float4 o;
+      o.x = expf(gend - gs[s4]) * ks[s4][i];
+      o.y = expf(gend - gs[s4 + 1]) * ks[s4 + 1][i];
+      o.z = expf(gend - gs[s4 + 2]) * ks[s4 + 2][i];
+      o.w = expf(gend - gs[s4 + 3]) * ks[s4 + 3][i];
+      *(float4 *)(kdt + i * C + s4) = o;
+    }
+  }
+  // K K^T and Q K^T, row tile = wave, column tiles 0..3; the MFMA k index of
+  // lane l at step kk is 4 kk + l / 16 (the same in both operands; rows 132
+  // floats apart put a step's 64 reads on distinct banks two by two)
+  f32x4 kk_acc[4], qk_acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) kk_acc[j] = qk_acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int kk = 0; kk < KQ; ++kk) {
+    const int d = 4 * kk + g;
+    const float ak = ks[16 * wave + r16][d], aq = qs[16 * wave + r16][d];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float bk = ks[16 * j + r16][d];
+      kk_acc[j] = mfma4(ak, bk, kk_acc[j]);
+      qk_acc[j] = mfma4(aq, bk, qk_acc[j]);
+    }
+  }
+  // lane holds rows t = 16 wave + 4 g + r, columns s = 16 j + r16
+  float *pm = a.pm + ch * C * C;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * g + r, s2 = 16 * j + r16;
+      // (gam is non-increasing, so the exponent is <= 0 wherever s <= t)
+      const float e = expf(fminf(gs[t] - gs[s2], 0.f));
+      as[t][s2] = s2 < t ? bs[t] * e * kk_acc[j][r] : 0.f;
+      pm[t * C + s2] = s2 <= t ? e * qk_acc[j][r] : 0.f;
+    }
+  __syncthreads();
+  // forward substitution, thread = one column of X = [U | W]:
+  //   X_t = B_t - sum_{s<t} A_ts X_s,  B_t = beta_t v_t (U), beta_t Gamma_t k_t (W)
+  if (tid < 2 * DL) {
+    const bool is_w = tid >= DL;
+    const int col = is_w ? tid - DL : tid;
+#pragma unroll
+    for (int t = 0; t < C; ++t) x[t] = (is_w ? bs[t] * expf(gs[t]) * ks[t][col] : bs[t] * x[t]);
+    // row t's A values are read while row t - 1 is reduced (one LDS round
+    // trip per row, not one per pair of reads)
+    float4 arow[2][C / 4];
+    arow[1][0] = *(const float4 *)&as[1][0];
+#pragma unroll
+    for (int t = 1; t < C; ++t) {
+      const int cur = t & 1;
+      if (t + 1 < C)
+#pragma unroll
+        for (int q = 0; q < (t + 4) / 4; ++q) arow[cur ^ 1][q] = *(const float4 *)&as[t + 1][4 * q];
+      float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < t; s2 += 4) {  // A_ts = 0 for s >= t
+        const float4 a4 = arow[cur][s2 / 4];
+        p0 += a4.x * x[s2];
+        if (s2 + 1 < t) p1 += a4.y * x[s2 + 1];
+        if (s2 + 2 < t) p2 += a4.z * x[s2 + 2];
+        if (s2 + 3 < t) p3 += a4.w * x[s2 + 3];
+      }
+      x[t] -= (p0 + p1) + (p2 + p3);
+    }
+    float *dst = (is_w ? a.wm : a.u) + ch * C * DL + col;
+#pragma unroll
+    for (int t = 0; t < C; ++t) dst[t * DL] = x[t];
+  }
+  if (tid < C) a.gam[ch * C + tid] = gs[tid];
+}
+
+// The chunks of one (sequence, head) in order for 16 columns of the state
+// (grid B * Hl * DL / 16, 256 threads). Wave w owns rows 16 w .. 16 w + 15 of
+// the chunk for Delta and O, and state rows 16 it .. + 15 for it = w,
+// w + 4, .. (DL / 64 tiles per wave) for the update. The state and Delta pass
+// between waves through LDS.
+template <int DL>
+__device__ void delta_scan(const Q35ChunkArgs &a) {
+  constexpr int C = 64, KQ = DL / 4, GROUPS = DL / 16, IT = DL / 64;
+  __shared__ float ss[DL][17], ds[C][17];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int bh = blockIdx.x / GROUPS, grp = blockIdx.x - bh * GROUPS;
+  const int b = bh / a.Hl, h = bh - b * a.Hl;
+  const int c0 = grp * 16;
+  const int64_t W = (int64_t)a.Hl * DL;
+  for (int e = tid; e < DL * 17; e += 256) (&ss[0][0])[e] = 0.f;
+  // Operands of one chunk, each loaded a chunk ahead, right after the current
+  // chunk has consumed the registers it goes to:
+  //   wreg / qreg  W and Qg rows of this wave's tile (lane k index KQ (l / 16) + kk)
+  //   preg         P row (lane k index 16 (l / 16) + kk), ureg  U in the output layout
+  //   kreg         KdT rows 16 it + l % 16, columns s = 16 (l / 16) + kk
+  float wreg[KQ], qreg[KQ], preg[16], ureg[4], kreg[IT][16], gend;
+  auto load_wq = [&](int c) {
+    const int64_t ch = (int64_t)bh * a.NC + c;
+    const int t = 16 * wave + r16;
+    const float *wr = a.wm + (ch * C + t) * DL + KQ * g;
+    const float *qr = a.qg + (ch * C + t) * DL + KQ * g;
+#pragma unroll
+    for (int kk = 0; kk < KQ; kk += 4) {
+      const float4 w4 = *(const float4 *)(wr + kk);
+      const float4 q4 = *(const float4 *)(qr + kk);
+      wreg[kk] = w4.x, wreg[kk + 1] = w4.y, wreg[kk + 2] = w4.z, wreg[kk + 3] = w4.w;
+      qreg[kk] = q4.x, qreg[kk + 1] = q4.y, qreg[kk + 2] = q4.z, qreg[kk + 3] = q4.w;
+    }
+  };
+  auto load_pu = [&](int c) {
+    const int64_t ch = (int64_t)bh * a.NC + c;
+    const float *pr = a.pm + (ch * C + 16 * wave + r16) * C + 16 * g;
+#pragma unroll
+    for (int kk = 0; kk < 16; kk += 4) {
+      const float4 p4 = *(const float4 *)(pr + kk);
+      preg[kk] = p4.x, preg[kk + 1] = p4.y, preg[kk + 2] = p4.z, preg[kk + 3] = p4.w;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ureg[r] = a.u[(ch * C + 16 * wave + 4 * g + r) * DL + c0 + r16];
+  };
+  auto load_k = [&](int c) {
+    const int64_t ch = (int64_t)bh * a.NC + c;
+#pragma unroll
+    for (int q2 = 0; q2 < IT; ++q2) {
+      const float *kr = a.kdt + (ch * DL + 16 * (wave + 4 * q2) + r16) * C + 16 * g;
+#pragma unroll
+      for (int kk = 0; kk < 16; kk += 4) {
+        const float4 k4 = *(const float4 *)(kr + kk);
+        kreg[q2][kk] = k4.x, kreg[q2][kk + 1] = k4.y, kreg[q2][kk + 2] = k4.z, kreg[q2][kk + 3] = k4.w;
+      }
+    }
+    gend = a.gam[ch * C + C - 1];
+  };
+  load_wq(0);
+  load_pu(0);
+  load_k(0);
+  __syncthreads();
+  for (int c = 0; c < a.NC; ++c) {
+    const int n = min(C, a.S - c * C);
+    const int64_t row0 = (int64_t)b * a.S + c * C;
+    // the next chunk's operands (the last chunk re-reads its own: every
+    // iteration issues the same loads, so the waits for them stay counted)
+    const int cn = min(c + 1, a.NC - 1);
+    // W S0 and Qg S0 (16 x 16 each); the state fragments read first
+    f32x4 wsa, qsa;
+    {
+      float sv[KQ];
+#pragma unroll
+      for (int kk = 0; kk < KQ; ++kk) sv[kk] = ss[KQ * g + kk][r16];
+      f32x4 w2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, q2v[2] = {w2[0], w2[0]};
+#pragma unroll
+      for (int kk = 0; kk < KQ; ++kk) {
+        w2[kk & 1] = mfma4(wreg[kk], sv[kk], w2[kk & 1]);
+        q2v[kk & 1] = mfma4(qreg[kk], sv[kk], q2v[kk & 1]);
+      }
+      wsa = w2[0] + w2[1];
+      qsa = q2v[0] + q2v[1];
+    }
+    load_wq(cn);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ds[16 * wave + 4 * g + r][r16] = ureg[r] - wsa[r];
+    __syncthreads();  // Delta in LDS; every read of S0 for W S0 / Qg S0 done
+    // O = Qg S0 + P Delta (the Delta fragments, read once, also feed the update)
+    float dv[16];
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) dv[kk] = ds[16 * g + kk][r16];
+    f32x4 o = qsa, o2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 16; kk += 2) {
+      o = mfma4(preg[kk], dv[kk], o);
+      o2 = mfma4(preg[kk + 1], dv[kk + 1], o2);
+    }
+    o += o2;
+    load_pu(cn);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * wave + 4 * g + r;
+      if (t < n) a.out[(row0 + t) * W + (int64_t)h * DL + c0 + r16] = o[r];
+    }
+    // S_end = Gamma_end S0 + KdT Delta
+    f32x4 sn[IT];
+    const float eg = expf(gend);
+#pragma unroll
+    for (int q2 = 0; q2 < IT; ++q2) {
+      const int it = wave + 4 * q2;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sn[q2][r] = eg * ss[16 * it + 4 * g + r][r16];
+      f32x4 s2v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 16; kk += 2) {
+        sn[q2] = mfma4(kreg[q2][kk], dv[kk], sn[q2]);
+        s2v = mfma4(kreg[q2][kk + 1], dv[kk + 1], s2v);
+      }
+      sn[q2] += s2v;
+    }
+    load_k(cn);
+    __syncthreads();  // every read of S0 done
+#pragma unroll
+    for (int q2 = 0; q2 < IT; ++q2) {
+      const int it = wave + 4 * q2;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ss[16 * it + 4 * g + r][r16] = sn[q2][r];
+    }
+    __syncthreads();  // the new state in LDS; Delta free
+  }
+}
+
+#define RXW8_Q35_CHUNK(DL)                                                         \
+  extern "C" __global__ void __launch_bounds__(256) rxw8_q35_delta_chunk_d##DL(Q35ChunkArgs a) { \
+    delta_chunk<DL>(a);                                                            \
+  }                                                                                \
+  extern "C" __global__ void __launch_bounds__(256) rxw8_q35_delta_scan_d##DL(Q35ChunkArgs a) { \
+    delta_scan<DL>(a);                                                             \
+  }
+RXW8_Q35_CHUNK(64)
+RXW8_Q35_CHUNK(128)
 
 // Dl 64: 256 threads = 16 columns x 16 lanes, grid B * Hl * 4; Dl 128: 256
 // threads = 8 columns x 32 lanes (4 rows per lane), grid B * Hl * 16, which

@@ -125,6 +125,34 @@ def test_short_sequence_mixer(rt, monkeypatch, name, b, s):
     assert e_pair <= 1e-5
 
 
+@pytest.mark.parametrize("name,b,s", [("mid", 2, 1), ("mid", 2, 37), ("mid", 1, 64),
+                                      ("mid_long", 2, 150), ("wide_linear", 1, 65),
+                                      ("wide_linear", 1, 128), ("wide_linear", 1, 203)])
+def test_chunked_delta_rule(rt, monkeypatch, name, b, s):
+    """The delta rule in chunks of 64 positions (rxw8_q35_delta_chunk_d* /
+    rxw8_q35_delta_scan_d*: per chunk (I + A) Delta = diag(beta) (V -
+    diag(Gamma) K S0) solved in parallel, the state carried from chunk to
+    chunk on the matrix cores), forced on at every length here (the default
+    takes it from 256 positions), against the sequential recurrence forced on:
+    one partial chunk, exactly one chunk, several with a partial last one, Dl
+    64 and 128; both within TOL of the oracle and within 1e-4 of each other
+    (the same terms, reassociated)."""
+    cfg = CONFIGS[name]
+    p = q35.random_params(cfg, seed=61, std=0.05)
+    ids = np.random.default_rng(62).integers(0, cfg["vocab"], (b, s))
+    want = q35.forward(cfg, p, ids)
+    monkeypatch.setenv("RXW8_Q35_SHORT", "0")
+    monkeypatch.setenv("RXW8_Q35_CHUNKED", "1")
+    chunked = run(rt, build(rt, cfg, p), ids)
+    monkeypatch.setenv("RXW8_Q35_CHUNKED", "0")
+    seq = run(rt, build(rt, cfg, p), ids)
+    e_c, e_s, e_pair = rel_err(chunked, want), rel_err(seq, want), rel_err(chunked, seq)
+    print(f"qwen35 chunked delta rule {name} b={b} s={s}: chunked {e_c:.2e}, sequential {e_s:.2e}, "
+          f"between {e_pair:.2e}")
+    assert e_c <= TOL and e_s <= TOL
+    assert e_pair <= 1e-4
+
+
 @pytest.mark.parametrize("name,b,s", [("mid_long", 2, 150), ("wide_full", 1, 160)])
 def test_f32_gemm_split_k_residuals(rt, monkeypatch, name, b, s):
     """Every F32 projection that fits the GEMM tiles forced onto them
