@@ -663,13 +663,14 @@ struct SplitXArgs {
 // once per 128 rows of x. Shapes with fewer tiles than half a round of CUs
 // split K (at scale-group boundaries, at least 4 k tiles per split, up to 8
 // splits) toward a round of work items, and a reduce launch adds the
-// partials in split order. Taken from 128 rows on (RXW8_F32_GEMM=0 / 1
+// partials in split order. Taken from 17 rows on (RXW8_F32_GEMM=0 / 1
 // forces it off / on where it applies; RXW8_F32_GEMM_KSPLIT=n forces n
-// splits): even at 32-64 work items (Qwen3.5's 1024-channel projections at
-// 256 rows) it beats the row kernels, which read the weights once per 32
-// rows and cut K into LDS-sized launches. UNIMPLEMENTED (nothing launched)
-// when the shape or the 16-byte alignment of the weights and y does not fit
-// its contract.
+// splits): even with mostly empty 128-row tiles and 32-64 work items it
+// beats the row kernels, which read the weights once per 32 rows and cut K
+// into LDS-sized launches (Qwen3.5-0.8B forward at 17 / 64 positions: 2.80
+// / 3.39 ms against 3.95 / 4.61); up to 16 rows the F32 GEMV stays.
+// UNIMPLEMENTED (nothing launched) when the shape or the 16-byte alignment
+// of the weights and y does not fit its contract.
 static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bool packed,
                                const float *scale, float *y, int64_t M, int64_t N, int64_t K,
                                int64_t G, int y_mode) {
@@ -691,7 +692,7 @@ static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bo
       if (tiles * c >= rt->cus) break;
     }
   }
-  if (env < 0 && M < 128) return RXW8_UNIMPLEMENTED;
+  if (env < 0 && M <= 16) return RXW8_UNIMPLEMENTED;
   int rc = ensure_workspace(rt, rt->xcast, (size_t)(M * K) * 4, false);
   if (rc) return rc;
   if (ks > 1 && (rc = ensure_workspace(rt, rt->partials, (size_t)(ks * M * N) * 4, false))) return rc;
