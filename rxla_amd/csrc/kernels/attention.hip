@@ -1289,9 +1289,11 @@ __device__ void attn_prefill_rt(const PrefillArgs &a) {
         // key 0 is visible to every row and block 0 is never skipped, so
         // m_new is finite from the first block on (f = exp2(-inf) = 0 there).
         // p = exp(scale (s - m)) = exp2(c s - c m) on v_exp_f32 (terms below
-        // 2^-126 of the row maximum flush to zero): exactly 1 at the maximum,
-        // and f exactly 1 while the maximum stays
-        const float m_new = fmaxf(m_run[r], mb);
+        // 2^-126 of the reference flush to zero). The reference m moves only
+        // when a block's maximum exceeds it by more than 8 (log2 units), so
+        // p <= 2^8 (exact in bf16's range; l and O carry the same factor and
+        // O / l is unchanged) and most blocks rescale nothing
+        const float m_new = mb > m_run[r] + 8.f ? mb : m_run[r];
         const float f = __builtin_amdgcn_exp2f(m_run[r] - m_new);
         float ls = 0.f;
 #pragma unroll
