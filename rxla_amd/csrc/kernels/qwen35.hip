@@ -349,14 +349,20 @@ __device__ void q35_attention(const Q35AttnArgs &a) {
     }
     return;
   }
+  // a row's gate values are all loaded before its stores (a load after a
+  // store to possibly the same memory would wait for it: one round trip per
+  // value)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int qpos = q0 + 4 * j + i;
     if (qpos < a.S) {
       const float inv = 1.0f / l[i];
       const int64_t off = ((int64_t)b * a.S + qpos) * a.Hq * D + (int64_t)h * D + col;
+      float gv[DT];
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) a.out[off + 16 * dt] = (o[dt][i] * inv) * a.gate[off + 16 * dt];
+      for (int dt = 0; dt < DT; ++dt) gv[dt] = a.gate[off + 16 * dt];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) a.out[off + 16 * dt] = (o[dt][i] * inv) * gv[dt];
     }
   }
 }
@@ -383,8 +389,11 @@ __device__ void q35_attention_combine(const Q35AttnArgs &a) {
   }
   const float inv = 1.0f / L;
   const int64_t off = row * D;  // [T, Hq * D] = row-major (t * Hq + h) * D
+  float gv[D / 64];  // loaded before the stores (see q35_attention)
 #pragma unroll
-  for (int e = 0; e < D / 64; ++e) a.out[off + 64 * e + lane] = (o[e] * inv) * a.gate[off + 64 * e + lane];
+  for (int e = 0; e < D / 64; ++e) gv[e] = a.gate[off + 64 * e + lane];
+#pragma unroll
+  for (int e = 0; e < D / 64; ++e) a.out[off + 64 * e + lane] = (o[e] * inv) * gv[e];
 }
 
 #define RXW8_Q35_ATTN(D)                                                                    \
