@@ -81,17 +81,30 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a
   float tot = 0.f;
   for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += red[i];
   const float sc = 1.0f / sqrtf(tot / (float)a.L + a.eps);
-  for (int64_t i = threadIdx.x; i < a.L; i += blockDim.x) {
-    const float w = a.zero_centered ? 1.0f + a.w[i] : a.w[i];
-    float y = (x[i] * sc) * w;
-    if (a.z) {
-      const float zv = ld(a.z, (r / a.z_group) * a.z_stride + (r % a.z_group) * a.L + i, a.z_f32);
-      y *= zv * sigmoid_f32(zv);
+  // four elements' loads per thread go out before their stores (a load after
+  // a store the compiler cannot tell apart from it would wait for it)
+  const int64_t zrow = (r / a.z_group) * a.z_stride + (r % a.z_group) * a.L;
+  for (int64_t i0 = threadIdx.x; i0 < a.L; i0 += 4 * (int64_t)blockDim.x) {
+    float xv[4], wv[4], zv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t i = i0 + e * (int64_t)blockDim.x;
+      const bool in = i < a.L;
+      xv[e] = in ? x[i] : 0.f;
+      wv[e] = in ? a.w[i] : 0.f;
+      zv[e] = in && a.z ? ld(a.z, zrow + i, a.z_f32) : 0.f;
     }
-    if (a.out_f32)
-      ((float *)a.out)[r * a.out_stride + i] = y;
-    else
-      ((uint16_t *)a.out)[r * a.out_stride + i] = f32_to_bf16_bits(y);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t i = i0 + e * (int64_t)blockDim.x;
+      if (i >= a.L) continue;
+      float y = (xv[e] * sc) * (a.zero_centered ? 1.0f + wv[e] : wv[e]);
+      if (a.z) y *= zv[e] * sigmoid_f32(zv[e]);
+      if (a.out_f32)
+        ((float *)a.out)[r * a.out_stride + i] = y;
+      else
+        ((uint16_t *)a.out)[r * a.out_stride + i] = f32_to_bf16_bits(y);
+    }
   }
 }
 
@@ -145,23 +158,41 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
   const int half = a.rot / 2;
   float *dst = is_q ? a.q_out + ((int64_t)t * a.Hq + h) * D
                     : a.kc + (((int64_t)bseq * a.Hkv + (h - a.Hq)) * a.Lmax + pos) * D;
-  for (int i = lane; i < D; i += 64) {
+  // Each loop's global loads (up to D / 64 = 4 per lane) go out before its
+  // stores: a load after a store the compiler cannot tell apart from it
+  // would wait for that store, one round trip per element.
+  constexpr int NE = 4;  // D <= 256
+  float fr[NE], gq[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const int i = lane + 64 * e;
+    fr[e] = i < a.rot ? a.freqs[i < half ? i : i - half] : 0.f;
+    gq[e] = i < D ? (is_q ? ld(a.qg, src + D + i, a.src_f32)
+                          : ld(a.vp, (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D + i, a.src_f32))
+                  : 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const int i = lane + 64 * e;
+    if (i >= D) continue;
     float y = row[i];
     if (i < a.rot) {
-      const int fi = i < half ? i : i - half;
       float sn, cs;
-      sincosf((float)pos * a.freqs[fi], &sn, &cs);
+      sincosf((float)pos * fr[e], &sn, &cs);
       y = i < half ? row[i] * cs - row[i + half] * sn : row[i] * cs + row[i - half] * sn;
     }
     dst[i] = y;
   }
   if (is_q) {
-    for (int i = lane; i < D; i += 64)
-      a.gate_out[(int64_t)t * a.Hq * D + (int64_t)h * D + i] = sigmoid_f32(ld(a.qg, src + D + i, a.src_f32));
+    float *go = a.gate_out + (int64_t)t * a.Hq * D + (int64_t)h * D;
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+      if (lane + 64 * e < D) go[lane + 64 * e] = sigmoid_f32(gq[e]);
   } else {
-    const int64_t vs = (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
     float *vd = a.vc + (((int64_t)bseq * a.Hkv + (h - a.Hq)) * a.Lmax + pos) * D;
-    for (int i = lane; i < D; i += 64) vd[i] = ld(a.vp, vs + i, a.src_f32);
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+      if (lane + 64 * e < D) vd[lane + 64 * e] = gq[e];
   }
 }
 
