@@ -92,6 +92,10 @@ struct GemvArgs {
   // ss_out[g * ss_ld + b]): the rows of the whole product when the host runs
   // it in chunks of rows (the pointers then start at the chunk)
   int ss_ld;
+  // F32-compute kernels: grid row blockIdx.y takes rows [blockIdx.y *
+  // chunk_rows, min(M, (blockIdx.y + 1) * chunk_rows)) (x, y and the
+  // sum-of-squares pointers start at row 0 of the whole product)
+  int chunk_rows;
 };
 
 // Grouped launch: several independent products, each with its own operands
@@ -235,13 +239,169 @@ __device__ __forceinline__ void lds_dma16(const void *g, void *l_base) {
 // parts, hi = bf16(v) in LDS row b and lo = bf16(v - hi) in row LO + b
 // (|v - hi - lo| <= 2^-17 |v|), with v the row value (x_mode 0) or its
 // RMSNorm (h * factor) * w (modes 1, 3, the f32 value the reference's norm
-// produces). Pieces of 8 values, SB of them loaded before any is stored.
+// produces), and the workgroup's nsc grouped scales (ss[row_in_block * gps +
+// g_local], see gemv_w8). Pieces of 8 values, SB per thread per round.
+//
+// stage_x_fc_impl (short inputs): the scales, the norm's sum-of-squares
+// partials (mode 3) and the first round of pieces are requested before any
+// of them is used, so they share one memory round trip with the first weight
+// group. They are raw buffer loads: a lane past the end reads an offset
+// beyond its buffer's size and gets zeros without touching memory, so no
+// lane branches around them (a load under a branch made the compiler wait
+// for it at once, to copy its register at the join). The mode is
+// compile-time, so the idle lanes issue no loads their mode does not use
+// (zero-filled returns still take the return path's cycles: with them,
+// one-row launches ran 0.3-0.7 us slower).
 __device__ __forceinline__ void norm_row_scales(const GemvArgs &a, float *row_scale, float *red);
-__device__ __forceinline__ void stage_x_fc(const GemvArgs &a, uint16_t *xs, int k0, int Kc, int LO) {
+template <int NT, int MODE, int SB>
+__device__ __forceinline__ void stage_x_fc_impl(const GemvArgs &a, uint16_t *xs, float *ss, int k0,
+                                                int Kc, int LO, int nsc, int rows0, int gps) {
   const int ldx = Kc + kXPad;
   const int per_row = Kc / 8;
   const int total = a.M * per_row;
-  const int nt = blockDim.x;
+  constexpr bool norm = MODE != 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int NWV = NT / 64;
+  __shared__ float red[4];
+  __shared__ float row_scale[16];
+  constexpr uint32_t kOob = 0x80000000u;
+  const int groups = a.K / a.G, g0 = k0 / a.G;
+  const int gpsd = gps > 0 ? gps : 1;
+  auto scale_off = [&](int i) {  // byte offset of staged scale i (kOob past nsc)
+    const int rr = i / gpsd, gl = i - rr * gpsd;
+    return i < nsc ? (uint32_t)(min(rows0 + rr, a.N - 1) * groups + g0 + gl) * 4u : kOob;
+  };
+  const auto srsrc = buf_rsrc(a.scale, (uint32_t)(a.N * groups) * 4u);
+  float sv[SB];
+#pragma unroll
+  for (int q = 0; q < SB; ++q)
+    sv[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, scale_off(threadIdx.x + q * NT), 0, 0));
+  // mode 3: the first 4 partials (p = lane + 64 s) of this wave's first SB
+  // rows (b = wave + r NWV)
+  float t0[SB][4];
+  if constexpr (MODE == 3) {
+    const auto trsrc =
+        buf_rsrc(a.ss_in, a.ss_parts > 0 ? (uint32_t)((a.ss_parts - 1) * a.ss_ld + a.M) * 4u : 0u);
+#pragma unroll
+    for (int r = 0; r < SB; ++r) {
+      const int b = wave + r * NWV;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int pp = lane + 64 * q;
+        const uint32_t off = b < a.M && pp < a.ss_parts ? (uint32_t)(pp * a.ss_ld + b) * 4u : kOob;
+        t0[r][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trsrc, off, 0, 0));
+      }
+    }
+  }
+  u32x4 hv[SB][2], wv[SB][2];
+  const auto xrsrc = buf_rsrc((const float *)a.x + a.x_off + k0, (uint32_t)((a.M - 1) * a.x_stride + Kc) * 4u);
+  const auto wrsrc = buf_rsrc(norm ? a.norm_w + k0 : (const float *)a.x, norm ? (uint32_t)Kc * 4u : 0u);
+  auto load_pieces = [&](int i0) {
+#pragma unroll
+    for (int q = 0; q < SB; ++q) {
+      const int i = i0 + q * NT;
+      const int b = i / per_row, kk = (i - b * per_row) * 8;
+      const uint32_t xo = i < total ? (uint32_t)(b * a.x_stride + kk) * 4u : kOob;
+      hv[q][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, xo, 0, 0));
+      hv[q][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, xo + 16u, 0, 0));
+      if constexpr (norm) {
+        const uint32_t wo = i < total ? (uint32_t)kk * 4u : kOob;
+        wv[q][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, wo, 0, 0));
+        wv[q][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, wo + 16u, 0, 0));
+      }
+    }
+  };
+  auto store_pieces = [&](int i0) {
+#pragma unroll
+    for (int q = 0; q < SB; ++q) {
+      const int i = i0 + q * NT;
+      if (i < total) {
+        const int b = i / per_row, kk = (i - b * per_row) * 8;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = __uint_as_float(hv[q][0][e]);
+          v[4 + e] = __uint_as_float(hv[q][1][e]);
+        }
+        if constexpr (norm) {
+          const float sc = row_scale[b];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = (v[e] * sc) * __uint_as_float(wv[q][0][e]);
+            v[4 + e] = (v[4 + e] * sc) * __uint_as_float(wv[q][1][e]);
+          }
+        }
+        u32x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float h0 = round_bf16(v[2 * e]), h1 = round_bf16(v[2 * e + 1]);
+          hi[e] = pack_bf16x2(h0, h1);
+          lo[e] = pack_bf16x2(v[2 * e] - h0, v[2 * e + 1] - h1);
+        }
+        *(u32x4 *)(xs + b * ldx + kk) = hi;
+        *(u32x4 *)(xs + (LO + b) * ldx + kk) = lo;
+      }
+    }
+  };
+  load_pieces(threadIdx.x);
+  // scales to LDS (rows past N weigh 0; any beyond SB per thread in a loop)
+#pragma unroll
+  for (int q = 0; q < SB; ++q) {
+    const int i = threadIdx.x + q * NT;
+    if (i < nsc) ss[i] = rows0 + i / gpsd < a.N ? sv[q] : 0.f;
+  }
+  for (int i = threadIdx.x + SB * NT; i < nsc; i += NT)
+    ss[i] = rows0 + i / gpsd < a.N ? a.scale[scale_off(i) / 4u] : 0.f;
+  if constexpr (MODE == 3) {
+    // one wave per row, lane l adding partials l, l + 64, ... in that order,
+    // then a fixed butterfly (deterministic)
+    auto row_sum = [&](int b, const float(&tf)[4], bool pre) {
+      float sum = 0.f;
+      for (int p0 = lane; p0 < a.ss_parts; p0 += 256) {
+        float t[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          t[q] = pre && p0 == lane ? tf[q] : a.ss_in[(int64_t)min(p0 + 64 * q, a.ss_parts - 1) * a.ss_ld + b];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (p0 + 64 * q < a.ss_parts) sum += t[q];
+      }
+      sum = wave_sum64(sum);
+      if (lane == 0) row_scale[b] = 1.0f / sqrtf(sum / (float)a.K + a.eps);
+    };
+#pragma unroll
+    for (int r = 0; r < SB; ++r)
+      if (wave + r * NWV < a.M) row_sum(wave + r * NWV, t0[r], true);
+    for (int b = wave + SB * NWV; b < a.M; b += NWV) row_sum(b, t0[0], false);
+  } else if constexpr (MODE == 1) {
+    norm_row_scales(a, row_scale, red);
+  }
+  if constexpr (norm) __syncthreads();
+  store_pieces(threadIdx.x);
+  for (int i0 = threadIdx.x + SB * NT; i0 < total; i0 += SB * NT) {
+    load_pieces(i0);
+    store_pieces(i0);
+  }
+}
+// stage_x_fc_rounds (longer inputs): the scales, then the norm factors, then
+// rounds of SB = 2 pieces per thread, each a memory round trip after the one
+// before (measured faster there than two batches requested up front: the
+// Qwen3.5-0.8B forward at 16 rows, 1.39 against 1.42 ms).
+template <int NT>
+__device__ __forceinline__ void stage_x_fc_rounds(const GemvArgs &a, uint16_t *xs, float *ss, int k0, int Kc,
+                                                  int LO, int nsc, int rows0, int gps) {
+  if (nsc > 0) {
+    const int groups = a.K / a.G, g0 = k0 / a.G;
+    for (int i = threadIdx.x; i < nsc; i += NT) {
+      const int rr = i / gps, gl = i - rr * gps;
+      const int n = rows0 + rr;
+      ss[i] = n < a.N ? a.scale[(int64_t)n * groups + g0 + gl] : 0.f;
+    }
+  }
+  const int ldx = Kc + kXPad;
+  const int per_row = Kc / 8;
+  const int total = a.M * per_row;
+  const int nt = NT;
   const bool norm = a.x_mode == 1 || a.x_mode == 3;
   __shared__ float red[4];
   __shared__ float row_scale[16];
@@ -292,6 +452,23 @@ __device__ __forceinline__ void stage_x_fc(const GemvArgs &a, uint16_t *xs, int 
       }
     }
   }
+}
+
+// One straight-line prologue per mode when one batch of pieces and scales
+// per thread covers the rows (up to a few rows: the Qwen3.5-0.8B forward at
+// one row 0.892 against 0.904 ms staged in rounds), else rounds.
+template <int NT>
+__device__ __forceinline__ void stage_x_fc(const GemvArgs &a, uint16_t *xs, float *ss, int k0, int Kc,
+                                           int LO, int nsc, int rows0, int gps) {
+  const bool one = a.M * (Kc / 8) <= NT && nsc <= NT && a.M <= NT / 64;
+  if (!one)
+    stage_x_fc_rounds<NT>(a, xs, ss, k0, Kc, LO, nsc, rows0, gps);
+  else if (a.x_mode == 3)
+    stage_x_fc_impl<NT, 3, 1>(a, xs, ss, k0, Kc, LO, nsc, rows0, gps);
+  else if (a.x_mode == 1)
+    stage_x_fc_impl<NT, 1, 1>(a, xs, ss, k0, Kc, LO, nsc, rows0, gps);
+  else
+    stage_x_fc_impl<NT, 0, 1>(a, xs, ss, k0, Kc, LO, nsc, rows0, gps);
 }
 
 // RMSNorm factors 1/sqrt(mean(h^2) + eps) of rows [0, M) into row_scale
@@ -745,18 +922,19 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a, const int blk) {
   } else {
     // Grouped scales of this workgroup's rows and K-split, staged after x:
     // ss[row_in_block * gps + g_local] (f32).
-    if (!per_channel) {
-      const int g0 = k0 / a.G;
-      for (int i = threadIdx.x; i < 16 * RW * gps; i += blockDim.x) {
-        const int rr = i / gps, gl = i - rr * gps;
-        const int n = rows0 + rr;
-        ss[i] = n < a.N ? a.scale[(int64_t)n * groups + g0 + gl] : 0.f;
+    if (FC) {
+      stage_x_fc<NW * 64>(a, xs, ss, k0, Kc, LO, per_channel ? 0 : 16 * RW * gps, rows0, gps);
+    } else {
+      if (!per_channel) {
+        const int g0 = k0 / a.G;
+        for (int i = threadIdx.x; i < 16 * RW * gps; i += blockDim.x) {
+          const int rr = i / gps, gl = i - rr * gps;
+          const int n = rows0 + rr;
+          ss[i] = n < a.N ? a.scale[(int64_t)n * groups + g0 + gl] : 0.f;
+        }
       }
-    }
-    if (FC)
-      stage_x_fc(a, xs, k0, Kc, LO);
-    else
       stage_x(a, xs, k0, Kc);
+    }
     __syncthreads();
   }
 
@@ -1156,10 +1334,25 @@ RXW8_GEMV_BF16_RN(4, 1)
 
 // F32-compute variants (packed weights, up to 16 rows as 2 x 16 staged
 // rows, MB = 2; up to 8 rows as 2 x 8, MB = 1). Names: plain name + "_fc".
+// Workgroup (x, y) runs tile x over row chunk y, so the chunks of a longer
+// input run side by side (they write disjoint rows). (No gridDim or division
+// here: reading the grid size put a vector load and its wait in front of the
+// first weight group's use.)
+template <int MB, int RW, int U, int NW>
+__device__ __forceinline__ void gemv_fc_rows(const GemvArgs &a) {
+  const int m0 = (int)blockIdx.y * a.chunk_rows;
+  GemvArgs c = a;
+  c.x = (const float *)a.x + m0 * a.x_stride;
+  c.y = (float *)a.y + (int64_t)m0 * (a.y_mode == 2 ? a.N / 2 : a.N);
+  if (a.ss_out) c.ss_out = a.ss_out + m0;
+  if (a.ss_in) c.ss_in = a.ss_in + m0;
+  c.M = min(a.chunk_rows, a.M - m0);
+  gemv_w8<MB, RW, U, true, NW, false, false, true>(c, blockIdx.x);
+}
 #define RXW8_GEMV_FC_WIDE(MB, RW, U, NW)                                        \
   extern "C" __global__ void __launch_bounds__(NW * 64)                         \
       rxw8_gemv_w8_pk_mb##MB##_rw##RW##_u##U##_w##NW##_fc(GemvArgs a) {         \
-    gemv_w8<MB, RW, U, true, NW, false, false, true>(a, blockIdx.x);                        \
+    gemv_fc_rows<MB, RW, U, NW>(a);                                             \
   }
 #define RXW8_GEMV_FC_WIDE_U(MB, RW, NW) \
   RXW8_GEMV_FC_WIDE(MB, RW, 4, NW)      \
@@ -1169,7 +1362,7 @@ RXW8_GEMV_BF16_RN(4, 1)
 #define RXW8_GEMV_FC4(MB, RW, U)                                                \
   extern "C" __global__ void __launch_bounds__(256)                             \
       rxw8_gemv_w8_pk_mb##MB##_rw##RW##_u##U##_fc(GemvArgs a) {                 \
-    gemv_w8<MB, RW, U, true, 4, false, false, true>(a, blockIdx.x);                         \
+    gemv_fc_rows<MB, RW, U, 4>(a);                                              \
   }
 #define RXW8_GEMV_FC_MB(MB)      \
   RXW8_GEMV_FC4(MB, 1, 8)        \

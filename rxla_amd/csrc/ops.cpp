@@ -38,6 +38,7 @@ struct GemvArgs {
   const float *xw_norm;
   uint16_t *xw_out;
   int ss_ld;  // row stride of the sum-of-squares partials
+  int chunk_rows;  // F32-compute kernels: rows per grid row (blockIdx.y)
 };
 
 struct PackArgs {
@@ -506,6 +507,7 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
     a.xw_norm = pro->xw_norm;
     a.xw_out = pro->xw_out;
     a.ss_ld = (int)M;  // (ss modes run as one chunk of rows)
+    a.chunk_rows = (int)mm;
     // bf16 rows whose split is whole 512-element runs, 16-byte aligned, are
     // staged by LDS DMA (B = 16, K = 4096: 8.9 -> 7.4 us for N = 4096).
     // RXW8_GEMV_LDS_DMA=0 turns it off.
@@ -538,10 +540,10 @@ static int run_gemv(Runtime *rt, const void *x, int x_f32, const void *w, bool w
 // prologues 1 / 3), packed u8 weights, f32 y (y_mode 0), f32 residual
 // (y_mode 1, optional ss_out) or f32 SwiGLU activation (y_mode 2, interleaved
 // gate|up tiles). Each f32 row is staged as two bf16 rows (hi, lo), so a
-// launch takes up to 16 rows (2 x 16 staged rows), or 8 when 32 staged rows
-// of K do not fit in LDS; longer inputs run in chunks of rows (the ss
-// partials then carry the whole product's row stride). UNIMPLEMENTED (nothing
-// launched) when no single-launch plan fits.
+// workgroup takes up to 16 rows (2 x 16 staged rows), or 8 when 32 staged
+// rows of K do not fit in LDS; longer inputs run as chunks of rows side by
+// side in the same launch (the ss partials carry the whole product's row
+// stride). UNIMPLEMENTED (nothing launched) when no single-launch plan fits.
 static int run_gemv_fc(Runtime *rt, const float *x, const uint8_t *w, const float *scale, float *y,
                        int64_t M, int64_t N, int64_t K, int64_t G, int y_mode, const GemvOptions *pro) {
   GemvOptions plain;
@@ -552,8 +554,10 @@ static int run_gemv_fc(Runtime *rt, const float *x, const uint8_t *w, const floa
     return RXW8_UNIMPLEMENTED;
   const bool allow_wide = pro->mode != 1;  // mode 1 sums rows with 256-thread reductions
   GemvPlan p;
-  int rows = 0;  // staged rows per launch: 2 x 16 or 2 x 8
-  for (int r : {M > 8 ? 32 : 16, 16}) {
+  int rows = 0;  // staged rows per workgroup: 2 x 16 or 2 x 8
+  // RXW8_GEMV_FC_ROWS=8 takes chunks of 8 rows also where 16 would fit
+  static const int rows_env = env_int("RXW8_GEMV_FC_ROWS", 0);
+  for (int r : {M > 8 && rows_env != 8 ? 32 : 16, 16}) {
     GemvPlan q = plan_gemv(rt, r, N, K, G, false, true, allow_wide);
     if (q.ks == 1 && q.lds + 256 <= rt->lds_max) {
       p = q;
@@ -567,36 +571,44 @@ static int run_gemv_fc(Runtime *rt, const float *x, const uint8_t *w, const floa
   if (p.nw != 4) std::snprintf(wide, sizeof wide, "_w%d", p.nw);
   std::snprintf(kname, sizeof kname, "rxw8_gemv_w8_pk_mb%d_rw%d_u%d%s_fc", (int)mb, p.rw, p.u, wide);
   const int64_t xstride = pro->stride > 0 ? pro->stride : K;
-  const int64_t ycols = pro->swiglu ? N / 2 : N;
-  for (int64_t m0 = 0; m0 < M; m0 += mchunk) {
-    const int64_t mm = std::min(mchunk, M - m0);
-    GemvArgs a{};
-    a.x = x + m0 * xstride;
-    a.w = w;
-    a.scale = scale;
-    a.y = y + m0 * ycols;
-    a.M = (int)mm;
-    a.N = (int)N;
-    a.K = (int)K;
-    a.G = (int)G;
-    a.ksplit = 1;
-    a.x_f32 = 1;
-    a.y_f32 = 1;
-    a.y_mode = pro->swiglu ? 2 : y_mode;
-    a.ss_out = pro->ss_out ? pro->ss_out + m0 : nullptr;
-    a.x_mode = pro->mode;
-    a.x_stride = xstride;
-    a.x_off = pro->off;
-    a.norm_w = pro->norm_w;
-    a.eps = pro->eps;
-    a.ss_in = pro->ss_in ? pro->ss_in + m0 : nullptr;
-    a.ss_parts = pro->ss_parts;
-    a.ss_ld = (int)M;
-    const size_t lds = gemv_lds(rows, K, K, G, p.rw, (int)mb, false, p.nw);
-    int rc = launch(rt, kname, dim3((unsigned)((N + 16 * p.rw - 1) / (16 * p.rw))), dim3(64 * p.nw), a, lds);
-    if (rc) return rc;
-  }
-  return RXW8_OK;
+  // Longer inputs: one launch whose grid holds a row of tiles per chunk of
+  // rows (blockIdx.y), so the chunks run side by side (each workgroup re-reads
+  // its weight tile, mostly from the caches; 2 x 8 rows of the Qwen3.5-0.8B
+  // down projection, K = 3584: one launch of 8.96 us instead of two of 7.96)
+  const int64_t chunks = (M + mchunk - 1) / mchunk;
+  const int64_t tiles = (N + 16 * p.rw - 1) / (16 * p.rw);
+  if (tiles * chunks >= ((int64_t)1 << 31) || chunks > 65535) return RXW8_UNIMPLEMENTED;
+  // the staging reads x, the scales and the sum-of-squares partials through
+  // raw buffer loads (32-bit byte offsets)
+  constexpr int64_t kBufMax = (int64_t)1 << 31;
+  if (((M - 1) * xstride + pro->off + K) * 4 >= kBufMax || N * (K / G) * 4 >= kBufMax ||
+      (pro->mode == 3 && ((int64_t)pro->ss_parts * M) * 4 >= kBufMax))
+    return RXW8_UNIMPLEMENTED;
+  GemvArgs a{};
+  a.x = x;
+  a.w = w;
+  a.scale = scale;
+  a.y = y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.G = (int)G;
+  a.ksplit = 1;
+  a.x_f32 = 1;
+  a.y_f32 = 1;
+  a.y_mode = pro->swiglu ? 2 : y_mode;
+  a.ss_out = pro->ss_out;
+  a.x_mode = pro->mode;
+  a.x_stride = xstride;
+  a.x_off = pro->off;
+  a.norm_w = pro->norm_w;
+  a.eps = pro->eps;
+  a.ss_in = pro->ss_in;
+  a.ss_parts = pro->ss_parts;
+  a.ss_ld = (int)M;
+  a.chunk_rows = (int)mchunk;
+  const size_t lds = gemv_lds(rows, K, K, G, p.rw, (int)mb, false, p.nw);
+  return launch(rt, kname, dim3((unsigned)tiles, (unsigned)chunks), dim3(64 * p.nw), a, lds);
 }
 
 bool gemv_single_launch(const Runtime *rt, int64_t M, int64_t N, int64_t K, int64_t G) {

@@ -196,14 +196,18 @@ def run_linear_packed_f32(rt, x, u8, s):
 
 @pytest.mark.parametrize("m,n,k,g", [(1, 1024, 1024, 128), (5, 4096, 1024, 128), (8, 256, 2048, 2048),
                                      (9, 7168, 1024, 128), (16, 1024, 2048, 128),
-                                     # 32 staged rows of K do not fit: launches of 8 rows
-                                     (16, 1024, 3584, 128),
+                                     # 32 staged rows of K do not fit: chunks of 8 rows
+                                     (16, 1024, 3584, 128), (40, 1024, 3584, 128),
                                      # chunks of 16 rows
                                      (37, 512, 1024, 64)])
-def test_f32_compute_packed_gemv(rt, m, n, k, g):
+def test_f32_compute_packed_gemv(rt, monkeypatch, m, n, k, g):
     """F32 compute on packed weights: the GEMV stages each f32 row as bf16
     hi and lo rows (batch columns t and 8 / 16 + t), multiplies the exact
-    codes u - 128 and adds the two parts in f32 (no bf16 rounding)."""
+    codes u - 128 and adds the two parts in f32 (no bf16 rounding). Inputs
+    longer than one workgroup's rows run as chunks of rows side by side in
+    one launch (beyond 16 rows the GEMM tiles are switched off here)."""
+    if m > 16:
+        monkeypatch.setenv("RXW8_F32_GEMM", "0")
     rng = np.random.default_rng(m * 11 + n + k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     u8, s = quantized(rng, n, k, g)
