@@ -139,19 +139,23 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_linear_generic(GenericLin
 // row per wave load) with PF loads in flight, all other reads being LDS. The
 // 16 codes of a slice are the B operands of two MFMAs (k permuted identically
 // in A and B). Rows of x >= T and channels >= N read clamped, valid addresses
-// and are never stored.
+// and are never stored. PK: the weights in the GEMV tile layout ([N / 16]
+// [K / 64] tiles of 1 KiB, lane l's 16 bytes at l * 16: row l % 16, k 16 (l /
+// 16) of the tile), so each wave load is one contiguous KiB (nontemporal)
+// instead of 16 rows x 64 bytes.
 struct LinearF32Args {
   const float *x;      // [T, K] rows of ldx elements
-  const uint8_t *w;    // [N, K] rows of ldw bytes
+  const uint8_t *w;    // [N, K] rows of ldw bytes (PK: tile (0, k0 / 64) of the K range)
   const float *scale;  // [N, K / G] rows of ldsc elements
   float *y;            // [T, N]
   int T, N, K, G;
   int y_mode;          // 0: y = result; 1: y += result (f32 residual)
   int tiles;           // channel tiles (16 WV channels each) per workgroup
-  int64_t ldx, ldw, ldsc;  // row strides: a K-range of a wider product (host K chunks)
+  int64_t ldx, ldw, ldsc;  // row strides: a K-range of a wider product (host K chunks);
+                           // PK: ldw = 64-k tiles per 16-row group
 };
 
-template <int R, int WV>
+template <int R, int WV, bool PK = false>
 __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
   constexpr int PF = 8;
   extern __shared__ __attribute__((aligned(16))) uint16_t f32lin_lds[];
@@ -190,7 +194,14 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
   __syncthreads();
   // ---- stream the weight rows
   const int nrow = min(n0 + 16 * wv + col, a.N - 1);
-  const uint8_t *wp = a.w + (int64_t)nrow * a.ldw + 16 * part;
+  // (PK: the wave's 16-row group, clamped like the rows; N % 16 == 0)
+  const uint8_t *wp = PK ? a.w + (int64_t)min((n0 + 16 * wv) / 16, a.N / 16 - 1) * a.ldw * 1024 + lane * 16
+                         : a.w + (int64_t)nrow * a.ldw + 16 * part;
+  constexpr int wstep = PK ? 1024 : 64;  // bytes from one 64-k step to the next
+  auto wload = [&](int st) {
+    const u32x4 *p = (const u32x4 *)(wp + (int64_t)wstep * st);
+    return PK ? __builtin_nontemporal_load(p) : *p;
+  };
   const float *scl = sc + (16 * wv + col) * ng;
   f32x4 acc[R], accg[R];
 #pragma unroll
@@ -236,13 +247,13 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
   // consumed (clamped to the last slice at the end: re-reads of cached bytes)
   u32x4 buf[PF];
 #pragma unroll
-  for (int j = 0; j < PF; ++j) buf[j] = *(const u32x4 *)(wp + 64 * min(j, steps - 1));
+  for (int j = 0; j < PF; ++j) buf[j] = wload(min(j, steps - 1));
   int s0 = 0;
   for (; s0 + PF <= steps; s0 += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const u32x4 cur = buf[j];
-      buf[j] = *(const u32x4 *)(wp + 64 * min(s0 + j + PF, steps - 1));
+      buf[j] = wload(min(s0 + j + PF, steps - 1));
       step(cur, s0 + j);
     }
   }
@@ -270,6 +281,10 @@ __device__ __forceinline__ void linear_f32_mfma(const LinearF32Args &a) {
   extern "C" __global__ void __launch_bounds__(64 * WV)                                 \
       rxw8_linear_f32_mfma_r##R##_w##WV(LinearF32Args a) {                              \
     linear_f32_mfma<R, WV>(a);                                                          \
+  }                                                                                     \
+  extern "C" __global__ void __launch_bounds__(64 * WV)                                 \
+      rxw8_linear_f32_mfma_pk_r##R##_w##WV(LinearF32Args a) {                           \
+    linear_f32_mfma<R, WV, true>(a);                                                    \
   }
 RXW8_LINEAR_F32(1, 8)
 RXW8_LINEAR_F32(2, 8)

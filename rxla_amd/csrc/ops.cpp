@@ -722,17 +722,19 @@ static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bo
 }
 
 // QuantizedLinear with compute dtype F32 on the matrix cores (x split into
-// bf16 hi + lo parts, exact codes, f32 accumulation): f32 x, row-major U8
-// weights, K and G multiples of 64, 16-byte aligned operands and the staged
-// rows of x within the LDS limit. Returns UNIMPLEMENTED otherwise.
-static int run_linear_f32(Runtime *rt, const float *x, const uint8_t *w, const float *scale,
-                          float *y, int64_t M, int64_t N, int64_t K, int64_t G, int y_mode) {
+// bf16 hi + lo parts, exact codes, f32 accumulation): f32 x, row-major or
+// packed (N % 16 == 0) U8 weights, K and G multiples of 64, 16-byte aligned
+// operands and the staged rows of x within the LDS limit. Returns
+// UNIMPLEMENTED otherwise.
+static int run_linear_f32(Runtime *rt, const float *x, const uint8_t *w, bool packed,
+                          const float *scale, float *y, int64_t M, int64_t N, int64_t K, int64_t G,
+                          int y_mode) {
   {
-    const int rc = run_linear_f32_gemm(rt, x, w, false, scale, y, M, N, K, G, y_mode);
+    const int rc = run_linear_f32_gemm(rt, x, w, packed, scale, y, M, N, K, G, y_mode);
     if (rc != RXW8_UNIMPLEMENTED) return rc;
   }
   if (K % 64 != 0 || G % 64 != 0 || K > (1 << 24) || N > (1LL << 30) || M > (1LL << 30) ||
-      ((uintptr_t)x | (uintptr_t)w) % 16 != 0 || env_int("RXW8_FORCE_GENERIC", 0))
+      ((uintptr_t)x | (uintptr_t)w) % 16 != 0 || (packed && N % 16) || env_int("RXW8_FORCE_GENERIC", 0))
     return RXW8_UNIMPLEMENTED;
   constexpr int WV = 8;
   // x (hi and lo) of the workgroup's rows is staged in LDS for its K range:
@@ -768,11 +770,13 @@ static int run_linear_f32(Runtime *rt, const float *x, const uint8_t *w, const f
     const int64_t ntiles = (N + 16 * WV - 1) / (16 * WV);
     const int64_t per = std::max<int64_t>(1, std::min<int64_t>(16, ntiles * gy / 2048));
     char kname[40];
-    std::snprintf(kname, sizeof kname, "rxw8_linear_f32_mfma_r%d_w%d", R, WV);
+    std::snprintf(kname, sizeof kname, "rxw8_linear_f32_mfma%s_r%d_w%d", packed ? "_pk" : "", R, WV);
     for (int64_t k0 = 0; k0 < K; k0 += kc_max) {
       const int64_t kc = std::min(kc_max, K - k0);
-      LinearF32Args a{x + k0, w + k0, scale + k0 / G, y, (int)M, (int)N, (int)kc, (int)gk,
-                      k0 == 0 ? y_mode : 1, (int)per, K, K, K / G};
+      // packed: the K range starts at tile column k0 / 64 of row group 0, and
+      // a row group holds K / 64 tiles
+      LinearF32Args a{x + k0, packed ? w + k0 / 64 * 1024 : w + k0, scale + k0 / G, y, (int)M, (int)N,
+                      (int)kc, (int)gk, k0 == 0 ? y_mode : 1, (int)per, K, packed ? K / 64 : K, K / G};
       int rc = launch(rt, kname, dim3((unsigned)((ntiles + per - 1) / per), (unsigned)gy),
                       dim3(64 * WV), a, lds_for(R, kc, gk));
       if (rc) return rc;
@@ -959,6 +963,12 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
     if (!compute_bf16 && x_f32 && y_f32) {
       const int rc = run_linear_f32_gemm(rt, (const float *)x, w, true, s, (float *)y, M, N, K, G, y_mode);
       if (rc != RXW8_UNIMPLEMENTED) return rc;
+      // many channel tiles (an LM head): the row kernel that stages x once
+      // per workgroup for several 128-channel tiles
+      if (N / 128 >= 4 * (int64_t)rt->cus) {
+        const int rl = run_linear_f32(rt, (const float *)x, w, true, s, (float *)y, M, N, K, G, y_mode);
+        if (rl != RXW8_UNIMPLEMENTED) return rl;
+      }
     }
     int rc = compute_bf16 ? run_gemv(rt, x, x_f32, w, false, true, s, y, y_f32, M, N, K, G, y_mode)
              : x_f32 && y_f32
@@ -972,7 +982,7 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
     return rc;
   }
   if (!compute_bf16 && x_f32 && y_f32) {
-    int rc = run_linear_f32(rt, (const float *)x, w, s, (float *)y, M, N, K, G, y_mode);
+    int rc = run_linear_f32(rt, (const float *)x, w, false, s, (float *)y, M, N, K, G, y_mode);
     if (rc != RXW8_UNIMPLEMENTED) return rc;
   }
   const bool mfma_ok = compute_bf16 && K % 64 == 0 && N % 16 == 0 && (G == K || G % 64 == 0) &&

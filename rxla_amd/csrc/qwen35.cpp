@@ -225,6 +225,9 @@ struct Qwen35 {
   // the fused projection weights (built when the last parameter is bound)
   void *block = nullptr;
   void *fused = nullptr;
+  // the tied head's table in the GEMV tile layout (packed and F32-compute
+  // models, V % 16 == 0), read by the head of inputs up to 16 rows
+  uint8_t *head_pk = nullptr;
   int64_t n_in_max = 0;
   bool packed = false;  // BF16 compute and widths that allow the tile layout (decided at create)
   // F32 compute and widths that allow the tile layout: packed copies beside
@@ -666,8 +669,10 @@ int enqueue_forward(Qwen35 *m, const int32_t *ids, float *logits, int64_t B, int
     if ((rc = mlp(m, L, T))) return rc;
   }
   if ((rc = norm(m, m->h, m->f32(m->final_norm), m->fin, T, m->H, true, true))) return rc;
-  // tied head: f32 hidden . f32 dequantised table (compute F32)
-  if ((rc = qlinear_launch(rt, m->fin, 1, (const uint8_t *)m->ptr(m->embed), false,
+  // tied head: f32 hidden . f32 dequantised table (compute F32); up to 16
+  // rows from the tile-layout copy (one contiguous KiB per wave load)
+  const bool hpk = m->head_pk && T <= 16;
+  if ((rc = qlinear_launch(rt, m->fin, 1, hpk ? m->head_pk : (const uint8_t *)m->ptr(m->embed), hpk,
                            m->f32(m->embed + 1), logits, 1, T, m->V, m->H, m->G, 0, 0)))
     return rc;
   if (m->cfg.lora_rank > 0) {
@@ -706,6 +711,8 @@ int prepare(Qwen35 *m) {
     if (m->fc)  // packed copies of the fused input projections and gate|up (+ scales)
       total += al((size_t)L.n_in * m->H) + al((size_t)2 * m->I * m->H) + al((size_t)2 * m->I * ng * 4);
   }
+  const bool head_pk = (m->packed || m->fc) && m->V % 16 == 0 && m->H % 64 == 0;
+  if (head_pk) total += al((size_t)m->V * m->H);
   hipError_t e = hipMalloc(&m->fused, total);
   void *tmp = nullptr;
   if (e == hipSuccess && stage) e = hipMalloc(&tmp, stage);
@@ -789,12 +796,17 @@ int prepare(Qwen35 *m) {
     if ((rc = launch(rt, "rxw8_q35_one_plus", dim3(grid_n(m->H)), dim3(256), s1))) break;
     if ((rc = launch(rt, "rxw8_q35_one_plus", dim3(grid_n(m->H)), dim3(256), s2))) break;
   }
+  if (!rc && head_pk) {
+    m->head_pk = (uint8_t *)take((size_t)m->V * m->H);
+    rc = pack(m->ptr(m->embed), m->head_pk, m->V, m->H, 0);
+  }
   const hipError_t se = hipStreamSynchronize(rt->stream);  // the staging buffer is free after this
   if (tmp) (void)hipFree(tmp);
   if (!rc && se != hipSuccess) rc = hip_fail(se, "hipStreamSynchronize");
   if (rc) {
     (void)hipFree(m->fused);
     m->fused = nullptr;
+    m->head_pk = nullptr;
   }
   return rc;
 }
@@ -854,6 +866,7 @@ void free_model(Qwen35 *m) {
   if (m->block) (void)hipFree(m->block);
   if (m->fused) (void)hipFree(m->fused);
   m->block = m->fused = nullptr;
+  m->head_pk = nullptr;
   for (Param &p : m->params)
     if (p.bound) rxw8_buffer_release(static_cast<rxw8_buffer *>(p.bound));
 }
