@@ -218,6 +218,23 @@ def test_f32_compute_packed_gemv(rt, monkeypatch, m, n, k, g):
     assert err < 1e-5
 
 
+@pytest.mark.parametrize("m", [1, 7, 16])
+def test_f32_compute_packed_many_channels(rt, m):
+    """F32 compute on packed weights with many 128-channel tiles (an LM head,
+    N / 128 >= 4 x 256 CUs): the row kernel that stages x once per workgroup
+    (rxw8_linear_f32_mfma_pk_*), reading the tile layout; a channel count
+    that is not a multiple of 128 (a partial last tile)."""
+    n, k, g = 131072 + 144, 1024, 128
+    rng = np.random.default_rng(m * 7 + 3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    u8, s = quantized(rng, n, k, g)
+    ref = oracle.quantized_linear(x, u8, s, oracle.COMPUTE_F32, oracle.ACCUM_F64)
+    y = run_linear_packed_f32(rt, x, u8, s)
+    err = rel_err(y, ref)
+    print(f"F32 compute packed (row kernel) m={m} n={n} rel_err={err:.3e}")
+    assert err < 1e-5
+
+
 def test_f32_compute_packed_exact_on_integer_inputs(rt):
     """The packed F32 GEMV on the integer case of the row-major path above:
     bit for bit, including the row whose value needs the lo part."""
