@@ -66,6 +66,10 @@ struct Q35NormArgs {
   int64_t rows, L, x_stride, out_stride, z_stride, z_group;
   float eps;
   int zero_centered, out_f32, z_f32;
+  // non-null: instead of out, the F32 GEMM's operand split of each result y,
+  // hi = bf16(y) and lo = bf16(y - hi) at the same index (rxw8_gemm_split_x's
+  // arithmetic, so the GEMM sees the bits the split launch would give it)
+  uint16_t *hi, *lo;
 };
 
 extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a) {
@@ -100,10 +104,15 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a
       if (i >= a.L) continue;
       float y = (xv[e] * sc) * (a.zero_centered ? 1.0f + wv[e] : wv[e]);
       if (a.z) y *= zv[e] * sigmoid_f32(zv[e]);
-      if (a.out_f32)
+      if (a.hi) {
+        const uint16_t h = f32_to_bf16_bits(y);
+        a.hi[r * a.out_stride + i] = h;
+        a.lo[r * a.out_stride + i] = f32_to_bf16_bits(y - bf16_bits_to_f32(h));
+      } else if (a.out_f32) {
         ((float *)a.out)[r * a.out_stride + i] = y;
-      else
+      } else {
         ((uint16_t *)a.out)[r * a.out_stride + i] = f32_to_bf16_bits(y);
+      }
     }
   }
 }

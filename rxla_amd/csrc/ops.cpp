@@ -683,13 +683,27 @@ struct SplitXArgs {
 // / 3.39 ms against 3.95 / 4.61); up to 16 rows the F32 GEMV stays.
 // UNIMPLEMENTED (nothing launched) when the shape or the 16-byte alignment
 // of the weights and y does not fit its contract.
+bool f32_gemm_applies(const void *w, const float *y, int64_t M, int64_t N, int64_t K, int64_t G) {
+  const int env = env_int("RXW8_F32_GEMM", -1);
+  return !(env == 0 || N % 16 || K % 64 || G % 64 || K % G || K / G > 32 || M * K * 2 >= (1LL << 31) ||
+           N * K >= (1LL << 32) || ((uintptr_t)w | (uintptr_t)y) % 16 != 0 || (env < 0 && M <= 16));
+}
+
+// The operand buffers of the F32 GEMM's x parts: hi and lo, [M, K] bf16 each.
+int f32_gemm_operands(Runtime *rt, int64_t M, int64_t K, uint16_t **hi, uint16_t **lo) {
+  const int rc = ensure_workspace(rt, rt->xcast, (size_t)(M * K) * 4, false);
+  if (rc) return rc;
+  *hi = (uint16_t *)rt->xcast.ptr;
+  *lo = *hi + M * K;
+  return RXW8_OK;
+}
+
+// (x == nullptr: the caller has written x's parts into f32_gemm_operands'
+// buffers, e.g. the Qwen3.5 RMSNorm; no split launch)
 static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bool packed,
                                const float *scale, float *y, int64_t M, int64_t N, int64_t K,
                                int64_t G, int y_mode) {
-  const int env = env_int("RXW8_F32_GEMM", -1);
-  if (env == 0 || N % 16 || K % 64 || G % 64 || K % G || K / G > 32 || M * K * 2 >= (1LL << 31) ||
-      N * K >= (1LL << 32) || ((uintptr_t)w | (uintptr_t)y) % 16 != 0)
-    return RXW8_UNIMPLEMENTED;
+  if (!f32_gemm_applies(w, y, M, N, K, G)) return RXW8_UNIMPLEMENTED;
   const int64_t tiles = (M + 127) / 128 * ((N + 255) / 256);
   // split units: scale groups, or the k tiles of a single group
   const int64_t ng = K / G, units = ng > 1 ? ng : K / 64, upt = ng > 1 ? G / 64 : 1;
@@ -704,13 +718,12 @@ static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bo
       if (tiles * c >= rt->cus) break;
     }
   }
-  if (env < 0 && M <= 16) return RXW8_UNIMPLEMENTED;
-  int rc = ensure_workspace(rt, rt->xcast, (size_t)(M * K) * 4, false);
+  uint16_t *xh, *xl;
+  int rc = f32_gemm_operands(rt, M, K, &xh, &xl);
   if (rc) return rc;
   if (ks > 1 && (rc = ensure_workspace(rt, rt->partials, (size_t)(ks * M * N) * 4, false))) return rc;
-  uint16_t *xh = (uint16_t *)rt->xcast.ptr, *xl = xh + M * K;
   SplitXArgs sx{x, xh, xl, M * K};
-  if ((rc = launch(rt, "rxw8_gemm_split_x", dim3(grid_for(M * K / 4, 256, 4096)), dim3(256), sx)))
+  if (x && (rc = launch(rt, "rxw8_gemm_split_x", dim3(grid_for(M * K / 4, 256, 4096)), dim3(256), sx)))
     return rc;
   LinearF32GemmArgs a{xh, xl, w, scale, y, (int)M, (int)N, (int)K, (int)G, y_mode, packed ? 1 : 0,
                       (int)ks, ks > 1 ? (float *)rt->partials.ptr : nullptr};
@@ -719,6 +732,13 @@ static int run_linear_f32_gemm(Runtime *rt, const float *x, const uint8_t *w, bo
   if (ks == 1) return RXW8_OK;
   F32ReduceArgs r{(const float *)rt->partials.ptr, y, M * N, (int)ks, y_mode};
   return launch(rt, "rxw8_gemm_f32c_reduce", dim3(grid_for(M * N / 4, 256, 4096)), dim3(256), r);
+}
+
+// The F32 GEMM on operands already split into f32_gemm_operands' buffers
+// (f32_gemm_applies must hold).
+int f32_gemm_presplit(Runtime *rt, const uint8_t *w, bool packed, const float *scale, float *y,
+                      int64_t M, int64_t N, int64_t K, int64_t G, int y_mode) {
+  return run_linear_f32_gemm(rt, nullptr, w, packed, scale, y, M, N, K, G, y_mode);
 }
 
 // QuantizedLinear with compute dtype F32 on the matrix cores (x split into

@@ -49,6 +49,10 @@ int qlinear_launch(Runtime *rt, const void *x, int x_f32, const uint8_t *w, bool
                    const float *s, void *y, int y_f32, int64_t M, int64_t N, int64_t K,
                    int64_t G, int compute_bf16, int y_mode);
 bool gemm_eligible(int64_t M, int64_t N, int64_t K, int64_t G);
+bool f32_gemm_applies(const void *w, const float *y, int64_t M, int64_t N, int64_t K, int64_t G);
+int f32_gemm_operands(Runtime *rt, int64_t M, int64_t K, uint16_t **hi, uint16_t **lo);
+int f32_gemm_presplit(Runtime *rt, const uint8_t *w, bool packed, const float *scale, float *y,
+                      int64_t M, int64_t N, int64_t K, int64_t G, int y_mode);
 
 namespace {
 
@@ -74,6 +78,7 @@ struct Q35NormArgs {
   int64_t rows, L, x_stride, out_stride, z_stride, z_group;
   float eps;
   int zero_centered, out_f32, z_f32;
+  uint16_t *hi, *lo;  // the F32 GEMM's operand split instead of out
 };
 struct Q35FaPrepArgs {
   const void *qg, *kp, *vp;
@@ -446,8 +451,29 @@ int norm(Qwen35 *m, const float *x, const float *w, void *out, int64_t rows, int
   // z (the output gate of the linear layers) is a projection output: f32
   // under F32 compute, else bf16
   Q35NormArgs a{x, w, z, out, rows, L, L, L, z_stride, z_group, m->cfg.eps, zero_centered ? 1 : 0,
-                out_f32 ? 1 : 0, m->f32c ? 1 : 0};
+                out_f32 ? 1 : 0, m->f32c ? 1 : 0, nullptr, nullptr};
   return launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)rows), dim3(256), a);
+}
+
+// y (+)= norm(x) w^T under F32 compute on the GEMM tiles (from 17 rows): the
+// norm writes the GEMM's bf16 hi / lo operand parts itself, so neither the
+// f32 normed rows nor the split launch exist. The norm's rows of L values
+// tile the T x K operand row-major (K = rows * L / T). Returns UNIMPLEMENTED
+// (nothing launched) where the GEMM does not apply; the caller then runs
+// norm and projection apart.
+int norm_linear(Qwen35 *m, const float *x, const float *nw, int64_t rows, int64_t L, bool zero_centered,
+                const void *z, int64_t z_stride, int64_t z_group, const uint8_t *w, const float *sc,
+                float *y, int64_t T, int64_t N, int y_mode) {
+  const int64_t K = rows * L / T;
+  if (!m->f32c || m->packed || !f32_gemm_applies(w, y, T, N, K, m->G) || env_off("RXW8_Q35_NORM_SPLIT"))
+    return RXW8_UNIMPLEMENTED;
+  uint16_t *hi, *lo;
+  int rc = f32_gemm_operands(m->rt, T, K, &hi, &lo);
+  if (rc) return rc;
+  Q35NormArgs a{x, nw, z, nullptr, rows, L, L, L, z_stride, z_group, m->cfg.eps, zero_centered ? 1 : 0,
+                1, 1, hi, lo};
+  if ((rc = launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)rows), dim3(256), a))) return rc;
+  return f32_gemm_presplit(m->rt, w, false, sc, y, T, N, K, m->G, y_mode);
 }
 
 // raw = norm_in(h) [parts]^T (linear layers [qkv; z; b; a], full layers [q; k; v]).
@@ -462,6 +488,9 @@ int in_proj(Qwen35 *m, const Layer &L, int64_t T) {
                      m->H, m->G, 0, o);
     if (rc != RXW8_UNIMPLEMENTED) return rc;
   }
+  rc = norm_linear(m, m->h, m->f32(L.in_norm), T, m->H, true, nullptr, 0, 1, L.in_w, L.in_s,
+                   (float *)m->raw, T, L.n_in, 0);
+  if (rc != RXW8_UNIMPLEMENTED) return rc;
   if ((rc = norm(m, m->h, m->f32(L.in_norm), m->xn, T, m->H, true, m->f32c))) return rc;
   return qlinear_launch(m->rt, m->xn, m->f32c, L.in_w, m->packed, L.in_s, m->raw, m->f32c, T,
                         L.n_in, m->H, m->G, m->f32c ? 0 : 1, 0);
@@ -506,8 +535,13 @@ int mlp(Qwen35 *m, const Layer &L, int64_t T) {
     if (rc != RXW8_UNIMPLEMENTED && rc) return rc;
   }
   if (rc == RXW8_UNIMPLEMENTED && !m->packed) {
-    if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, m->f32c))) return rc;
-    if ((rc = proj_fused(m, L.gu_w, L.gu_s, L.n_gu, m->xn, m->gu, T))) return rc;
+    rc = norm_linear(m, m->h, m->f32(L.post_norm), T, m->H, true, nullptr, 0, 1, L.gu_w, L.gu_s,
+                     (float *)m->gu, T, L.n_gu, 0);
+    if (rc == RXW8_UNIMPLEMENTED) {
+      if ((rc = norm(m, m->h, m->f32(L.post_norm), m->xn, T, m->H, true, m->f32c))) return rc;
+      rc = proj_fused(m, L.gu_w, L.gu_s, L.n_gu, m->xn, m->gu, T);
+    }
+    if (rc) return rc;
     Q35SiluArgs sa{m->gu, m->at(m->gu, m->I), m->act, T * m->I, m->I, L.n_gu, m->f32c ? 1 : 0};
     if ((rc = launch(rt, "rxw8_q35_silu_mul", dim3(grid_n(T * m->I)), dim3(256), sa))) return rc;
     m->ss_cur = nullptr;
@@ -534,6 +568,14 @@ int mlp(Qwen35 *m, const Layer &L, int64_t T) {
 // silu(z); row r = (t, head) takes z at raw + t * n_in + head * Dl), then out_proj.
 int finish_linear(Qwen35 *m, const Layer &L, int64_t T, const void *zp) {
   int rc;
+  if (!m->chain) {  // (chained short inputs: out_proj is a GEMV writing h's row sums)
+    rc = norm_linear(m, m->dout, m->f32(L.lnorm), T * m->Hl, m->Dl, false, zp, L.n_in, m->Hl,
+                     (const uint8_t *)m->ptr(L.out), m->f32(L.out + 1), m->h, T, m->H, 1);
+    if (rc != RXW8_UNIMPLEMENTED) {
+      m->ss_cur = nullptr;
+      return rc;
+    }
+  }
   if ((rc = norm(m, m->dout, m->f32(L.lnorm), m->gated, T * m->Hl, m->Dl, false, m->f32c, zp,
                  L.n_in, m->Hl)))
     return rc;

@@ -174,6 +174,23 @@ def test_f32_gemm_split_k_residuals(rt, monkeypatch, name, b, s):
     assert e_pair <= 1e-5
 
 
+@pytest.mark.parametrize("name,b,s", [("mid_long", 2, 40), ("wide_linear", 1, 65)])
+def test_norm_writes_the_gemm_operands(rt, monkeypatch, name, b, s):
+    """From 17 rows under F32 compute, the RMSNorms ahead of the input
+    projections and gate|up, and the gated norm ahead of out_proj, write the
+    F32 GEMM's bf16 hi / lo operand parts themselves (no f32 rows, no split
+    launch): the same arithmetic as norm + rxw8_gemm_split_x, so the logits
+    equal the separate launches' bit for bit."""
+    cfg = CONFIGS[name]
+    p = q35.random_params(cfg, seed=71, std=0.05)
+    ids = np.random.default_rng(72).integers(0, cfg["vocab"], (b, s))
+    fused = run(rt, build(rt, cfg, p), ids)
+    monkeypatch.setenv("RXW8_Q35_NORM_SPLIT", "0")
+    apart = run(rt, build(rt, cfg, p), ids)
+    np.testing.assert_array_equal(fused, apart)
+    assert rel_err(fused, q35.forward(cfg, p, ids)) <= TOL
+
+
 @pytest.mark.parametrize("name,b,s,std", [("tiny", 2, 13, 0.05), ("small", 2, 13, 0.05),
                                           ("small", 2, 70, 0.05), ("mid", 2, 37, 0.03),
                                           ("wide", 1, 16, 0.02), ("wide_full", 1, 77, 0.02)])
