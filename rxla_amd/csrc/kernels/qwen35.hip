@@ -117,6 +117,65 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a
   }
 }
 
+// The same norm with one wave per row (rows of L <= 64 E values, 4 rows per
+// workgroup): lane l holds elements l + 64 e. Every load of the row (x, the
+// weight, the gate) is a raw buffer load issued before any arithmetic (lanes
+// past L read zeros without touching memory), the sum of squares is a wave
+// butterfly (no barrier), so a row costs one memory round trip; the
+// 256-thread kernel above waits for x, a barrier, then w and z. (The sum is
+// taken in another order than there: per lane, then across the wave.)
+template <int E>
+__device__ __forceinline__ void q35_rmsnorm_wave(const Q35NormArgs &a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;  // uniform per wave
+  const uint32_t L = (uint32_t)a.L;
+  const auto xr = buf_rsrc(a.x + r * a.x_stride, L * 4u);
+  const auto wr = buf_rsrc(a.w, L * 4u);
+  const int64_t zrow = (r / a.z_group) * a.z_stride + (r % a.z_group) * a.L;
+  const int zsz = a.z_f32 ? 4 : 2;
+  const auto zr = buf_rsrc(a.z ? (const char *)a.z + zrow * zsz : (const char *)a.x, a.z ? L * zsz : 0u);
+  float xv[E], wv[E], zv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const uint32_t i = lane + 64 * e;
+    xv[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, i * 4u, 0, 0));
+    wv[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, i * 4u, 0, 0));
+    zv[e] = a.z_f32 ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(zr, i * 4u, 0, 0))
+                    : bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(zr, i * 2u, 0, 0));
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) ss += xv[e] * xv[e];
+  ss = wave_sum64(ss);
+  const float sc = 1.0f / sqrtf(ss / (float)a.L + a.eps);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int64_t i = lane + 64 * e;
+    if (i >= a.L) continue;
+    float y = (xv[e] * sc) * (a.zero_centered ? 1.0f + wv[e] : wv[e]);
+    if (a.z) y *= zv[e] * sigmoid_f32(zv[e]);
+    if (a.hi) {
+      const uint16_t h = f32_to_bf16_bits(y);
+      a.hi[r * a.out_stride + i] = h;
+      a.lo[r * a.out_stride + i] = f32_to_bf16_bits(y - bf16_bits_to_f32(h));
+    } else if (a.out_f32) {
+      ((float *)a.out)[r * a.out_stride + i] = y;
+    } else {
+      ((uint16_t *)a.out)[r * a.out_stride + i] = f32_to_bf16_bits(y);
+    }
+  }
+}
+#define RXW8_Q35_NORM_W(E)                                                      \
+  extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm_w##E(Q35NormArgs a) { \
+    q35_rmsnorm_wave<E>(a);                                                     \
+  }
+RXW8_Q35_NORM_W(1)
+RXW8_Q35_NORM_W(2)
+RXW8_Q35_NORM_W(4)
+RXW8_Q35_NORM_W(8)
+RXW8_Q35_NORM_W(16)
+
 // ---- full attention prologue (layers.rs:28-99): one wave per (token, head).
 // Query heads h < Hq: qg[t, h] = [query (D) | gate (D)] (bf16 projection);
 // gate_out[t, h*D + d] = sigmoid(gate); q_out[t, h, :] = RoPE(norm(query)).

@@ -445,6 +445,20 @@ int proj_fused(Qwen35 *m, const uint8_t *w, const float *sc, int64_t n, const vo
                         m->f32c ? 0 : 1, 0);
 }
 
+// The RMSNorm launch: rows of up to 1024 values one wave each (the
+// rxw8_q35_rmsnorm_w* kernels: one memory round trip per row,
+// RXW8_Q35_NORM_WAVE=0 turns them off), longer ones a workgroup each.
+int launch_norm(Qwen35 *m, const Q35NormArgs &a) {
+  int e = 1;
+  while (64 * e < a.L) e *= 2;
+  if (e <= 16 && !env_off("RXW8_Q35_NORM_WAVE")) {
+    char kname[32];
+    std::snprintf(kname, sizeof kname, "rxw8_q35_rmsnorm_w%d", e);
+    return launch(m->rt, kname, dim3((unsigned)((a.rows + 3) / 4)), dim3(256), a);
+  }
+  return launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)a.rows), dim3(256), a);
+}
+
 int norm(Qwen35 *m, const float *x, const float *w, void *out, int64_t rows, int64_t L,
          bool zero_centered, bool out_f32, const void *z = nullptr, int64_t z_stride = 0,
          int64_t z_group = 1) {
@@ -452,7 +466,7 @@ int norm(Qwen35 *m, const float *x, const float *w, void *out, int64_t rows, int
   // under F32 compute, else bf16
   Q35NormArgs a{x, w, z, out, rows, L, L, L, z_stride, z_group, m->cfg.eps, zero_centered ? 1 : 0,
                 out_f32 ? 1 : 0, m->f32c ? 1 : 0, nullptr, nullptr};
-  return launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)rows), dim3(256), a);
+  return launch_norm(m, a);
 }
 
 // y (+)= norm(x) w^T under F32 compute on the GEMM tiles (from 17 rows): the
@@ -472,7 +486,7 @@ int norm_linear(Qwen35 *m, const float *x, const float *nw, int64_t rows, int64_
   if (rc) return rc;
   Q35NormArgs a{x, nw, z, nullptr, rows, L, L, L, z_stride, z_group, m->cfg.eps, zero_centered ? 1 : 0,
                 1, 1, hi, lo};
-  if ((rc = launch(m->rt, "rxw8_q35_rmsnorm", dim3((unsigned)rows), dim3(256), a))) return rc;
+  if ((rc = launch_norm(m, a))) return rc;
   return f32_gemm_presplit(m->rt, w, false, sc, y, T, N, K, m->G, y_mode);
 }
 
