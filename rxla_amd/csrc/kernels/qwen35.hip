@@ -127,7 +127,10 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_rmsnorm(Q35NormArgs a
 template <int E>
 __device__ __forceinline__ void q35_rmsnorm_wave(const Q35NormArgs &a) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // (the row as a wave-uniform value, so the buffer descriptors sit in
+  // scalar registers: from a plain thread index the compiler wraps each
+  // buffer load in a loop over the lanes' descriptors)
+  const int64_t r = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (r >= a.rows) return;  // uniform per wave
   const uint32_t L = (uint32_t)a.L;
   const auto xr = buf_rsrc(a.x + r * a.x_stride, L * 4u);
@@ -144,6 +147,7 @@ __device__ __forceinline__ void q35_rmsnorm_wave(const Q35NormArgs &a) {
     zv[e] = a.z_f32 ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(zr, i * 4u, 0, 0))
                     : bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(zr, i * 2u, 0, 0));
   }
+  __builtin_amdgcn_sched_barrier(0);  // (all of them issued before the first use)
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < E; ++e) ss += xv[e] * xv[e];
@@ -196,9 +200,11 @@ struct Q35FaPrepArgs {
   int src_f32;           // projection rows in f32 (F32 compute) or bf16
 };
 
-extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs a) {
+template <bool F32>
+__device__ __forceinline__ void q35_fa_prep(const Q35FaPrepArgs &a) {
   __shared__ float rowbuf[4][256 + 8];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // (wv wave-uniform: the buffer descriptors below then sit in scalar registers)
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int heads = a.Hq + a.Hkv;
   const int64_t unit = (int64_t)blockIdx.x * 4 + wv;
   if (unit >= (int64_t)a.T * heads) return;  // wave-uniform
@@ -210,35 +216,48 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
                             : (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
   const void *sbase = is_q ? a.qg : a.kp;
   float *row = rowbuf[wv];
-  float ss = 0.f;
-  for (int i = lane; i < D; i += 64) {
-    const float v = ld(sbase, src + i, a.src_f32);
-    row[i] = v;
-    ss += v * v;
-  }
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-  const float sc = 1.0f / sqrtf(ss / (float)D + a.eps);
-  const float *nw = is_q ? a.q_norm : a.k_norm;
-  for (int i = lane; i < D; i += 64) row[i] = (row[i] * sc) * (1.0f + nw[i]);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int half = a.rot / 2;
-  float *dst = is_q ? a.q_out + ((int64_t)t * a.Hq + h) * D
-                    : a.kc + (((int64_t)bseq * a.Hkv + (h - a.Hq)) * a.Lmax + pos) * D;
-  // Each loop's global loads (up to D / 64 = 4 per lane) go out before its
-  // stores: a load after a store the compiler cannot tell apart from it
-  // would wait for that store, one round trip per element.
+  // Every load of the unit goes out at once, as raw buffer loads (lanes past
+  // D or rot read zeros, no branch): the row, its norm weight, the RoPE
+  // frequencies and the gate / v row. (Loaded in that order of need, they
+  // cost three memory round trips.)
   constexpr int NE = 4;  // D <= 256
-  float fr[NE], gq[NE];
+  const int half = a.rot / 2;
+  constexpr int esz = F32 ? 4 : 2;
+  const int64_t gsrc = is_q ? src + D : (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D;
+  const auto rr = buf_rsrc((const char *)sbase + src * esz, (uint32_t)(D * esz));
+  const auto gr = buf_rsrc((const char *)(is_q ? a.qg : a.vp) + gsrc * esz, (uint32_t)(D * esz));
+  const auto nr = buf_rsrc(is_q ? a.q_norm : a.k_norm, (uint32_t)D * 4u);
+  const auto fq = buf_rsrc(a.freqs, (uint32_t)half * 4u);
+  auto ldb = [&](const __amdgpu_buffer_rsrc_t &r, int i) {
+    if constexpr (F32)
+      return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t)i * 4u, 0, 0));
+    else
+      return bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, (uint32_t)i * 2u, 0, 0));
+  };
+  float xv[NE], nv[NE], fr[NE], gq[NE];
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
     const int i = lane + 64 * e;
-    fr[e] = i < a.rot ? a.freqs[i < half ? i : i - half] : 0.f;
-    gq[e] = i < D ? (is_q ? ld(a.qg, src + D + i, a.src_f32)
-                          : ld(a.vp, (int64_t)t * a.stride + (int64_t)(h - a.Hq) * D + i, a.src_f32))
-                  : 0.f;
+    xv[e] = ldb(rr, i);
+    gq[e] = ldb(gr, i);
+    nv[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(nr, (uint32_t)i * 4u, 0, 0));
+    const uint32_t fo = i < a.rot ? (uint32_t)(i < half ? i : i - half) * 4u : 0x80000000u;
+    fr[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fq, fo, 0, 0));
   }
+  __builtin_amdgcn_sched_barrier(0);  // (all of them issued before the first use)
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) ss += xv[e] * xv[e];
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const float sc = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+  for (int e = 0; e < NE; ++e)
+    if (lane + 64 * e < D) row[lane + 64 * e] = (xv[e] * sc) * (1.0f + nv[e]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float *dst = is_q ? a.q_out + ((int64_t)t * a.Hq + h) * D
+                    : a.kc + (((int64_t)bseq * a.Hkv + (h - a.Hq)) * a.Lmax + pos) * D;
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
     const int i = lane + 64 * e;
@@ -262,6 +281,13 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs
     for (int e = 0; e < NE; ++e)
       if (lane + 64 * e < D) vd[lane + 64 * e] = gq[e];
   }
+}
+// (one straight-line body per source dtype)
+extern "C" __global__ void __launch_bounds__(256) rxw8_q35_fa_prep(Q35FaPrepArgs a) {
+  if (a.src_f32)
+    q35_fa_prep<true>(a);
+  else
+    q35_fa_prep<false>(a);
 }
 
 // ---- causal full-sequence attention in f32 on the matrix cores
