@@ -581,31 +581,69 @@ struct Q35MixPrepArgs {
   int raw_f32;
 };
 
-extern "C" __global__ void __launch_bounds__(128) rxw8_q35_mix_prep(Q35MixPrepArgs a) {
+// Every load of the workgroup goes out before the first use (one memory
+// round trip): the k taps of its channels at clamped rows (a tap before
+// position 0 adds an exact 0 in its place, so each sum keeps the order and
+// value of the skipped form), the conv weights, and the head's b, a, dt_bias
+// and A_log (loaded by every thread, used by thread 0). One body per source
+// dtype and for k = 4 (any other k takes the loop after the loads).
+template <bool F32, int KT>
+__device__ __forceinline__ void q35_mix_prep(const Q35MixPrepArgs &a) {
   __shared__ float red[2][2];
   const int64_t t = blockIdx.x / a.Hl;
   const int h = (int)(blockIdx.x - t * a.Hl);
   const int pos = (int)(t % a.S);
   const int64_t W = (int64_t)a.Hl * a.Dl;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int k = KT > 0 ? KT : a.k;
+  auto ldr = [&](int64_t i) {
+    if constexpr (F32)
+      return ((const float *)a.raw)[i];
+    else
+      return bf16_bits_to_f32(((const uint16_t *)a.raw)[i]);
+  };
+  const int64_t hrow = t * a.stride + 4 * W;
+  const float b_raw = ldr(hrow + h), a_raw = ldr(hrow + a.Hl + h);
+  const float dtb = a.dt_bias[h], alog = a.a_log[h];
+  constexpr int NK = KT > 0 ? KT : 1;
+  float xv[2][3][NK], cw[2][3][NK];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = min((int)threadIdx.x + 128 * r, a.Dl - 1);  // (lanes past Dl: clamped, not stored)
+#pragma unroll
+    for (int part = 0; part < 3; ++part) {
+      const int64_t ch = part * W + (int64_t)h * a.Dl + c;
+#pragma unroll
+      for (int j = 0; j < NK; ++j) {
+        const int src = max(pos - (k - 1) + j, 0);
+        xv[r][part][j] = ldr((t - pos + src) * a.stride + ch);
+        cw[r][part][j] = a.conv_w[ch * k + j];
+      }
+    }
+  }
   float qv[2], kv[2], vv[2];  // channels c = threadIdx.x and c + 128 (Dl <= 256)
   float sq = 0.f, sk = 0.f;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int c = threadIdx.x + 128 * r;
     qv[r] = kv[r] = vv[r] = 0.f;
-    if (c < a.Dl) {
-      float acc[3] = {0.f, 0.f, 0.f};
-      for (int j = 0; j < a.k; ++j) {
-        const int src = pos - (a.k - 1) + j;
-        if (src < 0) continue;
-        const int64_t row = (t - pos + src) * a.stride;
+    float acc[3] = {0.f, 0.f, 0.f};
 #pragma unroll
-        for (int part = 0; part < 3; ++part) {
-          const int64_t ch = part * W + (int64_t)h * a.Dl + c;
-          acc[part] += a.conv_w[ch * a.k + j] * ld(a.raw, row + ch, a.raw_f32);
+    for (int part = 0; part < 3; ++part) {
+      if constexpr (KT > 0) {
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+          acc[part] += pos - (KT - 1) + j >= 0 ? cw[r][part][j] * xv[r][part][j] : 0.f;
+      } else {
+        const int64_t ch = part * W + (int64_t)h * a.Dl + min(c, a.Dl - 1);
+        for (int j = 0; j < k; ++j) {
+          const int src = pos - (k - 1) + j;
+          if (src < 0) continue;
+          acc[part] += a.conv_w[ch * k + j] * ldr((t - pos + src) * a.stride + ch);
         }
       }
+    }
+    if (c < a.Dl) {
       qv[r] = acc[0] * sigmoid_f32(acc[0]);
       kv[r] = acc[1] * sigmoid_f32(acc[1]);
       vv[r] = acc[2] * sigmoid_f32(acc[2]);
@@ -632,13 +670,25 @@ extern "C" __global__ void __launch_bounds__(128) rxw8_q35_mix_prep(Q35MixPrepAr
     }
   }
   if (threadIdx.x == 0) {
-    const int64_t row = t * a.stride + 4 * W;
-    a.beta[t * a.Hl + h] = sigmoid_f32(ld(a.raw, row + h, a.raw_f32));
-    const float x = ld(a.raw, row + a.Hl + h, a.raw_f32) + a.dt_bias[h];
+    a.beta[t * a.Hl + h] = sigmoid_f32(b_raw);
+    const float x = a_raw + dtb;
     const float sp = fmaxf(x, 0.f) + log1pf(expf(-fabsf(x)));
-    const float lgv = sp * -expf(a.a_log[h]);
+    const float lgv = sp * -expf(alog);
     a.g[t * a.Hl + h] = expf(lgv);
     if (a.lg) a.lg[t * a.Hl + h] = lgv;
+  }
+}
+extern "C" __global__ void __launch_bounds__(128) rxw8_q35_mix_prep(Q35MixPrepArgs a) {
+  if (a.k == 4) {
+    if (a.raw_f32)
+      q35_mix_prep<true, 4>(a);
+    else
+      q35_mix_prep<false, 4>(a);
+  } else {
+    if (a.raw_f32)
+      q35_mix_prep<true, 0>(a);
+    else
+      q35_mix_prep<false, 0>(a);
   }
 }
 
