@@ -127,6 +127,45 @@ __device__ __forceinline__ void norm_rope_lane(float (&x)[4][8], const float *nw
   }
 }
 
+// The rope row's and the norm weights' values norm_rope_lane reads, loaded
+// ahead (issued before a K/V tile's loads, the q prologue then waits for
+// these alone, not for the tile behind them: vector loads complete in order).
+struct RopeRow {
+  f32x4 cs[2][2], sn[2][2], w0[2][2], w1[2][2];
+};
+__device__ __forceinline__ void load_rope_row(RopeRow &r, const float *nw, const float *rope, int g4) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = 32 * t + 8 * g4 + 4 * j;
+      r.cs[t][j] = *(const f32x4 *)(rope + i);
+      r.sn[t][j] = *(const f32x4 *)(rope + D / 2 + i);
+      r.w0[t][j] = *(const f32x4 *)(nw + i);
+      r.w1[t][j] = *(const f32x4 *)(nw + D / 2 + i);
+    }
+}
+// norm_rope_lane on preloaded values (nw non-null: the norm is applied)
+__device__ __forceinline__ void norm_rope_lane(float (&x)[4][8], const RopeRow &r, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[t][e] * x[t][e];
+  ss = wave_sum4(ss);
+  const float sc = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x0 = (x[t][e] * sc) * r.w0[t][e >> 2][e & 3];
+      const float x1 = (x[t + 2][e] * sc) * r.w1[t][e >> 2][e & 3];
+      const float c = r.cs[t][e >> 2][e & 3], s = r.sn[t][e >> 2][e & 3];
+      x[t][e] = x0 * c - x1 * s;
+      x[t + 2][e] = x1 * c + x0 * s;
+    }
+}
+
 __device__ __forceinline__ void unpack_bf16x8(const u32x4 &r, float *x) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -392,8 +431,12 @@ __device__ void attn_pass(const AttnArgs &a) {
   const int first = start + wave * KT;
   constexpr int kStep = NP * KT;
   Tile ta, tb;
-  // The first tile is in flight during the q prologue (the fused norm + RoPE
-  // waits on q and the RoPE row).
+  // The first tile is in flight during the q prologue; the q norm weights and
+  // the RoPE row go out before it (with a q norm; without one the plain
+  // form below reads them after the tile)
+  RopeRow rrow;
+  const bool pre_rope = FUSE && a.q_norm != nullptr;  // uniform
+  if (pre_rope) load_rope_row(rrow, a.q_norm, a.rope + (int64_t)pnew * D, g4);
   load(ta, first);
   float m_run = kNegInf, l_run = 0.f;  // per lane: head col (all g4 lanes agree)
   float o[G][8];
@@ -407,7 +450,10 @@ __device__ void attn_pass(const AttnArgs &a) {
     float qv[4][8];
 #pragma unroll
     for (int t = 0; t < 4; ++t) unpack_bf16x8(qraw[t][0], qv[t]);
-    norm_rope_lane(qv, a.q_norm, a.rope + (int64_t)pnew * D, a.eps, g4);
+    if (pre_rope)
+      norm_rope_lane(qv, rrow, a.eps);
+    else
+      norm_rope_lane(qv, a.q_norm, a.rope + (int64_t)pnew * D, a.eps, g4);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
