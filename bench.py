@@ -516,9 +516,35 @@ def bench_f32_linear(rt, rx, torch, stream, reps=10, n=248320, k=1024, g=128):
                             "mfma_frac": round(2 * tf / MFMA_BF16_PEAK_TFLOPS, 4),
                             "flops": 2 * S * n * k}
         del x, y
+    # S = 16 on the tile-layout copies (the Qwen3.5 plan's head up to 16 rows:
+    # rxw8_linear_f32_mfma_pk_r1_w8, contiguous 1 KiB wave loads)
+    pk = [(rx.pack_weight(rt, w), s) for w, s in ws]
+    with torch.cuda.stream(stream):
+        x = torch.randn((16, k), device="cuda", generator=gen)
+        y = torch.empty((16, n), dtype=torch.float32, device="cuda")
+    stream.synchronize()
+    xb, yb = rt.wrap_tensor(x), rt.wrap_tensor(y)
+    for i in range(4):
+        rx.quantized_linear(rt, xb, pk[i % 2][0], pk[i % 2][1], rx.DType.F32, out=yb)
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(SPIN_CYCLES)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        rx.quantized_linear(rt, xb, pk[i % 2][0], pk[i % 2][1], rx.DType.F32, out=yb)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / reps
+    nbytes = n * k + 4 * n * (k // g) + 4 * 16 * k + 4 * 16 * n
+    gbs = nbytes / sec / 1e9
+    out["S16_packed"] = {"bound": "hbm", "us": round(sec * 1e6, 2), "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "bytes": nbytes}
+    del x, y, pk
     del ws
-    return {"kernel": "rxw8_linear_f32_mfma_r1_w8 (S 16) / rxw8_gemm_split_x + rxw8_gemm_f32c "
-                      "(S 1024)",
+    return {"kernel": "rxw8_linear_f32_mfma_r1_w8 (S 16, row-major) / rxw8_linear_f32_mfma_pk_r1_w8 "
+                      "(S16_packed, tile layout) / rxw8_gemm_split_x + rxw8_gemm_f32c (S 1024)",
             "shape": f"W [{n}, {k}] U8, G {g} (the Qwen3.5-0.8B tied LM head), x F32 [S, {k}]",
             "runs": out,
             "note": "mfma_frac counts the hi and lo MFMAs (twice the algorithmic flops)",
