@@ -785,10 +785,14 @@ static int run_linear_f32(Runtime *rt, const float *x, const uint8_t *w, bool pa
     if (kc_max == 0) continue;
     const int64_t gy = (M + 16 * R - 1) / (16 * R);
     if (gy > 65535) return RXW8_UNIMPLEMENTED;
-    // several channel tiles per workgroup when there are many row tiles, so
-    // the staged rows of x are reused (about 2048 workgroups in all)
+    // several channel tiles per workgroup, so the staged rows of x are
+    // reused: just enough that the workgroups fit one round at the LDS-bound
+    // residency (the Qwen3.5 head at 16 rows: 4 tiles each, 485 workgroups,
+    // 69.7 -> 64.2 us packed, 82.7 -> 71.1 us row-major; 3 tiles each spill
+    // into a second round: 70.9 us)
     const int64_t ntiles = (N + 16 * WV - 1) / (16 * WV);
-    const int64_t per = std::max<int64_t>(1, std::min<int64_t>(16, ntiles * gy / 2048));
+    const int64_t resident = std::max<int64_t>(1, (int64_t)rt->lds_max / (int64_t)lds_for(R, kc_max, gk)) * rt->cus;
+    const int64_t per = std::max<int64_t>(1, std::min<int64_t>(16, (ntiles * gy + resident - 1) / resident));
     char kname[40];
     std::snprintf(kname, sizeof kname, "rxw8_linear_f32_mfma%s_r%d_w%d", packed ? "_pk" : "", R, WV);
     for (int64_t k0 = 0; k0 < K; k0 += kc_max) {
