@@ -96,6 +96,7 @@ struct GemvArgs {
   // chunk_rows, min(M, (blockIdx.y + 1) * chunk_rows)) (x, y and the
   // sum-of-squares pointers start at row 0 of the whole product)
   int chunk_rows;
+  int fc_kmajor;  // F32 staging: column-major piece order where it fits (host switch)
 };
 
 // Grouped launch: several independent products, each with its own operands
@@ -454,14 +455,84 @@ __device__ __forceinline__ void stage_x_fc_rounds(const GemvArgs &a, uint16_t *x
   }
 }
 
+// stage_x_fc_kmajor (up to 4 rows per thread): thread t takes the piece at
+// k = 8 (t % (Kc / 8)) of rows t / (Kc / 8) + j NT / (Kc / 8), j < 4, so its
+// norm weights load once for all of its rows, and every row piece, the
+// scales and the norm partials are requested before any is used (one memory
+// round trip instead of the rounds' three or four).
+template <int NT>
+__device__ __forceinline__ void stage_x_fc_kmajor(const GemvArgs &a, uint16_t *xs, float *ss, int k0, int Kc,
+                                                  int LO, int nsc, int rows0, int gps) {
+  const int ldx = Kc + kXPad;
+  const int per_row = Kc / 8, rpb = NT / per_row;  // pieces per row, rows per batch
+  const bool norm = a.x_mode == 3;
+  const int kk = ((int)threadIdx.x % per_row) * 8, b0 = (int)threadIdx.x / per_row;
+  __shared__ float red[4];
+  __shared__ float row_scale[16];
+  float4 xv[4][2], wv[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = b0 + j * rpb;
+    if (b < a.M) {
+      const float *h = (const float *)a.x + b * a.x_stride + a.x_off + k0 + kk;
+      xv[j][0] = *(const float4 *)h;
+      xv[j][1] = *(const float4 *)(h + 4);
+    }
+  }
+  if (norm) {
+    wv[0] = *(const float4 *)(a.norm_w + k0 + kk);
+    wv[1] = *(const float4 *)(a.norm_w + k0 + kk + 4);
+  }
+  if (nsc > 0) {
+    const int groups = a.K / a.G, g0 = k0 / a.G;
+    for (int i = threadIdx.x; i < nsc; i += NT) {
+      const int rr = i / gps, gl = i - rr * gps;
+      const int n = rows0 + rr;
+      ss[i] = n < a.N ? a.scale[(int64_t)n * groups + g0 + gl] : 0.f;
+    }
+  }
+  if (norm) {
+    norm_row_scales(a, row_scale, red);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b = b0 + j * rpb;
+    if (b < a.M) {
+      float v[8] = {xv[j][0].x, xv[j][0].y, xv[j][0].z, xv[j][0].w,
+                    xv[j][1].x, xv[j][1].y, xv[j][1].z, xv[j][1].w};
+      if (norm) {
+        const float sc = row_scale[b];
+        const float w[8] = {wv[0].x, wv[0].y, wv[0].z, wv[0].w, wv[1].x, wv[1].y, wv[1].z, wv[1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (v[e] * sc) * w[e];
+      }
+      u32x4 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float h0 = round_bf16(v[2 * e]), h1 = round_bf16(v[2 * e + 1]);
+        hi[e] = pack_bf16x2(h0, h1);
+        lo[e] = pack_bf16x2(v[2 * e] - h0, v[2 * e + 1] - h1);
+      }
+      *(u32x4 *)(xs + b * ldx + kk) = hi;
+      *(u32x4 *)(xs + (LO + b) * ldx + kk) = lo;
+    }
+  }
+}
 // One straight-line prologue per mode when one batch of pieces and scales
 // per thread covers the rows (up to a few rows: the Qwen3.5-0.8B forward at
-// one row 0.892 against 0.904 ms staged in rounds), else rounds.
-template <int NT>
+// one row 0.892 against 0.904 ms staged in rounds), else rounds, or (KM: the
+// 16-row kernels) the column-major pieces where they fit.
+template <int NT, bool KM>
 __device__ __forceinline__ void stage_x_fc(const GemvArgs &a, uint16_t *xs, float *ss, int k0, int Kc,
                                            int LO, int nsc, int rows0, int gps) {
   const bool one = a.M * (Kc / 8) <= NT && nsc <= NT && a.M <= NT / 64;
-  if (!one)
+  const int per_row = Kc / 8;
+  const bool kmajor = KM && a.fc_kmajor && (a.x_mode == 0 || a.x_mode == 3) && per_row <= NT &&
+                      NT % per_row == 0 && a.M <= 4 * (NT / per_row) && a.M <= 16;
+  if (KM && !one && kmajor)
+    stage_x_fc_kmajor<NT>(a, xs, ss, k0, Kc, LO, nsc, rows0, gps);
+  else if (!one)
     stage_x_fc_rounds<NT>(a, xs, ss, k0, Kc, LO, nsc, rows0, gps);
   else if (a.x_mode == 3)
     stage_x_fc_impl<NT, 3, 1>(a, xs, ss, k0, Kc, LO, nsc, rows0, gps);
@@ -923,7 +994,7 @@ __device__ __forceinline__ void gemv_w8(const GemvArgs &a, const int blk) {
     // Grouped scales of this workgroup's rows and K-split, staged after x:
     // ss[row_in_block * gps + g_local] (f32).
     if (FC) {
-      stage_x_fc<NW * 64>(a, xs, ss, k0, Kc, LO, per_channel ? 0 : 16 * RW * gps, rows0, gps);
+      stage_x_fc<NW * 64, MB == 2>(a, xs, ss, k0, Kc, LO, per_channel ? 0 : 16 * RW * gps, rows0, gps);
     } else {
       if (!per_channel) {
         const int g0 = k0 / a.G;

@@ -39,6 +39,7 @@ struct GemvArgs {
   uint16_t *xw_out;
   int ss_ld;  // row stride of the sum-of-squares partials
   int chunk_rows;  // F32-compute kernels: rows per grid row (blockIdx.y)
+  int fc_kmajor;   // F32 staging in column-major piece order where it fits
 };
 
 struct PackArgs {
@@ -607,6 +608,7 @@ static int run_gemv_fc(Runtime *rt, const float *x, const uint8_t *w, const floa
   a.ss_parts = pro->ss_parts;
   a.ss_ld = (int)M;
   a.chunk_rows = (int)mchunk;
+  a.fc_kmajor = env_int("RXW8_GEMV_FC_KMAJOR", 1) != 0;
   const size_t lds = gemv_lds(rows, K, K, G, p.rw, (int)mb, false, p.nw);
   return launch(rt, kname, dim3((unsigned)tiles, (unsigned)chunks), dim3(64 * p.nw), a, lds);
 }
