@@ -686,11 +686,6 @@ __device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a)
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
   __shared__ float sc[32 * TNB];  // [group][row]
 
-  // rows past N (the last n tile of N % 256 == 128) repeat row N - 1 and are not stored
-  for (int e = tid; e < ng * TNB; e += 512) {
-    const int g = e / TNB, row = e - g * TNB;
-    sc[e] = a.scale[(int64_t)min(n0 + row, a.N - 1) * ng + g];
-  }
   // activation DMA: instruction i of this wave fills rows 8 (2 wave + i) .. + 8
   uint32_t xoff[XDMA];
 #pragma unroll
@@ -751,6 +746,16 @@ __device__ __forceinline__ void linear_f32_gemm_tile(const LinearF32GemmArgs &a)
 
   load_w(kb);
   issue_x(kb, 0);
+  // this split's scale groups only (sc keeps the absolute group index), their
+  // loads behind the first tile's: rows past N (the last n tile of N % 256 ==
+  // 128) repeat row N - 1 and are not stored
+  {
+    const int g_lo = kb / tpg, g_hi = (ke - 1) / tpg + 1;
+    for (int e = g_lo * TNB + tid; e < g_hi * TNB; e += 512) {
+      const int g = e / TNB, row = e - g * TNB;
+      sc[e] = a.scale[(int64_t)min(n0 + row, a.N - 1) * ng + g];
+    }
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   store_w(0);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
