@@ -926,8 +926,19 @@ extern "C" __global__ void __launch_bounds__(256) rxw8_gemm_f32c_reduce(F32Reduc
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < q4;
        i += (int64_t)gridDim.x * blockDim.x) {
     const f32x4 h = a.y_mode == 1 ? ((const f32x4 *)a.y)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 sum = ((const f32x4 *)a.ws)[i];
-    for (int s = 1; s < a.ksplit; ++s) sum += ((const f32x4 *)(a.ws + (int64_t)s * a.mn))[i];
+    // partials in batches of 8 loaded before they are added (a loop adding
+    // each as it arrives waited one memory round trip per split); the sum
+    // stays in split order (indices past the last split re-read it, unused)
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < a.ksplit; s0 += 8) {
+      f32x4 p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        p[j] = ((const f32x4 *)(a.ws + (int64_t)min(s0 + j, a.ksplit - 1) * a.mn))[i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < a.ksplit) sum = s0 + j == 0 ? p[j] : sum + p[j];
+    }
     ((f32x4 *)a.y)[i] = a.y_mode == 1 ? h + sum : sum;
   }
 }
